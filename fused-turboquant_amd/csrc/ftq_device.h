@@ -1,0 +1,175 @@
+// Device helpers shared by the fused-turboquant HIP kernels (gfx950 / CDNA4).
+//
+// Lane layout used by the codec kernels: one vector of D elements is held by
+// a group of LPV = D / E lanes, lane j holding the E contiguous elements
+// [j*E, (j+1)*E).  The Walsh-Hadamard butterflies with stride h < E run inside
+// the lane's registers; strides h >= E pair lane j with lane j ^ (h / E) and
+// use DPP row permutes (no LDS traffic).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <hip/hip_bf16.h>
+#include <stdint.h>
+
+namespace ftq {
+
+// ---- DPP cross-lane moves inside a 16-lane row ----------------------------
+// dpp_ctrl encodings (GFX9 DPP): quad_perm = p0 | p1<<2 | p2<<4 | p3<<6,
+// row_shl:n = 0x100+n (lane l reads l+n), row_shr:n = 0x110+n (lane l reads
+// l-n), row_ror:n = 0x120+n.
+__device__ __forceinline__ float dpp_xor1(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float dpp_xor2(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float dpp_xor4(float v) {
+  int x = __float_as_int(v);
+  // banks 0 and 2 (lanes 0-3, 8-11 of each row) read lane+4, banks 1 and 3 read lane-4
+  int t = __builtin_amdgcn_update_dpp(x, x, 0x104, 0xF, 0x5, false);
+  t = __builtin_amdgcn_update_dpp(t, x, 0x114, 0xF, 0xA, false);
+  return __int_as_float(t);
+}
+__device__ __forceinline__ float dpp_xor8(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false));
+}
+__device__ __forceinline__ uint32_t dpp_xor1_u(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false);
+}
+// lane q of each quad reads lane min(q+1, 3) of the same quad
+__device__ __forceinline__ uint32_t dpp_quad_next(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xF9, 0xF, 0xF, false);
+}
+
+template <int M>
+__device__ __forceinline__ float lane_xor(float v) {
+  static_assert(M == 1 || M == 2 || M == 4 || M == 8, "lane xor within a 16-lane row");
+  if constexpr (M == 1) return dpp_xor1(v);
+  else if constexpr (M == 2) return dpp_xor2(v);
+  else if constexpr (M == 4) return dpp_xor4(v);
+  else return dpp_xor8(v);
+}
+
+// Sum over the LPV lanes of a vector group.  Every lane ends with the same
+// bits: each xor stage adds the same two operands in either order.
+template <int LPV>
+__device__ __forceinline__ float group_sum(float v) {
+  if constexpr (LPV >= 2) v += lane_xor<1>(v);
+  if constexpr (LPV >= 4) v += lane_xor<2>(v);
+  if constexpr (LPV >= 8) v += lane_xor<4>(v);
+  if constexpr (LPV >= 16) v += lane_xor<8>(v);
+  return v;
+}
+
+// ---- Walsh-Hadamard butterflies ------------------------------------------
+// Unnormalised FWHT of a D-vector held as E elements per lane in LPV lanes,
+// stages in the order h = 1, 2, 4, ..., D/2.  Each stage maps the pair
+// (x[i], x[i+h]) to (x[i] + x[i+h], x[i] - x[i+h]), so the result is
+// bit-identical to any implementation that uses the same stage order.
+template <int E, int LPV>
+__device__ __forceinline__ void fwht_lanes(float (&x)[E], int lane_in_group) {
+#pragma unroll
+  for (int h = 1; h < E; h <<= 1) {
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+      if ((i & h) == 0) {
+        float a = x[i], b = x[i + h];
+        x[i] = a + b;
+        x[i + h] = a - b;
+      }
+    }
+  }
+#pragma unroll
+  for (int m = 1; m < LPV; m <<= 1) {
+    const bool upper = (lane_in_group & m) != 0;
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+      float p;
+      if (m == 1) p = lane_xor<1>(x[i]);
+      else if (m == 2) p = lane_xor<2>(x[i]);
+      else if (m == 4) p = lane_xor<4>(x[i]);
+      else p = lane_xor<8>(x[i]);
+      x[i] = upper ? (p - x[i]) : (x[i] + p);
+    }
+  }
+}
+
+// ---- element loads / stores ----------------------------------------------
+enum DType : int { F32 = 0, F16 = 1, BF16 = 2 };
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
+
+// float -> bf16 bits, round to nearest even (NaN kept quiet)
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+__device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
+  return (uint32_t)__half_as_ushort(__float2half_rn(f));
+}
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t b) {
+  return __half2float(__ushort_as_half((unsigned short)b));
+}
+
+// Load E contiguous elements (E multiple of 8 for 16-bit types, of 4 for f32).
+template <int DT, int E>
+__device__ __forceinline__ void load_elems(const void* base, int64_t elem_off, float (&x)[E]) {
+  if constexpr (DT == F32) {
+    const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(base) + elem_off);
+#pragma unroll
+    for (int k = 0; k < E / 4; ++k) {
+      float4 v = p[k];
+      x[4 * k + 0] = v.x; x[4 * k + 1] = v.y; x[4 * k + 2] = v.z; x[4 * k + 3] = v.w;
+    }
+  } else {
+    const uint4* p = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + elem_off);
+#pragma unroll
+    for (int k = 0; k < E / 8; ++k) {
+      uint4 v = p[k];
+      uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if constexpr (DT == BF16) {
+          x[8 * k + 2 * j] = bf16_bits_to_f32(w[j] & 0xffffu);
+          x[8 * k + 2 * j + 1] = bf16_bits_to_f32(w[j] >> 16);
+        } else {
+          x[8 * k + 2 * j] = f16_bits_to_f32(w[j] & 0xffffu);
+          x[8 * k + 2 * j + 1] = f16_bits_to_f32(w[j] >> 16);
+        }
+      }
+    }
+  }
+}
+
+template <int DT, int E>
+__device__ __forceinline__ void store_elems(void* base, int64_t elem_off, const float (&x)[E]) {
+  if constexpr (DT == F32) {
+    float4* p = reinterpret_cast<float4*>(static_cast<float*>(base) + elem_off);
+#pragma unroll
+    for (int k = 0; k < E / 4; ++k) p[k] = make_float4(x[4 * k], x[4 * k + 1], x[4 * k + 2], x[4 * k + 3]);
+  } else {
+    uint4* p = reinterpret_cast<uint4*>(static_cast<uint16_t*>(base) + elem_off);
+#pragma unroll
+    for (int k = 0; k < E / 8; ++k) {
+      uint32_t w[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        uint32_t lo, hi;
+        if constexpr (DT == BF16) {
+          lo = f32_to_bf16_bits(x[8 * k + 2 * j]);
+          hi = f32_to_bf16_bits(x[8 * k + 2 * j + 1]);
+        } else {
+          lo = f32_to_f16_bits(x[8 * k + 2 * j]);
+          hi = f32_to_f16_bits(x[8 * k + 2 * j + 1]);
+        }
+        w[j] = lo | (hi << 16);
+      }
+      p[k] = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+  }
+}
+
+}  // namespace ftq

@@ -1,0 +1,298 @@
+"""CPU oracle for the fused-turboquant KV-cache hot path (TEST INFRASTRUCTURE).
+
+This module is the checker, never the product: only ``tests/``,
+``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
+import it.  The shipped path (``fused_turboquant``) never calls into it and has
+no CPU fallback.
+
+It restates, in numpy, the reference's unfused PyTorch algorithm:
+
+* ``fwht`` / ``rht`` / ``inverse_rht`` -- reference ``core/hadamard.py:23-48``
+  (butterfly order h = 1, 2, 4, ...; pairs ``[a+b, a-b]``; final ``* d**-0.5``
+  rounded to float32) and ``:70-100`` (sign flip before / after).
+* ``lloyd_max_codebook`` -- reference ``core/lloyd_max.py:24-88`` (grid
+  Lloyd-Max on the Beta coordinate density, 300 iterations, float64).
+* ``quantize`` -- reference ``core/lloyd_max.py:121-132``
+  (``bucketize(right=False) - 1`` clamped to ``[0, 2^b - 1]``).
+* ``pack_*`` / ``unpack_*`` -- reference ``core/packing.py:14-128``.
+* ``encode`` / ``decode`` -- reference ``core/quantizer.py:137-160`` and
+  ``:191-205`` (``TurboQuantMSE._encode_unfused`` / ``_decode_unfused``).
+* ``dense_decode_attention`` -- the semantics of library-format decode
+  attention, reference ``vllm_plugin/attention_impl.py:431-521`` and
+  ``kernels/triton_flash_decode.py:66-221``: softmax(q . K^ * scale) . V^ with
+  K^, V^ the decoded cache, computed in float64.
+* ``v1_*`` -- the vLLM v1 ``TURBOQUANT`` slot format: store
+  ``vllm_plugin/triton_inkernel_store.py:38-440`` and decode stage 1/2
+  ``vllm_plugin/triton_decode_offset.py:42-442`` + ``v1_backend.py:975-1093``.
+
+Pinning (each check lives in ``tests/test_oracle.py``):
+
+* fwht: the reference's d=2 known answer, an explicit Sylvester matrix product,
+  involution, and the reference's own outputs (``tests/golden/fwht.npz``).
+* codebook: the reference's own outputs for d in {64,128,256} x bits in
+  {1,2,3,4} (``tests/golden/codebooks.npz``), plus sortedness / symmetry.
+* signs: the reference's own outputs (``tests/golden/signs.npz``).
+* quantize/pack: brute force over every 3-bit group and random bytes, and the
+  reference's codes (``tests/golden/encode.npz``).
+* encode/decode: the reference's own codes, fp16 norms and decoded vectors
+  (``tests/golden/encode.npz``).
+* dense attention: an independent float64 computation in the test of the
+  rotated-domain identity <q, RHT^-1 c> = <RHT q, c>, and the reference's
+  structure (softmax over masked scores).
+* v1 store/decode: parity unpinned against vLLM (vLLM's ``get_centroids`` and
+  stage-2 kernel are not in the reference tree); pinned by closed forms (LSE
+  merge == single softmax, uniform quantiser error bound, Hadamard matrix).
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+# --------------------------------------------------------------------------
+# Hadamard transforms  (reference core/hadamard.py:23-100)
+# --------------------------------------------------------------------------
+
+
+def _check_pow2(d: int) -> None:
+    if d < 1 or (d & (d - 1)) != 0:
+        raise ValueError(f"d must be a power of 2, got {d}")
+
+
+def fwht_unscaled(x: np.ndarray) -> np.ndarray:
+    """Butterflies only, float32, h = 1, 2, 4, ... (reference hadamard.py:37-47)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    d = x.shape[-1]
+    _check_pow2(d)
+    lead = x.shape[:-1]
+    h = 1
+    while h < d:
+        v = x.reshape(*lead, d // (2 * h), 2, h)
+        a = v[..., 0, :]
+        b = v[..., 1, :]
+        x = np.stack([a + b, a - b], axis=-2).reshape(*lead, d)
+        h *= 2
+    return x
+
+
+def fwht_scale(d: int) -> np.float32:
+    """``d ** -0.5`` as the float32 constant torch multiplies by."""
+    return np.float32(d ** -0.5)
+
+
+def fwht(x: np.ndarray) -> np.ndarray:
+    """Orthonormal FWHT (reference hadamard.py:23-48)."""
+    x = fwht_unscaled(x)
+    return (x * fwht_scale(x.shape[-1])).astype(np.float32)
+
+
+def rht(x: np.ndarray, signs: np.ndarray) -> np.ndarray:
+    """y = fwht(x * s)  (reference hadamard.py:70-90)."""
+    return fwht(np.asarray(x, np.float32) * np.asarray(signs, np.float32))
+
+
+def inverse_rht(y: np.ndarray, signs: np.ndarray) -> np.ndarray:
+    """x = fwht(y) * s  (reference hadamard.py:93-100)."""
+    return (fwht(y) * np.asarray(signs, np.float32)).astype(np.float32)
+
+
+def sylvester(d: int) -> np.ndarray:
+    """Unnormalised Sylvester Hadamard matrix H_d (float64)."""
+    _check_pow2(d)
+    h = np.ones((1, 1))
+    while h.shape[0] < d:
+        h = np.block([[h, h], [h, -h]])
+    return h
+
+
+# --------------------------------------------------------------------------
+# Lloyd-Max codebook  (reference core/lloyd_max.py:24-88)
+# --------------------------------------------------------------------------
+
+
+def lloyd_max_codebook(dim: int, bits: int, max_iterations: int = 300,
+                       num_grid_points: int = 50000):
+    """Grid Lloyd-Max on the density (1 - z^2)^((d-3)/2) over [-6/sqrt d, 6/sqrt d].
+
+    Returns ``(boundaries[2^b + 1], levels[2^b])`` in float64.
+    """
+    n = 1 << bits
+    expo = (dim - 3) / 2.0
+    sigma = 1.0 / math.sqrt(dim)
+    lo = max(-1.0, -6.0 * sigma)
+    hi = min(1.0, 6.0 * sigma)
+    grid = np.linspace(lo, hi, num_grid_points)
+    w = np.maximum(1.0 - grid ** 2, 0.0) ** expo
+    w /= w.sum()
+    bnd = np.interp(np.linspace(0, 1, n + 1), np.cumsum(w), grid)
+    bnd[0] = lo
+    bnd[-1] = hi
+    lev = np.zeros(n)
+
+    def centroids():
+        for i in range(n):
+            if i == n - 1:
+                m = (grid >= bnd[i]) & (grid <= bnd[i + 1])
+            else:
+                m = (grid >= bnd[i]) & (grid < bnd[i + 1])
+            ww = w[m]
+            if ww.sum() > 0:
+                lev[i] = np.average(grid[m], weights=ww)
+            else:
+                lev[i] = (bnd[i] + bnd[i + 1]) / 2.0
+
+    centroids()
+    for _ in range(max_iterations):
+        for i in range(1, n):
+            bnd[i] = (lev[i - 1] + lev[i]) / 2.0
+        centroids()
+    return bnd, lev
+
+
+# --------------------------------------------------------------------------
+# Quantise / pack  (reference core/lloyd_max.py:121-136, core/packing.py)
+# --------------------------------------------------------------------------
+
+
+def quantize(u: np.ndarray, boundaries: np.ndarray, bits: int) -> np.ndarray:
+    """``clamp(bucketize(u, B, right=False) - 1, 0, 2^b - 1)`` as uint8.
+
+    torch.bucketize(right=False) returns i with B[i-1] < u <= B[i], i.e. the
+    number of boundaries strictly below u -- numpy's searchsorted(side='left').
+    """
+    b = np.asarray(boundaries, np.float32)
+    idx = np.searchsorted(b, np.asarray(u, np.float32), side="left").astype(np.int64) - 1
+    return np.clip(idx, 0, (1 << bits) - 1).astype(np.uint8)
+
+
+def pack(codes: np.ndarray, bits: int) -> np.ndarray:
+    c = np.asarray(codes).astype(np.uint32)
+    d = c.shape[-1]
+    lead = c.shape[:-1]
+    if bits == 4:
+        v = c.reshape(*lead, d // 2, 2)
+        return ((v[..., 1] << 4) | v[..., 0]).astype(np.uint8)
+    if bits == 2:
+        v = c.reshape(*lead, d // 4, 4)
+        return (v[..., 0] | (v[..., 1] << 2) | (v[..., 2] << 4) | (v[..., 3] << 6)).astype(np.uint8)
+    if bits == 3:
+        v = c.reshape(*lead, d // 8, 8)
+        w = np.zeros(v.shape[:-1], np.uint32)
+        for k in range(8):
+            w |= (v[..., k] & 7) << (3 * k)
+        out = np.stack([w & 255, (w >> 8) & 255, (w >> 16) & 255], axis=-1)
+        return out.reshape(*lead, d * 3 // 8).astype(np.uint8)
+    if bits == 1:
+        v = c.reshape(*lead, d // 8, 8)
+        w = np.zeros(v.shape[:-1], np.uint32)
+        for k in range(8):
+            w |= (v[..., k] & 1) << k
+        return w.astype(np.uint8)
+    if bits == 8:
+        return c.astype(np.uint8)
+    raise ValueError(bits)
+
+
+def unpack(packed: np.ndarray, bits: int, d: int) -> np.ndarray:
+    p = np.asarray(packed).astype(np.uint32)
+    lead = p.shape[:-1]
+    if bits == 4:
+        return np.stack([p & 15, p >> 4], axis=-1).reshape(*lead, d).astype(np.uint8)
+    if bits == 2:
+        return np.stack([(p >> s) & 3 for s in (0, 2, 4, 6)], axis=-1).reshape(*lead, d).astype(np.uint8)
+    if bits == 3:
+        g = p.reshape(*lead, d // 8, 3)
+        w = g[..., 0] | (g[..., 1] << 8) | (g[..., 2] << 16)
+        return np.stack([(w >> (3 * k)) & 7 for k in range(8)], axis=-1).reshape(*lead, d).astype(np.uint8)
+    if bits == 1:
+        return np.stack([(p >> k) & 1 for k in range(8)], axis=-1).reshape(*lead, d).astype(np.uint8)
+    if bits == 8:
+        return p.astype(np.uint8)
+    raise ValueError(bits)
+
+
+def packed_dim(d: int, bits: int) -> int:
+    return (d * bits + 7) // 8
+
+
+# --------------------------------------------------------------------------
+# Library-format encode / decode  (reference core/quantizer.py:137-205)
+# --------------------------------------------------------------------------
+
+
+def l2norm_f32(y: np.ndarray) -> np.ndarray:
+    """Per-vector Euclidean norm of float32 rows, correctly rounded to float32."""
+    y64 = np.asarray(y, np.float64)
+    return np.sqrt(np.sum(y64 * y64, axis=-1)).astype(np.float32)
+
+
+def encode(x: np.ndarray, signs: np.ndarray, boundaries: np.ndarray, bits: int):
+    """Returns ``(packed u8, norms f16, u f32, norms f32)``.
+
+    ``u`` are the normalised rotated coordinates fed to the quantiser; the
+    tests use them to identify codebook-boundary ties.
+    """
+    y = rht(np.asarray(x, np.float32), signs)
+    n = l2norm_f32(y)
+    u = (y / (n[..., None] + np.float32(1e-8))).astype(np.float32)
+    codes = quantize(u, boundaries, bits)
+    return pack(codes, bits), n.astype(np.float16), u, n
+
+
+def decode(packed: np.ndarray, norms16: np.ndarray, levels: np.ndarray, signs: np.ndarray,
+           bits: int, d: int) -> np.ndarray:
+    codes = unpack(packed, bits, d)
+    lev = np.asarray(levels, np.float32)[codes]
+    r = (lev * np.asarray(norms16, np.float16).astype(np.float32)[..., None]).astype(np.float32)
+    return inverse_rht(r, signs)
+
+
+def boundary_distance(u: np.ndarray, boundaries: np.ndarray) -> np.ndarray:
+    """|u - nearest interior boundary| (float64), for tie accounting."""
+    b = np.asarray(boundaries, np.float32).astype(np.float64)[1:-1]
+    uu = np.asarray(u, np.float64)[..., None]
+    return np.min(np.abs(uu - b), axis=-1)
+
+
+# --------------------------------------------------------------------------
+# Dense library-format decode attention (float64)
+# reference vllm_plugin/attention_impl.py:431-521, kernels/triton_flash_decode.py
+# --------------------------------------------------------------------------
+
+
+def dense_decode_attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, seq_lens, scale: float):
+    """q [B, Hq, d]; k, v [B, Hkv, S, d] (already decoded); returns [B, Hq, d] float64.
+
+    Positions >= seq_lens[b] are masked (reference attention_impl.py:492-498).
+    GQA: q-head h reads kv-head h // (Hq // Hkv) (reference triton_flash_decode.py:71-75).
+    """
+    q = np.asarray(q, np.float64)
+    B, Hq, d = q.shape
+    Hkv = k.shape[1]
+    g = Hq // Hkv
+    out = np.zeros((B, Hq, d))
+    for b in range(B):
+        L = int(seq_lens[b])
+        for h in range(Hq):
+            kk = np.asarray(k[b, h // g, :L], np.float64)
+            vv = np.asarray(v[b, h // g, :L], np.float64)
+            s = kk @ q[b, h] * scale
+            if L == 0:
+                continue
+            s = s - s.max()
+            p = np.exp(s)
+            out[b, h] = (p / p.sum()) @ vv
+    return out
+
+
+def lse_merge(parts_o: np.ndarray, parts_lse: np.ndarray):
+    """Log-sum-exp merge of split results (vLLM stage 2 semantics).
+
+    parts_o [..., S, d], parts_lse [..., S]; splits with lse = -inf are dropped.
+    """
+    m = np.max(parts_lse, axis=-1, keepdims=True)
+    m = np.where(np.isfinite(m), m, 0.0)
+    w = np.exp(parts_lse - m)
+    den = w.sum(-1)
+    o = (w[..., None] * parts_o).sum(-2) / np.where(den > 0, den, 1.0)[..., None]
+    return o, (m[..., 0] + np.log(np.where(den > 0, den, 1.0)))
