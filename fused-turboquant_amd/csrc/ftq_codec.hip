@@ -1,0 +1,348 @@
+// Library-format TurboQuant codec kernels for gfx950:
+//   encode  = RHT (sign flip + FWHT) -> per-vector L2 norm -> u = y / (norm + 1e-8)
+//             -> Lloyd-Max bucketize -> 2/3/4-bit pack, fp16 norm
+//   decode  = unpack -> levels[code] * norm -> FWHT -> sign flip
+//   rht     = forward / inverse randomized Hadamard transform
+//
+// Semantics follow the reference's unfused PyTorch path
+// (core/quantizer.py:137-160 encode, :191-205 decode, core/hadamard.py:23-100),
+// which the Triton kernels (kernels/triton_encode.py, triton_decode.py,
+// triton_rht.py) replace on CUDA.  The C entry points are declared in
+// include/fused_tq.h.
+//
+// Mapping: one vector per LPV lanes (E elements per lane, see ftq_device.h);
+// a 256-thread workgroup holds 256/LPV vectors and walks the batch with a
+// grid-stride loop.  Codes are packed with DPP neighbour exchanges into
+// dword stores; nothing goes through HBM scratch.
+#include "ftq_device.h"
+#include "ftq_internal.h"
+
+#include <cmath>
+
+namespace ftq {
+
+template <int D> struct CodecShape {
+  static constexpr int E = (D == 256) ? 16 : 8;
+  static constexpr int LPV = D / E;
+  static constexpr int GPB = 256 / LPV;
+};
+
+// Pack the E codes of this lane (BITS each) into the vector's packed row.
+template <int E, int BITS>
+__device__ __forceinline__ void pack_store(const uint32_t (&c)[E], uint8_t* row, int lane) {
+  if constexpr (E == 8 && BITS == 4) {
+    uint32_t w = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) w |= c[k] << (4 * k);
+    reinterpret_cast<uint32_t*>(row)[lane] = w;
+  } else if constexpr (E == 8 && BITS == 2) {
+    uint32_t w = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) w |= c[k] << (2 * k);
+    uint32_t wn = dpp_xor1_u(w);
+    if ((lane & 1) == 0) reinterpret_cast<uint32_t*>(row)[lane >> 1] = w | (wn << 16);
+  } else if constexpr (E == 8 && BITS == 3) {
+    uint32_t w = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) w |= c[k] << (3 * k);
+    uint32_t wn = dpp_quad_next(w);
+    const int q = lane & 3;
+    if (q < 3)
+      reinterpret_cast<uint32_t*>(row)[3 * (lane >> 2) + q] = (w >> (8 * q)) | (wn << (24 - 8 * q));
+  } else if constexpr (E == 16 && BITS == 4) {
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) { lo |= c[k] << (4 * k); hi |= c[k + 8] << (4 * k); }
+    reinterpret_cast<uint2*>(row)[lane] = make_uint2(lo, hi);
+  } else if constexpr (E == 16 && BITS == 2) {
+    uint32_t w = 0;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) w |= c[k] << (2 * k);
+    reinterpret_cast<uint32_t*>(row)[lane] = w;
+  } else if constexpr (E == 16 && BITS == 3) {
+    uint64_t w = 0;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) w |= (uint64_t)c[k] << (3 * k);
+    uint32_t lo = (uint32_t)w, hi = (uint32_t)(w >> 32);
+    uint32_t plo = dpp_xor1_u(lo), phi = dpp_xor1_u(hi);
+    if ((lane & 1) == 0) {
+      uint32_t* dst = reinterpret_cast<uint32_t*>(row) + 3 * (lane >> 1);
+      dst[0] = lo;
+      dst[1] = (hi & 0xffffu) | (plo << 16);
+      dst[2] = (plo >> 16) | (phi << 16);
+    }
+  } else {
+    static_assert(BITS == 2 || BITS == 3 || BITS == 4, "unsupported bit width");
+  }
+}
+
+// Read the E codes of this lane from the vector's packed row.
+template <int E, int BITS>
+__device__ __forceinline__ void unpack_load(const uint8_t* row, int lane, uint32_t (&c)[E]) {
+  constexpr int B = E * BITS / 8;  // packed bytes per lane
+  const int o = lane * B;
+  const uint32_t* dw = reinterpret_cast<const uint32_t*>(row);
+  uint64_t win;
+  if constexpr (B == 8) {
+    uint2 v = reinterpret_cast<const uint2*>(row)[lane];
+    win = ((uint64_t)v.y << 32) | v.x;
+  } else if constexpr (B == 4) {
+    win = dw[lane];
+  } else if constexpr (B == 2) {
+    win = reinterpret_cast<const uint16_t*>(row)[lane];
+  } else {
+    uint32_t d0 = dw[o >> 2];
+    uint32_t d1 = dw[(o + B - 1) >> 2];
+    win = ((((uint64_t)d1) << 32) | d0) >> (8 * (o & 3));
+  }
+  constexpr uint32_t mask = (1u << BITS) - 1u;
+#pragma unroll
+  for (int k = 0; k < E; ++k) c[k] = (uint32_t)(win >> (BITS * k)) & mask;
+}
+
+template <int D, int BITS, int DT>
+__global__ __launch_bounds__(256) void encode_kernel(const void* __restrict__ x, int64_t n,
+                                                     const float* __restrict__ signs,
+                                                     const float* __restrict__ boundaries,
+                                                     float scale, uint8_t* __restrict__ packed,
+                                                     uint16_t* __restrict__ norms) {
+  using S = CodecShape<D>;
+  constexpr int E = S::E, LPV = S::LPV, GPB = S::GPB;
+  constexpr int L = 1 << BITS;
+  constexpr int PD = D * BITS / 8;
+  const int lane = threadIdx.x % LPV;
+  const int grp = threadIdx.x / LPV;
+
+  float bnd[L - 1];
+#pragma unroll
+  for (int j = 0; j < L - 1; ++j) bnd[j] = boundaries[j + 1];
+  float sg[E];
+#pragma unroll
+  for (int i = 0; i < E; ++i) sg[i] = signs[lane * E + i];
+
+  for (int64_t v = (int64_t)blockIdx.x * GPB + grp; v < n; v += (int64_t)gridDim.x * GPB) {
+    float y[E];
+    load_elems<DT, E>(x, v * D + lane * E, y);
+#pragma unroll
+    for (int i = 0; i < E; ++i) y[i] *= sg[i];
+    fwht_lanes<E, LPV>(y, lane);
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+      y[i] *= scale;
+      ss = __builtin_fmaf(y[i], y[i], ss);
+    }
+    ss = group_sum<LPV>(ss);
+    const float nrm = __builtin_sqrtf(ss);
+    const float den = nrm + 1e-8f;
+    uint32_t c[E];
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+      const float u = y[i] / den;
+      uint32_t q = 0;
+#pragma unroll
+      for (int j = 0; j < L - 1; ++j) q += (bnd[j] < u) ? 1u : 0u;
+      c[i] = q;
+    }
+    pack_store<E, BITS>(c, packed + v * PD, lane);
+    if (lane == 0) norms[v] = (uint16_t)f32_to_f16_bits(nrm);
+  }
+}
+
+template <int D, int BITS, int OT>
+__global__ __launch_bounds__(256) void decode_kernel(const uint8_t* __restrict__ packed,
+                                                     const uint16_t* __restrict__ norms, int64_t n,
+                                                     const float* __restrict__ levels,
+                                                     const float* __restrict__ signs, float scale,
+                                                     void* __restrict__ out) {
+  using S = CodecShape<D>;
+  constexpr int E = S::E, LPV = S::LPV, GPB = S::GPB;
+  constexpr int L = 1 << BITS;
+  constexpr int PD = D * BITS / 8;
+  __shared__ float slev[L];
+  if (threadIdx.x < L) slev[threadIdx.x] = levels[threadIdx.x];
+  __syncthreads();
+  const int lane = threadIdx.x % LPV;
+  const int grp = threadIdx.x / LPV;
+  float sg[E];
+#pragma unroll
+  for (int i = 0; i < E; ++i) sg[i] = signs[lane * E + i];
+
+  for (int64_t v = (int64_t)blockIdx.x * GPB + grp; v < n; v += (int64_t)gridDim.x * GPB) {
+    uint32_t c[E];
+    unpack_load<E, BITS>(packed + v * PD, lane, c);
+    const float nrm = f16_bits_to_f32(norms[v]);
+    float y[E];
+#pragma unroll
+    for (int i = 0; i < E; ++i) y[i] = slev[c[i]] * nrm;
+    fwht_lanes<E, LPV>(y, lane);
+#pragma unroll
+    for (int i = 0; i < E; ++i) y[i] = (y[i] * scale) * sg[i];
+    store_elems<OT, E>(out, v * D + lane * E, y);
+  }
+}
+
+template <int D, int IT, int OT>
+__global__ __launch_bounds__(256) void rht_kernel(const void* __restrict__ x, int64_t n,
+                                                  const float* __restrict__ signs, float scale,
+                                                  int inverse, void* __restrict__ out) {
+  using S = CodecShape<D>;
+  constexpr int E = S::E, LPV = S::LPV, GPB = S::GPB;
+  const int lane = threadIdx.x % LPV;
+  const int grp = threadIdx.x / LPV;
+  float sg[E];
+#pragma unroll
+  for (int i = 0; i < E; ++i) sg[i] = signs[lane * E + i];
+  for (int64_t v = (int64_t)blockIdx.x * GPB + grp; v < n; v += (int64_t)gridDim.x * GPB) {
+    float y[E];
+    load_elems<IT, E>(x, v * D + lane * E, y);
+    if (!inverse) {
+#pragma unroll
+      for (int i = 0; i < E; ++i) y[i] *= sg[i];
+    }
+    fwht_lanes<E, LPV>(y, lane);
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+      y[i] *= scale;
+      if (inverse) y[i] *= sg[i];
+    }
+    store_elems<OT, E>(out, v * D + lane * E, y);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+
+float fwht_scale(int d) { return (float)std::pow((double)d, -0.5); }
+
+int codec_grid(int64_t n, int gpb) {
+  int64_t want = (n + gpb - 1) / gpb;
+  const int64_t cap = 256 * 16;  // 16 workgroups per CU on 256 CUs
+  if (want > cap) want = cap;
+  if (want < 1) want = 1;
+  return (int)want;
+}
+
+template <int D, int BITS>
+static hipError_t launch_encode_db(const void* x, int dt, int64_t n, const float* signs,
+                                   const float* bnd, uint8_t* packed, uint16_t* norms,
+                                   hipStream_t st) {
+  using S = CodecShape<D>;
+  dim3 grid(codec_grid(n, S::GPB)), block(256);
+  const float sc = fwht_scale(D);
+  if (dt == F32) encode_kernel<D, BITS, F32><<<grid, block, 0, st>>>(x, n, signs, bnd, sc, packed, norms);
+  else if (dt == F16) encode_kernel<D, BITS, F16><<<grid, block, 0, st>>>(x, n, signs, bnd, sc, packed, norms);
+  else encode_kernel<D, BITS, BF16><<<grid, block, 0, st>>>(x, n, signs, bnd, sc, packed, norms);
+  return hipGetLastError();
+}
+
+template <int D>
+static hipError_t launch_encode_d(const void* x, int dt, int64_t n, const float* signs,
+                                  const float* bnd, int bits, uint8_t* packed, uint16_t* norms,
+                                  hipStream_t st) {
+  if (bits == 2) return launch_encode_db<D, 2>(x, dt, n, signs, bnd, packed, norms, st);
+  if (bits == 3) return launch_encode_db<D, 3>(x, dt, n, signs, bnd, packed, norms, st);
+  return launch_encode_db<D, 4>(x, dt, n, signs, bnd, packed, norms, st);
+}
+
+template <int D, int BITS>
+static hipError_t launch_decode_db(const uint8_t* packed, const uint16_t* norms, int64_t n,
+                                   const float* lev, const float* signs, void* out, int ot,
+                                   hipStream_t st) {
+  using S = CodecShape<D>;
+  dim3 grid(codec_grid(n, S::GPB)), block(256);
+  const float sc = fwht_scale(D);
+  if (ot == F32) decode_kernel<D, BITS, F32><<<grid, block, 0, st>>>(packed, norms, n, lev, signs, sc, out);
+  else if (ot == F16) decode_kernel<D, BITS, F16><<<grid, block, 0, st>>>(packed, norms, n, lev, signs, sc, out);
+  else decode_kernel<D, BITS, BF16><<<grid, block, 0, st>>>(packed, norms, n, lev, signs, sc, out);
+  return hipGetLastError();
+}
+
+template <int D>
+static hipError_t launch_decode_d(const uint8_t* packed, const uint16_t* norms, int64_t n,
+                                  const float* lev, const float* signs, int bits, void* out, int ot,
+                                  hipStream_t st) {
+  if (bits == 2) return launch_decode_db<D, 2>(packed, norms, n, lev, signs, out, ot, st);
+  if (bits == 3) return launch_decode_db<D, 3>(packed, norms, n, lev, signs, out, ot, st);
+  return launch_decode_db<D, 4>(packed, norms, n, lev, signs, out, ot, st);
+}
+
+template <int D, int IT>
+static hipError_t launch_rht_di(const void* x, int64_t n, const float* signs, int inverse,
+                                void* out, int ot, hipStream_t st) {
+  using S = CodecShape<D>;
+  dim3 grid(codec_grid(n, S::GPB)), block(256);
+  const float sc = fwht_scale(D);
+  if (ot == F32) rht_kernel<D, IT, F32><<<grid, block, 0, st>>>(x, n, signs, sc, inverse, out);
+  else if (ot == F16) rht_kernel<D, IT, F16><<<grid, block, 0, st>>>(x, n, signs, sc, inverse, out);
+  else rht_kernel<D, IT, BF16><<<grid, block, 0, st>>>(x, n, signs, sc, inverse, out);
+  return hipGetLastError();
+}
+
+template <int D>
+static hipError_t launch_rht_d(const void* x, int it, int64_t n, const float* signs, int inverse,
+                               void* out, int ot, hipStream_t st) {
+  if (it == F32) return launch_rht_di<D, F32>(x, n, signs, inverse, out, ot, st);
+  if (it == F16) return launch_rht_di<D, F16>(x, n, signs, inverse, out, ot, st);
+  return launch_rht_di<D, BF16>(x, n, signs, inverse, out, ot, st);
+}
+
+}  // namespace ftq
+
+using namespace ftq;
+
+extern "C" int ftq_encode(const void* x, int x_dtype, int64_t n, int d, const float* signs,
+                          const float* boundaries, int bits, uint8_t* packed_out,
+                          uint16_t* norms_out, void* stream) {
+  FTQ_REQUIRE(n >= 0, "n must be >= 0");
+  FTQ_REQUIRE(d == 64 || d == 128 || d == 256, "head_dim must be 64, 128 or 256");
+  FTQ_REQUIRE(bits >= 2 && bits <= 4, "bits must be 2, 3, or 4");
+  FTQ_REQUIRE(x_dtype >= F32 && x_dtype <= BF16, "x_dtype must be FTQ_F32, FTQ_F16 or FTQ_BF16");
+  if (n == 0) return FTQ_OK;
+  FTQ_REQUIRE(x && signs && boundaries && packed_out && norms_out, "null pointer argument");
+  FTQ_REQUIRE(aligned16(x), "x must be 16-byte aligned");
+  FTQ_REQUIRE(aligned4(packed_out), "packed_out must be 4-byte aligned");
+  hipStream_t st = (hipStream_t)stream;
+  hipError_t e;
+  if (d == 64) e = launch_encode_d<64>(x, x_dtype, n, signs, boundaries, bits, packed_out, norms_out, st);
+  else if (d == 128) e = launch_encode_d<128>(x, x_dtype, n, signs, boundaries, bits, packed_out, norms_out, st);
+  else e = launch_encode_d<256>(x, x_dtype, n, signs, boundaries, bits, packed_out, norms_out, st);
+  return hip_status(e);
+}
+
+extern "C" int ftq_decode(const uint8_t* packed, const uint16_t* norms, int64_t n, int d,
+                          const float* levels, const float* signs, int bits, void* out,
+                          int out_dtype, void* stream) {
+  FTQ_REQUIRE(n >= 0, "n must be >= 0");
+  FTQ_REQUIRE(d == 64 || d == 128 || d == 256, "head_dim must be 64, 128 or 256");
+  FTQ_REQUIRE(bits >= 2 && bits <= 4, "bits must be 2, 3, or 4");
+  FTQ_REQUIRE(out_dtype >= F32 && out_dtype <= BF16, "out_dtype must be FTQ_F32, FTQ_F16 or FTQ_BF16");
+  if (n == 0) return FTQ_OK;
+  FTQ_REQUIRE(packed && norms && levels && signs && out, "null pointer argument");
+  FTQ_REQUIRE(aligned16(out), "out must be 16-byte aligned");
+  FTQ_REQUIRE(aligned4(packed), "packed must be 4-byte aligned");
+  hipStream_t st = (hipStream_t)stream;
+  hipError_t e;
+  if (d == 64) e = launch_decode_d<64>(packed, norms, n, levels, signs, bits, out, out_dtype, st);
+  else if (d == 128) e = launch_decode_d<128>(packed, norms, n, levels, signs, bits, out, out_dtype, st);
+  else e = launch_decode_d<256>(packed, norms, n, levels, signs, bits, out, out_dtype, st);
+  return hip_status(e);
+}
+
+extern "C" int ftq_rht(const void* x, int x_dtype, int64_t n, int d, const float* signs,
+                       int inverse, void* out, int out_dtype, void* stream) {
+  FTQ_REQUIRE(n >= 0, "n must be >= 0");
+  FTQ_REQUIRE(d == 64 || d == 128 || d == 256, "head_dim must be 64, 128 or 256");
+  FTQ_REQUIRE(x_dtype >= F32 && x_dtype <= BF16 && out_dtype >= F32 && out_dtype <= BF16,
+              "dtype must be FTQ_F32, FTQ_F16 or FTQ_BF16");
+  if (n == 0) return FTQ_OK;
+  FTQ_REQUIRE(x && signs && out, "null pointer argument");
+  FTQ_REQUIRE(aligned16(x) && aligned16(out), "x and out must be 16-byte aligned");
+  hipStream_t st = (hipStream_t)stream;
+  hipError_t e;
+  if (d == 64) e = launch_rht_d<64>(x, x_dtype, n, signs, inverse, out, out_dtype, st);
+  else if (d == 128) e = launch_rht_d<128>(x, x_dtype, n, signs, inverse, out, out_dtype, st);
+  else e = launch_rht_d<256>(x, x_dtype, n, signs, inverse, out, out_dtype, st);
+  return hip_status(e);
+}
