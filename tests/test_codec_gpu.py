@@ -1,0 +1,146 @@
+"""Parity of the gfx950 encode / decode / RHT kernels with the CPU oracle.
+
+Codes must be bit-identical except at codebook-boundary ties (the GPU and
+oracle norms can differ in the last bit, which moves u by ~1 ulp); the tie
+count is printed.  Norms: fp16 within 1e-3 relative.  Decode and RHT:
+bit-identical (same butterfly pairs and stage order as the oracle).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import tq_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+TIE = 2e-6  # |u - boundary| below this counts as a boundary tie
+
+
+def _mk(n, d, dtype, seed, outliers=False):
+    g = torch.Generator().manual_seed(seed)
+    scales = torch.exp(0.5 * torch.randn(d, generator=g))
+    x = torch.randn(n, d, generator=g) * scales
+    if outliers:
+        x[:, :: d // 4] *= 10
+    return x.to(dtype)
+
+
+def _check_encode(tq, x_cpu, ct, bits, d, label):
+    xs = x_cpu.float().numpy()
+    s = tq.rotation.signs.cpu().numpy()
+    bnd = tq.quantizer.boundaries.cpu().numpy()
+    p_ref, n_ref, u_ref, _ = O.encode(xs, s, bnd, bits)
+    got = ct.indices.cpu().numpy().reshape(-1, d * bits // 8)
+    codes = O.unpack(got, bits, d)
+    codes_ref = O.unpack(p_ref.reshape(-1, d * bits // 8), bits, d)
+    diff = codes != codes_ref
+    ties = int(diff.sum())
+    if ties:
+        dist = O.boundary_distance(u_ref.reshape(-1, d), bnd)[diff]
+        assert dist.max() < TIE, f"{label}: code mismatch {dist.max():.3g} away from a boundary"
+        assert np.all(np.abs(codes.astype(int) - codes_ref.astype(int))[diff] == 1)
+    nn = ct.norms.cpu().numpy().reshape(-1).astype(np.float32)
+    nr = n_ref.reshape(-1).astype(np.float32)
+    assert np.all(np.abs(nn - nr) <= 1e-3 * np.abs(nr) + 1e-7), f"{label}: norm mismatch"
+    print(f"[{label}] vectors={codes.shape[0]} code_ties={ties}")
+    return ties
+
+
+@pytest.mark.parametrize("d", [64, 128, 256])
+@pytest.mark.parametrize("bits", [2, 3, 4])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_encode_decode_parity(cuda, d, bits, dtype):
+    from fused_turboquant import TurboQuantMSE
+    tq = TurboQuantMSE(d, bits=bits, seed=42, device=cuda)
+    x = _mk(2053, d, dtype, seed=d * 10 + bits)  # ragged count: not a multiple of any group size
+    x[0] = 0
+    x[1] = 1
+    ct = tq.encode(x.to(cuda))
+    _check_encode(tq, x, ct, bits, d, f"d={d} bits={bits} {dtype}")
+    dec = tq.decode(ct).cpu().numpy()
+    ref = O.decode(ct.indices.cpu().numpy(), ct.norms.cpu().numpy(),
+                   tq.quantizer.levels.cpu().numpy(), tq.rotation.signs.cpu().numpy(), bits, d)
+    assert np.array_equal(dec, ref)
+    for odt in (torch.bfloat16, torch.float16):
+        dh = tq.decode(ct, out_dtype=odt).float().cpu().numpy()
+        assert np.allclose(dh, ref, rtol=1e-2, atol=1e-3)
+
+
+@pytest.mark.parametrize("d", [64, 128, 256])
+@pytest.mark.parametrize("bits", [2, 3, 4])
+def test_encode_matches_reference_golden(cuda, golden, d, bits):
+    from fused_turboquant import TurboQuantMSE
+    enc = golden["encode"]
+    key = f"{d}_{bits}"
+    x = torch.from_numpy(enc["x_" + key].view(np.int16)).view(torch.bfloat16)
+    tq = TurboQuantMSE(d, bits=bits, seed=42, device=cuda)
+    ct = tq.encode(x.to(cuda))
+    codes = O.unpack(ct.indices.cpu().numpy(), bits, d)
+    ref = O.unpack(enc["packed_" + key], bits, d)
+    diff = codes != ref
+    if diff.any():
+        assert O.boundary_distance(enc["u_" + key], tq.quantizer.boundaries.cpu().numpy())[diff].max() < TIE
+    assert np.allclose(ct.norms.cpu().numpy().astype(np.float32),
+                       enc["norms_" + key].view(np.float16).astype(np.float32), rtol=1e-3)
+    dec = tq.decode(ct).cpu().numpy()
+    if not diff.any() and np.array_equal(ct.norms.cpu().numpy().view(np.uint16), enc["norms_" + key]):
+        assert np.array_equal(dec, enc["dec_" + key])
+
+
+def test_config1_outliers_4bit(cuda, golden):
+    from fused_turboquant import TurboQuantMSE
+    enc = golden["encode"]
+    x = torch.from_numpy(enc["x_cfg1"].view(np.int16)).view(torch.bfloat16)
+    tq = TurboQuantMSE(128, bits=4, seed=0, device=cuda)
+    ct = tq.encode(x.to(cuda))
+    assert np.array_equal(ct.indices.cpu().numpy(), enc["packed_cfg1"])
+    assert np.array_equal(ct.norms.cpu().numpy().view(np.uint16), enc["norms_cfg1"])
+    assert np.array_equal(tq.decode(ct).cpu().numpy(), enc["dec_cfg1"])
+
+
+@pytest.mark.parametrize("d", [64, 128, 256])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_rht_forward_inverse(cuda, d, dtype):
+    from fused_turboquant.core.hadamard import (fwht, generate_rht_signs, inverse_randomized_hadamard,
+                                                randomized_hadamard)
+    x = _mk(333, d, dtype, seed=5)
+    s = generate_rht_signs(d, 7)
+    y = randomized_hadamard(x.to(cuda), s.to(cuda)).cpu().numpy()
+    assert np.array_equal(y, O.rht(x.float().numpy(), s.numpy()))
+    z = inverse_randomized_hadamard(torch.from_numpy(y).to(cuda), s.to(cuda)).cpu().numpy()
+    assert np.array_equal(z, O.inverse_rht(y, s.numpy()))
+    assert np.array_equal(fwht(x.to(cuda)).cpu().numpy(), O.fwht(x.float().numpy()))
+
+
+def test_small_and_empty_batches(cuda):
+    from fused_turboquant import TurboQuantMSE
+    tq = TurboQuantMSE(128, bits=3, device=cuda)
+    for n in (0, 1, 3, 15, 17):
+        x = _mk(max(n, 1), 128, torch.bfloat16, seed=n)[:n]
+        ct = tq.encode(x.to(cuda))
+        assert ct.indices.shape == (n, 48) and ct.norms.shape == (n,)
+        if n:
+            _check_encode(tq, x, ct, 3, 128, f"n={n}")
+        assert tq.decode(ct).shape == (n, 128)
+
+
+@pytest.mark.parametrize("d", [128, 256])
+def test_config2_full_size_parity(cuda, d):
+    """Config 2 at full size: [32768, 8, d] bf16, per-channel lognormal(0, 0.5) scales."""
+    from fused_turboquant import TurboQuantMSE
+    g = torch.Generator().manual_seed(0)
+    sc = torch.exp(0.5 * torch.randn(d, generator=torch.Generator().manual_seed(1)))
+    x = (torch.randn(32768, 8, d, generator=g) * sc).to(torch.bfloat16)
+    tq = TurboQuantMSE(d, bits=3, seed=42, device=cuda)
+    ct = tq.encode(x.to(cuda))
+    assert ct.indices.shape == (32768, 8, d * 3 // 8)
+    ties = _check_encode(tq, x.reshape(-1, d), ct, 3, d, f"config2 d={d}")
+    assert ties <= 64
+    dec = tq.decode(ct)
+    # round trip quality (reference tests/test_quantizer.py:55-79 thresholds)
+    cos = torch.nn.functional.cosine_similarity(dec.cpu().reshape(-1, d), x.float().reshape(-1, d), dim=-1)
+    assert cos.mean() > 0.95
+    # idempotence: re-encoding the decoded vectors reproduces the codes (up to ties)
+    ct2 = tq.encode(dec)
+    same = (ct2.indices == ct.indices).float().mean().item()
+    assert same > 0.99

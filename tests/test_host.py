@@ -1,0 +1,97 @@
+"""Host-side logic and the C ABI surface, without a GPU."""
+import ctypes
+import glob
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import ROOT
+
+
+def _built_lib():
+    from fused_turboquant import _lib
+    if not os.path.exists(_lib.LIB_PATH):
+        import __graft_entry__
+        __graft_entry__.build()
+    return _lib
+
+
+def _declared_symbols():
+    names = set()
+    for h in glob.glob(os.path.join(ROOT, "include", "*.h")):
+        txt = open(h).read()
+        txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+        names |= set(re.findall(r"\b(ftq_\w+)\s*\(", txt))
+    return sorted(names)
+
+
+def test_header_declares_entry_points():
+    names = _declared_symbols()
+    for must in ("ftq_encode", "ftq_decode", "ftq_rht", "ftq_last_error", "ftq_version"):
+        assert must in names
+
+
+def test_library_exports_every_declared_symbol():
+    L = _built_lib().lib()
+    for name in _declared_symbols():
+        assert hasattr(L, name), f"{name} declared in include/ but not exported"
+    assert L.ftq_version() == 1
+
+
+def test_argument_errors_raise_without_touching_the_gpu():
+    _lib = _built_lib()
+    L = _lib.lib()
+    rc = L.ftq_encode(None, 2, 4, 100, None, None, 3, None, None, None)
+    assert rc == -1 and b"head_dim" in L.ftq_last_error()
+    rc = L.ftq_encode(None, 2, 4, 128, None, None, 5, None, None, None)
+    assert rc == -1 and b"bits" in L.ftq_last_error()
+    with pytest.raises(ValueError, match="head_dim"):
+        _lib.check(L.ftq_decode(None, None, 4, 96, None, None, 3, None, 0, None))
+    assert L.ftq_encode(None, 2, 0, 128, None, None, 3, None, None, None) == 0  # empty input
+
+
+@pytest.mark.parametrize("d", [64, 128, 256])
+@pytest.mark.parametrize("bits", [1, 2, 3, 4])
+def test_product_codebook_matches_reference(golden, d, bits):
+    from fused_turboquant.core.lloyd_max import compute_lloyd_max_codebook
+    b, l = compute_lloyd_max_codebook(d, bits)
+    assert np.array_equal(b, golden["codebooks"][f"b_{d}_{bits}"])
+    assert np.array_equal(l, golden["codebooks"][f"l_{d}_{bits}"])
+
+
+@pytest.mark.parametrize("d", [64, 128, 256])
+@pytest.mark.parametrize("seed", [0, 1, 42])
+def test_signs_match_reference(golden, d, seed):
+    from fused_turboquant.core.hadamard import generate_rht_signs
+    assert np.array_equal(generate_rht_signs(d, seed).numpy(), golden["signs"][f"s_{d}_{seed}"])
+
+
+def test_cpu_tensors_are_rejected():
+    from fused_turboquant import TurboQuantMSE
+    from fused_turboquant._lib import FusedTQError
+    tq = TurboQuantMSE(128, bits=3)
+    with pytest.raises(FusedTQError, match="ROCm"):
+        tq.encode(torch.zeros(4, 128))
+
+
+def test_quantizer_validation():
+    from fused_turboquant import TurboQuantMSE
+    with pytest.raises(ValueError, match="power of 2"):
+        TurboQuantMSE(100)
+    with pytest.raises(ValueError, match="bits"):
+        TurboQuantMSE(128, bits=5)
+
+
+def test_torch_packers_match_oracle():
+    from fused_turboquant.core import packing as P
+    from oracle import tq_oracle as O
+    rng = np.random.default_rng(0)
+    for bits, pk, up in ((4, P.pack_nibbles, P.unpack_nibbles), (3, P.pack_3bit, P.unpack_3bit),
+                         (2, P.pack_2bit, P.unpack_2bit)):
+        c = rng.integers(0, 1 << bits, (7, 128)).astype(np.uint8)
+        p = pk(torch.from_numpy(c)).numpy()
+        assert np.array_equal(p, O.pack(c, bits))
+        assert np.array_equal(up(torch.from_numpy(p), 128).numpy(), c)
