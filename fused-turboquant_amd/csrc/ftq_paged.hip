@@ -1,0 +1,641 @@
+// Paged library-format KV cache on gfx950: fused store (encode + scatter) and
+// split-K decode attention computed directly over the packed codes.
+//
+// Semantics: decode attention of the library format, i.e.
+//   q_rot = RHT_K(q);  s_t = ||k_t||_16 * <q_rot, C_K[idx_t]> * scale
+//   o = RHT_V^-1( sum_t softmax(s)_t * ||v_t||_16 * C_V[vidx_t] )
+// == softmax(q . K^T * scale) . V with K, V the decoded cache
+// (reference vllm_plugin/attention_impl.py:431-521 for the paged semantics,
+// kernels/triton_flash_decode.py:66-221 for the fused rotated-domain form).
+//
+// HBM layout (this library's page format; the reference's paged format for
+// this codec is the Python v0 slot [2, nb, bs, Hkv, packed + fp32 norm],
+// vllm_plugin/cache_ops.py:64-108):
+//   kv_cache[num_blocks][Hkv][page_size/16][SUB] bytes, where one 16-token
+//   sub-block of one kv head holds
+//     K codes  [16 tokens][D*BK/8]   per-token packed, reference bit layout
+//     V codes  [64 lanes][D*BV/32]   "lane-major": chunk (q, r) holds, for each
+//              d-block b = 0..D/16-1, the codes of tokens 4q..4q+3 at
+//              d = 16b + r, token i at bit (4b + i) * BV
+//     K norms  [16] fp16, V norms [16] fp16
+//   The V order is the operand order of the P.V MFMA below, so a lane's V
+//   operand for a whole sub-block is one contiguous D*BV/32-byte load.
+//
+// Decode attention kernel: one workgroup (4 waves) per (batch, kv head,
+// split); each wave walks 32-token tiles (two sub-blocks) of its split.
+//   S^T[t][h] = K[t][:] . Q^T[:][h]  : v_mfma_f32_16x16x32_f16, A = K codes
+//               turned into f16 pairs by a pair lookup table, B = rotated
+//               query of the GQA group (columns h >= G are zero)
+//   O^T[d][h] += V^T[d][t] . P'^T[t][h] : same MFMA, A = V codes (lane-major
+//               layout), B = softmax weights * ||v_t|| kept in registers from
+//               the S^T output (no shuffle: the k-slot order of the P.V MFMA
+//               is chosen to be the row order of the S^T output).
+// Online softmax in the log2 domain (scale * log2 e folded into q).  Waves
+// merge through LDS; splits merge in a second kernel that also applies the
+// inverse RHT of V and writes the output dtype.
+#include "ftq_codec_dev.h"
+#include "ftq_internal.h"
+
+#include <cmath>
+
+namespace ftq {
+
+template <int D, int BK, int BV> struct PagedGeom {
+  static constexpr int KTOK = D * BK / 8;   // K code bytes per token
+  static constexpr int KSEC = 16 * KTOK;    // K codes of one sub-block
+  static constexpr int KLANE = KTOK / 4;    // K bytes one lane reads per sub-block
+  static constexpr int VLANE = D * BV / 32; // V bytes of one lane chunk
+  static constexpr int VSEC = 64 * VLANE;
+  static constexpr int KNORM = KSEC + VSEC;
+  static constexpr int VNORM = KNORM + 32;
+  static constexpr int SUB = VNORM + 32;    // bytes per (sub-block, kv head)
+  static constexpr int NS = D / 32;         // Q.K MFMAs per sub-block
+  static constexpr int NB = D / 16;         // P.V MFMAs per tile (d-blocks)
+  static_assert(KLANE % 4 == 0 && VLANE % 4 == 0, "lane chunks must be dword multiples");
+};
+
+int64_t paged_sub_bytes(int d, int bk, int bv) {
+  return (int64_t)2 * d * (bk + bv) + 64;
+}
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+union Op8 {
+  uint32_t u[4];
+  half8 h;
+};
+
+// bits [P, P+W) of a little-endian multi-dword value (P, W compile-time after unrolling)
+template <int N>
+__device__ __forceinline__ uint32_t bits_at(const uint32_t (&w)[N], int P, int W) {
+  const int i = P >> 5, o = P & 31;
+  uint32_t v = w[i] >> o;
+  if (o + W > 32) v |= w[i + 1] << (32 - o);
+  return v & ((1u << W) - 1u);
+}
+
+template <int NDW>
+__device__ __forceinline__ void load_dwords(const uint8_t* p, uint32_t (&w)[NDW]) {
+  const uint32_t* q = reinterpret_cast<const uint32_t*>(p);
+#pragma unroll
+  for (int i = 0; i < NDW; ++i) w[i] = q[i];
+}
+
+// ---------------------------------------------------------------------------
+// store: encode K and V of n tokens x Hkv heads and scatter into the pages
+// ---------------------------------------------------------------------------
+template <int D, int BK, int BV, int DT>
+__global__ __launch_bounds__(256) void paged_store_kernel(
+    const void* __restrict__ key, const void* __restrict__ value, int64_t n_tokens, int hkv,
+    const float* __restrict__ ksigns, const float* __restrict__ vsigns,
+    const float* __restrict__ kbnd_g, const float* __restrict__ vbnd_g,
+    const int64_t* __restrict__ slot_mapping, uint8_t* __restrict__ cache, int page_size,
+    int64_t num_blocks, float scale) {
+  using Gm = PagedGeom<D, BK, BV>;
+  constexpr int E = D / 16, LPV = 16;
+  __shared__ uint8_t vcode[16][D];
+  const int lane = threadIdx.x & 15;
+  const int grp = threadIdx.x >> 4;
+
+  float kb[(1 << BK) - 1], vb[(1 << BV) - 1];
+#pragma unroll
+  for (int j = 0; j < (1 << BK) - 1; ++j) kb[j] = kbnd_g[j + 1];
+#pragma unroll
+  for (int j = 0; j < (1 << BV) - 1; ++j) vb[j] = vbnd_g[j + 1];
+  float ks[E], vs[E];
+#pragma unroll
+  for (int i = 0; i < E; ++i) {
+    ks[i] = ksigns[lane * E + i];
+    vs[i] = vsigns[lane * E + i];
+  }
+  const int nsub = page_size / 16;
+  const int64_t nvec = n_tokens * hkv * 2;  // (token, head, K|V)
+
+  for (int64_t base = (int64_t)blockIdx.x * 16; base < nvec; base += (int64_t)gridDim.x * 16) {
+    const int64_t gv = base + grp;
+    bool active = gv < nvec;
+    const bool is_v = (gv & 1) != 0;
+    const int64_t th = gv >> 1;
+    const int64_t tok = active ? th / hkv : 0;
+    const int head = active ? (int)(th % hkv) : 0;
+    const int64_t slot = active ? slot_mapping[tok] : -1;
+    active = active && slot >= 0 && slot / page_size < num_blocks;
+    uint8_t* sb = nullptr;
+    int tt = 0;
+    if (active) {
+      const int64_t blk = slot / page_size;
+      const int off = (int)(slot % page_size);
+      tt = off & 15;
+      sb = cache + (((blk * hkv + head) * nsub) + (off >> 4)) * (int64_t)Gm::SUB;
+      float y[E];
+      uint32_t c[E];
+      const int64_t eoff = (tok * hkv + head) * D + lane * E;
+      if (!is_v) {
+        load_elems<DT, E>(key, eoff, y);
+        const float nrm = encode_core<E, LPV, BK>(y, ks, kb, scale, lane, c);
+        pack_store<E, BK>(c, sb + tt * Gm::KTOK, lane);
+        if (lane == 0)
+          reinterpret_cast<uint16_t*>(sb + Gm::KNORM)[tt] = (uint16_t)f32_to_f16_bits(nrm);
+      } else {
+        load_elems<DT, E>(value, eoff, y);
+        const float nrm = encode_core<E, LPV, BV>(y, vs, vb, scale, lane, c);
+#pragma unroll
+        for (int i = 0; i < E; ++i) vcode[grp][lane * E + i] = (uint8_t)c[i];
+        if (lane == 0)
+          reinterpret_cast<uint16_t*>(sb + Gm::VNORM)[tt] = (uint16_t)f32_to_f16_bits(nrm);
+      }
+    }
+    __syncthreads();
+    if (active && is_v) {
+      // lane r owns chunk (q = tt/4, r): this token's code for d = 16b + r sits at
+      // bit (4b + tt%4) * BV.  Other tokens share the chunk's dwords, so clear and
+      // set only this token's bits with atomics (correct for any slot mapping).
+      constexpr int NDW = Gm::VLANE / 4;
+      uint32_t v0[NDW], m0[NDW];  // this token's bits as if it were token 0 of its quad
+#pragma unroll
+      for (int w = 0; w < NDW; ++w) { v0[w] = 0; m0[w] = 0; }
+#pragma unroll
+      for (int b = 0; b < D / 16; ++b) {
+        const uint32_t code = vcode[grp][16 * b + lane];
+        const int P = 4 * b * BV;  // compile-time after unrolling; fields never straddle here
+        v0[P >> 5] |= code << (P & 31);
+        m0[P >> 5] |= ((1u << BV) - 1u) << (P & 31);
+      }
+      // move to token (tt % 4): shift the whole chunk left by (tt % 4) * BV bits
+      const int sh = (tt & 3) * BV;
+      uint32_t val[NDW], msk[NDW];
+#pragma unroll
+      for (int w = 0; w < NDW; ++w) {
+        const uint64_t vv = ((uint64_t)v0[w] << 32) | (w ? v0[w - 1] : 0u);
+        const uint64_t mm = ((uint64_t)m0[w] << 32) | (w ? m0[w - 1] : 0u);
+        val[w] = (uint32_t)((vv << sh) >> 32);
+        msk[w] = (uint32_t)((mm << sh) >> 32);
+      }
+      uint32_t* chunk = reinterpret_cast<uint32_t*>(sb + Gm::KSEC + ((tt >> 2) * 16 + lane) * Gm::VLANE);
+#pragma unroll
+      for (int w = 0; w < NDW; ++w) {
+        if (msk[w]) {
+          atomicAnd(chunk + w, ~msk[w]);
+          atomicOr(chunk + w, val[w]);
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------
+// decode attention, stage 1 (per split)
+// ---------------------------------------------------------------------------
+template <int D, int BK, int BV>
+struct TileRegs {
+  using Gm = PagedGeom<D, BK, BV>;
+  uint32_t k[2][Gm::KLANE / 4];
+  uint32_t v[2][Gm::VLANE / 4];
+  uint32_t kn[2][2];  // 4 fp16 K norms per sub-block (tokens 4q..4q+3)
+  uint32_t vn[2][2];
+};
+
+template <int D, int BK, int BV>
+__device__ __forceinline__ void load_tile(TileRegs<D, BK, BV>& r, const uint8_t* __restrict__ cache,
+                                          const int32_t* __restrict__ bt_row, int tile, int seq_len,
+                                          int page_size, int nsub, int hkv, int kvh, int lane,
+                                          int max_blocks, int64_t num_blocks) {
+  using Gm = PagedGeom<D, BK, BV>;
+  const int t = lane & 15, q = lane >> 4;
+#pragma unroll
+  for (int sb = 0; sb < 2; ++sb) {
+    const int tok0 = tile * 32 + sb * 16;
+    const int page = tok0 / page_size;
+    const int64_t phys = (tok0 < seq_len && page < max_blocks) ? (int64_t)bt_row[page] : -1;
+    if (phys >= 0 && phys < num_blocks) {
+      const int sub = (tok0 % page_size) >> 4;
+      const uint8_t* base = cache + ((phys * hkv + kvh) * nsub + sub) * (int64_t)Gm::SUB;
+      load_dwords(base + t * Gm::KTOK + q * Gm::KLANE, r.k[sb]);
+      load_dwords(base + Gm::KSEC + lane * Gm::VLANE, r.v[sb]);
+      load_dwords(base + Gm::KNORM + q * 8, r.kn[sb]);
+      load_dwords(base + Gm::VNORM + q * 8, r.vn[sb]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < Gm::KLANE / 4; ++i) r.k[sb][i] = 0;
+#pragma unroll
+      for (int i = 0; i < Gm::VLANE / 4; ++i) r.v[sb][i] = 0;
+      r.kn[sb][0] = r.kn[sb][1] = r.vn[sb][0] = r.vn[sb][1] = 0;
+    }
+  }
+}
+
+__device__ __forceinline__ float warp_max_q(float x) {
+  x = fmaxf(x, __shfl_xor(x, 16));
+  x = fmaxf(x, __shfl_xor(x, 32));
+  return x;
+}
+__device__ __forceinline__ float warp_sum_q(float x) {
+  x += __shfl_xor(x, 16);
+  x += __shfl_xor(x, 32);
+  return x;
+}
+
+template <int D, int BK, int BV, int QT>
+__global__ __launch_bounds__(256) void paged_attn_kernel(
+    const void* __restrict__ query, const uint8_t* __restrict__ cache,
+    const int32_t* __restrict__ block_table, const int32_t* __restrict__ seq_lens, int hq, int hkv,
+    int page_size, int max_blocks, int64_t num_blocks, const float* __restrict__ ksigns,
+    const float* __restrict__ klev, const float* __restrict__ vlev, float qscale, int num_splits,
+    float* __restrict__ ws_o, float* __restrict__ ws_lse) {
+  using Gm = PagedGeom<D, BK, BV>;
+  constexpr int NS = Gm::NS, NB = Gm::NB;
+  constexpr int E = D / 16;
+  const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int G = hq / hkv;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int h = lane & 15, q = lane >> 4;
+
+  __shared__ uint32_t lutK[1 << (2 * BK)];
+  __shared__ uint32_t lutV[1 << (2 * BV)];
+  __shared__ float red_m[4][16], red_l[4][16];
+  // the rotated queries are only read before the tile loop; the wave-merge
+  // buffer reuses their LDS afterwards
+  __shared__ float lds_big[4 * 16 * (D + 1)];
+  _Float16 (*qs)[D + 8] = reinterpret_cast<_Float16 (*)[D + 8]>(lds_big);
+  float (*red_o)[16][D + 1] = reinterpret_cast<float (*)[16][D + 1]>(lds_big);
+
+  // pair lookup tables: entry (lo | hi << B) = f16(C[lo]) | f16(C[hi]) << 16
+  for (int e = tid; e < (1 << (2 * BK)); e += 256)
+    lutK[e] = f32_to_f16_bits(klev[e & ((1 << BK) - 1)]) | (f32_to_f16_bits(klev[e >> BK]) << 16);
+  for (int e = tid; e < (1 << (2 * BV)); e += 256)
+    lutV[e] = f32_to_f16_bits(vlev[e & ((1 << BV) - 1)]) | (f32_to_f16_bits(vlev[e >> BV]) << 16);
+
+  // rotate the G query heads of this kv head: one head per 16 lanes
+  {
+    const int g = tid >> 4, l16 = tid & 15;
+    if (g < G) {
+      float y[E], sg[E];
+      load_elems<QT, E>(query, ((int64_t)b * hq + kvh * G + g) * D + l16 * E, y);
+#pragma unroll
+      for (int i = 0; i < E; ++i) {
+        sg[i] = ksigns[l16 * E + i];
+        y[i] *= sg[i];
+      }
+      fwht_lanes<E, 16>(y, l16);
+      const float sc = (float)(1.0 / __builtin_sqrt((double)D)) * qscale;
+#pragma unroll
+      for (int i = 0; i < E; ++i) qs[g][l16 * E + i] = (_Float16)(y[i] * sc);
+    }
+  }
+  __syncthreads();
+
+  // B operand of the Q.K MFMAs: lane (h, q), MFMA s -> Q[h][q*D/4 + 8s + j]
+  Op8 qb[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      uint32_t w = 0;
+      if (h < G) {
+        const _Float16 a0 = qs[h][q * (D / 4) + 8 * s + 2 * j];
+        const _Float16 a1 = qs[h][q * (D / 4) + 8 * s + 2 * j + 1];
+        w = (uint32_t)__builtin_bit_cast(uint16_t, a0) | ((uint32_t)__builtin_bit_cast(uint16_t, a1) << 16);
+      }
+      qb[s].u[j] = w;
+    }
+  }
+  __syncthreads();  // qs is dead from here on (its LDS becomes red_o)
+
+  const int seq_len = seq_lens[b];
+  const int n_tiles = (seq_len + 31) >> 5;
+  const int tps = (n_tiles + num_splits - 1) / num_splits;
+  const int t_begin = split * tps;
+  const int t_end = min(t_begin + tps, n_tiles);
+  const int nsub = page_size >> 4;
+  const int32_t* bt_row = block_table + (int64_t)b * max_blocks;
+
+  float m_run = -INFINITY, l_run = 0.f;
+  floatx4 acc[NB];
+#pragma unroll
+  for (int i = 0; i < NB; ++i) acc[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  TileRegs<D, BK, BV> cur, nxt;
+  int tile = t_begin + wave;
+  if (tile < t_end) load_tile(nxt, cache, bt_row, tile, seq_len, page_size, nsub, hkv, kvh, lane, max_blocks, num_blocks);
+  for (; tile < t_end; tile += 4) {
+    cur = nxt;
+    if (tile + 4 < t_end) load_tile(nxt, cache, bt_row, tile + 4, seq_len, page_size, nsub, hkv, kvh, lane, max_blocks, num_blocks);
+
+    // ---- scores S^T (rows = tokens 4q+i of each sub-block, column = head h) ----
+    float s[2][4];
+#pragma unroll
+    for (int sb = 0; sb < 2; ++sb) {
+      floatx4 c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int st = 0; st < NS; ++st) {
+        Op8 a;
+#pragma unroll
+        for (int p = 0; p < 4; ++p)
+          a.u[p] = lutK[bits_at(cur.k[sb], (8 * st + 2 * p) * BK, 2 * BK)];
+        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a.h, qb[st].h, c, 0, 0, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t nb = (cur.kn[sb][i >> 1] >> (16 * (i & 1))) & 0xffffu;
+        const int tok = tile * 32 + sb * 16 + 4 * q + i;
+        s[sb][i] = (tok < seq_len) ? c[i] * f16_bits_to_f32(nb) : -INFINITY;
+      }
+    }
+    // ---- online softmax (log2 domain) ----
+    float tmax = fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
+                       fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
+    tmax = warp_max_q(tmax);
+    const float m_new = fmaxf(m_run, tmax);
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+    m_run = m_new;
+    float psum = 0.f;
+    Op8 pb;
+#pragma unroll
+    for (int sb = 0; sb < 2; ++sb) {
+      float pv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float p = __builtin_amdgcn_exp2f(s[sb][i] - m_new);
+        psum += p;
+        const uint32_t nb = (cur.vn[sb][i >> 1] >> (16 * (i & 1))) & 0xffffu;
+        pv[i] = p * f16_bits_to_f32(nb);
+      }
+      pb.u[2 * sb] = f32_to_f16_bits(pv[0]) | (f32_to_f16_bits(pv[1]) << 16);
+      pb.u[2 * sb + 1] = f32_to_f16_bits(pv[2]) | (f32_to_f16_bits(pv[3]) << 16);
+    }
+    l_run = l_run * alpha + psum;
+    // ---- O^T += V^T P'^T ----
+#pragma unroll
+    for (int bb = 0; bb < NB; ++bb) {
+      Op8 a;
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb) {
+        a.u[2 * sb] = lutV[bits_at(cur.v[sb], (4 * bb) * BV, 2 * BV)];
+        a.u[2 * sb + 1] = lutV[bits_at(cur.v[sb], (4 * bb + 2) * BV, 2 * BV)];
+      }
+      acc[bb] *= alpha;
+      acc[bb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a.h, pb.h, acc[bb], 0, 0, 0);
+    }
+  }
+
+  // ---- merge the 4 waves through LDS ----
+  const float l_tot = warp_sum_q(l_run);
+  if (q == 0) {
+    red_m[wave][h] = m_run;
+    red_l[wave][h] = l_tot;
+  }
+#pragma unroll
+  for (int bb = 0; bb < NB; ++bb)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red_o[wave][h][16 * bb + 4 * q + i] = acc[bb][i];
+  __syncthreads();
+
+  const int64_t row0 = ((int64_t)b * hq + kvh * G) * num_splits + split;  // (b, head g=0, split)
+  for (int idx = tid; idx < G * D; idx += 256) {
+    const int g = idx / D, d = idx % D;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) M = fmaxf(M, red_m[w][g]);
+    float L = 0.f, o = 0.f;
+    if (M != -INFINITY) {
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float f = __builtin_amdgcn_exp2f(red_m[w][g] - M);
+        L += f * red_l[w][g];
+        o += f * red_o[w][g][d];
+      }
+    }
+    const int64_t row = row0 + (int64_t)g * num_splits;
+    ws_o[row * D + d] = (L > 0.f) ? o / L : 0.f;
+    if (d == 0) ws_lse[row] = (L > 0.f) ? M + __builtin_log2f(L) : -INFINITY;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// decode attention, stage 2: merge splits + inverse RHT of V + output cast
+// ---------------------------------------------------------------------------
+template <int D, int OT>
+__global__ __launch_bounds__(256) void paged_merge_kernel(const float* __restrict__ ws_o,
+                                                          const float* __restrict__ ws_lse,
+                                                          int64_t rows, int num_splits,
+                                                          const float* __restrict__ vsigns,
+                                                          float scale, void* __restrict__ out) {
+  constexpr int E = D / 16;
+  const int lane = threadIdx.x & 15;
+  const int64_t r = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+  if (r >= rows) return;  // whole 16-lane group exits together
+  float M = -INFINITY;
+  for (int s = 0; s < num_splits; ++s) M = fmaxf(M, ws_lse[r * num_splits + s]);
+  float y[E];
+#pragma unroll
+  for (int i = 0; i < E; ++i) y[i] = 0.f;
+  float W = 0.f;
+  if (M != -INFINITY) {
+    for (int s = 0; s < num_splits; ++s) {
+      const float l = ws_lse[r * num_splits + s];
+      const float w = __builtin_amdgcn_exp2f(l - M);
+      W += w;
+      float x[E];
+      load_elems<F32, E>(ws_o, (r * num_splits + s) * D + lane * E, x);
+#pragma unroll
+      for (int i = 0; i < E; ++i) y[i] = __builtin_fmaf(w, x[i], y[i]);
+    }
+  }
+  const float inv = (W > 0.f) ? 1.f / W : 0.f;
+#pragma unroll
+  for (int i = 0; i < E; ++i) y[i] *= inv;
+  fwht_lanes<E, 16>(y, lane);
+#pragma unroll
+  for (int i = 0; i < E; ++i) y[i] = (y[i] * scale) * vsigns[lane * E + i];
+  store_elems<OT, E>(out, r * D + lane * E, y);
+}
+
+// ---------------------------------------------------------------------------
+// host launchers
+// ---------------------------------------------------------------------------
+float fwht_scale(int d);
+
+template <int D, int BK, int BV>
+static hipError_t launch_store3(const void* k, const void* v, int dt, int64_t n, int hkv,
+                                const float* ks, const float* vs, const float* kb, const float* vb,
+                                const int64_t* slots, uint8_t* cache, int page_size,
+                                int64_t num_blocks, hipStream_t st) {
+  const int64_t nvec = n * hkv * 2;
+  int64_t g = (nvec + 15) / 16;
+  if (g > 256 * 8) g = 256 * 8;
+  const float sc = fwht_scale(D);
+  dim3 grid((unsigned)g), block(256);
+  if (dt == F32)
+    paged_store_kernel<D, BK, BV, F32><<<grid, block, 0, st>>>(k, v, n, hkv, ks, vs, kb, vb, slots, cache, page_size, num_blocks, sc);
+  else if (dt == F16)
+    paged_store_kernel<D, BK, BV, F16><<<grid, block, 0, st>>>(k, v, n, hkv, ks, vs, kb, vb, slots, cache, page_size, num_blocks, sc);
+  else
+    paged_store_kernel<D, BK, BV, BF16><<<grid, block, 0, st>>>(k, v, n, hkv, ks, vs, kb, vb, slots, cache, page_size, num_blocks, sc);
+  return hipGetLastError();
+}
+
+template <int D, int BK>
+static hipError_t launch_store2(int bv, const void* k, const void* v, int dt, int64_t n, int hkv,
+                                const float* ks, const float* vs, const float* kb, const float* vb,
+                                const int64_t* slots, uint8_t* cache, int page_size,
+                                int64_t num_blocks, hipStream_t st) {
+  if (bv == 2) return launch_store3<D, BK, 2>(k, v, dt, n, hkv, ks, vs, kb, vb, slots, cache, page_size, num_blocks, st);
+  if (bv == 3) return launch_store3<D, BK, 3>(k, v, dt, n, hkv, ks, vs, kb, vb, slots, cache, page_size, num_blocks, st);
+  return launch_store3<D, BK, 4>(k, v, dt, n, hkv, ks, vs, kb, vb, slots, cache, page_size, num_blocks, st);
+}
+
+template <int D>
+static hipError_t launch_store1(int bk, int bv, const void* k, const void* v, int dt, int64_t n,
+                                int hkv, const float* ks, const float* vs, const float* kb,
+                                const float* vb, const int64_t* slots, uint8_t* cache,
+                                int page_size, int64_t num_blocks, hipStream_t st) {
+  if (bk == 2) return launch_store2<D, 2>(bv, k, v, dt, n, hkv, ks, vs, kb, vb, slots, cache, page_size, num_blocks, st);
+  if (bk == 3) return launch_store2<D, 3>(bv, k, v, dt, n, hkv, ks, vs, kb, vb, slots, cache, page_size, num_blocks, st);
+  return launch_store2<D, 4>(bv, k, v, dt, n, hkv, ks, vs, kb, vb, slots, cache, page_size, num_blocks, st);
+}
+
+struct AttnArgs {
+  const void* q;
+  int qt;
+  const uint8_t* cache;
+  const int32_t* bt;
+  const int32_t* sl;
+  int B, hq, hkv, page_size, max_blocks;
+  int64_t num_blocks;
+  const float *ks, *vs, *kl, *vl;
+  float qscale;
+  int splits;
+  float *wo, *wl;
+  void* out;
+  int ot;
+};
+
+template <int D, int BK, int BV>
+static hipError_t launch_attn3(const AttnArgs& a, hipStream_t st) {
+  dim3 grid(a.splits, a.hkv, a.B), block(256);
+  if (a.qt == F32)
+    paged_attn_kernel<D, BK, BV, F32><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.hq, a.hkv, a.page_size, a.max_blocks, a.num_blocks, a.ks, a.kl, a.vl, a.qscale, a.splits, a.wo, a.wl);
+  else if (a.qt == F16)
+    paged_attn_kernel<D, BK, BV, F16><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.hq, a.hkv, a.page_size, a.max_blocks, a.num_blocks, a.ks, a.kl, a.vl, a.qscale, a.splits, a.wo, a.wl);
+  else
+    paged_attn_kernel<D, BK, BV, BF16><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.hq, a.hkv, a.page_size, a.max_blocks, a.num_blocks, a.ks, a.kl, a.vl, a.qscale, a.splits, a.wo, a.wl);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int64_t rows = (int64_t)a.B * a.hq;
+  dim3 g2((unsigned)((rows + 15) / 16)), b2(256);
+  const float sc = fwht_scale(D);
+  if (a.ot == F32) paged_merge_kernel<D, F32><<<g2, b2, 0, st>>>(a.wo, a.wl, rows, a.splits, a.vs, sc, a.out);
+  else if (a.ot == F16) paged_merge_kernel<D, F16><<<g2, b2, 0, st>>>(a.wo, a.wl, rows, a.splits, a.vs, sc, a.out);
+  else paged_merge_kernel<D, BF16><<<g2, b2, 0, st>>>(a.wo, a.wl, rows, a.splits, a.vs, sc, a.out);
+  return hipGetLastError();
+}
+
+template <int D, int BK>
+static hipError_t launch_attn2(int bv, const AttnArgs& a, hipStream_t st) {
+  if (bv == 2) return launch_attn3<D, BK, 2>(a, st);
+  if (bv == 3) return launch_attn3<D, BK, 3>(a, st);
+  return launch_attn3<D, BK, 4>(a, st);
+}
+
+template <int D>
+static hipError_t launch_attn1(int bk, int bv, const AttnArgs& a, hipStream_t st) {
+  if (bk == 2) return launch_attn2<D, 2>(bv, a, st);
+  if (bk == 3) return launch_attn2<D, 3>(bv, a, st);
+  return launch_attn2<D, 4>(bv, a, st);
+}
+
+int auto_splits(int batch, int hkv, int seq_hint) {
+  // aim for ~1024 workgroups (4 per CU) with at least 8 tiles per wave
+  const int units = batch * hkv;
+  int s = (1024 + units - 1) / units;
+  const int max_by_len = seq_hint / (32 * 4 * 8);
+  if (s > max_by_len) s = max_by_len;
+  if (s < 1) s = 1;
+  if (s > 64) s = 64;
+  return s;
+}
+
+}  // namespace ftq
+
+using namespace ftq;
+
+extern "C" int64_t ftq_paged_subblock_bytes(int d, int bits_k, int bits_v) {
+  if (!(d == 128 || d == 256) || bits_k < 2 || bits_k > 4 || bits_v < 2 || bits_v > 4) return -1;
+  return paged_sub_bytes(d, bits_k, bits_v);
+}
+
+extern "C" int64_t ftq_paged_workspace_bytes(int batch, int num_q_heads, int d, int num_splits) {
+  if (batch < 0 || num_q_heads < 0 || d <= 0 || num_splits <= 0) return -1;
+  return (int64_t)batch * num_q_heads * num_splits * (d + 1) * 4;
+}
+
+extern "C" int ftq_paged_default_splits(int batch, int num_kv_heads, int max_seq_len) {
+  return auto_splits(batch, num_kv_heads, max_seq_len);
+}
+
+extern "C" int ftq_paged_store(const void* key, const void* value, int dtype, int64_t n_tokens,
+                               int num_kv_heads, int d, const float* k_signs, const float* v_signs,
+                               const float* k_boundaries, const float* v_boundaries, int bits_k,
+                               int bits_v, const int64_t* slot_mapping, uint8_t* kv_cache,
+                               int page_size, int64_t num_blocks, void* stream) {
+  FTQ_REQUIRE(d == 128 || d == 256, "paged cache: head_dim must be 128 or 256");
+  FTQ_REQUIRE(num_blocks >= 0, "num_blocks must be >= 0");
+  FTQ_REQUIRE(bits_k >= 2 && bits_k <= 4 && bits_v >= 2 && bits_v <= 4, "bits must be 2, 3, or 4");
+  FTQ_REQUIRE(page_size >= 16 && page_size % 16 == 0, "page_size must be a multiple of 16");
+  FTQ_REQUIRE(n_tokens >= 0 && num_kv_heads > 0, "bad token / head count");
+  FTQ_REQUIRE(dtype >= F32 && dtype <= BF16, "dtype must be FTQ_F32, FTQ_F16 or FTQ_BF16");
+  if (n_tokens == 0) return FTQ_OK;
+  FTQ_REQUIRE(key && value && k_signs && v_signs && k_boundaries && v_boundaries && slot_mapping && kv_cache,
+              "null pointer argument");
+  FTQ_REQUIRE(aligned16(key) && aligned16(value), "key/value must be 16-byte aligned");
+  FTQ_REQUIRE(aligned16(kv_cache), "kv_cache must be 16-byte aligned");
+  hipStream_t st = (hipStream_t)stream;
+  hipError_t e;
+  if (d == 128)
+    e = launch_store1<128>(bits_k, bits_v, key, value, dtype, n_tokens, num_kv_heads, k_signs, v_signs,
+                           k_boundaries, v_boundaries, slot_mapping, kv_cache, page_size, num_blocks, st);
+  else
+    e = launch_store1<256>(bits_k, bits_v, key, value, dtype, n_tokens, num_kv_heads, k_signs, v_signs,
+                           k_boundaries, v_boundaries, slot_mapping, kv_cache, page_size, num_blocks, st);
+  return hip_status(e);
+}
+
+extern "C" int ftq_paged_decode_attention(
+    const void* query, int q_dtype, const uint8_t* kv_cache, const int32_t* block_table,
+    const int32_t* seq_lens, int batch, int num_q_heads, int num_kv_heads, int d, int page_size,
+    int max_blocks_per_seq, int64_t num_blocks, const float* k_signs, const float* v_signs, const float* k_levels,
+    const float* v_levels, int bits_k, int bits_v, float scale, int num_splits, void* workspace,
+    int64_t workspace_bytes, void* out, int out_dtype, void* stream) {
+  FTQ_REQUIRE(d == 128 || d == 256, "paged attention: head_dim must be 128 or 256");
+  FTQ_REQUIRE(bits_k >= 2 && bits_k <= 4 && bits_v >= 2 && bits_v <= 4, "bits must be 2, 3, or 4");
+  FTQ_REQUIRE(page_size >= 16 && page_size % 16 == 0, "page_size must be a multiple of 16");
+  FTQ_REQUIRE(batch >= 0 && num_kv_heads > 0 && num_q_heads > 0, "bad batch / head counts");
+  FTQ_REQUIRE(num_q_heads % num_kv_heads == 0, "num_q_heads must be a multiple of num_kv_heads");
+  FTQ_REQUIRE(num_q_heads / num_kv_heads <= 16, "GQA group (num_q_heads / num_kv_heads) must be <= 16");
+  FTQ_REQUIRE(num_splits >= 1 && num_splits <= 1024, "num_splits must be in [1, 1024]");
+  FTQ_REQUIRE(max_blocks_per_seq >= 0, "max_blocks_per_seq must be >= 0");
+  FTQ_REQUIRE(q_dtype >= F32 && q_dtype <= BF16 && out_dtype >= F32 && out_dtype <= BF16,
+              "dtype must be FTQ_F32, FTQ_F16 or FTQ_BF16");
+  if (batch == 0) return FTQ_OK;
+  FTQ_REQUIRE(query && kv_cache && block_table && seq_lens && k_signs && v_signs && k_levels &&
+                  v_levels && workspace && out,
+              "null pointer argument");
+  FTQ_REQUIRE(workspace_bytes >= ftq_paged_workspace_bytes(batch, num_q_heads, d, num_splits),
+              "workspace too small (see ftq_paged_workspace_bytes)");
+  FTQ_REQUIRE(aligned16(query) && aligned16(out) && aligned16(workspace) && aligned16(kv_cache),
+              "query, out, workspace and kv_cache must be 16-byte aligned");
+  AttnArgs a;
+  a.q = query; a.qt = q_dtype; a.cache = kv_cache; a.bt = block_table; a.sl = seq_lens;
+  a.B = batch; a.hq = num_q_heads; a.hkv = num_kv_heads; a.page_size = page_size;
+  a.max_blocks = max_blocks_per_seq; a.num_blocks = num_blocks; a.ks = k_signs; a.vs = v_signs; a.kl = k_levels; a.vl = v_levels;
+  a.qscale = scale * 1.4426950408889634f;
+  a.splits = num_splits;
+  a.wo = static_cast<float*>(workspace);
+  a.wl = a.wo + (int64_t)batch * num_q_heads * num_splits * d;
+  a.out = out; a.ot = out_dtype;
+  hipStream_t st = (hipStream_t)stream;
+  hipError_t e = (d == 128) ? launch_attn1<128>(bits_k, bits_v, a, st) : launch_attn1<256>(bits_k, bits_v, a, st);
+  return hip_status(e);
+}

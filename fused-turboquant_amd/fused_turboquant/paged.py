@@ -1,0 +1,258 @@
+"""Paged TurboQuant KV cache (library format) with fused decode attention on gfx950.
+
+The library format is the one ``TurboQuantMSE`` produces (RHT with random
+signs, Lloyd-Max codebook, fp16 norm of the rotated vector; reference
+``core/quantizer.py:137-160``).  This module keeps it in pages addressed by a
+block table, as a vLLM-style paged backend does, and computes decode
+attention straight from the packed codes:
+
+* ``paged_store`` -- encode K and V of new tokens and scatter them to their
+  slots (``slot = block * page_size + offset``; negative slots are skipped,
+  like the reference store, ``vllm_plugin/triton_inkernel_store.py:398-399``).
+* ``paged_decode_attention`` -- one query token per sequence; semantics of the
+  reference's library-format decode (``vllm_plugin/attention_impl.py:431-521``,
+  ``kernels/triton_flash_decode.py:66-221``): softmax(q . K^T * scale) . V over
+  the decoded cache, GQA head h -> kv head h // (Hq / Hkv), positions
+  >= seq_lens[b] masked.
+
+Cache layout: ``uint8[num_blocks, num_kv_heads, page_size // 16, sub_bytes]``
+(see ``csrc/ftq_paged.hip`` for the byte layout of one 16-token sub-block).
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _lib
+from .core.quantizer import TurboQuantMSE
+
+_SIG = {
+    "ftq_paged_store": ["vp", "vp", "i32", "i64", "i32", "i32", "vp", "vp", "vp", "vp", "i32", "i32",
+                        "vp", "vp", "i32", "i64", "vp"],
+    "ftq_paged_decode_attention": ["vp", "i32", "vp", "vp", "vp", "i32", "i32", "i32", "i32", "i32",
+                                   "i32", "i64", "vp", "vp", "vp", "vp", "i32", "i32", "f32", "i32",
+                                   "vp", "i64", "vp", "i32", "vp"],
+}
+
+
+def _bind():
+    import ctypes
+    L = _lib.lib()
+    if getattr(L, "_paged_bound", False):
+        return L
+    m = {"vp": ctypes.c_void_p, "i32": ctypes.c_int, "i64": ctypes.c_int64, "f32": ctypes.c_float}
+    for name, sig in _SIG.items():
+        fn = getattr(L, name)
+        fn.argtypes = [m[t] for t in sig]
+        fn.restype = ctypes.c_int
+    for name in ("ftq_paged_subblock_bytes",):
+        getattr(L, name).restype = ctypes.c_int64
+        getattr(L, name).argtypes = [ctypes.c_int] * 3
+    L.ftq_paged_workspace_bytes.restype = ctypes.c_int64
+    L.ftq_paged_workspace_bytes.argtypes = [ctypes.c_int] * 4
+    L.ftq_paged_default_splits.restype = ctypes.c_int
+    L.ftq_paged_default_splits.argtypes = [ctypes.c_int] * 3
+    L._paged_bound = True
+    return L
+
+
+def subblock_bytes(head_dim: int, bits_k: int, bits_v: int) -> int:
+    """Bytes of one 16-token sub-block of one kv head: 2*d*(bk+bv) + 64."""
+    if head_dim not in (128, 256) or not (2 <= bits_k <= 4) or not (2 <= bits_v <= 4):
+        raise ValueError("paged cache supports head_dim 128/256 and 2/3/4-bit K and V")
+    return 2 * head_dim * (bits_k + bits_v) + 64
+
+
+def cache_shape(num_blocks: int, page_size: int, num_kv_heads: int, head_dim: int,
+                bits_k: int, bits_v: int) -> tuple:
+    if page_size % 16 != 0 or page_size <= 0:
+        raise ValueError("page_size must be a positive multiple of 16")
+    return (num_blocks, num_kv_heads, page_size // 16, subblock_bytes(head_dim, bits_k, bits_v))
+
+
+def paged_store(key: torch.Tensor, value: torch.Tensor, kv_cache: torch.Tensor,
+                slot_mapping: torch.Tensor, k_quant: TurboQuantMSE, v_quant: TurboQuantMSE) -> None:
+    """Encode ``key``/``value`` [n, Hkv, d] and write them to ``slot_mapping`` [n] (int64)."""
+    n, hkv, d = key.shape
+    if value.shape != key.shape:
+        raise ValueError("key and value shapes differ")
+    nb, hk2, nsub, sub = kv_cache.shape
+    if hk2 != hkv or sub != subblock_bytes(d, k_quant.bits, v_quant.bits) or kv_cache.dtype != torch.uint8:
+        raise ValueError("kv_cache shape does not match (num_kv_heads, head_dim, bits)")
+    if slot_mapping.dtype != torch.int64 or slot_mapping.numel() != n:
+        raise ValueError("slot_mapping must be int64 with one entry per token")
+    dev = _lib.require_device(key, value, kv_cache, slot_mapping)
+    k = key.contiguous()
+    v = value.to(k.dtype).contiguous()
+    if k.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+        k, v = k.float(), v.float()
+    L = _bind()
+    _lib.check(L.ftq_paged_store(
+        k.data_ptr(), v.data_ptr(), _lib.dtype_code(k.dtype), n, hkv, d,
+        k_quant.rotation.signs.data_ptr(), v_quant.rotation.signs.data_ptr(),
+        k_quant.quantizer.boundaries.data_ptr(), v_quant.quantizer.boundaries.data_ptr(),
+        k_quant.bits, v_quant.bits, slot_mapping.contiguous().data_ptr(), kv_cache.data_ptr(),
+        nsub * 16, nb, _lib.stream_ptr(dev)))
+
+
+def default_splits(batch: int, num_kv_heads: int, max_seq_len: int) -> int:
+    return int(_bind().ftq_paged_default_splits(batch, num_kv_heads, max_seq_len))
+
+
+def workspace_bytes(batch: int, num_q_heads: int, head_dim: int, num_splits: int) -> int:
+    return int(_bind().ftq_paged_workspace_bytes(batch, num_q_heads, head_dim, num_splits))
+
+
+def paged_decode_attention(query: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.Tensor,
+                           seq_lens: torch.Tensor, k_quant: TurboQuantMSE, v_quant: TurboQuantMSE,
+                           scale: float | None = None, num_splits: int | None = None,
+                           max_seq_len: int | None = None, out: torch.Tensor | None = None,
+                           workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """query [B, Hq, d] -> attention output [B, Hq, d] (query dtype unless ``out`` given).
+
+    ``num_splits`` (split-K factor over the context) defaults to a value that
+    fills the GPU; pass ``max_seq_len`` to size it without a device sync.
+    ``workspace`` (uint8, >= ``workspace_bytes``) may be preallocated for
+    graph capture.
+    """
+    B, hq, d = query.shape
+    nb, hkv, nsub, sub = kv_cache.shape
+    if sub != subblock_bytes(d, k_quant.bits, v_quant.bits):
+        raise ValueError("kv_cache sub-block size does not match (head_dim, bits)")
+    if block_table.dtype != torch.int32 or seq_lens.dtype != torch.int32:
+        raise ValueError("block_table and seq_lens must be int32")
+    if block_table.dim() != 2 or block_table.shape[0] != B or seq_lens.numel() != B:
+        raise ValueError("block_table must be [B, max_blocks] and seq_lens [B]")
+    dev = _lib.require_device(query, kv_cache, block_table, seq_lens)
+    q = query.contiguous()
+    if q.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+        q = q.float()
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    if num_splits is None:
+        msl = max_seq_len if max_seq_len is not None else block_table.shape[1] * nsub * 16
+        num_splits = default_splits(B, hkv, msl)
+    if out is None:
+        out = torch.empty(B, hq, d, dtype=q.dtype, device=dev)
+    need = workspace_bytes(B, hq, d, num_splits)
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=dev)
+    bt = block_table.contiguous()
+    L = _bind()
+    _lib.check(L.ftq_paged_decode_attention(
+        q.data_ptr(), _lib.dtype_code(q.dtype), kv_cache.data_ptr(), bt.data_ptr(),
+        seq_lens.contiguous().data_ptr(), B, hq, hkv, d, nsub * 16, bt.shape[1], nb,
+        k_quant.rotation.signs.data_ptr(), v_quant.rotation.signs.data_ptr(),
+        k_quant.quantizer.levels.data_ptr(), v_quant.quantizer.levels.data_ptr(),
+        k_quant.bits, v_quant.bits, float(scale), int(num_splits), workspace.data_ptr(),
+        workspace.numel(), out.data_ptr(), _lib.dtype_code(out.dtype), _lib.stream_ptr(dev)))
+    return out
+
+
+class PagedTurboQuantCache:
+    """A paged, compressed KV cache of one attention layer.
+
+    K and V get their own ``TurboQuantMSE`` (same seed by default, as
+    ``patch_model`` shares one quantizer per (head_dim, bits) across K and V,
+    reference ``hf/fused_cache.py:1143-1202``).
+    """
+
+    def __init__(self, num_blocks: int, page_size: int, num_kv_heads: int, head_dim: int,
+                 bits_k: int = 3, bits_v: int = 3, seed: int = 42, device="cuda"):
+        self.page_size = page_size
+        self.num_kv_heads = num_kv_heads
+        self.head_dim = head_dim
+        self.k_quant = TurboQuantMSE(head_dim, bits=bits_k, seed=seed, device=device)
+        self.v_quant = TurboQuantMSE(head_dim, bits=bits_v, seed=seed, device=device)
+        self.kv_cache = torch.zeros(cache_shape(num_blocks, page_size, num_kv_heads, head_dim, bits_k, bits_v),
+                                    dtype=torch.uint8, device=device)
+
+    def store(self, key: torch.Tensor, value: torch.Tensor, slot_mapping: torch.Tensor) -> None:
+        paged_store(key, value, self.kv_cache, slot_mapping, self.k_quant, self.v_quant)
+
+    def decode_attention(self, query, block_table, seq_lens, **kw) -> torch.Tensor:
+        return paged_decode_attention(query, self.kv_cache, block_table, seq_lens,
+                                      self.k_quant, self.v_quant, **kw)
+
+
+# --------------------------------------------------------------------------
+# benchmark / smoke helpers (config 3 of the benchmark plan)
+# --------------------------------------------------------------------------
+
+
+def make_config3(dev, B=32, hq=32, hkv=8, d=128, ctx=8192, page=16, bits=3, seed=0):
+    """B sequences of ctx tokens, block table = seeded random permutation of the pages."""
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    pages_per_seq = (ctx + page - 1) // page
+    nblocks = B * pages_per_seq
+    cache = PagedTurboQuantCache(nblocks, page, hkv, d, bits, bits, seed=42, device=dev)
+    perm = torch.randperm(nblocks, generator=g).to(torch.int32)
+    block_table = perm.view(B, pages_per_seq).to(dev)
+    # slots of every (sequence, position) in order
+    pos = torch.arange(ctx, dtype=torch.int64)
+    slots = (block_table.cpu().long()[:, pos // page] * page + (pos % page)).reshape(-1).to(dev)
+    chunk = 1 << 16
+    n = B * ctx
+    for s in range(0, n, chunk):
+        e = min(n, s + chunk)
+        k = torch.randn(e - s, hkv, d, generator=g).to(torch.bfloat16).to(dev)
+        v = torch.randn(e - s, hkv, d, generator=g).to(torch.bfloat16).to(dev)
+        cache.store(k, v, slots[s:e])
+    q = torch.randn(B, hq, d, generator=g).to(torch.bfloat16).to(dev)
+    seq_lens = torch.full((B,), ctx, dtype=torch.int32, device=dev)
+    return cache, q, block_table, seq_lens
+
+
+def bench_setup(dev):
+    B, hq, hkv, d, ctx, page = 32, 32, 8, 128, 8192, 16
+    cache, q, bt, sl = make_config3(dev, B, hq, hkv, d, ctx, page)
+    splits = default_splits(B, hkv, ctx)
+    out = torch.empty(B, hq, d, dtype=torch.bfloat16, device=dev)
+    ws = torch.empty(workspace_bytes(B, hq, d, splits), dtype=torch.uint8, device=dev)
+
+    def run():
+        paged_decode_attention(q, cache.kv_cache, bt, sl, cache.k_quant, cache.v_quant,
+                               num_splits=splits, out=out, workspace=ws)
+
+    kv_bytes = B * ctx * hkv * (subblock_bytes(d, 3, 3) // 16)
+    total = kv_bytes + q.numel() * 2 + out.numel() * 2 + bt.numel() * 4 + sl.numel() * 4
+    return {"run": run, "kv_bytes": kv_bytes, "total_bytes": total, "splits": splits,
+            "cache": cache, "q": q, "bt": bt, "sl": sl, "out": out}
+
+
+def smoke_paged(dev):
+    """Tiny paged store + decode attention checked against the CPU oracle."""
+    import numpy as np
+    from oracle import tq_oracle as O
+    B, hq, hkv, d, page = 2, 8, 2, 128, 16
+    lens = [37, 70]
+    g = torch.Generator().manual_seed(3)
+    nblk = 12
+    cache = PagedTurboQuantCache(nblk, page, hkv, d, 3, 3, device=dev)
+    bt = torch.randperm(nblk, generator=g)[: B * 6].view(B, 6).to(torch.int32)
+    ks, vs = [], []
+    for b in range(B):
+        k = torch.randn(lens[b], hkv, d, generator=g).to(torch.bfloat16)
+        v = torch.randn(lens[b], hkv, d, generator=g).to(torch.bfloat16)
+        pos = torch.arange(lens[b])
+        slots = (bt[b].long()[pos // page] * page + pos % page)
+        cache.store(k.to(dev), v.to(dev), slots.to(dev))
+        ks.append(k)
+        vs.append(v)
+    q = torch.randn(B, hq, d, generator=g).to(torch.bfloat16)
+    out = cache.decode_attention(q.to(dev), bt.to(dev), torch.tensor(lens, dtype=torch.int32, device=dev),
+                                 num_splits=2).float().cpu().numpy()
+    kq, vq = cache.k_quant, cache.v_quant
+    S = max(lens)
+    Kd = np.zeros((B, hkv, S, d))
+    Vd = np.zeros((B, hkv, S, d))
+    for b in range(B):
+        for src, dst, tq in ((ks[b], Kd, kq), (vs[b], Vd, vq)):
+            p, n16, _, _ = O.encode(src.float().numpy(), tq.rotation.signs.cpu().numpy(),
+                                    tq.quantizer.boundaries.cpu().numpy(), 3)
+            dec = O.decode(p, n16, tq.quantizer.levels.cpu().numpy(), tq.rotation.signs.cpu().numpy(), 3, d)
+            dst[b, :, : lens[b]] = dec.transpose(1, 0, 2)
+    ref = O.dense_decode_attention(q.float().numpy(), Kd, Vd, lens, 1.0 / math.sqrt(d))
+    err = np.abs(out - ref)
+    assert err.max() <= 2e-2 and err.mean() <= 2e-3, (err.max(), err.mean())
