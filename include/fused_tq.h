@@ -66,6 +66,56 @@ int ftq_decode(const uint8_t* packed, const uint16_t* norms, int64_t n, int d,
 int ftq_rht(const void* x, int x_dtype, int64_t n, int d, const float* signs, int inverse,
             void* out, int out_dtype, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * Paged library-format KV cache (this library's page format).
+ *
+ * kv_cache: uint8 [num_blocks][num_kv_heads][page_size/16][sub_bytes], one
+ * 16-token sub-block of one kv head = K codes [16][d*bits_k/8] (reference bit
+ * layout) | V codes in MFMA lane order [64][d*bits_v/32] | K norms fp16[16] |
+ * V norms fp16[16].  sub_bytes = 2*d*(bits_k+bits_v) + 64.  d in {128, 256},
+ * page_size a multiple of 16.  A token's slot is block*page_size + offset.
+ * ------------------------------------------------------------------------- */
+int64_t ftq_paged_subblock_bytes(int d, int bits_k, int bits_v);
+
+/*
+ * Encode K and V ([n_tokens][num_kv_heads][d], dtype) with the library
+ * codec and scatter them to slot_mapping[n_tokens] (int64; slots < 0 or in a
+ * block >= num_blocks are skipped).  Replaces the reference's per-token
+ * compressed-slot writes (vllm_plugin/attention_impl.py:217-254 with
+ * cache_ops.py:85-108 write_compressed_to_slot) and the fused v1 store
+ * launch (vllm_plugin/triton_inkernel_store.py:554-616) for this codec.
+ */
+int ftq_paged_store(const void* key, const void* value, int dtype, int64_t n_tokens,
+                    int num_kv_heads, int d, const float* k_signs, const float* v_signs,
+                    const float* k_boundaries, const float* v_boundaries, int bits_k, int bits_v,
+                    const int64_t* slot_mapping, uint8_t* kv_cache, int page_size,
+                    int64_t num_blocks, void* stream);
+
+/* Workspace bytes ftq_paged_decode_attention needs: batch*Hq*splits*(d+1)*4. */
+int64_t ftq_paged_workspace_bytes(int batch, int num_q_heads, int d, int num_splits);
+/* Split-K factor that fills the GPU for this shape (host-side heuristic). */
+int ftq_paged_default_splits(int batch, int num_kv_heads, int max_seq_len);
+
+/*
+ * Decode attention (one query token per sequence) over the paged cache:
+ * out[b][h] = softmax(q[b][h] . K_b^T * scale) . V_b, K/V the decoded cache,
+ * kv head = h / (Hq/Hkv), positions >= seq_lens[b] masked, block_table
+ * [batch][max_blocks_per_seq] int32 physical block ids.  q is RHT-rotated
+ * in-kernel with k_signs; the output is un-rotated with v_signs.
+ * Replaces the library-format decode of the reference
+ * (vllm_plugin/attention_impl.py:431-521: _gather_compressed_k +
+ * randomized_hadamard + fused_qk_scores_rht + softmax + V decode + matmul) and
+ * flash_decode_compressed (kernels/triton_flash_decode.py:224-324).
+ * Two launches on `stream`: split-K stage 1, then merge + inverse RHT.
+ */
+int ftq_paged_decode_attention(const void* query, int q_dtype, const uint8_t* kv_cache,
+                               const int32_t* block_table, const int32_t* seq_lens, int batch,
+                               int num_q_heads, int num_kv_heads, int d, int page_size,
+                               int max_blocks_per_seq, int64_t num_blocks, const float* k_signs,
+                               const float* v_signs, const float* k_levels, const float* v_levels,
+                               int bits_k, int bits_v, float scale, int num_splits, void* workspace,
+                               int64_t workspace_bytes, void* out, int out_dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

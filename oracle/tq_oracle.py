@@ -296,3 +296,46 @@ def lse_merge(parts_o: np.ndarray, parts_lse: np.ndarray):
     den = w.sum(-1)
     o = (w[..., None] * parts_o).sum(-2) / np.where(den > 0, den, 1.0)[..., None]
     return o, (m[..., 0] + np.log(np.where(den > 0, den, 1.0)))
+
+
+# --------------------------------------------------------------------------
+# Page layout reader (checker for the paged store of fused_turboquant.paged)
+# --------------------------------------------------------------------------
+
+
+def paged_unpack(cache: np.ndarray, d: int, bk: int, bv: int):
+    """Read a paged library-format cache uint8[nb, Hkv, nsub, sub] back into
+    per-token arrays: K codes / V codes [nb, Hkv, page, d] (uint8) and K / V
+    norms [nb, Hkv, page] (float16).
+
+    Sub-block layout (16 tokens): K codes [16][d*bk/8] per-token packed;
+    V codes [64 chunks][d*bv/32] where chunk c = 16*q + r holds, for d-block
+    b, the codes of tokens 4q+i (i = 0..3) at d = 16b + r, bit (4b + i)*bv;
+    then K norms fp16[16], V norms fp16[16].
+    """
+    nb, hkv, nsub, sub = cache.shape
+    ktok = d * bk // 8
+    ksec = 16 * ktok
+    vlane = d * bv // 32
+    vsec = 64 * vlane
+    assert sub == ksec + vsec + 64
+    c = cache.reshape(nb, hkv, nsub, sub)
+    kc = unpack(c[..., :ksec].reshape(nb, hkv, nsub, 16, ktok), bk, d)
+    vbytes = c[..., ksec:ksec + vsec].reshape(nb, hkv, nsub, 64, vlane)
+    bits = np.unpackbits(vbytes, axis=-1, bitorder="little").astype(np.uint32)
+    vc = np.zeros((nb, hkv, nsub, 16, d), np.uint8)
+    for q in range(4):
+        for r in range(16):
+            ch = bits[..., 16 * q + r, :]
+            for b in range(d // 16):
+                for i in range(4):
+                    p = (4 * b + i) * bv
+                    code = np.zeros(ch.shape[:-1], np.uint32)
+                    for k in range(bv):
+                        code |= ch[..., p + k] << k
+                    vc[..., 4 * q + i, 16 * b + r] = code
+    kn = c[..., ksec + vsec:ksec + vsec + 32].copy().view(np.float16).reshape(nb, hkv, nsub, 16)
+    vn = c[..., ksec + vsec + 32:].copy().view(np.float16).reshape(nb, hkv, nsub, 16)
+    page = nsub * 16
+    return (kc.reshape(nb, hkv, page, d), vc.reshape(nb, hkv, page, d),
+            kn.reshape(nb, hkv, page), vn.reshape(nb, hkv, page))

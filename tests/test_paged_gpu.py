@@ -1,0 +1,166 @@
+"""Paged library-format store + decode attention on gfx950 vs the CPU oracle.
+
+Store: the codes read back from the pages equal the oracle's encode of the same
+vectors except at codebook-boundary ties; norms fp16 within 1e-3 relative.
+Attention: against float64 dense softmax attention over the oracle's decode of
+the stored codes; max abs error <= 2e-2, mean <= 2e-3 (bf16 tolerance).
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import tq_oracle as O
+
+pytestmark = pytest.mark.gpu
+TIE = 2e-6
+
+
+def _quants(cache):
+    return cache.k_quant, cache.v_quant
+
+
+def _fill(cache, lens, bt, hkv, d, g, dev, dtype=torch.bfloat16):
+    page = cache.page_size
+    ks, vs = [], []
+    for b, L in enumerate(lens):
+        k = torch.randn(L, hkv, d, generator=g).to(dtype)
+        v = torch.randn(L, hkv, d, generator=g).to(dtype)
+        if L:
+            pos = torch.arange(L)
+            slots = bt[b].long()[pos // page] * page + pos % page
+            cache.store(k.to(dev), v.to(dev), slots.to(dev))
+        ks.append(k)
+        vs.append(v)
+    return ks, vs
+
+
+def _decoded(tq, x, bits, d):
+    s = tq.rotation.signs.cpu().numpy()
+    p, n16, u, _ = O.encode(x.float().numpy(), s, tq.quantizer.boundaries.cpu().numpy(), bits)
+    return O.decode(p, n16, tq.quantizer.levels.cpu().numpy(), s, bits, d), p, n16, u
+
+
+@pytest.mark.parametrize("bk,bv", [(3, 3), (4, 2), (2, 4), (4, 4), (2, 2)])
+@pytest.mark.parametrize("page", [16, 32])
+def test_store_layout_parity(cuda, bk, bv, page):
+    from fused_turboquant.paged import PagedTurboQuantCache
+    d, hkv, nblk = 128, 2, 6
+    g = torch.Generator().manual_seed(bk * 10 + bv + page)
+    cache = PagedTurboQuantCache(nblk, page, hkv, d, bk, bv, device=cuda)
+    n = nblk * page - 5  # leave a few slots untouched
+    slots = torch.randperm(nblk * page, generator=g)[:n]
+    slots[3] = -1  # skipped slot
+    k = torch.randn(n, hkv, d, generator=g).to(torch.bfloat16)
+    v = torch.randn(n, hkv, d, generator=g).to(torch.bfloat16)
+    cache.store(k.to(cuda), v.to(cuda), slots.to(cuda))
+    kc, vc, kn, vn = O.paged_unpack(cache.kv_cache.cpu().numpy(), d, bk, bv)
+    ties = 0
+    for src, codes, norms, tq, bits in ((k, kc, kn, cache.k_quant, bk), (v, vc, vn, cache.v_quant, bv)):
+        _, p, n16, u = _decoded(tq, src.reshape(-1, d), bits, d)
+        want = O.unpack(p, bits, d).reshape(n, hkv, d)
+        u = u.reshape(n, hkv, d)
+        n16 = n16.reshape(n, hkv)
+        sl = slots.numpy()
+        ok = sl >= 0
+        blk, off = sl[ok] // page, sl[ok] % page
+        got = codes[blk, :, off]  # [m, hkv, d]
+        diff = got != want[ok]
+        if diff.any():
+            dist = O.boundary_distance(u[ok], tq.quantizer.boundaries.cpu().numpy())[diff]
+            assert dist.max() < TIE
+            ties += int(diff.sum())
+        gn = norms[blk, :, off].astype(np.float32)
+        wn = n16[ok].astype(np.float32)
+        assert np.all(np.abs(gn - wn) <= 1e-3 * np.abs(wn) + 1e-7)
+    print(f"[store bk={bk} bv={bv} page={page}] ties={ties}")
+
+
+@pytest.mark.parametrize("bk,bv", [(3, 3), (4, 2), (2, 4), (4, 4)])
+@pytest.mark.parametrize("hq,hkv", [(32, 8), (8, 8), (16, 2)])
+def test_decode_attention_parity(cuda, bk, bv, hq, hkv):
+    from fused_turboquant.paged import PagedTurboQuantCache
+    d, page = 128, 16
+    lens = [1, 17, 33, 100, 515, 1000]
+    B = len(lens)
+    maxp = max((L + page - 1) // page for L in lens)
+    g = torch.Generator().manual_seed(bk * 100 + bv * 10 + hq)
+    nblk = B * maxp + 3
+    cache = PagedTurboQuantCache(nblk, page, hkv, d, bk, bv, device=cuda)
+    bt = torch.randperm(nblk, generator=g)[: B * maxp].view(B, maxp).to(torch.int32)
+    ks, vs = _fill(cache, lens, bt, hkv, d, g, cuda)
+    q = torch.randn(B, hq, d, generator=g).to(torch.bfloat16)
+    S = max(lens)
+    Kd = np.zeros((B, hkv, S, d))
+    Vd = np.zeros((B, hkv, S, d))
+    for b, L in enumerate(lens):
+        Kd[b, :, :L] = _decoded(cache.k_quant, ks[b].reshape(-1, d), bk, d)[0].reshape(L, hkv, d).transpose(1, 0, 2)
+        Vd[b, :, :L] = _decoded(cache.v_quant, vs[b].reshape(-1, d), bv, d)[0].reshape(L, hkv, d).transpose(1, 0, 2)
+    ref = O.dense_decode_attention(q.float().numpy(), Kd, Vd, lens, 1 / math.sqrt(d))
+    sl = torch.tensor(lens, dtype=torch.int32, device=cuda)
+    for splits in (1, 3, 8):
+        out = cache.decode_attention(q.to(cuda), bt.to(cuda), sl, num_splits=splits).float().cpu().numpy()
+        err = np.abs(out - ref)
+        print(f"[attn bk={bk} bv={bv} hq={hq} hkv={hkv} splits={splits}] max={err.max():.2e} mean={err.mean():.2e}")
+        assert err.max() <= 2e-2 and err.mean() <= 2e-3
+    out32 = cache.decode_attention(q.to(cuda), bt.to(cuda), sl, num_splits=2,
+                                   out=torch.empty(B, hq, d, device=cuda)).cpu().numpy()
+    assert np.abs(out32 - ref).max() <= 2e-2
+
+
+def test_decode_attention_page32_and_zero_len(cuda):
+    from fused_turboquant.paged import PagedTurboQuantCache
+    d, page, hq, hkv = 128, 32, 8, 2
+    lens = [0, 5, 64, 77]
+    B = len(lens)
+    maxp = 3
+    g = torch.Generator().manual_seed(9)
+    cache = PagedTurboQuantCache(B * maxp, page, hkv, d, 3, 3, device=cuda)
+    bt = torch.randperm(B * maxp, generator=g).view(B, maxp).to(torch.int32)
+    ks, vs = _fill(cache, lens, bt, hkv, d, g, cuda)
+    q = torch.randn(B, hq, d, generator=g).to(torch.bfloat16)
+    Kd = np.zeros((B, hkv, 77, d))
+    Vd = np.zeros((B, hkv, 77, d))
+    for b, L in enumerate(lens):
+        if L:
+            Kd[b, :, :L] = _decoded(cache.k_quant, ks[b].reshape(-1, d), 3, d)[0].reshape(L, hkv, d).transpose(1, 0, 2)
+            Vd[b, :, :L] = _decoded(cache.v_quant, vs[b].reshape(-1, d), 3, d)[0].reshape(L, hkv, d).transpose(1, 0, 2)
+    ref = O.dense_decode_attention(q.float().numpy(), Kd, Vd, lens, 1 / math.sqrt(d))
+    out = cache.decode_attention(q.to(cuda), bt.to(cuda), torch.tensor(lens, dtype=torch.int32, device=cuda),
+                                 num_splits=4).float().cpu().numpy()
+    assert np.all(out[0] == 0)  # empty context -> zeros
+    assert np.abs(out - ref).max() <= 2e-2
+
+
+def test_config3_full_size(cuda):
+    """Config 3 at full size; two sequences checked against the oracle, the rest
+    through split-count invariance (1 split vs the default split)."""
+    from fused_turboquant import paged as P
+    cache, q, bt, sl = P.make_config3(cuda)
+    B, hq, d = q.shape
+    out = P.paged_decode_attention(q, cache.kv_cache, bt, sl, cache.k_quant, cache.v_quant)
+    out1 = P.paged_decode_attention(q, cache.kv_cache, bt, sl, cache.k_quant, cache.v_quant, num_splits=1)
+    a, b1 = out.float().cpu().numpy(), out1.float().cpu().numpy()
+    assert np.isfinite(a).all()
+    assert np.abs(a - b1).max() <= 1e-2
+    kq, vq = cache.k_quant, cache.v_quant
+    ctx = int(sl[0])
+    full = cache.kv_cache.cpu().numpy()
+    for bsel in (0, B - 1):
+        kc, vc, kn, vn = O.paged_unpack(full[bt[bsel].cpu().numpy()], d, 3, 3)
+        hkv = kc.shape[1]
+        blocks = np.arange(kc.shape[0])
+        Kd = np.zeros((1, hkv, ctx, d))
+        Vd = np.zeros((1, hkv, ctx, d))
+        for h in range(hkv):
+            kcodes = kc[blocks, h].reshape(-1, d)[:ctx]
+            vcodes = vc[blocks, h].reshape(-1, d)[:ctx]
+            knr = kn[blocks, h].reshape(-1)[:ctx]
+            vnr = vn[blocks, h].reshape(-1)[:ctx]
+            Kd[0, h] = O.decode(O.pack(kcodes, 3), knr, kq.quantizer.levels.cpu().numpy(), kq.rotation.signs.cpu().numpy(), 3, d)
+            Vd[0, h] = O.decode(O.pack(vcodes, 3), vnr, vq.quantizer.levels.cpu().numpy(), vq.rotation.signs.cpu().numpy(), 3, d)
+        ref = O.dense_decode_attention(q[bsel:bsel + 1].float().cpu().numpy(), Kd, Vd, [ctx], 1 / math.sqrt(d))
+        err = np.abs(a[bsel] - ref[0])
+        print(f"[config3 seq {bsel}] max={err.max():.2e} mean={err.mean():.2e}")
+        assert err.max() <= 2e-2 and err.mean() <= 2e-3
