@@ -7,7 +7,7 @@ OUT="$HERE/fused_turboquant/libfused_tq.so"
 OBJ="$HERE/_build"
 mkdir -p "$OBJ"
 FLAGS=(-O3 -std=c++17 -fPIC --offload-arch=gfx950 -ffp-contract=off
-       -Xclang -target-feature -Xclang -packed-fp32-ops
+       -Xclang -target-feature -Xclang -packed-fp32-ops -mllvm -amdgpu-mfma-vgpr-form
        -I"$HERE/../include" -Wall -Wno-unused-function)
 pids=()
 for f in "$SRC"/*.hip "$SRC"/*.cpp; do

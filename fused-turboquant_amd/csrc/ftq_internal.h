@@ -5,7 +5,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-#include "../../include/fused_tq.h"
+#include "fused_tq.h"  // from include/ (on the -I path)
 
 namespace ftq {
 void set_error(const char* msg);

@@ -75,6 +75,18 @@ __device__ __forceinline__ uint32_t bits_at(const uint32_t (&w)[N], int P, int W
   return v & ((1u << W) - 1u);
 }
 
+// 4 * bits [P, P+W)  (a byte address into a table of dwords)
+template <int N>
+__device__ __forceinline__ uint32_t addr4_at(const uint32_t (&w)[N], int P, int W) {
+  if (P >= 2) {
+    const int Q = P - 2, i = Q >> 5, o = Q & 31;
+    uint32_t v = w[i] >> o;
+    if (o + W + 2 > 32 && i + 1 < N) v |= w[i + 1] << (32 - o);
+    return v & (((1u << W) - 1u) << 2);
+  }
+  return (w[0] << 2) & (((1u << W) - 1u) << 2);
+}
+
 template <int NDW>
 __device__ __forceinline__ void load_dwords(const uint8_t* p, uint32_t (&w)[NDW]) {
   const uint32_t* q = reinterpret_cast<const uint32_t*>(p);
@@ -188,6 +200,62 @@ __global__ __launch_bounds__(256) void paged_store_kernel(
 // ---------------------------------------------------------------------------
 // decode attention, stage 1 (per split)
 // ---------------------------------------------------------------------------
+
+// Code lookup tables in LDS.  For B <= 3 bits an entry covers 4 codes
+// (index = c0 | c1 << B | c2 << 2B | c3 << 3B, 8 bytes = 4 f16), so one
+// ds_read_b64 dequantises 4 codes; 4-bit codes use 2-code entries (f16x2).
+template <int B>
+struct CodeLut {
+  static constexpr bool QUAD = false;  // 4-code tables: bank conflicts outweigh the saved VALU on gfx950
+  static constexpr int CODES = QUAD ? 4 : 2;
+  static constexpr int IDX_BITS = CODES * B;
+  static constexpr int ENTRIES = 1 << IDX_BITS;
+  static constexpr int ENTRY_BYTES = 2 * CODES;
+  static constexpr int BYTES = ENTRIES * ENTRY_BYTES;
+};
+
+// fill a code table from the fp16 level values already staged in LDS:
+// entry e -> f16(levels[code k of e]) for k < CODES
+template <int B>
+__device__ void build_code_lut(uint8_t* lut, const uint16_t* single, int tid, int nthreads) {
+  using C = CodeLut<B>;
+  for (int e = tid; e < C::ENTRIES; e += nthreads) {
+    uint32_t w[2] = {0u, 0u};
+#pragma unroll
+    for (int k = 0; k < C::CODES; ++k)
+      w[k >> 1] |= (uint32_t)single[(e >> (k * B)) & ((1 << B) - 1)] << (16 * (k & 1));
+    if constexpr (C::QUAD) reinterpret_cast<uint2*>(lut)[e] = make_uint2(w[0], w[1]);
+    else reinterpret_cast<uint32_t*>(lut)[e] = w[0];
+  }
+}
+
+// entry_bytes * bits [P, P+W) of a little-endian multi-dword value: the byte
+// offset of a table entry (P, W compile-time after unrolling)
+template <int SH, int N>
+__device__ __forceinline__ uint32_t field_off(const uint32_t (&w)[N], int P, int W) {
+  const uint32_t m = ((1u << W) - 1u) << SH;
+  if (P >= SH) {
+    const int Q = P - SH, i = Q >> 5, o = Q & 31;
+    uint32_t v = w[i] >> o;
+    if (o + W + SH > 32 && i + 1 < N) v |= w[i + 1] << (32 - o);
+    return v & m;
+  }
+  return (w[0] << (SH - P)) & m;
+}
+
+// dequantise the codes at bits [P, P + 4B) (quad) into two f16x2 dwords
+template <int B, int N>
+__device__ __forceinline__ uint2 lut_quad(const uint8_t* lut, const uint32_t (&w)[N], int P) {
+  using C = CodeLut<B>;
+  if constexpr (C::QUAD) {
+    return *reinterpret_cast<const uint2*>(lut + field_off<3>(w, P, C::IDX_BITS));
+  } else {
+    const uint32_t lo = *reinterpret_cast<const uint32_t*>(lut + field_off<2>(w, P, C::IDX_BITS));
+    const uint32_t hi = *reinterpret_cast<const uint32_t*>(lut + field_off<2>(w, P + 2 * B, C::IDX_BITS));
+    return make_uint2(lo, hi);
+  }
+}
+
 template <int D, int BK, int BV>
 struct TileRegs {
   using Gm = PagedGeom<D, BK, BV>;
@@ -195,34 +263,34 @@ struct TileRegs {
   uint32_t v[2][Gm::VLANE / 4];
   uint32_t kn[2][2];  // 4 fp16 K norms per sub-block (tokens 4q..4q+3)
   uint32_t vn[2][2];
+  bool ok[2];         // wave-uniform: sub-block holds real tokens
 };
 
 template <int D, int BK, int BV>
 __device__ __forceinline__ void load_tile(TileRegs<D, BK, BV>& r, const uint8_t* __restrict__ cache,
                                           const int32_t* __restrict__ bt_row, int tile, int seq_len,
-                                          int page_size, int nsub, int hkv, int kvh, int lane,
-                                          int max_blocks, int64_t num_blocks) {
+                                          int page_size, int nsub, int hkv, int kvh, uint32_t lane,
+                                          int max_blocks, int64_t num_blocks, bool active) {
   using Gm = PagedGeom<D, BK, BV>;
-  const int t = lane & 15, q = lane >> 4;
+  const uint32_t t = lane & 15u, q = lane >> 4;
 #pragma unroll
   for (int sb = 0; sb < 2; ++sb) {
+    // tile, page, block id and base are wave-uniform (scalar).  An inactive or
+    // invalid sub-block (past seq_len, or a bad block id) reads block 0 instead
+    // (always issuing the loads keeps the wait counts static) and is flagged so
+    // the consumer zeroes its V norms; its scores are masked to -inf there too.
     const int tok0 = tile * 32 + sb * 16;
     const int page = tok0 / page_size;
-    const int64_t phys = (tok0 < seq_len && page < max_blocks) ? (int64_t)bt_row[page] : -1;
-    if (phys >= 0 && phys < num_blocks) {
-      const int sub = (tok0 % page_size) >> 4;
-      const uint8_t* base = cache + ((phys * hkv + kvh) * nsub + sub) * (int64_t)Gm::SUB;
-      load_dwords(base + t * Gm::KTOK + q * Gm::KLANE, r.k[sb]);
-      load_dwords(base + Gm::KSEC + lane * Gm::VLANE, r.v[sb]);
-      load_dwords(base + Gm::KNORM + q * 8, r.kn[sb]);
-      load_dwords(base + Gm::VNORM + q * 8, r.vn[sb]);
-    } else {
-#pragma unroll
-      for (int i = 0; i < Gm::KLANE / 4; ++i) r.k[sb][i] = 0;
-#pragma unroll
-      for (int i = 0; i < Gm::VLANE / 4; ++i) r.v[sb][i] = 0;
-      r.kn[sb][0] = r.kn[sb][1] = r.vn[sb][0] = r.vn[sb][1] = 0;
-    }
+    int64_t phys = (active && tok0 < seq_len && page < max_blocks) ? (int64_t)bt_row[page] : -1;
+    const bool valid = phys >= 0 && phys < num_blocks;
+    if (!valid) phys = 0;
+    const int sub = valid ? (tok0 % page_size) >> 4 : 0;
+    const uint8_t* base = cache + ((phys * hkv + kvh) * nsub + sub) * (int64_t)Gm::SUB;
+    load_dwords(base + (t * (uint32_t)Gm::KTOK + q * (uint32_t)Gm::KLANE), r.k[sb]);
+    load_dwords(base + ((uint32_t)Gm::KSEC + lane * (uint32_t)Gm::VLANE), r.v[sb]);
+    load_dwords(base + ((uint32_t)Gm::KNORM + q * 8u), r.kn[sb]);
+    load_dwords(base + ((uint32_t)Gm::VNORM + q * 8u), r.vn[sb]);
+    r.ok[sb] = valid;
   }
 }
 
@@ -237,8 +305,8 @@ __device__ __forceinline__ float warp_sum_q(float x) {
   return x;
 }
 
-template <int D, int BK, int BV, int QT>
-__global__ __launch_bounds__(256) void paged_attn_kernel(
+template <int D, int BK, int BV, int QT, bool SHARE>
+__global__ __launch_bounds__(256, 4) void paged_attn_kernel(
     const void* __restrict__ query, const uint8_t* __restrict__ cache,
     const int32_t* __restrict__ block_table, const int32_t* __restrict__ seq_lens, int hq, int hkv,
     int page_size, int max_blocks, int64_t num_blocks, const float* __restrict__ ksigns,
@@ -252,20 +320,25 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int h = lane & 15, q = lane >> 4;
 
-  __shared__ uint32_t lutK[1 << (2 * BK)];
-  __shared__ uint32_t lutV[1 << (2 * BV)];
+  // LDS pool, reused in three phases: rotated queries (prologue), code tables
+  // (tile loop), wave-merge buffer (epilogue)
+  constexpr int LUTK_BYTES = CodeLut<BK>::BYTES;
+  constexpr int LUTV_BYTES = SHARE ? 0 : CodeLut<BV>::BYTES;
+  constexpr int RED_BYTES = 4 * 16 * (D + 1) * 4;
+  constexpr int QS_BYTES = 16 * (D + 8) * 2;
+  constexpr int POOL = (LUTK_BYTES + LUTV_BYTES > RED_BYTES ? LUTK_BYTES + LUTV_BYTES : RED_BYTES) > QS_BYTES
+                           ? (LUTK_BYTES + LUTV_BYTES > RED_BYTES ? LUTK_BYTES + LUTV_BYTES : RED_BYTES)
+                           : QS_BYTES;
+  __shared__ __attribute__((aligned(16))) uint8_t pool[POOL];
   __shared__ float red_m[4][16], red_l[4][16];
-  // the rotated queries are only read before the tile loop; the wave-merge
-  // buffer reuses their LDS afterwards
-  __shared__ float lds_big[4 * 16 * (D + 1)];
-  _Float16 (*qs)[D + 8] = reinterpret_cast<_Float16 (*)[D + 8]>(lds_big);
-  float (*red_o)[16][D + 1] = reinterpret_cast<float (*)[16][D + 1]>(lds_big);
+  __shared__ uint16_t lev16[2][16];  // fp16 K / V levels
+  _Float16 (*qs)[D + 8] = reinterpret_cast<_Float16 (*)[D + 8]>(pool);
+  float (*red_o)[16][D + 1] = reinterpret_cast<float (*)[16][D + 1]>(pool);
+  uint8_t* lutK = pool;
+  uint8_t* lutV = SHARE ? pool : pool + LUTK_BYTES;
 
-  // pair lookup tables: entry (lo | hi << B) = f16(C[lo]) | f16(C[hi]) << 16
-  for (int e = tid; e < (1 << (2 * BK)); e += 256)
-    lutK[e] = f32_to_f16_bits(klev[e & ((1 << BK) - 1)]) | (f32_to_f16_bits(klev[e >> BK]) << 16);
-  for (int e = tid; e < (1 << (2 * BV)); e += 256)
-    lutV[e] = f32_to_f16_bits(vlev[e & ((1 << BV) - 1)]) | (f32_to_f16_bits(vlev[e >> BV]) << 16);
+  if (tid < (1 << BK)) lev16[0][tid] = (uint16_t)f32_to_f16_bits(klev[tid]);
+  if (tid >= 64 && tid - 64 < (1 << BV)) lev16[1][tid - 64] = (uint16_t)f32_to_f16_bits(vlev[tid - 64]);
 
   // rotate the G query heads of this kv head: one head per 16 lanes
   {
@@ -301,7 +374,10 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(
       qb[s].u[j] = w;
     }
   }
-  __syncthreads();  // qs is dead from here on (its LDS becomes red_o)
+  __syncthreads();  // qs is dead from here on; its LDS holds the code tables
+  build_code_lut<BK>(lutK, lev16[0], tid, 256);
+  if (!SHARE) build_code_lut<BV>(lutV, lev16[1], tid, 256);
+  __syncthreads();
 
   const int seq_len = seq_lens[b];
   const int n_tiles = (seq_len + 31) >> 5;
@@ -310,20 +386,20 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(
   const int t_end = min(t_begin + tps, n_tiles);
   const int nsub = page_size >> 4;
   const int32_t* bt_row = block_table + (int64_t)b * max_blocks;
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);  // wave-uniform -> scalar tile math
 
   float m_run = -INFINITY, l_run = 0.f;
   floatx4 acc[NB];
 #pragma unroll
   for (int i = 0; i < NB; ++i) acc[i] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  TileRegs<D, BK, BV> cur, nxt;
-  int tile = t_begin + wave;
-  if (tile < t_end) load_tile(nxt, cache, bt_row, tile, seq_len, page_size, nsub, hkv, kvh, lane, max_blocks, num_blocks);
-  for (; tile < t_end; tile += 4) {
-    cur = nxt;
-    if (tile + 4 < t_end) load_tile(nxt, cache, bt_row, tile + 4, seq_len, page_size, nsub, hkv, kvh, lane, max_blocks, num_blocks);
-
-    // ---- scores S^T (rows = tokens 4q+i of each sub-block, column = head h) ----
+  // One 32-token tile: scores, lazily rescaled online softmax, P.V.
+  // Exponentials use the running reference max m_run; it is only raised (and
+  // acc / l rescaled) when a tile max exceeds it by more than TAU, so
+  // p <= 2^TAU.  P' = p * ||v|| * 2^-(TAU+1) then stays below the f16 maximum
+  // for any fp16 norm; the final output is multiplied back by 2^(TAU+1).
+  constexpr float TAU = 8.f;  // 2^(TAU+1) == 512
+  auto process = [&](const TileRegs<D, BK, BV>& cur, int tile) __attribute__((always_inline)) {
     float s[2][4];
 #pragma unroll
     for (int sb = 0; sb < 2; ++sb) {
@@ -331,56 +407,87 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(
 #pragma unroll
       for (int st = 0; st < NS; ++st) {
         Op8 a;
-#pragma unroll
-        for (int p = 0; p < 4; ++p)
-          a.u[p] = lutK[bits_at(cur.k[sb], (8 * st + 2 * p) * BK, 2 * BK)];
+        const uint2 c01 = lut_quad<BK>(lutK, cur.k[sb], (8 * st) * BK);
+        const uint2 c23 = lut_quad<BK>(lutK, cur.k[sb], (8 * st + 4) * BK);
+        a.u[0] = c01.x; a.u[1] = c01.y; a.u[2] = c23.x; a.u[3] = c23.y;
         c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a.h, qb[st].h, c, 0, 0, 0);
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const uint32_t nb = (cur.kn[sb][i >> 1] >> (16 * (i & 1))) & 0xffffu;
-        const int tok = tile * 32 + sb * 16 + 4 * q + i;
-        s[sb][i] = (tok < seq_len) ? c[i] * f16_bits_to_f32(nb) : -INFINITY;
+        const _Float16 kn = __builtin_bit_cast(_Float16, (uint16_t)(cur.kn[sb][i >> 1] >> (16 * (i & 1))));
+        s[sb][i] = __builtin_fmaf(c[i], (float)kn, 0.f);
       }
     }
-    // ---- online softmax (log2 domain) ----
+    if (tile * 32 + 32 > seq_len) {  // only the last tile of a sequence is partial
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (tile * 32 + sb * 16 + 4 * q + i >= seq_len) s[sb][i] = -INFINITY;
+    }
     float tmax = fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
                        fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
     tmax = warp_max_q(tmax);
-    const float m_new = fmaxf(m_run, tmax);
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-    m_run = m_new;
+    if (__builtin_amdgcn_ballot_w64(tmax > m_run + TAU) != 0) {  // wave-uniform, rare
+      const float m_new = fmaxf(m_run, tmax);
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+      m_run = m_new;
+      l_run *= alpha;
+#pragma unroll
+      for (int bb = 0; bb < NB; ++bb) acc[bb] *= alpha;
+    }
+    // p is taken pre-scaled by 2^-(TAU+1) (folded into the exponent); l gets it back
+    const float m_sc = m_run + (TAU + 1.f);
     float psum = 0.f;
     Op8 pb;
 #pragma unroll
     for (int sb = 0; sb < 2; ++sb) {
-      float pv[4];
+      uint32_t h16[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float p = __builtin_amdgcn_exp2f(s[sb][i] - m_new);
+        const float p = __builtin_amdgcn_exp2f(s[sb][i] - m_sc);
         psum += p;
-        const uint32_t nb = (cur.vn[sb][i >> 1] >> (16 * (i & 1))) & 0xffffu;
-        pv[i] = p * f16_bits_to_f32(nb);
+        const uint32_t vnw = cur.ok[sb] ? cur.vn[sb][i >> 1] : 0u;
+        const _Float16 vn = __builtin_bit_cast(_Float16, (uint16_t)(vnw >> (16 * (i & 1))));
+        h16[i] = __builtin_bit_cast(uint16_t, (_Float16)__builtin_fmaf(p, (float)vn, 0.f));
       }
-      pb.u[2 * sb] = f32_to_f16_bits(pv[0]) | (f32_to_f16_bits(pv[1]) << 16);
-      pb.u[2 * sb + 1] = f32_to_f16_bits(pv[2]) | (f32_to_f16_bits(pv[3]) << 16);
+      pb.u[2 * sb] = h16[0] | (h16[1] << 16);
+      pb.u[2 * sb + 1] = h16[2] | (h16[3] << 16);
     }
-    l_run = l_run * alpha + psum;
-    // ---- O^T += V^T P'^T ----
+    psum *= 512.f;
+    l_run += psum;
 #pragma unroll
     for (int bb = 0; bb < NB; ++bb) {
       Op8 a;
 #pragma unroll
       for (int sb = 0; sb < 2; ++sb) {
-        a.u[2 * sb] = lutV[bits_at(cur.v[sb], (4 * bb) * BV, 2 * BV)];
-        a.u[2 * sb + 1] = lutV[bits_at(cur.v[sb], (4 * bb + 2) * BV, 2 * BV)];
+        const uint2 t4 = lut_quad<BV>(lutV, cur.v[sb], (4 * bb) * BV);
+        a.u[2 * sb] = t4.x;
+        a.u[2 * sb + 1] = t4.y;
       }
-      acc[bb] *= alpha;
       acc[bb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a.h, pb.h, acc[bb], 0, 0, 0);
     }
-  }
+  };
 
-  // ---- merge the 4 waves through LDS ----
+  // ping-pong over two register sets so the next tile's loads overlap this tile's math
+  TileRegs<D, BK, BV> ra, rb;
+  int tile = t_begin + wave_u;
+  if (tile < t_end) load_tile(ra, cache, bt_row, tile, seq_len, page_size, nsub, hkv, kvh, (uint32_t)lane, max_blocks, num_blocks, true);
+  while (tile < t_end) {
+    load_tile(rb, cache, bt_row, tile + 4, seq_len, page_size, nsub, hkv, kvh, (uint32_t)lane, max_blocks, num_blocks, tile + 4 < t_end);
+    process(ra, tile);
+    tile += 4;
+    if (tile >= t_end) break;
+    load_tile(ra, cache, bt_row, tile + 4, seq_len, page_size, nsub, hkv, kvh, (uint32_t)lane, max_blocks, num_blocks, tile + 4 < t_end);
+    process(rb, tile);
+    tile += 4;
+  }
+  // undo the P' pre-scale
+#pragma unroll
+  for (int bb = 0; bb < NB; ++bb) acc[bb] *= 512.f;
+
+  // ---- merge the 4 waves through LDS (the code tables' LDS is reused) ----
+  __syncthreads();
   const float l_tot = warp_sum_q(l_run);
   if (q == 0) {
     red_m[wave][h] = m_run;
@@ -512,15 +619,26 @@ struct AttnArgs {
   int ot;
 };
 
-template <int D, int BK, int BV>
-static hipError_t launch_attn3(const AttnArgs& a, hipStream_t st) {
+template <int D, int BK, int BV, bool SHARE>
+static void launch_attn_kernel(const AttnArgs& a, hipStream_t st) {
   dim3 grid(a.splits, a.hkv, a.B), block(256);
   if (a.qt == F32)
-    paged_attn_kernel<D, BK, BV, F32><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.hq, a.hkv, a.page_size, a.max_blocks, a.num_blocks, a.ks, a.kl, a.vl, a.qscale, a.splits, a.wo, a.wl);
+    paged_attn_kernel<D, BK, BV, F32, SHARE><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.hq, a.hkv, a.page_size, a.max_blocks, a.num_blocks, a.ks, a.kl, a.vl, a.qscale, a.splits, a.wo, a.wl);
   else if (a.qt == F16)
-    paged_attn_kernel<D, BK, BV, F16><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.hq, a.hkv, a.page_size, a.max_blocks, a.num_blocks, a.ks, a.kl, a.vl, a.qscale, a.splits, a.wo, a.wl);
+    paged_attn_kernel<D, BK, BV, F16, SHARE><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.hq, a.hkv, a.page_size, a.max_blocks, a.num_blocks, a.ks, a.kl, a.vl, a.qscale, a.splits, a.wo, a.wl);
   else
-    paged_attn_kernel<D, BK, BV, BF16><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.hq, a.hkv, a.page_size, a.max_blocks, a.num_blocks, a.ks, a.kl, a.vl, a.qscale, a.splits, a.wo, a.wl);
+    paged_attn_kernel<D, BK, BV, BF16, SHARE><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.hq, a.hkv, a.page_size, a.max_blocks, a.num_blocks, a.ks, a.kl, a.vl, a.qscale, a.splits, a.wo, a.wl);
+}
+
+template <int D, int BK, int BV>
+static hipError_t launch_attn3(const AttnArgs& a, hipStream_t st) {
+  // K and V share one code table when they use the same codebook array
+  if constexpr (BK == BV) {
+    if (a.kl == a.vl) launch_attn_kernel<D, BK, BV, true>(a, st);
+    else launch_attn_kernel<D, BK, BV, false>(a, st);
+  } else {
+    launch_attn_kernel<D, BK, BV, false>(a, st);
+  }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int64_t rows = (int64_t)a.B * a.hq;
