@@ -15,6 +15,7 @@
 // grid-stride loop.  Codes are packed with DPP neighbour exchanges into
 // dword stores; nothing goes through HBM scratch.
 #include "ftq_codec_dev.h"
+#include "ftq_encode_fast.h"
 #include "ftq_internal.h"
 
 #include <cmath>
@@ -25,29 +26,67 @@ template <int D, int BITS, int DT>
 __global__ __launch_bounds__(256) void encode_kernel(const void* __restrict__ x, int64_t n,
                                                      const float* __restrict__ signs,
                                                      const float* __restrict__ boundaries,
-                                                     float scale, uint8_t* __restrict__ packed,
+                                                     float scale, double rscale,
+                                                     uint8_t* __restrict__ packed,
                                                      uint16_t* __restrict__ norms) {
-  using S = CodecShape<D>;
-  constexpr int E = S::E, LPV = S::LPV, GPB = S::GPB;
-  constexpr int L = 1 << BITS;
+  using S = FastShape<D>;
+  constexpr int E = S::E, LPV = S::LPV, VPB = 256 / LPV;
   constexpr int PD = D * BITS / 8;
-  const int lane = threadIdx.x % LPV;
+  constexpr int NT = (1 << BITS) - 1;
+  __shared__ float bnd[NT];
+  if (threadIdx.x < NT) bnd[threadIdx.x] = boundaries[threadIdx.x + 1];
+  const int lane = threadIdx.x & 63;        // lane in the wave
+  const int lv = threadIdx.x & (LPV - 1);   // lane in the vector
   const int grp = threadIdx.x / LPV;
-
-  float bnd[L - 1];
+  // sign flips of this lane's elements, as xor masks on the input bits
+  constexpr int PER_DW = (DT == F32) ? 1 : 2;
+  uint32_t smask[E / PER_DW];
 #pragma unroll
-  for (int j = 0; j < L - 1; ++j) bnd[j] = boundaries[j + 1];
-  float sg[E];
+  for (int k = 0; k < E / PER_DW; ++k) {
+    uint32_t m = 0;
 #pragma unroll
-  for (int i = 0; i < E; ++i) sg[i] = signs[lane * E + i];
+    for (int j = 0; j < PER_DW; ++j)
+      if (signs[lv * E + k * PER_DW + j] < 0.f) m |= (DT == F32) ? 0x80000000u : (0x8000u << (16 * j));
+    smask[k] = m;
+  }
+  __syncthreads();
 
-  for (int64_t v = (int64_t)blockIdx.x * GPB + grp; v < n; v += (int64_t)gridDim.x * GPB) {
+  for (int64_t v = (int64_t)blockIdx.x * VPB + grp; v < n; v += (int64_t)gridDim.x * VPB) {
     float y[E];
-    load_elems<DT, E>(x, v * D + lane * E, y);
+    if constexpr (DT == F32) {
+      const uint4* p = reinterpret_cast<const uint4*>(static_cast<const float*>(x) + v * D + lv * E);
+#pragma unroll
+      for (int k = 0; k < E / 4; ++k) {
+        const uint4 w = p[k];
+        y[4 * k + 0] = __uint_as_float(w.x ^ smask[4 * k + 0]);
+        y[4 * k + 1] = __uint_as_float(w.y ^ smask[4 * k + 1]);
+        y[4 * k + 2] = __uint_as_float(w.z ^ smask[4 * k + 2]);
+        y[4 * k + 3] = __uint_as_float(w.w ^ smask[4 * k + 3]);
+      }
+    } else {
+      const uint4* p = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(x) + v * D + lv * E);
+#pragma unroll
+      for (int k = 0; k < E / 8; ++k) {
+        const uint4 w4 = p[k];
+        const uint32_t w[4] = {w4.x ^ smask[4 * k], w4.y ^ smask[4 * k + 1], w4.z ^ smask[4 * k + 2],
+                               w4.w ^ smask[4 * k + 3]};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if constexpr (DT == BF16) {
+            y[8 * k + 2 * j] = __uint_as_float(w[j] << 16);
+            y[8 * k + 2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
+          } else {
+            y[8 * k + 2 * j] = f16_bits_to_f32(w[j] & 0xffffu);
+            y[8 * k + 2 * j + 1] = f16_bits_to_f32(w[j] >> 16);
+          }
+        }
+      }
+    }
     uint32_t c[E];
-    const float nrm = encode_core<E, LPV, BITS>(y, sg, bnd, scale, lane, c);
-    pack_store<E, BITS>(c, packed + v * PD, lane);
-    if (lane == 0) norms[v] = (uint16_t)f32_to_f16_bits(nrm);
+    bool flip;
+    const float nrm = encode_fast<D, BITS>(y, bnd, scale, rscale, lane, c, flip);
+    store_lane_codes<E, BITS>(c, flip, packed + v * PD, lv);
+    if (lv == 0) norms[v] = (uint16_t)f32_to_f16_bits(nrm);
   }
 }
 
@@ -130,12 +169,13 @@ template <int D, int BITS>
 static hipError_t launch_encode_db(const void* x, int dt, int64_t n, const float* signs,
                                    const float* bnd, uint8_t* packed, uint16_t* norms,
                                    hipStream_t st) {
-  using S = CodecShape<D>;
-  dim3 grid(codec_grid(n, S::GPB)), block(256);
+  constexpr int VPB = 256 / FastShape<D>::LPV;
+  dim3 grid(codec_grid(n, VPB)), block(256);
   const float sc = fwht_scale(D);
-  if (dt == F32) encode_kernel<D, BITS, F32><<<grid, block, 0, st>>>(x, n, signs, bnd, sc, packed, norms);
-  else if (dt == F16) encode_kernel<D, BITS, F16><<<grid, block, 0, st>>>(x, n, signs, bnd, sc, packed, norms);
-  else encode_kernel<D, BITS, BF16><<<grid, block, 0, st>>>(x, n, signs, bnd, sc, packed, norms);
+  const double rsc = 1.0 / (double)sc;
+  if (dt == F32) encode_kernel<D, BITS, F32><<<grid, block, 0, st>>>(x, n, signs, bnd, sc, rsc, packed, norms);
+  else if (dt == F16) encode_kernel<D, BITS, F16><<<grid, block, 0, st>>>(x, n, signs, bnd, sc, rsc, packed, norms);
+  else encode_kernel<D, BITS, BF16><<<grid, block, 0, st>>>(x, n, signs, bnd, sc, rsc, packed, norms);
   return hipGetLastError();
 }
 

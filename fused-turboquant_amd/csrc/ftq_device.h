@@ -18,11 +18,13 @@ namespace ftq {
 // dpp_ctrl encodings (GFX9 DPP): quad_perm = p0 | p1<<2 | p2<<4 | p3<<6,
 // row_shl:n = 0x100+n (lane l reads l+n), row_shr:n = 0x110+n (lane l reads
 // l-n), row_ror:n = 0x120+n.
+// (mov_dpp with bound_ctrl set: every lane's source is inside its row, so no
+// "old" value is needed and LLVM can fold the permute into the consuming VALU op)
 __device__ __forceinline__ float dpp_xor1(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, true));
 }
 __device__ __forceinline__ float dpp_xor2(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, true));
 }
 __device__ __forceinline__ float dpp_xor4(float v) {
   int x = __float_as_int(v);
@@ -32,7 +34,7 @@ __device__ __forceinline__ float dpp_xor4(float v) {
   return __int_as_float(t);
 }
 __device__ __forceinline__ float dpp_xor8(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false));
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xF, 0xF, true));
 }
 __device__ __forceinline__ uint32_t dpp_xor1_u(uint32_t v) {
   return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false);
