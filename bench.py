@@ -77,7 +77,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this path runs on one GPU; --gpus above 1 is not supported "
-                          "(the hot path has no collectives; see DESIGN.md for how it would shard)"}))
+                          "(the hot path has no collectives; each GPU would run the same kernels on its own shard)"}))
         sys.exit(2)
 
     import torch
