@@ -116,9 +116,15 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t b) {
   return __half2float(__ushort_as_half((unsigned short)b));
 }
 
-// Load E contiguous elements (E multiple of 8 for 16-bit types, of 4 for f32).
+__device__ __forceinline__ float half_bits_to_f32(int DT, uint32_t h) {
+  return DT == BF16 ? bf16_bits_to_f32(h) : f16_bits_to_f32(h);
+}
+
+// Load E contiguous elements (E a multiple of 4; 16-byte chunks, then one
+// 8-byte chunk when E % 8 == 4 for 16-bit types).
 template <int DT, int E>
 __device__ __forceinline__ void load_elems(const void* base, int64_t elem_off, float (&x)[E]) {
+  static_assert(E % 4 == 0, "E must be a multiple of 4");
   if constexpr (DT == F32) {
     const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(base) + elem_off);
 #pragma unroll
@@ -127,49 +133,55 @@ __device__ __forceinline__ void load_elems(const void* base, int64_t elem_off, f
       x[4 * k + 0] = v.x; x[4 * k + 1] = v.y; x[4 * k + 2] = v.z; x[4 * k + 3] = v.w;
     }
   } else {
-    const uint4* p = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + elem_off);
+    const uint16_t* b16 = static_cast<const uint16_t*>(base) + elem_off;
+    const uint4* p = reinterpret_cast<const uint4*>(b16);
 #pragma unroll
     for (int k = 0; k < E / 8; ++k) {
       uint4 v = p[k];
       uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        if constexpr (DT == BF16) {
-          x[8 * k + 2 * j] = bf16_bits_to_f32(w[j] & 0xffffu);
-          x[8 * k + 2 * j + 1] = bf16_bits_to_f32(w[j] >> 16);
-        } else {
-          x[8 * k + 2 * j] = f16_bits_to_f32(w[j] & 0xffffu);
-          x[8 * k + 2 * j + 1] = f16_bits_to_f32(w[j] >> 16);
-        }
+        x[8 * k + 2 * j] = half_bits_to_f32(DT, w[j] & 0xffffu);
+        x[8 * k + 2 * j + 1] = half_bits_to_f32(DT, w[j] >> 16);
       }
+    }
+    if constexpr (E % 8 == 4) {
+      const uint2 v = *reinterpret_cast<const uint2*>(b16 + (E / 8) * 8);
+      x[E - 4] = half_bits_to_f32(DT, v.x & 0xffffu);
+      x[E - 3] = half_bits_to_f32(DT, v.x >> 16);
+      x[E - 2] = half_bits_to_f32(DT, v.y & 0xffffu);
+      x[E - 1] = half_bits_to_f32(DT, v.y >> 16);
     }
   }
 }
 
+__device__ __forceinline__ uint32_t f32_to_half_bits(int DT, float f) {
+  return DT == BF16 ? f32_to_bf16_bits(f) : f32_to_f16_bits(f);
+}
+
+// Store E contiguous elements (same chunking as load_elems).
 template <int DT, int E>
 __device__ __forceinline__ void store_elems(void* base, int64_t elem_off, const float (&x)[E]) {
+  static_assert(E % 4 == 0, "E must be a multiple of 4");
   if constexpr (DT == F32) {
     float4* p = reinterpret_cast<float4*>(static_cast<float*>(base) + elem_off);
 #pragma unroll
     for (int k = 0; k < E / 4; ++k) p[k] = make_float4(x[4 * k], x[4 * k + 1], x[4 * k + 2], x[4 * k + 3]);
   } else {
-    uint4* p = reinterpret_cast<uint4*>(static_cast<uint16_t*>(base) + elem_off);
+    uint16_t* b16 = static_cast<uint16_t*>(base) + elem_off;
+    uint4* p = reinterpret_cast<uint4*>(b16);
 #pragma unroll
     for (int k = 0; k < E / 8; ++k) {
       uint32_t w[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        uint32_t lo, hi;
-        if constexpr (DT == BF16) {
-          lo = f32_to_bf16_bits(x[8 * k + 2 * j]);
-          hi = f32_to_bf16_bits(x[8 * k + 2 * j + 1]);
-        } else {
-          lo = f32_to_f16_bits(x[8 * k + 2 * j]);
-          hi = f32_to_f16_bits(x[8 * k + 2 * j + 1]);
-        }
-        w[j] = lo | (hi << 16);
-      }
+      for (int j = 0; j < 4; ++j)
+        w[j] = f32_to_half_bits(DT, x[8 * k + 2 * j]) | (f32_to_half_bits(DT, x[8 * k + 2 * j + 1]) << 16);
       p[k] = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+    if constexpr (E % 8 == 4) {
+      const uint32_t lo = f32_to_half_bits(DT, x[E - 4]) | (f32_to_half_bits(DT, x[E - 3]) << 16);
+      const uint32_t hi = f32_to_half_bits(DT, x[E - 2]) | (f32_to_half_bits(DT, x[E - 1]) << 16);
+      *reinterpret_cast<uint2*>(b16 + (E / 8) * 8) = make_uint2(lo, hi);
     }
   }
 }

@@ -33,6 +33,7 @@
 // Online softmax in the log2 domain (scale * log2 e folded into q).  Waves
 // merge through LDS; splits merge in a second kernel that also applies the
 // inverse RHT of V and writes the output dtype.
+#include "ftq_attn_dev.h"
 #include "ftq_codec_dev.h"
 #include "ftq_internal.h"
 
@@ -56,42 +57,6 @@ template <int D, int BK, int BV> struct PagedGeom {
 
 int64_t paged_sub_bytes(int d, int bk, int bv) {
   return (int64_t)2 * d * (bk + bv) + 64;
-}
-
-typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-typedef float floatx4 __attribute__((ext_vector_type(4)));
-
-union Op8 {
-  uint32_t u[4];
-  half8 h;
-};
-
-// bits [P, P+W) of a little-endian multi-dword value (P, W compile-time after unrolling)
-template <int N>
-__device__ __forceinline__ uint32_t bits_at(const uint32_t (&w)[N], int P, int W) {
-  const int i = P >> 5, o = P & 31;
-  uint32_t v = w[i] >> o;
-  if (o + W > 32) v |= w[i + 1] << (32 - o);
-  return v & ((1u << W) - 1u);
-}
-
-// 4 * bits [P, P+W)  (a byte address into a table of dwords)
-template <int N>
-__device__ __forceinline__ uint32_t addr4_at(const uint32_t (&w)[N], int P, int W) {
-  if (P >= 2) {
-    const int Q = P - 2, i = Q >> 5, o = Q & 31;
-    uint32_t v = w[i] >> o;
-    if (o + W + 2 > 32 && i + 1 < N) v |= w[i + 1] << (32 - o);
-    return v & (((1u << W) - 1u) << 2);
-  }
-  return (w[0] << 2) & (((1u << W) - 1u) << 2);
-}
-
-template <int NDW>
-__device__ __forceinline__ void load_dwords(const uint8_t* p, uint32_t (&w)[NDW]) {
-  const uint32_t* q = reinterpret_cast<const uint32_t*>(p);
-#pragma unroll
-  for (int i = 0; i < NDW; ++i) w[i] = q[i];
 }
 
 // ---------------------------------------------------------------------------
@@ -229,20 +194,6 @@ __device__ void build_code_lut(uint8_t* lut, const uint16_t* single, int tid, in
   }
 }
 
-// entry_bytes * bits [P, P+W) of a little-endian multi-dword value: the byte
-// offset of a table entry (P, W compile-time after unrolling)
-template <int SH, int N>
-__device__ __forceinline__ uint32_t field_off(const uint32_t (&w)[N], int P, int W) {
-  const uint32_t m = ((1u << W) - 1u) << SH;
-  if (P >= SH) {
-    const int Q = P - SH, i = Q >> 5, o = Q & 31;
-    uint32_t v = w[i] >> o;
-    if (o + W + SH > 32 && i + 1 < N) v |= w[i + 1] << (32 - o);
-    return v & m;
-  }
-  return (w[0] << (SH - P)) & m;
-}
-
 // dequantise the codes at bits [P, P + 4B) (quad) into two f16x2 dwords
 template <int B, int N>
 __device__ __forceinline__ uint2 lut_quad(const uint8_t* lut, const uint32_t (&w)[N], int P) {
@@ -292,17 +243,6 @@ __device__ __forceinline__ void load_tile(TileRegs<D, BK, BV>& r, const uint8_t*
     load_dwords(base + ((uint32_t)Gm::VNORM + q * 8u), r.vn[sb]);
     r.ok[sb] = valid;
   }
-}
-
-__device__ __forceinline__ float warp_max_q(float x) {
-  x = fmaxf(x, __shfl_xor(x, 16));
-  x = fmaxf(x, __shfl_xor(x, 32));
-  return x;
-}
-__device__ __forceinline__ float warp_sum_q(float x) {
-  x += __shfl_xor(x, 16);
-  x += __shfl_xor(x, 32);
-  return x;
 }
 
 template <int D, int BK, int BV, int QT, bool SHARE>

@@ -1,0 +1,788 @@
+// vLLM v1 TURBOQUANT slot-format KV cache on gfx950: fused store and split-K
+// decode attention over the packed slots.
+//
+// Slot format (reference vllm_plugin/triton_inkernel_store.py:38-440,
+// boundary_tq_config.py:66-81, v1_backend.py:171-220), per (token, kv head),
+// byte-addressed inside kv_cache[num_blocks][block_size][Hkv][slot]:
+//   [K codes: MSE = D*KB/8][K norm f16][V codes: VDB = D*VB/8][V scale f16][V min f16][pad]
+// K codes use the library bit layout (4-bit: low nibble = even dim; 3-bit: 8
+// codes in 24 bits; 2-bit: LSB first).
+//
+// Store semantics (reference triton_inkernel_store.py:394-440, :91-100, :202-330):
+//   K: n = sqrt(sum k^2 + 1e-16); y = H (k / (n + 1e-8)) / sqrt(D) with the
+//      unsigned Sylvester butterflies; code = #{midpoints m : y >= m}; n -> f16.
+//   V (optionally rotated first, v' = dtype(v H / sqrt(D)), v1_backend.py:736-740):
+//      sc = max((max - min) / (2^VB - 1), 1e-8); q = clamp(trunc((v - min)/sc + 0.5));
+//      sc, min -> f16.
+// Decode semantics (reference triton_decode_offset.py:42-442, v1_backend.py:975-1093):
+//   q_rot = q H / sqrt(D); c^ = C[idx] / sqrt(sum C[idx]^2 + 1e-16);
+//   s_t = ||k_t||_16 <q_rot, c^_t> scale; o = softmax(s) . (q_v sc_16 + min_16);
+//   o <- o H / sqrt(D) when V was rotated; out = dtype(o).
+//
+// Decode kernel: one workgroup (4 waves) per (batch, kv head, split); a wave
+// walks 32-token tiles (two 16-token S-tiles), reading each slot's K codes,
+// K norm, V codes and V scale/min once for the whole GQA group.
+//   S^T[t][h] = K[t][:] . Q^T[:][h]   v_mfma_f32_16x16x32_f16; A = K codes as f16
+//                pairs from an LDS pair table, B = rotated query (scale*log2 e folded)
+//   Gram[t][t'] = K[t][:] . K[t'][:]   same MFMA with A = B = the K operand; its
+//                diagonal is sum C[idx]^2 for the norm correction
+//   O^T[d][h] += V^T[d][t] . P'^T[t][h]  A = V codes as f16 2^e_t (1 + q / 2^VB),
+//                taken straight from the packed bits with one shift and one
+//                and-or, e_t the exponent of the token's fp16 V scale sc_t;
+//                B = p_t * sc_t / 2^e_t (in [p, 2p)), so
+//                o = 2^VB (acc - sum p sc) + sum p * min.
+// Precision: P' and the rotated query enter the MFMAs as f16 hi + lo pairs (two
+// MFMAs each), ~22 bits: with uniform V, sc * q cancels against min, and one
+// f16 rounding of P' would show in the output.  Keeping sc's exponent in the A
+// operand keeps P' in [p, 2p) <= 2^(TAU+1): never subnormal for the tokens that
+// matter, never above the f16 range for any fp16 scale.
+// Online softmax in the log2 domain with lazy rescaling (the reference max is
+// only raised when a tile exceeds it by 2^8).  Waves merge through LDS; splits
+// merge in a second kernel that also un-rotates V and writes the output dtype.
+#include "ftq_attn_dev.h"
+#include "ftq_codec_dev.h"
+#include "ftq_internal.h"
+
+#include <cmath>
+
+namespace ftq {
+
+float fwht_scale(int d);
+
+typedef unsigned short us2 __attribute__((ext_vector_type(2)));
+
+struct V1Geom {
+  int mse, kps, vdb, raw;
+};
+__host__ __device__ constexpr V1Geom v1_geom(int d, int kb, int vb) {
+  return V1Geom{d * kb / 8, d * kb / 8 + 2, d * vb / 8, d * kb / 8 + 2 + d * vb / 8 + 4};
+}
+
+// ---------------------------------------------------------------------------
+// store
+// ---------------------------------------------------------------------------
+
+// bits [pos, pos + n) (n <= 32) of the little-endian stream of B-bit codes c[0..D)
+template <int D>
+__device__ __forceinline__ uint32_t packed_bits(const uint8_t* c, int B, int pos, int n) {
+  uint32_t r = 0;
+  const int d0 = pos / B;
+  int d1 = (pos + n - 1) / B;
+  if (d1 > D - 1) d1 = D - 1;
+  for (int d = d0; d <= d1; ++d) {
+    const int sh = d * B - pos;
+    const uint32_t v = c[d];
+    r |= sh >= 0 ? (v << sh) : (v >> -sh);
+  }
+  return n == 32 ? r : (r & ((1u << n) - 1u));
+}
+
+template <int DT>
+__device__ __forceinline__ float round_to_dtype(float x) {
+  if constexpr (DT == BF16) return bf16_bits_to_f32(f32_to_bf16_bits(x));
+  else if constexpr (DT == F16) return f16_bits_to_f32(f32_to_f16_bits(x));
+  else return x;
+}
+
+// One (token, kv head) per 16 lanes, D/16 contiguous elements per lane.
+template <int D, int DT>
+__global__ __launch_bounds__(256) void v1_store_kernel(
+    const void* __restrict__ key, const void* __restrict__ value, int64_t n_tokens, int hkv,
+    const float* __restrict__ mid_g, int kb, int vb, int v_rotate,
+    const int64_t* __restrict__ slot_mapping, uint8_t* __restrict__ cache, int64_t num_blocks,
+    int block_size, int64_t s_blk, int64_t s_pos, int64_t s_head, float rscale) {
+  constexpr int E = D / 16;
+  __shared__ uint8_t kc[16][D];
+  __shared__ uint8_t vc[16][D];
+  __shared__ float mids[16];
+  const int lane = threadIdx.x & 15, grp = threadIdx.x >> 4;
+  const int nmid = (1 << kb) - 1;
+  if ((int)threadIdx.x < nmid) mids[threadIdx.x] = mid_g[threadIdx.x];
+  __syncthreads();
+  const V1Geom g = v1_geom(D, kb, vb);
+  const int vtop = (1 << vb) - 1;
+  const int64_t nvec = n_tokens * hkv;
+
+  for (int64_t base = (int64_t)blockIdx.x * 16; base < nvec; base += (int64_t)gridDim.x * 16) {
+    const int64_t vi = base + grp;
+    bool active = vi < nvec;
+    const int64_t tok = active ? vi / hkv : 0;
+    const int head = active ? (int)(vi % hkv) : 0;
+    const int64_t slot = active ? slot_mapping[tok] : -1;
+    const int64_t blk = slot >= 0 ? slot / block_size : -1;
+    active = active && slot >= 0 && blk < num_blocks;  // negative slots are skipped
+    float nrm = 0.f, sc = 0.f, mn = 0.f;
+    if (active) {  // uniform over the 16 lanes of the vector
+      // ---- K: norm, normalise, unsigned Hadamard, midpoint search
+      float x[E];
+      load_elems<DT, E>(key, vi * D + lane * E, x);
+      float ss = 0.f;
+#pragma unroll
+      for (int i = 0; i < E; ++i) ss += x[i] * x[i];
+      ss = group_sum<16>(ss);
+      nrm = sqrtf(ss + 1e-16f);
+      const float den = nrm + 1e-8f;
+#pragma unroll
+      for (int i = 0; i < E; ++i) x[i] = x[i] / den;
+      fwht_lanes<E, 16>(x, lane);
+#pragma unroll
+      for (int i = 0; i < E; ++i) {
+        const float y = x[i] * rscale;
+        int c = 0;
+        for (int j = 0; j < nmid; ++j) c += (y >= mids[j]) ? 1 : 0;
+        kc[grp][lane * E + i] = (uint8_t)c;
+      }
+      // ---- V: optional rotation (rounded back to the value dtype), min/max quantiser
+      float v[E];
+      load_elems<DT, E>(value, vi * D + lane * E, v);
+      if (v_rotate) {
+        fwht_lanes<E, 16>(v, lane);
+#pragma unroll
+        for (int i = 0; i < E; ++i) v[i] = round_to_dtype<DT>(v[i] * rscale);
+      }
+      mn = v[0];
+      float mx = v[0];
+#pragma unroll
+      for (int i = 1; i < E; ++i) {
+        mn = fminf(mn, v[i]);
+        mx = fmaxf(mx, v[i]);
+      }
+      mn = fminf(mn, lane_xor<1>(mn)); mx = fmaxf(mx, lane_xor<1>(mx));
+      mn = fminf(mn, lane_xor<2>(mn)); mx = fmaxf(mx, lane_xor<2>(mx));
+      mn = fminf(mn, lane_xor<4>(mn)); mx = fmaxf(mx, lane_xor<4>(mx));
+      mn = fminf(mn, lane_xor<8>(mn)); mx = fmaxf(mx, lane_xor<8>(mx));
+      sc = (vb == 1) ? (mx - mn) : (mx - mn) / (float)vtop;
+      sc = sc > 1e-8f ? sc : 1e-8f;
+#pragma unroll
+      for (int i = 0; i < E; ++i) {
+        const float t = (v[i] - mn) / sc + 0.5f;
+        // trunc toward zero, clamped; NaN -> 0
+        const int q = t >= 1.f ? (int)fminf(t, (float)vtop) : 0;
+        vc[grp][lane * E + i] = (uint8_t)q;
+      }
+    }
+    __syncthreads();
+    if (active) {
+      const int off = (int)(slot - blk * block_size);
+      uint8_t* sp = cache + blk * s_blk + off * s_pos + head * s_head;
+      for (int w = lane; w < g.mse / 4; w += 16)
+        *reinterpret_cast<uint32_t*>(sp + 4 * w) = packed_bits<D>(kc[grp], kb, 32 * w, 32);
+      for (int w = lane; w < g.vdb / 2; w += 16)
+        *reinterpret_cast<uint16_t*>(sp + g.kps + 2 * w) = (uint16_t)packed_bits<D>(vc[grp], vb, 16 * w, 16);
+      if (lane == 0) {
+        *reinterpret_cast<uint16_t*>(sp + g.mse) = (uint16_t)f32_to_f16_bits(nrm);
+        *reinterpret_cast<uint16_t*>(sp + g.kps + g.vdb) = (uint16_t)f32_to_f16_bits(sc);
+        *reinterpret_cast<uint16_t*>(sp + g.kps + g.vdb + 2) = (uint16_t)f32_to_f16_bits(mn);
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------
+// decode attention, stage 1 (per split)
+// ---------------------------------------------------------------------------
+
+template <int D, int KB, int VB>
+struct V1A {
+  static constexpr V1Geom G = v1_geom(D, KB, VB);
+  static constexpr int MSE = G.mse, KPS = G.kps, VDB = G.vdb;
+  static constexpr int KQ = MSE / 4;      // K bytes one lane reads per token
+  static constexpr int KQW = KQ / 4;      // ... in dwords
+  static constexpr int NS = D / 32;       // Q.K MFMAs per S-tile
+  static constexpr int NB = D / 16;       // P.V MFMAs per tile
+  static constexpr int NV = VB == 2 ? 4 : 8;  // V operand registers per tile
+  static_assert(D == 128, "the v1 decode kernel is laid out for head_dim 128");
+  static_assert(KQ % 4 == 0, "K lane chunk must be whole dwords");
+};
+
+template <int D, int KB, int VB>
+struct V1Tile {
+  using A = V1A<D, KB, VB>;
+  uint32_t k[2][A::KQW];  // per S-tile: K code dwords of token (lane & 15), bytes (lane >> 4) * KQ
+  uint32_t v[A::NV];      // V codes of the lane's 8 tokens (see v1_load)
+  uint32_t tail[2];       // per S-tile: K norm / V scale / V min (by lane >> 4), f16 bits
+  bool ok[2];             // wave-uniform: S-tile has a real page
+};
+
+// Loads of one 32-token tile.  Every address is a wave-uniform page base plus
+// a lane offset fixed for the whole kernel.  An S-tile past the sequence (or on
+// a bad block id) reads block 0 instead -- the loads always issue, so the wait
+// counts stay static -- and the consumer masks it.
+//   K:    lane (m, g) = token m, K bytes [g*KQ, (g+1)*KQ)
+//   tail: lane (m, g) = token m, field g (0 K norm, 1 V scale, 2 V min, 3 unused)
+//   V:    lane (m, g) = tokens 4g+i (i < 4) of each S-tile, the codes of dims
+//         8m .. 8m+7.  P.V operand pair j holds tokens (4g + 2(j&1), +1) of S-tile j/2:
+//         VB 2: v[j] = the two 16-bit chunks;  VB 4: v[j] / v[4+j] = low / high
+//         16 bits of the two 32-bit chunks;  VB 3: v[2j], v[2j+1] = 32 bits around
+//         each 24-bit chunk (starting at an even byte).
+template <int D, int KB, int VB>
+__device__ __forceinline__ void v1_load(V1Tile<D, KB, VB>& r, const uint8_t* __restrict__ cache,
+                                        const int32_t* __restrict__ bt_row, int tile, int seq_len,
+                                        int bs, int max_blocks, int64_t num_blocks, int64_t s_blk,
+                                        int64_t s_pos, int64_t kvh_off, uint32_t koff, uint32_t toff,
+                                        const uint32_t (&voff)[4], bool active) {
+#pragma unroll
+  for (int st = 0; st < 2; ++st) {
+    const int pos0 = tile * 32 + st * 16;
+    const int page = pos0 / bs;
+    int64_t phys = (active && pos0 < seq_len && page < max_blocks) ? (int64_t)bt_row[page] : -1;
+    const bool valid = phys >= 0 && phys < num_blocks;
+    if (!valid) phys = 0;
+    const int64_t within = valid ? (int64_t)(pos0 - page * bs) : 0;
+    const uint8_t* bst = cache + (phys * s_blk + within * s_pos + kvh_off);
+    load_dwords(bst + koff, r.k[st]);
+    r.tail[st] = *reinterpret_cast<const uint16_t*>(bst + toff);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint8_t* p = bst + voff[i];
+      if constexpr (VB == 2) {
+        const uint32_t h = *reinterpret_cast<const uint16_t*>(p);
+        if (i & 1) r.v[2 * st + (i >> 1)] |= h << 16;
+        else r.v[2 * st + (i >> 1)] = h;
+      } else if constexpr (VB == 4) {
+        const uint32_t lo = *reinterpret_cast<const uint16_t*>(p);
+        const uint32_t hi = *reinterpret_cast<const uint16_t*>(p + 2);
+        if (i & 1) {
+          r.v[2 * st + (i >> 1)] |= lo << 16;
+          r.v[4 + 2 * st + (i >> 1)] |= hi << 16;
+        } else {
+          r.v[2 * st + (i >> 1)] = lo;
+          r.v[4 + 2 * st + (i >> 1)] = hi;
+        }
+      } else {
+        const uint32_t lo = *reinterpret_cast<const uint16_t*>(p);
+        const uint32_t hi = *reinterpret_cast<const uint16_t*>(p + 2);
+        r.v[4 * st + i] = lo | (hi << 16);
+      }
+    }
+    r.ok[st] = valid;
+  }
+}
+
+// f16 pair (1 + q_a / 2^VB, 1 + q_b / 2^VB) for dim 8m + bb of the two tokens of pair j
+// ex = the two tokens' f16 exponent fields (2^e_t (1 + q / 2^VB) once the code
+// bits fill the top of the mantissa)
+template <int VB, int NV>
+__device__ __forceinline__ uint32_t v1_vpair(const uint32_t (&v)[NV], const uint32_t (&w)[8], int j, int bb,
+                                             uint32_t ex) {
+  const uint32_t ONE2 = ex;
+  if constexpr (VB == 2) {
+    const int sh = 8 - 2 * bb;
+    const uint32_t x = sh >= 0 ? (v[j] << sh) : (v[j] >> -sh);
+    return (x & 0x03000300u) | ONE2;
+  } else if constexpr (VB == 4) {
+    const uint32_t X = bb < 4 ? v[j] : v[4 + j];
+    const int sh = 6 - 4 * (bb & 3);
+    const uint32_t x = sh >= 0 ? (X << sh) : (X >> -sh);
+    return (x & 0x03C003C0u) | ONE2;
+  } else {
+    // w[2j] = bytes 0-1 of each chunk (dims 0..4 + 1 bit), w[2j+1] = bytes 1-2 (dims 3..7)
+    const uint32_t X = bb <= 2 ? w[2 * j] : w[2 * j + 1];
+    const int sh = bb <= 2 ? 7 - 3 * bb : 15 - 3 * bb;
+    const uint32_t x = sh >= 0 ? (X << sh) : (X >> -sh);
+    return (x & 0x03800380u) | ONE2;
+  }
+}
+
+__device__ __forceinline__ void wave_lds_fence() {
+  // orders this wave's LDS accesses (LDS executes in order within a wave)
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+template <int D, int KB, int VB, int QT>
+__global__ __launch_bounds__(256, 4) void v1_attn_kernel(
+    const void* __restrict__ query, const uint8_t* __restrict__ cache,
+    const int32_t* __restrict__ block_table, const int32_t* __restrict__ seq_lens,
+    const int32_t* __restrict__ kv_start, int hq, int hkv, int bs, int max_blocks,
+    int64_t num_blocks, int64_t s_blk, int64_t s_pos, int64_t s_head,
+    const float* __restrict__ cent, float qscale, int num_splits, float* __restrict__ ws_o,
+    float* __restrict__ ws_lse) {
+  using A = V1A<D, KB, VB>;
+  constexpr int NS = A::NS, NB = A::NB, E = D / 16;
+  const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int G = hq / hkv;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int m = lane & 15, g = lane >> 4;
+
+  // LDS pool, reused in three phases: rotated queries (prologue), the K code
+  // pair table (tile loop), the wave-merge buffer (epilogue)
+  constexpr int LUT_BYTES = 4 << (2 * KB);
+  constexpr int RED_BYTES = 4 * 16 * (D + 1) * 4;
+  constexpr int QS_BYTES = 16 * (D + 4) * 4;
+  constexpr int POOL0 = LUT_BYTES > RED_BYTES ? LUT_BYTES : RED_BYTES;
+  constexpr int POOL = POOL0 > QS_BYTES ? POOL0 : QS_BYTES;
+  __shared__ __attribute__((aligned(16))) uint8_t pool[POOL];
+  __shared__ float red_m[4][16], red_l[4][16];
+  __shared__ __attribute__((aligned(16))) uint16_t tail_l[4][2][4][16];
+  __shared__ __attribute__((aligned(16))) float diag_l[4][2][16];
+  __shared__ uint16_t cent16[16];
+  float (*qs)[D + 4] = reinterpret_cast<float (*)[D + 4]>(pool);
+  float (*red_o)[16][D + 1] = reinterpret_cast<float (*)[16][D + 1]>(pool);
+  uint8_t* lut = pool;
+
+  if (tid < (1 << KB)) cent16[tid] = (uint16_t)f32_to_f16_bits(cent[tid]);
+  // q_rot = q H / sqrt(D) for the G query heads of this kv head (one per 16 lanes),
+  // with scale * log2(e) folded in
+  {
+    const int gg = tid >> 4, l16 = tid & 15;
+    if (gg < G) {
+      float y[E];
+      load_elems<QT, E>(query, ((int64_t)b * hq + kvh * G + gg) * D + l16 * E, y);
+      fwht_lanes<E, 16>(y, l16);
+#pragma unroll
+      for (int i = 0; i < E; ++i) qs[gg][l16 * E + i] = y[i] * qscale;
+    }
+  }
+  __syncthreads();
+  // B operand of the Q.K MFMAs (f16 hi + lo): lane (n, g), MFMA s -> Q[n][g*D/4 + 8s + j]
+  Op8 qb[NS], ql[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      uint32_t wh = 0, wl = 0;
+      if (m < G) {
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const float x = qs[m][g * (D / 4) + 8 * s + 2 * j + e];
+          const _Float16 hi = (_Float16)x;
+          const _Float16 lo = (_Float16)(x - (float)hi);
+          wh |= (uint32_t)__builtin_bit_cast(uint16_t, hi) << (16 * e);
+          wl |= (uint32_t)__builtin_bit_cast(uint16_t, lo) << (16 * e);
+        }
+      }
+      qb[s].u[j] = wh;
+      ql[s].u[j] = wl;
+    }
+  }
+  __syncthreads();  // qs is dead; its LDS now holds the pair table
+  for (int e = tid; e < (1 << (2 * KB)); e += 256)
+    reinterpret_cast<uint32_t*>(lut)[e] = (uint32_t)cent16[e & ((1 << KB) - 1)] | ((uint32_t)cent16[e >> KB] << 16);
+  __syncthreads();
+
+  const int seq_len = seq_lens[b];
+  int k0 = kv_start ? kv_start[b] : 0;
+  if (k0 < 0) k0 = 0;
+  const int t_first = k0 >> 5;
+  const int t_last = (seq_len + 31) >> 5;
+  const int n_tiles = t_last > t_first ? t_last - t_first : 0;
+  const int tps = (n_tiles + num_splits - 1) / num_splits;
+  const int t_begin = t_first + split * tps;
+  const int t_end = min(t_begin + tps, t_last);
+  const int32_t* bt_row = block_table + (int64_t)b * max_blocks;
+  const int64_t kvh_off = (int64_t)kvh * s_head;
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+
+  // lane offsets (fixed for the kernel)
+  const uint32_t sp = (uint32_t)s_pos;
+  const uint32_t koff = (uint32_t)m * sp + (uint32_t)(g * A::KQ);
+  const uint32_t toff = (uint32_t)m * sp +
+                        (uint32_t)(g == 1 ? A::KPS + A::VDB : (g == 2 ? A::KPS + A::VDB + 2 : A::MSE));
+  const uint32_t vch = VB == 3 ? (uint32_t)((A::KPS + 3 * m) & ~1) : (uint32_t)(A::KPS + VB * m);
+  uint32_t voff[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) voff[i] = (uint32_t)(4 * g + i) * sp + vch;
+  // VB 3: byte selectors that re-align each chunk to its first code bit
+  const uint32_t o3 = (uint32_t)((A::KPS + 3 * m) & 1);
+  const uint32_t sel0 = o3 | ((o3 + 1) << 8) | ((o3 + 4) << 16) | ((o3 + 5) << 24);
+  const uint32_t sel1 = (o3 + 1) | ((o3 + 2) << 8) | ((o3 + 5) << 16) | ((o3 + 6) << 24);
+
+  float m_run = -INFINITY, l_run = 0.f, z_run = 0.f, u_run = 0.f;
+  floatx4 acc[NB];
+#pragma unroll
+  for (int i = 0; i < NB; ++i) acc[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  constexpr float TAU = 8.f;  // p <= 2^TAU
+  auto process = [&](const V1Tile<D, KB, VB>& cur, int tile) __attribute__((always_inline)) {
+    // scores and Gram diagonal per S-tile; the per-token fields (K norm, V
+    // scale, V min, sum C^2) go to the score layout (lane (n, g) holds tokens
+    // 4g+i) through LDS
+    floatx4 sacc[2];
+    wave_lds_fence();
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      sacc[st] = floatx4{0.f, 0.f, 0.f, 0.f};
+      floatx4 gacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        Op8 a;
+#pragma unroll
+        for (int p = 0; p < 4; ++p)
+          a.u[p] = *reinterpret_cast<const uint32_t*>(lut + field_off<2>(cur.k[st], (8 * s + 2 * p) * KB, 2 * KB));
+        sacc[st] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a.h, qb[s].h, sacc[st], 0, 0, 0);
+        sacc[st] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a.h, ql[s].h, sacc[st], 0, 0, 0);
+        gacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a.h, a.h, gacc, 0, 0, 0);
+      }
+      tail_l[wave][st][g][m] = (uint16_t)cur.tail[st];
+      if ((m >> 2) == g) {
+        const int i = m & 3;
+        diag_l[wave][st][m] = i == 0 ? gacc[0] : i == 1 ? gacc[1] : i == 2 ? gacc[2] : gacc[3];
+      }
+    }
+    wave_lds_fence();
+    float s[2][4];
+    uint2 scw[2], zw[2];  // f16 pairs: tokens (4g, 4g+1), (4g+2, 4g+3)
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      const uint2 kn = *reinterpret_cast<const uint2*>(&tail_l[wave][st][0][4 * g]);
+      scw[st] = *reinterpret_cast<const uint2*>(&tail_l[wave][st][1][4 * g]);
+      zw[st] = *reinterpret_cast<const uint2*>(&tail_l[wave][st][2][4 * g]);
+      const float4 dg = *reinterpret_cast<const float4*>(&diag_l[wave][st][4 * g]);
+      const float dga[4] = {dg.x, dg.y, dg.z, dg.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t kw = (i < 2 ? kn.x : kn.y) >> (16 * (i & 1));
+        const float knf = (float)__builtin_bit_cast(_Float16, (uint16_t)kw);
+        s[st][i] = sacc[st][i] * knf * __builtin_amdgcn_rsqf(dga[i] + 1e-16f);
+      }
+    }
+    // edge tiles: positions outside [k0, seq_len) and S-tiles without a page
+    if (tile * 32 < k0 || tile * 32 + 32 > seq_len || !cur.ok[0] || !cur.ok[1]) {
+#pragma unroll
+      for (int st = 0; st < 2; ++st)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int pos = tile * 32 + st * 16 + 4 * g + i;
+          if (pos >= seq_len || pos < k0 || !cur.ok[st]) {
+            s[st][i] = -INFINITY;
+            const uint32_t keep = (i & 1) ? 0x0000FFFFu : 0xFFFF0000u;
+            if (i < 2) { scw[st].x &= keep; zw[st].x &= keep; }
+            else { scw[st].y &= keep; zw[st].y &= keep; }
+          }
+        }
+    }
+    float tmax = fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
+                       fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
+    tmax = warp_max_q(tmax);
+    if (__builtin_amdgcn_ballot_w64(tmax > m_run + TAU) != 0) {  // wave-uniform, rare
+      const float m_new = fmaxf(m_run, tmax);
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+      m_run = m_new;
+      l_run *= alpha;
+      z_run *= alpha;
+      u_run *= alpha;
+#pragma unroll
+      for (int bb = 0; bb < NB; ++bb) acc[bb] *= alpha;
+    }
+    float psum = 0.f;
+    Op8 pb, pl;
+    uint32_t ex[4];  // per P.V operand pair: the two tokens' V-scale exponent fields
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      uint32_t h16[4], l16[4];
+#pragma unroll
+      for (int hp = 0; hp < 2; ++hp) {
+        const uint32_t scp = hp ? scw[st].y : scw[st].x;
+        // exponent field clamped to [1, 29]: a zero / subnormal scale uses 2^-14
+        // and carries its value in P'; a scale >= 2^15 uses 2^14 and P' < 2^(TAU+2)
+        us2 e2 = __builtin_bit_cast(us2, scp & 0x7C007C00u);
+        e2 = __builtin_elementwise_max(e2, us2{0x0400, 0x0400});
+        e2 = __builtin_elementwise_min(e2, us2{0x7400, 0x7400});
+        const uint32_t e = __builtin_bit_cast(uint32_t, e2);
+        ex[2 * st + hp] = e;
+        const uint32_t r = 0x78007800u - e;  // f16 2^(15 - exponent field) per token
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const int i = 2 * hp + t;
+          const float p = __builtin_amdgcn_exp2f(s[st][i] - m_run);
+          psum += p;
+          const uint32_t zq = (hp ? zw[st].y : zw[st].x) >> (16 * t);
+          const float scf = (float)__builtin_bit_cast(_Float16, (uint16_t)(scp >> (16 * t)));
+          z_run = __builtin_fmaf(p, (float)__builtin_bit_cast(_Float16, (uint16_t)zq), z_run);
+          const float ps = p * scf;
+          u_run += ps;
+          const float u = ps * (float)__builtin_bit_cast(_Float16, (uint16_t)(r >> (16 * t)));
+          const _Float16 uh = (_Float16)u;
+          h16[i] = __builtin_bit_cast(uint16_t, uh);
+          l16[i] = __builtin_bit_cast(uint16_t, (_Float16)(u - (float)uh));
+        }
+      }
+      pb.u[2 * st] = h16[0] | (h16[1] << 16);
+      pb.u[2 * st + 1] = h16[2] | (h16[3] << 16);
+      pl.u[2 * st] = l16[0] | (l16[1] << 16);
+      pl.u[2 * st + 1] = l16[2] | (l16[3] << 16);
+    }
+    l_run += psum;
+    uint32_t w3[8];
+    if constexpr (VB == 3) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        w3[2 * j] = __builtin_amdgcn_perm(cur.v[2 * j + 1], cur.v[2 * j], sel0);
+        w3[2 * j + 1] = __builtin_amdgcn_perm(cur.v[2 * j + 1], cur.v[2 * j], sel1);
+      }
+    }
+#pragma unroll
+    for (int bb = 0; bb < NB; ++bb) {
+      Op8 a;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) a.u[j] = v1_vpair<VB>(cur.v, w3, j, bb, ex[j]);
+      acc[bb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a.h, pb.h, acc[bb], 0, 0, 0);
+      acc[bb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a.h, pl.h, acc[bb], 0, 0, 0);
+    }
+  };
+
+  V1Tile<D, KB, VB> ra, rb;
+  int tile = t_begin + wave_u;
+  if (tile < t_end)
+    v1_load(ra, cache, bt_row, tile, seq_len, bs, max_blocks, num_blocks, s_blk, s_pos, kvh_off, koff, toff, voff, true);
+  while (tile < t_end) {
+    v1_load(rb, cache, bt_row, tile + 4, seq_len, bs, max_blocks, num_blocks, s_blk, s_pos, kvh_off, koff, toff, voff, tile + 4 < t_end);
+    process(ra, tile);
+    tile += 4;
+    if (tile >= t_end) break;
+    v1_load(ra, cache, bt_row, tile + 4, seq_len, bs, max_blocks, num_blocks, s_blk, s_pos, kvh_off, koff, toff, voff, tile + 4 < t_end);
+    process(rb, tile);
+    tile += 4;
+  }
+
+  // ---- merge the 4 waves through LDS (the pair table's LDS is reused) ----
+  __syncthreads();
+  const float l_tot = warp_sum_q(l_run);
+  const float z_tot = warp_sum_q(z_run);
+  const float u_tot = warp_sum_q(u_run);
+  if (g == 0) {
+    red_m[wave][m] = m_run;
+    red_l[wave][m] = l_tot;
+  }
+  constexpr float VSC = (float)(1 << VB);
+#pragma unroll
+  for (int bb = 0; bb < NB; ++bb)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      red_o[wave][m][8 * (4 * g + i) + bb] = __builtin_fmaf(acc[bb][i] - u_tot, VSC, z_tot);
+  __syncthreads();
+
+  const int64_t row0 = ((int64_t)b * hq + kvh * G) * num_splits + split;  // (b, head 0 of the group, split)
+  for (int idx = tid; idx < G * D; idx += 256) {
+    const int gg = idx / D, d = idx % D;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) M = fmaxf(M, red_m[w][gg]);
+    float L = 0.f, o = 0.f;
+    if (M != -INFINITY) {
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float f = __builtin_amdgcn_exp2f(red_m[w][gg] - M);
+        L += f * red_l[w][gg];
+        o += f * red_o[w][gg][d];
+      }
+    }
+    const int64_t row = row0 + (int64_t)gg * num_splits;
+    ws_o[row * D + d] = (L > 0.f) ? o / L : 0.f;
+    if (d == 0) ws_lse[row] = (L > 0.f) ? M + __builtin_log2f(L) : -INFINITY;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// decode attention, stage 2: LSE merge of the splits, V un-rotation, output cast
+// (the merge of vLLM's stage-2 kernel, v1_backend.py:1070-1093)
+// ---------------------------------------------------------------------------
+template <int D, int OT>
+__global__ __launch_bounds__(256) void v1_merge_kernel(const float* __restrict__ ws_o,
+                                                       const float* __restrict__ ws_lse, int64_t rows,
+                                                       int num_splits, int v_rotate, float rscale,
+                                                       void* __restrict__ out) {
+  constexpr int E = D / 16;
+  const int lane = threadIdx.x & 15;
+  const int64_t r = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+  if (r >= rows) return;  // whole 16-lane group exits together
+  float M = -INFINITY;
+  for (int s = 0; s < num_splits; ++s) M = fmaxf(M, ws_lse[r * num_splits + s]);
+  float y[E];
+#pragma unroll
+  for (int i = 0; i < E; ++i) y[i] = 0.f;
+  float W = 0.f;
+  if (M != -INFINITY) {
+    for (int s = 0; s < num_splits; ++s) {
+      const float w = __builtin_amdgcn_exp2f(ws_lse[r * num_splits + s] - M);
+      W += w;
+      float x[E];
+      load_elems<F32, E>(ws_o, (r * num_splits + s) * D + lane * E, x);
+#pragma unroll
+      for (int i = 0; i < E; ++i) y[i] = __builtin_fmaf(w, x[i], y[i]);
+    }
+  }
+  const float inv = (W > 0.f) ? 1.f / W : 0.f;
+#pragma unroll
+  for (int i = 0; i < E; ++i) y[i] *= inv;
+  if (v_rotate) {  // uniform
+    fwht_lanes<E, 16>(y, lane);
+#pragma unroll
+    for (int i = 0; i < E; ++i) y[i] *= rscale;
+  }
+  store_elems<OT, E>(out, r * D + lane * E, y);
+}
+
+// ---------------------------------------------------------------------------
+// host launchers
+// ---------------------------------------------------------------------------
+
+template <int D>
+static hipError_t v1_launch_store(const void* k, const void* v, int dt, int64_t n, int hkv,
+                                  const float* mids, int kb, int vb, int vrot, const int64_t* slots,
+                                  uint8_t* cache, int64_t nb, int bs, int64_t sb, int64_t sp,
+                                  int64_t sh, hipStream_t st) {
+  const int64_t nvec = n * hkv;
+  int64_t gsz = (nvec + 15) / 16;
+  if (gsz > 256 * 16) gsz = 256 * 16;
+  const float rs = fwht_scale(D);
+  dim3 grid((unsigned)gsz), block(256);
+  if (dt == F32)
+    v1_store_kernel<D, F32><<<grid, block, 0, st>>>(k, v, n, hkv, mids, kb, vb, vrot, slots, cache, nb, bs, sb, sp, sh, rs);
+  else if (dt == F16)
+    v1_store_kernel<D, F16><<<grid, block, 0, st>>>(k, v, n, hkv, mids, kb, vb, vrot, slots, cache, nb, bs, sb, sp, sh, rs);
+  else
+    v1_store_kernel<D, BF16><<<grid, block, 0, st>>>(k, v, n, hkv, mids, kb, vb, vrot, slots, cache, nb, bs, sb, sp, sh, rs);
+  return hipGetLastError();
+}
+
+struct V1Args {
+  const void* q;
+  int qt;
+  const uint8_t* cache;
+  const int32_t *bt, *sl, *ks;
+  int B, hq, hkv, bs, max_blocks;
+  int64_t nb, sblk, spos, shead;
+  const float* cent;
+  float qscale;
+  int splits, vrot;
+  float *wo, *wl;
+  void* out;
+  int ot;
+};
+
+template <int D, int KB, int VB>
+static hipError_t v1_launch_attn3(const V1Args& a, hipStream_t st) {
+  dim3 grid(a.splits, a.hkv, a.B), block(256);
+  if (a.qt == F32)
+    v1_attn_kernel<D, KB, VB, F32><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.ks, a.hq, a.hkv, a.bs, a.max_blocks, a.nb, a.sblk, a.spos, a.shead, a.cent, a.qscale, a.splits, a.wo, a.wl);
+  else if (a.qt == F16)
+    v1_attn_kernel<D, KB, VB, F16><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.ks, a.hq, a.hkv, a.bs, a.max_blocks, a.nb, a.sblk, a.spos, a.shead, a.cent, a.qscale, a.splits, a.wo, a.wl);
+  else
+    v1_attn_kernel<D, KB, VB, BF16><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.ks, a.hq, a.hkv, a.bs, a.max_blocks, a.nb, a.sblk, a.spos, a.shead, a.cent, a.qscale, a.splits, a.wo, a.wl);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int64_t rows = (int64_t)a.B * a.hq;
+  dim3 g2((unsigned)((rows + 15) / 16)), b2(256);
+  const float rs = fwht_scale(D);
+  if (a.ot == F32) v1_merge_kernel<D, F32><<<g2, b2, 0, st>>>(a.wo, a.wl, rows, a.splits, a.vrot, rs, a.out);
+  else if (a.ot == F16) v1_merge_kernel<D, F16><<<g2, b2, 0, st>>>(a.wo, a.wl, rows, a.splits, a.vrot, rs, a.out);
+  else v1_merge_kernel<D, BF16><<<g2, b2, 0, st>>>(a.wo, a.wl, rows, a.splits, a.vrot, rs, a.out);
+  return hipGetLastError();
+}
+
+template <int D, int KB>
+static hipError_t v1_launch_attn2(int vb, const V1Args& a, hipStream_t st) {
+  if (vb == 2) return v1_launch_attn3<D, KB, 2>(a, st);
+  if (vb == 3) return v1_launch_attn3<D, KB, 3>(a, st);
+  return v1_launch_attn3<D, KB, 4>(a, st);
+}
+
+int auto_splits(int batch, int hkv, int seq_hint);
+
+}  // namespace ftq
+
+using namespace ftq;
+
+extern "C" int64_t ftq_v1_slot_bytes(int d, int key_bits, int value_bits) {
+  if (!(d == 64 || d == 128 || d == 256) || key_bits < 2 || key_bits > 4 || value_bits < 2 || value_bits > 4)
+    return -1;
+  return v1_geom(d, key_bits, value_bits).raw;
+}
+
+extern "C" int ftq_v1_store(const void* key, const void* value, int dtype, int64_t n_tokens,
+                            int num_kv_heads, int d, const float* midpoints, int key_bits,
+                            int value_bits, int v_rotate, const int64_t* slot_mapping,
+                            uint8_t* kv_cache, int64_t num_blocks, int block_size,
+                            int64_t stride_block, int64_t stride_pos, int64_t stride_head,
+                            void* stream) {
+  FTQ_REQUIRE(d == 64 || d == 128 || d == 256, "v1 store: head_dim must be 64, 128 or 256");
+  FTQ_REQUIRE(key_bits >= 2 && key_bits <= 4 && value_bits >= 2 && value_bits <= 4,
+              "v1 store: key_bits and value_bits must be 2, 3 or 4");
+  FTQ_REQUIRE(n_tokens >= 0 && num_kv_heads > 0 && num_blocks >= 0 && block_size > 0,
+              "bad token / head / block counts");
+  FTQ_REQUIRE(dtype >= F32 && dtype <= BF16, "dtype must be FTQ_F32, FTQ_F16 or FTQ_BF16");
+  const V1Geom g = v1_geom(d, key_bits, value_bits);
+  FTQ_REQUIRE(stride_head >= g.raw, "stride_head is smaller than the slot bytes (see ftq_v1_slot_bytes)");
+  FTQ_REQUIRE(stride_pos >= stride_head * num_kv_heads && stride_block >= stride_pos * block_size,
+              "kv_cache strides must describe [num_blocks][block_size][num_kv_heads][slot]");
+  FTQ_REQUIRE(stride_head % 4 == 0 && stride_pos % 4 == 0 && stride_block % 4 == 0,
+              "kv_cache strides must be multiples of 4 bytes");
+  if (n_tokens == 0) return FTQ_OK;
+  FTQ_REQUIRE(key && value && midpoints && slot_mapping && kv_cache, "null pointer argument");
+  FTQ_REQUIRE(aligned16(key) && aligned16(value), "key/value must be 16-byte aligned");
+  FTQ_REQUIRE(aligned4(kv_cache), "kv_cache must be 4-byte aligned");
+  hipStream_t st = (hipStream_t)stream;
+  hipError_t e;
+  if (d == 64)
+    e = v1_launch_store<64>(key, value, dtype, n_tokens, num_kv_heads, midpoints, key_bits, value_bits, v_rotate != 0, slot_mapping, kv_cache, num_blocks, block_size, stride_block, stride_pos, stride_head, st);
+  else if (d == 128)
+    e = v1_launch_store<128>(key, value, dtype, n_tokens, num_kv_heads, midpoints, key_bits, value_bits, v_rotate != 0, slot_mapping, kv_cache, num_blocks, block_size, stride_block, stride_pos, stride_head, st);
+  else
+    e = v1_launch_store<256>(key, value, dtype, n_tokens, num_kv_heads, midpoints, key_bits, value_bits, v_rotate != 0, slot_mapping, kv_cache, num_blocks, block_size, stride_block, stride_pos, stride_head, st);
+  return hip_status(e);
+}
+
+extern "C" int64_t ftq_v1_workspace_bytes(int batch, int num_q_heads, int d, int num_splits) {
+  if (batch < 0 || num_q_heads < 0 || d <= 0 || num_splits <= 0) return -1;
+  return (int64_t)batch * num_q_heads * num_splits * (d + 1) * 4;
+}
+
+extern "C" int ftq_v1_default_splits(int batch, int num_kv_heads, int max_seq_len) {
+  return auto_splits(batch, num_kv_heads, max_seq_len);
+}
+
+extern "C" int ftq_v1_decode_attention(
+    const void* query, int q_dtype, const uint8_t* kv_cache, int64_t num_blocks, int block_size,
+    int64_t stride_block, int64_t stride_pos, int64_t stride_head, const int32_t* block_table,
+    int max_blocks_per_seq, const int32_t* seq_lens, const int32_t* kv_start, int batch,
+    int num_q_heads, int num_kv_heads, int d, const float* centroids, int key_bits,
+    int value_bits, float scale, int v_rotate, int num_splits, void* workspace,
+    int64_t workspace_bytes, void* out, int out_dtype, void* stream) {
+  FTQ_REQUIRE(d == 128, "v1 decode attention: head_dim must be 128");
+  FTQ_REQUIRE(key_bits >= 2 && key_bits <= 4 && value_bits >= 2 && value_bits <= 4,
+              "v1 decode attention: key_bits and value_bits must be 2, 3 or 4");
+  FTQ_REQUIRE(block_size >= 16 && block_size % 16 == 0, "block_size must be a multiple of 16");
+  FTQ_REQUIRE(batch >= 0 && num_kv_heads > 0 && num_q_heads > 0 && num_blocks >= 0,
+              "bad batch / head / block counts");
+  FTQ_REQUIRE(num_q_heads % num_kv_heads == 0, "num_q_heads must be a multiple of num_kv_heads");
+  FTQ_REQUIRE(num_q_heads / num_kv_heads <= 16, "GQA group (num_q_heads / num_kv_heads) must be <= 16");
+  FTQ_REQUIRE(num_splits >= 1 && num_splits <= 1024, "num_splits must be in [1, 1024]");
+  FTQ_REQUIRE(max_blocks_per_seq >= 0, "max_blocks_per_seq must be >= 0");
+  FTQ_REQUIRE(q_dtype >= F32 && q_dtype <= BF16 && out_dtype >= F32 && out_dtype <= BF16,
+              "dtype must be FTQ_F32, FTQ_F16 or FTQ_BF16");
+  const V1Geom g = v1_geom(d, key_bits, value_bits);
+  FTQ_REQUIRE(stride_head >= g.raw, "stride_head is smaller than the slot bytes (see ftq_v1_slot_bytes)");
+  FTQ_REQUIRE(stride_pos >= stride_head * num_kv_heads && stride_block >= stride_pos * block_size,
+              "kv_cache strides must describe [num_blocks][block_size][num_kv_heads][slot]");
+  FTQ_REQUIRE(stride_head % 4 == 0 && stride_pos % 4 == 0 && stride_block % 4 == 0,
+              "kv_cache strides must be multiples of 4 bytes");
+  FTQ_REQUIRE(stride_pos * 16 < ((int64_t)1 << 31), "stride_pos too large");
+  if (batch == 0) return FTQ_OK;
+  FTQ_REQUIRE(num_blocks >= 1, "kv_cache must hold at least one block");
+  FTQ_REQUIRE(query && kv_cache && block_table && seq_lens && centroids && workspace && out,
+              "null pointer argument");
+  FTQ_REQUIRE(workspace_bytes >= ftq_v1_workspace_bytes(batch, num_q_heads, d, num_splits),
+              "workspace too small (see ftq_v1_workspace_bytes)");
+  FTQ_REQUIRE(aligned16(query) && aligned16(out) && aligned16(workspace) && aligned4(kv_cache),
+              "query, out and workspace must be 16-byte aligned, kv_cache 4-byte aligned");
+  V1Args a;
+  a.q = query; a.qt = q_dtype; a.cache = kv_cache; a.bt = block_table; a.sl = seq_lens; a.ks = kv_start;
+  a.B = batch; a.hq = num_q_heads; a.hkv = num_kv_heads; a.bs = block_size; a.max_blocks = max_blocks_per_seq;
+  a.nb = num_blocks; a.sblk = stride_block; a.spos = stride_pos; a.shead = stride_head;
+  a.cent = centroids;
+  a.qscale = fwht_scale(d) * scale * 1.4426950408889634f;
+  a.splits = num_splits; a.vrot = v_rotate != 0;
+  a.wo = static_cast<float*>(workspace);
+  a.wl = a.wo + (int64_t)batch * num_q_heads * num_splits * d;
+  a.out = out; a.ot = out_dtype;
+  hipStream_t st = (hipStream_t)stream;
+  hipError_t e;
+  if (key_bits == 2) e = v1_launch_attn2<128, 2>(value_bits, a, st);
+  else if (key_bits == 3) e = v1_launch_attn2<128, 3>(value_bits, a, st);
+  else e = v1_launch_attn2<128, 4>(value_bits, a, st);
+  return hip_status(e);
+}

@@ -1,0 +1,254 @@
+"""vLLM v1 ``TURBOQUANT`` slot-format KV cache on gfx950: fused store and
+split-K decode attention over the packed slots.
+
+The cache is vLLM's ``uint8[num_blocks, block_size, num_kv_heads, slot]``
+(reference ``vllm_plugin/v1_backend.py:171-220``); one slot holds, per
+(token, kv head),
+``[K codes d*kb/8][K norm f16][V codes d*vb/8][V scale f16][V min f16][pad]``
+(``vllm_plugin/triton_inkernel_store.py:38-330``,
+``boundary_tq_config.py:66-81``).
+
+* ``v1_store`` replaces the rotation strategy's in-kernel store for
+  ``kind=rht`` (``rotation/hadamard.py:43-58`` -> ``_launch_rht``,
+  ``triton_inkernel_store.py:554-616``) plus the V pre-rotation of
+  ``_launch_store`` (``v1_backend.py:712-749``).
+* ``v1_decode_attention`` replaces ``_decode_attention_offset_only``
+  (``v1_backend.py:975-1093``): query rotation, ``_tq_decode_stage1_offset``
+  (``triton_decode_offset.py:42-442``), the stage-2 LSE merge, the V
+  un-rotation and the output cast.
+* ``TurboQuantV1Layer`` holds what ``MatrixRotationStrategy.setup_layer``
+  keeps per layer (``rotation/matrix.py:34-42``): sorted centroids and their
+  midpoints.
+
+The centroid table of vLLM's ``get_centroids(d, bits)``
+(``v1_backend.py:624-629``) is not available here; the default is this
+library's Lloyd-Max levels for (d, bits) (reference ``core/lloyd_max.py``).
+Any sorted float32 table of 2^bits entries may be passed instead.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _lib
+from .core.lloyd_max import compute_lloyd_max_codebook
+
+_SIG = {
+    "ftq_v1_store": ["vp", "vp", "i32", "i64", "i32", "i32", "vp", "i32", "i32", "i32", "vp", "vp",
+                     "i64", "i32", "i64", "i64", "i64", "vp"],
+    "ftq_v1_decode_attention": ["vp", "i32", "vp", "i64", "i32", "i64", "i64", "i64", "vp", "i32",
+                                "vp", "vp", "i32", "i32", "i32", "i32", "vp", "i32", "i32", "f32",
+                                "i32", "i32", "vp", "i64", "vp", "i32", "vp"],
+}
+
+
+def _bind():
+    import ctypes
+    L = _lib.lib()
+    if getattr(L, "_v1_bound", False):
+        return L
+    m = {"vp": ctypes.c_void_p, "i32": ctypes.c_int, "i64": ctypes.c_int64, "f32": ctypes.c_float}
+    for name, sig in _SIG.items():
+        fn = getattr(L, name)
+        fn.argtypes = [m[t] for t in sig]
+        fn.restype = ctypes.c_int
+    L.ftq_v1_slot_bytes.restype = ctypes.c_int64
+    L.ftq_v1_slot_bytes.argtypes = [ctypes.c_int] * 3
+    L.ftq_v1_workspace_bytes.restype = ctypes.c_int64
+    L.ftq_v1_workspace_bytes.argtypes = [ctypes.c_int] * 4
+    L.ftq_v1_default_splits.restype = ctypes.c_int
+    L.ftq_v1_default_splits.argtypes = [ctypes.c_int] * 3
+    L._v1_bound = True
+    return L
+
+
+def _check_bits(head_dim: int, key_bits: int, value_bits: int) -> None:
+    if head_dim not in (64, 128, 256):
+        raise ValueError(f"head_dim must be 64, 128 or 256, got {head_dim}")
+    if not (2 <= key_bits <= 4) or not (2 <= value_bits <= 4):
+        raise ValueError("key_bits and value_bits must be 2, 3 or 4")
+
+
+def slot_bytes(head_dim: int, key_bits: int, value_bits: int) -> int:
+    """Bytes of a slot that hold data: key_packed_size + value bytes + 4
+    (reference ``boundary_tq_config.py:66-81``)."""
+    _check_bits(head_dim, key_bits, value_bits)
+    return (head_dim * key_bits // 8 + 2) + (head_dim * value_bits // 8) + 4
+
+
+def host_preset_bits(key_bits: int, value_bits: int) -> tuple:
+    """(K, V) bits of the smallest stock preset whose slot fits a per-K/V bit
+    override (reference ``vllm_plugin/plugin.py:390-402``)."""
+    if key_bits <= 3 and value_bits <= 3:
+        return 3, 3
+    if key_bits <= 3 and value_bits <= 4:
+        return 3, 4
+    return 4, 4
+
+
+def slot_size(head_dim: int, key_bits: int, value_bits: int, boundary_protect: bool = False) -> int:
+    """Last-dim size of the cache: the host preset's slot bytes rounded up to a
+    power of two, at least 2*head_dim bf16 elements worth when boundary
+    protection shares the allocation (reference ``v1_backend.py:171-209``)."""
+    hk, hv = host_preset_bits(key_bits, value_bits)
+    raw = slot_bytes(head_dim, hk, hv)
+    if boundary_protect:
+        raw = max(raw, 2 * head_dim)
+    return 1 << (raw - 1).bit_length()
+
+
+def get_kv_cache_shape(num_blocks: int, block_size: int, num_kv_heads: int, head_size: int,
+                       key_bits: int = 4, value_bits: int = 4) -> tuple:
+    """(num_blocks, block_size, num_kv_heads, slot) (reference ``v1_backend.py:211-220``)."""
+    return (num_blocks, block_size, num_kv_heads, slot_size(head_size, key_bits, value_bits))
+
+
+def default_centroids(head_dim: int, bits: int, device=None) -> torch.Tensor:
+    """Sorted float32 Lloyd-Max levels for the coordinate distribution at head_dim."""
+    _, levels = compute_lloyd_max_codebook(head_dim, bits)
+    c = torch.as_tensor(levels, dtype=torch.float32)
+    return torch.sort(c).values.to(device) if device is not None else torch.sort(c).values
+
+
+def midpoints_of(centroids: torch.Tensor) -> torch.Tensor:
+    """(c[i] + c[i+1]) / 2 of the sorted table (reference ``rotation/matrix.py:38-41``)."""
+    c = torch.sort(centroids.to(torch.float32)).values
+    return (c[:-1] + c[1:]) / 2
+
+
+def _strides(kv_cache: torch.Tensor):
+    if kv_cache.dtype != torch.uint8 or kv_cache.dim() != 4:
+        raise ValueError("kv_cache must be uint8 [num_blocks, block_size, num_kv_heads, slot]")
+    if kv_cache.stride(3) != 1:
+        raise ValueError("kv_cache slot bytes must be contiguous")
+    return kv_cache.stride(0), kv_cache.stride(1), kv_cache.stride(2)
+
+
+def v1_store(key: torch.Tensor, value: torch.Tensor, kv_cache: torch.Tensor,
+             slot_mapping: torch.Tensor, midpoints: torch.Tensor, key_bits: int,
+             value_bits: int, v_rotate: bool = False) -> None:
+    """Quantise ``key``/``value`` [n, Hkv, d] into their slots (``slot_mapping`` [n]
+    int64; negative entries are skipped)."""
+    n, hkv, d = key.shape
+    _check_bits(d, key_bits, value_bits)
+    if value.shape != key.shape:
+        raise ValueError("key and value shapes differ")
+    nb, bs, hk2, slot = kv_cache.shape
+    if hk2 != hkv:
+        raise ValueError("kv_cache num_kv_heads does not match key")
+    if slot < slot_bytes(d, key_bits, value_bits):
+        raise ValueError("kv_cache slot is smaller than the slot bytes for these bits")
+    if slot_mapping.dtype != torch.int64 or slot_mapping.numel() != n:
+        raise ValueError("slot_mapping must be int64 with one entry per token")
+    if midpoints.numel() != (1 << key_bits) - 1:
+        raise ValueError("midpoints must have 2^key_bits - 1 entries")
+    dev = _lib.require_device(key, value, kv_cache, slot_mapping, midpoints)
+    k = key.contiguous()
+    if k.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+        k = k.float()
+    v = value.to(k.dtype).contiguous()
+    sb, sp, sh = _strides(kv_cache)
+    mids = midpoints.to(torch.float32).contiguous()
+    L = _bind()
+    _lib.check(L.ftq_v1_store(
+        k.data_ptr(), v.data_ptr(), _lib.dtype_code(k.dtype), n, hkv, d, mids.data_ptr(),
+        key_bits, value_bits, int(bool(v_rotate)), slot_mapping.contiguous().data_ptr(),
+        kv_cache.data_ptr(), nb, bs, sb, sp, sh, _lib.stream_ptr(dev)))
+
+
+def default_splits(batch: int, num_kv_heads: int, max_seq_len: int) -> int:
+    return int(_bind().ftq_v1_default_splits(batch, num_kv_heads, max_seq_len))
+
+
+def workspace_bytes(batch: int, num_q_heads: int, head_dim: int, num_splits: int) -> int:
+    return int(_bind().ftq_v1_workspace_bytes(batch, num_q_heads, head_dim, num_splits))
+
+
+def v1_decode_attention(query: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.Tensor,
+                        seq_lens: torch.Tensor, centroids: torch.Tensor, key_bits: int,
+                        value_bits: int, scale: float | None = None, v_rotate: bool = False,
+                        kv_start: torch.Tensor | None = None, num_splits: int | None = None,
+                        max_seq_len: int | None = None, out: torch.Tensor | None = None,
+                        workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """query [B, Hq, d] -> [B, Hq, d] (query dtype unless ``out`` is given).
+
+    Attends positions [kv_start[b], seq_lens[b]) of block-table row b
+    (``kv_start`` None = 0, reference ``triton_decode_offset.py:95-106``).
+    ``num_splits`` defaults to a value that fills the GPU (pass ``max_seq_len``
+    to size it without reading ``block_table``'s width); ``workspace`` (uint8,
+    >= ``workspace_bytes``) may be preallocated for graph capture.
+    """
+    B, hq, d = query.shape
+    _check_bits(d, key_bits, value_bits)
+    if d != 128:
+        raise ValueError("v1 decode attention supports head_dim 128")
+    nb, bs, hkv, slot = kv_cache.shape
+    if slot < slot_bytes(d, key_bits, value_bits):
+        raise ValueError("kv_cache slot is smaller than the slot bytes for these bits")
+    if block_table.dtype != torch.int32 or seq_lens.dtype != torch.int32:
+        raise ValueError("block_table and seq_lens must be int32")
+    if block_table.dim() != 2 or block_table.shape[0] != B or seq_lens.numel() != B:
+        raise ValueError("block_table must be [B, max_blocks] and seq_lens [B]")
+    if kv_start is not None and (kv_start.dtype != torch.int32 or kv_start.numel() != B):
+        raise ValueError("kv_start must be int32 [B]")
+    if centroids.numel() != (1 << key_bits):
+        raise ValueError("centroids must have 2^key_bits entries")
+    tensors = [query, kv_cache, block_table, seq_lens, centroids] + ([kv_start] if kv_start is not None else [])
+    dev = _lib.require_device(*tensors)
+    q = query.contiguous()
+    if q.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+        q = q.float()
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    if num_splits is None:
+        msl = max_seq_len if max_seq_len is not None else block_table.shape[1] * bs
+        num_splits = default_splits(B, hkv, msl)
+    if out is None:
+        out = torch.empty(B, hq, d, dtype=q.dtype, device=dev)
+    need = workspace_bytes(B, hq, d, num_splits)
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=dev)
+    sb, sp, sh = _strides(kv_cache)
+    bt = block_table.contiguous()
+    cent = torch.sort(centroids.to(torch.float32)).values.contiguous()
+    ks = kv_start.contiguous() if kv_start is not None else None
+    L = _bind()
+    _lib.check(L.ftq_v1_decode_attention(
+        q.data_ptr(), _lib.dtype_code(q.dtype), kv_cache.data_ptr(), nb, bs, sb, sp, sh,
+        bt.data_ptr(), bt.shape[1], seq_lens.contiguous().data_ptr(),
+        ks.data_ptr() if ks is not None else None, B, hq, hkv, d, cent.data_ptr(), key_bits,
+        value_bits, float(scale), int(bool(v_rotate)), int(num_splits), workspace.data_ptr(),
+        workspace.numel(), out.data_ptr(), _lib.dtype_code(out.dtype), _lib.stream_ptr(dev)))
+    return out
+
+
+class TurboQuantV1Layer:
+    """Per-layer state of the v1 backend for ``kind=rht``: sorted centroids and
+    midpoints (reference ``rotation/matrix.py:34-42``), bit widths and the
+    V-rotation switch (``TURBOQUANT_V_ROTATE``, ``v1_backend.py:733-740``)."""
+
+    def __init__(self, head_dim: int, key_bits: int, value_bits: int, v_rotate: bool = False,
+                 centroids: torch.Tensor | None = None, device="cuda"):
+        _check_bits(head_dim, key_bits, value_bits)
+        self.head_dim = head_dim
+        self.key_bits = key_bits
+        self.value_bits = value_bits
+        self.v_rotate = bool(v_rotate)
+        c = centroids if centroids is not None else default_centroids(head_dim, key_bits)
+        if c.numel() != (1 << key_bits):
+            raise ValueError("centroids must have 2^key_bits entries")
+        self.centroids = torch.sort(c.to(torch.float32)).values.to(device)
+        self.midpoints = midpoints_of(self.centroids)
+
+    def kv_cache_shape(self, num_blocks: int, block_size: int, num_kv_heads: int) -> tuple:
+        return get_kv_cache_shape(num_blocks, block_size, num_kv_heads, self.head_dim,
+                                  self.key_bits, self.value_bits)
+
+    def store(self, key, value, kv_cache, slot_mapping) -> None:
+        v1_store(key, value, kv_cache, slot_mapping, self.midpoints, self.key_bits,
+                 self.value_bits, self.v_rotate)
+
+    def decode(self, query, kv_cache, block_table, seq_lens, **kw) -> torch.Tensor:
+        return v1_decode_attention(query, kv_cache, block_table, seq_lens, self.centroids,
+                                   self.key_bits, self.value_bits, v_rotate=self.v_rotate, **kw)

@@ -116,6 +116,62 @@ int ftq_paged_decode_attention(const void* query, int q_dtype, const uint8_t* kv
                                int bits_k, int bits_v, float scale, int num_splits, void* workspace,
                                int64_t workspace_bytes, void* out, int out_dtype, void* stream);
 
+/* ---- vLLM v1 TURBOQUANT slot format ------------------------------------
+ * kv_cache uint8 [num_blocks][block_size][num_kv_heads][slot] (strides in
+ * bytes); per (token, kv head) slot:
+ *   [K codes d*kb/8][K norm f16][V codes d*vb/8][V scale f16][V min f16][pad]
+ * (reference vllm_plugin/triton_inkernel_store.py:38-330,
+ * boundary_tq_config.py:66-81, v1_backend.py:171-220).
+ */
+
+/* Bytes of a slot that hold data (key_packed_size + value bytes + 4), or -1
+ * for an unsupported shape.  Replaces BoundaryTurboQuantConfig.key_packed_size /
+ * value_data_bytes (boundary_tq_config.py:66-81); the slot stride itself is the
+ * caller's (v1_backend.py:171-209 rounds it up to a power of two). */
+int64_t ftq_v1_slot_bytes(int d, int key_bits, int value_bits);
+
+/*
+ * Store n_tokens x num_kv_heads K/V vectors ([n][Hkv][d], dtype) into their
+ * slots: K normalised, rotated by the unsigned Hadamard H/sqrt(d), quantised
+ * against `midpoints` (2^key_bits - 1 sorted float32; code = number of
+ * midpoints <= y), norm stored fp16; V (rotated first and rounded back to
+ * dtype when v_rotate) quantised uniformly between its min and max.
+ * slot_mapping[i] < 0 skips token i.  Replaces _launch_rht / _fused_store_rht
+ * (vllm_plugin/triton_inkernel_store.py:376-440, 554-616) and the V
+ * pre-rotation of _launch_store (v1_backend.py:712-749).  One launch.
+ */
+int ftq_v1_store(const void* key, const void* value, int dtype, int64_t n_tokens,
+                 int num_kv_heads, int d, const float* midpoints, int key_bits, int value_bits,
+                 int v_rotate, const int64_t* slot_mapping, uint8_t* kv_cache,
+                 int64_t num_blocks, int block_size, int64_t stride_block, int64_t stride_pos,
+                 int64_t stride_head, void* stream);
+
+/* Workspace bytes ftq_v1_decode_attention needs: batch*Hq*splits*(d+1)*4. */
+int64_t ftq_v1_workspace_bytes(int batch, int num_q_heads, int d, int num_splits);
+/* Split-K factor that fills the GPU for this shape (host-side heuristic). */
+int ftq_v1_default_splits(int batch, int num_kv_heads, int max_seq_len);
+
+/*
+ * Decode attention over the slot cache, one query token per sequence:
+ * positions [kv_start[b], seq_lens[b]) of block_table row b (kv_start may be
+ * NULL = 0), kv head = h / (Hq/Hkv); scores use the rotated query q H/sqrt(d)
+ * against the norm-corrected centroids (2^key_bits sorted float32) times the
+ * fp16 K norm; V = code * scale + min; with v_rotate the output is multiplied
+ * by H/sqrt(d).  Rows with no positions give 0.  Replaces the stage-1 kernel
+ * _tq_decode_stage1_offset (vllm_plugin/triton_decode_offset.py:42-442), the
+ * stage-2 merge, the un-rotation and the output cast of
+ * _decode_attention_offset_only (v1_backend.py:975-1093).  Head dim 128.
+ * Two launches on `stream`: split-K stage 1, then merge.
+ */
+int ftq_v1_decode_attention(const void* query, int q_dtype, const uint8_t* kv_cache,
+                            int64_t num_blocks, int block_size, int64_t stride_block,
+                            int64_t stride_pos, int64_t stride_head, const int32_t* block_table,
+                            int max_blocks_per_seq, const int32_t* seq_lens,
+                            const int32_t* kv_start, int batch, int num_q_heads, int num_kv_heads,
+                            int d, const float* centroids, int key_bits, int value_bits,
+                            float scale, int v_rotate, int num_splits, void* workspace,
+                            int64_t workspace_bytes, void* out, int out_dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -339,3 +339,199 @@ def paged_unpack(cache: np.ndarray, d: int, bk: int, bv: int):
     page = nsub * 16
     return (kc.reshape(nb, hkv, page, d), vc.reshape(nb, hkv, page, d),
             kn.reshape(nb, hkv, page), vn.reshape(nb, hkv, page))
+
+
+# --------------------------------------------------------------------------
+# vLLM v1 TURBOQUANT slot format
+# store:  reference vllm_plugin/triton_inkernel_store.py:38-440 (_fused_store_rht
+#         + _bucketize_pack_norm_v_store), v1_backend.py:712-749 (v_rotate)
+# decode: reference vllm_plugin/triton_decode_offset.py:42-442 (stage 1),
+#         v1_backend.py:975-1093 (stage 2 merge, un-rotation, output cast)
+# geometry: reference boundary_tq_config.py:66-81, v1_backend.py:171-220
+# --------------------------------------------------------------------------
+
+
+def v1_geometry(d: int, kb: int, vb: int) -> dict:
+    """Byte offsets inside one (token, kv head) slot.
+
+    ``[K codes: mse][K norm f16][V codes: vdb][V scale f16][V zero f16][pad]``;
+    key_packed_size = mse + 2 (boundary_tq_config.py:66-75), value data bytes =
+    ceil(d * vb / 8) (:77-81), raw = kps + vdb + 4, slot = next power of 2
+    (v1_backend.py:206-209, boundary protection off).
+    """
+    mse = -(-d * kb // 8)
+    kps = mse + 2
+    vdb = d if vb == 8 else -(-d * vb // 8)
+    raw = kps + vdb + 4
+    slot = 1 << (raw - 1).bit_length()
+    return dict(mse=mse, kps=kps, vdb=vdb, raw=raw, slot=slot)
+
+
+def v1_midpoints(centroids: np.ndarray) -> np.ndarray:
+    """Sorted centroids -> float32 midpoints (c[i] + c[i+1]) / 2
+    (reference rotation/matrix.py:34-42)."""
+    c = np.sort(np.asarray(centroids, np.float32))
+    return ((c[:-1] + c[1:]) / np.float32(2)).astype(np.float32)
+
+
+def v1_quantize_k(y: np.ndarray, midpoints: np.ndarray) -> np.ndarray:
+    """Binary search over the midpoints with ``y >= m`` going up
+    (triton_inkernel_store.py:91-100): the number of midpoints <= y."""
+    m = np.asarray(midpoints, np.float32)
+    return np.searchsorted(m, np.asarray(y, np.float32), side="right").astype(np.uint8)
+
+
+def v1_k_rotate(k: np.ndarray):
+    """K path before the quantiser (triton_inkernel_store.py:406-430):
+    norm = sqrt(sum k^2 + 1e-16); x = k / (norm + 1e-8); y = H x / sqrt(d)
+    (Sylvester butterflies, no random signs).  Returns (y f32, norm f32)."""
+    k = np.asarray(k, np.float32)
+    d = k.shape[-1]
+    k64 = k.astype(np.float64)
+    norm = np.sqrt(np.sum(k64 * k64, axis=-1) + 1e-16).astype(np.float32)
+    x = (k / (norm[..., None] + np.float32(1e-8))).astype(np.float32)
+    y = (fwht_unscaled(x) * fwht_scale(d)).astype(np.float32)
+    return y, norm
+
+
+def v1_quantize_v(v: np.ndarray, vb: int):
+    """Per-vector uniform min/max quantiser (triton_inkernel_store.py:202-330).
+
+    Returns (codes u8, scale f32, min f32, t f32) where t = (v - mn) / sc + 0.5
+    is the value truncated to the code (kept for tie accounting).
+    """
+    v = np.asarray(v, np.float32)
+    mn = v.min(axis=-1)
+    mx = v.max(axis=-1)
+    top = (1 << vb) - 1
+    if vb == 1:
+        sc = (mx - mn).astype(np.float32)
+    else:
+        sc = ((mx - mn) / np.float32(top)).astype(np.float32)
+    sc = np.where(sc > np.float32(1e-8), sc, np.float32(1e-8)).astype(np.float32)
+    t = (((v - mn[..., None]).astype(np.float32) / sc[..., None]).astype(np.float32) + np.float32(0.5)).astype(np.float32)
+    q = np.clip(np.trunc(t), 0, top).astype(np.uint8)
+    return q, sc, mn, t
+
+
+def v1_round_dtype(x: np.ndarray, dtype: str) -> np.ndarray:
+    """float32 -> value dtype -> float32 (round to nearest even)."""
+    x = np.asarray(x, np.float32)
+    if dtype == "f32":
+        return x
+    if dtype == "f16":
+        return x.astype(np.float16).astype(np.float32)
+    if dtype == "bf16":
+        u = x.view(np.uint32).astype(np.uint64)
+        r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+        nan = np.isnan(x)
+        out = r.astype(np.uint32).view(np.float32)
+        return np.where(nan, x, out).astype(np.float32)
+    raise ValueError(dtype)
+
+
+def v1_store(key: np.ndarray, value: np.ndarray, slot_mapping: np.ndarray, kv_cache: np.ndarray,
+             midpoints: np.ndarray, kb: int, vb: int, v_rotate: bool = False,
+             value_dtype: str = "f32"):
+    """Write [N, H, d] float32 K/V (already converted from their dtype) into
+    ``kv_cache`` uint8[nb, bs, H, slot] in place.  Negative slots are skipped
+    (triton_inkernel_store.py:394-395).  With ``v_rotate`` V is first rotated
+    by M = H/sqrt(d) and rounded back to the value dtype (v1_backend.py:736-740).
+
+    Returns a dict of per-(token, head) intermediates for tie accounting.
+    """
+    key = np.asarray(key, np.float32)
+    value = np.asarray(value, np.float32)
+    N, H, d = key.shape
+    nb, bs, Hc, slot = kv_cache.shape
+    assert Hc == H
+    g = v1_geometry(d, kb, vb)
+    y, norm = v1_k_rotate(key)
+    kcodes = v1_quantize_k(y, midpoints)
+    if v_rotate:
+        value = v1_round_dtype((fwht_unscaled(value) * fwht_scale(d)).astype(np.float32), value_dtype)
+    vq, sc, mn, t = v1_quantize_v(value, vb)
+    kp = pack(kcodes, kb)
+    vp = pack(vq, vb)
+    n16 = norm.astype(np.float16).view(np.uint8).reshape(N, H, 2)
+    sc16 = sc.astype(np.float16).view(np.uint8).reshape(N, H, 2)
+    mn16 = mn.astype(np.float16).view(np.uint8).reshape(N, H, 2)
+    for i in range(N):
+        s = int(slot_mapping[i])
+        if s < 0:
+            continue
+        blk, off = divmod(s, bs)
+        row = kv_cache[blk, off]
+        row[:, 0:g["mse"]] = kp[i]
+        row[:, g["mse"]:g["kps"]] = n16[i]
+        row[:, g["kps"]:g["kps"] + g["vdb"]] = vp[i]
+        row[:, g["kps"] + g["vdb"]:g["kps"] + g["vdb"] + 2] = sc16[i]
+        row[:, g["kps"] + g["vdb"] + 2:g["raw"]] = mn16[i]
+    return dict(y=y, norm=norm, kcodes=kcodes, vcodes=vq, vscale=sc, vmin=mn, vt=t, value=value)
+
+
+def v1_unpack(kv_cache: np.ndarray, d: int, kb: int, vb: int):
+    """uint8[nb, bs, H, slot] -> (K codes, K norm f16, V codes, V scale f16,
+    V zero f16), codes [nb, bs, H, d]."""
+    g = v1_geometry(d, kb, vb)
+    c = np.asarray(kv_cache)
+    kc = unpack(c[..., :g["mse"]], kb, d)
+    kn = c[..., g["mse"]:g["kps"]].copy().view(np.float16)[..., 0]
+    vc = unpack(c[..., g["kps"]:g["kps"] + g["vdb"]], vb, d)
+    sc = c[..., g["kps"] + g["vdb"]:g["kps"] + g["vdb"] + 2].copy().view(np.float16)[..., 0]
+    zr = c[..., g["kps"] + g["vdb"] + 2:g["raw"]].copy().view(np.float16)[..., 0]
+    return kc, kn, vc, sc, zr
+
+
+def v1_dequant(kv_cache: np.ndarray, d: int, kb: int, vb: int, centroids: np.ndarray,
+               norm_correction: bool = True):
+    """Per-slot reconstructions in the rotated domain (float64):
+    K^ = ||k||_16 * c / sqrt(sum c^2 + 1e-16)  (triton_decode_offset.py:210-242),
+    V^ = q * scale_16 + zero_16               (:256-428)."""
+    kc, kn, vc, sc, zr = v1_unpack(kv_cache, d, kb, vb)
+    c = np.sort(np.asarray(centroids, np.float32)).astype(np.float64)[kc]
+    if norm_correction:
+        c = c / np.sqrt(np.sum(c * c, axis=-1, keepdims=True) + 1e-16)
+    k_hat = c * kn.astype(np.float64)[..., None]
+    v_hat = vc.astype(np.float64) * sc.astype(np.float64)[..., None] + zr.astype(np.float64)[..., None]
+    return k_hat, v_hat
+
+
+def v1_decode_attention(q: np.ndarray, kv_cache: np.ndarray, block_table: np.ndarray,
+                        seq_lens: np.ndarray, centroids: np.ndarray, kb: int, vb: int,
+                        scale: float, kv_start=None, v_rotate: bool = False,
+                        norm_correction: bool = True):
+    """Decode attention over the v1 slot cache, float64.
+
+    q [B, Hq, d] (float32 values of the query); q_rot = q @ M with
+    M = H / sqrt(d) (v1_backend.py:1004, rotation/matrix.py:44-48).  Positions
+    [kv_start[b], seq_lens[b]) of sequence b are attended
+    (triton_decode_offset.py:104-106); GQA head h reads kv head h // (Hq/Hkv).
+    Output = softmax(s) . V^, then o @ M^T when v_rotate (v1_backend.py:1086-1092).
+    Rows with no positions return zeros (this library's convention).
+    """
+    q = np.asarray(q, np.float64)
+    B, Hq, d = q.shape
+    nb, bs, Hkv, slot = kv_cache.shape
+    G = Hq // Hkv
+    M = sylvester(d) / math.sqrt(d)
+    q_rot = q @ M
+    k_hat, v_hat = v1_dequant(kv_cache, d, kb, vb, centroids, norm_correction)
+    out = np.zeros((B, Hq, d))
+    for b in range(B):
+        L = int(seq_lens[b])
+        s0 = 0 if kv_start is None else int(kv_start[b])
+        if L <= s0:
+            continue
+        pos = np.arange(s0, L)
+        blk = np.asarray(block_table[b])[pos // bs]
+        off = pos % bs
+        for h in range(Hq):
+            kk = k_hat[blk, off, h // G]
+            vv = v_hat[blk, off, h // G]
+            s = kk @ q_rot[b, h] * scale
+            s = s - s.max()
+            p = np.exp(s)
+            o = (p / p.sum()) @ vv
+            out[b, h] = (o @ M.T) if v_rotate else o
+    return out

@@ -1,0 +1,188 @@
+"""The v1 TURBOQUANT slot-format oracle pinned against the reference's stated
+byte counts and against closed forms.
+
+vLLM (``get_centroids``, the stage-2 merge kernel, ``TurboQuantConfig``) is not
+in the reference tree, so nothing here compares against vLLM outputs; each
+check below is one a plausible restatement mistake would fail.
+"""
+import math
+
+import numpy as np
+import pytest
+
+from oracle import tq_oracle as O
+
+
+@pytest.mark.parametrize("bits,raw", [(2, 70), (3, 102), (4, 134), (8, 262)])
+def test_geometry_matches_reference_slot_bytes(bits, raw):
+    # reference README.md:247-252: bytes used per slot at head_dim 128
+    g = O.v1_geometry(128, bits, bits)
+    assert g["raw"] == raw
+    assert g["kps"] == 128 * bits // 8 + 2
+
+
+def test_geometry_mixed_bits():
+    # K4V2: K region 66, V region 32 + 4 (reference boundary_tq_config.py:66-81)
+    g = O.v1_geometry(128, 4, 2)
+    assert (g["mse"], g["kps"], g["vdb"], g["raw"], g["slot"]) == (64, 66, 32, 102, 128)
+    assert O.v1_geometry(128, 4, 4)["slot"] == 256
+
+
+def test_quantize_k_is_nearest_centroid_with_upper_ties():
+    c = np.sort(np.random.default_rng(0).standard_normal(16).astype(np.float32) * 0.1)
+    m = O.v1_midpoints(c)
+    y = np.random.default_rng(1).standard_normal(4000).astype(np.float32) * 0.15
+    y = np.concatenate([y, m, np.nextafter(m, -np.inf, dtype=np.float32)])
+    got = O.v1_quantize_k(y, m)
+    # brute force: nearest centroid; at an exact midpoint the upper one
+    dist = np.abs(y[:, None].astype(np.float64) - c[None, :].astype(np.float64))
+    mids64 = m.astype(np.float64)
+    want = np.argmin(dist, axis=1)
+    on_mid = np.isin(y.astype(np.float64), mids64)
+    idx_mid = np.searchsorted(mids64, y.astype(np.float64))
+    want = np.where(on_mid, idx_mid + 1, want)
+    # away from midpoints the float32 midpoint rounding cannot move the answer
+    assert np.array_equal(got, want)
+    # exact midpoints go up (the reference's `y >= mid` branch)
+    assert np.array_equal(O.v1_quantize_k(m, m), np.arange(1, 16))
+
+
+def test_midpoints_are_float32_half_sums():
+    c = np.array([-0.3, -0.1, 0.1, 0.3], np.float32)
+    assert np.array_equal(O.v1_midpoints(c[::-1]), np.array([-0.2, 0.0, 0.2], np.float32))
+
+
+@pytest.mark.parametrize("d", [64, 128, 256])
+def test_k_rotate_is_normalised_sylvester(d):
+    rng = np.random.default_rng(d)
+    k = rng.standard_normal((7, d)).astype(np.float32) * 3
+    y, n = O.v1_k_rotate(k)
+    want = (k.astype(np.float64) / np.linalg.norm(k, axis=-1, keepdims=True)) @ O.sylvester(d).T / math.sqrt(d)
+    assert np.allclose(y, want, atol=2e-6)
+    assert np.allclose(n, np.linalg.norm(k.astype(np.float64), axis=-1), rtol=1e-6)
+    # no random signs: the first coordinate is the scaled sum
+    assert np.allclose(y[:, 0], want[:, 0], atol=2e-6)
+
+
+@pytest.mark.parametrize("vb", [1, 2, 3, 4, 8])
+def test_quantize_v_error_bound_and_endpoints(vb):
+    rng = np.random.default_rng(vb)
+    v = rng.standard_normal((50, 128)).astype(np.float32)
+    q, sc, mn, _ = O.v1_quantize_v(v, vb)
+    top = (1 << vb) - 1
+    rec = q.astype(np.float64) * sc[:, None] + mn[:, None]
+    assert np.all(np.abs(rec - v) <= sc[:, None] * 0.5 * (1 + 1e-5) + 1e-7)
+    assert np.array_equal(q[np.arange(50), v.argmin(-1)], np.zeros(50))
+    assert np.array_equal(q[np.arange(50), v.argmax(-1)], np.full(50, top))
+    want_sc = (v.max(-1) - v.min(-1)) / (np.float32(top) if vb > 1 else np.float32(1))
+    assert np.array_equal(sc, want_sc.astype(np.float32))
+
+
+def test_quantize_v_constant_vector_uses_floor_scale():
+    q, sc, mn, _ = O.v1_quantize_v(np.full((1, 64), 2.5, np.float32), 3)
+    assert sc[0] == np.float32(1e-8) and mn[0] == np.float32(2.5) and not q.any()
+
+
+def test_store_roundtrip_and_skip():
+    rng = np.random.default_rng(5)
+    N, H, d, kb, vb = 9, 2, 128, 4, 2
+    g = O.v1_geometry(d, kb, vb)
+    cache = np.full((3, 4, H, 256), 0xAB, np.uint8)
+    k = rng.standard_normal((N, H, d)).astype(np.float32)
+    v = rng.standard_normal((N, H, d)).astype(np.float32)
+    c = O.lloyd_max_codebook(d, kb)[1].astype(np.float32)
+    slots = np.array([0, 5, -1, 11, 2, 3, 7, 6, 1])
+    st = O.v1_store(k, v, slots, cache, O.v1_midpoints(c), kb, vb)
+    kc, kn, vc, sc, zr = O.v1_unpack(cache, d, kb, vb)
+    for i, s in enumerate(slots):
+        if s < 0:
+            continue
+        b, o = divmod(int(s), 4)
+        assert np.array_equal(kc[b, o], st["kcodes"][i])
+        assert np.array_equal(vc[b, o], st["vcodes"][i])
+        assert np.array_equal(kn[b, o], st["norm"][i].astype(np.float16))
+        assert np.array_equal(sc[b, o], st["vscale"][i].astype(np.float16))
+        assert np.array_equal(zr[b, o], st["vmin"][i].astype(np.float16))
+    # slot 4 (never mapped) and the padding are untouched
+    assert (cache[1, 0] == 0xAB).all()
+    assert (cache[..., g["raw"]:] == 0xAB).all()
+
+
+def _rand_cache(rng, nb, bs, H, d, kb, vb, n_tok, v_rotate=False):
+    g = O.v1_geometry(d, kb, vb)
+    cache = np.zeros((nb, bs, H, max(g["slot"], 128)), np.uint8)
+    k = rng.standard_normal((n_tok, H, d)).astype(np.float32)
+    v = rng.standard_normal((n_tok, H, d)).astype(np.float32)
+    c = O.lloyd_max_codebook(d, kb)[1].astype(np.float32)
+    slots = rng.permutation(nb * bs)[:n_tok]
+    O.v1_store(k, v, slots, cache, O.v1_midpoints(c), kb, vb, v_rotate=v_rotate)
+    return cache, c, k, v, slots
+
+
+@pytest.mark.parametrize("v_rotate", [False, True])
+def test_decode_equals_dense_attention_in_original_domain(v_rotate):
+    # <q M, k^> = <q, k^ M^T>: attention over the un-rotated reconstructions
+    rng = np.random.default_rng(11)
+    nb, bs, H, d, kb, vb, Hq, B = 12, 16, 2, 64, 4, 2, 4, 2
+    cache, c, _, _, _ = _rand_cache(rng, nb, bs, H, d, kb, vb, nb * bs, v_rotate)
+    bt = rng.permutation(nb).reshape(B, nb // B).astype(np.int32)
+    seq = np.array([37, 96], np.int32)
+    q = rng.standard_normal((B, Hq, d)).astype(np.float32)
+    got = O.v1_decode_attention(q, cache, bt, seq, c, kb, vb, 1 / math.sqrt(d), v_rotate=v_rotate)
+    k_hat, v_hat = O.v1_dequant(cache, d, kb, vb, c)
+    M = O.sylvester(d) / math.sqrt(d)
+    kd = np.zeros((B, H, 96, d))
+    vd = np.zeros((B, H, 96, d))
+    for b in range(B):
+        for p in range(seq[b]):
+            blk, off = bt[b, p // bs], p % bs
+            kd[b, :, p] = k_hat[blk, off] @ M.T
+            vd[b, :, p] = (v_hat[blk, off] @ M.T) if v_rotate else v_hat[blk, off]
+    want = O.dense_decode_attention(q, kd, vd, seq, 1 / math.sqrt(d))
+    assert np.allclose(got, want, atol=1e-9)
+
+
+def test_decode_norm_correction_makes_unit_directions():
+    rng = np.random.default_rng(2)
+    cache, c, _, _, _ = _rand_cache(rng, 4, 16, 1, 128, 3, 3, 64)
+    k_hat, _ = O.v1_dequant(cache, 128, 3, 3, c)
+    kc, kn, *_ = O.v1_unpack(cache, 128, 3, 3)
+    assert np.allclose(np.linalg.norm(k_hat, axis=-1), kn.astype(np.float64), rtol=1e-12)
+    k_raw, _ = O.v1_dequant(cache, 128, 3, 3, c, norm_correction=False)
+    assert not np.allclose(np.linalg.norm(k_raw, axis=-1), kn.astype(np.float64), rtol=1e-3)
+
+
+def test_decode_kv_start_masks_prefix():
+    rng = np.random.default_rng(3)
+    nb, bs, H, d = 8, 16, 1, 64
+    cache, c, _, _, _ = _rand_cache(rng, nb, bs, H, d, 3, 3, nb * bs)
+    bt = np.arange(nb, dtype=np.int32)[None]
+    q = rng.standard_normal((1, 2, d)).astype(np.float32)
+    full = O.v1_decode_attention(q, cache, bt, np.array([100]), c, 3, 3, 0.125, kv_start=np.array([40]))
+    # the same attention with positions 40..99 relabelled to 0..59
+    bt2 = bt.copy()
+    cache2 = np.zeros_like(cache)
+    for p in range(40, 100):
+        cache2[(p - 40) // bs, (p - 40) % bs] = cache[p // bs, p % bs]
+    part = O.v1_decode_attention(q, cache2, bt2, np.array([60]), c, 3, 3, 0.125)
+    assert np.allclose(full, part, atol=1e-12)
+    empty = O.v1_decode_attention(q, cache, bt, np.array([40]), c, 3, 3, 0.125, kv_start=np.array([40]))
+    assert not empty.any()
+
+
+@pytest.mark.parametrize("kb,vb,floor", [(4, 2, 0.8), (4, 4, 0.93), (8, 8, 0.999)])
+def test_decode_quality(kb, vb, floor):
+    # the compressed attention tracks exact attention on the raw K/V, and
+    # more bits track it more closely
+    rng = np.random.default_rng(4)
+    nb, bs, H, d, Hq = 16, 16, 1, 128, 4
+    cache, c, k, v, slots = _rand_cache(rng, nb, bs, H, d, kb, vb, nb * bs)
+    inv = np.argsort(slots)
+    bt = np.arange(nb, dtype=np.int32)[None]
+    q = rng.standard_normal((1, Hq, d)).astype(np.float32) * 3
+    got = O.v1_decode_attention(q, cache, bt, np.array([nb * bs]), c, kb, vb, 1 / math.sqrt(d))
+    kk = k[inv].transpose(1, 0, 2)[None]
+    vv = v[inv].transpose(1, 0, 2)[None]
+    want = O.dense_decode_attention(q, kk, vv, [nb * bs], 1 / math.sqrt(d))
+    cos = np.sum(got * want) / np.linalg.norm(got) / np.linalg.norm(want)
+    assert cos > floor, cos

@@ -1,0 +1,238 @@
+"""vLLM v1 TURBOQUANT slot format on gfx950 vs the CPU oracle.
+
+Store: every slot byte read back equals the oracle's store of the same vectors,
+except K codes at midpoint ties (|y - midpoint| < 2e-6, code off by one; the
+K norm is a float reduction whose order differs) and the fp16 K norm (within
+1e-3 relative).  V codes, V scale and V min are bit-exact (their arithmetic
+is order-independent).  Padding and unmapped slots stay untouched.
+Decode attention: against the oracle's float64 attention over the same cache
+bytes; max abs error <= 2e-2 + 2^-8 |want|, mean <= 2e-3 max(1, mean |want|)
+(bf16 tolerance, widened by one bf16 ulp for large outputs).
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import tq_oracle as O
+
+pytestmark = pytest.mark.gpu
+TIE = 2e-6
+DT = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}
+
+
+def _kv(g, n, h, d, dtype, outliers=False):
+    k = torch.randn(n, h, d, generator=g)
+    v = torch.randn(n, h, d, generator=g)
+    if outliers:
+        sel = torch.rand(n, generator=g) < 0.02
+        k[sel] *= 8
+        v[sel] *= 8
+    return k.to(dtype), v.to(dtype)
+
+
+@pytest.mark.parametrize("d", [64, 128, 256])
+@pytest.mark.parametrize("kb,vb", [(4, 2), (3, 3), (2, 4), (4, 4), (2, 2)])
+@pytest.mark.parametrize("vrot", [False, True])
+def test_store_parity(cuda, d, kb, vb, vrot):
+    from fused_turboquant import v1
+    dtn = "bf16" if (d + kb) % 2 == 0 else "f16"
+    if d == 128 and kb == 3:
+        dtn = "f32"
+    nb, bs, h = 5, 16, 3
+    g = torch.Generator().manual_seed(d * 100 + kb * 10 + vb + vrot)
+    layer = v1.TurboQuantV1Layer(d, kb, vb, v_rotate=vrot, device=cuda)
+    slot = max(v1.slot_size(d, kb, vb), 128)
+    cache = torch.full((nb, bs, h, slot), 0xAB, dtype=torch.uint8, device=cuda)
+    n = nb * bs - 7
+    slots = torch.randperm(nb * bs, generator=g)[:n]
+    slots[4] = -1
+    slots[9] = -5
+    k, v = _kv(g, n, h, d, DT[dtn])
+    layer.store(k.to(cuda), v.to(cuda), cache, slots.to(cuda))
+    got = cache.cpu().numpy()
+
+    want = np.full(got.shape, 0xAB, np.uint8)
+    st = O.v1_store(k.float().numpy(), v.float().numpy(), slots.numpy(), want,
+                    layer.midpoints.cpu().numpy(), kb, vb, v_rotate=vrot, value_dtype=dtn)
+    geo = O.v1_geometry(d, kb, vb)
+    # bytes outside the K region (K norm, V codes, V scale, V min, padding, unmapped slots)
+    mse = geo["mse"]
+    sl = slots.numpy()
+    ok = sl >= 0
+    blk, off = sl[ok] // bs, sl[ok] % bs
+    assert np.array_equal(got[..., geo["kps"]:], want[..., geo["kps"]:])
+    unmapped = np.ones((nb, bs), bool)
+    unmapped[blk, off] = False
+    assert np.array_equal(got[unmapped], want[unmapped])
+    # K codes: equal except at midpoint ties
+    gk = O.unpack(got[blk, off, :, :mse], kb, d)
+    wk = st["kcodes"][ok]
+    diff = gk != wk
+    ties = int(diff.sum())
+    if ties:
+        y = st["y"][ok][diff].astype(np.float64)
+        mids = layer.midpoints.cpu().numpy().astype(np.float64)
+        dist = np.min(np.abs(y[:, None] - mids[None, :]), axis=1)
+        assert dist.max() < TIE
+        assert np.all(np.abs(gk[diff].astype(int) - wk[diff].astype(int)) == 1)
+    # K norm fp16
+    gn = got[blk, off, :, mse:mse + 2].copy().view(np.float16)[..., 0].astype(np.float32)
+    wn = st["norm"][ok].astype(np.float16).astype(np.float32)
+    assert np.all(np.abs(gn - wn) <= 1e-3 * np.abs(wn))
+    print(f"[v1 store d={d} kb={kb} vb={vb} vrot={vrot} {dtn}] K code ties={ties} of {wk.size}")
+
+
+def _oracle_cache(g, nb, bs, h, d, kb, vb, n_tok, vrot, dtype="bf16", outliers=False):
+    """Cache bytes written by the oracle (the decode tests do not depend on the GPU store)."""
+    from fused_turboquant import v1
+    slot = max(v1.slot_size(d, kb, vb), 128)
+    cache = np.zeros((nb, bs, h, slot), np.uint8)
+    k, v = _kv(g, n_tok, h, d, DT[dtype], outliers)
+    c = v1.default_centroids(d, kb).numpy()
+    slots = torch.randperm(nb * bs, generator=g)[:n_tok].numpy()
+    O.v1_store(k.float().numpy(), v.float().numpy(), slots, cache, O.v1_midpoints(c), kb, vb,
+               v_rotate=vrot, value_dtype=dtype)
+    return cache, c
+
+
+def _check_attn(got, want, tag):
+    """max |err| <= 2e-2 and mean |err| <= 2e-3 for outputs of magnitude <= 1;
+    above that the bound grows with |want| by one bf16 ulp (2^-8 relative),
+    since rounding the exact answer to bf16 alone errs by up to half of that
+    (outlier tokens give outputs near 30, where a bf16 ulp is 0.125)."""
+    err = np.abs(got.astype(np.float64) - want)
+    bound = 2e-2 + 2.0 ** -8 * np.abs(want)
+    mean_bound = 2e-3 * max(1.0, float(np.abs(want).mean()))
+    print(f"[{tag}] max {err.max():.2e} mean {err.mean():.2e} (|want| max {np.abs(want).max():.2f}) "
+          f"worst/bound {(err / bound).max():.2f}")
+    assert (err <= bound).all() and err.mean() <= mean_bound, tag
+
+
+@pytest.mark.parametrize("kb,vb", [(4, 2), (3, 3), (4, 4), (2, 2), (3, 4), (2, 3)])
+@pytest.mark.parametrize("hq,hkv", [(8, 2), (4, 4), (16, 1)])
+@pytest.mark.parametrize("splits", [1, 3, 16])
+def test_decode_parity(cuda, kb, vb, hq, hkv, splits):
+    from fused_turboquant import v1
+    d, bs, nb = 128, 16, 48
+    g = torch.Generator().manual_seed(kb * 1000 + vb * 100 + hq * 10 + splits)
+    vrot = (kb + vb + splits) % 2 == 0
+    cache, c = _oracle_cache(g, nb, bs, hkv, d, kb, vb, nb * bs, vrot)
+    lens = [0, 1, 15, 17, 100, 257, 16, 64]
+    B = len(lens)
+    mb = 20
+    bt = torch.randint(0, nb, (B, mb), generator=g, dtype=torch.int32)
+    q = torch.randn(B, hq, d, generator=g).to(torch.bfloat16)
+    sl = torch.tensor(lens, dtype=torch.int32)
+    out = v1.v1_decode_attention(q.to(cuda), torch.from_numpy(cache).to(cuda), bt.to(cuda),
+                                 sl.to(cuda), torch.from_numpy(c).to(cuda), kb, vb,
+                                 v_rotate=vrot, num_splits=splits)
+    want = O.v1_decode_attention(q.float().numpy(), cache, bt.numpy(), sl.numpy(), c, kb, vb,
+                                 1 / math.sqrt(d), v_rotate=vrot)
+    assert out.dtype == torch.bfloat16
+    got = out.float().cpu().numpy()
+    assert not got[0].any()  # empty sequence -> zeros
+    _check_attn(got, want, f"v1 attn kb={kb} vb={vb} hq={hq} hkv={hkv} S={splits} vrot={vrot}")
+
+
+@pytest.mark.parametrize("bs", [16, 32, 64])
+def test_decode_kv_start_and_block_size(cuda, bs):
+    from fused_turboquant import v1
+    d, hkv, hq, kb, vb = 128, 2, 8, 4, 2
+    nb = 1024 // bs
+    g = torch.Generator().manual_seed(bs)
+    cache, c = _oracle_cache(g, nb, bs, hkv, d, kb, vb, nb * bs, True)
+    lens = [300, 31, 1000, 64]
+    starts = [40, 31, 999, 0]
+    bt = torch.stack([torch.randperm(nb, generator=g)[: 1024 // bs].to(torch.int32) for _ in lens])
+    q = torch.randn(len(lens), hq, d, generator=g, dtype=torch.float32)
+    sl = torch.tensor(lens, dtype=torch.int32)
+    ks = torch.tensor(starts, dtype=torch.int32)
+    out = v1.v1_decode_attention(q.to(cuda), torch.from_numpy(cache).to(cuda), bt.to(cuda), sl.to(cuda),
+                                 torch.from_numpy(c).to(cuda), kb, vb, v_rotate=True, kv_start=ks.to(cuda),
+                                 num_splits=5, out=torch.empty(len(lens), hq, d, device=cuda))
+    want = O.v1_decode_attention(q.numpy(), cache, bt.numpy(), sl.numpy(), c, kb, vb, 1 / math.sqrt(d),
+                                 kv_start=ks.numpy(), v_rotate=True)
+    got = out.cpu().numpy()
+    assert not got[1].any()  # kv_start == seq_len -> nothing attended
+    _check_attn(got, want, f"v1 kv_start bs={bs}")
+
+
+def test_store_then_decode_end_to_end(cuda):
+    """GPU store followed by GPU decode against the oracle pipeline on the same inputs."""
+    from fused_turboquant import v1
+    d, bs, hkv, hq, kb, vb = 128, 16, 4, 16, 3, 3
+    g = torch.Generator().manual_seed(77)
+    layer = v1.TurboQuantV1Layer(d, kb, vb, v_rotate=True, device=cuda)
+    lens = [513, 77, 1024]
+    nb = sum((L + bs - 1) // bs for L in lens) + 3
+    cache = torch.zeros(layer.kv_cache_shape(nb, bs, hkv), dtype=torch.uint8, device=cuda)
+    perm = torch.randperm(nb, generator=g).to(torch.int32)
+    mb = max((L + bs - 1) // bs for L in lens)
+    bt = torch.zeros(len(lens), mb, dtype=torch.int32)
+    used = 0
+    for b, L in enumerate(lens):
+        npg = (L + bs - 1) // bs
+        bt[b, :npg] = perm[used:used + npg]
+        used += npg
+        k, v = _kv(g, L, hkv, d, torch.bfloat16, outliers=True)
+        pos = torch.arange(L)
+        slots = bt[b].long()[pos // bs] * bs + pos % bs
+        layer.store(k.to(cuda), v.to(cuda), cache, slots.to(cuda))
+    q = torch.randn(len(lens), hq, d, generator=g).to(torch.bfloat16)
+    sl = torch.tensor(lens, dtype=torch.int32)
+    out = layer.decode(q.to(cuda), cache, bt.to(cuda), sl.to(cuda))
+    want = O.v1_decode_attention(q.float().numpy(), cache.cpu().numpy(), bt.numpy(), sl.numpy(),
+                                 layer.centroids.cpu().numpy(), kb, vb, 1 / math.sqrt(d), v_rotate=True)
+    _check_attn(out.float().cpu().numpy(), want, "v1 store+decode")
+
+
+def test_config4_full_size(cuda):
+    """K4V2, v_rotate, B=4, 32/8 heads, ctx ~ U[65536, 131072],
+    2% of tokens x8.  Oracle on a subset of (sequence, kv head); split-count
+    invariance over the whole output."""
+    from fused_turboquant import v1
+    d, bs, hkv, hq, kb, vb = 128, 16, 8, 32, 4, 2
+    g = torch.Generator().manual_seed(4)
+    lens = torch.randint(65536, 131073, (4,), generator=g).tolist()
+    layer = v1.TurboQuantV1Layer(d, kb, vb, v_rotate=True, device=cuda)
+    pages = [(L + bs - 1) // bs for L in lens]
+    nb = sum(pages)
+    cache = torch.zeros(layer.kv_cache_shape(nb, bs, hkv), dtype=torch.uint8, device=cuda)
+    perm = torch.randperm(nb, generator=g).to(torch.int32)
+    bt = torch.zeros(4, max(pages), dtype=torch.int32)
+    used = 0
+    gd = torch.Generator(device=cuda).manual_seed(5)
+    for b, L in enumerate(lens):
+        bt[b, :pages[b]] = perm[used:used + pages[b]]
+        used += pages[b]
+        btd = bt[b].to(cuda).long()
+        for s0 in range(0, L, 32768):
+            n = min(32768, L - s0)
+            k = torch.randn(n, hkv, d, generator=gd, device=cuda)
+            v = torch.randn(n, hkv, d, generator=gd, device=cuda)
+            sel = torch.rand(n, generator=gd, device=cuda) < 0.02
+            k[sel] *= 8
+            v[sel] *= 8
+            pos = torch.arange(s0, s0 + n, device=cuda)
+            layer.store(k.to(torch.bfloat16), v.to(torch.bfloat16), cache, btd[pos // bs] * bs + pos % bs)
+    q = torch.randn(4, hq, d, generator=g).to(torch.bfloat16)
+    sl = torch.tensor(lens, dtype=torch.int32)
+    out = layer.decode(q.to(cuda), cache, bt.to(cuda), sl.to(cuda))
+    f32 = [layer.decode(q.to(cuda), cache, bt.to(cuda), sl.to(cuda), num_splits=s,
+                        out=torch.empty(4, hq, d, device=cuda)).cpu().numpy() for s in (8, 64)]
+    o1 = out.float().cpu().numpy()
+    assert np.isfinite(o1).all()
+    # the split factor only changes the order of the final merge
+    assert np.abs(f32[0] - f32[1]).max() <= 1e-3 * max(1.0, float(np.abs(f32[1]).max()))
+    # oracle on (b, kv head) subsets: gather that head's slots into a small cache
+    for b, kvh in ((0, 0), (3, 5)):
+        L = lens[b]
+        rows = bt[b, :pages[b]].long()
+        sub = cache[rows.to(cuda)][:, :, kvh:kvh + 1].cpu().numpy()
+        want = O.v1_decode_attention(q[b:b + 1, kvh * 4:kvh * 4 + 4].float().numpy(), sub,
+                                     np.arange(pages[b], dtype=np.int32)[None], np.array([L]),
+                                     layer.centroids.cpu().numpy(), kb, vb, 1 / math.sqrt(d),
+                                     v_rotate=True)
+        _check_attn(o1[b:b + 1, kvh * 4:kvh * 4 + 4], want, f"config4 b={b} kvh={kvh} ctx={L}")
