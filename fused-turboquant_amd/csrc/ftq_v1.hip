@@ -286,14 +286,15 @@ __device__ __forceinline__ uint32_t v1_vpair(const uint32_t (&v)[NV], const uint
 }
 
 __device__ __forceinline__ void wave_lds_fence() {
-  // orders this wave's LDS accesses (LDS executes in order within a wave)
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  // LDS accesses of one wave execute in order, so a write by one lane is seen
+  // by a later read of another lane of the same wave; only the compiler must
+  // not reorder them (a hardware fence here would also wait for the prefetch
+  // loads in flight)
+  __asm__ volatile("" ::: "memory");
 }
 
 template <int D, int KB, int VB, int QT>
-__global__ __launch_bounds__(256, 4) void v1_attn_kernel(
+__global__ __launch_bounds__(256, 2) void v1_attn_kernel(
     const void* __restrict__ query, const uint8_t* __restrict__ cache,
     const int32_t* __restrict__ block_table, const int32_t* __restrict__ seq_lens,
     const int32_t* __restrict__ kv_start, int hq, int hkv, int bs, int max_blocks,
