@@ -205,10 +205,12 @@ struct V1Tile {
   bool ok[2];             // wave-uniform: S-tile has a real page
 };
 
-// Loads of one 32-token tile.  Every address is a wave-uniform page base plus
-// a lane offset fixed for the whole kernel.  An S-tile past the sequence (or on
-// a bad block id) reads block 0 instead -- the loads always issue, so the wait
-// counts stay static -- and the consumer masks it.
+// Loads of one 32-token tile, as raw buffer loads: one wave-uniform buffer
+// descriptor per S-tile (its page base; the byte range ends after its 16 token
+// rows, so no lane can read past them) plus a lane offset fixed for the
+// kernel.  An S-tile past the sequence (or on a bad block id) reads block 0
+// instead -- the loads always issue, so the wait counts stay static -- and the
+// consumer masks it.
 //   K:    lane (m, g) = token m, K bytes [g*KQ, (g+1)*KQ)
 //   tail: lane (m, g) = token m, field g (0 K norm, 1 V scale, 2 V min, 3 unused)
 //   V:    lane (m, g) = tokens 4g+i (i < 4) of each S-tile, the codes of dims
@@ -216,33 +218,55 @@ struct V1Tile {
 //         VB 2: v[j] = the two 16-bit chunks;  VB 4: v[j] / v[4+j] = low / high
 //         16 bits of the two 32-bit chunks;  VB 3: v[2j], v[2j+1] = 32 bits around
 //         each 24-bit chunk (starting at an even byte).
+struct V1Addr {
+  const uint8_t* cache;
+  const int32_t* bt_row;
+  int64_t num_blocks, s_blk, kvh_off;
+  uint32_t s_pos;
+  int lbs, max_blocks, seq_len;
+  uint32_t koff, toff, voff;  // lane offsets; token 4g+i of a V load adds i * s_pos (scalar)
+};
+
+__device__ __forceinline__ uint32_t buf_u16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0);
+}
+
 template <int D, int KB, int VB>
-__device__ __forceinline__ void v1_load(V1Tile<D, KB, VB>& r, const uint8_t* __restrict__ cache,
-                                        const int32_t* __restrict__ bt_row, int tile, int seq_len,
-                                        int bs, int max_blocks, int64_t num_blocks, int64_t s_blk,
-                                        int64_t s_pos, int64_t kvh_off, uint32_t koff, uint32_t toff,
-                                        const uint32_t (&voff)[4], bool active) {
+__device__ __forceinline__ void v1_load(V1Tile<D, KB, VB>& r, const V1Addr& ad, int tile, bool active) {
+  using A = V1A<D, KB, VB>;
 #pragma unroll
   for (int st = 0; st < 2; ++st) {
     const int pos0 = tile * 32 + st * 16;
-    const int page = pos0 / bs;
-    int64_t phys = (active && pos0 < seq_len && page < max_blocks) ? (int64_t)bt_row[page] : -1;
-    const bool valid = phys >= 0 && phys < num_blocks;
+    const int page = pos0 >> ad.lbs;
+    int64_t phys = (active && pos0 < ad.seq_len && page < ad.max_blocks) ? (int64_t)ad.bt_row[page] : -1;
+    const bool valid = phys >= 0 && phys < ad.num_blocks;
     if (!valid) phys = 0;
-    const int64_t within = valid ? (int64_t)(pos0 - page * bs) : 0;
-    const uint8_t* bst = cache + (phys * s_blk + within * s_pos + kvh_off);
-    load_dwords(bst + koff, r.k[st]);
-    r.tail[st] = *reinterpret_cast<const uint16_t*>(bst + toff);
+    const uint32_t within = valid ? (uint32_t)(pos0 & ((1 << ad.lbs) - 1)) : 0u;
+    const uint8_t* bst = ad.cache + (phys * ad.s_blk + (int64_t)(within * ad.s_pos) + ad.kvh_off);
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(bst), (short)0, (int)(16u * ad.s_pos), 0x00020000);
+    if constexpr (A::KQW == 4) {
+      const uint4 k = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, ad.koff, 0, 0));
+      r.k[st][0] = k.x; r.k[st][1] = k.y; r.k[st][2] = k.z; r.k[st][3] = k.w;
+    } else if constexpr (A::KQW == 3) {
+      typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+      const u32x3 k = __builtin_bit_cast(u32x3, __builtin_amdgcn_raw_buffer_load_b96(rs, ad.koff, 0, 0));
+      r.k[st][0] = k.x; r.k[st][1] = k.y; r.k[st][2] = k.z;
+    } else {
+      const uint2 k = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs, ad.koff, 0, 0));
+      r.k[st][0] = k.x; r.k[st][1] = k.y;
+    }
+    r.tail[st] = buf_u16(rs, ad.toff, 0);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const uint8_t* p = bst + voff[i];
+      const uint32_t so = (uint32_t)i * ad.s_pos;
       if constexpr (VB == 2) {
-        const uint32_t h = *reinterpret_cast<const uint16_t*>(p);
+        const uint32_t h = buf_u16(rs, ad.voff, so);
         if (i & 1) r.v[2 * st + (i >> 1)] |= h << 16;
         else r.v[2 * st + (i >> 1)] = h;
       } else if constexpr (VB == 4) {
-        const uint32_t lo = *reinterpret_cast<const uint16_t*>(p);
-        const uint32_t hi = *reinterpret_cast<const uint16_t*>(p + 2);
+        const uint32_t lo = buf_u16(rs, ad.voff, so);
+        const uint32_t hi = buf_u16(rs, ad.voff + 2u, so);
         if (i & 1) {
           r.v[2 * st + (i >> 1)] |= lo << 16;
           r.v[4 + 2 * st + (i >> 1)] |= hi << 16;
@@ -251,8 +275,8 @@ __device__ __forceinline__ void v1_load(V1Tile<D, KB, VB>& r, const uint8_t* __r
           r.v[4 + 2 * st + (i >> 1)] = hi;
         }
       } else {
-        const uint32_t lo = *reinterpret_cast<const uint16_t*>(p);
-        const uint32_t hi = *reinterpret_cast<const uint16_t*>(p + 2);
+        const uint32_t lo = buf_u16(rs, ad.voff, so);
+        const uint32_t hi = buf_u16(rs, ad.voff + 2u, so);
         r.v[4 * st + i] = lo | (hi << 16);
       }
     }
@@ -297,7 +321,7 @@ template <int D, int KB, int VB, int QT>
 __global__ __launch_bounds__(256, 2) void v1_attn_kernel(
     const void* __restrict__ query, const uint8_t* __restrict__ cache,
     const int32_t* __restrict__ block_table, const int32_t* __restrict__ seq_lens,
-    const int32_t* __restrict__ kv_start, int hq, int hkv, int bs, int max_blocks,
+    const int32_t* __restrict__ kv_start, int hq, int hkv, int lbs, int max_blocks,
     int64_t num_blocks, int64_t s_blk, int64_t s_pos, int64_t s_head,
     const float* __restrict__ cent, float qscale, int num_splits, float* __restrict__ ws_o,
     float* __restrict__ ws_lse) {
@@ -378,14 +402,21 @@ __global__ __launch_bounds__(256, 2) void v1_attn_kernel(
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
 
   // lane offsets (fixed for the kernel)
-  const uint32_t sp = (uint32_t)s_pos;
-  const uint32_t koff = (uint32_t)m * sp + (uint32_t)(g * A::KQ);
-  const uint32_t toff = (uint32_t)m * sp +
-                        (uint32_t)(g == 1 ? A::KPS + A::VDB : (g == 2 ? A::KPS + A::VDB + 2 : A::MSE));
-  const uint32_t vch = VB == 3 ? (uint32_t)((A::KPS + 3 * m) & ~1) : (uint32_t)(A::KPS + VB * m);
-  uint32_t voff[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) voff[i] = (uint32_t)(4 * g + i) * sp + vch;
+  V1Addr ad;
+  ad.cache = cache;
+  ad.bt_row = bt_row;
+  ad.num_blocks = num_blocks;
+  ad.s_blk = s_blk;
+  ad.kvh_off = kvh_off;
+  ad.s_pos = (uint32_t)s_pos;
+  ad.lbs = lbs;
+  ad.max_blocks = max_blocks;
+  ad.seq_len = seq_len;
+  ad.koff = (uint32_t)m * ad.s_pos + (uint32_t)(g * A::KQ);
+  ad.toff = (uint32_t)m * ad.s_pos +
+            (uint32_t)(g == 1 ? A::KPS + A::VDB : (g == 2 ? A::KPS + A::VDB + 2 : A::MSE));
+  ad.voff = (uint32_t)(4 * g) * ad.s_pos +
+            (VB == 3 ? (uint32_t)((A::KPS + 3 * m) & ~1) : (uint32_t)(A::KPS + VB * m));
   // VB 3: byte selectors that re-align each chunk to its first code bit
   const uint32_t o3 = (uint32_t)((A::KPS + 3 * m) & 1);
   const uint32_t sel0 = o3 | ((o3 + 1) << 8) | ((o3 + 4) << 16) | ((o3 + 5) << 24);
@@ -528,13 +559,13 @@ __global__ __launch_bounds__(256, 2) void v1_attn_kernel(
   V1Tile<D, KB, VB> ra, rb;
   int tile = t_begin + wave_u;
   if (tile < t_end)
-    v1_load(ra, cache, bt_row, tile, seq_len, bs, max_blocks, num_blocks, s_blk, s_pos, kvh_off, koff, toff, voff, true);
+    v1_load(ra, ad, tile, true);
   while (tile < t_end) {
-    v1_load(rb, cache, bt_row, tile + 4, seq_len, bs, max_blocks, num_blocks, s_blk, s_pos, kvh_off, koff, toff, voff, tile + 4 < t_end);
+    v1_load(rb, ad, tile + 4, tile + 4 < t_end);
     process(ra, tile);
     tile += 4;
     if (tile >= t_end) break;
-    v1_load(ra, cache, bt_row, tile + 4, seq_len, bs, max_blocks, num_blocks, s_blk, s_pos, kvh_off, koff, toff, voff, tile + 4 < t_end);
+    v1_load(ra, ad, tile + 4, tile + 4 < t_end);
     process(rb, tile);
     tile += 4;
   }
@@ -557,6 +588,338 @@ __global__ __launch_bounds__(256, 2) void v1_attn_kernel(
   __syncthreads();
 
   const int64_t row0 = ((int64_t)b * hq + kvh * G) * num_splits + split;  // (b, head 0 of the group, split)
+  for (int idx = tid; idx < G * D; idx += 256) {
+    const int gg = idx / D, d = idx % D;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) M = fmaxf(M, red_m[w][gg]);
+    float L = 0.f, o = 0.f;
+    if (M != -INFINITY) {
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float f = __builtin_amdgcn_exp2f(red_m[w][gg] - M);
+        L += f * red_l[w][gg];
+        o += f * red_o[w][gg][d];
+      }
+    }
+    const int64_t row = row0 + (int64_t)gg * num_splits;
+    ws_o[row * D + d] = (L > 0.f) ? o / L : 0.f;
+    if (d == 0) ws_lse[row] = (L > 0.f) ? M + __builtin_log2f(L) : -INFINITY;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// decode attention, stage 1, GQA group of 4 (e.g. 32 query / 8 kv heads)
+// ---------------------------------------------------------------------------
+// Same tiles, loads and MFMAs as v1_attn_kernel, but the per-(token, head)
+// work runs in a compact layout: after the score MFMA only 4 of its 16
+// columns are real heads, so the scores of an S-tile (16 tokens x 4 heads) are
+// moved with three DPP row shifts to one value per lane,
+//   compact lane 16g + 4i + n  <->  token 4g + i of the S-tile, head n,
+// the softmax, P' and its hi/lo split run once per value, and three DPP row
+// shifts plus byte permutes build the P.V operand back.
+// The V operand needs no shift: dim 8m + bb's code stays at its bit position
+// inside the 16-bit chunk (for the first 8 bits; the rest from the chunk
+// shifted by 8), which is mantissa bit pos_bb of the f16 2^e (1 + q 2^(pos_bb-10));
+// accumulator bb is scaled by 2^(10 - pos_bb) at the end.
+
+// mantissa position of the code of dim 8m + bb in the V operand, and the
+// source word: 0 = the chunk pair, 1 = it shifted right by 8, 2 = by 16 (VB 3)
+template <int VB> __host__ __device__ constexpr int v1_vpos(int bb) {
+  return VB == 2 ? (bb <= 4 ? 2 * bb : 2 * bb - 8)
+       : VB == 4 ? (4 * (bb & 1))
+       : (bb <= 2 ? 3 * bb : bb <= 5 ? 3 * bb - 8 : 3 * bb - 16);
+}
+
+template <int D, int KB, int VB, int QT>
+__global__ __launch_bounds__(256, 2) void v1_attn_g4_kernel(
+    const void* __restrict__ query, const uint8_t* __restrict__ cache,
+    const int32_t* __restrict__ block_table, const int32_t* __restrict__ seq_lens,
+    const int32_t* __restrict__ kv_start, int hq, int hkv, int lbs, int max_blocks,
+    int64_t num_blocks, int64_t s_blk, int64_t s_pos, int64_t s_head,
+    const float* __restrict__ cent, float qscale, int num_splits, float* __restrict__ ws_o,
+    float* __restrict__ ws_lse) {
+  using A = V1A<D, KB, VB>;
+  constexpr int NS = A::NS, NB = A::NB, E = D / 16;
+  constexpr int G = 4;
+  const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int m = lane & 15, g = lane >> 4;      // MFMA layout: row / column m, k-group g
+  const int ci = (lane >> 2) & 3;  // compact layout: head lane & 3, token 4g + ci
+
+  constexpr int LUT_BYTES = 4 << (2 * KB);
+  constexpr int RED_BYTES = 4 * G * (D + 1) * 4;
+  constexpr int QS_BYTES = G * (D + 4) * 4;
+  constexpr int POOL0 = LUT_BYTES > RED_BYTES ? LUT_BYTES : RED_BYTES;
+  constexpr int POOL = POOL0 > QS_BYTES ? POOL0 : QS_BYTES;
+  __shared__ __attribute__((aligned(16))) uint8_t pool[POOL];
+  __shared__ float red_m[4][G], red_l[4][G];
+  __shared__ __attribute__((aligned(16))) uint16_t tail_l[4][2][4][16];  // [wave][S-tile][field][token]
+  __shared__ __attribute__((aligned(16))) float diag_l[4][2][64][4];  // [wave][S-tile][lane][register]
+  __shared__ uint16_t cent16[16];
+  float (*qs)[D + 4] = reinterpret_cast<float (*)[D + 4]>(pool);
+  float (*red_o)[G][D + 1] = reinterpret_cast<float (*)[G][D + 1]>(pool);
+  uint8_t* lut = pool;
+
+  if (tid < (1 << KB)) cent16[tid] = (uint16_t)f32_to_f16_bits(cent[tid]);
+  {
+    const int gg = tid >> 4, l16 = tid & 15;
+    if (gg < G) {
+      float y[E];
+      load_elems<QT, E>(query, ((int64_t)b * hq + kvh * G + gg) * D + l16 * E, y);
+      fwht_lanes<E, 16>(y, l16);
+#pragma unroll
+      for (int i = 0; i < E; ++i) qs[gg][l16 * E + i] = y[i] * qscale;
+    }
+  }
+  __syncthreads();
+  Op8 qb[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      uint32_t w = 0;
+      if (m < G) {
+        const _Float16 a0 = (_Float16)qs[m][g * (D / 4) + 8 * s + 2 * j];
+        const _Float16 a1 = (_Float16)qs[m][g * (D / 4) + 8 * s + 2 * j + 1];
+        w = (uint32_t)__builtin_bit_cast(uint16_t, a0) | ((uint32_t)__builtin_bit_cast(uint16_t, a1) << 16);
+      }
+      qb[s].u[j] = w;
+    }
+  }
+  __syncthreads();
+  for (int e = tid; e < (1 << (2 * KB)); e += 256)
+    reinterpret_cast<uint32_t*>(lut)[e] = (uint32_t)cent16[e & ((1 << KB) - 1)] | ((uint32_t)cent16[e >> KB] << 16);
+  __syncthreads();
+
+  const int seq_len = seq_lens[b];
+  int k0 = kv_start ? kv_start[b] : 0;
+  if (k0 < 0) k0 = 0;
+  const int t_first = k0 >> 5;
+  const int t_last = (seq_len + 31) >> 5;
+  const int n_tiles = t_last > t_first ? t_last - t_first : 0;
+  const int tps = (n_tiles + num_splits - 1) / num_splits;
+  const int t_begin = t_first + split * tps;
+  const int t_end = min(t_begin + tps, t_last);
+  const int32_t* bt_row = block_table + (int64_t)b * max_blocks;
+  const int64_t kvh_off = (int64_t)kvh * s_head;
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+
+  V1Addr ad;
+  ad.cache = cache;
+  ad.bt_row = bt_row;
+  ad.num_blocks = num_blocks;
+  ad.s_blk = s_blk;
+  ad.kvh_off = kvh_off;
+  ad.s_pos = (uint32_t)s_pos;
+  ad.lbs = lbs;
+  ad.max_blocks = max_blocks;
+  ad.seq_len = seq_len;
+  ad.koff = (uint32_t)m * ad.s_pos + (uint32_t)(g * A::KQ);
+  ad.toff = (uint32_t)m * ad.s_pos +
+            (uint32_t)(g == 1 ? A::KPS + A::VDB : (g == 2 ? A::KPS + A::VDB + 2 : A::MSE));
+  ad.voff = (uint32_t)(4 * g) * ad.s_pos +
+            (VB == 3 ? (uint32_t)((A::KPS + 3 * m) & ~1) : (uint32_t)(A::KPS + VB * m));
+  // VB 3: byte selectors giving chunk bits [0,16), [8,24), [16,24) of both tokens of a pair
+  const uint32_t o3 = (uint32_t)((A::KPS + 3 * m) & 1);
+  const uint32_t sel0 = o3 | ((o3 + 1) << 8) | ((o3 + 4) << 16) | ((o3 + 5) << 24);
+  const uint32_t sel1 = (o3 + 1) | ((o3 + 2) << 8) | ((o3 + 5) << 16) | ((o3 + 6) << 24);
+  const uint32_t sel2 = (o3 + 2) | (0x0Cu << 8) | ((o3 + 6) << 16) | (0x0Cu << 24);
+
+  float m_run = -INFINITY, l_run = 0.f, z_run = 0.f, u_run = 0.f;  // per compact lane, head cn
+  floatx4 acc[NB];
+#pragma unroll
+  for (int i = 0; i < NB; ++i) acc[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  constexpr float TAU = 8.f;  // p <= 2^TAU
+  auto process = [&](const V1Tile<D, KB, VB>& cur, int tile) __attribute__((always_inline)) {
+    floatx4 sacc[2];
+    wave_lds_fence();
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      sacc[st] = floatx4{0.f, 0.f, 0.f, 0.f};
+      floatx4 gacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        Op8 a;
+#pragma unroll
+        for (int p = 0; p < 4; ++p)
+          a.u[p] = *reinterpret_cast<const uint32_t*>(lut + field_off<2>(cur.k[st], (8 * s + 2 * p) * KB, 2 * KB));
+        sacc[st] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a.h, qb[s].h, sacc[st], 0, 0, 0);
+        gacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a.h, a.h, gacc, 0, 0, 0);
+      }
+      tail_l[wave][st][g][m] = (uint16_t)cur.tail[st];
+      // Gram[t][t] of token t sits in lane 16(t/4) + t, register t % 4: every
+      // lane stores its 4 registers and the readers pick the diagonal
+      *reinterpret_cast<floatx4*>(&diag_l[wave][st][lane][0]) = gacc;
+    }
+    wave_lds_fence();
+    // scores to the compact layout: lane 16g + 4i + n <- lane 16g + n, register i
+    float sc_[2];
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      int x = __float_as_int(sacc[st][0]);
+      x = __builtin_amdgcn_update_dpp(x, __float_as_int(sacc[st][1]), 0x114, 0xF, 0x2, false);
+      x = __builtin_amdgcn_update_dpp(x, __float_as_int(sacc[st][2]), 0x118, 0xF, 0x4, false);
+      x = __builtin_amdgcn_update_dpp(x, __float_as_int(sacc[st][3]), 0x11C, 0xF, 0x8, false);
+      sc_[st] = __int_as_float(x);
+    }
+    // per-token fields of token 4g + ci (compact) and the V scale pairs (MFMA layout)
+    float s[2], scf[2], zf[2];
+    uint2 scw[2];
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      const int tok = 4 * g + ci;
+      const float knf = (float)__builtin_bit_cast(_Float16, tail_l[wave][st][0][tok]);
+      scf[st] = (float)__builtin_bit_cast(_Float16, tail_l[wave][st][1][tok]);
+      zf[st] = (float)__builtin_bit_cast(_Float16, tail_l[wave][st][2][tok]);
+      const float dg = diag_l[wave][st][16 * g + tok][ci];
+      s[st] = sc_[st] * knf * __builtin_amdgcn_rsqf(dg + 1e-16f);
+      scw[st] = *reinterpret_cast<const uint2*>(&tail_l[wave][st][1][4 * g]);
+    }
+    if (tile * 32 < k0 || tile * 32 + 32 > seq_len || !cur.ok[0] || !cur.ok[1]) {
+#pragma unroll
+      for (int st = 0; st < 2; ++st) {
+        // the MFMA-layout scale pairs of masked tokens only feed exponents (P' is 0 there)
+        const int pos = tile * 32 + st * 16 + 4 * g + ci;
+        const bool bad = pos >= seq_len || pos < k0 || !cur.ok[st];
+        s[st] = bad ? -INFINITY : s[st];
+        scf[st] = bad ? 0.f : scf[st];
+        zf[st] = bad ? 0.f : zf[st];
+      }
+    }
+    if (__builtin_amdgcn_ballot_w64(fmaxf(s[0], s[1]) > m_run + TAU) != 0) {  // wave-uniform, rare
+      float t = fmaxf(s[0], s[1]);
+      t = fmaxf(t, dpp_xor4(t));
+      t = fmaxf(t, dpp_xor8(t));
+      t = fmaxf(t, __shfl_xor(t, 16));
+      t = fmaxf(t, __shfl_xor(t, 32));
+      const float m_new = fmaxf(m_run, t);
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+      m_run = m_new;
+      l_run *= alpha;
+      z_run *= alpha;
+      u_run *= alpha;
+      // acc column (lane & 15) < 4 is head lane & 3: the same lane's alpha
+#pragma unroll
+      for (int bb = 0; bb < NB; ++bb) acc[bb] *= alpha;
+    }
+    // P' = p sc / 2^e (f16 hi + lo), packed hi | lo << 16 per compact lane
+    uint32_t w[2];
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      const float p = __builtin_amdgcn_exp2f(s[st] - m_run);
+      l_run += p;
+      z_run = __builtin_fmaf(p, zf[st], z_run);
+      const float ps = p * scf[st];
+      u_run += ps;
+      uint32_t eb = __builtin_bit_cast(uint16_t, (_Float16)scf[st]) & 0x7C00u;
+      eb = eb < 0x0400u ? 0x0400u : (eb > 0x7400u ? 0x7400u : eb);
+      const float r = (float)__builtin_bit_cast(_Float16, (uint16_t)(0x7800u - eb));
+      const float u = ps * r;
+      const _Float16 uh = (_Float16)u;
+      const _Float16 ul = (_Float16)(u - (float)uh);
+      w[st] = (uint32_t)__builtin_bit_cast(uint16_t, uh) | ((uint32_t)__builtin_bit_cast(uint16_t, ul) << 16);
+    }
+    // back to the P.V operand: lane (n, g) takes tokens 4g..4g+3 of head n from
+    // compact lanes n, n+4, n+8, n+12 of its row
+    Op8 pb, pl;
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      const uint32_t w0 = w[st];
+      const uint32_t w1 = (uint32_t)__builtin_amdgcn_mov_dpp((int)w0, 0x104, 0xF, 0xF, true);
+      const uint32_t w2 = (uint32_t)__builtin_amdgcn_mov_dpp((int)w0, 0x108, 0xF, 0xF, true);
+      const uint32_t w3 = (uint32_t)__builtin_amdgcn_mov_dpp((int)w0, 0x10C, 0xF, 0xF, true);
+      pb.u[2 * st] = __builtin_amdgcn_perm(w1, w0, 0x05040100u);
+      pb.u[2 * st + 1] = __builtin_amdgcn_perm(w3, w2, 0x05040100u);
+      pl.u[2 * st] = __builtin_amdgcn_perm(w1, w0, 0x07060302u);
+      pl.u[2 * st + 1] = __builtin_amdgcn_perm(w3, w2, 0x07060302u);
+    }
+    // V operand exponent words (pair j: tokens 4g + 2(j&1), +1 of S-tile j/2)
+    uint32_t ex[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t scp = (j & 1) ? scw[j >> 1].y : scw[j >> 1].x;
+      us2 e2 = __builtin_bit_cast(us2, scp & 0x7C007C00u);
+      e2 = __builtin_elementwise_max(e2, us2{0x0400, 0x0400});
+      e2 = __builtin_elementwise_min(e2, us2{0x7400, 0x7400});
+      ex[j] = __builtin_bit_cast(uint32_t, e2);
+    }
+    // V code words: [0] the chunk pairs, [1] shifted by 8, [2] by 16 (VB 3 only)
+    uint32_t vw[3][A::NV];
+#pragma unroll
+    for (int j = 0; j < A::NV; ++j) {
+      if constexpr (VB == 3) {
+        if (j < 4) {
+          vw[0][j] = __builtin_amdgcn_perm(cur.v[2 * j + 1], cur.v[2 * j], sel0);
+          vw[1][j] = __builtin_amdgcn_perm(cur.v[2 * j + 1], cur.v[2 * j], sel1);
+          vw[2][j] = __builtin_amdgcn_perm(cur.v[2 * j + 1], cur.v[2 * j], sel2);
+        }
+      } else {
+        vw[0][j] = cur.v[j];
+        vw[1][j] = cur.v[j] >> 8;
+      }
+    }
+#pragma unroll
+    for (int bb = 0; bb < NB; ++bb) {
+      const int pos = v1_vpos<VB>(bb);
+      const uint32_t msk = ((uint32_t)((1 << VB) - 1) << pos) * 0x00010001u;
+      Op8 a;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        uint32_t x;
+        if constexpr (VB == 2) x = bb <= 4 ? vw[0][j] : vw[1][j];
+        else if constexpr (VB == 4) x = vw[(bb >> 1) & 1][(bb < 4 ? 0 : 4) + j];
+        else x = vw[bb <= 2 ? 0 : (bb <= 5 ? 1 : 2)][j];
+        a.u[j] = (x & msk) | ex[j];
+      }
+      acc[bb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a.h, pb.h, acc[bb], 0, 0, 0);
+      acc[bb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a.h, pl.h, acc[bb], 0, 0, 0);
+    }
+  };
+
+  V1Tile<D, KB, VB> ra, rb;
+  int tile = t_begin + wave_u;
+  if (tile < t_end)
+    v1_load(ra, ad, tile, true);
+  while (tile < t_end) {
+    v1_load(rb, ad, tile + 4, tile + 4 < t_end);
+    process(ra, tile);
+    tile += 4;
+    if (tile >= t_end) break;
+    v1_load(ra, ad, tile + 4, tile + 4 < t_end);
+    process(rb, tile);
+    tile += 4;
+  }
+
+  // ---- per-head totals over the 16 compact lanes of each head, wave merge ----
+  __syncthreads();
+  auto head_sum = [](float x) __attribute__((always_inline)) {
+    x += dpp_xor4(x);
+    x += dpp_xor8(x);
+    x += __shfl_xor(x, 16);
+    x += __shfl_xor(x, 32);
+    return x;
+  };
+  const float l_tot = head_sum(l_run);
+  const float z_tot = head_sum(z_run);
+  const float u_tot = head_sum(u_run);
+  if (lane < G) {
+    red_m[wave][lane] = m_run;
+    red_l[wave][lane] = l_tot;
+  }
+  if (m < G) {  // MFMA column m is head m; this lane's compact head (lane & 3) is m too
+#pragma unroll
+    for (int bb = 0; bb < NB; ++bb) {
+      const float vsc = (float)(1 << (10 - v1_vpos<VB>(bb)));
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        red_o[wave][m][8 * (4 * g + i) + bb] = __builtin_fmaf(acc[bb][i] - u_tot, vsc, z_tot);
+    }
+  }
+  __syncthreads();
+
+  const int64_t row0 = ((int64_t)b * hq + kvh * G) * num_splits + split;
   for (int idx = tid; idx < G * D; idx += 256) {
     const int gg = idx / D, d = idx % D;
     float M = -INFINITY;
@@ -645,7 +1008,7 @@ struct V1Args {
   int qt;
   const uint8_t* cache;
   const int32_t *bt, *sl, *ks;
-  int B, hq, hkv, bs, max_blocks;
+  int B, hq, hkv, lbs, max_blocks;
   int64_t nb, sblk, spos, shead;
   const float* cent;
   float qscale;
@@ -658,12 +1021,19 @@ struct V1Args {
 template <int D, int KB, int VB>
 static hipError_t v1_launch_attn3(const V1Args& a, hipStream_t st) {
   dim3 grid(a.splits, a.hkv, a.B), block(256);
-  if (a.qt == F32)
-    v1_attn_kernel<D, KB, VB, F32><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.ks, a.hq, a.hkv, a.bs, a.max_blocks, a.nb, a.sblk, a.spos, a.shead, a.cent, a.qscale, a.splits, a.wo, a.wl);
+  if (a.hq == 4 * a.hkv) {
+    if (a.qt == F32)
+      v1_attn_g4_kernel<D, KB, VB, F32><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.ks, a.hq, a.hkv, a.lbs, a.max_blocks, a.nb, a.sblk, a.spos, a.shead, a.cent, a.qscale, a.splits, a.wo, a.wl);
+    else if (a.qt == F16)
+      v1_attn_g4_kernel<D, KB, VB, F16><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.ks, a.hq, a.hkv, a.lbs, a.max_blocks, a.nb, a.sblk, a.spos, a.shead, a.cent, a.qscale, a.splits, a.wo, a.wl);
+    else
+      v1_attn_g4_kernel<D, KB, VB, BF16><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.ks, a.hq, a.hkv, a.lbs, a.max_blocks, a.nb, a.sblk, a.spos, a.shead, a.cent, a.qscale, a.splits, a.wo, a.wl);
+  } else if (a.qt == F32)
+    v1_attn_kernel<D, KB, VB, F32><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.ks, a.hq, a.hkv, a.lbs, a.max_blocks, a.nb, a.sblk, a.spos, a.shead, a.cent, a.qscale, a.splits, a.wo, a.wl);
   else if (a.qt == F16)
-    v1_attn_kernel<D, KB, VB, F16><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.ks, a.hq, a.hkv, a.bs, a.max_blocks, a.nb, a.sblk, a.spos, a.shead, a.cent, a.qscale, a.splits, a.wo, a.wl);
+    v1_attn_kernel<D, KB, VB, F16><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.ks, a.hq, a.hkv, a.lbs, a.max_blocks, a.nb, a.sblk, a.spos, a.shead, a.cent, a.qscale, a.splits, a.wo, a.wl);
   else
-    v1_attn_kernel<D, KB, VB, BF16><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.ks, a.hq, a.hkv, a.bs, a.max_blocks, a.nb, a.sblk, a.spos, a.shead, a.cent, a.qscale, a.splits, a.wo, a.wl);
+    v1_attn_kernel<D, KB, VB, BF16><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.ks, a.hq, a.hkv, a.lbs, a.max_blocks, a.nb, a.sblk, a.spos, a.shead, a.cent, a.qscale, a.splits, a.wo, a.wl);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int64_t rows = (int64_t)a.B * a.hq;
@@ -746,7 +1116,8 @@ extern "C" int ftq_v1_decode_attention(
   FTQ_REQUIRE(d == 128, "v1 decode attention: head_dim must be 128");
   FTQ_REQUIRE(key_bits >= 2 && key_bits <= 4 && value_bits >= 2 && value_bits <= 4,
               "v1 decode attention: key_bits and value_bits must be 2, 3 or 4");
-  FTQ_REQUIRE(block_size >= 16 && block_size % 16 == 0, "block_size must be a multiple of 16");
+  FTQ_REQUIRE(block_size >= 16 && block_size <= 4096 && (block_size & (block_size - 1)) == 0,
+              "block_size must be a power of two in [16, 4096]");
   FTQ_REQUIRE(batch >= 0 && num_kv_heads > 0 && num_q_heads > 0 && num_blocks >= 0,
               "bad batch / head / block counts");
   FTQ_REQUIRE(num_q_heads % num_kv_heads == 0, "num_q_heads must be a multiple of num_kv_heads");
@@ -772,7 +1143,9 @@ extern "C" int ftq_v1_decode_attention(
               "query, out and workspace must be 16-byte aligned, kv_cache 4-byte aligned");
   V1Args a;
   a.q = query; a.qt = q_dtype; a.cache = kv_cache; a.bt = block_table; a.sl = seq_lens; a.ks = kv_start;
-  a.B = batch; a.hq = num_q_heads; a.hkv = num_kv_heads; a.bs = block_size; a.max_blocks = max_blocks_per_seq;
+  a.B = batch; a.hq = num_q_heads; a.hkv = num_kv_heads; a.max_blocks = max_blocks_per_seq;
+  a.lbs = 0;
+  while ((1 << a.lbs) < block_size) ++a.lbs;
   a.nb = num_blocks; a.sblk = stride_block; a.spos = stride_pos; a.shead = stride_head;
   a.cent = centroids;
   a.qscale = fwht_scale(d) * scale * 1.4426950408889634f;
