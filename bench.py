@@ -1,14 +1,17 @@
 """Benchmark of the MI355X fused-turboquant KV-cache hot path (one GPU).
 
-One step = the BASELINE workload on one GPU, inputs resident in HBM:
+One step = the BASELINE headline workload on one GPU, inputs resident in HBM:
   * config 2: fused 3-bit encode of K and of V, each [32768, 8, 128] bf16
     (262 144 vectors per tensor), TurboQuantMSE(128, bits=3, seed=42);
   * config 3: one paged decode-attention step over the 3-bit compressed
-    cache (B=32, Hq=32, Hkv=8, d=128, ctx 8192, page 16), when the paged
-    kernel is built.
-``value`` is the encode throughput in GB/s of bf16 input consumed.  Kernel
-times come from HIP events on the stream the kernels are launched on (torch's
-current stream, which the library launches on).
+    library-format cache (B=32, Hq=32, Hkv=8, d=128, ctx 8192, page 16).
+``value`` is the encode throughput in GB/s of bf16 input consumed.
+
+Also timed (not part of the step): the d=256 encode and the d=128 decode of
+config 2, and config 4 (vLLM v1 slot format, K4V2, v_rotate, B=4, contexts
+U[65536, 131072]).  Every kernel gets a roofline entry: algorithmic bytes per
+launch / average launch time, from HIP events on the stream the library
+launches on (torch's current stream).
 
 Prints ONE JSON line.
 """
@@ -27,6 +30,12 @@ sys.path.insert(0, os.path.join(ROOT, "fused-turboquant_amd"))
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, AMD published
 
+# HBM bytes per launch from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs of this
+# script, each scaled by the factor a 256 MiB device-to-device copy reads
+# (FETCH x2.0, WRITE x1.0); the summaries are in profiles/hbm_traffic_counters.md.
+# Keyed by roofline entry; None where no counter run covers the kernel.
+TRAFFIC_BYTES: dict = {}
+
 
 def log(msg):
     print(msg, file=sys.stderr, flush=True)
@@ -37,6 +46,7 @@ def time_launches(fn, iters, torch):
     st = torch.cuda.current_stream()
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
+    fn()
     e0.record(st)
     for _ in range(iters):
         fn()
@@ -66,6 +76,14 @@ def cpu_baseline_encode(n_vec=65536, d=128, bits=3):
     return n_vec * d * 2 / t / 1e9, f"{n_vec} vectors x d={d} bf16, 3-bit encode, median of 5"
 
 
+def roof(name, alg_bytes, t_us):
+    gbs = alg_bytes / (t_us * 1e-6) / 1e9
+    tr = TRAFFIC_BYTES.get(name)
+    return {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": tr, "kernel_us": round(t_us, 2),
+            "algorithmic_bytes": alg_bytes}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -81,51 +99,51 @@ def main():
         sys.exit(2)
 
     import torch
-    from fused_turboquant import TurboQuantMSE
+    from fused_turboquant import TurboQuantMSE, _lib
+    from fused_turboquant import paged as P
+    from fused_turboquant import v1 as V1
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    d, bits, T, H = 128, 3, 32768, 8
-    n = T * H
-    log(f"[bench] config2 encode: [{T},{H},{d}] bf16 3-bit, K and V")
-    g = torch.Generator(device="cpu").manual_seed(0)
-    sc = torch.exp(0.5 * torch.randn(d, generator=torch.Generator().manual_seed(1)))
-    k = (torch.randn(T, H, d, generator=g) * sc).to(torch.bfloat16).to(dev)
-    v = (torch.randn(T, H, d, generator=g) * sc).to(torch.bfloat16).to(dev)
-    tq = TurboQuantMSE(d, bits=bits, seed=42, device=dev)
-    ck = tq.encode(k)
-    cv = tq.encode(v)
-
-    from fused_turboquant import _lib
     L = _lib.lib()
     sp = _lib.stream_ptr(dev)
-    signs, bnd, lev = tq.rotation.signs, tq.quantizer.boundaries, tq.quantizer.levels
-    dec_out = torch.empty(T, H, d, dtype=torch.float32, device=dev)
+    bits, T, H = 3, 32768, 8
+    n = T * H
 
-    def enc_k():
-        L.ftq_encode(k.data_ptr(), 2, n, d, signs.data_ptr(), bnd.data_ptr(), bits,
-                     ck.indices.data_ptr(), ck.norms.data_ptr(), sp)
+    def codec_setup(d, seed):
+        g = torch.Generator(device="cpu").manual_seed(seed)
+        sc = torch.exp(0.5 * torch.randn(d, generator=torch.Generator().manual_seed(seed + 1)))
+        k = (torch.randn(T, H, d, generator=g) * sc).to(torch.bfloat16).to(dev)
+        v = (torch.randn(T, H, d, generator=g) * sc).to(torch.bfloat16).to(dev)
+        tq = TurboQuantMSE(d, bits=bits, seed=42, device=dev)
+        ck, cv = tq.encode(k), tq.encode(v)
+        signs, bnd = tq.rotation.signs, tq.quantizer.boundaries
 
-    def enc_v():
-        L.ftq_encode(v.data_ptr(), 2, n, d, signs.data_ptr(), bnd.data_ptr(), bits,
-                     cv.indices.data_ptr(), cv.norms.data_ptr(), sp)
+        def enc(x, c):
+            return lambda: _lib.check(L.ftq_encode(x.data_ptr(), 2, n, d, signs.data_ptr(), bnd.data_ptr(),
+                                                   bits, c.indices.data_ptr(), c.norms.data_ptr(), sp))
+        return tq, ck, enc(k, ck), enc(v, cv)
+
+    log(f"[bench] config2 encode: [{T},{H},128] and [{T},{H},256] bf16 3-bit, K and V")
+    tq128, ck128, enc_k, enc_v = codec_setup(128, 0)
+    _, _, enc_k256, _ = codec_setup(256, 10)
+    dec_out = torch.empty(T, H, 128, dtype=torch.float32, device=dev)
+    lev, sg = tq128.quantizer.levels, tq128.rotation.signs
 
     def dec_k():
-        L.ftq_decode(ck.indices.data_ptr(), ck.norms.data_ptr(), n, d, lev.data_ptr(),
-                     signs.data_ptr(), bits, dec_out.data_ptr(), 0, sp)
+        _lib.check(L.ftq_decode(ck128.indices.data_ptr(), ck128.norms.data_ptr(), n, 128, lev.data_ptr(),
+                                sg.data_ptr(), bits, dec_out.data_ptr(), 0, sp))
 
-    attn = None
-    try:
-        from fused_turboquant import paged as P
-        attn = P.bench_setup(dev)
-    except (ImportError, AttributeError):
-        attn = None
+    log("[bench] config3 paged cache (B=32 ctx=8192 K3V3)")
+    attn3 = P.bench_setup(dev)
+    log("[bench] config4 v1 cache (B=4 ctx~U[64K,128K] K4V2 v_rotate)")
+    attn4 = V1.bench_setup(dev)
+    torch.cuda.synchronize()
 
     def step():
         enc_k()
         enc_v()
-        if attn is not None:
-            attn["run"]()
+        attn3["run"]()
 
     if args.calib_copy:
         src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
@@ -149,32 +167,26 @@ def main():
     ms_step = e0.elapsed_time(e1) / args.steps
     log(f"[bench] {args.steps} steps: {ms_step * 1e3:.1f} us/step (event), {wall_ms * 1e3:.1f} us/step (wall)")
 
-    # per-kernel averages on the launch stream
     it = max(args.steps, 20)
     t_enc = time_launches(enc_k, it, torch)
+    t_enc256 = time_launches(enc_k256, it, torch)
     t_dec = time_launches(dec_k, it, torch)
-    enc_bytes = n * d * 2 + n * (d * bits // 8) + n * 2
-    dec_bytes = n * (d * bits // 8) + n * 2 + n * d * 4
-    enc_in_gbs = n * d * 2 / (t_enc * 1e-6) / 1e9
-    enc_gbs = enc_bytes / (t_enc * 1e-6) / 1e9
-    dec_gbs = dec_bytes / (t_dec * 1e-6) / 1e9
-    log(f"[bench] encode {t_enc:.2f} us  {enc_gbs:.0f} GB/s total ({enc_in_gbs:.0f} GB/s bf16 in)")
-    log(f"[bench] decode {t_dec:.2f} us  {dec_gbs:.0f} GB/s total")
+    t_a3 = time_launches(attn3["run"], it, torch)
+    t_a4 = time_launches(attn4["run"], it, torch)
 
-    extra = {}
-    if attn is not None:
-        t_attn = time_launches(attn["run"], it, torch)
-        kv = attn["kv_bytes"]
-        tot = attn["total_bytes"]
-        extra["attn_us_per_step"] = round(t_attn, 2)
-        extra["attn_kv_gbs"] = round(kv / (t_attn * 1e-6) / 1e9, 1)
-        extra["attn_frac_hbm"] = round(tot / (t_attn * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
-        for kname, t in attn.get("kernels", {}).items():
-            extra[f"attn_{kname}_us"] = round(time_launches(t, it, torch), 2)
-        log(f"[bench] paged decode attention {t_attn:.2f} us/step, {extra['attn_kv_gbs']} GB/s KV")
-
-    extra["decode_us"] = round(t_dec, 2)
-    extra["decode_frac_hbm"] = round(dec_gbs / HBM_PEAK_GBS, 4)
+    enc_bytes = n * 128 * 2 + n * (128 * bits // 8) + n * 2
+    enc256_bytes = n * 256 * 2 + n * (256 * bits // 8) + n * 2
+    dec_bytes = n * (128 * bits // 8) + n * 2 + n * 128 * 4
+    rl = {
+        "encode_d128_3bit": roof("encode_d128_3bit", enc_bytes, t_enc),
+        "encode_d256_3bit": roof("encode_d256_3bit", enc256_bytes, t_enc256),
+        "decode_d128_3bit_f32": roof("decode_d128_3bit_f32", dec_bytes, t_dec),
+        "paged_attn_config3": roof("paged_attn_config3", attn3["total_bytes"], t_a3),
+        "v1_attn_config4": roof("v1_attn_config4", attn4["total_bytes"], t_a4),
+    }
+    for k, r in rl.items():
+        log(f"[bench] {k}: {r['kernel_us']} us  {r['achieved']} GB/s  frac {r['frac']}")
+    enc_in_gbs = n * 128 * 2 / (t_enc * 1e-6) / 1e9
 
     cpu = None
     if not args.no_cpu:
@@ -184,6 +196,8 @@ def main():
                "sample": sample + f"; host {platform.processor() or platform.machine()}, "
                                   f"os.cpu_count()={os.cpu_count()}, numpy single thread"}
 
+    main_roof = dict(rl["encode_d128_3bit"])
+    main_roof["kernel"] = "ftq::encode_kernel<128,3,bf16>"
     out = {
         "metric": "3-bit d128 encode GB/s + paged decode-attn us/step @8K ctx; % of HBM peak",
         "value": round(enc_in_gbs, 1),
@@ -192,16 +206,19 @@ def main():
         "ms_per_step": round(ms_step, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "bf16 in / fp32 math / u8 codes", "data": "synthetic",
-        "config": {"workload": "config2 encode K+V [32768,8,128] bf16 3-bit"
-                               + (" + config3 paged decode attention B=32 Hq=32 Hkv=8 ctx=8192 page=16"
-                                  if attn is not None else ""),
-                   "encode_us": round(t_enc, 2)},
-        "roofline": {"bound": "hbm", "achieved": round(enc_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(enc_gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "encode_kernel<128,3,bf16>", "algorithmic_bytes": enc_bytes},
+        "config": {"workload": "config2 encode K+V [32768,8,128] bf16 3-bit + config3 paged decode "
+                               "attention B=32 Hq=32 Hkv=8 d=128 ctx=8192 page=16 K3V3",
+                   "encode_us": round(t_enc, 2),
+                   "attn_us_per_step": round(t_a3, 2),
+                   "attn_kv_gbs": round(attn3["kv_bytes"] / (t_a3 * 1e-6) / 1e9, 1),
+                   "attn_splits": attn3["splits"],
+                   "config4_attn_us_per_step": round(t_a4, 2),
+                   "config4_kv_gbs": round(attn4["kv_bytes"] / (t_a4 * 1e-6) / 1e9, 1),
+                   "config4_ctx": attn4["lens"], "config4_splits": attn4["splits"]},
+        "roofline": main_roof,
+        "rooflines": rl,
         "cpu_baseline": cpu,
     }
-    out.update(extra)
     print(json.dumps(out), flush=True)
 
 
