@@ -16,6 +16,7 @@
 // dword stores; nothing goes through HBM scratch.
 #include "ftq_codec_dev.h"
 #include "ftq_encode_fast.h"
+#include "ftq_encode_mfma.h"
 #include "ftq_internal.h"
 
 #include <cmath>
@@ -157,6 +158,18 @@ __global__ __launch_bounds__(256) void rht_kernel(const void* __restrict__ x, in
 
 float fwht_scale(int d) { return (float)std::pow((double)d, -0.5); }
 
+// Workgroups (256 threads) that fit on the device at once for kernel k.
+template <typename K>
+static int resident_workgroups(K k) {
+  int dev = 0, cus = 0, per_cu = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, 256, 0) != hipSuccess || cus <= 0 ||
+      per_cu <= 0)
+    return 512;
+  return cus * per_cu;
+}
+
 int codec_grid(int64_t n, int gpb) {
   int64_t want = (n + gpb - 1) / gpb;
   const int64_t cap = 256 * 16;  // 16 workgroups per CU on 256 CUs
@@ -169,10 +182,27 @@ template <int D, int BITS>
 static hipError_t launch_encode_db(const void* x, int dt, int64_t n, const float* signs,
                                    const float* bnd, uint8_t* packed, uint16_t* norms,
                                    hipStream_t st) {
-  constexpr int VPB = 256 / FastShape<D>::LPV;
-  dim3 grid(codec_grid(n, VPB)), block(256);
   const float sc = fwht_scale(D);
   const double rsc = 1.0 / (double)sc;
+  if constexpr (D == 128 || D == 256) {
+    if (dt != F32) {  // 16-bit inputs: Hadamard transform on the matrix cores
+      // one pass of resident workgroups, each wave looping over groups of 16 vectors
+      const int64_t want = (n + 63) / 64;
+      dim3 block(256);
+      if (dt == F16) {
+        static const int cap = resident_workgroups(encode_mfma_kernel<D, BITS, F16>);
+        encode_mfma_kernel<D, BITS, F16><<<dim3((unsigned)(want < cap ? want : cap)), block, 0, st>>>(
+            x, n, signs, bnd, sc, rsc, packed, norms);
+      } else {
+        static const int cap = resident_workgroups(encode_mfma_kernel<D, BITS, BF16>);
+        encode_mfma_kernel<D, BITS, BF16><<<dim3((unsigned)(want < cap ? want : cap)), block, 0, st>>>(
+            x, n, signs, bnd, sc, rsc, packed, norms);
+      }
+      return hipGetLastError();
+    }
+  }
+  constexpr int VPB = 256 / FastShape<D>::LPV;
+  dim3 grid(codec_grid(n, VPB)), block(256);
   if (dt == F32) encode_kernel<D, BITS, F32><<<grid, block, 0, st>>>(x, n, signs, bnd, sc, rsc, packed, norms);
   else if (dt == F16) encode_kernel<D, BITS, F16><<<grid, block, 0, st>>>(x, n, signs, bnd, sc, rsc, packed, norms);
   else encode_kernel<D, BITS, BF16><<<grid, block, 0, st>>>(x, n, signs, bnd, sc, rsc, packed, norms);
