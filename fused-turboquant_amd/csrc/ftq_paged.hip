@@ -34,6 +34,7 @@
 // merge through LDS; splits merge in a second kernel that also applies the
 // inverse RHT of V and writes the output dtype.
 #include "ftq_attn_dev.h"
+#include "ftq_merge.h"
 #include "ftq_codec_dev.h"
 #include "ftq_internal.h"
 
@@ -461,46 +462,8 @@ __global__ __launch_bounds__(256, 4) void paged_attn_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// decode attention, stage 2: merge splits + inverse RHT of V + output cast
-// ---------------------------------------------------------------------------
-template <int D, int OT>
-__global__ __launch_bounds__(256) void paged_merge_kernel(const float* __restrict__ ws_o,
-                                                          const float* __restrict__ ws_lse,
-                                                          int64_t rows, int num_splits,
-                                                          const float* __restrict__ vsigns,
-                                                          float scale, void* __restrict__ out) {
-  constexpr int E = D / 16;
-  const int lane = threadIdx.x & 15;
-  const int64_t r = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
-  if (r >= rows) return;  // whole 16-lane group exits together
-  float M = -INFINITY;
-  for (int s = 0; s < num_splits; ++s) M = fmaxf(M, ws_lse[r * num_splits + s]);
-  float y[E];
-#pragma unroll
-  for (int i = 0; i < E; ++i) y[i] = 0.f;
-  float W = 0.f;
-  if (M != -INFINITY) {
-    for (int s = 0; s < num_splits; ++s) {
-      const float l = ws_lse[r * num_splits + s];
-      const float w = __builtin_amdgcn_exp2f(l - M);
-      W += w;
-      float x[E];
-      load_elems<F32, E>(ws_o, (r * num_splits + s) * D + lane * E, x);
-#pragma unroll
-      for (int i = 0; i < E; ++i) y[i] = __builtin_fmaf(w, x[i], y[i]);
-    }
-  }
-  const float inv = (W > 0.f) ? 1.f / W : 0.f;
-#pragma unroll
-  for (int i = 0; i < E; ++i) y[i] *= inv;
-  fwht_lanes<E, 16>(y, lane);
-#pragma unroll
-  for (int i = 0; i < E; ++i) y[i] = (y[i] * scale) * vsigns[lane * E + i];
-  store_elems<OT, E>(out, r * D + lane * E, y);
-}
-
-// ---------------------------------------------------------------------------
-// host launchers
+// host launchers (stage 2 -- merge of the splits, inverse RHT of V, output
+// cast -- is merge_splits_kernel in ftq_merge.h)
 // ---------------------------------------------------------------------------
 float fwht_scale(int d);
 
@@ -582,12 +545,10 @@ static hipError_t launch_attn3(const AttnArgs& a, hipStream_t st) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int64_t rows = (int64_t)a.B * a.hq;
-  dim3 g2((unsigned)((rows + 15) / 16)), b2(256);
   const float sc = fwht_scale(D);
-  if (a.ot == F32) paged_merge_kernel<D, F32><<<g2, b2, 0, st>>>(a.wo, a.wl, rows, a.splits, a.vs, sc, a.out);
-  else if (a.ot == F16) paged_merge_kernel<D, F16><<<g2, b2, 0, st>>>(a.wo, a.wl, rows, a.splits, a.vs, sc, a.out);
-  else paged_merge_kernel<D, BF16><<<g2, b2, 0, st>>>(a.wo, a.wl, rows, a.splits, a.vs, sc, a.out);
-  return hipGetLastError();
+  if (a.ot == F32) return launch_merge_splits<D, F32, ROT_SIGNS>(a.wo, a.wl, rows, a.splits, a.vs, sc, a.out, st);
+  if (a.ot == F16) return launch_merge_splits<D, F16, ROT_SIGNS>(a.wo, a.wl, rows, a.splits, a.vs, sc, a.out, st);
+  return launch_merge_splits<D, BF16, ROT_SIGNS>(a.wo, a.wl, rows, a.splits, a.vs, sc, a.out, st);
 }
 
 template <int D, int BK>

@@ -40,6 +40,7 @@
 // only raised when a tile exceeds it by 2^8).  Waves merge through LDS; splits
 // merge in a second kernel that also un-rotates V and writes the output dtype.
 #include "ftq_attn_dev.h"
+#include "ftq_merge.h"
 #include "ftq_codec_dev.h"
 #include "ftq_internal.h"
 
@@ -941,47 +942,9 @@ __global__ __launch_bounds__(256, 2) void v1_attn_g4_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// decode attention, stage 2: LSE merge of the splits, V un-rotation, output cast
-// (the merge of vLLM's stage-2 kernel, v1_backend.py:1070-1093)
-// ---------------------------------------------------------------------------
-template <int D, int OT>
-__global__ __launch_bounds__(256) void v1_merge_kernel(const float* __restrict__ ws_o,
-                                                       const float* __restrict__ ws_lse, int64_t rows,
-                                                       int num_splits, int v_rotate, float rscale,
-                                                       void* __restrict__ out) {
-  constexpr int E = D / 16;
-  const int lane = threadIdx.x & 15;
-  const int64_t r = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
-  if (r >= rows) return;  // whole 16-lane group exits together
-  float M = -INFINITY;
-  for (int s = 0; s < num_splits; ++s) M = fmaxf(M, ws_lse[r * num_splits + s]);
-  float y[E];
-#pragma unroll
-  for (int i = 0; i < E; ++i) y[i] = 0.f;
-  float W = 0.f;
-  if (M != -INFINITY) {
-    for (int s = 0; s < num_splits; ++s) {
-      const float w = __builtin_amdgcn_exp2f(ws_lse[r * num_splits + s] - M);
-      W += w;
-      float x[E];
-      load_elems<F32, E>(ws_o, (r * num_splits + s) * D + lane * E, x);
-#pragma unroll
-      for (int i = 0; i < E; ++i) y[i] = __builtin_fmaf(w, x[i], y[i]);
-    }
-  }
-  const float inv = (W > 0.f) ? 1.f / W : 0.f;
-#pragma unroll
-  for (int i = 0; i < E; ++i) y[i] *= inv;
-  if (v_rotate) {  // uniform
-    fwht_lanes<E, 16>(y, lane);
-#pragma unroll
-    for (int i = 0; i < E; ++i) y[i] *= rscale;
-  }
-  store_elems<OT, E>(out, r * D + lane * E, y);
-}
-
-// ---------------------------------------------------------------------------
-// host launchers
+// host launchers (stage 2 -- LSE merge of the splits, V un-rotation, output
+// cast, the merge of vLLM's stage-2 kernel, v1_backend.py:1070-1093 -- is
+// merge_splits_kernel in ftq_merge.h)
 // ---------------------------------------------------------------------------
 
 template <int D>
@@ -1037,12 +1000,15 @@ static hipError_t v1_launch_attn3(const V1Args& a, hipStream_t st) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int64_t rows = (int64_t)a.B * a.hq;
-  dim3 g2((unsigned)((rows + 15) / 16)), b2(256);
   const float rs = fwht_scale(D);
-  if (a.ot == F32) v1_merge_kernel<D, F32><<<g2, b2, 0, st>>>(a.wo, a.wl, rows, a.splits, a.vrot, rs, a.out);
-  else if (a.ot == F16) v1_merge_kernel<D, F16><<<g2, b2, 0, st>>>(a.wo, a.wl, rows, a.splits, a.vrot, rs, a.out);
-  else v1_merge_kernel<D, BF16><<<g2, b2, 0, st>>>(a.wo, a.wl, rows, a.splits, a.vrot, rs, a.out);
-  return hipGetLastError();
+  if (a.vrot) {
+    if (a.ot == F32) return launch_merge_splits<D, F32, ROT_PLAIN>(a.wo, a.wl, rows, a.splits, nullptr, rs, a.out, st);
+    if (a.ot == F16) return launch_merge_splits<D, F16, ROT_PLAIN>(a.wo, a.wl, rows, a.splits, nullptr, rs, a.out, st);
+    return launch_merge_splits<D, BF16, ROT_PLAIN>(a.wo, a.wl, rows, a.splits, nullptr, rs, a.out, st);
+  }
+  if (a.ot == F32) return launch_merge_splits<D, F32, ROT_NONE>(a.wo, a.wl, rows, a.splits, nullptr, rs, a.out, st);
+  if (a.ot == F16) return launch_merge_splits<D, F16, ROT_NONE>(a.wo, a.wl, rows, a.splits, nullptr, rs, a.out, st);
+  return launch_merge_splits<D, BF16, ROT_NONE>(a.wo, a.wl, rows, a.splits, nullptr, rs, a.out, st);
 }
 
 template <int D, int KB>
