@@ -246,6 +246,18 @@ __device__ __forceinline__ void load_tile(TileRegs<D, BK, BV>& r, const uint8_t*
   }
 }
 
+// LDS bytes of one paged_attn_kernel workgroup for a GQA group of G heads:
+// one pool reused for the rotated queries (prologue), the code tables (tile
+// loop) and the wave-merge buffer (epilogue)
+template <int D, int BK, int BV, bool SHARE>
+__host__ __device__ constexpr int paged_attn_lds(int G) {
+  const int lut = CodeLut<BK>::BYTES + (SHARE ? 0 : CodeLut<BV>::BYTES);
+  const int red = 4 * G * (D + 1) * 4;
+  const int qs = G * (D + 8) * 2;
+  const int m = lut > red ? lut : red;
+  return m > qs ? m : qs;
+}
+
 template <int D, int BK, int BV, int QT, bool SHARE>
 __global__ __launch_bounds__(256, 4) void paged_attn_kernel(
     const void* __restrict__ query, const uint8_t* __restrict__ cache,
@@ -261,20 +273,15 @@ __global__ __launch_bounds__(256, 4) void paged_attn_kernel(
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int h = lane & 15, q = lane >> 4;
 
-  // LDS pool, reused in three phases: rotated queries (prologue), code tables
-  // (tile loop), wave-merge buffer (epilogue)
+  // LDS pool (paged_attn_lds(G) bytes, dynamic), reused in three phases:
+  // rotated queries (prologue), code tables (tile loop), wave-merge buffer
+  // (epilogue)
   constexpr int LUTK_BYTES = CodeLut<BK>::BYTES;
-  constexpr int LUTV_BYTES = SHARE ? 0 : CodeLut<BV>::BYTES;
-  constexpr int RED_BYTES = 4 * 16 * (D + 1) * 4;
-  constexpr int QS_BYTES = 16 * (D + 8) * 2;
-  constexpr int POOL = (LUTK_BYTES + LUTV_BYTES > RED_BYTES ? LUTK_BYTES + LUTV_BYTES : RED_BYTES) > QS_BYTES
-                           ? (LUTK_BYTES + LUTV_BYTES > RED_BYTES ? LUTK_BYTES + LUTV_BYTES : RED_BYTES)
-                           : QS_BYTES;
-  __shared__ __attribute__((aligned(16))) uint8_t pool[POOL];
+  extern __shared__ __attribute__((aligned(16))) uint8_t pool[];
   __shared__ float red_m[4][16], red_l[4][16];
   __shared__ uint16_t lev16[2][16];  // fp16 K / V levels
   _Float16 (*qs)[D + 8] = reinterpret_cast<_Float16 (*)[D + 8]>(pool);
-  float (*red_o)[16][D + 1] = reinterpret_cast<float (*)[16][D + 1]>(pool);
+  float* red_o = reinterpret_cast<float*>(pool);  // [4 waves][G heads][D + 1]
   uint8_t* lutK = pool;
   uint8_t* lutV = SHARE ? pool : pool + LUTK_BYTES;
 
@@ -383,17 +390,19 @@ __global__ __launch_bounds__(256, 4) void paged_attn_kernel(
     Op8 pb;
 #pragma unroll
     for (int sb = 0; sb < 2; ++sb) {
-      uint32_t h16[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float p = __builtin_amdgcn_exp2f(s[sb][i] - m_sc);
-        psum += p;
-        const uint32_t vnw = cur.ok[sb] ? cur.vn[sb][i >> 1] : 0u;
-        const _Float16 vn = __builtin_bit_cast(_Float16, (uint16_t)(vnw >> (16 * (i & 1))));
-        h16[i] = __builtin_bit_cast(uint16_t, (_Float16)__builtin_fmaf(p, (float)vn, 0.f));
+      for (int i2 = 0; i2 < 2; ++i2) {
+        // V norms of two tokens as f16 halves (zero for a flagged sub-block);
+        // the products are rounded straight into the two halves of the operand
+        const half2_t vn = __builtin_bit_cast(half2_t, cur.ok[sb] ? cur.vn[sb][i2] : 0u);
+        const float p0 = __builtin_amdgcn_exp2f(s[sb][2 * i2] - m_sc);
+        const float p1 = __builtin_amdgcn_exp2f(s[sb][2 * i2 + 1] - m_sc);
+        psum += p0;
+        psum += p1;
+        const half2_t pv = {(_Float16)__builtin_fmaf(p0, (float)vn[0], 0.f),
+                            (_Float16)__builtin_fmaf(p1, (float)vn[1], 0.f)};
+        pb.u[2 * sb + i2] = __builtin_bit_cast(uint32_t, pv);
       }
-      pb.u[2 * sb] = h16[0] | (h16[1] << 16);
-      pb.u[2 * sb + 1] = h16[2] | (h16[3] << 16);
     }
     psum *= 512.f;
     l_run += psum;
@@ -434,10 +443,13 @@ __global__ __launch_bounds__(256, 4) void paged_attn_kernel(
     red_m[wave][h] = m_run;
     red_l[wave][h] = l_tot;
   }
+  if (h < G) {
+    float* ro = red_o + (wave * G + h) * (D + 1);
 #pragma unroll
-  for (int bb = 0; bb < NB; ++bb)
+    for (int bb = 0; bb < NB; ++bb)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) red_o[wave][h][16 * bb + 4 * q + i] = acc[bb][i];
+      for (int i = 0; i < 4; ++i) ro[16 * bb + 4 * q + i] = acc[bb][i];
+  }
   __syncthreads();
 
   const int64_t row0 = ((int64_t)b * hq + kvh * G) * num_splits + split;  // (b, head g=0, split)
@@ -452,7 +464,7 @@ __global__ __launch_bounds__(256, 4) void paged_attn_kernel(
       for (int w = 0; w < 4; ++w) {
         const float f = __builtin_amdgcn_exp2f(red_m[w][g] - M);
         L += f * red_l[w][g];
-        o += f * red_o[w][g][d];
+        o += f * red_o[(w * G + g) * (D + 1) + d];
       }
     }
     const int64_t row = row0 + (int64_t)g * num_splits;
@@ -525,12 +537,13 @@ struct AttnArgs {
 template <int D, int BK, int BV, bool SHARE>
 static void launch_attn_kernel(const AttnArgs& a, hipStream_t st) {
   dim3 grid(a.splits, a.hkv, a.B), block(256);
+  const size_t lds = (size_t)paged_attn_lds<D, BK, BV, SHARE>(a.hq / a.hkv);
   if (a.qt == F32)
-    paged_attn_kernel<D, BK, BV, F32, SHARE><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.hq, a.hkv, a.page_size, a.max_blocks, a.num_blocks, a.ks, a.kl, a.vl, a.qscale, a.splits, a.wo, a.wl);
+    paged_attn_kernel<D, BK, BV, F32, SHARE><<<grid, block, lds, st>>>(a.q, a.cache, a.bt, a.sl, a.hq, a.hkv, a.page_size, a.max_blocks, a.num_blocks, a.ks, a.kl, a.vl, a.qscale, a.splits, a.wo, a.wl);
   else if (a.qt == F16)
-    paged_attn_kernel<D, BK, BV, F16, SHARE><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.hq, a.hkv, a.page_size, a.max_blocks, a.num_blocks, a.ks, a.kl, a.vl, a.qscale, a.splits, a.wo, a.wl);
+    paged_attn_kernel<D, BK, BV, F16, SHARE><<<grid, block, lds, st>>>(a.q, a.cache, a.bt, a.sl, a.hq, a.hkv, a.page_size, a.max_blocks, a.num_blocks, a.ks, a.kl, a.vl, a.qscale, a.splits, a.wo, a.wl);
   else
-    paged_attn_kernel<D, BK, BV, BF16, SHARE><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.hq, a.hkv, a.page_size, a.max_blocks, a.num_blocks, a.ks, a.kl, a.vl, a.qscale, a.splits, a.wo, a.wl);
+    paged_attn_kernel<D, BK, BV, BF16, SHARE><<<grid, block, lds, st>>>(a.q, a.cache, a.bt, a.sl, a.hq, a.hkv, a.page_size, a.max_blocks, a.num_blocks, a.ks, a.kl, a.vl, a.qscale, a.splits, a.wo, a.wl);
 }
 
 template <int D, int BK, int BV>
@@ -565,10 +578,10 @@ static hipError_t launch_attn1(int bk, int bv, const AttnArgs& a, hipStream_t st
   return launch_attn2<D, 4>(bv, a, st);
 }
 
-int auto_splits(int batch, int hkv, int seq_hint) {
-  // aim for ~1024 workgroups (4 per CU) with at least 8 tiles per wave
+int auto_splits(int batch, int hkv, int seq_hint, int target_wgs) {
+  // aim for target_wgs workgroups with at least 8 tiles per wave
   const int units = batch * hkv;
-  int s = (1024 + units - 1) / units;
+  int s = (target_wgs + units - 1) / units;
   const int max_by_len = seq_hint / (32 * 4 * 8);
   if (s > max_by_len) s = max_by_len;
   if (s < 1) s = 1;
@@ -591,7 +604,7 @@ extern "C" int64_t ftq_paged_workspace_bytes(int batch, int num_q_heads, int d, 
 }
 
 extern "C" int ftq_paged_default_splits(int batch, int num_kv_heads, int max_seq_len) {
-  return auto_splits(batch, num_kv_heads, max_seq_len);
+  return auto_splits(batch, num_kv_heads, max_seq_len, 1024);  // 4 workgroups per CU
 }
 
 extern "C" int ftq_paged_store(const void* key, const void* value, int dtype, int64_t n_tokens,

@@ -1018,7 +1018,7 @@ static hipError_t v1_launch_attn2(int vb, const V1Args& a, hipStream_t st) {
   return v1_launch_attn3<D, KB, 4>(a, st);
 }
 
-int auto_splits(int batch, int hkv, int seq_hint);
+int auto_splits(int batch, int hkv, int seq_hint, int target_wgs);
 
 }  // namespace ftq
 
@@ -1069,7 +1069,7 @@ extern "C" int64_t ftq_v1_workspace_bytes(int batch, int num_q_heads, int d, int
 }
 
 extern "C" int ftq_v1_default_splits(int batch, int num_kv_heads, int max_seq_len) {
-  return auto_splits(batch, num_kv_heads, max_seq_len);
+  return auto_splits(batch, num_kv_heads, max_seq_len, 1024);
 }
 
 extern "C" int ftq_v1_decode_attention(
