@@ -34,7 +34,13 @@ HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, AMD published
 # script, each scaled by the factor a 256 MiB device-to-device copy reads
 # (FETCH x2.0, WRITE x1.0); the summaries are in profiles/hbm_traffic_counters.md.
 # Keyed by roofline entry; None where no counter run covers the kernel.
-TRAFFIC_BYTES: dict = {}
+TRAFFIC_BYTES: dict = {
+    "encode_d128_3bit": 80316450,
+    "encode_d256_3bit": 160081395,
+    "decode_d128_3bit_f32": 149026181,
+    "paged_attn_config3": 224276668,
+    "v1_attn_config4": 406898134,
+}
 
 
 def log(msg):
