@@ -167,45 +167,77 @@ __global__ __launch_bounds__(256) void paged_store_kernel(
 // decode attention, stage 1 (per split)
 // ---------------------------------------------------------------------------
 
-// Code lookup tables in LDS.  For B <= 3 bits an entry covers 4 codes
-// (index = c0 | c1 << B | c2 << 2B | c3 << 3B, 8 bytes = 4 f16), so one
-// ds_read_b64 dequantises 4 codes; 4-bit codes use 2-code entries (f16x2).
+// Code lookup tables in LDS: an entry holds the f16 levels of two codes
+// (index = c0 | c1 << B, one ds_read_b32 dequantises two codes).  The LDS
+// serves a wave in 32-lane phases over 32 four-byte banks, so a 64-entry
+// table (3-bit codes) has two entries per bank and random indices collide.
+// For 3 bits the table is therefore stored in 32 copies, one per bank: entry
+// e of copy c sits at dword e * 32 + c, and lane l reads copy l % 32, so every
+// lane of a phase hits its own bank.  (2-bit tables have 16 entries and are
+// conflict-free as they are; 4-bit tables keep one 256-entry copy.)
 template <int B>
 struct CodeLut {
-  static constexpr bool QUAD = false;  // 4-code tables: bank conflicts outweigh the saved VALU on gfx950
-  static constexpr int CODES = QUAD ? 4 : 2;
+  static constexpr int CODES = 2;
   static constexpr int IDX_BITS = CODES * B;
   static constexpr int ENTRIES = 1 << IDX_BITS;
-  static constexpr int ENTRY_BYTES = 2 * CODES;
-  static constexpr int BYTES = ENTRIES * ENTRY_BYTES;
+  static constexpr int LOG_COPIES = (B == 3) ? 5 : 0;
+  static constexpr int COPIES = 1 << LOG_COPIES;
+  static constexpr int BYTES = ENTRIES * 4 * COPIES;
 };
 
 // fill a code table from the fp16 level values already staged in LDS:
-// entry e -> f16(levels[code k of e]) for k < CODES
+// entry e -> f16(levels[e & (2^B - 1)]) | f16(levels[e >> B]) << 16, in every copy
 template <int B>
 __device__ void build_code_lut(uint8_t* lut, const uint16_t* single, int tid, int nthreads) {
   using C = CodeLut<B>;
-  for (int e = tid; e < C::ENTRIES; e += nthreads) {
-    uint32_t w[2] = {0u, 0u};
-#pragma unroll
-    for (int k = 0; k < C::CODES; ++k)
-      w[k >> 1] |= (uint32_t)single[(e >> (k * B)) & ((1 << B) - 1)] << (16 * (k & 1));
-    if constexpr (C::QUAD) reinterpret_cast<uint2*>(lut)[e] = make_uint2(w[0], w[1]);
-    else reinterpret_cast<uint32_t*>(lut)[e] = w[0];
+  for (int k = tid; k < C::ENTRIES * C::COPIES; k += nthreads) {
+    const int e = k >> C::LOG_COPIES;
+    reinterpret_cast<uint32_t*>(lut)[k] =
+        (uint32_t)single[e & ((1 << B) - 1)] | ((uint32_t)single[e >> B] << 16);
   }
 }
 
-// dequantise the codes at bits [P, P + 4B) (quad) into two f16x2 dwords
-template <int B, int N>
-__device__ __forceinline__ uint2 lut_quad(const uint8_t* lut, const uint32_t (&w)[N], int P) {
-  using C = CodeLut<B>;
-  if constexpr (C::QUAD) {
-    return *reinterpret_cast<const uint2*>(lut + field_off<3>(w, P, C::IDX_BITS));
-  } else {
-    const uint32_t lo = *reinterpret_cast<const uint32_t*>(lut + field_off<2>(w, P, C::IDX_BITS));
-    const uint32_t hi = *reinterpret_cast<const uint32_t*>(lut + field_off<2>(w, P + 2 * B, C::IDX_BITS));
-    return make_uint2(lo, hi);
+// LDS byte address of this lane's copy of a code table
+template <int B>
+__device__ __forceinline__ uint32_t lut_lane_base(int lane, uint32_t table_addr) {
+  return table_addr + (((uint32_t)lane & (CodeLut<B>::COPIES - 1u)) << 2);
+}
+
+// dequantise the 4 codes at bits [P, P + 4B) into two f16x2 dwords; the
+// address of each is one shift and one and-or
+// Byte offset of the table entry whose index is bits [P, P + W) of the code
+// words: (field << SH) + base, as v_bfe_u32 + v_lshl_add_u32 (LLVM would
+// otherwise split it into shift, and, add).  A field across two words first
+// goes through v_alignbit_b32.
+template <int SH, int W, int N>
+__device__ __forceinline__ uint32_t lut_entry_off(const uint32_t (&w)[N], int P, uint32_t base) {
+  const int i = P >> 5, o = P & 31;  // compile-time after unrolling
+  uint32_t src = w[i], f, r;
+  int off = o;
+  if (o + W > 32 && i + 1 < N) {
+    src = __builtin_amdgcn_alignbit(w[i + 1], w[i], o);
+    off = 0;
   }
+  asm("v_bfe_u32 %0, %1, %2, %3" : "=v"(f) : "v"(src), "n"(off), "n"(W));
+  asm("v_lshl_add_u32 %0, %1, %2, %3" : "=v"(r) : "v"(f), "n"(SH), "v"(base));
+  return r;
+}
+
+typedef __attribute__((address_space(3))) const uint32_t lds_u32;
+
+// LDS address of a __shared__ object
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
+}
+
+// base = LDS address of this lane's copy of the table (lds_addr(table) | copy)
+template <int B, int N>
+__device__ __forceinline__ uint2 lut_quad(const uint32_t (&w)[N], int P, uint32_t base) {
+  using C = CodeLut<B>;
+  constexpr int SH = 2 + C::LOG_COPIES;
+  const uint32_t lo = *(lds_u32*)(uintptr_t)lut_entry_off<SH, C::IDX_BITS>(w, P, base);
+  const uint32_t hi = *(lds_u32*)(uintptr_t)lut_entry_off<SH, C::IDX_BITS>(w, P + 2 * B, base);
+  return make_uint2(lo, hi);
 }
 
 template <int D, int BK, int BV>
@@ -335,6 +367,8 @@ __global__ __launch_bounds__(256, 4) void paged_attn_kernel(
   const int nsub = page_size >> 4;
   const int32_t* bt_row = block_table + (int64_t)b * max_blocks;
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);  // wave-uniform -> scalar tile math
+  const uint32_t baseK = lut_lane_base<BK>(lane, lds_addr(lutK));
+  const uint32_t baseV = lut_lane_base<BV>(lane, lds_addr(lutV));
 
   float m_run = -INFINITY, l_run = 0.f;
   floatx4 acc[NB];
@@ -355,8 +389,8 @@ __global__ __launch_bounds__(256, 4) void paged_attn_kernel(
 #pragma unroll
       for (int st = 0; st < NS; ++st) {
         Op8 a;
-        const uint2 c01 = lut_quad<BK>(lutK, cur.k[sb], (8 * st) * BK);
-        const uint2 c23 = lut_quad<BK>(lutK, cur.k[sb], (8 * st + 4) * BK);
+        const uint2 c01 = lut_quad<BK>(cur.k[sb], (8 * st) * BK, baseK);
+        const uint2 c23 = lut_quad<BK>(cur.k[sb], (8 * st + 4) * BK, baseK);
         a.u[0] = c01.x; a.u[1] = c01.y; a.u[2] = c23.x; a.u[3] = c23.y;
         c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a.h, qb[st].h, c, 0, 0, 0);
       }
@@ -411,7 +445,7 @@ __global__ __launch_bounds__(256, 4) void paged_attn_kernel(
       Op8 a;
 #pragma unroll
       for (int sb = 0; sb < 2; ++sb) {
-        const uint2 t4 = lut_quad<BV>(lutV, cur.v[sb], (4 * bb) * BV);
+        const uint2 t4 = lut_quad<BV>(cur.v[sb], (4 * bb) * BV, baseV);
         a.u[2 * sb] = t4.x;
         a.u[2 * sb + 1] = t4.y;
       }
