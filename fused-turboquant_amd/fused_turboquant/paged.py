@@ -150,6 +150,59 @@ def paged_decode_attention(query: torch.Tensor, kv_cache: torch.Tensor, block_ta
     return out
 
 
+_V_GATHER: dict = {}
+
+
+def _v_gather_index(head_dim: int, bits_v: int, device) -> torch.Tensor:
+    """Bit index, into the 64 V lane chunks of a sub-block laid out as one bit
+    stream, of bit k of the code of (token t, dim e): chunk 16 (t // 4) + e % 16,
+    bit (4 (e // 16) + t % 4) bits_v + k.  Shape [16, head_dim, bits_v]."""
+    key = (head_dim, bits_v, str(device))
+    if key not in _V_GATHER:
+        vlane_bits = head_dim * bits_v // 4
+        t = torch.arange(16).view(16, 1, 1)
+        e = torch.arange(head_dim).view(1, head_dim, 1)
+        k = torch.arange(bits_v).view(1, 1, bits_v)
+        chunk = 16 * (t // 4) + e % 16
+        bit = (4 * (e // 16) + t % 4) * bits_v + k
+        _V_GATHER[key] = (chunk * vlane_bits + bit).to(device)
+    return _V_GATHER[key]
+
+
+def _pack_codes(codes: torch.Tensor, bits: int) -> torch.Tensor:
+    from .core.packing import pack_2bit, pack_3bit, pack_nibbles
+    return {2: pack_2bit, 3: pack_3bit, 4: pack_nibbles}[bits](codes)
+
+
+def paged_read(kv_cache: torch.Tensor, blocks: torch.Tensor, head_dim: int, bits_k: int,
+               bits_v: int):
+    """Codes and norms of the pages ``blocks`` [n] in the flat library format
+    (``CompressedTensor`` layout, reference ``core/packing.py``):
+    K packed [n, Hkv, page, d*bk/8], K norms [n, Hkv, page] f16, and the same
+    for V.  Plain torch gathers on the device (not on the decode path: the
+    attention kernel reads pages directly)."""
+    nb, hkv, nsub, sub = kv_cache.shape
+    ktok = head_dim * bits_k // 8
+    ksec = 16 * ktok
+    vsec = 64 * (head_dim * bits_v // 32)
+    if sub != ksec + vsec + 64:
+        raise ValueError("kv_cache sub-block size does not match (head_dim, bits)")
+    c = kv_cache.index_select(0, blocks.to(torch.int64))  # [n, Hkv, nsub, sub]
+    n = c.shape[0]
+    k_packed = c[..., :ksec].reshape(n, hkv, nsub * 16, ktok)
+    norms = c[..., ksec + vsec:].contiguous().view(torch.float16)  # [n, Hkv, nsub, 32]
+    k_norms = norms[..., :16].reshape(n, hkv, nsub * 16)
+    v_norms = norms[..., 16:].reshape(n, hkv, nsub * 16)
+    vbytes = c[..., ksec:ksec + vsec].to(torch.int32)  # [n, Hkv, nsub, vsec]
+    vbits = ((vbytes.unsqueeze(-1) >> torch.arange(8, device=c.device, dtype=torch.int32)) & 1)
+    vbits = vbits.reshape(n, hkv, nsub, vsec * 8)
+    idx = _v_gather_index(head_dim, bits_v, c.device)
+    g = vbits[..., idx.reshape(-1)].reshape(n, hkv, nsub, 16, head_dim, bits_v)
+    v_codes = (g << torch.arange(bits_v, device=c.device, dtype=torch.int32)).sum(-1)
+    v_packed = _pack_codes(v_codes.reshape(n, hkv, nsub * 16, head_dim), bits_v)
+    return k_packed, k_norms, v_packed, v_norms
+
+
 class PagedTurboQuantCache:
     """A paged, compressed KV cache of one attention layer.
 

@@ -1,0 +1,127 @@
+"""HF integration on gfx950: the patched model's decode runs the paged decode
+kernel over codes stored by the paged store kernel.
+
+* cache level: decode_attention == float64 softmax attention over the oracle's
+  decode of the stored codes (bf16 tolerance, as for the paged kernel);
+* model level: a left-padded batch gives each sequence the logits it gets
+  alone (padding is not stored); patched vs unpatched first decode logits
+  agree to quantisation accuracy; K-only layers and unpatch work.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import tq_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _tiny_llama(cuda, layers=2, heads=4, kv_heads=2, head_dim=128):
+    from transformers import LlamaConfig, LlamaForCausalLM
+    cfg = LlamaConfig(hidden_size=heads * head_dim, intermediate_size=512, num_hidden_layers=layers,
+                      num_attention_heads=heads, num_key_value_heads=kv_heads, head_dim=head_dim,
+                      vocab_size=320, max_position_embeddings=512)
+    torch.manual_seed(0)
+    return LlamaForCausalLM(cfg).to(device=cuda, dtype=torch.bfloat16).eval()
+
+
+@pytest.mark.parametrize("bk,bv", [(3, 3), (4, 2)])
+def test_cache_decode_attention_matches_dense(cuda, bk, bv):
+    from fused_turboquant import TurboQuantMSE
+    from fused_turboquant.hf import CompressedKVCache
+    g = torch.Generator(device="cpu").manual_seed(bk * 10 + bv)
+    B, hkv, hq, d = 3, 2, 8, 128
+    k_tq, v_tq = TurboQuantMSE(d, bits=bk, device=cuda), TurboQuantMSE(d, bits=bv, device=cuda)
+    cache = CompressedKVCache(k_tq)
+    cache.set_layer_quantizer(0, k_tq)
+    cache.set_layer_quantizer_v(0, v_tq)
+    # prefill of 37 tokens with the first 5 of sequence 0 masked out, then 40 decode steps
+    k = torch.randn(B, hkv, 37, d, generator=g).to(torch.bfloat16).to(cuda)
+    v = torch.randn(B, hkv, 37, d, generator=g).to(torch.bfloat16).to(cuda)
+    keep = torch.ones(B, 37, dtype=torch.bool, device=cuda)
+    keep[0, :5] = False
+    cache.store_compressed_kv(k, v, 0, keep=keep)
+    for _ in range(40):
+        cache.store_compressed_kv(torch.randn(B, hkv, 1, d, generator=g).to(torch.bfloat16).to(cuda),
+                                  torch.randn(B, hkv, 1, d, generator=g).to(torch.bfloat16).to(cuda), 0)
+    assert cache.seq_lens(0) == [72, 77, 77]
+    q = torch.randn(B, hq, d, generator=g).to(torch.bfloat16)
+    out = cache.decode_attention(q.to(cuda), 0, 1 / math.sqrt(d)).float().cpu().numpy()
+    ke, ve = cache.get_compressed_key(0), cache.get_compressed_value(0)
+    S = ke["packed_indices"].shape[2]
+    kd = O.decode(ke["packed_indices"].cpu().numpy().reshape(-1, d * bk // 8), ke["norms"].cpu().numpy().reshape(-1),
+                  k_tq.quantizer.levels.cpu().numpy(), k_tq.rotation.signs.cpu().numpy(), bk, d).reshape(B, hkv, S, d)
+    vd = O.decode(ve["packed_indices"].cpu().numpy().reshape(-1, d * bv // 8), ve["norms"].cpu().numpy().reshape(-1),
+                  v_tq.quantizer.levels.cpu().numpy(), v_tq.rotation.signs.cpu().numpy(), bv, d).reshape(B, hkv, S, d)
+    want = O.dense_decode_attention(q.float().numpy(), kd, vd, cache.seq_lens(0), 1 / math.sqrt(d))
+    err = np.abs(out - want)
+    print(f"[hf cache K{bk}V{bv}] max {err.max():.2e} mean {err.mean():.2e}")
+    assert err.max() <= 2e-2 and err.mean() <= 2e-3
+    # the decoded cache reproduces the stored vectors to quantisation accuracy
+    vv = v[1].float().cpu().numpy()  # sequence 1 stored all 37 prefill tokens
+    cos = (vd[1, :, :37] * vv).sum(-1) / np.linalg.norm(vd[1, :, :37], axis=-1) / np.linalg.norm(vv, axis=-1)
+    assert cos.mean() > (0.97 if bv >= 3 else 0.9)
+
+
+def _gen(model, ids, mask, cache, n):
+    out = model.generate(input_ids=ids, attention_mask=mask, past_key_values=cache, max_new_tokens=n,
+                         do_sample=False, output_logits=True, return_dict_in_generate=True, pad_token_id=0)
+    return out.sequences, torch.stack(out.logits, 1).float()
+
+
+def test_padded_batch_matches_single_sequences(cuda):
+    from fused_turboquant.hf import patch_model
+    model = _tiny_llama(cuda)
+    cache = patch_model(model, bits=4, verify=True)
+    g = torch.Generator().manual_seed(5)
+    a = torch.randint(1, 320, (1, 5), generator=g)
+    b = torch.randint(1, 320, (1, 9), generator=g)
+    ids = torch.zeros(2, 9, dtype=torch.long)
+    mask = torch.zeros(2, 9, dtype=torch.long)
+    ids[0, 4:], mask[0, 4:] = a[0], 1
+    ids[1], mask[1] = b[0], 1
+    with torch.inference_mode():
+        _, lb = _gen(model, ids.to(cuda), mask.to(cuda), cache, 4)
+        cache.reset()
+        _, la = _gen(model, a.to(cuda), torch.ones_like(a).to(cuda), cache, 4)
+        cache.reset()
+        _, l1 = _gen(model, b.to(cuda), torch.ones_like(b).to(cuda), cache, 4)
+        cache.reset()
+    for got, want, tag in ((lb[0], la[0], "seq a"), (lb[1], l1[0], "seq b")):
+        diff = (got - want).abs().max().item()
+        print(f"[hf padded batch {tag}] max logit diff {diff:.3e} (|logit| max {want.abs().max().item():.2f})")
+        assert diff <= 2e-2 * max(1.0, want.abs().max().item())
+
+
+def test_patched_logits_close_to_unpatched(cuda):
+    from fused_turboquant.hf import patch_model, unpatch_model
+    model = _tiny_llama(cuda)
+    ids = torch.randint(1, 320, (2, 24), generator=torch.Generator().manual_seed(9)).to(cuda)
+    mask = torch.ones_like(ids)
+    with torch.inference_mode():
+        _, ref = _gen(model, ids, mask, None, 3)
+        cache = patch_model(model, bits=4, verify=False)
+        _, got = _gen(model, ids, mask, cache, 3)
+        unpatch_model(model)
+        _, again = _gen(model, ids, mask, None, 3)
+    # step 0 comes from the prefill (full precision in both), later steps read the 4-bit cache
+    assert torch.allclose(got[:, 0], ref[:, 0], atol=1e-2, rtol=1e-2)
+    cos = torch.nn.functional.cosine_similarity(got[:, 1:].reshape(-1, got.shape[-1]), ref[:, 1:].reshape(-1, ref.shape[-1]), dim=-1)
+    print(f"[hf patched vs unpatched] decode logits cos min {cos.min().item():.4f}")
+    assert cos.min() > 0.98
+    assert torch.equal(again, ref)
+
+
+@pytest.mark.parametrize("compress_v", [False, "boundary"])
+def test_k_only_layers(cuda, compress_v):
+    from fused_turboquant.hf import patch_model
+    model = _tiny_llama(cuda, layers=4)
+    ids = torch.randint(1, 320, (2, 12), generator=torch.Generator().manual_seed(3)).to(cuda)
+    with torch.inference_mode():
+        _, ref = _gen(model, ids, torch.ones_like(ids), None, 3)
+        cache = patch_model(model, bits=4, compress_v=compress_v, verify=False)
+        _, got = _gen(model, ids, torch.ones_like(ids), cache, 3)
+    cos = torch.nn.functional.cosine_similarity(got.reshape(-1, got.shape[-1]), ref.reshape(-1, ref.shape[-1]), dim=-1)
+    assert torch.isfinite(got).all() and cos.min() > 0.98, cos.min()

@@ -1,0 +1,73 @@
+"""HF integration host logic on the CPU: page reader vs the oracle's, argument
+checks, compatibility report, quantizer routing (no kernel calls)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import tq_oracle as O
+
+
+@pytest.mark.parametrize("d,bk,bv", [(128, 3, 3), (128, 4, 2), (256, 2, 4)])
+def test_paged_read_matches_oracle_page_reader(d, bk, bv):
+    from fused_turboquant import paged as P
+    rng = np.random.default_rng(d + bk * 7 + bv)
+    shape = P.cache_shape(5, 32, 2, d, bk, bv)
+    cache = rng.integers(0, 256, size=shape, dtype=np.uint8)
+    # keep the norm bytes finite fp16 (exponent < 31) so views compare cleanly
+    sub = shape[-1]
+    cache[..., sub - 64 + 1::2] &= 0x7B
+    blocks = torch.tensor([3, 0, 4])
+    kp, kn, vp, vn = P.paged_read(torch.from_numpy(cache), blocks, d, bk, bv)
+    kc, vc, kn_o, vn_o = O.paged_unpack(cache, d, bk, bv)
+    sel = blocks.numpy()
+    assert np.array_equal(O.unpack(kp.numpy(), bk, d), kc[sel])
+    assert np.array_equal(O.unpack(vp.numpy(), bv, d), vc[sel])
+    assert np.array_equal(kn.numpy(), kn_o[sel])
+    assert np.array_equal(vn.numpy(), vn_o[sel])
+
+
+def test_patch_model_rejects_bad_bits():
+    from fused_turboquant.hf import patch_model
+
+    class _Dummy:
+        pass
+
+    with pytest.raises(ValueError, match="v_bits"):
+        patch_model(_Dummy(), bits=4, v_bits=5)
+    with pytest.raises(ValueError, match="bits"):
+        patch_model(_Dummy(), bits=5)
+    with pytest.raises(NotImplementedError):
+        patch_model(_Dummy(), quantizer_kind="planar")
+    with pytest.raises(ValueError, match="boundary_protect"):
+        patch_model(_Dummy(), boundary_protect=-1)
+
+
+def _tiny_llama(head_dim=128, layers=2, heads=4, kv_heads=2):
+    from transformers import LlamaConfig, LlamaForCausalLM
+    cfg = LlamaConfig(hidden_size=heads * head_dim, intermediate_size=512, num_hidden_layers=layers,
+                      num_attention_heads=heads, num_key_value_heads=kv_heads, head_dim=head_dim,
+                      vocab_size=320, max_position_embeddings=512)
+    torch.manual_seed(0)
+    return LlamaForCausalLM(cfg)
+
+
+def test_check_model_compatibility():
+    from fused_turboquant.hf import check_model_compatibility
+    r = check_model_compatibility(_tiny_llama())
+    assert r["compatible"] and r["eligible_layers"] == 2 and r["head_dim"] == 128
+    assert r["n_q_heads"] == 4 and r["n_kv_heads"] == 2 and r["known_compatible"]
+    r64 = check_model_compatibility(_tiny_llama(head_dim=64))
+    assert not r64["compatible"] and any("head_dim" in i for i in r64["issues"])
+
+
+def test_quantizer_routing():
+    from fused_turboquant import TurboQuantMSE
+    from fused_turboquant.hf import CompressedKVCache
+    k_tq = TurboQuantMSE(128, bits=4)
+    v_tq = TurboQuantMSE(128, bits=3)
+    cache = CompressedKVCache(k_tq)
+    cache.set_layer_quantizer(0, k_tq)
+    assert cache.get_layer_quantizer_v(0) is k_tq  # V falls back to K
+    cache.set_layer_quantizer_v(0, v_tq)
+    assert cache.get_layer_quantizer(0) is k_tq and cache.get_layer_quantizer_v(0) is v_tq
+    assert cache.get_layer_quantizer(7) is k_tq  # unregistered layer -> default
