@@ -1,0 +1,254 @@
+"""vLLM v1 ``TURBOQUANT`` attention backend on the gfx950 kernels
+(reference ``vllm_plugin/v1_backend.py:120-1866``, ``kind=rht``).
+
+The class surface is vLLM's (``AttentionBackend`` / ``AttentionImpl``
+methods, the Impl ``__init__`` signature, ``do_kv_cache_update`` and
+``forward`` over vLLM's metadata fields).  The classes derive from vLLM's
+bases when vLLM is importable and stand alone otherwise, so the backend can
+be driven directly (the tests feed it plain metadata objects).
+
+Per call:
+
+* ``do_kv_cache_update`` -> ``ftq_v1_store`` (K: norm, Hadamard, midpoint
+  search, pack, fp16 norm; V: optional rotation, min/max uniform quant), the
+  reference's ``_launch_store`` (``:712-749``).
+* decode tokens -> ``ftq_v1_decode_attention`` (query rotation, split-K
+  attention over the packed slots with norm correction, LSE merge, V
+  un-rotation, output cast), the reference's ``_decode_attention*``
+  (``:842-1093``).
+* prefill of a fresh sequence -> SDPA over the full-precision K/V of the
+  batch (the reference uses flash-attn varlen there, ``:1283-1443``).
+* prefill continuing a cached sequence -> the decode kernel with one
+  synthetic sequence per query token (seq_len = cached + i + 1, same block
+  table row): causal attention over the stored slots, the reference's
+  continuation path (``:1359-1384``).
+
+Per-layer state (sorted centroids, midpoints) is cached on the ``layer``
+object, like the reference's ``setup_layer`` (``rotation/matrix.py:34-42``).
+The centroid table of vLLM's ``get_centroids`` is not available here; this
+library's Lloyd-Max levels for (head_size, key bits) are used, and a table
+vLLM attached as ``layer._tq_centroids`` with the right size takes precedence.
+"""
+from __future__ import annotations
+
+import math
+from typing import Any, ClassVar, Optional
+
+import torch
+import torch.nn.functional as F
+
+from .. import v1 as V1
+from .plugin import TQ_PRESETS, boundary_protect_enabled, env_flag, host_preset
+
+try:  # vLLM's base classes when present (not installed in every environment)
+    from vllm.attention.backends.abstract import AttentionBackend as _BackendBase  # type: ignore
+    from vllm.attention.backends.abstract import AttentionImpl as _ImplBase  # type: ignore
+except Exception:  # pragma: no cover - depends on the environment
+    _BackendBase = object
+    _ImplBase = object
+
+
+class FusedTurboQuantV1Backend(_BackendBase):
+    """Backend class vLLM resolves from ``attention_backend="TURBOQUANT"``."""
+
+    accept_output_buffer: bool = True
+    forward_includes_kv_cache_update: bool = False
+    supported_dtypes: ClassVar[list] = [torch.float16, torch.bfloat16]
+    supported_kv_cache_dtypes: ClassVar[list] = [
+        "auto", "float16", "bfloat16", "turboquant_4bit_nc", "turboquant_k3v4_nc", "turboquant_3bit_nc",
+    ]
+
+    @staticmethod
+    def get_supported_kernel_block_sizes():
+        return [16, 32, 64, 128]
+
+    @staticmethod
+    def get_name() -> str:
+        return "TURBOQUANT"
+
+    @staticmethod
+    def get_impl_cls():
+        return FusedTurboQuantV1Impl
+
+    @staticmethod
+    def get_builder_cls():
+        from vllm.v1.attention.backends.turboquant_attn import TurboQuantMetadataBuilder  # type: ignore
+        return TurboQuantMetadataBuilder
+
+    @staticmethod
+    def _slot_size_for(head_size: int, cache_dtype_str: Optional[str]) -> int:
+        """Last-dim size: the preset's slot bytes (at least 2*head_size bf16
+        elements when boundary layers share the allocation), rounded up to a
+        power of two (reference ``v1_backend.py:171-209``)."""
+        if isinstance(cache_dtype_str, str) and cache_dtype_str.startswith("turboquant_"):
+            preset, _, _ = host_preset(cache_dtype_str)
+            pk, pv = TQ_PRESETS[preset]
+            return V1.slot_size(head_size, pk, pv, boundary_protect=boundary_protect_enabled())
+        raw = 2 * head_size
+        return 1 << (raw - 1).bit_length()
+
+    @staticmethod
+    def get_kv_cache_shape(num_blocks: int, block_size: int, num_kv_heads: int, head_size: int,
+                           cache_dtype_str: str = "turboquant_4bit_nc") -> tuple:
+        slot = FusedTurboQuantV1Backend._slot_size_for(head_size, cache_dtype_str)
+        return (num_blocks, block_size, num_kv_heads, slot)
+
+    @classmethod
+    def supports_kv_cache_dtype(cls, kv_cache_dtype) -> bool:
+        if kv_cache_dtype is None:
+            return True
+        if kv_cache_dtype in cls.supported_kv_cache_dtypes:
+            return True
+        try:
+            host_preset(kv_cache_dtype)
+            return True
+        except (ValueError, TypeError):
+            return False
+
+    @classmethod
+    def supports_head_size(cls, head_size: int) -> bool:
+        return head_size in (64, 128, 256)
+
+    @classmethod
+    def supports_compute_capability(cls, capability) -> bool:
+        return True
+
+    @classmethod
+    def supports_sink(cls) -> bool:
+        return False
+
+    @staticmethod
+    def use_cascade_attention(*args, **kwargs) -> bool:
+        return False
+
+
+class FusedTurboQuantV1Impl(_ImplBase):
+    """Per-layer attention implementation (reference ``v1_backend.py:292-1866``)."""
+
+    accept_output_buffer: bool = True
+    supports_quant_query_input: bool = False
+
+    def __init__(self, num_heads: int, head_size: int, scale: float, num_kv_heads: int,
+                 alibi_slopes: Optional[list] = None, sliding_window: Optional[int] = None,
+                 kv_cache_dtype: str = "auto", logits_soft_cap: Optional[float] = None,
+                 attn_type=None, kv_sharing_target_layer_name: Optional[str] = None, **kwargs: Any) -> None:
+        if alibi_slopes is not None:
+            raise NotImplementedError("ALiBi attention is not supported")
+        if kv_sharing_target_layer_name is not None:
+            raise NotImplementedError("KV sharing is not yet supported")
+        if sliding_window is not None:
+            raise NotImplementedError("sliding-window attention is not supported by the TURBOQUANT backend")
+        if logits_soft_cap is not None:
+            raise NotImplementedError("logit soft-capping is not supported by the TURBOQUANT backend")
+        if not (isinstance(kv_cache_dtype, str) and kv_cache_dtype.startswith("turboquant_")):
+            raise NotImplementedError(
+                f"kv_cache_dtype={kv_cache_dtype!r}: raw fp16 boundary layers are not part of this build")
+        if head_size != 128:
+            raise NotImplementedError("the gfx950 v1 decode kernel supports head_size 128")
+        if num_heads % num_kv_heads != 0 or num_heads // num_kv_heads > 16:
+            raise ValueError("num_heads must be a multiple of num_kv_heads with a group of at most 16")
+        self.num_heads = num_heads
+        self.head_size = head_size
+        self.scale = float(scale)
+        self.num_kv_heads = num_kv_heads
+        self.num_kv_groups = num_heads // num_kv_heads
+        self.kv_cache_dtype = kv_cache_dtype
+        self.preset, self.key_bits, self.value_bits = host_preset(kv_cache_dtype)
+        self.v_rotate = env_flag("TURBOQUANT_V_ROTATE") or env_flag("TURBOQUANT_V_LLOYD_MAX")
+        if env_flag("TURBOQUANT_V_LLOYD_MAX"):
+            raise NotImplementedError("TURBOQUANT_V_LLOYD_MAX (Lloyd-Max V codes) is not part of this build")
+
+    # -- per-layer state ---------------------------------------------------
+    def _state(self, layer, device) -> V1.TurboQuantV1Layer:
+        st = getattr(layer, "_fused_tq_state", None)
+        if st is None or st.centroids.device != torch.device(device):
+            cent = getattr(layer, "_tq_centroids", None)
+            if cent is not None and cent.numel() != (1 << self.key_bits):
+                cent = None
+            st = V1.TurboQuantV1Layer(self.head_size, self.key_bits, self.value_bits,
+                                      v_rotate=self.v_rotate, centroids=cent, device=device)
+            layer._fused_tq_state = st
+        return st
+
+    # -- store ---------------------------------------------------------------
+    def do_kv_cache_update(self, layer, key: torch.Tensor, value: torch.Tensor, kv_cache: torch.Tensor,
+                           slot_mapping: torch.Tensor) -> None:
+        N = slot_mapping.shape[0]
+        if N <= 0:
+            return
+        if kv_cache.dtype != torch.uint8:
+            kv_cache = kv_cache.view(torch.uint8)
+        st = self._state(layer, key.device)
+        k = key[:N].reshape(N, self.num_kv_heads, self.head_size)
+        v = value[:N].reshape(N, self.num_kv_heads, self.head_size)
+        st.store(k, v, kv_cache, slot_mapping[:N].to(torch.int64))
+
+    # -- attention -----------------------------------------------------------
+    def forward(self, layer, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                kv_cache: torch.Tensor, attn_metadata, output: Optional[torch.Tensor] = None,
+                output_scale: Optional[torch.Tensor] = None,
+                output_block_scale: Optional[torch.Tensor] = None) -> torch.Tensor:
+        num_tokens = query.shape[0]
+        if output is None:
+            output = torch.zeros(num_tokens, self.num_heads * self.head_size, dtype=query.dtype,
+                                 device=query.device)
+        if attn_metadata is None or attn_metadata.num_actual_tokens <= 0:
+            return output.fill_(0)
+        if kv_cache.dtype != torch.uint8:
+            kv_cache = kv_cache.view(torch.uint8)
+        N = attn_metadata.num_actual_tokens
+        st = self._state(layer, query.device)
+        q = query[:N].view(N, self.num_heads, self.head_size)
+        nd = attn_metadata.num_decodes
+        ndt = attn_metadata.num_decode_tokens
+        out = torch.empty(N, self.num_heads, self.head_size, dtype=query.dtype, device=query.device)
+        if not attn_metadata.is_prefill:
+            nd, ndt = attn_metadata.seq_lens.shape[0], N
+        if ndt > 0:
+            out[:ndt] = self._decode(q[:ndt], kv_cache, attn_metadata.block_table[:nd],
+                                     attn_metadata.seq_lens[:nd], st,
+                                     max_seq_len=getattr(attn_metadata, "max_seq_len", None))
+        if ndt < N:
+            k = key[:N].view(N, self.num_kv_heads, self.head_size)
+            v = value[:N].view(N, self.num_kv_heads, self.head_size)
+            out[ndt:] = self._prefill(q, k, v, kv_cache, attn_metadata, nd, ndt, st)
+        if output.ndim == 3:
+            output[:N] = out.to(output.dtype)
+        else:
+            output[:N] = out.reshape(N, -1).to(output.dtype)
+        return output
+
+    def _decode(self, q, kv_cache, block_table, seq_lens, st, max_seq_len=None):
+        bt = block_table if block_table.dtype == torch.int32 else block_table.to(torch.int32)
+        sl = seq_lens if seq_lens.dtype == torch.int32 else seq_lens.to(torch.int32)
+        msl = max_seq_len if max_seq_len is not None else bt.shape[1] * kv_cache.shape[1]
+        return V1.v1_decode_attention(q, kv_cache, bt, sl, st.centroids, self.key_bits, self.value_bits,
+                                      scale=self.scale, v_rotate=self.v_rotate, max_seq_len=msl)
+
+    def _prefill(self, q, k, v, kv_cache, md, nd, ndt, st):
+        """Prefill sequences nd.. of the batch (tokens ndt..N)."""
+        qsl = md.query_start_loc.tolist()
+        sls = md.seq_lens.tolist()
+        res = []
+        for i in range(nd, len(sls)):
+            a, b = qsl[i], qsl[i + 1]
+            n_q = b - a
+            if n_q == 0:
+                continue
+            past = sls[i] - n_q
+            if past <= 0:
+                # fresh sequence: causal attention over the full-precision K/V of the chunk
+                qq = q[a:b].transpose(0, 1).unsqueeze(0)
+                kk = k[a:b].transpose(0, 1).unsqueeze(0)
+                vv = v[a:b].transpose(0, 1).unsqueeze(0)
+                if self.num_kv_groups > 1:
+                    kk = kk.repeat_interleave(self.num_kv_groups, dim=1)
+                    vv = vv.repeat_interleave(self.num_kv_groups, dim=1)
+                o = F.scaled_dot_product_attention(qq, kk, vv, is_causal=True, scale=self.scale)
+                res.append(o[0].transpose(0, 1))
+            else:
+                # continuation: one synthetic decode per query token over the stored slots
+                row = md.block_table[i:i + 1].to(torch.int32).expand(n_q, -1).contiguous()
+                syn = torch.arange(past + 1, past + n_q + 1, device=q.device, dtype=torch.int32)
+                res.append(self._decode(q[a:b], kv_cache, row, syn, st, max_seq_len=sls[i]))
+        return torch.cat(res, dim=0) if res else q[ndt:ndt]

@@ -1,0 +1,151 @@
+"""vLLM TURBOQUANT backend on gfx950, driven the way vLLM's v1 runner drives
+it: ``do_kv_cache_update`` with the step's slot mapping, then ``forward`` with
+the step's metadata (reference ``vllm_plugin/v1_backend.py:712-840``).
+
+Expected values:
+* decode tokens and continuation-chunk tokens: the oracle's float64 attention
+  over the cache bytes the GPU store wrote, with the causal length of each
+  query (cached + i + 1);
+* fresh-prefill tokens: float64 causal attention over the raw bf16 K/V.
+Tolerance: max abs error <= 2e-2 + 2^-8 |want|, mean <= 2e-3 max(1, mean |want|).
+"""
+import math
+from types import SimpleNamespace
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import tq_oracle as O
+
+pytestmark = pytest.mark.gpu
+D = 128
+
+
+def _check(got, want, tag):
+    err = np.abs(got.astype(np.float64) - want)
+    bound = 2e-2 + 2.0 ** -8 * np.abs(want)
+    mean_bound = 2e-3 * max(1.0, float(np.abs(want).mean()))
+    print(f"[{tag}] max {err.max():.2e} mean {err.mean():.2e} worst/bound {(err / bound).max():.2f}", flush=True)
+    assert (err <= bound).all() and err.mean() <= mean_bound, tag
+
+
+def _causal_ref(q, k, v, scale):
+    """float64 causal attention; q [n, Hq, d], k/v [n, Hkv, d] (the chunk is the whole sequence)."""
+    q, k, v = (np.asarray(t, np.float64) for t in (q, k, v))
+    n, hq, d = q.shape
+    G = hq // k.shape[1]
+    out = np.zeros_like(q)
+    for h in range(hq):
+        s = q[:, h] @ k[:, h // G].T * scale
+        s = s + np.triu(np.full((n, n), -np.inf), 1)
+        s = s - s.max(axis=1, keepdims=True)
+        p = np.exp(s)
+        out[:, h] = (p / p.sum(axis=1, keepdims=True)) @ v[:, h // G]
+    return out
+
+
+def _run_step(cuda, seqs, dtype_str, hq, hkv, vrot, monkeypatch, seed, bs=16, protect="0"):
+    """seqs: list of (cached_len, query_len), decodes (query_len 1, cached > 0) first.
+    Stores the cached tokens in earlier update calls, then runs one step."""
+    from fused_turboquant import vllm_plugin as vp
+    monkeypatch.setenv("TURBOQUANT_BOUNDARY_PROTECT", protect)
+    monkeypatch.setenv("TURBOQUANT_V_ROTATE", "1" if vrot else "0")
+    g = torch.Generator().manual_seed(seed)
+    Bk = vp.FusedTurboQuantV1Backend
+    impl = vp.FusedTurboQuantV1Impl(hq, D, 1 / math.sqrt(D), hkv, kv_cache_dtype=dtype_str)
+    layer = SimpleNamespace()
+    pages = [(c + q + bs - 1) // bs for c, q in seqs]
+    nb = sum(pages) + 5
+    shape = Bk.get_kv_cache_shape(nb, bs, hkv, D, dtype_str)
+    cache = torch.zeros(shape, dtype=torch.uint8, device=cuda)
+    perm = torch.randperm(nb, generator=g).to(torch.int32)
+    mb = max(pages)
+    bt = torch.zeros(len(seqs), mb, dtype=torch.int32)
+    used = 0
+    full_k, full_v = [], []
+    for i, (c, q) in enumerate(seqs):
+        bt[i, :pages[i]] = perm[used:used + pages[i]]
+        used += pages[i]
+        k = torch.randn(c + q, hkv, D, generator=g).to(torch.bfloat16)
+        v = torch.randn(c + q, hkv, D, generator=g).to(torch.bfloat16)
+        full_k.append(k)
+        full_v.append(v)
+
+    def slots(i, lo, hi):
+        pos = torch.arange(lo, hi)
+        return bt[i].long()[pos // bs] * bs + pos % bs
+
+    # earlier steps: the cached prefix of every sequence
+    for i, (c, q) in enumerate(seqs):
+        if c:
+            impl.do_kv_cache_update(layer, full_k[i][:c].reshape(c, -1).to(cuda), full_v[i][:c].reshape(c, -1).to(cuda),
+                                    cache, slots(i, 0, c).to(cuda))
+    # this step's tokens
+    qs = [torch.randn(q, hq, D, generator=g).to(torch.bfloat16) for _, q in seqs]
+    key = torch.cat([full_k[i][c:] for i, (c, _) in enumerate(seqs)])
+    val = torch.cat([full_v[i][c:] for i, (c, _) in enumerate(seqs)])
+    query = torch.cat(qs)
+    sm = torch.cat([slots(i, c, c + q) for i, (c, q) in enumerate(seqs)])
+    N = query.shape[0]
+    impl.do_kv_cache_update(layer, key.reshape(N, -1).to(cuda), val.reshape(N, -1).to(cuda), cache, sm.to(cuda))
+    qlens = [q for _, q in seqs]
+    qsl = torch.tensor([0] + np.cumsum(qlens).tolist(), dtype=torch.int32)
+    nd = sum(1 for c, q in seqs if q == 1 and c > 0)
+    md = SimpleNamespace(
+        seq_lens=torch.tensor([c + q for c, q in seqs], dtype=torch.int32, device=cuda),
+        block_table=bt.to(cuda), query_start_loc=qsl.to(cuda), slot_mapping=sm.to(cuda),
+        num_actual_tokens=N, max_query_len=max(qlens), max_seq_len=max(c + q for c, q in seqs),
+        is_prefill=nd < len(seqs), num_decodes=nd, num_decode_tokens=nd)
+    output = torch.full((N, hq * D), float("nan"), dtype=torch.bfloat16, device=cuda)
+    ret = impl.forward(layer, query.reshape(N, -1).to(cuda), key.reshape(N, -1).to(cuda),
+                       val.reshape(N, -1).to(cuda), cache, md, output=output)
+    torch.cuda.synchronize()
+    assert ret is output
+    got = output.float().cpu().numpy().reshape(N, hq, D)
+
+    st = layer._fused_tq_state
+    cache_np = cache.cpu().numpy()
+    cent = st.centroids.cpu().numpy()
+    kb, vb = impl.key_bits, impl.value_bits
+    for i, (c, q) in enumerate(seqs):
+        a = int(qsl[i])
+        if c == 0:
+            want = _causal_ref(qs[i].float().numpy(), full_k[i].float().numpy(), full_v[i].float().numpy(),
+                               1 / math.sqrt(D))
+        else:
+            sl = np.arange(c + 1, c + q + 1, dtype=np.int32)
+            btr = np.repeat(bt[i:i + 1].numpy(), q, axis=0)
+            want = O.v1_decode_attention(qs[i].float().numpy(), cache_np, btr, sl, cent, kb, vb,
+                                         1 / math.sqrt(D), v_rotate=vrot)
+        kind = "prefill" if c == 0 else ("decode" if q == 1 else "continuation")
+        _check(got[a:a + q], want, f"{dtype_str} vrot={vrot} seq{i} {kind} cached={c} q={q}")
+
+
+@pytest.mark.parametrize("dtype_str,vrot", [("turboquant_3bit_nc", False), ("turboquant_k4v2_nc", True),
+                                            ("turboquant_4bit_nc", True), ("turboquant_k3v4_nc", False)])
+def test_decode_batch(cuda, monkeypatch, dtype_str, vrot):
+    _run_step(cuda, [(1, 1), (100, 1), (513, 1), (4000, 1)], dtype_str, 32, 8, vrot, monkeypatch, seed=1)
+
+
+def test_fresh_prefill_batch(cuda, monkeypatch):
+    _run_step(cuda, [(0, 37), (0, 1), (0, 200)], "turboquant_3bit_nc", 16, 4, False, monkeypatch, seed=2)
+
+
+def test_continuation_chunks(cuda, monkeypatch):
+    _run_step(cuda, [(64, 17), (300, 64), (15, 2)], "turboquant_k4v2_nc", 8, 2, True, monkeypatch, seed=3)
+
+
+def test_mixed_batch(cuda, monkeypatch):
+    _run_step(cuda, [(40, 1), (2048, 1), (0, 33), (129, 9), (0, 1)], "turboquant_3bit_nc", 32, 8, True,
+              monkeypatch, seed=4, bs=32, protect="1")
+
+
+def test_no_metadata_zeroes_output(cuda):
+    from fused_turboquant import vllm_plugin as vp
+    impl = vp.FusedTurboQuantV1Impl(8, D, 0.1, 2, kv_cache_dtype="turboquant_3bit_nc")
+    out = torch.ones(4, 8 * D, dtype=torch.bfloat16, device=cuda)
+    cache = torch.zeros(2, 16, 2, 128, dtype=torch.uint8, device=cuda)
+    q = torch.randn(4, 8 * D, device=cuda, dtype=torch.bfloat16)
+    impl.forward(SimpleNamespace(), q, q[:, :2 * D], q[:, :2 * D], cache, None, output=out)
+    assert not out.any()

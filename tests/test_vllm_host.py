@@ -1,0 +1,118 @@
+"""Host logic of the vLLM TURBOQUANT backend surface (no GPU): cache-dtype
+presets and per-K/V overrides (reference ``vllm_plugin/plugin.py:380-412``),
+the cache shape vLLM allocates (``v1_backend.py:171-220``), dtype support and
+the Impl's refusal of features this build does not carry."""
+import pytest
+
+from fused_turboquant import vllm_plugin as vp
+
+B = vp.FusedTurboQuantV1Backend
+
+
+@pytest.fixture(autouse=True)
+def _clean_env(monkeypatch):
+    for k in ("TURBOQUANT_KEY_BITS", "TURBOQUANT_VALUE_BITS", "TURBOQUANT_V_ROTATE",
+              "TURBOQUANT_V_LLOYD_MAX", "TURBOQUANT_BOUNDARY_PROTECT", "TURBOQUANT_KIND"):
+        monkeypatch.setenv(k, "")  # records the original value, restored at teardown
+        monkeypatch.delenv(k)
+
+
+@pytest.mark.parametrize("dt,want", [
+    ("turboquant_3bit_nc", ("turboquant_3bit_nc", 3, 3)),
+    ("turboquant_k3v4_nc", ("turboquant_k3v4_nc", 3, 4)),
+    ("turboquant_4bit_nc", ("turboquant_4bit_nc", 4, 4)),
+    ("turboquant_k4v2_nc", ("turboquant_4bit_nc", 4, 2)),
+    ("turboquant_k2v4_nc", ("turboquant_k3v4_nc", 2, 4)),
+    ("turboquant_k2v2_nc", ("turboquant_3bit_nc", 2, 2)),
+    ("turboquant_k3v3_nc", ("turboquant_3bit_nc", 3, 3)),
+])
+def test_host_preset(dt, want):
+    assert vp.host_preset(dt) == want
+
+
+def test_host_preset_env_override(monkeypatch):
+    monkeypatch.setenv("TURBOQUANT_KEY_BITS", "2")
+    monkeypatch.setenv("TURBOQUANT_VALUE_BITS", "3")
+    assert vp.host_preset("turboquant_4bit_nc") == ("turboquant_4bit_nc", 2, 3)
+    monkeypatch.setenv("TURBOQUANT_KEY_BITS", "4")
+    with pytest.raises(ValueError, match="exceeds the slot"):
+        vp.host_preset("turboquant_3bit_nc")
+
+
+@pytest.mark.parametrize("dt", ["fp8", "turboquant_5bit_nc", "turboquant_k1v2_nc", "auto"])
+def test_host_preset_rejects(dt):
+    with pytest.raises(ValueError):
+        vp.host_preset(dt)
+
+
+@pytest.mark.parametrize("dt,protect,slot", [
+    # K3V3 d128: 48 + 2 + 48 + 4 = 102 bytes -> 128; K3V4: 118 -> 128; K4V4: 134 -> 256
+    ("turboquant_3bit_nc", "0", 128), ("turboquant_k3v4_nc", "0", 128), ("turboquant_4bit_nc", "0", 256),
+    ("turboquant_k4v2_nc", "0", 256), ("turboquant_k2v3_nc", "0", 128),
+    # boundary layers share the allocation: at least 2 * head_size
+    ("turboquant_3bit_nc", "1", 256), ("turboquant_4bit_nc", "1", 256),
+])
+def test_kv_cache_shape(monkeypatch, dt, protect, slot):
+    monkeypatch.setenv("TURBOQUANT_BOUNDARY_PROTECT", protect)
+    assert B.get_kv_cache_shape(100, 16, 8, 128, dt) == (100, 16, 8, slot)
+
+
+def test_kv_cache_shape_d64_d256(monkeypatch):
+    monkeypatch.setenv("TURBOQUANT_BOUNDARY_PROTECT", "0")
+    # d64 K3V3: 24 + 2 + 24 + 4 = 54 -> 64; d256 K4V4: 128 + 2 + 128 + 4 = 262 -> 512
+    assert B.get_kv_cache_shape(4, 16, 2, 64, "turboquant_3bit_nc")[-1] == 64
+    assert B.get_kv_cache_shape(4, 16, 2, 256, "turboquant_4bit_nc")[-1] == 512
+
+
+def test_backend_surface():
+    assert B.get_name() == "TURBOQUANT"
+    assert B.get_impl_cls() is vp.FusedTurboQuantV1Impl
+    assert B.accept_output_buffer and not B.forward_includes_kv_cache_update
+    assert 16 in B.get_supported_kernel_block_sizes()
+    assert B.supports_kv_cache_dtype("turboquant_k4v2_nc")
+    assert B.supports_kv_cache_dtype("turboquant_3bit_nc")
+    assert not B.supports_kv_cache_dtype("fp8_e4m3")
+    assert B.supports_head_size(128) and not B.supports_head_size(96)
+
+
+def test_impl_init_and_refusals(monkeypatch):
+    monkeypatch.setenv("TURBOQUANT_V_ROTATE", "1")
+    im = vp.FusedTurboQuantV1Impl(32, 128, 128 ** -0.5, 8, kv_cache_dtype="turboquant_k4v2_nc")
+    assert (im.key_bits, im.value_bits, im.v_rotate, im.num_kv_groups) == (4, 2, True, 4)
+    mk = lambda **kw: vp.FusedTurboQuantV1Impl(**{**dict(num_heads=8, head_size=128, scale=0.1,
+                                                         num_kv_heads=2, kv_cache_dtype="turboquant_3bit_nc"), **kw})
+    with pytest.raises(NotImplementedError):
+        mk(alibi_slopes=[1.0] * 8)
+    with pytest.raises(NotImplementedError):
+        mk(kv_sharing_target_layer_name="layers.0")
+    with pytest.raises(NotImplementedError):
+        mk(sliding_window=128)
+    with pytest.raises(NotImplementedError):
+        mk(kv_cache_dtype="auto")
+    with pytest.raises(NotImplementedError):
+        mk(head_size=64)
+    with pytest.raises(ValueError):
+        mk(num_heads=8, num_kv_heads=3)
+    with pytest.raises(ValueError):
+        mk(num_heads=64, num_kv_heads=2)
+
+
+def test_apply_additional_config(monkeypatch):
+    class EA:
+        additional_config = {"turboquant": {"v_rotate": True, "key_bits": 2, "boundary_protect": False}}
+    monkeypatch.setenv("TURBOQUANT_KEY_BITS", "3")  # explicit environment wins
+    vp.apply_additional_config(EA())
+    import os
+    assert os.environ["TURBOQUANT_V_ROTATE"] == "1"
+    assert os.environ["TURBOQUANT_KEY_BITS"] == "3"
+    assert os.environ["TURBOQUANT_BOUNDARY_PROTECT"] == "0"
+    assert not vp.boundary_protect_enabled()
+
+
+def test_register_without_vllm():
+    try:
+        import vllm  # noqa: F401
+        pytest.skip("vLLM is installed")
+    except ImportError:
+        pass
+    assert vp.register_backend() is False
