@@ -125,9 +125,11 @@ def main():
         ck, cv = tq.encode(k), tq.encode(v)
         signs, bnd = tq.rotation.signs, tq.quantizer.boundaries
 
+        cls = tq.quantizer.codebook_class  # symmetric at d=128: the |t|-search kernel
+
         def enc(x, c):
-            return lambda: _lib.check(L.ftq_encode(x.data_ptr(), 2, n, d, signs.data_ptr(), bnd.data_ptr(),
-                                                   bits, c.indices.data_ptr(), c.norms.data_ptr(), sp))
+            return lambda: _lib.check(L.ftq_encode_cb(x.data_ptr(), 2, n, d, signs.data_ptr(), bnd.data_ptr(),
+                                                      bits, cls, c.indices.data_ptr(), c.norms.data_ptr(), sp))
         return tq, ck, enc(k, ck), enc(v, cv)
 
     log(f"[bench] config2 encode: [{T},{H},128] and [{T},{H},256] bf16 3-bit, K and V")
@@ -203,7 +205,7 @@ def main():
                                   f"os.cpu_count()={os.cpu_count()}, numpy single thread"}
 
     main_roof = dict(rl["encode_d128_3bit"])
-    main_roof["kernel"] = "ftq::encode_kernel<128,3,bf16>"
+    main_roof["kernel"] = "ftq::encode_mfma_kernel<128,3,bf16,sym>"
     out = {
         "metric": "3-bit d128 encode GB/s + paged decode-attn us/step @8K ctx; % of HBM peak",
         "value": round(enc_in_gbs, 1),

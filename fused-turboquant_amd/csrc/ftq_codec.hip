@@ -178,25 +178,31 @@ int codec_grid(int64_t n, int gpb) {
   return (int)want;
 }
 
+template <int D, int BITS, int DT, bool SYM>
+static void launch_encode_mfma(const void* x, int64_t n, const float* signs, const float* bnd,
+                               float sc, double rsc, uint8_t* packed, uint16_t* norms, hipStream_t st) {
+  // one pass of resident workgroups, each wave looping over groups of 16 vectors
+  static const int cap = resident_workgroups(encode_mfma_kernel<D, BITS, DT, SYM>);
+  const int64_t want = (n + 63) / 64;
+  encode_mfma_kernel<D, BITS, DT, SYM><<<dim3((unsigned)(want < cap ? want : cap)), dim3(256), 0, st>>>(
+      x, n, signs, bnd, sc, rsc, packed, norms);
+}
+
 template <int D, int BITS>
 static hipError_t launch_encode_db(const void* x, int dt, int64_t n, const float* signs,
-                                   const float* bnd, uint8_t* packed, uint16_t* norms,
+                                   const float* bnd, int cb_class, uint8_t* packed, uint16_t* norms,
                                    hipStream_t st) {
   const float sc = fwht_scale(D);
   const double rsc = 1.0 / (double)sc;
   if constexpr (D == 128 || D == 256) {
     if (dt != F32) {  // 16-bit inputs: Hadamard transform on the matrix cores
-      // one pass of resident workgroups, each wave looping over groups of 16 vectors
-      const int64_t want = (n + 63) / 64;
-      dim3 block(256);
+      const bool sym = cb_class == FTQ_CB_SYMMETRIC;
       if (dt == F16) {
-        static const int cap = resident_workgroups(encode_mfma_kernel<D, BITS, F16>);
-        encode_mfma_kernel<D, BITS, F16><<<dim3((unsigned)(want < cap ? want : cap)), block, 0, st>>>(
-            x, n, signs, bnd, sc, rsc, packed, norms);
+        if (sym) launch_encode_mfma<D, BITS, F16, true>(x, n, signs, bnd, sc, rsc, packed, norms, st);
+        else launch_encode_mfma<D, BITS, F16, false>(x, n, signs, bnd, sc, rsc, packed, norms, st);
       } else {
-        static const int cap = resident_workgroups(encode_mfma_kernel<D, BITS, BF16>);
-        encode_mfma_kernel<D, BITS, BF16><<<dim3((unsigned)(want < cap ? want : cap)), block, 0, st>>>(
-            x, n, signs, bnd, sc, rsc, packed, norms);
+        if (sym) launch_encode_mfma<D, BITS, BF16, true>(x, n, signs, bnd, sc, rsc, packed, norms, st);
+        else launch_encode_mfma<D, BITS, BF16, false>(x, n, signs, bnd, sc, rsc, packed, norms, st);
       }
       return hipGetLastError();
     }
@@ -211,11 +217,11 @@ static hipError_t launch_encode_db(const void* x, int dt, int64_t n, const float
 
 template <int D>
 static hipError_t launch_encode_d(const void* x, int dt, int64_t n, const float* signs,
-                                  const float* bnd, int bits, uint8_t* packed, uint16_t* norms,
-                                  hipStream_t st) {
-  if (bits == 2) return launch_encode_db<D, 2>(x, dt, n, signs, bnd, packed, norms, st);
-  if (bits == 3) return launch_encode_db<D, 3>(x, dt, n, signs, bnd, packed, norms, st);
-  return launch_encode_db<D, 4>(x, dt, n, signs, bnd, packed, norms, st);
+                                  const float* bnd, int bits, int cb_class, uint8_t* packed,
+                                  uint16_t* norms, hipStream_t st) {
+  if (bits == 2) return launch_encode_db<D, 2>(x, dt, n, signs, bnd, cb_class, packed, norms, st);
+  if (bits == 3) return launch_encode_db<D, 3>(x, dt, n, signs, bnd, cb_class, packed, norms, st);
+  return launch_encode_db<D, 4>(x, dt, n, signs, bnd, cb_class, packed, norms, st);
 }
 
 template <int D, int BITS>
@@ -264,23 +270,43 @@ static hipError_t launch_rht_d(const void* x, int it, int64_t n, const float* si
 
 using namespace ftq;
 
-extern "C" int ftq_encode(const void* x, int x_dtype, int64_t n, int d, const float* signs,
-                          const float* boundaries, int bits, uint8_t* packed_out,
-                          uint16_t* norms_out, void* stream) {
+extern "C" int ftq_codebook_class(const float* boundaries, int bits) {
+  FTQ_REQUIRE(bits >= 2 && bits <= 4, "bits must be 2, 3, or 4");
+  FTQ_REQUIRE(boundaries, "null pointer argument");
+  const int mid = 1 << (bits - 1), nb = (1 << bits) + 1;
+  for (int k = 1; k < nb; ++k)
+    if (!(boundaries[k - 1] <= boundaries[k])) return FTQ_CB_ANY;  // unsorted or NaN: no claims
+  if (!(std::fabs(boundaries[mid]) < boundaries[mid + 1])) return FTQ_CB_ANY;
+  for (int k = 1; k < mid; ++k)
+    if (!(boundaries[mid + k] == -boundaries[mid - k])) return FTQ_CB_ANY;
+  return FTQ_CB_SYMMETRIC;
+}
+
+extern "C" int ftq_encode_cb(const void* x, int x_dtype, int64_t n, int d, const float* signs,
+                             const float* boundaries, int bits, int codebook_class,
+                             uint8_t* packed_out, uint16_t* norms_out, void* stream) {
   FTQ_REQUIRE(n >= 0, "n must be >= 0");
   FTQ_REQUIRE(d == 64 || d == 128 || d == 256, "head_dim must be 64, 128 or 256");
   FTQ_REQUIRE(bits >= 2 && bits <= 4, "bits must be 2, 3, or 4");
   FTQ_REQUIRE(x_dtype >= F32 && x_dtype <= BF16, "x_dtype must be FTQ_F32, FTQ_F16 or FTQ_BF16");
+  FTQ_REQUIRE(codebook_class == FTQ_CB_ANY || codebook_class == FTQ_CB_SYMMETRIC,
+              "codebook_class must be FTQ_CB_ANY or FTQ_CB_SYMMETRIC");
   if (n == 0) return FTQ_OK;
   FTQ_REQUIRE(x && signs && boundaries && packed_out && norms_out, "null pointer argument");
   FTQ_REQUIRE(aligned16(x), "x must be 16-byte aligned");
   FTQ_REQUIRE(aligned4(packed_out), "packed_out must be 4-byte aligned");
   hipStream_t st = (hipStream_t)stream;
   hipError_t e;
-  if (d == 64) e = launch_encode_d<64>(x, x_dtype, n, signs, boundaries, bits, packed_out, norms_out, st);
-  else if (d == 128) e = launch_encode_d<128>(x, x_dtype, n, signs, boundaries, bits, packed_out, norms_out, st);
-  else e = launch_encode_d<256>(x, x_dtype, n, signs, boundaries, bits, packed_out, norms_out, st);
+  if (d == 64) e = launch_encode_d<64>(x, x_dtype, n, signs, boundaries, bits, codebook_class, packed_out, norms_out, st);
+  else if (d == 128) e = launch_encode_d<128>(x, x_dtype, n, signs, boundaries, bits, codebook_class, packed_out, norms_out, st);
+  else e = launch_encode_d<256>(x, x_dtype, n, signs, boundaries, bits, codebook_class, packed_out, norms_out, st);
   return hip_status(e);
+}
+
+extern "C" int ftq_encode(const void* x, int x_dtype, int64_t n, int d, const float* signs,
+                          const float* boundaries, int bits, uint8_t* packed_out,
+                          uint16_t* norms_out, void* stream) {
+  return ftq_encode_cb(x, x_dtype, n, d, signs, boundaries, bits, FTQ_CB_ANY, packed_out, norms_out, stream);
 }
 
 extern "C" int ftq_decode(const uint8_t* packed, const uint16_t* norms, int64_t n, int d,

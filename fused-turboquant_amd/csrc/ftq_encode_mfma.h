@@ -8,8 +8,19 @@
 //                               matrix cores
 //   code = #{interior boundaries B_j : B_j < RN(RN(t*c) / (norm + 1e-8))}
 //
-// The quantiser is the exact per-vector threshold search of ftq_encode_fast.h
-// (T_j in the t domain, binary search, no per-element division).
+// Quantiser.  code = #{j : t > T_j} with per-vector thresholds in the t
+// domain, T_j = RN(B_j * RN((norm + 1e-8) / c)) in fp32: no per-element
+// division.  T_j sits within a few ulp of the exact preimage of B_j under
+// t -> RN(RN(t c) / den), so a code can differ from the reference's only where
+// u lies within that distance of B_j (a boundary tie, like those of the
+// accumulation order below).  When the codebook is symmetric in fp32
+// (B[2^b - j] == -B[j] for every j but the middle one, as the Lloyd-Max
+// codebooks of d = 64 and 128 are) the search runs on |t| over the positive
+// thresholds, the sign test against the middle threshold picking the half:
+// 3 compares, 1 select and 3 carry-adds per 3-bit element instead of 3, 4, 3.
+// The symmetric form is a separate instantiation (SYM), chosen by the host
+// from its copy of the codebook: one loop per kernel keeps the register count
+// at 126 (4 waves per SIMD) at d = 128.
 //
 // Transform.  A wave encodes 16 vectors at a time.  The input, sign-flipped,
 // is the B operand of v_mfma_f32_16x16x32_{bf16,f16} (K = input element,
@@ -55,51 +66,6 @@ __device__ __forceinline__ f32x4_t mfma_16x16x32(const Op16x8& a, const Op16x8& 
   else return __builtin_amdgcn_mfma_f32_16x16x32_f16(a.h, b.h, c, 0, 0, 0);
 }
 
-// next representable float above / below a nonzero finite x (integer step
-// on the bit pattern: +1 away from zero for positives, toward zero for negatives)
-__device__ __forceinline__ float nz_next_up(float x) {
-  const int i = __float_as_int(x);
-  return __int_as_float(i + ((i >> 31) | 1));
-}
-__device__ __forceinline__ float nz_next_down(float x) {
-  const int i = __float_as_int(x);
-  return __int_as_float(i - ((i >> 31) | 1));
-}
-
-// Per-boundary constants of the exact threshold: m1 = (B + B+) / 2 (exact in
-// fp64, B+ the float after B) and whether B+ has an odd significand.
-struct BoundaryK {
-  double m1;
-  bool odd;
-};
-__device__ __forceinline__ BoundaryK boundary_k(float B) {
-  const float Bp = nz_next_up(B == 0.f ? 0.f : B);  // +-0 -> smallest subnormal
-  return BoundaryK{((double)B + (double)Bp) * 0.5, (__float_as_uint(Bp) & 1u) != 0u};
-}
-
-// Smallest fp32 t with  B < RN(RN(t c) / den)  (same value as exact_threshold
-// in ftq_encode_fast.h, without branches):
-//   Y = smallest float with RN(Y / den) > B: Y > P = m1 den (exact in fp64),
-//       or Y == P when B+ is even (the tie then rounds up to B+);
-//   T = smallest float with RN(T c) >= Y: T c > M2 = (Y- + Y) / 2, or
-//       T c == M2 when Y is even.  t0 = RN(M2 / c) is T or the float below it;
-//       t0 c (exact in fp64) decides.  S = Y- + Y and t0 (2c) are exact.
-// The integer steps never meet +0 (Y = +0 would need P > 0 rounding to +0
-// without a bump) and are exact for every other finite value.
-__device__ __forceinline__ float exact_threshold_k(const BoundaryK& k, double den, double c2,
-                                                   double rc_half) {
-  const double P = k.m1 * den;
-  const float Yr = (float)P;
-  const double Yd = (double)Yr;
-  const bool bump = (Yd < P) || (Yd == P && k.odd);
-  const float Y = bump ? nz_next_up(Yr) : Yr;
-  const double S = (double)nz_next_down(Y) + (double)Y;
-  const float t0 = (float)(S * rc_half);
-  const double tc2 = (double)t0 * c2;
-  const bool ok = (tc2 > S) || (tc2 == S && (__float_as_uint(Y) & 1u) == 0u);
-  return ok ? t0 : nz_next_up(t0);
-}
-
 // w = 2 w + (lane's bit of mask m): one v_addc per code bit.  m is the
 // wave's compare mask (EXEC must be full where this is used).
 __device__ __forceinline__ uint32_t shift_in(uint32_t w, bool bit) {
@@ -110,11 +76,12 @@ __device__ __forceinline__ uint32_t shift_in(uint32_t w, bool bit) {
   return r;
 }
 
-// Codes of E elements, code = #{k : a >= V_k} over NT = 2^BITS - 1 sorted
+// Codes of E elements, code = #{k : a > V_k} over NT = 2^BITS - 1 sorted
 // thresholds by binary search, packed little-endian (element e at bits
 // [BITS e, BITS e + BITS)) into E*BITS/32 words.  Bits are shifted in from
 // the highest position down; four elements per step keep independent
-// compares queued behind each select.
+// compares queued behind each select.  Strict, like the reference's
+// bucketize(right=False): a value on a threshold takes the lower code.
 template <int BITS, int E>
 __device__ __forceinline__ void quantize_pack(const float (&x)[E], const float (&V)[(1 << BITS) - 1],
                                               uint32_t (&w)[E * BITS / 32]) {
@@ -126,36 +93,36 @@ __device__ __forceinline__ void quantize_pack(const float (&x)[E], const float (
     bool s[4][BITS];
     if constexpr (BITS == 2) {
 #pragma unroll
-      for (int u = 0; u < 4; ++u) s[u][1] = x[i0 + u] >= V[1];
+      for (int u = 0; u < 4; ++u) s[u][1] = x[i0 + u] > V[1];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) s[u][0] = x[i0 + u] >= (s[u][1] ? V[2] : V[0]);
+      for (int u = 0; u < 4; ++u) s[u][0] = x[i0 + u] > (s[u][1] ? V[2] : V[0]);
     } else if constexpr (BITS == 3) {
 #pragma unroll
-      for (int u = 0; u < 4; ++u) s[u][2] = x[i0 + u] >= V[3];
+      for (int u = 0; u < 4; ++u) s[u][2] = x[i0 + u] > V[3];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) s[u][1] = x[i0 + u] >= (s[u][2] ? V[5] : V[1]);
+      for (int u = 0; u < 4; ++u) s[u][1] = x[i0 + u] > (s[u][2] ? V[5] : V[1]);
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const float lo = s[u][2] ? V[4] : V[0];
         const float hi = s[u][2] ? V[6] : V[2];
-        s[u][0] = x[i0 + u] >= (s[u][1] ? hi : lo);
+        s[u][0] = x[i0 + u] > (s[u][1] ? hi : lo);
       }
     } else {
 #pragma unroll
-      for (int u = 0; u < 4; ++u) s[u][3] = x[i0 + u] >= V[7];
+      for (int u = 0; u < 4; ++u) s[u][3] = x[i0 + u] > V[7];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) s[u][2] = x[i0 + u] >= (s[u][3] ? V[11] : V[3]);
+      for (int u = 0; u < 4; ++u) s[u][2] = x[i0 + u] > (s[u][3] ? V[11] : V[3]);
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const float a = s[u][3] ? V[13] : V[5], bq = s[u][3] ? V[9] : V[1];
-        s[u][1] = x[i0 + u] >= (s[u][2] ? a : bq);
+        s[u][1] = x[i0 + u] > (s[u][2] ? a : bq);
       }
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const float t00 = s[u][3] ? V[8] : V[0], t01 = s[u][3] ? V[10] : V[2];
         const float t10 = s[u][3] ? V[12] : V[4], t11 = s[u][3] ? V[14] : V[6];
         const float lo = s[u][1] ? t01 : t00, hi = s[u][1] ? t11 : t10;
-        s[u][0] = x[i0 + u] >= (s[u][2] ? hi : lo);
+        s[u][0] = x[i0 + u] > (s[u][2] ? hi : lo);
       }
     }
 #pragma unroll
@@ -169,7 +136,75 @@ __device__ __forceinline__ void quantize_pack(const float (&x)[E], const float (
   }
 }
 
-template <int D, int BITS, int DT>
+// sqrt rounded to nearest: the hardware estimate r, then r - ulp or r + ulp
+// when the residual a - r' r (one fma, sign exact) shows the true root lies
+// nearer to it.  No rescaling for inputs below 2^-96 (norms that small store
+// as fp16 zero either way); fewer registers than the library sqrt, which
+// keeps the d = 128 encoder at 4 waves per SIMD.
+__device__ __forceinline__ float sqrt_rn(float a) {
+  float r = __builtin_amdgcn_sqrtf(a);
+  const float rd = __int_as_float(__float_as_int(r) - 1);
+  const float ru = __int_as_float(__float_as_int(r) + 1);
+  if (__builtin_fmaf(-rd, r, a) <= 0.f) r = rd;
+  if (__builtin_fmaf(-ru, r, a) > 0.f) r = ru;
+  return r;
+}
+
+// shift_in with the lane mask given directly
+__device__ __forceinline__ uint32_t shift_in_mask(uint32_t w, uint64_t m) {
+  uint32_t r;
+  uint64_t co;
+  asm("v_addc_co_u32_e64 %0, %1, %2, %2, %3" : "=v"(r), "=s"(co) : "v"(w), "s"(m));
+  return r;
+}
+
+// Symmetric codebook: sg = (a > Tm) against the middle threshold, then a
+// binary search of |a| over the H = 2^(BITS-1) - 1 positive thresholds P,
+// m = #{k : |a| > P_k}.  code = 2^(BITS-1) + m when sg, else
+// 2^(BITS-1) - 1 - m (the negative thresholds are -P_k), so the top bit is sg
+// and the low bits are m XNOR sg, combined on the compare masks.  (a == -P_k
+// exactly gives the code one below #{j : a > T_j}: a boundary tie.)  Bits go
+// in from the highest element down, as in quantize_pack.
+template <int BITS, int E>
+__device__ __forceinline__ void quantize_pack_sym(const float (&x)[E], float Tm,
+                                                  const float (&P)[(1 << (BITS - 1)) - 1],
+                                                  uint32_t (&w)[E * BITS / 32]) {
+  static_assert((E * BITS) % 32 == 0, "whole words per lane");
+#pragma unroll
+  for (int k = 0; k < E * BITS / 32; ++k) w[k] = 0;
+#pragma unroll
+  for (int i = E - 1; i >= 0; --i) {
+    const float xv = x[i];
+    const float a = __builtin_fabsf(xv);
+    const uint64_t sg = __builtin_amdgcn_ballot_w64(xv > Tm);
+    uint64_t mb[BITS - 1];
+    if constexpr (BITS == 2) {
+      mb[0] = __builtin_amdgcn_ballot_w64(a > P[0]);
+    } else if constexpr (BITS == 3) {
+      const bool m1 = a > P[1];
+      mb[1] = __builtin_amdgcn_ballot_w64(m1);
+      mb[0] = __builtin_amdgcn_ballot_w64(a > (m1 ? P[2] : P[0]));
+    } else {
+      const bool m2 = a > P[3];
+      const bool m1 = a > (m2 ? P[5] : P[1]);
+      const float lo = m2 ? P[4] : P[0], hi = m2 ? P[6] : P[2];
+      mb[2] = __builtin_amdgcn_ballot_w64(m2);
+      mb[1] = __builtin_amdgcn_ballot_w64(m1);
+      mb[0] = __builtin_amdgcn_ballot_w64(a > (m1 ? hi : lo));
+    }
+    {
+      const int k = (BITS * i + BITS - 1) >> 5;
+      w[k] = shift_in_mask(w[k], sg);
+    }
+#pragma unroll
+    for (int b = BITS - 2; b >= 0; --b) {
+      const int k = (BITS * i + b) >> 5;
+      w[k] = shift_in_mask(w[k], ~(mb[b] ^ sg));
+    }
+  }
+}
+
+template <int D, int BITS, int DT, bool SYM>
 __global__ __launch_bounds__(256) void encode_mfma_kernel(const void* __restrict__ x, int64_t n,
                                                           const float* __restrict__ signs,
                                                           const float* __restrict__ boundaries,
@@ -182,20 +217,13 @@ __global__ __launch_bounds__(256) void encode_mfma_kernel(const void* __restrict
   constexpr int KS = D / 32;  // K steps
   constexpr int MB = D / 16;  // M blocks
   constexpr int NT = (1 << BITS) - 1;
-  constexpr int PERQ = (NT + 3) / 4;  // thresholds computed per lane
+  constexpr int MID = 1 << (BITS - 1);  // boundaries[MID] is the middle one
+  constexpr int NH = MID - 1;
   constexpr int PD = D * BITS / 8;
 
   const int lane = threadIdx.x & 63;
   const int q = lane >> 4, j = lane & 15;
   const int qp = (lane >> 2) & 3, r = lane & 3;
-  // boundary constants of the thresholds this lane computes (j = PERQ q + k)
-  BoundaryK bk[PERQ];
-#pragma unroll
-  for (int k = 0; k < PERQ; ++k) {
-    const int jj = PERQ * q + k;
-    bk[k] = boundary_k(boundaries[1 + (jj < NT ? jj : 0)]);
-  }
-  const double c2 = 2.0 * (double)c, rc_half = 0.5 * rc;
   // A patterns: P0[t] = (-1)^(popc(r & t) + popc(q' & q)), P1[t] = P0[t] (-1)^(t >> 2)
   const uint32_t one = (DT == BF16) ? 0x3F80u : 0x3C00u;
   Op16x8 P0, P1, N0, N1;
@@ -234,10 +262,17 @@ __global__ __launch_bounds__(256) void encode_mfma_kernel(const void* __restrict
   const int64_t wstride = (int64_t)gridDim.x * 4 * 16;
   const uint16_t* xb = static_cast<const uint16_t*>(x);
 
-  // groups of 16 vectors; the next group's input is loaded while the
-  // current one is encoded
+  // interior boundaries (wave-uniform)
+  float Bv[NT];
+#pragma unroll
+  for (int k = 0; k < NT; ++k) Bv[k] = boundaries[1 + k];
+  const float rcf = (float)rc;
+
+  // groups of 16 vectors; the next group's input is loaded while the current
+  // one is encoded.  Past the end the load repeats the last vector, so every
+  // iteration issues the same loads and the wait counts stay static.
   auto load_group = [&](int64_t g0, Op16x8 (&dst)[KS]) {
-    const int64_t vv = g0 + j < n ? g0 + j : g0;
+    const int64_t vv = g0 + j < n ? g0 + j : n - 1;
     const uint4* src = reinterpret_cast<const uint4*>(xb + vv * D + EL * q);
 #pragma unroll
     for (int s = 0; s < KS; ++s) dst[s].v = src[s];
@@ -248,32 +283,19 @@ __global__ __launch_bounds__(256) void encode_mfma_kernel(const void* __restrict
 #pragma unroll
       for (int w = 0; w < 4; ++w) v[s].u[w] ^= sm[s][w];
   };
-  // norm and the NT thresholds of the group held (sign-flipped) in v
-  auto norm_thresholds = [&](const Op16x8 (&v)[KS], float& nrm, float (&T)[NT]) {
+  // t domain scale of the thresholds, RN((norm + 1e-8) / c), of the group held
+  // (sign-flipped) in v; the norm itself goes to nrm
+  auto norm_scale = [&](const Op16x8 (&v)[KS], float& nrm) {
     f32x4_t gram = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < KS; ++s) gram = mfma_16x16x32<DT>(v[s], v[s], gram);
     const float pick = jr_hi ? (jr_lo ? gram[3] : gram[2]) : (jr_lo ? gram[1] : gram[0]);
     const float xx = __int_as_float(__builtin_amdgcn_ds_bpermute(diag_src, __float_as_int(pick)));
     // ||t||^2 = D ||x||^2 (Parseval for the unnormalised transform)
-    nrm = __builtin_sqrtf(xx * (float)D) * c;
-    const double den = (double)(nrm + 1e-8f);
-    float mine[PERQ];
-#pragma unroll
-    for (int k = 0; k < PERQ; ++k) mine[k] = exact_threshold_k(bk[k], den, c2, rc_half);
-#pragma unroll
-    for (int jj = 0; jj < NT; ++jj) T[jj] = __shfl(mine[jj % PERQ], ((jj / PERQ) << 4) | j);
+    nrm = sqrt_rn(xx * (float)D) * c;
+    return (nrm + 1e-8f) * rcf;
   };
-
-  int64_t v0 = wave * 16;
-  if (v0 >= n) return;
-  Op16x8 nxt[KS];
-  load_group(v0, nxt);
-  for (; v0 < n; v0 += wstride) {
-    Op16x8 cur[KS];
-#pragma unroll
-    for (int s = 0; s < KS; ++s) cur[s] = nxt[s];
-    if (v0 + wstride < n) load_group(v0 + wstride, nxt);
+  auto encode_group = [&](Op16x8 (&cur)[KS], int64_t g0) {
     flip_signs(cur);
     f32x4_t acc[MB];
 #pragma unroll
@@ -287,8 +309,6 @@ __global__ __launch_bounds__(256) void encode_mfma_kernel(const void* __restrict
         acc[mb] = mfma_16x16x32<DT>(a, cur[s], acc[mb]);
       }
     }
-    float T[NT], nrm;
-    norm_thresholds(cur, nrm, T);
     float t[EL];
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
@@ -296,8 +316,20 @@ __global__ __launch_bounds__(256) void encode_mfma_kernel(const void* __restrict
       for (int i = 0; i < 4; ++i) t[4 * mb + i] = acc[mb][i];
     constexpr int NW = EL * BITS / 32;
     uint32_t w[NW];
-    quantize_pack<BITS, EL>(t, T, w);
-    const int64_t v = v0 + j;
+    float nrm;
+    const float sv = norm_scale(cur, nrm);
+    if constexpr (SYM) {
+      float P[NH];
+#pragma unroll
+      for (int k = 0; k < NH; ++k) P[k] = Bv[MID + k] * sv;
+      quantize_pack_sym<BITS, EL>(t, Bv[MID - 1] * sv, P, w);
+    } else {
+      float T[NT];
+#pragma unroll
+      for (int k = 0; k < NT; ++k) T[k] = Bv[k] * sv;
+      quantize_pack<BITS, EL>(t, T, w);
+    }
+    const int64_t v = g0 + j;
     if (v < n) {
       uint32_t* dst = reinterpret_cast<uint32_t*>(packed + v * PD) + NW * q;
       if constexpr (NW == 2) {
@@ -311,6 +343,21 @@ __global__ __launch_bounds__(256) void encode_mfma_kernel(const void* __restrict
       }
       if (q == 0) norms[v] = (uint16_t)f32_to_f16_bits(nrm);
     }
+  };
+  if (wave * 16 >= n) return;
+  // two register sets alternate, so no copies between iterations
+  int64_t v0 = wave * 16;
+  Op16x8 b0[KS], b1[KS];
+  load_group(v0, b0);
+  for (;;) {
+    load_group(v0 + wstride, b1);
+    encode_group(b0, v0);
+    v0 += wstride;
+    if (v0 >= n) break;
+    load_group(v0 + wstride, b0);
+    encode_group(b1, v0);
+    v0 += wstride;
+    if (v0 >= n) break;
   }
 }
 

@@ -28,6 +28,8 @@ _i64 = ctypes.c_int64
 # name -> argtypes (all return int status)
 SIGNATURES = {
     "ftq_encode": [_vp, _i32, _i64, _i32, _vp, _vp, _i32, _vp, _vp, _vp],
+    "ftq_encode_cb": [_vp, _i32, _i64, _i32, _vp, _vp, _i32, _i32, _vp, _vp, _vp],
+    "ftq_codebook_class": [_vp, _i32],
     "ftq_decode": [_vp, _vp, _i64, _i32, _vp, _vp, _i32, _vp, _i32, _vp],
     "ftq_rht": [_vp, _i32, _i64, _i32, _vp, _i32, _vp, _i32, _vp],
 }

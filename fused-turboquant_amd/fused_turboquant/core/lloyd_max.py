@@ -53,6 +53,26 @@ def _get_cached_codebook(dim: int, bits: int, max_iterations: int = 300,
     return compute_lloyd_max_codebook(dim, bits, max_iterations, num_grid_points)
 
 
+CB_ANY, CB_SYMMETRIC = 0, 1  # FTQ_CB_ANY / FTQ_CB_SYMMETRIC of the C ABI
+
+
+def codebook_class(boundaries, bits: int) -> int:
+    """Host-side class of a float32 codebook, as the C ABI's ``ftq_codebook_class``
+    computes it: ``CB_SYMMETRIC`` when sorted, ``B[2^bits - j] == -B[j]`` for every
+    interior j but the middle one, and ``|B[mid]| < B[mid + 1]``; else ``CB_ANY``.
+    The encoder's symmetric kernel searches |t| over the positive thresholds."""
+    b = np.asarray(boundaries, dtype=np.float32)
+    if b.shape != ((1 << bits) + 1,) or not np.all(b[:-1] <= b[1:]):
+        return CB_ANY
+    mid = 1 << (bits - 1)
+    if not abs(b[mid]) < b[mid + 1]:
+        return CB_ANY
+    for k in range(1, mid):
+        if not b[mid + k] == -b[mid - k]:
+            return CB_ANY
+    return CB_SYMMETRIC
+
+
 class LloydMaxQuantizer:
     """Precomputed Lloyd-Max scalar quantizer, shared by all layers/heads/tokens."""
 
@@ -64,6 +84,7 @@ class LloydMaxQuantizer:
         b, l = _get_cached_codebook(dim, bits, max_iterations, num_grid_points)
         self.boundaries = torch.tensor(b, dtype=torch.float32, device=device)
         self.levels = torch.tensor(l, dtype=torch.float32, device=device)
+        self.codebook_class = codebook_class(np.asarray(b, dtype=np.float32), bits)
 
     def quantize(self, x: torch.Tensor) -> torch.Tensor:
         idx = torch.bucketize(x, self.boundaries) - 1

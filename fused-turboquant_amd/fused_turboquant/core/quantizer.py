@@ -78,9 +78,10 @@ class TurboQuantMSE:
         packed = torch.empty(lead + (packed_dim(self.head_dim, self.bits),), dtype=torch.uint8, device=dev)
         norms = torch.empty(lead, dtype=torch.float16, device=dev)
         L = _lib.lib()
-        _lib.check(L.ftq_encode(xc.data_ptr(), _lib.dtype_code(xc.dtype), n, self.head_dim,
-                                self.rotation.signs.data_ptr(), self.quantizer.boundaries.data_ptr(),
-                                self.bits, packed.data_ptr(), norms.data_ptr(), _lib.stream_ptr(dev)))
+        _lib.check(L.ftq_encode_cb(xc.data_ptr(), _lib.dtype_code(xc.dtype), n, self.head_dim,
+                                   self.rotation.signs.data_ptr(), self.quantizer.boundaries.data_ptr(),
+                                   self.bits, self.quantizer.codebook_class, packed.data_ptr(),
+                                   norms.data_ptr(), _lib.stream_ptr(dev)))
         return CompressedTensor(indices=packed, norms=norms, original_dim=self.head_dim, bits=self.bits)
 
     # -- decode ------------------------------------------------------------

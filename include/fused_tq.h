@@ -27,6 +27,9 @@ extern "C" {
 
 enum { FTQ_F32 = 0, FTQ_F16 = 1, FTQ_BF16 = 2 };
 
+/* Codebook classes for ftq_encode_cb (see ftq_codebook_class). */
+enum { FTQ_CB_ANY = 0, FTQ_CB_SYMMETRIC = 1 };
+
 /* Message of the last FTQ_ERR_ARG / HIP error raised on this host thread. */
 const char* ftq_last_error(void);
 int ftq_version(void);
@@ -45,6 +48,30 @@ int ftq_version(void);
 int ftq_encode(const void* x, int x_dtype, int64_t n, int d, const float* signs,
                const float* boundaries, int bits, uint8_t* packed_out, uint16_t* norms_out,
                void* stream);
+
+/*
+ * Class of a codebook, from a HOST copy of boundaries [2^bits + 1]:
+ * FTQ_CB_SYMMETRIC when it is sorted, boundaries[2^bits - j] == -boundaries[j]
+ * in fp32 for every interior j but the middle one (j = 2^(bits-1)), and
+ * |middle| < boundaries[middle + 1] -- the Lloyd-Max codebooks of d = 64 and
+ * 128 are; else FTQ_CB_ANY.  Host-only: reads no device memory.
+ * No reference counterpart: the reference's encode has a single path
+ * (kernels/triton_encode.py:150-209).
+ */
+int ftq_codebook_class(const float* boundaries_host, int bits);
+
+/*
+ * ftq_encode with the codebook's class, as ftq_codebook_class returned it for
+ * the values behind `boundaries`.  FTQ_CB_SYMMETRIC selects, for 16-bit x at
+ * d = 128 / 256, a kernel whose search runs on |t| over the positive
+ * thresholds (fewer instructions per element); given a codebook that is not
+ * symmetric it returns codes as if the negative boundaries were the negated
+ * positive ones.  FTQ_CB_ANY is correct for every sorted codebook.
+ * ftq_encode(...) == ftq_encode_cb(..., FTQ_CB_ANY, ...).
+ */
+int ftq_encode_cb(const void* x, int x_dtype, int64_t n, int d, const float* signs,
+                  const float* boundaries, int bits, int codebook_class, uint8_t* packed_out,
+                  uint16_t* norms_out, void* stream);
 
 /*
  * Fused library-format decode: unpack, levels[code] * norm, FWHT, * d^-1/2,

@@ -29,11 +29,14 @@ def _mk(n, d, dtype, seed, outliers=False):
 
 
 def _check_encode(tq, x_cpu, ct, bits, d, label):
+    return _check_arrays(x_cpu, tq.rotation.signs.cpu().numpy(), tq.quantizer.boundaries.cpu().numpy(),
+                         ct.indices.cpu().numpy(), ct.norms.cpu().numpy(), bits, d, label)
+
+
+def _check_arrays(x_cpu, s, bnd, packed, norms, bits, d, label):
     xs = x_cpu.float().numpy()
-    s = tq.rotation.signs.cpu().numpy()
-    bnd = tq.quantizer.boundaries.cpu().numpy()
     p_ref, n_ref, u_ref, _ = O.encode(xs, s, bnd, bits)
-    got = ct.indices.cpu().numpy().reshape(-1, d * bits // 8)
+    got = packed.reshape(-1, d * bits // 8)
     codes = O.unpack(got, bits, d)
     codes_ref = O.unpack(p_ref.reshape(-1, d * bits // 8), bits, d)
     diff = codes != codes_ref
@@ -42,7 +45,7 @@ def _check_encode(tq, x_cpu, ct, bits, d, label):
         dist = O.boundary_distance(u_ref.reshape(-1, d), bnd)[diff]
         assert dist.max() < TIE, f"{label}: code mismatch {dist.max():.3g} away from a boundary"
         assert np.all(np.abs(codes.astype(int) - codes_ref.astype(int))[diff] == 1)
-    nn = ct.norms.cpu().numpy().reshape(-1).astype(np.float32)
+    nn = norms.reshape(-1).astype(np.float32)
     nr = n_ref.reshape(-1).astype(np.float32)
     assert np.all(np.abs(nn - nr) <= 1e-3 * np.abs(nr) + 1e-7), f"{label}: norm mismatch"
     print(f"[{label}] vectors={codes.shape[0]} code_ties={ties}")
@@ -99,6 +102,56 @@ def test_config1_outliers_4bit(cuda, golden):
     assert np.array_equal(ct.indices.cpu().numpy(), enc["packed_cfg1"])
     assert np.array_equal(ct.norms.cpu().numpy().view(np.uint16), enc["norms_cfg1"])
     assert np.array_equal(tq.decode(ct).cpu().numpy(), enc["dec_cfg1"])
+
+
+def _encode_c(x, signs, bnd, bits, cls, dev):
+    """ftq_encode_cb on device tensors x [n, d], signs [d], boundaries [2^bits + 1]."""
+    from fused_turboquant import _lib
+    n, d = x.shape
+    pk = torch.empty(n, d * bits // 8, dtype=torch.uint8, device=dev)
+    nm = torch.empty(n, dtype=torch.float16, device=dev)
+    L = _lib.lib()
+    _lib.check(L.ftq_encode_cb(x.data_ptr(), _lib.dtype_code(x.dtype), n, d, signs.data_ptr(), bnd.data_ptr(),
+                               bits, cls, pk.data_ptr(), nm.data_ptr(), _lib.stream_ptr(dev)))
+    return pk, nm
+
+
+@pytest.mark.parametrize("d", [128, 256])
+@pytest.mark.parametrize("bits", [2, 3, 4])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_encode_both_codebook_kernels(cuda, d, bits, dtype):
+    """The general (FTQ_CB_ANY) and symmetric (FTQ_CB_SYMMETRIC) encoder kernels
+    against the oracle on one symmetric codebook each: the library's at d = 128,
+    a symmetrised copy of the library's at d = 256 (whose own codebook is
+    asymmetric by ~2e-5 relative and always takes the general kernel).  Both
+    kernels: codes exact up to boundary ties, and the same norms."""
+    from fused_turboquant.core.hadamard import generate_rht_signs
+    from fused_turboquant.core.lloyd_max import CB_ANY, CB_SYMMETRIC, codebook_class, compute_lloyd_max_codebook
+    b = compute_lloyd_max_codebook(d, bits)[0].astype(np.float32)
+    mid = 1 << (bits - 1)
+    if d == 256:
+        pos = ((b[mid + 1:-1].astype(np.float64) - b[1:mid][::-1]) / 2).astype(np.float32)
+        b = np.concatenate([[b[0]], -pos[::-1], [0.0], pos, [b[-1]]]).astype(np.float32)
+    assert codebook_class(b, bits) == CB_SYMMETRIC
+    x = _mk(4099, d, dtype, seed=bits * 7 + d, outliers=(bits == 4))
+    x[0] = 0
+    sd = generate_rht_signs(d, 42).to(cuda)
+    bd = torch.from_numpy(b).to(cuda)
+    norms = []
+    for cls in (CB_ANY, CB_SYMMETRIC):
+        pk, nm = _encode_c(x.to(cuda), sd, bd, bits, cls, cuda)
+        _check_arrays(x, sd.cpu().numpy(), b, pk.cpu().numpy(), nm.cpu().numpy(), bits, d,
+                      f"d={d} bits={bits} {dtype} class={cls}")
+        norms.append(nm)
+    assert torch.equal(norms[0], norms[1])
+
+
+def test_quantizer_uses_the_symmetric_kernel_at_d128(cuda):
+    """TurboQuantMSE passes its codebook class: symmetric at d = 128, general at d = 256."""
+    from fused_turboquant import TurboQuantMSE
+    from fused_turboquant.core.lloyd_max import CB_ANY, CB_SYMMETRIC
+    assert TurboQuantMSE(128, bits=3, device=cuda).quantizer.codebook_class == CB_SYMMETRIC
+    assert TurboQuantMSE(256, bits=3, device=cuda).quantizer.codebook_class == CB_ANY
 
 
 @pytest.mark.parametrize("d", [64, 128, 256])

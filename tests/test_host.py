@@ -53,6 +53,48 @@ def test_argument_errors_raise_without_touching_the_gpu():
     assert L.ftq_encode(None, 2, 0, 128, None, None, 3, None, None, None) == 0  # empty input
 
 
+def _c_class(L, b, bits):
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    return L.ftq_codebook_class(b.ctypes.data_as(ctypes.c_void_p), bits)
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4])
+def test_codebook_class_host_and_c_agree(bits):
+    """The encoder's symmetric kernel is chosen from the codebook class; the
+    Python rule and the C ABI's must agree, and the library codebooks of
+    d = 64 / 128 are symmetric in fp32 while those of d = 256 are not."""
+    from fused_turboquant.core.lloyd_max import CB_ANY, CB_SYMMETRIC, codebook_class, compute_lloyd_max_codebook
+    L = _built_lib().lib()
+    for d, want in ((64, CB_SYMMETRIC), (128, CB_SYMMETRIC), (256, CB_ANY)):
+        b = compute_lloyd_max_codebook(d, bits)[0].astype(np.float32)
+        assert codebook_class(b, bits) == want == _c_class(L, b, bits), (d, bits)
+    mid = 1 << (bits - 1)
+    pos = np.sort(np.random.default_rng(bits).uniform(0.01, 0.3, mid - 1)).astype(np.float32)
+    sym = np.concatenate([[-1.0], -pos[::-1], [0.0], pos, [1.0]]).astype(np.float32)
+    cases = {"symmetric": (sym, CB_SYMMETRIC)}
+    tilt = sym.copy()
+    tilt[mid + 1] = np.nextafter(tilt[mid + 1], np.float32(1))  # one ulp off
+    cases["one ulp asymmetric"] = (tilt, CB_ANY)
+    wide = sym.copy()
+    wide[mid] = sym[mid + 1] * 1.5  # middle beyond the first positive boundary
+    cases["middle too wide"] = (np.sort(wide), CB_ANY)
+    uns = sym.copy()
+    uns[1], uns[2] = uns[2], uns[1]
+    cases["unsorted"] = (uns, CB_ANY)
+    nan = sym.copy()
+    nan[mid] = np.nan
+    cases["nan"] = (nan, CB_ANY)
+    for name, (b, want) in cases.items():
+        assert codebook_class(b, bits) == want == _c_class(L, b, bits), name
+    assert _c_class(L, sym, 5) == -1 and b"bits" in L.ftq_last_error()
+
+
+def test_encode_cb_rejects_unknown_class():
+    L = _built_lib().lib()
+    rc = L.ftq_encode_cb(None, 2, 4, 128, None, None, 3, 7, None, None, None)
+    assert rc == -1 and b"codebook_class" in L.ftq_last_error()
+
+
 @pytest.mark.parametrize("d", [64, 128, 256])
 @pytest.mark.parametrize("bits", [1, 2, 3, 4])
 def test_product_codebook_matches_reference(golden, d, bits):
