@@ -109,8 +109,14 @@ __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
   u += 0x7fffu + ((u >> 16) & 1u);
   return u >> 16;
 }
+// fp32 -> fp16 bits, round to nearest even, as an instruction of its own: left
+// to the compiler, a conversion of a product becomes one v_fma_mix* (a single
+// rounding of the exact product to fp16), where the reference rounds the
+// product to fp32 first and then to fp16 (.half() of a float32 tensor)
 __device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
-  return (uint32_t)__half_as_ushort(__float2half_rn(f));
+  uint32_t r;
+  asm("v_cvt_f16_f32 %0, %1" : "=v"(r) : "v"(f));
+  return r & 0xffffu;
 }
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t b) {
   return __half2float(__ushort_as_half((unsigned short)b));

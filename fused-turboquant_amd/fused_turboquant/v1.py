@@ -312,8 +312,12 @@ def bench_setup(dev):
             splits, ws.data_ptr(), ws.numel(), out.data_ptr(), _lib.dtype_code(out.dtype),
             _lib.stream_ptr(dev))
 
+    # the launch holds raw pointers: keep every tensor behind them alive with it
+    keep = (layer, cache, q, bt, sl, ws, out)
+
     def run():
         _lib.check(L.ftq_v1_decode_attention(*args))
+    run.keep = keep
 
     per_tok = slot_bytes(d, layer.key_bits, layer.value_bits)  # 66 B of K + 36 B of V
     kv_bytes = sum(lens) * hkv * per_tok
