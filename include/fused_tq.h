@@ -199,6 +199,50 @@ int ftq_v1_decode_attention(const void* query, int q_dtype, const uint8_t* kv_ca
                             float scale, int v_rotate, int num_splits, void* workspace,
                             int64_t workspace_bytes, void* out, int out_dtype, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * Raw fp16 slots of the boundary-protection layers (TURBOQUANT_BOUNDARY_PROTECT
+ * = fp16): the same [num_blocks][block_size][Hkv][slot] byte cache, per
+ * (token, kv head) [K fp16 (2 d bytes)][V fp16 (2 d bytes)][pad], the layout of
+ * the reference's _store_raw_kv (vllm_plugin/v1_backend.py:1449-1505).
+ * ------------------------------------------------------------------------- */
+
+/* Bytes of a raw slot that hold data: 4 * d (-1 for an unsupported d). */
+int64_t ftq_raw_slot_bytes(int d);
+
+/*
+ * Store n_tokens x num_kv_heads K/V vectors ([n][Hkv][d], dtype) as fp16
+ * (round to nearest even) into their raw slots; slot_mapping[i] < 0 skips
+ * token i (and a slot past the cache is skipped too).  Replaces _store_raw_kv
+ * (vllm_plugin/v1_backend.py:1449-1505).  One launch.  Strides in bytes,
+ * multiples of 16.
+ */
+int ftq_raw_store(const void* key, const void* value, int dtype, int64_t n_tokens,
+                  int num_kv_heads, int d, const int64_t* slot_mapping, uint8_t* kv_cache,
+                  int64_t num_blocks, int block_size, int64_t stride_block, int64_t stride_pos,
+                  int64_t stride_head, void* stream);
+
+/* Workspace bytes ftq_raw_decode_attention needs: batch*Hq*splits*(d+1)*4. */
+int64_t ftq_raw_workspace_bytes(int batch, int num_q_heads, int d, int num_splits);
+/* Split-K factor that fills the GPU for this shape (host-side heuristic). */
+int ftq_raw_default_splits(int batch, int num_kv_heads, int max_seq_len);
+
+/*
+ * Decode attention over raw fp16 slots, one query token per sequence:
+ * softmax(q . K^T * scale) . V over positions [kv_start[b], seq_lens[b]) of
+ * block_table row b (kv_start may be NULL = 0), kv head = h / (Hq/Hkv); rows
+ * with no positions give 0.  Replaces boundary_fp16_decode_attention
+ * (vllm_plugin/triton_boundary_attn.py:28-219) as called by _forward_raw
+ * (v1_backend.py:1547-1640).  Head dim 128, GQA group <= 8.  Two launches on
+ * `stream`: split-K stage 1, then merge.
+ */
+int ftq_raw_decode_attention(const void* query, int q_dtype, const uint8_t* kv_cache,
+                             int64_t num_blocks, int block_size, int64_t stride_block,
+                             int64_t stride_pos, int64_t stride_head, const int32_t* block_table,
+                             int max_blocks_per_seq, const int32_t* seq_lens,
+                             const int32_t* kv_start, int batch, int num_q_heads,
+                             int num_kv_heads, int d, float scale, int num_splits, void* workspace,
+                             int64_t workspace_bytes, void* out, int out_dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -42,6 +42,11 @@ Pinning (each check lives in ``tests/test_oracle.py``):
 * v1 store/decode: parity unpinned against vLLM (vLLM's ``get_centroids`` and
   stage-2 kernel are not in the reference tree); pinned by closed forms (LSE
   merge == single softmax, uniform quantiser error bound, Hadamard matrix).
+* raw_* (boundary-layer fp16 slots, ``vllm_plugin/v1_backend.py:1449-1545``,
+  ``triton_boundary_attn.py:28-219``): the store is numpy's float16 rounding
+  (IEEE round to nearest even, as torch's ``.to(float16)``); the attention is
+  float64 softmax attention, checked against an independent dense computation
+  over the K/V arrays before they enter the cache.
 """
 from __future__ import annotations
 
@@ -534,4 +539,66 @@ def v1_decode_attention(q: np.ndarray, kv_cache: np.ndarray, block_table: np.nda
             p = np.exp(s)
             o = (p / p.sum()) @ vv
             out[b, h] = (o @ M.T) if v_rotate else o
+    return out
+
+
+# --------------------------------------------------------------------------
+# raw fp16 slots of the boundary layers
+#   store:  vllm_plugin/v1_backend.py:1449-1505 (_store_raw_kv)
+#   decode: vllm_plugin/triton_boundary_attn.py:28-219 (one program per
+#           (batch, q head), online softmax over the block-table positions)
+# --------------------------------------------------------------------------
+
+
+def raw_store(key: np.ndarray, value: np.ndarray, slot_mapping: np.ndarray,
+              kv_cache: np.ndarray) -> None:
+    """Write key/value [n, Hkv, d] as float16 into kv_cache
+    uint8[nb, bs, Hkv, slot] at [K fp16 | V fp16]; negative slots skipped."""
+    n, hkv, d = key.shape
+    nb, bs = kv_cache.shape[0], kv_cache.shape[1]
+    with np.errstate(over="ignore"):  # fp16 overflow -> inf, as .to(float16) does
+        k16 = np.asarray(key, np.float32).astype(np.float16).view(np.uint8).reshape(n, hkv, 2 * d)
+        v16 = np.asarray(value, np.float32).astype(np.float16).view(np.uint8).reshape(n, hkv, 2 * d)
+    for i in range(n):
+        s = int(slot_mapping[i])
+        if s < 0 or s // bs >= nb:
+            continue
+        kv_cache[s // bs, s % bs, :, : 2 * d] = k16[i]
+        kv_cache[s // bs, s % bs, :, 2 * d: 4 * d] = v16[i]
+
+
+def raw_unpack(kv_cache: np.ndarray, d: int):
+    """(K, V) float64 [nb, bs, Hkv, d] from raw slots."""
+    nb, bs, hkv, slot = kv_cache.shape
+    c = np.ascontiguousarray(kv_cache[..., : 4 * d])
+    k = c[..., : 2 * d].copy().view(np.float16).astype(np.float64)
+    v = c[..., 2 * d: 4 * d].copy().view(np.float16).astype(np.float64)
+    return k, v
+
+
+def raw_decode_attention(q: np.ndarray, kv_cache: np.ndarray, block_table: np.ndarray,
+                         seq_lens: np.ndarray, scale: float, kv_start=None) -> np.ndarray:
+    """float64 softmax(q . K^T * scale) . V over positions [kv_start[b],
+    seq_lens[b]) of block-table row b; kv head h // (Hq/Hkv); empty rows 0."""
+    q = np.asarray(q, np.float64)
+    B, Hq, d = q.shape
+    nb, bs, Hkv, slot = kv_cache.shape
+    G = Hq // Hkv
+    k_all, v_all = raw_unpack(kv_cache, d)
+    out = np.zeros((B, Hq, d))
+    for b in range(B):
+        L = int(seq_lens[b])
+        s0 = 0 if kv_start is None else int(kv_start[b])
+        if L <= s0:
+            continue
+        pos = np.arange(s0, L)
+        blk = np.asarray(block_table[b])[pos // bs]
+        off = pos % bs
+        for h in range(Hq):
+            kk = k_all[blk, off, h // G]
+            vv = v_all[blk, off, h // G]
+            s = kk @ q[b, h] * scale
+            s = s - s.max()
+            p = np.exp(s)
+            out[b, h] = (p / p.sum()) @ vv
     return out

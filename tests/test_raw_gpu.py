@@ -1,0 +1,155 @@
+"""Raw fp16 boundary-layer slots on gfx950 vs the CPU oracle.
+
+Store: every slot byte equals the oracle's (fp16 round to nearest even of the
+bf16 / f16 / f32 input, [K | V] layout); negative slots and padding untouched.
+Decode attention: against the oracle's float64 attention over the same cache
+bytes.  K and V are exact fp16, the query enters the MFMA as f16 hi + lo and P
+stays fp32, so the error is the output rounding plus fp32 accumulation:
+f32 output  max |err| <= 1e-4 + 1e-4 |want|;
+bf16 output max |err| <= 2^-8 |want| + 1e-3 (one bf16 rounding).
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import tq_oracle as O
+
+pytestmark = pytest.mark.gpu
+DT = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}
+
+
+def _check(got, want, out_dtype, tag):
+    err = np.abs(got.astype(np.float64) - want)
+    if out_dtype == torch.float32:
+        bound = 1e-4 + 1e-4 * np.abs(want)
+    else:
+        bound = 1e-3 + 2.0 ** -8 * np.abs(want)
+    print(f"[{tag}] max {err.max():.2e} mean {err.mean():.2e} worst/bound {(err / bound).max():.2f}", flush=True)
+    assert (err <= bound).all(), tag
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16", "f32"])
+@pytest.mark.parametrize("d", [64, 128, 256])
+def test_store_parity(cuda, dtype, d):
+    from fused_turboquant import raw
+    g = torch.Generator().manual_seed(d)
+    n, hkv, nb, bs = 77, 3, 9, 16
+    k = (torch.randn(n, hkv, d, generator=g) * 4).to(DT[dtype])
+    v = torch.randn(n, hkv, d, generator=g).to(DT[dtype])
+    if dtype == "f32":
+        k[0, 0, :3] = torch.tensor([70000.0, 3e-6, -6e-8])
+    slots = torch.randperm(nb * bs, generator=g)[:n]
+    slots[::7] = -1
+    slot = 4 * d + 32
+    cache = torch.full((nb, bs, hkv, slot), 0x5A, dtype=torch.uint8)
+    want = cache.numpy().copy()
+    O.raw_store(k.float().numpy(), v.float().numpy(), slots.numpy(), want)
+    got = cache.to(cuda)
+    raw.raw_store(k.to(cuda), v.to(cuda), got, slots.to(cuda))
+    np.testing.assert_array_equal(got.cpu().numpy(), want)
+
+
+def _oracle_cache(g, nb, bs, hkv, d, n_tok, slot=None):
+    slot = slot or 4 * d
+    cache = np.zeros((nb, bs, hkv, slot), np.uint8)
+    k = torch.randn(n_tok, hkv, d, generator=g).numpy()
+    v = torch.randn(n_tok, hkv, d, generator=g).numpy()
+    slots = torch.randperm(nb * bs, generator=g)[:n_tok].numpy()
+    O.raw_store(k, v, slots, cache)
+    return cache
+
+
+@pytest.mark.parametrize("hq,hkv", [(8, 8), (8, 4), (8, 2), (14, 2), (16, 2)])
+@pytest.mark.parametrize("splits", [1, 3, 16])
+def test_decode_parity(cuda, hq, hkv, splits):
+    from fused_turboquant import raw
+    d, bs, nb = 128, 16, 48
+    g = torch.Generator().manual_seed(hq * 100 + hkv * 10 + splits)
+    cache = _oracle_cache(g, nb, bs, hkv, d, nb * bs)
+    lens = [0, 1, 15, 17, 100, 257, 16, 64]
+    B = len(lens)
+    bt = torch.randint(0, nb, (B, 20), generator=g, dtype=torch.int32)
+    q = torch.randn(B, hq, d, generator=g).to(torch.bfloat16)
+    sl = torch.tensor(lens, dtype=torch.int32)
+    want = O.raw_decode_attention(q.float().numpy(), cache, bt.numpy(), sl.numpy(), 1 / math.sqrt(d))
+    for odt in (torch.bfloat16, torch.float32):
+        out = torch.empty(B, hq, d, dtype=odt, device=cuda)
+        raw.raw_decode_attention(q.to(cuda), torch.from_numpy(cache).to(cuda), bt.to(cuda), sl.to(cuda),
+                                 num_splits=splits, out=out)
+        got = out.float().cpu().numpy()
+        assert not got[0].any()  # empty sequence -> zeros
+        _check(got, want, odt, f"raw hq={hq} hkv={hkv} S={splits} out={odt}")
+
+
+@pytest.mark.parametrize("bs", [16, 32, 64])
+def test_decode_kv_start_block_size_and_padded_slot(cuda, bs):
+    from fused_turboquant import raw
+    d, hkv, hq = 128, 2, 8
+    nb = 1024 // bs
+    g = torch.Generator().manual_seed(bs)
+    cache = _oracle_cache(g, nb, bs, hkv, d, nb * bs, slot=4 * d + 64)  # slot wider than the data
+    lens = [300, 31, 1000, 64]
+    starts = [40, 31, 999, 0]
+    bt = torch.stack([torch.randperm(nb, generator=g)[: 1024 // bs].to(torch.int32) for _ in lens])
+    q = torch.randn(len(lens), hq, d, generator=g, dtype=torch.float32)
+    sl = torch.tensor(lens, dtype=torch.int32)
+    ks = torch.tensor(starts, dtype=torch.int32)
+    out = raw.raw_decode_attention(q.to(cuda), torch.from_numpy(cache).to(cuda), bt.to(cuda), sl.to(cuda),
+                                   kv_start=ks.to(cuda), num_splits=5,
+                                   out=torch.empty(len(lens), hq, d, device=cuda))
+    want = O.raw_decode_attention(q.numpy(), cache, bt.numpy(), sl.numpy(), 1 / math.sqrt(d), kv_start=ks.numpy())
+    got = out.cpu().numpy()
+    assert not got[1].any()  # kv_start == seq_len -> nothing attended
+    _check(got, want, torch.float32, f"raw kv_start bs={bs}")
+
+
+def test_store_then_decode_end_to_end(cuda):
+    """GPU store, then GPU decode, against the oracle pipeline on the same inputs
+    (large-magnitude outliers, bf16 input)."""
+    from fused_turboquant import raw
+    d, bs, hkv, hq = 128, 16, 4, 16
+    g = torch.Generator().manual_seed(77)
+    lens = [513, 77, 1024]
+    nb = sum((L + bs - 1) // bs for L in lens) + 3
+    cache = torch.zeros(nb, bs, hkv, 4 * d, dtype=torch.uint8, device=cuda)
+    perm = torch.randperm(nb, generator=g).to(torch.int32)
+    mb = max((L + bs - 1) // bs for L in lens)
+    bt = torch.zeros(len(lens), mb, dtype=torch.int32)
+    used = 0
+    for b, L in enumerate(lens):
+        npg = (L + bs - 1) // bs
+        bt[b, :npg] = perm[used:used + npg]
+        used += npg
+        k = torch.randn(L, hkv, d, generator=g)
+        v = torch.randn(L, hkv, d, generator=g)
+        sel = torch.rand(L, generator=g) < 0.02
+        k[sel] *= 8
+        v[sel] *= 8
+        pos = torch.arange(L)
+        slots = bt[b].long()[pos // bs] * bs + pos % bs
+        raw.raw_store(k.to(torch.bfloat16).to(cuda), v.to(torch.bfloat16).to(cuda), cache, slots.to(cuda))
+    q = torch.randn(len(lens), hq, d, generator=g).to(torch.bfloat16)
+    sl = torch.tensor(lens, dtype=torch.int32)
+    out = raw.raw_decode_attention(q.to(cuda), cache, bt.to(cuda), sl.to(cuda))
+    want = O.raw_decode_attention(q.float().numpy(), cache.cpu().numpy(), bt.numpy(), sl.numpy(), 1 / math.sqrt(d))
+    _check(out.float().cpu().numpy(), want, torch.bfloat16, "raw store+decode")
+
+
+def test_bench_shape_full_size(cuda):
+    """The benchmark's shape (B=32, Hq=32, Hkv=8, ctx 8192, 512-byte slots,
+    1.07 GB of K/V): oracle on two sequences, split-count invariance over all."""
+    from fused_turboquant import raw
+    setup = raw.bench_setup(cuda)
+    setup["run"]()
+    out = setup["out"].float().cpu().numpy()
+    cache, bt, sl, q = setup["cache"], setup["bt"], setup["sl"], setup["q"]
+    for b in (0, 31):
+        sub = cache[bt[b].long()].cpu().numpy()  # the sequence's pages, in order
+        want = O.raw_decode_attention(q[b:b + 1].float().cpu().numpy(), sub,
+                                      np.arange(sub.shape[0], dtype=np.int32)[None], sl[b:b + 1].cpu().numpy(),
+                                      1 / math.sqrt(128))
+        _check(out[b:b + 1], want, torch.bfloat16, f"raw bench shape b={b}")
+    other = raw.raw_decode_attention(q, cache, bt, sl, num_splits=1).float().cpu().numpy()
+    _check(other, out.astype(np.float64), torch.bfloat16, "raw split invariance")
