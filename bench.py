@@ -8,8 +8,9 @@ One step = the BASELINE headline workload on one GPU, inputs resident in HBM:
 ``value`` is the encode throughput in GB/s of bf16 input consumed.
 
 Also timed (not part of the step): the d=256 encode and the d=128 decode of
-config 2, and config 4 (vLLM v1 slot format, K4V2, v_rotate, B=4, contexts
-U[65536, 131072]).  Every kernel gets a roofline entry: algorithmic bytes per
+config 2, config 4 (vLLM v1 slot format, K4V2, v_rotate, B=4, contexts
+U[65536, 131072]) and the boundary-layer raw fp16 decode attention at the
+config-3 shape (512-byte K|V slots, 1.07 GB).  Every kernel gets a roofline entry: algorithmic bytes per
 launch / average launch time, from HIP events on the stream the library
 launches on (torch's current stream).
 
@@ -40,6 +41,7 @@ TRAFFIC_BYTES: dict = {
     "decode_d128_3bit_f32": 149026181,
     "paged_attn_config3": 224276668,
     "v1_attn_config4": 406898134,
+    "raw_attn_boundary": None,
 }
 
 
@@ -132,6 +134,7 @@ def main():
     import torch
     from fused_turboquant import TurboQuantMSE, _lib
     from fused_turboquant import paged as P
+    from fused_turboquant import raw as R
     from fused_turboquant import v1 as V1
 
     dev = torch.device("cuda:0")
@@ -170,6 +173,8 @@ def main():
     attn3 = P.bench_setup(dev)
     log("[bench] config4 v1 cache (B=4 ctx~U[64K,128K] K4V2 v_rotate)")
     attn4 = V1.bench_setup(dev)
+    log("[bench] boundary-layer raw fp16 cache (config3 shape, 512 B slots)")
+    attnr = R.bench_setup(dev)
     torch.cuda.synchronize()
 
     def step():
@@ -207,6 +212,7 @@ def main():
     t_dec = time_launches(dec_k, it, torch)
     t_a3 = time_launches(attn3["run"], it, torch)
     t_a4 = time_launches(attn4["run"], it, torch)
+    t_ar = time_launches(attnr["run"], it, torch)
     check_lean(enc_k, enc_k256, dec_k)
 
     enc_bytes = n * 128 * 2 + n * (128 * bits // 8) + n * 2
@@ -218,6 +224,7 @@ def main():
         "decode_d128_3bit_f32": roof("decode_d128_3bit_f32", dec_bytes, t_dec),
         "paged_attn_config3": roof("paged_attn_config3", attn3["total_bytes"], t_a3),
         "v1_attn_config4": roof("v1_attn_config4", attn4["total_bytes"], t_a4),
+        "raw_attn_boundary": roof("raw_attn_boundary", attnr["total_bytes"], t_ar),
     }
     for k, r in rl.items():
         log(f"[bench] {k}: {r['kernel_us']} us  {r['achieved']} GB/s  frac {r['frac']}")

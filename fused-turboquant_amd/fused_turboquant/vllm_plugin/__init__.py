@@ -10,14 +10,16 @@ on import so every vLLM process that touches the package registers the
 backend.  Environment variables: ``TURBOQUANT_KEY_BITS`` /
 ``TURBOQUANT_VALUE_BITS`` (per-K/V bit overrides inside the preset's slot),
 ``TURBOQUANT_V_ROTATE`` (Hadamard-rotate V before its uniform quantisation),
-``TURBOQUANT_BOUNDARY_PROTECT`` (slot sized for raw boundary layers).
+``TURBOQUANT_BOUNDARY_PROTECT`` (boundary layers: raw fp16 slots by default,
+or TurboQuant codes at 2/3/4 bits).
 """
-from .plugin import (TQ_PRESETS, apply_additional_config, boundary_protect_enabled, env_flag,
-                     host_preset, register_backend)
+from .plugin import (TQ_PRESETS, apply_additional_config, boundary_protect_enabled, boundary_protect_mode,
+                     env_flag, host_preset, register_backend)
 from .v1_backend import FusedTurboQuantV1Backend, FusedTurboQuantV1Impl
 
 __all__ = ["register_backend", "host_preset", "TQ_PRESETS", "apply_additional_config",
-           "boundary_protect_enabled", "env_flag", "FusedTurboQuantV1Backend", "FusedTurboQuantV1Impl"]
+           "boundary_protect_enabled", "boundary_protect_mode", "env_flag", "FusedTurboQuantV1Backend",
+           "FusedTurboQuantV1Impl"]
 
 try:
     register_backend()

@@ -73,12 +73,36 @@ def env_flag(name: str, default: bool = False) -> bool:
     return raw.strip().lower() in ("1", "true", "yes", "on")
 
 
-def boundary_protect_enabled() -> bool:
-    """``TURBOQUANT_BOUNDARY_PROTECT`` (reference ``plugin.py:64-122``): any
-    value but 0/off/false/no leaves boundary layers at raw fp16 slots, which
-    widens the shared slot to 2*head_size bf16 elements."""
+def boundary_protect_mode() -> "str | int":
+    """``TURBOQUANT_BOUNDARY_PROTECT`` (reference ``plugin.py:64-118``):
+    ``"off"`` (0/off/false/no), ``"fp16"`` (1/fp16/f16/bf16/bfloat16, the
+    default: vLLM keeps the first and last attention layers at raw fp16 slots),
+    ``"fp8"`` (fp8/f8), or a bit count in {2, 3, 4, 8} (boundary layers stored
+    as TurboQuant codes at that width in their fp16-sized slot).  Anything else
+    raises ``ValueError``."""
     raw = os.environ.get("TURBOQUANT_BOUNDARY_PROTECT", "1").strip().lower()
-    return raw not in ("0", "false", "off", "no")
+    if raw in ("0", "false", "off", "no"):
+        return "off"
+    if raw in ("1", "fp16", "f16", "bf16", "bfloat16"):
+        return "fp16"
+    if raw in ("fp8", "f8"):
+        return "fp8"
+    try:
+        bits = int(raw)
+    except ValueError as e:
+        raise ValueError(f"TURBOQUANT_BOUNDARY_PROTECT={raw!r} not understood. Use 0/off, "
+                         "1/fp16, fp8, or a bit count from {2, 3, 4, 8}.") from e
+    if bits not in (2, 3, 4, 8):
+        raise ValueError(f"TURBOQUANT_BOUNDARY_PROTECT={bits} not supported. Use one of {{2, 3, 4, 8}} "
+                         "for a quantized boundary, or 1/fp16 or fp8 for raw / FP8 boundary.")
+    return bits
+
+
+def boundary_protect_enabled() -> bool:
+    """Boolean view of ``boundary_protect_mode`` (reference ``plugin.py:120-122``):
+    any mode but ``"off"`` keeps boundary layers in fp16-sized slots, which
+    widens the shared slot to 2*head_size bf16 elements."""
+    return boundary_protect_mode() != "off"
 
 
 def apply_additional_config(engine_args) -> None:

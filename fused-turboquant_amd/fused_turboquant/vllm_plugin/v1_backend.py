@@ -23,6 +23,13 @@ Per call:
   table row): causal attention over the stored slots, the reference's
   continuation path (``:1359-1384``).
 
+Boundary-protection layers (a plain cache dtype such as ``"auto"``; reference
+``:335-366``) follow ``TURBOQUANT_BOUNDARY_PROTECT``: ``fp16`` stores raw fp16
+K|V slots (``ftq_raw_store``, the reference's ``_store_raw_kv``, ``:1449-1505``)
+and decodes them with ``ftq_raw_decode_attention`` (the reference's
+``boundary_fp16_decode_attention``, ``triton_boundary_attn.py:28-219``); 2/3/4
+run the TurboQuant path at that width inside the fp16-sized slot.
+
 Per-layer state (sorted centroids, midpoints) is cached on the ``layer``
 object, like the reference's ``setup_layer`` (``rotation/matrix.py:34-42``).
 The centroid table of vLLM's ``get_centroids`` is not available here; this
@@ -37,8 +44,9 @@ from typing import Any, ClassVar, Optional
 import torch
 import torch.nn.functional as F
 
+from .. import raw as RAW
 from .. import v1 as V1
-from .plugin import TQ_PRESETS, boundary_protect_enabled, env_flag, host_preset
+from .plugin import TQ_PRESETS, boundary_protect_enabled, boundary_protect_mode, env_flag, host_preset
 
 try:  # vLLM's base classes when present (not installed in every environment)
     from vllm.attention.backends.abstract import AttentionBackend as _BackendBase  # type: ignore
@@ -140,22 +148,39 @@ class FusedTurboQuantV1Impl(_ImplBase):
             raise NotImplementedError("sliding-window attention is not supported by the TURBOQUANT backend")
         if logits_soft_cap is not None:
             raise NotImplementedError("logit soft-capping is not supported by the TURBOQUANT backend")
-        if not (isinstance(kv_cache_dtype, str) and kv_cache_dtype.startswith("turboquant_")):
-            raise NotImplementedError(
-                f"kv_cache_dtype={kv_cache_dtype!r}: raw fp16 boundary layers are not part of this build")
+        # Boundary-protection layers arrive with a plain cache dtype ("auto",
+        # "float16", "bfloat16"; reference v1_backend.py:335-366): raw fp16
+        # slots in mode "fp16", TurboQuant codes at N bits in mode N.
+        is_boundary = not (isinstance(kv_cache_dtype, str) and kv_cache_dtype.startswith("turboquant_"))
+        mode = boundary_protect_mode()
+        self._is_raw = False
+        if is_boundary:
+            if mode == "fp16":
+                self._is_raw = True
+                self.preset, self.key_bits, self.value_bits = "raw_fp16", 16, 16
+            elif mode in (2, 3, 4):
+                self.preset, self.key_bits, self.value_bits = f"boundary_{mode}bit", mode, mode
+            elif mode in ("fp8", 8):
+                raise NotImplementedError("8-bit / FP8 boundary layers (TURBOQUANT_BOUNDARY_PROTECT=8 or fp8) "
+                                          "are not part of this build; use 1/fp16 or 2/3/4")
+            else:
+                raise NotImplementedError(f"kv_cache_dtype={kv_cache_dtype!r} needs a turboquant_* cache dtype "
+                                          "when TURBOQUANT_BOUNDARY_PROTECT is off")
+        else:
+            self.preset, self.key_bits, self.value_bits = host_preset(kv_cache_dtype)
         if head_size != 128:
-            raise NotImplementedError("the gfx950 v1 decode kernel supports head_size 128")
-        if num_heads % num_kv_heads != 0 or num_heads // num_kv_heads > 16:
-            raise ValueError("num_heads must be a multiple of num_kv_heads with a group of at most 16")
+            raise NotImplementedError("the gfx950 decode kernels support head_size 128")
+        group_limit = 8 if self._is_raw else 16
+        if num_heads % num_kv_heads != 0 or num_heads // num_kv_heads > group_limit:
+            raise ValueError(f"num_heads must be a multiple of num_kv_heads with a group of at most {group_limit}")
         self.num_heads = num_heads
         self.head_size = head_size
         self.scale = float(scale)
         self.num_kv_heads = num_kv_heads
         self.num_kv_groups = num_heads // num_kv_heads
         self.kv_cache_dtype = kv_cache_dtype
-        self.preset, self.key_bits, self.value_bits = host_preset(kv_cache_dtype)
-        self.v_rotate = env_flag("TURBOQUANT_V_ROTATE") or env_flag("TURBOQUANT_V_LLOYD_MAX")
-        if env_flag("TURBOQUANT_V_LLOYD_MAX"):
+        self.v_rotate = not self._is_raw and (env_flag("TURBOQUANT_V_ROTATE") or env_flag("TURBOQUANT_V_LLOYD_MAX"))
+        if env_flag("TURBOQUANT_V_LLOYD_MAX") and not self._is_raw:
             raise NotImplementedError("TURBOQUANT_V_LLOYD_MAX (Lloyd-Max V codes) is not part of this build")
 
     # -- per-layer state ---------------------------------------------------
@@ -178,9 +203,12 @@ class FusedTurboQuantV1Impl(_ImplBase):
             return
         if kv_cache.dtype != torch.uint8:
             kv_cache = kv_cache.view(torch.uint8)
-        st = self._state(layer, key.device)
         k = key[:N].reshape(N, self.num_kv_heads, self.head_size)
         v = value[:N].reshape(N, self.num_kv_heads, self.head_size)
+        if self._is_raw:
+            RAW.raw_store(k, v, kv_cache, slot_mapping[:N].to(torch.int64))
+            return
+        st = self._state(layer, key.device)
         st.store(k, v, kv_cache, slot_mapping[:N].to(torch.int64))
 
     # -- attention -----------------------------------------------------------
@@ -197,7 +225,7 @@ class FusedTurboQuantV1Impl(_ImplBase):
         if kv_cache.dtype != torch.uint8:
             kv_cache = kv_cache.view(torch.uint8)
         N = attn_metadata.num_actual_tokens
-        st = self._state(layer, query.device)
+        st = None if self._is_raw else self._state(layer, query.device)
         q = query[:N].view(N, self.num_heads, self.head_size)
         nd = attn_metadata.num_decodes
         ndt = attn_metadata.num_decode_tokens
@@ -222,6 +250,8 @@ class FusedTurboQuantV1Impl(_ImplBase):
         bt = block_table if block_table.dtype == torch.int32 else block_table.to(torch.int32)
         sl = seq_lens if seq_lens.dtype == torch.int32 else seq_lens.to(torch.int32)
         msl = max_seq_len if max_seq_len is not None else bt.shape[1] * kv_cache.shape[1]
+        if self._is_raw:
+            return RAW.raw_decode_attention(q, kv_cache, bt, sl, scale=self.scale, max_seq_len=msl)
         return V1.v1_decode_attention(q, kv_cache, bt, sl, st.centroids, self.key_bits, self.value_bits,
                                       scale=self.scale, v_rotate=self.v_rotate, max_seq_len=msl)
 

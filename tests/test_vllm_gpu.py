@@ -58,7 +58,8 @@ def _run_step(cuda, seqs, dtype_str, hq, hkv, vrot, monkeypatch, seed, bs=16, pr
     pages = [(c + q + bs - 1) // bs for c, q in seqs]
     nb = sum(pages) + 5
     shape = Bk.get_kv_cache_shape(nb, bs, hkv, D, dtype_str)
-    cache = torch.zeros(shape, dtype=torch.uint8, device=cuda)
+    # boundary layers ("auto") get vLLM's bf16 allocation of the same shape
+    cache = torch.zeros(shape, dtype=torch.bfloat16 if dtype_str == "auto" else torch.uint8, device=cuda)
     perm = torch.randperm(nb, generator=g).to(torch.int32)
     mb = max(pages)
     bt = torch.zeros(len(seqs), mb, dtype=torch.int32)
@@ -104,9 +105,9 @@ def _run_step(cuda, seqs, dtype_str, hq, hkv, vrot, monkeypatch, seed, bs=16, pr
     assert ret is output
     got = output.float().cpu().numpy().reshape(N, hq, D)
 
-    st = layer._fused_tq_state
-    cache_np = cache.cpu().numpy()
-    cent = st.centroids.cpu().numpy()
+    cache_np = cache.view(torch.uint8).cpu().numpy()
+    raw = impl._is_raw
+    cent = None if raw else layer._fused_tq_state.centroids.cpu().numpy()
     kb, vb = impl.key_bits, impl.value_bits
     for i, (c, q) in enumerate(seqs):
         a = int(qsl[i])
@@ -116,8 +117,11 @@ def _run_step(cuda, seqs, dtype_str, hq, hkv, vrot, monkeypatch, seed, bs=16, pr
         else:
             sl = np.arange(c + 1, c + q + 1, dtype=np.int32)
             btr = np.repeat(bt[i:i + 1].numpy(), q, axis=0)
-            want = O.v1_decode_attention(qs[i].float().numpy(), cache_np, btr, sl, cent, kb, vb,
-                                         1 / math.sqrt(D), v_rotate=vrot)
+            if raw:
+                want = O.raw_decode_attention(qs[i].float().numpy(), cache_np, btr, sl, 1 / math.sqrt(D))
+            else:
+                want = O.v1_decode_attention(qs[i].float().numpy(), cache_np, btr, sl, cent, kb, vb,
+                                             1 / math.sqrt(D), v_rotate=vrot)
         kind = "prefill" if c == 0 else ("decode" if q == 1 else "continuation")
         _check(got[a:a + q], want, f"{dtype_str} vrot={vrot} seq{i} {kind} cached={c} q={q}")
 
@@ -149,3 +153,12 @@ def test_no_metadata_zeroes_output(cuda):
     q = torch.randn(4, 8 * D, device=cuda, dtype=torch.bfloat16)
     impl.forward(SimpleNamespace(), q, q[:, :2 * D], q[:, :2 * D], cache, None, output=out)
     assert not out.any()
+
+
+@pytest.mark.parametrize("protect", ["1", "3"])
+def test_boundary_layer_mixed_batch(cuda, monkeypatch, protect):
+    """A boundary-protection layer (cache dtype "auto", vLLM's bf16 allocation):
+    raw fp16 slots by default, 3-bit TurboQuant codes in the fp16-sized slot
+    with TURBOQUANT_BOUNDARY_PROTECT=3; decode, fresh prefill and continuation."""
+    _run_step(cuda, [(40, 1), (700, 1), (0, 33), (129, 9)], "auto", 32, 8, False, monkeypatch,
+              seed=5, protect=protect)

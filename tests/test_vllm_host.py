@@ -88,8 +88,6 @@ def test_impl_init_and_refusals(monkeypatch):
     with pytest.raises(NotImplementedError):
         mk(sliding_window=128)
     with pytest.raises(NotImplementedError):
-        mk(kv_cache_dtype="auto")
-    with pytest.raises(NotImplementedError):
         mk(head_size=64)
     with pytest.raises(ValueError):
         mk(num_heads=8, num_kv_heads=3)
@@ -116,3 +114,37 @@ def test_register_without_vllm():
     except ImportError:
         pass
     assert vp.register_backend() is False
+
+
+@pytest.mark.parametrize("raw,want", [("0", "off"), ("off", "off"), ("1", "fp16"), ("bf16", "fp16"),
+                                      ("FP16", "fp16"), ("fp8", "fp8"), ("2", 2), ("3", 3), ("4", 4), ("8", 8)])
+def test_boundary_protect_mode(monkeypatch, raw, want):
+    monkeypatch.setenv("TURBOQUANT_BOUNDARY_PROTECT", raw)
+    assert vp.boundary_protect_mode() == want
+    assert vp.boundary_protect_enabled() == (want != "off")
+
+
+@pytest.mark.parametrize("raw", ["5", "yes please", "16"])
+def test_boundary_protect_mode_rejects(monkeypatch, raw):
+    monkeypatch.setenv("TURBOQUANT_BOUNDARY_PROTECT", raw)
+    with pytest.raises(ValueError):
+        vp.boundary_protect_mode()
+
+
+def test_boundary_layer_impl_modes(monkeypatch):
+    mk = lambda: vp.FusedTurboQuantV1Impl(32, 128, 0.1, 8, kv_cache_dtype="auto")
+    monkeypatch.setenv("TURBOQUANT_BOUNDARY_PROTECT", "1")   # default: raw fp16 slots
+    im = mk()
+    assert im._is_raw and im.preset == "raw_fp16" and not im.v_rotate
+    monkeypatch.setenv("TURBOQUANT_BOUNDARY_PROTECT", "3")   # TurboQuant codes at 3 bits in the fp16 slot
+    im = mk()
+    assert not im._is_raw and (im.key_bits, im.value_bits) == (3, 3)
+    for m in ("fp8", "8", "0"):
+        monkeypatch.setenv("TURBOQUANT_BOUNDARY_PROTECT", m)
+        with pytest.raises(NotImplementedError):
+            mk()
+    monkeypatch.setenv("TURBOQUANT_BOUNDARY_PROTECT", "fp16")
+    with pytest.raises(ValueError):  # raw decode kernel: GQA group <= 8
+        vp.FusedTurboQuantV1Impl(32, 128, 0.1, 2, kv_cache_dtype="bfloat16")
+    # the boundary layer's slot (bf16 elements) holds K|V in fp16: 4 * head_size bytes
+    assert B.get_kv_cache_shape(10, 16, 8, 128, "auto")[-1] * 2 == 4 * 128
