@@ -36,12 +36,12 @@ HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, AMD published
 # (FETCH x2.0, WRITE x1.0); the summaries are in profiles/hbm_traffic_counters.md.
 # Keyed by roofline entry; None where no counter run covers the kernel.
 TRAFFIC_BYTES: dict = {
-    "encode_d128_3bit": 80316450,
-    "encode_d256_3bit": 160081395,
-    "decode_d128_3bit_f32": 149026181,
-    "paged_attn_config3": 224276668,
-    "v1_attn_config4": 406898134,
-    "raw_attn_boundary": None,
+    "encode_d128_3bit": 80336999,
+    "encode_d256_3bit": 160155422,
+    "decode_d128_3bit_f32": 149015748,
+    "paged_attn_config3": 224235776,
+    "v1_attn_config4": 406842573,
+    "raw_attn_boundary": 1084918363,
 }
 
 
