@@ -37,15 +37,22 @@ __device__ __forceinline__ uint32_t field_off(const uint32_t (&w)[N], int P, int
   return (w[0] << (SH - P)) & m;
 }
 
+// Reductions over the four lanes l, l ^ 16, l ^ 32, l ^ 48 (the 16-lane rows):
+// v_permlane16_swap (x, x) leaves rows (0, 0, 2, 2) in one result and
+// (1, 1, 3, 3) in the other, v_permlane32_swap pairs row r with row r ^ 2.
+// Each stage combines the same two values in every lane of a pair, so all
+// four lanes end with the same bits.
 __device__ __forceinline__ float warp_max_q(float x) {
-  x = fmaxf(x, __shfl_xor(x, 16));
-  x = fmaxf(x, __shfl_xor(x, 32));
-  return x;
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 __device__ __forceinline__ float warp_sum_q(float x) {
-  x += __shfl_xor(x, 16);
-  x += __shfl_xor(x, 32);
-  return x;
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
 }  // namespace ftq

@@ -175,10 +175,12 @@ __global__ __launch_bounds__(256) void paged_store_kernel(
 // e of copy c sits at dword e * 32 + c, and lane l reads copy l % 32, so every
 // lane of a phase hits its own bank.  (2-bit tables have 16 entries and are
 // conflict-free as they are; 4-bit tables keep one 256-entry copy.)
+// Looking codes up through a register table with ds_bpermute_b32 instead
+// (one shift per pair, no address add) measured slower on gfx950: the
+// permute's throughput is below a conflict-free ds_read_b32's.
 template <int B>
 struct CodeLut {
-  static constexpr int CODES = 2;
-  static constexpr int IDX_BITS = CODES * B;
+  static constexpr int IDX_BITS = 2 * B;
   static constexpr int ENTRIES = 1 << IDX_BITS;
   static constexpr int LOG_COPIES = (B == 3) ? 5 : 0;
   static constexpr int COPIES = 1 << LOG_COPIES;
@@ -197,14 +199,19 @@ __device__ void build_code_lut(uint8_t* lut, const uint16_t* single, int tid, in
   }
 }
 
-// LDS byte address of this lane's copy of a code table
+typedef __attribute__((address_space(3))) const uint32_t lds_u32;
+
+// LDS address of a __shared__ object
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
+}
+
+// LDS address of this lane's copy of a code table
 template <int B>
 __device__ __forceinline__ uint32_t lut_lane_base(int lane, uint32_t table_addr) {
   return table_addr + (((uint32_t)lane & (CodeLut<B>::COPIES - 1u)) << 2);
 }
 
-// dequantise the 4 codes at bits [P, P + 4B) into two f16x2 dwords; the
-// address of each is one shift and one and-or
 // Byte offset of the table entry whose index is bits [P, P + W) of the code
 // words: (field << SH) + base, as v_bfe_u32 + v_lshl_add_u32 (LLVM would
 // otherwise split it into shift, and, add).  A field across two words first
@@ -223,14 +230,8 @@ __device__ __forceinline__ uint32_t lut_entry_off(const uint32_t (&w)[N], int P,
   return r;
 }
 
-typedef __attribute__((address_space(3))) const uint32_t lds_u32;
-
-// LDS address of a __shared__ object
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
-}
-
-// base = LDS address of this lane's copy of the table (lds_addr(table) | copy)
+// dequantise the 4 codes at bits [P, P + 4B) into two f16x2 dwords;
+// base = LDS address of this lane's copy of the table
 template <int B, int N>
 __device__ __forceinline__ uint2 lut_quad(const uint32_t (&w)[N], int P, uint32_t base) {
   using C = CodeLut<B>;
@@ -250,30 +251,83 @@ struct TileRegs {
   bool ok[2];         // wave-uniform: sub-block holds real tokens
 };
 
+// Page of sub-block j (16 tokens) of a sequence as a multiply-high:
+// (2j * m) >> 32 with m = ceil(2^31 / nsub) equals floor(j / nsub) whenever
+// j * nsub < 2^31, and always when nsub is a power of two (m is then exact).
+// Only sub-blocks of the block table (j < j_cap = max_blocks * nsub) are
+// divided, and the launcher checks j_cap * nsub < 2^31 for other page sizes.
+struct SubDiv {
+  uint32_t m;
+  int nsub, j_cap;
+  __device__ __forceinline__ int page(int j) const { return (int)__umulhi((uint32_t)j << 1, m); }
+};
+
+// Block-table entries of a tile's two sub-blocks, as a vector load issued one
+// tile ahead of the code loads that need them (lane l holds sub-block l & 1;
+// -1 past the split, past seq_len or past the row).  A vector load retires in
+// order, so the wait before the consumer's readlane covers only this load;
+// the table is a buffer (its row), so no lane reads outside it.
+__device__ __forceinline__ int fetch_bt(__amdgpu_buffer_rsrc_t bt_rs, int tile, bool active, int seq_subs,
+                                        const SubDiv& sd, uint32_t lane) {
+  const int j = 2 * tile + (int)(lane & 1u);
+  const bool ok = active && j < seq_subs && j < sd.j_cap;
+  const int page = sd.page(ok ? j : 0);
+  const int v = (int)__builtin_amdgcn_raw_buffer_load_b32(bt_rs, (uint32_t)page * 4u, 0, 0);
+  return ok ? v : -1;
+}
+
+// dwords [I, NDW) at lane offset voff of a buffer, as 16/12/8/4-byte loads
+template <int I = 0, int NDW>
+__device__ __forceinline__ void buf_dwords(__amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t (&w)[NDW]) {
+  typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+  constexpr int R = NDW - I;
+  const uint32_t o = voff + 4u * I;
+  if constexpr (R >= 4) {
+    const uint4 x = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, o, 0, 0));
+    w[I] = x.x; w[I + 1] = x.y; w[I + 2] = x.z; w[I + 3] = x.w;
+    if constexpr (R > 4) buf_dwords<I + 4>(rs, voff, w);
+  } else if constexpr (R == 3) {
+    const u32x3 x = __builtin_bit_cast(u32x3, __builtin_amdgcn_raw_buffer_load_b96(rs, o, 0, 0));
+    w[I] = x.x; w[I + 1] = x.y; w[I + 2] = x.z;
+  } else if constexpr (R == 2) {
+    const uint2 x = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs, o, 0, 0));
+    w[I] = x.x; w[I + 1] = x.y;
+  } else if constexpr (R == 1) {
+    w[I] = __builtin_amdgcn_raw_buffer_load_b32(rs, o, 0, 0);
+  }
+}
+
+// Lane offsets of the tile loads inside one sub-block (fixed for the kernel)
+struct TileOff {
+  uint32_t k, v, n;  // K codes, V codes, K norms (V norms at n + 32)
+};
+
+// Loads of one 32-token tile: per sub-block one wave-uniform buffer descriptor
+// (its base; the byte range ends with the sub-block, so no lane reads past it)
+// plus the lane offsets.
 template <int D, int BK, int BV>
-__device__ __forceinline__ void load_tile(TileRegs<D, BK, BV>& r, const uint8_t* __restrict__ cache,
-                                          const int32_t* __restrict__ bt_row, int tile, int seq_len,
-                                          int page_size, int nsub, int hkv, int kvh, uint32_t lane,
-                                          int max_blocks, int64_t num_blocks, bool active) {
+__device__ __forceinline__ void load_tile(TileRegs<D, BK, BV>& r, const uint8_t* __restrict__ cache, int btv,
+                                          int tile, const SubDiv& sd, int64_t blk_stride, int64_t kvh_off,
+                                          int nb32, const TileOff& lo) {
   using Gm = PagedGeom<D, BK, BV>;
-  const uint32_t t = lane & 15u, q = lane >> 4;
 #pragma unroll
   for (int sb = 0; sb < 2; ++sb) {
-    // tile, page, block id and base are wave-uniform (scalar).  An inactive or
-    // invalid sub-block (past seq_len, or a bad block id) reads block 0 instead
+    // block id and base are wave-uniform (scalar).  An inactive or invalid
+    // sub-block (past seq_len, or a bad block id) reads block 0 instead
     // (always issuing the loads keeps the wait counts static) and is flagged so
     // the consumer zeroes its V norms; its scores are masked to -inf there too.
-    const int tok0 = tile * 32 + sb * 16;
-    const int page = tok0 / page_size;
-    int64_t phys = (active && tok0 < seq_len && page < max_blocks) ? (int64_t)bt_row[page] : -1;
-    const bool valid = phys >= 0 && phys < num_blocks;
+    int phys = __builtin_amdgcn_readlane(btv, sb);
+    const bool valid = (uint32_t)phys < (uint32_t)nb32;  // -1 (no entry) and ids >= num_blocks fail
+    const int j = 2 * tile + sb;
+    const int sub = valid ? j - sd.page(j) * sd.nsub : 0;
     if (!valid) phys = 0;
-    const int sub = valid ? (tok0 % page_size) >> 4 : 0;
-    const uint8_t* base = cache + ((phys * hkv + kvh) * nsub + sub) * (int64_t)Gm::SUB;
-    load_dwords(base + (t * (uint32_t)Gm::KTOK + q * (uint32_t)Gm::KLANE), r.k[sb]);
-    load_dwords(base + ((uint32_t)Gm::KSEC + lane * (uint32_t)Gm::VLANE), r.v[sb]);
-    load_dwords(base + ((uint32_t)Gm::KNORM + q * 8u), r.kn[sb]);
-    load_dwords(base + ((uint32_t)Gm::VNORM + q * 8u), r.vn[sb]);
+    const uint8_t* base = cache + ((int64_t)phys * blk_stride + kvh_off + (int64_t)sub * Gm::SUB);
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(base), (short)0, Gm::SUB, 0x00020000);
+    buf_dwords(rs, lo.k, r.k[sb]);
+    buf_dwords(rs, lo.v, r.v[sb]);
+    buf_dwords(rs, lo.n, r.kn[sb]);
+    buf_dwords(rs, lo.n + 32u, r.vn[sb]);
     r.ok[sb] = valid;
   }
 }
@@ -290,8 +344,10 @@ __host__ __device__ constexpr int paged_attn_lds(int G) {
   return m > qs ? m : qs;
 }
 
+// d = 128: 4 workgroups per CU (<= 128 VGPRs); d = 256 holds twice the
+// accumulators and tile registers and runs 2 per CU (<= 256 VGPRs, no spills)
 template <int D, int BK, int BV, int QT, bool SHARE>
-__global__ __launch_bounds__(256, 4) void paged_attn_kernel(
+__global__ __launch_bounds__(256, D == 128 ? 4 : 2) void paged_attn_kernel(
     const void* __restrict__ query, const uint8_t* __restrict__ cache,
     const int32_t* __restrict__ block_table, const int32_t* __restrict__ seq_lens, int hq, int hkv,
     int page_size, int max_blocks, int64_t num_blocks, const float* __restrict__ ksigns,
@@ -358,17 +414,26 @@ __global__ __launch_bounds__(256, 4) void paged_attn_kernel(
   build_code_lut<BK>(lutK, lev16[0], tid, 256);
   if (!SHARE) build_code_lut<BV>(lutV, lev16[1], tid, 256);
   __syncthreads();
+  const uint32_t tabK = lut_lane_base<BK>(lane, lds_addr(lutK));
+  const uint32_t tabV = lut_lane_base<BV>(lane, lds_addr(lutV));
 
   const int seq_len = seq_lens[b];
   const int n_tiles = (seq_len + 31) >> 5;
   const int tps = (n_tiles + num_splits - 1) / num_splits;
   const int t_begin = split * tps;
   const int t_end = min(t_begin + tps, n_tiles);
-  const int nsub = page_size >> 4;
-  const int32_t* bt_row = block_table + (int64_t)b * max_blocks;
+  SubDiv sd;
+  sd.nsub = page_size >> 4;
+  sd.m = (0x80000000u + (uint32_t)sd.nsub - 1u) / (uint32_t)sd.nsub;
+  sd.j_cap = (int)min((int64_t)max_blocks * sd.nsub, (int64_t)0x7fffffff);
+  const int seq_subs = (int)(((int64_t)seq_len + 15) >> 4);
+  const int nb32 = (int)min(num_blocks, (int64_t)0x7fffffff);
+  const int64_t blk_stride = (int64_t)hkv * sd.nsub * Gm::SUB;
+  const int64_t kvh_off = (int64_t)kvh * sd.nsub * Gm::SUB;
+  const __amdgpu_buffer_rsrc_t bt_rs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<int32_t*>(block_table + (int64_t)b * max_blocks), (short)0,
+      (int)min((int64_t)max_blocks * 4, (int64_t)0x7ffffffc), 0x00020000);
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);  // wave-uniform -> scalar tile math
-  const uint32_t baseK = lut_lane_base<BK>(lane, lds_addr(lutK));
-  const uint32_t baseV = lut_lane_base<BV>(lane, lds_addr(lutV));
 
   float m_run = -INFINITY, l_run = 0.f;
   floatx4 acc[NB];
@@ -389,8 +454,8 @@ __global__ __launch_bounds__(256, 4) void paged_attn_kernel(
 #pragma unroll
       for (int st = 0; st < NS; ++st) {
         Op8 a;
-        const uint2 c01 = lut_quad<BK>(cur.k[sb], (8 * st) * BK, baseK);
-        const uint2 c23 = lut_quad<BK>(cur.k[sb], (8 * st + 4) * BK, baseK);
+        const uint2 c01 = lut_quad<BK>(cur.k[sb], (8 * st) * BK, tabK);
+        const uint2 c23 = lut_quad<BK>(cur.k[sb], (8 * st + 4) * BK, tabK);
         a.u[0] = c01.x; a.u[1] = c01.y; a.u[2] = c23.x; a.u[3] = c23.y;
         c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a.h, qb[st].h, c, 0, 0, 0);
       }
@@ -445,7 +510,7 @@ __global__ __launch_bounds__(256, 4) void paged_attn_kernel(
       Op8 a;
 #pragma unroll
       for (int sb = 0; sb < 2; ++sb) {
-        const uint2 t4 = lut_quad<BV>(cur.v[sb], (4 * bb) * BV, baseV);
+        const uint2 t4 = lut_quad<BV>(cur.v[sb], (4 * bb) * BV, tabV);
         a.u[2 * sb] = t4.x;
         a.u[2 * sb + 1] = t4.y;
       }
@@ -454,15 +519,34 @@ __global__ __launch_bounds__(256, 4) void paged_attn_kernel(
   };
 
   // ping-pong over two register sets so the next tile's loads overlap this tile's math
+  // and the block-table entries one tile further ahead
   TileRegs<D, BK, BV> ra, rb;
   int tile = t_begin + wave_u;
-  if (tile < t_end) load_tile(ra, cache, bt_row, tile, seq_len, page_size, nsub, hkv, kvh, (uint32_t)lane, max_blocks, num_blocks, true);
+  auto bt_of = [&](int t) __attribute__((always_inline)) {
+    return fetch_bt(bt_rs, t, t < t_end, seq_subs, sd, (uint32_t)lane);
+  };
+  TileOff lo;
+  lo.k = (uint32_t)h * Gm::KTOK + (uint32_t)q * Gm::KLANE;
+  lo.v = (uint32_t)Gm::KSEC + (uint32_t)lane * Gm::VLANE;
+  lo.n = (uint32_t)Gm::KNORM + (uint32_t)q * 8u;
+  auto load = [&](TileRegs<D, BK, BV>& r, int btv, int t) __attribute__((always_inline)) {
+    load_tile(r, cache, btv, t, sd, blk_stride, kvh_off, nb32, lo);
+  };
+  int btv = 0;
+  if (tile < t_end) {
+    load(ra, bt_of(tile), tile);
+    btv = bt_of(tile + 4);
+  }
   while (tile < t_end) {
-    load_tile(rb, cache, bt_row, tile + 4, seq_len, page_size, nsub, hkv, kvh, (uint32_t)lane, max_blocks, num_blocks, tile + 4 < t_end);
+    int btn = bt_of(tile + 8);
+    load(rb, btv, tile + 4);
+    btv = btn;
     process(ra, tile);
     tile += 4;
     if (tile >= t_end) break;
-    load_tile(ra, cache, bt_row, tile + 4, seq_len, page_size, nsub, hkv, kvh, (uint32_t)lane, max_blocks, num_blocks, tile + 4 < t_end);
+    btn = bt_of(tile + 8);
+    load(ra, btv, tile + 4);
+    btv = btn;
     process(rb, tile);
     tile += 4;
   }
@@ -682,6 +766,11 @@ extern "C" int ftq_paged_decode_attention(
   FTQ_REQUIRE(num_q_heads / num_kv_heads <= 16, "GQA group (num_q_heads / num_kv_heads) must be <= 16");
   FTQ_REQUIRE(num_splits >= 1 && num_splits <= 1024, "num_splits must be in [1, 1024]");
   FTQ_REQUIRE(max_blocks_per_seq >= 0, "max_blocks_per_seq must be >= 0");
+  {
+    const int64_t nsub = page_size / 16;
+    FTQ_REQUIRE((nsub & (nsub - 1)) == 0 || (int64_t)max_blocks_per_seq * nsub * nsub < ((int64_t)1 << 31),
+                "max_blocks_per_seq * (page_size / 16)^2 must be below 2^31 when page_size / 16 is not a power of two");
+  }
   FTQ_REQUIRE(q_dtype >= F32 && q_dtype <= BF16 && out_dtype >= F32 && out_dtype <= BF16,
               "dtype must be FTQ_F32, FTQ_F16 or FTQ_BF16");
   if (batch == 0) return FTQ_OK;
