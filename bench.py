@@ -11,8 +11,9 @@ Also timed (not part of the step): the d=256 encode and the d=128 decode of
 config 2, config 4 (vLLM v1 slot format, K4V2, v_rotate, B=4, contexts
 U[65536, 131072]) and the boundary-layer raw fp16 decode attention at the
 config-3 shape (512-byte K|V slots, 1.07 GB).  Every kernel gets a roofline entry: algorithmic bytes per
-launch / average launch time, from HIP events on the stream the library
-launches on (torch's current stream).
+launch / launch time, from HIP events on the stream the library launches on
+(torch's current stream), in steady state: 20 untimed launches, then the
+median of three windows of back-to-back launches.
 
 Prints ONE JSON line.
 """
@@ -49,18 +50,24 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-def time_launches(fn, iters, torch):
-    """Average device time of one fn() call, from HIP events on the current stream."""
+def time_launches(fn, iters, torch, warm=20, windows=3):
+    """Device time of one fn() call in steady state, from HIP events on the
+    current stream: `warm` untimed launches (clocks settle), then the median
+    over `windows` windows of `iters` back-to-back launches."""
     st = torch.cuda.current_stream()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    fn()
-    e0.record(st)
-    for _ in range(iters):
+    for _ in range(warm):
         fn()
-    e1.record(st)
-    e1.synchronize()
-    return e0.elapsed_time(e1) * 1e3 / iters  # us
+    per = []
+    for _ in range(windows):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(st)
+        for _ in range(iters):
+            fn()
+        e1.record(st)
+        e1.synchronize()
+        per.append(e0.elapsed_time(e1) * 1e3 / iters)  # us
+    return sorted(per)[len(per) // 2]
 
 
 def lean_launch(fn, keep, *args):

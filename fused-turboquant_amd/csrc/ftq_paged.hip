@@ -241,6 +241,47 @@ __device__ __forceinline__ uint2 lut_quad(const uint32_t (&w)[N], int P, uint32_
   return make_uint2(lo, hi);
 }
 
+
+// Schedule of a run of NM MFMAs whose A operands come from RD table reads
+// each: the reads of MFMA i+1 issue before MFMA i waits for its own (a
+// two-deep LDS pipeline; left alone, the scheduler waits for every read).
+template <int NM, int RD>
+__device__ __forceinline__ void sched_lds_mfma() {
+  __builtin_amdgcn_sched_group_barrier(0x100, RD, 0);
+#pragma unroll
+  for (int i = 0; i < NM - 1; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x100, RD, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+  }
+  __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+}
+
+// max without the NaN canonicalisation fmaxf carries (scores are finite or -inf)
+__device__ __forceinline__ float vmax(float a, float b) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+__device__ __forceinline__ float vmax3(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+// max over lanes l, l^16, l^32, l^48
+__device__ __forceinline__ float row_max4(float x) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = vmax(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return vmax(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+// f16x2 {p0 * vn.lo, p1 * vn.hi}, each product rounded once to f16
+__device__ __forceinline__ uint32_t pv_pair(float p0, float p1, uint32_t vn) {
+  uint32_t r;
+  asm("v_fma_mixlo_f16 %0, %1, %2, 0 op_sel_hi:[0,1,0]\n\t"
+      "v_fma_mixhi_f16 %0, %3, %2, 0 op_sel:[0,1,0] op_sel_hi:[0,1,0]"
+      : "=&v"(r) : "v"(p0), "v"(vn), "v"(p1));
+  return r;
+}
 template <int D, int BK, int BV>
 struct TileRegs {
   using Gm = PagedGeom<D, BK, BV>;
@@ -332,27 +373,56 @@ __device__ __forceinline__ void load_tile(TileRegs<D, BK, BV>& r, const uint8_t*
   }
 }
 
-// LDS bytes of one paged_attn_kernel workgroup for a GQA group of G heads:
-// one pool reused for the rotated queries (prologue), the code tables (tile
-// loop) and the wave-merge buffer (epilogue)
-template <int D, int BK, int BV, bool SHARE>
+// LDS bytes of one paged_attn_kernel workgroup of NW waves for a GQA group of
+// G heads: one pool reused for the rotated queries (prologue), the code tables
+// (tile loop) and the wave-merge buffer (epilogue)
+template <int D, int BK, int BV, bool SHARE, int NW>
 __host__ __device__ constexpr int paged_attn_lds(int G) {
   const int lut = CodeLut<BK>::BYTES + (SHARE ? 0 : CodeLut<BV>::BYTES);
-  const int red = 4 * G * (D + 1) * 4;
+  const int red = NW * G * (D + 1) * 4;
   const int qs = G * (D + 8) * 2;
   const int m = lut > red ? lut : red;
   return m > qs ? m : qs;
 }
 
-// d = 128: 4 workgroups per CU (<= 128 VGPRs); d = 256 holds twice the
-// accumulators and tile registers and runs 2 per CU (<= 256 VGPRs, no spills)
-template <int D, int BK, int BV, int QT, bool SHARE>
-__global__ __launch_bounds__(256, D == 128 ? 4 : 2) void paged_attn_kernel(
+// Output of a finished (batch, q head) row: o / L, inverse RHT of V
+// (unnormalised FWHT, times the 1/sqrt(d) scale and the signs), the output
+// dtype; lane l of the wave holds elements [E l, E l + E).  L == 0 (no token
+// attended) writes zeros.
+template <int D>
+__device__ __forceinline__ void finish_row(float (&y)[D / 64], float L, const float* __restrict__ vsigns,
+                                           float scale, int lane, void* __restrict__ out, int ot, int64_t row) {
+  constexpr int E = D / 64;
+  const float inv = (L > 0.f) ? 1.f / L : 0.f;
+#pragma unroll
+  for (int i = 0; i < E; ++i) y[i] *= inv;
+  fwht_wave64<E>(y, lane);
+#pragma unroll
+  for (int i = 0; i < E; ++i) y[i] = y[i] * scale * vsigns[lane * E + i];
+  if (ot == F32) store_small<F32, E>(out, row * D + lane * E, y);
+  else if (ot == F16) store_small<F16, E>(out, row * D + lane * E, y);
+  else store_small<BF16, E>(out, row * D + lane * E, y);
+}
+
+// One workgroup per (split, kv head, batch) with NW waves.
+//   NW = 4: the split form.  Each workgroup writes its split's partial
+//     output (divided by its own softmax sum) and log2-sum-exp to the
+//     workspace; merge_splits_kernel combines the splits.  d = 128 runs 4
+//     workgroups per CU (<= 128 VGPRs); d = 256 holds twice the accumulators
+//     and tile registers and runs 2 per CU (<= 256 VGPRs, no spills).
+//   NW = 16 (d = 128, G <= 4, one split): the whole sequence in one workgroup
+//     of 4 waves per SIMD (<= 128 VGPRs).  The waves merge in LDS and the
+//     workgroup writes the output itself (inverse RHT, output dtype): no
+//     workspace and no second launch.
+template <int D, int BK, int BV, int QT, bool SHARE, int NW>
+__global__ __launch_bounds__(NW * 64, NW == 16 ? 1 : (D == 128 ? 4 : 2)) void paged_attn_kernel(
     const void* __restrict__ query, const uint8_t* __restrict__ cache,
     const int32_t* __restrict__ block_table, const int32_t* __restrict__ seq_lens, int hq, int hkv,
     int page_size, int max_blocks, int64_t num_blocks, const float* __restrict__ ksigns,
     const float* __restrict__ klev, const float* __restrict__ vlev, float qscale, int num_splits,
-    float* __restrict__ ws_o, float* __restrict__ ws_lse) {
+    float* __restrict__ ws_o, float* __restrict__ ws_lse, const float* __restrict__ vsigns, float vscale,
+    void* __restrict__ out, int ot) {
+  static_assert(NW == 4 || (NW == 16 && D == 128), "4 waves, or 16 waves at d = 128");
   using Gm = PagedGeom<D, BK, BV>;
   constexpr int NS = Gm::NS, NB = Gm::NB;
   constexpr int E = D / 16;
@@ -366,10 +436,10 @@ __global__ __launch_bounds__(256, D == 128 ? 4 : 2) void paged_attn_kernel(
   // (epilogue)
   constexpr int LUTK_BYTES = CodeLut<BK>::BYTES;
   extern __shared__ __attribute__((aligned(16))) uint8_t pool[];
-  __shared__ float red_m[4][16], red_l[4][16];
+  __shared__ float red_m[NW][16], red_l[NW][16];
   __shared__ uint16_t lev16[2][16];  // fp16 K / V levels
   _Float16 (*qs)[D + 8] = reinterpret_cast<_Float16 (*)[D + 8]>(pool);
-  float* red_o = reinterpret_cast<float*>(pool);  // [4 waves][G heads][D + 1]
+  float* red_o = reinterpret_cast<float*>(pool);  // [NW waves][G heads][D + 1]
   uint8_t* lutK = pool;
   uint8_t* lutV = SHARE ? pool : pool + LUTK_BYTES;
 
@@ -411,8 +481,8 @@ __global__ __launch_bounds__(256, D == 128 ? 4 : 2) void paged_attn_kernel(
     }
   }
   __syncthreads();  // qs is dead from here on; its LDS holds the code tables
-  build_code_lut<BK>(lutK, lev16[0], tid, 256);
-  if (!SHARE) build_code_lut<BV>(lutV, lev16[1], tid, 256);
+  build_code_lut<BK>(lutK, lev16[0], tid, NW * 64);
+  if (!SHARE) build_code_lut<BV>(lutV, lev16[1], tid, NW * 64);
   __syncthreads();
   const uint32_t tabK = lut_lane_base<BK>(lane, lds_addr(lutK));
   const uint32_t tabV = lut_lane_base<BV>(lane, lds_addr(lutV));
@@ -465,6 +535,7 @@ __global__ __launch_bounds__(256, D == 128 ? 4 : 2) void paged_attn_kernel(
         s[sb][i] = __builtin_fmaf(c[i], (float)kn, 0.f);
       }
     }
+    if constexpr (BK <= 3 && BV <= 3) sched_lds_mfma<2 * NS, 4>();  // (4-bit tables: registers run out)
     if (tile * 32 + 32 > seq_len) {  // only the last tile of a sequence is partial
 #pragma unroll
       for (int sb = 0; sb < 2; ++sb)
@@ -472,9 +543,10 @@ __global__ __launch_bounds__(256, D == 128 ? 4 : 2) void paged_attn_kernel(
         for (int i = 0; i < 4; ++i)
           if (tile * 32 + sb * 16 + 4 * q + i >= seq_len) s[sb][i] = -INFINITY;
     }
-    float tmax = fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
-                       fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
-    tmax = warp_max_q(tmax);
+    float tmax = vmax3(s[0][0], s[0][1], s[0][2]);
+    tmax = vmax3(tmax, s[0][3], s[1][0]);
+    tmax = vmax3(tmax, s[1][1], s[1][2]);
+    tmax = row_max4(vmax(tmax, s[1][3]));
     if (__builtin_amdgcn_ballot_w64(tmax > m_run + TAU) != 0) {  // wave-uniform, rare
       const float m_new = fmaxf(m_run, tmax);
       const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
@@ -485,7 +557,7 @@ __global__ __launch_bounds__(256, D == 128 ? 4 : 2) void paged_attn_kernel(
     }
     // p is taken pre-scaled by 2^-(TAU+1) (folded into the exponent); l gets it back
     const float m_sc = m_run + (TAU + 1.f);
-    float psum = 0.f;
+    float pr[8];
     Op8 pb;
 #pragma unroll
     for (int sb = 0; sb < 2; ++sb) {
@@ -493,16 +565,15 @@ __global__ __launch_bounds__(256, D == 128 ? 4 : 2) void paged_attn_kernel(
       for (int i2 = 0; i2 < 2; ++i2) {
         // V norms of two tokens as f16 halves (zero for a flagged sub-block);
         // the products are rounded straight into the two halves of the operand
-        const half2_t vn = __builtin_bit_cast(half2_t, cur.ok[sb] ? cur.vn[sb][i2] : 0u);
+        const uint32_t vn = cur.ok[sb] ? cur.vn[sb][i2] : 0u;
         const float p0 = __builtin_amdgcn_exp2f(s[sb][2 * i2] - m_sc);
         const float p1 = __builtin_amdgcn_exp2f(s[sb][2 * i2 + 1] - m_sc);
-        psum += p0;
-        psum += p1;
-        const half2_t pv = {(_Float16)__builtin_fmaf(p0, (float)vn[0], 0.f),
-                            (_Float16)__builtin_fmaf(p1, (float)vn[1], 0.f)};
-        pb.u[2 * sb + i2] = __builtin_bit_cast(uint32_t, pv);
+        pr[4 * sb + 2 * i2] = p0;
+        pr[4 * sb + 2 * i2 + 1] = p1;
+        pb.u[2 * sb + i2] = pv_pair(p0, p1, vn);
       }
     }
+    float psum = ((pr[0] + pr[1]) + (pr[2] + pr[3])) + ((pr[4] + pr[5]) + (pr[6] + pr[7]));
     psum *= 512.f;
     l_run += psum;
 #pragma unroll
@@ -516,6 +587,7 @@ __global__ __launch_bounds__(256, D == 128 ? 4 : 2) void paged_attn_kernel(
       }
       acc[bb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a.h, pb.h, acc[bb], 0, 0, 0);
     }
+    if constexpr (BK <= 3 && BV <= 3) sched_lds_mfma<NB, 4>();
   };
 
   // ping-pong over two register sets so the next tile's loads overlap this tile's math
@@ -535,20 +607,20 @@ __global__ __launch_bounds__(256, D == 128 ? 4 : 2) void paged_attn_kernel(
   int btv = 0;
   if (tile < t_end) {
     load(ra, bt_of(tile), tile);
-    btv = bt_of(tile + 4);
+    btv = bt_of(tile + NW);
   }
   while (tile < t_end) {
-    int btn = bt_of(tile + 8);
-    load(rb, btv, tile + 4);
+    int btn = bt_of(tile + 2 * NW);
+    load(rb, btv, tile + NW);
     btv = btn;
     process(ra, tile);
-    tile += 4;
+    tile += NW;
     if (tile >= t_end) break;
-    btn = bt_of(tile + 8);
-    load(ra, btv, tile + 4);
+    btn = bt_of(tile + 2 * NW);
+    load(ra, btv, tile + NW);
     btv = btn;
     process(rb, tile);
-    tile += 4;
+    tile += NW;
   }
   // undo the P' pre-scale
 #pragma unroll
@@ -570,24 +642,48 @@ __global__ __launch_bounds__(256, D == 128 ? 4 : 2) void paged_attn_kernel(
   }
   __syncthreads();
 
-  const int64_t row0 = ((int64_t)b * hq + kvh * G) * num_splits + split;  // (b, head g=0, split)
-  for (int idx = tid; idx < G * D; idx += 256) {
-    const int g = idx / D, d = idx % D;
-    float M = -INFINITY;
+  if constexpr (NW == 16) {
+    // wave g < G finishes q head g: lane l combines elements [E2 l, E2 l + E2)
+    if (wave < G) {
+      constexpr int E2 = D / 64;
+      const int g = wave;
+      float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) M = fmaxf(M, red_m[w][g]);
-    float L = 0.f, o = 0.f;
-    if (M != -INFINITY) {
+      for (int w = 0; w < NW; ++w) M = fmaxf(M, red_m[w][g]);
+      float L = 0.f, y[E2];
 #pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const float f = __builtin_amdgcn_exp2f(red_m[w][g] - M);
-        L += f * red_l[w][g];
-        o += f * red_o[(w * G + g) * (D + 1) + d];
+      for (int i = 0; i < E2; ++i) y[i] = 0.f;
+      if (M != -INFINITY) {
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+          const float f = __builtin_amdgcn_exp2f(red_m[w][g] - M);
+          L += f * red_l[w][g];
+#pragma unroll
+          for (int i = 0; i < E2; ++i) y[i] += f * red_o[(w * G + g) * (D + 1) + lane * E2 + i];
+        }
       }
+      finish_row<D>(y, L, vsigns, vscale, lane, out, ot, (int64_t)b * hq + kvh * G + g);
     }
-    const int64_t row = row0 + (int64_t)g * num_splits;
-    ws_o[row * D + d] = (L > 0.f) ? o / L : 0.f;
-    if (d == 0) ws_lse[row] = (L > 0.f) ? M + __builtin_log2f(L) : -INFINITY;
+  } else {
+    const int64_t row0 = ((int64_t)b * hq + kvh * G) * num_splits + split;  // (b, head g=0, split)
+    for (int idx = tid; idx < G * D; idx += NW * 64) {
+      const int g = idx / D, d = idx % D;
+      float M = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) M = fmaxf(M, red_m[w][g]);
+      float L = 0.f, o = 0.f;
+      if (M != -INFINITY) {
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+          const float f = __builtin_amdgcn_exp2f(red_m[w][g] - M);
+          L += f * red_l[w][g];
+          o += f * red_o[(w * G + g) * (D + 1) + d];
+        }
+      }
+      const int64_t row = row0 + (int64_t)g * num_splits;
+      ws_o[row * D + d] = (L > 0.f) ? o / L : 0.f;
+      if (d == 0) ws_lse[row] = (L > 0.f) ? M + __builtin_log2f(L) : -INFINITY;
+    }
   }
 }
 
@@ -652,16 +748,33 @@ struct AttnArgs {
   int ot;
 };
 
+// the single-workgroup form applies: d = 128, GQA group <= 4, one split
+static bool fused_form(int d, int hq, int hkv, int splits) {
+  return d == 128 && hq / hkv <= 4 && splits == 1;
+}
+
+template <int D, int BK, int BV, bool SHARE, int NW>
+static void launch_attn_nw(const AttnArgs& a, hipStream_t st) {
+  dim3 grid(a.splits, a.hkv, a.B), block(NW * 64);
+  const size_t lds = (size_t)paged_attn_lds<D, BK, BV, SHARE, NW>(a.hq / a.hkv);
+  const float sc = fwht_scale(D);
+  if (a.qt == F32)
+    paged_attn_kernel<D, BK, BV, F32, SHARE, NW><<<grid, block, lds, st>>>(a.q, a.cache, a.bt, a.sl, a.hq, a.hkv, a.page_size, a.max_blocks, a.num_blocks, a.ks, a.kl, a.vl, a.qscale, a.splits, a.wo, a.wl, a.vs, sc, a.out, a.ot);
+  else if (a.qt == F16)
+    paged_attn_kernel<D, BK, BV, F16, SHARE, NW><<<grid, block, lds, st>>>(a.q, a.cache, a.bt, a.sl, a.hq, a.hkv, a.page_size, a.max_blocks, a.num_blocks, a.ks, a.kl, a.vl, a.qscale, a.splits, a.wo, a.wl, a.vs, sc, a.out, a.ot);
+  else
+    paged_attn_kernel<D, BK, BV, BF16, SHARE, NW><<<grid, block, lds, st>>>(a.q, a.cache, a.bt, a.sl, a.hq, a.hkv, a.page_size, a.max_blocks, a.num_blocks, a.ks, a.kl, a.vl, a.qscale, a.splits, a.wo, a.wl, a.vs, sc, a.out, a.ot);
+}
+
 template <int D, int BK, int BV, bool SHARE>
 static void launch_attn_kernel(const AttnArgs& a, hipStream_t st) {
-  dim3 grid(a.splits, a.hkv, a.B), block(256);
-  const size_t lds = (size_t)paged_attn_lds<D, BK, BV, SHARE>(a.hq / a.hkv);
-  if (a.qt == F32)
-    paged_attn_kernel<D, BK, BV, F32, SHARE><<<grid, block, lds, st>>>(a.q, a.cache, a.bt, a.sl, a.hq, a.hkv, a.page_size, a.max_blocks, a.num_blocks, a.ks, a.kl, a.vl, a.qscale, a.splits, a.wo, a.wl);
-  else if (a.qt == F16)
-    paged_attn_kernel<D, BK, BV, F16, SHARE><<<grid, block, lds, st>>>(a.q, a.cache, a.bt, a.sl, a.hq, a.hkv, a.page_size, a.max_blocks, a.num_blocks, a.ks, a.kl, a.vl, a.qscale, a.splits, a.wo, a.wl);
-  else
-    paged_attn_kernel<D, BK, BV, BF16, SHARE><<<grid, block, lds, st>>>(a.q, a.cache, a.bt, a.sl, a.hq, a.hkv, a.page_size, a.max_blocks, a.num_blocks, a.ks, a.kl, a.vl, a.qscale, a.splits, a.wo, a.wl);
+  if constexpr (D == 128) {
+    if (fused_form(D, a.hq, a.hkv, a.splits)) {
+      launch_attn_nw<D, BK, BV, SHARE, 16>(a, st);
+      return;
+    }
+  }
+  launch_attn_nw<D, BK, BV, SHARE, 4>(a, st);
 }
 
 template <int D, int BK, int BV>
@@ -675,6 +788,7 @@ static hipError_t launch_attn3(const AttnArgs& a, hipStream_t st) {
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
+  if (fused_form(D, a.hq, a.hkv, a.splits)) return hipSuccess;  // the kernel wrote the output
   const int64_t rows = (int64_t)a.B * a.hq;
   const float sc = fwht_scale(D);
   if (a.ot == F32) return launch_merge_splits<D, F32, ROT_SIGNS>(a.wo, a.wl, rows, a.splits, a.vs, sc, a.out, st);
@@ -723,6 +837,18 @@ extern "C" int64_t ftq_paged_workspace_bytes(int batch, int num_q_heads, int d, 
 
 extern "C" int ftq_paged_default_splits(int batch, int num_kv_heads, int max_seq_len) {
   return auto_splits(batch, num_kv_heads, max_seq_len, 1024);  // 4 workgroups per CU
+}
+
+extern "C" int ftq_paged_choose_splits(int batch, int num_q_heads, int num_kv_heads, int d, int max_seq_len) {
+  if (batch <= 0 || num_kv_heads <= 0 || num_q_heads <= 0) return 1;
+  // one split when the single-workgroup form applies and its 16-wave
+  // workgroups (one per CU at a time) keep the 256 CUs at least 3/4 busy
+  const int64_t units = (int64_t)batch * num_kv_heads;
+  if (fused_form(d, num_q_heads, num_kv_heads, 1) && units >= 256) {
+    const int64_t rounds = (units + 255) / 256;
+    if (units * 4 >= rounds * 256 * 3) return 1;
+  }
+  return ftq_paged_default_splits(batch, num_kv_heads, max_seq_len);
 }
 
 extern "C" int ftq_paged_store(const void* key, const void* value, int dtype, int64_t n_tokens,

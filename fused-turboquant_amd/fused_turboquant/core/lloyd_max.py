@@ -84,6 +84,7 @@ class LloydMaxQuantizer:
         b, l = _get_cached_codebook(dim, bits, max_iterations, num_grid_points)
         self.boundaries = torch.tensor(b, dtype=torch.float32, device=device)
         self.levels = torch.tensor(l, dtype=torch.float32, device=device)
+        self.levels_host = np.asarray(l, dtype=np.float32)  # host copy (kernel set-up decisions)
         self.codebook_class = codebook_class(np.asarray(b, dtype=np.float32), bits)
 
     def quantize(self, x: torch.Tensor) -> torch.Tensor:

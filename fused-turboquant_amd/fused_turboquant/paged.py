@@ -22,6 +22,7 @@ from __future__ import annotations
 
 import math
 
+import numpy as np
 import torch
 
 from . import _lib
@@ -53,6 +54,8 @@ def _bind():
     L.ftq_paged_workspace_bytes.argtypes = [ctypes.c_int] * 4
     L.ftq_paged_default_splits.restype = ctypes.c_int
     L.ftq_paged_default_splits.argtypes = [ctypes.c_int] * 3
+    L.ftq_paged_choose_splits.restype = ctypes.c_int
+    L.ftq_paged_choose_splits.argtypes = [ctypes.c_int] * 5
     L._paged_bound = True
     return L
 
@@ -96,8 +99,23 @@ def paged_store(key: torch.Tensor, value: torch.Tensor, kv_cache: torch.Tensor,
         nsub * 16, nb, _lib.stream_ptr(dev)))
 
 
-def default_splits(batch: int, num_kv_heads: int, max_seq_len: int) -> int:
+def default_splits(batch: int, num_kv_heads: int, max_seq_len: int, num_q_heads: int | None = None,
+                   head_dim: int | None = None) -> int:
+    """Split factor of the decode: with ``num_q_heads`` and ``head_dim`` it may
+    be 1, the single-launch form (d = 128, GQA group <= 4, batch * Hkv filling
+    the GPU); without them, the split form's own default."""
+    if num_q_heads is not None and head_dim is not None:
+        return int(_bind().ftq_paged_choose_splits(batch, num_q_heads, num_kv_heads, head_dim, max_seq_len))
     return int(_bind().ftq_paged_default_splits(batch, num_kv_heads, max_seq_len))
+
+
+def _levels_pair(k_quant: TurboQuantMSE, v_quant: TurboQuantMSE):
+    """Device pointers of the K and V levels; one pointer for both when the two
+    codebooks are equal (the kernel then builds one shared code table)."""
+    kq, vq = k_quant.quantizer, v_quant.quantizer
+    if kq is vq or (kq.bits == vq.bits and np.array_equal(kq.levels_host, vq.levels_host)):
+        return kq.levels.data_ptr(), kq.levels.data_ptr()
+    return kq.levels.data_ptr(), vq.levels.data_ptr()
 
 
 def workspace_bytes(batch: int, num_q_heads: int, head_dim: int, num_splits: int) -> int:
@@ -132,7 +150,7 @@ def paged_decode_attention(query: torch.Tensor, kv_cache: torch.Tensor, block_ta
         scale = 1.0 / math.sqrt(d)
     if num_splits is None:
         msl = max_seq_len if max_seq_len is not None else block_table.shape[1] * nsub * 16
-        num_splits = default_splits(B, hkv, msl)
+        num_splits = default_splits(B, hkv, msl, hq, d)
     if out is None:
         out = torch.empty(B, hq, d, dtype=q.dtype, device=dev)
     need = workspace_bytes(B, hq, d, num_splits)
@@ -144,7 +162,7 @@ def paged_decode_attention(query: torch.Tensor, kv_cache: torch.Tensor, block_ta
         q.data_ptr(), _lib.dtype_code(q.dtype), kv_cache.data_ptr(), bt.data_ptr(),
         seq_lens.contiguous().data_ptr(), B, hq, hkv, d, nsub * 16, bt.shape[1], nb,
         k_quant.rotation.signs.data_ptr(), v_quant.rotation.signs.data_ptr(),
-        k_quant.quantizer.levels.data_ptr(), v_quant.quantizer.levels.data_ptr(),
+        *_levels_pair(k_quant, v_quant),
         k_quant.bits, v_quant.bits, float(scale), int(num_splits), workspace.data_ptr(),
         workspace.numel(), out.data_ptr(), _lib.dtype_code(out.dtype), _lib.stream_ptr(dev)))
     return out
@@ -260,7 +278,7 @@ def make_config3(dev, B=32, hq=32, hkv=8, d=128, ctx=8192, page=16, bits=3, seed
 def bench_setup(dev):
     B, hq, hkv, d, ctx, page = 32, 32, 8, 128, 8192, 16
     cache, q, bt, sl = make_config3(dev, B, hq, hkv, d, ctx, page)
-    splits = default_splits(B, hkv, ctx)
+    splits = default_splits(B, hkv, ctx, hq, d)
     out = torch.empty(B, hq, d, dtype=torch.bfloat16, device=dev)
     ws = torch.empty(workspace_bytes(B, hq, d, splits), dtype=torch.uint8, device=dev)
 
@@ -274,7 +292,7 @@ def bench_setup(dev):
     kq, vq = cache.k_quant, cache.v_quant
     args = (q.data_ptr(), _lib.dtype_code(q.dtype), kv.data_ptr(), bt.data_ptr(), sl.data_ptr(), B, hq, hkv,
             d, nsub * 16, bt.shape[1], nb, kq.rotation.signs.data_ptr(), vq.rotation.signs.data_ptr(),
-            kq.quantizer.levels.data_ptr(), vq.quantizer.levels.data_ptr(), kq.bits, vq.bits,
+            *_levels_pair(kq, vq), kq.bits, vq.bits,
             1.0 / math.sqrt(d), splits, ws.data_ptr(), ws.numel(), out.data_ptr(), _lib.dtype_code(out.dtype),
             _lib.stream_ptr(dev))
     keep = (cache, q, bt, sl, ws, out)

@@ -122,6 +122,12 @@ int ftq_paged_store(const void* key, const void* value, int dtype, int64_t n_tok
 int64_t ftq_paged_workspace_bytes(int batch, int num_q_heads, int d, int num_splits);
 /* Split-K factor that fills the GPU for this shape (host-side heuristic). */
 int ftq_paged_default_splits(int batch, int num_kv_heads, int max_seq_len);
+/* Split factor for ftq_paged_decode_attention with the head geometry known: 1
+ * (the single-launch form below) when d = 128, Hq/Hkv <= 4 and batch*Hkv fills
+ * the 256 CUs in whole rounds of at least 3/4, else ftq_paged_default_splits.
+ * Host-side heuristic; no counterpart in the reference, whose Triton launch
+ * picks its grid in kernels/triton_flash_decode.py:224-324. */
+int ftq_paged_choose_splits(int batch, int num_q_heads, int num_kv_heads, int d, int max_seq_len);
 
 /*
  * Decode attention (one query token per sequence) over the paged cache:
@@ -133,7 +139,10 @@ int ftq_paged_default_splits(int batch, int num_kv_heads, int max_seq_len);
  * (vllm_plugin/attention_impl.py:431-521: _gather_compressed_k +
  * randomized_hadamard + fused_qk_scores_rht + softmax + V decode + matmul) and
  * flash_decode_compressed (kernels/triton_flash_decode.py:224-324).
- * Two launches on `stream`: split-K stage 1, then merge + inverse RHT.
+ * num_splits == 1 with d = 128 and Hq/Hkv <= 4: one launch on `stream`, one
+ * 16-wave workgroup per (batch, kv head) that merges its waves and writes the
+ * output (inverse RHT, out_dtype); the workspace is not touched.  Otherwise
+ * two launches: split-K stage 1 into the workspace, then merge + inverse RHT.
  */
 int ftq_paged_decode_attention(const void* query, int q_dtype, const uint8_t* kv_cache,
                                const int32_t* block_table, const int32_t* seq_lens, int batch,

@@ -57,11 +57,11 @@ def test_encode_under_graph(cuda):
     _replay_check(cuda, refill, lambda: tq.encode(x).indices, lambda: ct_graph.indices, g, "encode codes")
 
 
-def test_paged_decode_under_graph(cuda):
+@pytest.mark.parametrize("splits", [1, 3])  # single-launch form, split form + merge launch
+def test_paged_decode_under_graph(cuda, splits):
     from fused_turboquant import paged as P
     B, hq, hkv, d, ctx, page = 4, 16, 4, 128, 700, 16
     cache, q, bt, sl = P.make_config3(cuda, B, hq, hkv, d, ctx, page)
-    splits = 3
     out_g = torch.empty(B, hq, d, dtype=torch.bfloat16, device=cuda)
     ws = torch.empty(P.workspace_bytes(B, hq, d, splits), dtype=torch.uint8, device=cuda)
     g = _capture(lambda: P.paged_decode_attention(q, cache.kv_cache, bt, sl, cache.k_quant, cache.v_quant,
@@ -74,7 +74,7 @@ def test_paged_decode_under_graph(cuda):
     def eager():
         return P.paged_decode_attention(q, cache.kv_cache, bt, sl, cache.k_quant, cache.v_quant, num_splits=splits)
 
-    _replay_check(cuda, refill, eager, lambda: out_g, g, "paged decode")
+    _replay_check(cuda, refill, eager, lambda: out_g, g, f"paged decode splits={splits}")
 
 
 def test_v1_decode_under_graph(cuda):

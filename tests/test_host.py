@@ -137,3 +137,20 @@ def test_torch_packers_match_oracle():
         p = pk(torch.from_numpy(c)).numpy()
         assert np.array_equal(p, O.pack(c, bits))
         assert np.array_equal(up(torch.from_numpy(p), 128).numpy(), c)
+
+
+def test_paged_choose_splits_host_heuristic():
+    """ftq_paged_choose_splits: 1 (the single-launch form) only for d = 128,
+    GQA group <= 4 and batch * Hkv filling 256 CUs in rounds at least 3/4 full;
+    otherwise the split form's default."""
+    from fused_turboquant import paged as P
+    L = P._bind()
+    dflt = L.ftq_paged_default_splits
+    assert P.default_splits(32, 8, 8192, 32, 128) == 1       # config 3: 256 workgroups
+    assert P.default_splits(64, 8, 8192, 32, 128) == 1       # two full rounds
+    assert P.default_splits(48, 8, 8192, 32, 128) == 1       # 384 of 512 slots: 3/4
+    assert P.default_splits(40, 8, 8192, 32, 128) == dflt(40, 8, 8192)  # 320 of 512: below 3/4
+    assert P.default_splits(16, 8, 8192, 32, 128) == dflt(16, 8, 8192)  # 128 workgroups: too few
+    assert P.default_splits(32, 8, 8192, 64, 128) == dflt(32, 8, 8192)  # GQA 8
+    assert P.default_splits(32, 8, 8192, 32, 256) == dflt(32, 8, 8192)  # d = 256
+    assert P.default_splits(32, 8, 8192) == dflt(32, 8, 8192)           # geometry unknown

@@ -104,9 +104,10 @@ def test_decode_attention_parity(cuda, bk, bv, hq, hkv):
         err = np.abs(out - ref)
         print(f"[attn bk={bk} bv={bv} hq={hq} hkv={hkv} splits={splits}] max={err.max():.2e} mean={err.mean():.2e}")
         assert err.max() <= 2e-2 and err.mean() <= 2e-3
-    out32 = cache.decode_attention(q.to(cuda), bt.to(cuda), sl, num_splits=2,
-                                   out=torch.empty(B, hq, d, device=cuda)).cpu().numpy()
-    assert np.abs(out32 - ref).max() <= 2e-2
+    for splits in (1, 2):  # fp32 output: the single-launch form (splits 1, GQA <= 4) and the split form
+        out32 = cache.decode_attention(q.to(cuda), bt.to(cuda), sl, num_splits=splits,
+                                       out=torch.empty(B, hq, d, device=cuda)).cpu().numpy()
+        assert np.abs(out32 - ref).max() <= 2e-2
 
 
 def test_decode_attention_page32_and_zero_len(cuda):
@@ -127,23 +128,26 @@ def test_decode_attention_page32_and_zero_len(cuda):
             Kd[b, :, :L] = _decoded(cache.k_quant, ks[b].reshape(-1, d), 3, d)[0].reshape(L, hkv, d).transpose(1, 0, 2)
             Vd[b, :, :L] = _decoded(cache.v_quant, vs[b].reshape(-1, d), 3, d)[0].reshape(L, hkv, d).transpose(1, 0, 2)
     ref = O.dense_decode_attention(q.float().numpy(), Kd, Vd, lens, 1 / math.sqrt(d))
-    out = cache.decode_attention(q.to(cuda), bt.to(cuda), torch.tensor(lens, dtype=torch.int32, device=cuda),
-                                 num_splits=4).float().cpu().numpy()
-    assert np.all(out[0] == 0)  # empty context -> zeros
-    assert np.abs(out - ref).max() <= 2e-2
+    for splits in (1, 4):  # single-launch form and split form
+        out = cache.decode_attention(q.to(cuda), bt.to(cuda), torch.tensor(lens, dtype=torch.int32, device=cuda),
+                                     num_splits=splits).float().cpu().numpy()
+        assert np.all(out[0] == 0), splits  # empty context -> zeros
+        assert np.abs(out - ref).max() <= 2e-2, splits
 
 
 def test_config3_full_size(cuda):
     """Config 3 at full size; two sequences checked against the oracle, the rest
-    through split-count invariance (1 split vs the default split)."""
+    through the agreement of the default (the single-launch form: B * Hkv = 256
+    workgroups of 16 waves) with the split form (4 splits + merge launch)."""
     from fused_turboquant import paged as P
     cache, q, bt, sl = P.make_config3(cuda)
     B, hq, d = q.shape
+    assert P.default_splits(B, cache.num_kv_heads, int(sl[0]), hq, d) == 1
     out = P.paged_decode_attention(q, cache.kv_cache, bt, sl, cache.k_quant, cache.v_quant)
-    out1 = P.paged_decode_attention(q, cache.kv_cache, bt, sl, cache.k_quant, cache.v_quant, num_splits=1)
-    a, b1 = out.float().cpu().numpy(), out1.float().cpu().numpy()
+    out4 = P.paged_decode_attention(q, cache.kv_cache, bt, sl, cache.k_quant, cache.v_quant, num_splits=4)
+    a, b4 = out.float().cpu().numpy(), out4.float().cpu().numpy()
     assert np.isfinite(a).all()
-    assert np.abs(a - b1).max() <= 1e-2
+    assert np.abs(a - b4).max() <= 1e-2
     kq, vq = cache.k_quant, cache.v_quant
     ctx = int(sl[0])
     full = cache.kv_cache.cpu().numpy()
