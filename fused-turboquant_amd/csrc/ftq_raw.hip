@@ -84,12 +84,24 @@ struct RawTile {
 
 struct RawAddr {
   const uint8_t* cache;
-  const int32_t* bt_row;
-  int64_t num_blocks, s_blk, kvh_off;
+  __amdgpu_buffer_rsrc_t bt_rs;  // the sequence's block-table row as a buffer
+  int64_t s_blk, kvh_off;
   uint32_t s_pos;
-  int lbs, max_blocks, seq_len;
+  int lbs, max_blocks, seq_len, nb32;  // nb32 = min(num_blocks, 2^31 - 1)
   uint32_t koff, voff;  // lane offsets in the tile's descriptor
 };
+
+// Block-table entry of a 16-token tile, as a vector load issued one tile
+// ahead of the loads that need it (-1 when inactive, past seq_len or past the
+// row).  A vector load retires in order, so the wait before raw_load's
+// readfirstlane covers only this load.
+__device__ __forceinline__ int raw_fetch_bt(const RawAddr& ad, int tile, bool active) {
+  const int pos0 = tile * 16;
+  const int page = pos0 >> ad.lbs;
+  const bool ok = active && pos0 < ad.seq_len && page < ad.max_blocks;
+  const int v = (int)__builtin_amdgcn_raw_buffer_load_b32(ad.bt_rs, (uint32_t)(ok ? page : 0) * 4u, 0, 0);
+  return ok ? v : -1;
+}
 
 // Loads of one 16-token tile through one wave-uniform buffer descriptor (its
 // page base; the byte range ends after its 16 token rows, so no lane reads past
@@ -97,14 +109,13 @@ struct RawAddr {
 // -- the loads always issue, so the wait counts stay static -- and the
 // consumer masks it.
 template <int D>
-__device__ __forceinline__ void raw_load(RawTile& r, const RawAddr& ad, int tile, bool active) {
+__device__ __forceinline__ void raw_load(RawTile& r, const RawAddr& ad, int tile, int btv) {
   const int pos0 = tile * 16;
-  const int page = pos0 >> ad.lbs;
-  int64_t phys = (active && pos0 < ad.seq_len && page < ad.max_blocks) ? (int64_t)ad.bt_row[page] : -1;
-  const bool valid = phys >= 0 && phys < ad.num_blocks;
+  int phys = __builtin_amdgcn_readfirstlane(btv);
+  const bool valid = (uint32_t)phys < (uint32_t)ad.nb32;  // -1 (no entry) and ids >= num_blocks fail
   if (!valid) phys = 0;
   const uint32_t within = valid ? (uint32_t)(pos0 & ((1 << ad.lbs) - 1)) : 0u;
-  const uint8_t* base = ad.cache + (phys * ad.s_blk + (int64_t)(within * ad.s_pos) + ad.kvh_off);
+  const uint8_t* base = ad.cache + ((int64_t)phys * ad.s_blk + (int64_t)(within * ad.s_pos) + ad.kvh_off);
   const __amdgpu_buffer_rsrc_t rs =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(base), (short)0, (int)(16u * ad.s_pos), 0x00020000);
 #pragma unroll
@@ -188,8 +199,10 @@ __global__ __launch_bounds__(256) void raw_attn_kernel(
 
   RawAddr ad;
   ad.cache = cache;
-  ad.bt_row = block_table + (int64_t)b * max_blocks;
-  ad.num_blocks = num_blocks;
+  ad.bt_rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<int32_t*>(block_table + (int64_t)b * max_blocks),
+                                               (short)0, (int)min((int64_t)max_blocks * 4, (int64_t)0x7ffffffc),
+                                               0x00020000);
+  ad.nb32 = (int)min(num_blocks, (int64_t)0x7fffffff);
   ad.s_blk = s_blk;
   ad.kvh_off = (int64_t)kvh * s_head;
   ad.s_pos = (uint32_t)s_pos;
@@ -283,15 +296,25 @@ __global__ __launch_bounds__(256) void raw_attn_kernel(
     raw_lds_fence();
   };
 
+  // two register sets: the next tile's loads overlap this tile's math, and
+  // the block-table entry comes one tile further ahead
   RawTile ra, rb;
   int tile = t_begin + wave_u;
-  if (tile < t_end) raw_load<D>(ra, ad, tile, true);
+  int btv = 0;
+  if (tile < t_end) {
+    raw_load<D>(ra, ad, tile, raw_fetch_bt(ad, tile, true));
+    btv = raw_fetch_bt(ad, tile + 4, tile + 4 < t_end);
+  }
   while (tile < t_end) {
-    raw_load<D>(rb, ad, tile + 4, tile + 4 < t_end);
+    int btn = raw_fetch_bt(ad, tile + 8, tile + 8 < t_end);
+    raw_load<D>(rb, ad, tile + 4, btv);
+    btv = btn;
     process(ra, tile);
     tile += 4;
     if (tile >= t_end) break;
-    raw_load<D>(ra, ad, tile + 4, tile + 4 < t_end);
+    btn = raw_fetch_bt(ad, tile + 8, tile + 8 < t_end);
+    raw_load<D>(ra, ad, tile + 4, btv);
+    btv = btn;
     process(rb, tile);
     tile += 4;
   }

@@ -221,29 +221,47 @@ struct V1Tile {
 //         each 24-bit chunk (starting at an even byte).
 struct V1Addr {
   const uint8_t* cache;
-  const int32_t* bt_row;
-  int64_t num_blocks, s_blk, kvh_off;
+  __amdgpu_buffer_rsrc_t bt_rs;  // the sequence's block-table row as a buffer
+  int64_t s_blk, kvh_off;
   uint32_t s_pos;
-  int lbs, max_blocks, seq_len;
+  int lbs, max_blocks, seq_len, nb32;  // nb32 = min(num_blocks, 2^31 - 1)
   uint32_t koff, toff, voff;  // lane offsets; token 4g+i of a V load adds i * s_pos (scalar)
 };
+
+__device__ __forceinline__ void v1_addr_rows(V1Addr& ad, const int32_t* bt_row, int64_t num_blocks) {
+  ad.bt_rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<int32_t*>(bt_row), (short)0,
+                                               (int)min((int64_t)ad.max_blocks * 4, (int64_t)0x7ffffffc),
+                                               0x00020000);
+  ad.nb32 = (int)min(num_blocks, (int64_t)0x7fffffff);
+}
+
+// Block-table entries of a tile's two S-tiles, as a vector load issued one tile
+// ahead of the loads that need them (lane l holds S-tile l & 1; -1 when the
+// S-tile is inactive, past seq_len or past the row).  A vector load retires in
+// order, so the wait before v1_load's readlane covers only this load.
+__device__ __forceinline__ int v1_fetch_bt(const V1Addr& ad, int tile, bool active, int lane) {
+  const int pos0 = tile * 32 + (lane & 1) * 16;
+  const int page = pos0 >> ad.lbs;
+  const bool ok = active && pos0 < ad.seq_len && page < ad.max_blocks;
+  const int v = (int)__builtin_amdgcn_raw_buffer_load_b32(ad.bt_rs, (uint32_t)(ok ? page : 0) * 4u, 0, 0);
+  return ok ? v : -1;
+}
 
 __device__ __forceinline__ uint32_t buf_u16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
   return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0);
 }
 
 template <int D, int KB, int VB>
-__device__ __forceinline__ void v1_load(V1Tile<D, KB, VB>& r, const V1Addr& ad, int tile, bool active) {
+__device__ __forceinline__ void v1_load(V1Tile<D, KB, VB>& r, const V1Addr& ad, int tile, int btv) {
   using A = V1A<D, KB, VB>;
 #pragma unroll
   for (int st = 0; st < 2; ++st) {
     const int pos0 = tile * 32 + st * 16;
-    const int page = pos0 >> ad.lbs;
-    int64_t phys = (active && pos0 < ad.seq_len && page < ad.max_blocks) ? (int64_t)ad.bt_row[page] : -1;
-    const bool valid = phys >= 0 && phys < ad.num_blocks;
+    int phys = __builtin_amdgcn_readlane(btv, st);
+    const bool valid = (uint32_t)phys < (uint32_t)ad.nb32;  // -1 (no entry) and ids >= num_blocks fail
     if (!valid) phys = 0;
     const uint32_t within = valid ? (uint32_t)(pos0 & ((1 << ad.lbs) - 1)) : 0u;
-    const uint8_t* bst = ad.cache + (phys * ad.s_blk + (int64_t)(within * ad.s_pos) + ad.kvh_off);
+    const uint8_t* bst = ad.cache + ((int64_t)phys * ad.s_blk + (int64_t)(within * ad.s_pos) + ad.kvh_off);
     const __amdgpu_buffer_rsrc_t rs =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(bst), (short)0, (int)(16u * ad.s_pos), 0x00020000);
     if constexpr (A::KQW == 4) {
@@ -405,14 +423,13 @@ __global__ __launch_bounds__(256, 2) void v1_attn_kernel(
   // lane offsets (fixed for the kernel)
   V1Addr ad;
   ad.cache = cache;
-  ad.bt_row = bt_row;
-  ad.num_blocks = num_blocks;
   ad.s_blk = s_blk;
   ad.kvh_off = kvh_off;
   ad.s_pos = (uint32_t)s_pos;
   ad.lbs = lbs;
   ad.max_blocks = max_blocks;
   ad.seq_len = seq_len;
+  v1_addr_rows(ad, bt_row, num_blocks);
   ad.koff = (uint32_t)m * ad.s_pos + (uint32_t)(g * A::KQ);
   ad.toff = (uint32_t)m * ad.s_pos +
             (uint32_t)(g == 1 ? A::KPS + A::VDB : (g == 2 ? A::KPS + A::VDB + 2 : A::MSE));
@@ -557,16 +574,25 @@ __global__ __launch_bounds__(256, 2) void v1_attn_kernel(
     }
   };
 
+  // two register sets: the next tile's loads overlap this tile's math, and
+  // the block-table entries come one tile further ahead
   V1Tile<D, KB, VB> ra, rb;
   int tile = t_begin + wave_u;
-  if (tile < t_end)
-    v1_load(ra, ad, tile, true);
+  int btv = 0;
+  if (tile < t_end) {
+    v1_load(ra, ad, tile, v1_fetch_bt(ad, tile, true, lane));
+    btv = v1_fetch_bt(ad, tile + 4, tile + 4 < t_end, lane);
+  }
   while (tile < t_end) {
-    v1_load(rb, ad, tile + 4, tile + 4 < t_end);
+    int btn = v1_fetch_bt(ad, tile + 8, tile + 8 < t_end, lane);
+    v1_load(rb, ad, tile + 4, btv);
+    btv = btn;
     process(ra, tile);
     tile += 4;
     if (tile >= t_end) break;
-    v1_load(ra, ad, tile + 4, tile + 4 < t_end);
+    btn = v1_fetch_bt(ad, tile + 8, tile + 8 < t_end, lane);
+    v1_load(ra, ad, tile + 4, btv);
+    btv = btn;
     process(rb, tile);
     tile += 4;
   }
@@ -708,14 +734,13 @@ __global__ __launch_bounds__(256, 2) void v1_attn_g4_kernel(
 
   V1Addr ad;
   ad.cache = cache;
-  ad.bt_row = bt_row;
-  ad.num_blocks = num_blocks;
   ad.s_blk = s_blk;
   ad.kvh_off = kvh_off;
   ad.s_pos = (uint32_t)s_pos;
   ad.lbs = lbs;
   ad.max_blocks = max_blocks;
   ad.seq_len = seq_len;
+  v1_addr_rows(ad, bt_row, num_blocks);
   ad.koff = (uint32_t)m * ad.s_pos + (uint32_t)(g * A::KQ);
   ad.toff = (uint32_t)m * ad.s_pos +
             (uint32_t)(g == 1 ? A::KPS + A::VDB : (g == 2 ? A::KPS + A::VDB + 2 : A::MSE));
@@ -879,16 +904,25 @@ __global__ __launch_bounds__(256, 2) void v1_attn_g4_kernel(
     }
   };
 
+  // two register sets: the next tile's loads overlap this tile's math, and
+  // the block-table entries come one tile further ahead
   V1Tile<D, KB, VB> ra, rb;
   int tile = t_begin + wave_u;
-  if (tile < t_end)
-    v1_load(ra, ad, tile, true);
+  int btv = 0;
+  if (tile < t_end) {
+    v1_load(ra, ad, tile, v1_fetch_bt(ad, tile, true, lane));
+    btv = v1_fetch_bt(ad, tile + 4, tile + 4 < t_end, lane);
+  }
   while (tile < t_end) {
-    v1_load(rb, ad, tile + 4, tile + 4 < t_end);
+    int btn = v1_fetch_bt(ad, tile + 8, tile + 8 < t_end, lane);
+    v1_load(rb, ad, tile + 4, btv);
+    btv = btn;
     process(ra, tile);
     tile += 4;
     if (tile >= t_end) break;
-    v1_load(ra, ad, tile + 4, tile + 4 < t_end);
+    btn = v1_fetch_bt(ad, tile + 8, tile + 8 < t_end, lane);
+    v1_load(ra, ad, tile + 4, btv);
+    btv = btn;
     process(rb, tile);
     tile += 4;
   }
