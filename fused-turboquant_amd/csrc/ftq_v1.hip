@@ -278,7 +278,9 @@ __device__ __forceinline__ void v1_load(V1Tile<D, KB, VB>& r, const V1Addr& ad, 
     r.tail[st] = buf_u16(rs, ad.toff, 0);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const uint32_t so = (uint32_t)i * ad.s_pos;
+      // scalar offset of token 4g+i; uniform, but LLVM otherwise keeps the
+      // i >= 2 products in VGPRs and wraps each load in a waterfall loop
+      const uint32_t so = __builtin_amdgcn_readfirstlane((uint32_t)i * ad.s_pos);
       if constexpr (VB == 2) {
         const uint32_t h = buf_u16(rs, ad.voff, so);
         if (i & 1) r.v[2 * st + (i >> 1)] |= h << 16;
@@ -658,8 +660,10 @@ template <int VB> __host__ __device__ constexpr int v1_vpos(int bb) {
        : (bb <= 2 ? 3 * bb : bb <= 5 ? 3 * bb - 8 : 3 * bb - 16);
 }
 
+// 2-bit V: 4 workgroups per CU (<= 128 VGPRs, no spills; config 4 ran 83 us
+// against 90 us at 3 per CU); 3- and 4-bit V need more registers
 template <int D, int KB, int VB, int QT>
-__global__ __launch_bounds__(256, 2) void v1_attn_g4_kernel(
+__global__ __launch_bounds__(256, VB == 2 ? 4 : 2) void v1_attn_g4_kernel(
     const void* __restrict__ query, const uint8_t* __restrict__ cache,
     const int32_t* __restrict__ block_table, const int32_t* __restrict__ seq_lens,
     const int32_t* __restrict__ kv_start, int hq, int hkv, int lbs, int max_blocks,
