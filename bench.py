@@ -37,12 +37,8 @@ HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, AMD published
 # (FETCH x2.0, WRITE x1.0); the summaries are in profiles/hbm_traffic_counters.md.
 # Keyed by roofline entry; None where no counter run covers the kernel.
 TRAFFIC_BYTES: dict = {
-    "encode_d128_3bit": 80336999,
-    "encode_d256_3bit": 160155422,
-    "decode_d128_3bit_f32": 149015748,
-    "paged_attn_config3": 224235776,
-    "v1_attn_config4": 406842573,
-    "raw_attn_boundary": 1084918363,
+    "encode_d128_3bit": 80344854, "encode_d256_3bit": 160168819, "decode_d128_3bit_f32": 149010595,
+    "paged_attn_config3": 219911850, "v1_attn_config4": 406642033, "raw_attn_boundary": 1081617368,
 }
 
 
