@@ -8,7 +8,9 @@
 //   ROT_SIGNS  o <- (H o) * scale * signs   inverse RHT of library-format V
 //   ROT_PLAIN  o <- (H o) * scale            un-rotation of v1 V (v_rotate)
 //   ROT_NONE   o unchanged
-// A row with every split empty (lse = -inf) is written as zeros.
+// A row with every split empty (lse = -inf) is written as zeros.  With
+// lse_out, the row's natural-log log-sum-exp of the scaled scores goes there
+// too (-inf for an empty row): ln 2 * (M + log2 sum_s w_s).
 //
 // Layout: a row is handled by WPR waves (WPR = 1 or 4).  Lane l of a wave owns
 // elements [E l, E l + E) of the row (E = D / 64), so each split's partial
@@ -92,7 +94,8 @@ __global__ __launch_bounds__(256) void merge_splits_kernel(const float* __restri
                                                            const float* __restrict__ ws_lse,
                                                            int64_t rows, int num_splits,
                                                            const float* __restrict__ signs,
-                                                           float scale, void* __restrict__ out) {
+                                                           float scale, void* __restrict__ out,
+                                                           float* __restrict__ lse_out) {
   static_assert(WPR == 1 || WPR == 4, "one or four waves per row");
   constexpr int E = D / 64;
   constexpr int RPB = 4 / WPR;  // rows per workgroup
@@ -160,6 +163,8 @@ __global__ __launch_bounds__(256) void merge_splits_kernel(const float* __restri
       y[i] = (part[0][lane * E + i] + part[1][lane * E + i]) + (part[2][lane * E + i] + part[3][lane * E + i]);
   }
   if (!live) return;
+  if (lse_out != nullptr && lane == 0)
+    lse_out[r] = (W > 0.f) ? (M + __builtin_log2f(W)) * 0.69314718055994531f : -INFINITY;
   const float inv = (W > 0.f) ? 1.f / W : 0.f;
 #pragma unroll
   for (int i = 0; i < E; ++i) y[i] *= inv;
@@ -177,14 +182,15 @@ __global__ __launch_bounds__(256) void merge_splits_kernel(const float* __restri
 // Launch helper: four waves per row when there are enough splits to share.
 template <int D, int OT, int ROT>
 hipError_t launch_merge_splits(const float* ws_o, const float* ws_lse, int64_t rows, int num_splits,
-                               const float* signs, float scale, void* out, hipStream_t st) {
+                               const float* signs, float scale, void* out, hipStream_t st,
+                               float* lse_out = nullptr) {
   if (rows <= 0) return hipSuccess;
   if (num_splits >= 8) {
     merge_splits_kernel<D, OT, ROT, 4><<<dim3((unsigned)rows), dim3(256), 0, st>>>(
-        ws_o, ws_lse, rows, num_splits, signs, scale, out);
+        ws_o, ws_lse, rows, num_splits, signs, scale, out, lse_out);
   } else {
     merge_splits_kernel<D, OT, ROT, 1><<<dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st>>>(
-        ws_o, ws_lse, rows, num_splits, signs, scale, out);
+        ws_o, ws_lse, rows, num_splits, signs, scale, out, lse_out);
   }
   return hipGetLastError();
 }

@@ -370,6 +370,7 @@ struct RawArgs {
   float *wo, *wl;
   void* out;
   int ot;
+  float* lse;  // optional per-row natural-log LSE (B*Hq floats)
 };
 
 template <int GP, int QT>
@@ -381,9 +382,9 @@ static hipError_t raw_launch_q(const RawArgs& a, hipStream_t st) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int64_t rows = (int64_t)a.B * a.hq;
-  if (a.ot == F32) return launch_merge_splits<128, F32, ROT_NONE>(a.wo, a.wl, rows, a.splits, nullptr, 1.f, a.out, st);
-  if (a.ot == F16) return launch_merge_splits<128, F16, ROT_NONE>(a.wo, a.wl, rows, a.splits, nullptr, 1.f, a.out, st);
-  return launch_merge_splits<128, BF16, ROT_NONE>(a.wo, a.wl, rows, a.splits, nullptr, 1.f, a.out, st);
+  if (a.ot == F32) return launch_merge_splits<128, F32, ROT_NONE>(a.wo, a.wl, rows, a.splits, nullptr, 1.f, a.out, st, a.lse);
+  if (a.ot == F16) return launch_merge_splits<128, F16, ROT_NONE>(a.wo, a.wl, rows, a.splits, nullptr, 1.f, a.out, st, a.lse);
+  return launch_merge_splits<128, BF16, ROT_NONE>(a.wo, a.wl, rows, a.splits, nullptr, 1.f, a.out, st, a.lse);
 }
 
 template <int GP>
@@ -446,12 +447,12 @@ extern "C" int ftq_raw_default_splits(int batch, int num_kv_heads, int max_seq_l
   return auto_splits(batch, num_kv_heads, max_seq_len / 2, 1024);
 }
 
-extern "C" int ftq_raw_decode_attention(
+extern "C" int ftq_raw_decode_attention_lse(
     const void* query, int q_dtype, const uint8_t* kv_cache, int64_t num_blocks, int block_size,
     int64_t stride_block, int64_t stride_pos, int64_t stride_head, const int32_t* block_table,
     int max_blocks_per_seq, const int32_t* seq_lens, const int32_t* kv_start, int batch,
     int num_q_heads, int num_kv_heads, int d, float scale, int num_splits, void* workspace,
-    int64_t workspace_bytes, void* out, int out_dtype, void* stream) {
+    int64_t workspace_bytes, void* out, int out_dtype, float* lse_out, void* stream) {
   FTQ_REQUIRE(d == 128, "raw decode attention: head_dim must be 128");
   FTQ_REQUIRE(block_size >= 16 && block_size <= 4096 && (block_size & (block_size - 1)) == 0,
               "block_size must be a power of two in [16, 4096]");
@@ -486,7 +487,7 @@ extern "C" int ftq_raw_decode_attention(
   a.splits = num_splits;
   a.wo = static_cast<float*>(workspace);
   a.wl = a.wo + (int64_t)batch * num_q_heads * num_splits * d;
-  a.out = out; a.ot = out_dtype;
+  a.out = out; a.ot = out_dtype; a.lse = lse_out;
   const int G = num_q_heads / num_kv_heads;
   hipStream_t st = (hipStream_t)stream;
   hipError_t e;
@@ -495,4 +496,16 @@ extern "C" int ftq_raw_decode_attention(
   else if (G <= 4) e = raw_launch_g<4>(a, st);
   else e = raw_launch_g<8>(a, st);
   return hip_status(e);
+}
+
+extern "C" int ftq_raw_decode_attention(
+    const void* query, int q_dtype, const uint8_t* kv_cache, int64_t num_blocks, int block_size,
+    int64_t stride_block, int64_t stride_pos, int64_t stride_head, const int32_t* block_table,
+    int max_blocks_per_seq, const int32_t* seq_lens, const int32_t* kv_start, int batch,
+    int num_q_heads, int num_kv_heads, int d, float scale, int num_splits, void* workspace,
+    int64_t workspace_bytes, void* out, int out_dtype, void* stream) {
+  return ftq_raw_decode_attention_lse(query, q_dtype, kv_cache, num_blocks, block_size, stride_block, stride_pos,
+                                      stride_head, block_table, max_blocks_per_seq, seq_lens, kv_start, batch,
+                                      num_q_heads, num_kv_heads, d, scale, num_splits, workspace, workspace_bytes,
+                                      out, out_dtype, nullptr, stream);
 }

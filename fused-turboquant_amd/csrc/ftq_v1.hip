@@ -1017,6 +1017,7 @@ struct V1Args {
   float *wo, *wl;
   void* out;
   int ot;
+  float* lse;  // optional per-row natural-log LSE (B*Hq floats)
 };
 
 template <int D, int KB, int VB>
@@ -1040,13 +1041,13 @@ static hipError_t v1_launch_attn3(const V1Args& a, hipStream_t st) {
   const int64_t rows = (int64_t)a.B * a.hq;
   const float rs = fwht_scale(D);
   if (a.vrot) {
-    if (a.ot == F32) return launch_merge_splits<D, F32, ROT_PLAIN>(a.wo, a.wl, rows, a.splits, nullptr, rs, a.out, st);
-    if (a.ot == F16) return launch_merge_splits<D, F16, ROT_PLAIN>(a.wo, a.wl, rows, a.splits, nullptr, rs, a.out, st);
-    return launch_merge_splits<D, BF16, ROT_PLAIN>(a.wo, a.wl, rows, a.splits, nullptr, rs, a.out, st);
+    if (a.ot == F32) return launch_merge_splits<D, F32, ROT_PLAIN>(a.wo, a.wl, rows, a.splits, nullptr, rs, a.out, st, a.lse);
+    if (a.ot == F16) return launch_merge_splits<D, F16, ROT_PLAIN>(a.wo, a.wl, rows, a.splits, nullptr, rs, a.out, st, a.lse);
+    return launch_merge_splits<D, BF16, ROT_PLAIN>(a.wo, a.wl, rows, a.splits, nullptr, rs, a.out, st, a.lse);
   }
-  if (a.ot == F32) return launch_merge_splits<D, F32, ROT_NONE>(a.wo, a.wl, rows, a.splits, nullptr, rs, a.out, st);
-  if (a.ot == F16) return launch_merge_splits<D, F16, ROT_NONE>(a.wo, a.wl, rows, a.splits, nullptr, rs, a.out, st);
-  return launch_merge_splits<D, BF16, ROT_NONE>(a.wo, a.wl, rows, a.splits, nullptr, rs, a.out, st);
+  if (a.ot == F32) return launch_merge_splits<D, F32, ROT_NONE>(a.wo, a.wl, rows, a.splits, nullptr, rs, a.out, st, a.lse);
+  if (a.ot == F16) return launch_merge_splits<D, F16, ROT_NONE>(a.wo, a.wl, rows, a.splits, nullptr, rs, a.out, st, a.lse);
+  return launch_merge_splits<D, BF16, ROT_NONE>(a.wo, a.wl, rows, a.splits, nullptr, rs, a.out, st, a.lse);
 }
 
 template <int D, int KB>
@@ -1110,13 +1111,13 @@ extern "C" int ftq_v1_default_splits(int batch, int num_kv_heads, int max_seq_le
   return auto_splits(batch, num_kv_heads, max_seq_len, 1024);
 }
 
-extern "C" int ftq_v1_decode_attention(
+extern "C" int ftq_v1_decode_attention_lse(
     const void* query, int q_dtype, const uint8_t* kv_cache, int64_t num_blocks, int block_size,
     int64_t stride_block, int64_t stride_pos, int64_t stride_head, const int32_t* block_table,
     int max_blocks_per_seq, const int32_t* seq_lens, const int32_t* kv_start, int batch,
     int num_q_heads, int num_kv_heads, int d, const float* centroids, int key_bits,
     int value_bits, float scale, int v_rotate, int num_splits, void* workspace,
-    int64_t workspace_bytes, void* out, int out_dtype, void* stream) {
+    int64_t workspace_bytes, void* out, int out_dtype, float* lse_out, void* stream) {
   FTQ_REQUIRE(d == 128, "v1 decode attention: head_dim must be 128");
   FTQ_REQUIRE(key_bits >= 2 && key_bits <= 4 && value_bits >= 2 && value_bits <= 4,
               "v1 decode attention: key_bits and value_bits must be 2, 3 or 4");
@@ -1156,11 +1157,25 @@ extern "C" int ftq_v1_decode_attention(
   a.splits = num_splits; a.vrot = v_rotate != 0;
   a.wo = static_cast<float*>(workspace);
   a.wl = a.wo + (int64_t)batch * num_q_heads * num_splits * d;
-  a.out = out; a.ot = out_dtype;
+  a.out = out; a.ot = out_dtype; a.lse = lse_out;
   hipStream_t st = (hipStream_t)stream;
   hipError_t e;
   if (key_bits == 2) e = v1_launch_attn2<128, 2>(value_bits, a, st);
   else if (key_bits == 3) e = v1_launch_attn2<128, 3>(value_bits, a, st);
   else e = v1_launch_attn2<128, 4>(value_bits, a, st);
   return hip_status(e);
+}
+
+extern "C" int ftq_v1_decode_attention(
+    const void* query, int q_dtype, const uint8_t* kv_cache, int64_t num_blocks, int block_size,
+    int64_t stride_block, int64_t stride_pos, int64_t stride_head, const int32_t* block_table,
+    int max_blocks_per_seq, const int32_t* seq_lens, const int32_t* kv_start, int batch,
+    int num_q_heads, int num_kv_heads, int d, const float* centroids, int key_bits,
+    int value_bits, float scale, int v_rotate, int num_splits, void* workspace,
+    int64_t workspace_bytes, void* out, int out_dtype, void* stream) {
+  return ftq_v1_decode_attention_lse(query, q_dtype, kv_cache, num_blocks, block_size, stride_block, stride_pos,
+                                     stride_head, block_table, max_blocks_per_seq, seq_lens, kv_start, batch,
+                                     num_q_heads, num_kv_heads, d, centroids, key_bits, value_bits, scale,
+                                     v_rotate, num_splits, workspace, workspace_bytes, out, out_dtype, nullptr,
+                                     stream);
 }

@@ -27,6 +27,9 @@ _SIG = {
     "ftq_raw_decode_attention": ["vp", "i32", "vp", "i64", "i32", "i64", "i64", "i64", "vp", "i32",
                                  "vp", "vp", "i32", "i32", "i32", "i32", "f32", "i32", "vp", "i64",
                                  "vp", "i32", "vp"],
+    "ftq_raw_decode_attention_lse": ["vp", "i32", "vp", "i64", "i32", "i64", "i64", "i64", "vp", "i32",
+                                     "vp", "vp", "i32", "i32", "i32", "i32", "f32", "i32", "vp", "i64",
+                                     "vp", "i32", "vp", "vp"],
 }
 
 
@@ -103,13 +106,15 @@ def raw_decode_attention(query: torch.Tensor, kv_cache: torch.Tensor, block_tabl
                          seq_lens: torch.Tensor, scale: float | None = None,
                          kv_start: torch.Tensor | None = None, num_splits: int | None = None,
                          max_seq_len: int | None = None, out: torch.Tensor | None = None,
-                         workspace: torch.Tensor | None = None) -> torch.Tensor:
+                         workspace: torch.Tensor | None = None, lse: torch.Tensor | None = None) -> torch.Tensor:
     """query [B, Hq, d] -> [B, Hq, d] (query dtype unless ``out`` is given).
 
     Attends positions [kv_start[b], seq_lens[b]) of block-table row b over the
     raw fp16 slots.  ``num_splits`` defaults to a value that fills the GPU
     (pass ``max_seq_len`` to size it without reading ``block_table``'s width);
     ``workspace`` (uint8, >= ``workspace_bytes``) may be preallocated.
+    ``lse`` (float32 [B, Hq]) receives each row's natural-log log-sum-exp of
+    the scaled scores (-inf for a row with no positions).
     """
     B, hq, d = query.shape
     if d != 128:
@@ -125,7 +130,10 @@ def raw_decode_attention(query: torch.Tensor, kv_cache: torch.Tensor, block_tabl
         raise ValueError("block_table must be [B, max_blocks] and seq_lens [B]")
     if kv_start is not None and (kv_start.dtype != torch.int32 or kv_start.numel() != B):
         raise ValueError("kv_start must be int32 [B]")
+    if lse is not None and (lse.dtype != torch.float32 or lse.numel() != B * hq or not lse.is_contiguous()):
+        raise ValueError("lse must be a contiguous float32 tensor of B * num_q_heads entries")
     tensors = [query, kv_cache, block_table, seq_lens] + ([kv_start] if kv_start is not None else [])
+    tensors += [lse] if lse is not None else []
     dev = _lib.require_device(*tensors)
     q = query.contiguous()
     if q.dtype not in (torch.float32, torch.float16, torch.bfloat16):
@@ -144,12 +152,14 @@ def raw_decode_attention(query: torch.Tensor, kv_cache: torch.Tensor, block_tabl
     bt = block_table.contiguous()
     ks = kv_start.contiguous() if kv_start is not None else None
     L = _bind()
-    _lib.check(L.ftq_raw_decode_attention(
-        q.data_ptr(), _lib.dtype_code(q.dtype), kv_cache.data_ptr(), nb, bs, sb, sp, sh,
-        bt.data_ptr(), bt.shape[1], seq_lens.contiguous().data_ptr(),
-        ks.data_ptr() if ks is not None else None, B, hq, hkv, d, float(scale), int(num_splits),
-        workspace.data_ptr(), workspace.numel(), out.data_ptr(), _lib.dtype_code(out.dtype),
-        _lib.stream_ptr(dev)))
+    args = (q.data_ptr(), _lib.dtype_code(q.dtype), kv_cache.data_ptr(), nb, bs, sb, sp, sh,
+            bt.data_ptr(), bt.shape[1], seq_lens.contiguous().data_ptr(),
+            ks.data_ptr() if ks is not None else None, B, hq, hkv, d, float(scale), int(num_splits),
+            workspace.data_ptr(), workspace.numel(), out.data_ptr(), _lib.dtype_code(out.dtype))
+    if lse is None:
+        _lib.check(L.ftq_raw_decode_attention(*args, _lib.stream_ptr(dev)))
+    else:
+        _lib.check(L.ftq_raw_decode_attention_lse(*args, lse.data_ptr(), _lib.stream_ptr(dev)))
     return out
 
 

@@ -40,6 +40,9 @@ _SIG = {
     "ftq_v1_decode_attention": ["vp", "i32", "vp", "i64", "i32", "i64", "i64", "i64", "vp", "i32",
                                 "vp", "vp", "i32", "i32", "i32", "i32", "vp", "i32", "i32", "f32",
                                 "i32", "i32", "vp", "i64", "vp", "i32", "vp"],
+    "ftq_v1_decode_attention_lse": ["vp", "i32", "vp", "i64", "i32", "i64", "i64", "i64", "vp", "i32",
+                                    "vp", "vp", "i32", "i32", "i32", "i32", "vp", "i32", "i32", "f32",
+                                    "i32", "i32", "vp", "i64", "vp", "i32", "vp", "vp"],
 }
 
 
@@ -170,14 +173,16 @@ def v1_decode_attention(query: torch.Tensor, kv_cache: torch.Tensor, block_table
                         value_bits: int, scale: float | None = None, v_rotate: bool = False,
                         kv_start: torch.Tensor | None = None, num_splits: int | None = None,
                         max_seq_len: int | None = None, out: torch.Tensor | None = None,
-                        workspace: torch.Tensor | None = None) -> torch.Tensor:
+                        workspace: torch.Tensor | None = None, lse: torch.Tensor | None = None) -> torch.Tensor:
     """query [B, Hq, d] -> [B, Hq, d] (query dtype unless ``out`` is given).
 
     Attends positions [kv_start[b], seq_lens[b]) of block-table row b
     (``kv_start`` None = 0, reference ``triton_decode_offset.py:95-106``).
     ``num_splits`` defaults to a value that fills the GPU (pass ``max_seq_len``
     to size it without reading ``block_table``'s width); ``workspace`` (uint8,
-    >= ``workspace_bytes``) may be preallocated for graph capture.
+    >= ``workspace_bytes``) may be preallocated for graph capture.  ``lse``
+    (float32 [B, Hq]) receives each row's natural-log log-sum-exp of the
+    scaled scores (-inf for a row with no positions).
     """
     B, hq, d = query.shape
     _check_bits(d, key_bits, value_bits)
@@ -194,7 +199,10 @@ def v1_decode_attention(query: torch.Tensor, kv_cache: torch.Tensor, block_table
         raise ValueError("kv_start must be int32 [B]")
     if centroids.numel() != (1 << key_bits):
         raise ValueError("centroids must have 2^key_bits entries")
+    if lse is not None and (lse.dtype != torch.float32 or lse.numel() != B * hq or not lse.is_contiguous()):
+        raise ValueError("lse must be a contiguous float32 tensor of B * num_q_heads entries")
     tensors = [query, kv_cache, block_table, seq_lens, centroids] + ([kv_start] if kv_start is not None else [])
+    tensors += [lse] if lse is not None else []
     dev = _lib.require_device(*tensors)
     q = query.contiguous()
     if q.dtype not in (torch.float32, torch.float16, torch.bfloat16):
@@ -214,12 +222,15 @@ def v1_decode_attention(query: torch.Tensor, kv_cache: torch.Tensor, block_table
     cent = torch.sort(centroids.to(torch.float32)).values.contiguous()
     ks = kv_start.contiguous() if kv_start is not None else None
     L = _bind()
-    _lib.check(L.ftq_v1_decode_attention(
-        q.data_ptr(), _lib.dtype_code(q.dtype), kv_cache.data_ptr(), nb, bs, sb, sp, sh,
-        bt.data_ptr(), bt.shape[1], seq_lens.contiguous().data_ptr(),
-        ks.data_ptr() if ks is not None else None, B, hq, hkv, d, cent.data_ptr(), key_bits,
-        value_bits, float(scale), int(bool(v_rotate)), int(num_splits), workspace.data_ptr(),
-        workspace.numel(), out.data_ptr(), _lib.dtype_code(out.dtype), _lib.stream_ptr(dev)))
+    args = (q.data_ptr(), _lib.dtype_code(q.dtype), kv_cache.data_ptr(), nb, bs, sb, sp, sh,
+            bt.data_ptr(), bt.shape[1], seq_lens.contiguous().data_ptr(),
+            ks.data_ptr() if ks is not None else None, B, hq, hkv, d, cent.data_ptr(), key_bits,
+            value_bits, float(scale), int(bool(v_rotate)), int(num_splits), workspace.data_ptr(),
+            workspace.numel(), out.data_ptr(), _lib.dtype_code(out.dtype))
+    if lse is None:
+        _lib.check(L.ftq_v1_decode_attention(*args, _lib.stream_ptr(dev)))
+    else:
+        _lib.check(L.ftq_v1_decode_attention_lse(*args, lse.data_ptr(), _lib.stream_ptr(dev)))
     return out
 
 

@@ -33,8 +33,10 @@ TQ_CONFIG_ENV_MAP = {
     "kind": "TURBOQUANT_KIND",
     "boundary_protect": "TURBOQUANT_BOUNDARY_PROTECT",
     "v_rotate": "TURBOQUANT_V_ROTATE",
+    "v_lloyd_max": "TURBOQUANT_V_LLOYD_MAX",
     "key_bits": "TURBOQUANT_KEY_BITS",
     "value_bits": "TURBOQUANT_VALUE_BITS",
+    "defer_prefill": "TURBOQUANT_DEFER_PREFILL",
 }
 
 

@@ -30,6 +30,18 @@ and decodes them with ``ftq_raw_decode_attention`` (the reference's
 ``boundary_fp16_decode_attention``, ``triton_boundary_attn.py:28-219``); 2/3/4
 run the TurboQuant path at that width inside the fp16-sized slot.
 
+Deferred prefill (``TURBOQUANT_DEFER_PREFILL=1``, TurboQuant layers; reference
+``:331-332``, ``:673-686``, ``:1095-1277``): a prefill store of 1 < N <=
+capacity tokens skips the quantised store and writes the tokens as fp16 into
+one per-layer prefix buffer (raw slots, positions 0..N-1); decode tokens then
+run phase 1 = ``ftq_raw_decode_attention_lse`` over the prefix (sequence 0
+only, as the reference's cu_seqlens [0, P, P, ...] give), phase 2 =
+``ftq_v1_decode_attention_lse`` over positions [P, seq_len) of every
+sequence, and a log-sum-exp merge of the two.  As in the reference, the
+prefix length starts at 1 (one zero K/V row) until a prefill is deferred.
+The capacity is vLLM's max(max_model_len, max_num_batched_tokens), or
+``TURBOQUANT_DEFER_PREFILL_CAPACITY`` (default 32768) without vLLM.
+
 Per-layer state (sorted centroids, midpoints) is cached on the ``layer``
 object, like the reference's ``setup_layer`` (``rotation/matrix.py:34-42``).
 The centroid table of vLLM's ``get_centroids`` is not available here; this
@@ -39,6 +51,7 @@ vLLM attached as ``layer._tq_centroids`` with the right size takes precedence.
 from __future__ import annotations
 
 import math
+import os
 from typing import Any, ClassVar, Optional
 
 import torch
@@ -54,6 +67,23 @@ try:  # vLLM's base classes when present (not installed in every environment)
 except Exception:  # pragma: no cover - depends on the environment
     _BackendBase = object
     _ImplBase = object
+
+
+def _defer_capacity() -> int:
+    """Positions of the deferred-prefill buffer: vLLM's max(max_model_len,
+    max_num_batched_tokens) (reference :575-585), else
+    TURBOQUANT_DEFER_PREFILL_CAPACITY (default 32768)."""
+    try:
+        from vllm.config import get_current_vllm_config  # type: ignore
+        cfg = get_current_vllm_config()
+        sched = getattr(cfg, "scheduler_config", None)
+        mb = int(getattr(sched, "max_num_batched_tokens", 0) or 0) if sched is not None else 0
+        return max(int(cfg.model_config.max_model_len), mb)
+    except Exception:
+        v = int(os.environ.get("TURBOQUANT_DEFER_PREFILL_CAPACITY", "32768"))
+        if v < 2:
+            raise ValueError("TURBOQUANT_DEFER_PREFILL_CAPACITY must be at least 2")
+        return v
 
 
 class FusedTurboQuantV1Backend(_BackendBase):
@@ -180,6 +210,8 @@ class FusedTurboQuantV1Impl(_ImplBase):
         self.num_kv_groups = num_heads // num_kv_heads
         self.kv_cache_dtype = kv_cache_dtype
         self.v_rotate = not self._is_raw and (env_flag("TURBOQUANT_V_ROTATE") or env_flag("TURBOQUANT_V_LLOYD_MAX"))
+        self.defer_prefill = not self._is_raw and env_flag("TURBOQUANT_DEFER_PREFILL")
+        self._prefix_capacity = _defer_capacity() if self.defer_prefill else 0
         if env_flag("TURBOQUANT_V_LLOYD_MAX") and not self._is_raw:
             raise NotImplementedError("TURBOQUANT_V_LLOYD_MAX (Lloyd-Max V codes) is not part of this build")
 
@@ -195,6 +227,22 @@ class FusedTurboQuantV1Impl(_ImplBase):
             layer._fused_tq_state = st
         return st
 
+    def _prefix(self, layer, device):
+        """The deferred-prefill buffers of this layer: raw fp16 slots for
+        positions 0..capacity-1, the prefix length (device int32 [1]; 1 until a
+        prefill is deferred, the reference's seed, :688-711) and the block-table
+        row of the buffer."""
+        pf = getattr(layer, "_fused_tq_prefix", None)
+        if pf is None or pf[0].device != torch.device(device):
+            nblk = (self._prefix_capacity + 15) // 16
+            cache = torch.zeros(nblk, 16, self.num_kv_heads, RAW.raw_slot_bytes(self.head_size),
+                                dtype=torch.uint8, device=device)
+            plen = torch.ones(1, dtype=torch.int32, device=device)
+            row = torch.arange(nblk, dtype=torch.int32, device=device)
+            pf = (cache, plen, row)
+            layer._fused_tq_prefix = pf
+        return pf
+
     # -- store ---------------------------------------------------------------
     def do_kv_cache_update(self, layer, key: torch.Tensor, value: torch.Tensor, kv_cache: torch.Tensor,
                            slot_mapping: torch.Tensor) -> None:
@@ -207,6 +255,13 @@ class FusedTurboQuantV1Impl(_ImplBase):
         v = value[:N].reshape(N, self.num_kv_heads, self.head_size)
         if self._is_raw:
             RAW.raw_store(k, v, kv_cache, slot_mapping[:N].to(torch.int64))
+            return
+        if self.defer_prefill and 1 < N <= self._prefix_capacity:
+            # deferred prefill: fp16 copy at positions 0..N-1 of the prefix, no
+            # quantised store (one sequence at a time, as in the reference)
+            cache, plen, _ = self._prefix(layer, key.device)
+            RAW.raw_store(k, v, cache, torch.arange(N, dtype=torch.int64, device=key.device))
+            plen.fill_(N)
             return
         st = self._state(layer, key.device)
         st.store(k, v, kv_cache, slot_mapping[:N].to(torch.int64))
@@ -233,9 +288,9 @@ class FusedTurboQuantV1Impl(_ImplBase):
         if not attn_metadata.is_prefill:
             nd, ndt = attn_metadata.seq_lens.shape[0], N
         if ndt > 0:
-            out[:ndt] = self._decode(q[:ndt], kv_cache, attn_metadata.block_table[:nd],
-                                     attn_metadata.seq_lens[:nd], st,
-                                     max_seq_len=getattr(attn_metadata, "max_seq_len", None))
+            dec = self._decode_hybrid if self.defer_prefill else self._decode
+            out[:ndt] = dec(q[:ndt], kv_cache, attn_metadata.block_table[:nd], attn_metadata.seq_lens[:nd], st,
+                            max_seq_len=getattr(attn_metadata, "max_seq_len", None), layer=layer)
         if ndt < N:
             k = key[:N].view(N, self.num_kv_heads, self.head_size)
             v = value[:N].view(N, self.num_kv_heads, self.head_size)
@@ -246,7 +301,37 @@ class FusedTurboQuantV1Impl(_ImplBase):
             output[:N] = out.reshape(N, -1).to(output.dtype)
         return output
 
-    def _decode(self, q, kv_cache, block_table, seq_lens, st, max_seq_len=None):
+    def _decode_hybrid(self, q, kv_cache, block_table, seq_lens, st, max_seq_len=None, layer=None):
+        """Deferred-prefill decode (reference _decode_attention_hybrid,
+        :1095-1277): fp16 prefix attention for sequence 0, quantised attention
+        over [P, seq_len) for every sequence, merged by log-sum-exp."""
+        B, hq, d = q.shape
+        dev = q.device
+        pcache, plen, row = self._prefix(layer, dev)
+        bt = block_table if block_table.dtype == torch.int32 else block_table.to(torch.int32)
+        sl = seq_lens if seq_lens.dtype == torch.int32 else seq_lens.to(torch.int32)
+        msl = max_seq_len if max_seq_len is not None else bt.shape[1] * kv_cache.shape[1]
+        # phase 1: the prefix, sequence 0 only (the others get no positions)
+        sl_p = torch.zeros(B, dtype=torch.int32, device=dev)
+        sl_p[:1].copy_(plen)
+        o1 = torch.empty(B, hq, d, dtype=torch.float32, device=dev)
+        l1 = torch.empty(B, hq, dtype=torch.float32, device=dev)
+        RAW.raw_decode_attention(q, pcache, row.expand(B, -1).contiguous(), sl_p, scale=self.scale,
+                                 max_seq_len=self._prefix_capacity, out=o1, lse=l1)
+        # phase 2: the quantised positions [P, seq_len)
+        o2 = torch.empty(B, hq, d, dtype=torch.float32, device=dev)
+        l2 = torch.empty(B, hq, dtype=torch.float32, device=dev)
+        V1.v1_decode_attention(q, kv_cache, bt, sl, st.centroids, self.key_bits, self.value_bits,
+                               scale=self.scale, v_rotate=self.v_rotate, kv_start=plen.expand(B).contiguous(),
+                               max_seq_len=msl, out=o2, lse=l2)
+        # merge (a row empty in both phases stays 0)
+        m = torch.maximum(l1, l2)
+        m = torch.where(torch.isneginf(m), torch.zeros_like(m), m)
+        w1, w2 = torch.exp(l1 - m), torch.exp(l2 - m)
+        tot = (w1 + w2).clamp(min=1e-20)
+        return ((o1 * w1.unsqueeze(-1) + o2 * w2.unsqueeze(-1)) / tot.unsqueeze(-1)).to(q.dtype)
+
+    def _decode(self, q, kv_cache, block_table, seq_lens, st, max_seq_len=None, layer=None):
         bt = block_table if block_table.dtype == torch.int32 else block_table.to(torch.int32)
         sl = seq_lens if seq_lens.dtype == torch.int32 else seq_lens.to(torch.int32)
         msl = max_seq_len if max_seq_len is not None else bt.shape[1] * kv_cache.shape[1]

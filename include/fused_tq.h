@@ -207,6 +207,22 @@ int ftq_v1_decode_attention(const void* query, int q_dtype, const uint8_t* kv_ca
                             int d, const float* centroids, int key_bits, int value_bits,
                             float scale, int v_rotate, int num_splits, void* workspace,
                             int64_t workspace_bytes, void* out, int out_dtype, void* stream);
+/*
+ * ftq_v1_decode_attention that also writes each row's natural-log
+ * log-sum-exp of the scaled scores to lse_out[batch * Hq] (float32; -inf for a
+ * row with no positions; NULL = not written).  Replaces the (output, lse)
+ * pair of the quantised phase of _decode_attention_hybrid
+ * (vllm_plugin/v1_backend.py:1185-1262), merged there with the fp16 prefix.
+ */
+int ftq_v1_decode_attention_lse(const void* query, int q_dtype, const uint8_t* kv_cache,
+                                int64_t num_blocks, int block_size, int64_t stride_block,
+                                int64_t stride_pos, int64_t stride_head, const int32_t* block_table,
+                                int max_blocks_per_seq, const int32_t* seq_lens,
+                                const int32_t* kv_start, int batch, int num_q_heads, int num_kv_heads,
+                                int d, const float* centroids, int key_bits, int value_bits,
+                                float scale, int v_rotate, int num_splits, void* workspace,
+                                int64_t workspace_bytes, void* out, int out_dtype, float* lse_out,
+                                void* stream);
 
 /* ---------------------------------------------------------------------------
  * Raw fp16 slots of the boundary-protection layers (TURBOQUANT_BOUNDARY_PROTECT
@@ -251,6 +267,21 @@ int ftq_raw_decode_attention(const void* query, int q_dtype, const uint8_t* kv_c
                              const int32_t* kv_start, int batch, int num_q_heads,
                              int num_kv_heads, int d, float scale, int num_splits, void* workspace,
                              int64_t workspace_bytes, void* out, int out_dtype, void* stream);
+/*
+ * ftq_raw_decode_attention that also writes each row's natural-log
+ * log-sum-exp of the scaled scores to lse_out[batch * Hq] (float32; -inf for a
+ * row with no positions; NULL = not written).  Replaces the flash-attention
+ * call over the deferred fp16 prefix (out, softmax lse) of
+ * _decode_attention_hybrid (vllm_plugin/v1_backend.py:1131-1172).
+ */
+int ftq_raw_decode_attention_lse(const void* query, int q_dtype, const uint8_t* kv_cache,
+                                 int64_t num_blocks, int block_size, int64_t stride_block,
+                                 int64_t stride_pos, int64_t stride_head, const int32_t* block_table,
+                                 int max_blocks_per_seq, const int32_t* seq_lens,
+                                 const int32_t* kv_start, int batch, int num_q_heads,
+                                 int num_kv_heads, int d, float scale, int num_splits, void* workspace,
+                                 int64_t workspace_bytes, void* out, int out_dtype, float* lse_out,
+                                 void* stream);
 
 #ifdef __cplusplus
 }

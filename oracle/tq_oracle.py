@@ -47,6 +47,12 @@ Pinning (each check lives in ``tests/test_oracle.py``):
   (IEEE round to nearest even, as torch's ``.to(float16)``); the attention is
   float64 softmax attention, checked against an independent dense computation
   over the K/V arrays before they enter the cache.
+* v1_hybrid_decode_attention (deferred-prefill decode,
+  ``vllm_plugin/v1_backend.py:1095-1277``): one float64 softmax over the union
+  of the fp16 prefix (sequence 0) and the dequantised slots in [P, seq_len);
+  the reference's two phases and log-sum-exp merge equal it in closed form.
+  Checked against a two-phase computation (``v1_decode_attention`` with
+  ``kv_start`` plus dense attention over the prefix, merged by their LSEs).
 """
 from __future__ import annotations
 
@@ -539,6 +545,52 @@ def v1_decode_attention(q: np.ndarray, kv_cache: np.ndarray, block_table: np.nda
             p = np.exp(s)
             o = (p / p.sum()) @ vv
             out[b, h] = (o @ M.T) if v_rotate else o
+    return out
+
+
+def v1_hybrid_decode_attention(q: np.ndarray, prefix_k: np.ndarray, prefix_v: np.ndarray, prefix_len: int,
+                               kv_cache: np.ndarray, block_table: np.ndarray, seq_lens: np.ndarray,
+                               centroids: np.ndarray, kb: int, vb: int, scale: float,
+                               v_rotate: bool = False, norm_correction: bool = True):
+    """Deferred-prefill decode, float64 (reference v1_backend.py:1095-1277).
+
+    prefix_k / prefix_v [P_cap, Hkv, d]: the fp16 prefix rows (values as
+    stored).  Sequence 0 attends prefix rows [0, prefix_len) (the reference's
+    cu_seqlens_k = [0, P, P, ...] give the other sequences none) plus the
+    quantised slot positions [prefix_len, seq_lens[0]); sequence b > 0 attends
+    only its positions [prefix_len, seq_lens[b]).  Prefix scores are q . k in
+    the original domain, slot scores q M . K^ in the rotated one (equal for an
+    orthogonal M); rotated V^ rows are taken back by M^T when v_rotate.  One
+    softmax over all of them -- what the reference's LSE merge of the two
+    phases computes."""
+    q = np.asarray(q, np.float64)
+    B, Hq, d = q.shape
+    nb, bs, Hkv, slot = kv_cache.shape
+    G = Hq // Hkv
+    M = sylvester(d) / math.sqrt(d)
+    q_rot = q @ M
+    k_hat, v_hat = v1_dequant(kv_cache, d, kb, vb, centroids, norm_correction)
+    pk = np.asarray(prefix_k, np.float64)
+    pv = np.asarray(prefix_v, np.float64)
+    out = np.zeros((B, Hq, d))
+    for b in range(B):
+        P = prefix_len if b == 0 else 0
+        L = int(seq_lens[b])
+        pos = np.arange(prefix_len, L) if L > prefix_len else np.arange(0)
+        blk = np.asarray(block_table[b])[pos // bs]
+        off = pos % bs
+        for h in range(Hq):
+            kv = h // G
+            s_p = pk[:P, kv] @ q[b, h] * scale
+            s_q = k_hat[blk, off, kv] @ q_rot[b, h] * scale
+            vq = v_hat[blk, off, kv]
+            if v_rotate:
+                vq = vq @ M.T
+            s = np.concatenate([s_p, s_q])
+            if s.size == 0:
+                continue
+            w = np.exp(s - s.max())
+            out[b, h] = (w / w.sum()) @ np.concatenate([pv[:P, kv], vq])
     return out
 
 

@@ -186,3 +186,47 @@ def test_decode_quality(kb, vb, floor):
     want = O.dense_decode_attention(q, kk, vv, [nb * bs], 1 / math.sqrt(d))
     cos = np.sum(got * want) / np.linalg.norm(got) / np.linalg.norm(want)
     assert cos > floor, cos
+
+
+@pytest.mark.parametrize("v_rotate", [False, True])
+def test_hybrid_equals_two_phase_lse_merge(v_rotate):
+    """v1_hybrid_decode_attention (one softmax over the union) against the
+    reference's own construction (v1_backend.py:1131-1277): phase 1 dense
+    attention over the fp16 prefix with its log-sum-exp (sequence 0 only),
+    phase 2 the quantised decode from kv_start = P with its log-sum-exp,
+    merged by exp(lse - max) weights."""
+    rng = np.random.default_rng(21)
+    nb, bs, H, d, kb, vb, Hq, B = 12, 16, 2, 64, 4, 2, 4, 2
+    cache, c, _, _, _ = _rand_cache(rng, nb, bs, H, d, kb, vb, nb * bs, v_rotate)
+    bt = rng.permutation(nb).reshape(B, nb // B).astype(np.int32)
+    seq = np.array([90, 70], np.int32)
+    P = 33
+    pk = rng.standard_normal((48, H, d)).astype(np.float16)
+    pv = rng.standard_normal((48, H, d)).astype(np.float16)
+    q = rng.standard_normal((B, Hq, d)).astype(np.float32)
+    sc = 1 / math.sqrt(d)
+    got = O.v1_hybrid_decode_attention(q, pk, pv, P, cache, bt, seq, c, kb, vb, sc, v_rotate=v_rotate)
+
+    G = Hq // H
+    M = O.sylvester(d) / math.sqrt(d)
+    k_hat, _ = O.v1_dequant(cache, d, kb, vb, c)
+    o2 = O.v1_decode_attention(q, cache, bt, seq, c, kb, vb, sc, kv_start=np.full(B, P), v_rotate=v_rotate)
+    want = np.zeros_like(got)
+    for b in range(B):
+        pos = np.arange(P, seq[b])
+        for h in range(Hq):
+            s2 = k_hat[bt[b][pos // bs], pos % bs, h // G] @ (q[b, h].astype(np.float64) @ M) * sc
+            l2 = s2.max() + np.log(np.exp(s2 - s2.max()).sum())
+            if b == 0:
+                s1 = pk[:P, h // G].astype(np.float64) @ q[b, h].astype(np.float64) * sc
+                w1 = np.exp(s1 - s1.max())
+                o1 = (w1 / w1.sum()) @ pv[:P, h // G].astype(np.float64)
+                l1 = s1.max() + np.log(w1.sum())
+            else:
+                o1, l1 = np.zeros(d), -np.inf
+            m = max(l1, l2)
+            e1, e2 = np.exp(l1 - m), np.exp(l2 - m)
+            want[b, h] = (o1 * e1 + o2[b, h] * e2) / (e1 + e2)
+    assert np.allclose(got, want, atol=1e-10)
+    # sequence 1 sees no prefix: exactly the kv_start decode
+    assert np.allclose(got[1], o2[1], atol=1e-12)

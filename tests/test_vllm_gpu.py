@@ -162,3 +162,73 @@ def test_boundary_layer_mixed_batch(cuda, monkeypatch, protect):
     with TURBOQUANT_BOUNDARY_PROTECT=3; decode, fresh prefill and continuation."""
     _run_step(cuda, [(40, 1), (700, 1), (0, 33), (129, 9)], "auto", 32, 8, False, monkeypatch,
               seed=5, protect=protect)
+
+
+@pytest.mark.parametrize("dtype_str,vrot", [("turboquant_k4v2_nc", False), ("turboquant_3bit_nc", True)])
+def test_deferred_prefill_hybrid_decode(cuda, monkeypatch, dtype_str, vrot):
+    """TURBOQUANT_DEFER_PREFILL=1 (reference v1_backend.py:673-686, 1095-1277),
+    one sequence, as the reference supports it: a multi-token store goes to the
+    fp16 prefix, single-token stores go to the slots, and a decode attends the
+    prefix and the slots from position P on, merged by log-sum-exp.  First the
+    seeded one-row zero prefix (no prefill deferred yet), then a 200-token
+    deferred prefill followed by three decode steps.  Expected values: the
+    oracle's float64 softmax over the union (fp16 prefix values, dequantised
+    slot bytes the GPU wrote)."""
+    from fused_turboquant import vllm_plugin as vp
+    monkeypatch.setenv("TURBOQUANT_BOUNDARY_PROTECT", "0")
+    monkeypatch.setenv("TURBOQUANT_V_ROTATE", "1" if vrot else "0")
+    monkeypatch.setenv("TURBOQUANT_DEFER_PREFILL", "1")
+    monkeypatch.setenv("TURBOQUANT_DEFER_PREFILL_CAPACITY", "256")
+    hq, hkv, bs = 16, 4, 16
+    g = torch.Generator().manual_seed(6)
+    Bk = vp.FusedTurboQuantV1Backend
+    impl = vp.FusedTurboQuantV1Impl(hq, D, 1 / math.sqrt(D), hkv, kv_cache_dtype=dtype_str)
+    assert impl.defer_prefill and impl._prefix_capacity == 256
+    layer = SimpleNamespace()
+    nb = 20
+    cache = torch.zeros(Bk.get_kv_cache_shape(nb, bs, hkv, D, dtype_str), dtype=torch.uint8, device=cuda)
+    bt = torch.randperm(nb, generator=g).to(torch.int32)[None]
+    kb, vb = impl.key_bits, impl.value_bits
+
+    def slot(pos):
+        return int(bt[0, pos // bs]) * bs + pos % bs
+
+    def store1(pos, k, v):
+        impl.do_kv_cache_update(layer, k.reshape(1, -1).to(cuda), v.reshape(1, -1).to(cuda), cache,
+                                torch.tensor([slot(pos)], dtype=torch.int64, device=cuda))
+
+    def decode(L, prefix_k, prefix_v, P, tag):
+        q = torch.randn(1, hq, D, generator=g).to(torch.bfloat16)
+        md = SimpleNamespace(seq_lens=torch.tensor([L], dtype=torch.int32, device=cuda), block_table=bt.to(cuda),
+                             query_start_loc=torch.tensor([0, 1], dtype=torch.int32, device=cuda),
+                             slot_mapping=None, num_actual_tokens=1, max_query_len=1, max_seq_len=L,
+                             is_prefill=False, num_decodes=1, num_decode_tokens=1)
+        out = torch.full((1, hq * D), float("nan"), dtype=torch.bfloat16, device=cuda)
+        impl.forward(layer, q.reshape(1, -1).to(cuda), q.reshape(1, -1).to(cuda), q.reshape(1, -1).to(cuda),
+                     cache, md, output=out)
+        torch.cuda.synchronize()
+        cent = layer._fused_tq_state.centroids.cpu().numpy()
+        want = O.v1_hybrid_decode_attention(q.float().numpy(), prefix_k, prefix_v, P, cache.cpu().numpy(),
+                                            bt.numpy(), np.array([L]), cent, kb, vb, 1 / math.sqrt(D),
+                                            v_rotate=vrot)
+        _check(out.float().cpu().numpy().reshape(1, hq, D), want, tag)
+
+    # (1) no prefill deferred yet: the seeded prefix is one zero row, the slots start at 1
+    for pos in range(9):
+        store1(pos, torch.randn(hkv, D, generator=g).to(torch.bfloat16), torch.randn(hkv, D, generator=g).to(torch.bfloat16))
+    zeros = np.zeros((1, hkv, D), np.float16)
+    decode(9, zeros, zeros, 1, f"{dtype_str} seeded prefix")
+    # (2) a 200-token prefill is deferred: fp16 prefix, nothing written to the slots
+    P = 200
+    kp = torch.randn(P, hkv, D, generator=g).to(torch.bfloat16)
+    vp_ = torch.randn(P, hkv, D, generator=g).to(torch.bfloat16)
+    before = cache.clone()
+    impl.do_kv_cache_update(layer, kp.reshape(P, -1).to(cuda), vp_.reshape(P, -1).to(cuda), cache,
+                            torch.tensor([slot(p) for p in range(P)], dtype=torch.int64, device=cuda))
+    torch.cuda.synchronize()
+    assert torch.equal(cache, before)
+    pk, pv = kp.to(torch.float16).numpy(), vp_.to(torch.float16).numpy()
+    for t in range(3):
+        store1(P + t, torch.randn(hkv, D, generator=g).to(torch.bfloat16),
+               torch.randn(hkv, D, generator=g).to(torch.bfloat16))
+        decode(P + t + 1, pk, pv, P, f"{dtype_str} vrot={vrot} step {t}")

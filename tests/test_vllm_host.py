@@ -148,3 +148,29 @@ def test_boundary_layer_impl_modes(monkeypatch):
         vp.FusedTurboQuantV1Impl(32, 128, 0.1, 2, kv_cache_dtype="bfloat16")
     # the boundary layer's slot (bf16 elements) holds K|V in fp16: 4 * head_size bytes
     assert B.get_kv_cache_shape(10, 16, 8, 128, "auto")[-1] * 2 == 4 * 128
+
+
+def test_defer_prefill_flag_and_capacity(monkeypatch):
+    from fused_turboquant import vllm_plugin as vp
+    monkeypatch.setenv("TURBOQUANT_BOUNDARY_PROTECT", "0")
+    monkeypatch.delenv("TURBOQUANT_DEFER_PREFILL", raising=False)
+    impl = vp.FusedTurboQuantV1Impl(32, 128, 0.088, 8, kv_cache_dtype="turboquant_3bit_nc")
+    assert not impl.defer_prefill
+    monkeypatch.setenv("TURBOQUANT_DEFER_PREFILL", "1")
+    monkeypatch.setenv("TURBOQUANT_DEFER_PREFILL_CAPACITY", "4096")
+    impl = vp.FusedTurboQuantV1Impl(32, 128, 0.088, 8, kv_cache_dtype="turboquant_3bit_nc")
+    assert impl.defer_prefill and impl._prefix_capacity == 4096
+    # raw fp16 boundary layers never defer (reference: _store_raw_kv returns first)
+    monkeypatch.setenv("TURBOQUANT_BOUNDARY_PROTECT", "fp16")
+    raw = vp.FusedTurboQuantV1Impl(32, 128, 0.088, 8, kv_cache_dtype="auto")
+    assert not raw.defer_prefill
+    monkeypatch.setenv("TURBOQUANT_BOUNDARY_PROTECT", "0")
+    monkeypatch.setenv("TURBOQUANT_DEFER_PREFILL_CAPACITY", "1")
+    with pytest.raises(ValueError):
+        vp.FusedTurboQuantV1Impl(32, 128, 0.088, 8, kv_cache_dtype="turboquant_3bit_nc")
+
+
+def test_additional_config_maps_defer_and_lloyd_keys():
+    from fused_turboquant.vllm_plugin import plugin
+    assert plugin.TQ_CONFIG_ENV_MAP["defer_prefill"] == "TURBOQUANT_DEFER_PREFILL"
+    assert plugin.TQ_CONFIG_ENV_MAP["v_lloyd_max"] == "TURBOQUANT_V_LLOYD_MAX"
