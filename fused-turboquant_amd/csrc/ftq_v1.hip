@@ -133,14 +133,33 @@ __global__ __launch_bounds__(256) void v1_store_kernel(
         for (int j = 0; j < nmid; ++j) c += (y >= mids[j]) ? 1 : 0;
         kc[grp][lane * E + i] = (uint8_t)c;
       }
-      // ---- V: optional rotation (rounded back to the value dtype), min/max quantiser
+      // ---- V: optional rotation (rounded back to the value dtype), then
+      // Lloyd-Max codes (flag 2, 4-bit V) or the min/max quantiser
       float v[E];
       load_elems<DT, E>(value, vi * D + lane * E, v);
-      if (v_rotate) {
+      if (v_rotate & 1) {
         fwht_lanes<E, 16>(v, lane);
 #pragma unroll
         for (int i = 0; i < E; ++i) v[i] = round_to_dtype<DT>(v[i] * rscale);
       }
+      if ((v_rotate & 2) && vb == 4) {
+        // norm into the scale field, codes of v / (norm + 1e-8) by the K
+        // midpoint search, 0 in the min field
+        float vs = 0.f;
+#pragma unroll
+        for (int i = 0; i < E; ++i) vs += v[i] * v[i];
+        vs = group_sum<16>(vs);
+        sc = sqrtf(vs + 1e-16f);
+        mn = 0.f;
+        const float vden = sc + 1e-8f;
+#pragma unroll
+        for (int i = 0; i < E; ++i) {
+          const float u = v[i] / vden;
+          int c = 0;
+          for (int j = 0; j < nmid; ++j) c += (u >= mids[j]) ? 1 : 0;
+          vc[grp][lane * E + i] = (uint8_t)c;
+        }
+      } else {
       mn = v[0];
       float mx = v[0];
 #pragma unroll
@@ -160,6 +179,7 @@ __global__ __launch_bounds__(256) void v1_store_kernel(
         // trunc toward zero, clamped; NaN -> 0
         const int q = t >= 1.f ? (int)fminf(t, (float)vtop) : 0;
         vc[grp][lane * E + i] = (uint8_t)q;
+      }
       }
     }
     __syncthreads();
@@ -203,6 +223,7 @@ struct V1Tile {
   uint32_t k[2][A::KQW];  // per S-tile: K code dwords of token (lane & 15), bytes (lane >> 4) * KQ
   uint32_t v[A::NV];      // V codes of the lane's 8 tokens (see v1_load)
   uint32_t tail[2];       // per S-tile: K norm / V scale / V min (by lane >> 4), f16 bits
+  uint32_t vt[2][4];      // Lloyd-Max V only: token (lane & 15)'s V codes, bytes (lane >> 4) * 16 ..
   bool ok[2];             // wave-uniform: S-tile has a real page
 };
 
@@ -226,6 +247,7 @@ struct V1Addr {
   uint32_t s_pos;
   int lbs, max_blocks, seq_len, nb32;  // nb32 = min(num_blocks, 2^31 - 1)
   uint32_t koff, toff, voff;  // lane offsets; token 4g+i of a V load adds i * s_pos (scalar)
+  uint32_t vtoff;              // Lloyd-Max V: token-major V codes of the lane
 };
 
 __device__ __forceinline__ void v1_addr_rows(V1Addr& ad, const int32_t* bt_row, int64_t num_blocks) {
@@ -251,7 +273,7 @@ __device__ __forceinline__ uint32_t buf_u16(__amdgpu_buffer_rsrc_t r, uint32_t v
   return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0);
 }
 
-template <int D, int KB, int VB>
+template <int D, int KB, int VB, bool VLM = false>
 __device__ __forceinline__ void v1_load(V1Tile<D, KB, VB>& r, const V1Addr& ad, int tile, int btv) {
   using A = V1A<D, KB, VB>;
 #pragma unroll
@@ -276,6 +298,10 @@ __device__ __forceinline__ void v1_load(V1Tile<D, KB, VB>& r, const V1Addr& ad, 
       r.k[st][0] = k.x; r.k[st][1] = k.y;
     }
     r.tail[st] = buf_u16(rs, ad.toff, 0);
+    if constexpr (VLM) {
+      const uint4 x = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, ad.vtoff, 0, 0));
+      r.vt[st][0] = x.x; r.vt[st][1] = x.y; r.vt[st][2] = x.z; r.vt[st][3] = x.w;
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       // scalar offset of token 4g+i; uniform, but LLVM otherwise keeps the
@@ -338,7 +364,68 @@ __device__ __forceinline__ void wave_lds_fence() {
   __asm__ volatile("" ::: "memory");
 }
 
-template <int D, int KB, int VB, int QT>
+// Scale of the centroid tables behind the f16 MFMA operands.  A centroid c
+// enters the Q.K MFMAs as f16(sigma c); the scores divide by the norm of the
+// same f16 values (the norm correction), so any error common to all
+// centroids cancels and only the spread of the relative rounding errors
+// (f16(x) - x) / x across the table moves q.c / ||c||.  f16(c) itself has a
+// spread of up to 2^-11, which with keys 8x the typical norm shifts softmax
+// weights by about 0.5%.  sigma = 2^k (1 + j/256), 2^k putting the largest |c|
+// in [512, 1024): every thread tries one j, the workgroup keeps the j with the
+// smallest spread (lowest j on ties; the same on every workgroup).  For the
+// Lloyd-Max tables of 2-, 3- and 4-bit codes the spread drops to about 1e-7,
+// 3e-5 and 2e-4.  Called by all threads; c[0, n) in LDS; red[8] LDS scratch.
+__device__ float cent_scale(const float* c, int n, int tid, float* red) {
+  float mx = 0.f;
+  for (int i = 0; i < n; ++i) mx = fmaxf(mx, fabsf(c[i]));
+  if (!(mx > 0.f) || !(mx < INFINITY)) return 1.f;  // same branch in every thread
+  const int e = (int)((__float_as_uint(mx) >> 23) & 255u);  // mx in [2^(e-127), 2^(e-126))
+  const float p2 = __uint_as_float((uint32_t)min(max(263 - e, 1), 254) << 23);  // 2^(136 - e)
+  const float sg = p2 * (1.f + (float)(tid & 255) * (1.f / 256.f));
+  float rlo = 0.f, rhi = 0.f;
+  for (int i = 0; i < n; ++i) {
+    const float x = sg * c[i];
+    const float r = x != 0.f ? (f16_bits_to_f32(f32_to_f16_bits(x)) - x) / x : 0.f;
+    rlo = fminf(rlo, r);
+    rhi = fmaxf(rhi, r);
+  }
+  // argmin over the workgroup of (spread, j): spread >= 0, so its bits order as the value
+  uint64_t key = ((uint64_t)__float_as_uint(rhi - rlo) << 32) | (uint32_t)(tid & 255);
+  for (int o = 32; o >= 1; o >>= 1) {
+    const uint64_t other = ((uint64_t)(uint32_t)__shfl_xor((int)(key >> 32), o) << 32) |
+                           (uint32_t)__shfl_xor((int)(uint32_t)key, o);
+    key = other < key ? other : key;
+  }
+  uint32_t* r32 = reinterpret_cast<uint32_t*>(red);
+  if ((tid & 63) == 0) {
+    r32[2 * (tid >> 6)] = (uint32_t)(key >> 32);
+    r32[2 * (tid >> 6) + 1] = (uint32_t)key;
+  }
+  __syncthreads();
+  uint64_t best = ~0ull;
+  for (int w = 0; w < 4; ++w) {
+    const uint64_t k = ((uint64_t)r32[2 * w] << 32) | r32[2 * w + 1];
+    best = k < best ? k : best;
+  }
+  return p2 * (1.f + (float)(uint32_t)best * (1.f / 256.f));
+}
+// f16 pairs (a, b): hi | hi << 16 and lo | lo << 16, lo = f16(x - f16(x))
+__device__ __forceinline__ uint2 cent_hilo_pair(float a, float b) {
+  const uint32_t ha = f32_to_f16_bits(a), hb = f32_to_f16_bits(b);
+  const uint32_t la = f32_to_f16_bits(a - f16_bits_to_f32(ha));
+  const uint32_t lb = f32_to_f16_bits(b - f16_bits_to_f32(hb));
+  return make_uint2(ha | (hb << 16), la | (lb << 16));
+}
+
+// VLM: Lloyd-Max V (TURBOQUANT_V_LLOYD_MAX, 4-bit V; reference
+// triton_decode_offset.py:399-419): V = c[code] * ||v||_16 / ||c[codes]||,
+// the K centroids shared.  The V codes become f16 centroid pairs (hi + lo)
+// through a 4-bit pair table, ||c[codes]|| comes from the Gram diagonal of a
+// token-major copy of the codes (as the K norm correction does), and
+// P' = p ||v|| / ||c|| 2^-8 (hi + lo) feeds the P.V MFMA; accumulators are
+// scaled back by 2^8.  With p <= 2^8 and ||c[codes]|| near 1 (unit-norm
+// rotated vectors), P' stays below the f16 maximum for every f16 ||v||.
+template <int D, int KB, int VB, int QT, bool VLM = false>
 __global__ __launch_bounds__(256, 2) void v1_attn_kernel(
     const void* __restrict__ query, const uint8_t* __restrict__ cache,
     const int32_t* __restrict__ block_table, const int32_t* __restrict__ seq_lens,
@@ -355,7 +442,7 @@ __global__ __launch_bounds__(256, 2) void v1_attn_kernel(
 
   // LDS pool, reused in three phases: rotated queries (prologue), the K code
   // pair table (tile loop), the wave-merge buffer (epilogue)
-  constexpr int LUT_BYTES = 4 << (2 * KB);
+  constexpr int LUT_BYTES = 4 << (2 * KB);  // f16 pair f16(sigma c[e & mask]) | f16(sigma c[e >> KB]) << 16
   constexpr int RED_BYTES = 4 * 16 * (D + 1) * 4;
   constexpr int QS_BYTES = 16 * (D + 4) * 4;
   constexpr int POOL0 = LUT_BYTES > RED_BYTES ? LUT_BYTES : RED_BYTES;
@@ -364,12 +451,15 @@ __global__ __launch_bounds__(256, 2) void v1_attn_kernel(
   __shared__ float red_m[4][16], red_l[4][16];
   __shared__ __attribute__((aligned(16))) uint16_t tail_l[4][2][4][16];
   __shared__ __attribute__((aligned(16))) float diag_l[4][2][16];
-  __shared__ uint16_t cent16[16];
+  __shared__ float centl[16];
+  static_assert(!VLM || VB == 4, "Lloyd-Max V needs the 4-bit V layout");
+  __shared__ uint2 lutv[VLM ? 256 : 1];  // Lloyd-Max V: centroid pairs (c[e & 15], c[e >> 4]), hi and lo
+  __shared__ float diagv_l[VLM ? 4 : 1][2][16];   // Lloyd-Max V: sum c^2 per token
   float (*qs)[D + 4] = reinterpret_cast<float (*)[D + 4]>(pool);
   float (*red_o)[16][D + 1] = reinterpret_cast<float (*)[16][D + 1]>(pool);
   uint8_t* lut = pool;
 
-  if (tid < (1 << KB)) cent16[tid] = (uint16_t)f32_to_f16_bits(cent[tid]);
+  if (tid < (1 << KB)) centl[tid] = cent[tid];
   // q_rot = q H / sqrt(D) for the G query heads of this kv head (one per 16 lanes),
   // with scale * log2(e) folded in
   {
@@ -405,8 +495,15 @@ __global__ __launch_bounds__(256, 2) void v1_attn_kernel(
     }
   }
   __syncthreads();  // qs is dead; its LDS now holds the pair table
+  const float csc = cent_scale(centl, 1 << KB, tid, &red_m[0][0]);
+  const float vk = csc * (1.f / 256.f), vinv = 256.f / csc;  // Lloyd-Max V: P' scale and its inverse
   for (int e = tid; e < (1 << (2 * KB)); e += 256)
-    reinterpret_cast<uint32_t*>(lut)[e] = (uint32_t)cent16[e & ((1 << KB) - 1)] | ((uint32_t)cent16[e >> KB] << 16);
+    reinterpret_cast<uint32_t*>(lut)[e] = cent_hilo_pair(csc * centl[e & ((1 << KB) - 1)], csc * centl[e >> KB]).x;
+  if constexpr (VLM) {
+    constexpr int NC = 1 << KB;  // codes >= NC do not occur; they read the top centroid
+    const int c0 = tid & 15, c1 = tid >> 4;
+    lutv[tid] = cent_hilo_pair(csc * centl[c0 < NC ? c0 : NC - 1], csc * centl[c1 < NC ? c1 : NC - 1]);
+  }
   __syncthreads();
 
   const int seq_len = seq_lens[b];
@@ -437,6 +534,7 @@ __global__ __launch_bounds__(256, 2) void v1_attn_kernel(
             (uint32_t)(g == 1 ? A::KPS + A::VDB : (g == 2 ? A::KPS + A::VDB + 2 : A::MSE));
   ad.voff = (uint32_t)(4 * g) * ad.s_pos +
             (VB == 3 ? (uint32_t)((A::KPS + 3 * m) & ~1) : (uint32_t)(A::KPS + VB * m));
+  ad.vtoff = (uint32_t)m * ad.s_pos + (uint32_t)A::KPS + 16u * (uint32_t)g;
   // VB 3: byte selectors that re-align each chunk to its first code bit
   const uint32_t o3 = (uint32_t)((A::KPS + 3 * m) & 1);
   const uint32_t sel0 = o3 | ((o3 + 1) << 8) | ((o3 + 4) << 16) | ((o3 + 5) << 24);
@@ -473,9 +571,33 @@ __global__ __launch_bounds__(256, 2) void v1_attn_kernel(
         const int i = m & 3;
         diag_l[wave][st][m] = i == 0 ? gacc[0] : i == 1 ? gacc[1] : i == 2 ? gacc[2] : gacc[3];
       }
+      if constexpr (VLM) {
+        // sum over the 128 dims of c[code]^2 per token: Gram diagonal of the
+        // token-major V codes through the pair table (MFMA s takes codes 8s..8s+7)
+        floatx4 gv = {0.f, 0.f, 0.f, 0.f}, gv2 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4) {
+          Op8 a, alo;
+#pragma unroll
+          for (int p = 0; p < 4; ++p) {
+            const uint2 e = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint8_t*>(lutv) +
+                                                            field_off<3>(cur.vt[st], (8 * s4 + 2 * p) * 4, 8));
+            a.u[p] = e.x;
+            alo.u[p] = e.y;
+          }
+          gv = __builtin_amdgcn_mfma_f32_16x16x32_f16(a.h, a.h, gv, 0, 0, 0);
+          gv2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo.h, a.h, gv2, 0, 0, 0);
+        }
+        if ((m >> 2) == g) {
+          const int i = m & 3;
+          const floatx4 gd = gv + 2.f * gv2;
+          diagv_l[wave][st][m] = i == 0 ? gd[0] : i == 1 ? gd[1] : i == 2 ? gd[2] : gd[3];
+        }
+      }
     }
     wave_lds_fence();
     float s[2][4];
+    float dvv[2][4];      // Lloyd-Max V: sum c^2 of token 4g+i
     uint2 scw[2], zw[2];  // f16 pairs: tokens (4g, 4g+1), (4g+2, 4g+3)
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
@@ -484,6 +606,10 @@ __global__ __launch_bounds__(256, 2) void v1_attn_kernel(
       zw[st] = *reinterpret_cast<const uint2*>(&tail_l[wave][st][2][4 * g]);
       const float4 dg = *reinterpret_cast<const float4*>(&diag_l[wave][st][4 * g]);
       const float dga[4] = {dg.x, dg.y, dg.z, dg.w};
+      if constexpr (VLM) {
+        const float4 dv = *reinterpret_cast<const float4*>(&diagv_l[wave][st][4 * g]);
+        dvv[st][0] = dv.x; dvv[st][1] = dv.y; dvv[st][2] = dv.z; dvv[st][3] = dv.w;
+      }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const uint32_t kw = (i < 2 ? kn.x : kn.y) >> (16 * (i & 1));
@@ -522,6 +648,28 @@ __global__ __launch_bounds__(256, 2) void v1_attn_kernel(
     float psum = 0.f;
     Op8 pb, pl;
     uint32_t ex[4];  // per P.V operand pair: the two tokens' V-scale exponent fields
+    if constexpr (VLM) {
+      // P' = p ||v||_16 / sqrt(sum x^2 + 1e-16) 2^(k-8) for the scaled centroids x = c 2^k, hi + lo
+#pragma unroll
+      for (int st = 0; st < 2; ++st) {
+        uint32_t h16[4], l16[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float p = __builtin_amdgcn_exp2f(s[st][i] - m_run);
+          psum += p;
+          const uint32_t vw = (i < 2 ? scw[st].x : scw[st].y) >> (16 * (i & 1));
+          const float vn = (float)__builtin_bit_cast(_Float16, (uint16_t)vw);
+          const float u = p * vn * __builtin_amdgcn_rsqf(dvv[st][i] + 1e-16f) * vk;
+          const _Float16 uh = (_Float16)u;
+          h16[i] = __builtin_bit_cast(uint16_t, uh);
+          l16[i] = __builtin_bit_cast(uint16_t, (_Float16)(u - (float)uh));
+        }
+        pb.u[2 * st] = h16[0] | (h16[1] << 16);
+        pb.u[2 * st + 1] = h16[2] | (h16[3] << 16);
+        pl.u[2 * st] = l16[0] | (l16[1] << 16);
+        pl.u[2 * st + 1] = l16[2] | (l16[3] << 16);
+      }
+    } else {
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
       uint32_t h16[4], l16[4];
@@ -557,6 +705,7 @@ __global__ __launch_bounds__(256, 2) void v1_attn_kernel(
       pl.u[2 * st] = l16[0] | (l16[1] << 16);
       pl.u[2 * st + 1] = l16[2] | (l16[3] << 16);
     }
+    }
     l_run += psum;
     uint32_t w3[8];
     if constexpr (VB == 3) {
@@ -569,8 +718,24 @@ __global__ __launch_bounds__(256, 2) void v1_attn_kernel(
 #pragma unroll
     for (int bb = 0; bb < NB; ++bb) {
       Op8 a;
+      if constexpr (VLM) {
+        // pair j: the 4-bit codes of dim 8m + bb of its two tokens -> f16 centroid
+        // pair (hi), plus its remainder (lo) against P'_hi
+        Op8 alo;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) a.u[j] = v1_vpair<VB>(cur.v, w3, j, bb, ex[j]);
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t X = bb < 4 ? cur.v[j] : cur.v[4 + j];
+          const uint32_t idx = __builtin_amdgcn_ubfe(X, 4 * (bb & 3), 4) |
+                               (__builtin_amdgcn_ubfe(X, 16 + 4 * (bb & 3), 4) << 4);
+          const uint2 e = lutv[idx];
+          a.u[j] = e.x;
+          alo.u[j] = e.y;
+        }
+        acc[bb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo.h, pb.h, acc[bb], 0, 0, 0);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) a.u[j] = v1_vpair<VB>(cur.v, w3, j, bb, ex[j]);
+      }
       acc[bb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a.h, pb.h, acc[bb], 0, 0, 0);
       acc[bb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a.h, pl.h, acc[bb], 0, 0, 0);
     }
@@ -582,18 +747,18 @@ __global__ __launch_bounds__(256, 2) void v1_attn_kernel(
   int tile = t_begin + wave_u;
   int btv = 0;
   if (tile < t_end) {
-    v1_load(ra, ad, tile, v1_fetch_bt(ad, tile, true, lane));
+    v1_load<D, KB, VB, VLM>(ra, ad, tile, v1_fetch_bt(ad, tile, true, lane));
     btv = v1_fetch_bt(ad, tile + 4, tile + 4 < t_end, lane);
   }
   while (tile < t_end) {
     int btn = v1_fetch_bt(ad, tile + 8, tile + 8 < t_end, lane);
-    v1_load(rb, ad, tile + 4, btv);
+    v1_load<D, KB, VB, VLM>(rb, ad, tile + 4, btv);
     btv = btn;
     process(ra, tile);
     tile += 4;
     if (tile >= t_end) break;
     btn = v1_fetch_bt(ad, tile + 8, tile + 8 < t_end, lane);
-    v1_load(ra, ad, tile + 4, btv);
+    v1_load<D, KB, VB, VLM>(ra, ad, tile + 4, btv);
     btv = btn;
     process(rb, tile);
     tile += 4;
@@ -613,7 +778,7 @@ __global__ __launch_bounds__(256, 2) void v1_attn_kernel(
   for (int bb = 0; bb < NB; ++bb)
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      red_o[wave][m][8 * (4 * g + i) + bb] = __builtin_fmaf(acc[bb][i] - u_tot, VSC, z_tot);
+      red_o[wave][m][8 * (4 * g + i) + bb] = VLM ? acc[bb][i] * vinv : __builtin_fmaf(acc[bb][i] - u_tot, VSC, z_tot);
   __syncthreads();
 
   const int64_t row0 = ((int64_t)b * hq + kvh * G) * num_splits + split;  // (b, head 0 of the group, split)
@@ -678,7 +843,7 @@ __global__ __launch_bounds__(256, VB == 2 ? 4 : 2) void v1_attn_g4_kernel(
   const int m = lane & 15, g = lane >> 4;      // MFMA layout: row / column m, k-group g
   const int ci = (lane >> 2) & 3;  // compact layout: head lane & 3, token 4g + ci
 
-  constexpr int LUT_BYTES = 4 << (2 * KB);
+  constexpr int LUT_BYTES = 4 << (2 * KB);  // f16 pair f16(sigma c[e & mask]) | f16(sigma c[e >> KB]) << 16
   constexpr int RED_BYTES = 4 * G * (D + 1) * 4;
   constexpr int QS_BYTES = G * (D + 4) * 4;
   constexpr int POOL0 = LUT_BYTES > RED_BYTES ? LUT_BYTES : RED_BYTES;
@@ -687,12 +852,12 @@ __global__ __launch_bounds__(256, VB == 2 ? 4 : 2) void v1_attn_g4_kernel(
   __shared__ float red_m[4][G], red_l[4][G];
   __shared__ __attribute__((aligned(16))) uint16_t tail_l[4][2][4][16];  // [wave][S-tile][field][token]
   __shared__ __attribute__((aligned(16))) float diag_l[4][2][64][4];  // [wave][S-tile][lane][register]
-  __shared__ uint16_t cent16[16];
+  __shared__ float centl[16];
   float (*qs)[D + 4] = reinterpret_cast<float (*)[D + 4]>(pool);
   float (*red_o)[G][D + 1] = reinterpret_cast<float (*)[G][D + 1]>(pool);
   uint8_t* lut = pool;
 
-  if (tid < (1 << KB)) cent16[tid] = (uint16_t)f32_to_f16_bits(cent[tid]);
+  if (tid < (1 << KB)) centl[tid] = cent[tid];
   {
     const int gg = tid >> 4, l16 = tid & 15;
     if (gg < G) {
@@ -704,23 +869,34 @@ __global__ __launch_bounds__(256, VB == 2 ? 4 : 2) void v1_attn_g4_kernel(
     }
   }
   __syncthreads();
+  // B operand of the Q.K MFMAs: column n < G holds f16(q) of head n, column
+  // G + n its remainder q - f16(q); the two score columns are summed after the
+  // K loop, so q enters in about fp32 precision at no extra MFMA
   Op8 qb[NS];
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       uint32_t w = 0;
-      if (m < G) {
-        const _Float16 a0 = (_Float16)qs[m][g * (D / 4) + 8 * s + 2 * j];
-        const _Float16 a1 = (_Float16)qs[m][g * (D / 4) + 8 * s + 2 * j + 1];
-        w = (uint32_t)__builtin_bit_cast(uint16_t, a0) | ((uint32_t)__builtin_bit_cast(uint16_t, a1) << 16);
+      if (m < 2 * G) {
+        const int h = m < G ? m : m - G;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const float x = qs[h][g * (D / 4) + 8 * s + 2 * j + e];
+          const _Float16 hi = (_Float16)x;
+          const _Float16 v = m < G ? hi : (_Float16)(x - (float)hi);
+          w |= (uint32_t)__builtin_bit_cast(uint16_t, v) << (16 * e);
+        }
       }
       qb[s].u[j] = w;
     }
   }
   __syncthreads();
-  for (int e = tid; e < (1 << (2 * KB)); e += 256)
-    reinterpret_cast<uint32_t*>(lut)[e] = (uint32_t)cent16[e & ((1 << KB) - 1)] | ((uint32_t)cent16[e >> KB] << 16);
+  {
+    const float csc = cent_scale(centl, 1 << KB, tid, &red_m[0][0]);
+    for (int e = tid; e < (1 << (2 * KB)); e += 256)
+      reinterpret_cast<uint32_t*>(lut)[e] = cent_hilo_pair(csc * centl[e & ((1 << KB) - 1)], csc * centl[e >> KB]).x;
+  }
   __syncthreads();
 
   const int seq_len = seq_lens[b];
@@ -784,10 +960,14 @@ __global__ __launch_bounds__(256, VB == 2 ? 4 : 2) void v1_attn_g4_kernel(
       *reinterpret_cast<floatx4*>(&diag_l[wave][st][lane][0]) = gacc;
     }
     wave_lds_fence();
-    // scores to the compact layout: lane 16g + 4i + n <- lane 16g + n, register i
+    // score column n += column n + G (the q remainder), then to the compact
+    // layout: lane 16g + 4i + n <- lane 16g + n, register i
     float sc_[2];
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        sacc[st][i] += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sacc[st][i]), 0x100 + G, 0xF, 0xF, true));
       int x = __float_as_int(sacc[st][0]);
       x = __builtin_amdgcn_update_dpp(x, __float_as_int(sacc[st][1]), 0x114, 0xF, 0x2, false);
       x = __builtin_amdgcn_update_dpp(x, __float_as_int(sacc[st][2]), 0x118, 0xF, 0x4, false);
@@ -1023,6 +1203,17 @@ struct V1Args {
 template <int D, int KB, int VB>
 static hipError_t v1_launch_attn3(const V1Args& a, hipStream_t st) {
   dim3 grid(a.splits, a.hkv, a.B), block(256);
+  if constexpr (VB == 4) {
+    if (a.vrot & 2) {  // Lloyd-Max V codes
+      if (a.qt == F32)
+        v1_attn_kernel<D, KB, VB, F32, true><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.ks, a.hq, a.hkv, a.lbs, a.max_blocks, a.nb, a.sblk, a.spos, a.shead, a.cent, a.qscale, a.splits, a.wo, a.wl);
+      else if (a.qt == F16)
+        v1_attn_kernel<D, KB, VB, F16, true><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.ks, a.hq, a.hkv, a.lbs, a.max_blocks, a.nb, a.sblk, a.spos, a.shead, a.cent, a.qscale, a.splits, a.wo, a.wl);
+      else
+        v1_attn_kernel<D, KB, VB, BF16, true><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.ks, a.hq, a.hkv, a.lbs, a.max_blocks, a.nb, a.sblk, a.spos, a.shead, a.cent, a.qscale, a.splits, a.wo, a.wl);
+      goto merge;
+    }
+  }
   if (a.hq == 4 * a.hkv) {
     if (a.qt == F32)
       v1_attn_g4_kernel<D, KB, VB, F32><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.ks, a.hq, a.hkv, a.lbs, a.max_blocks, a.nb, a.sblk, a.spos, a.shead, a.cent, a.qscale, a.splits, a.wo, a.wl);
@@ -1036,11 +1227,12 @@ static hipError_t v1_launch_attn3(const V1Args& a, hipStream_t st) {
     v1_attn_kernel<D, KB, VB, F16><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.ks, a.hq, a.hkv, a.lbs, a.max_blocks, a.nb, a.sblk, a.spos, a.shead, a.cent, a.qscale, a.splits, a.wo, a.wl);
   else
     v1_attn_kernel<D, KB, VB, BF16><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.ks, a.hq, a.hkv, a.lbs, a.max_blocks, a.nb, a.sblk, a.spos, a.shead, a.cent, a.qscale, a.splits, a.wo, a.wl);
+merge:
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int64_t rows = (int64_t)a.B * a.hq;
   const float rs = fwht_scale(D);
-  if (a.vrot) {
+  if (a.vrot & 1) {
     if (a.ot == F32) return launch_merge_splits<D, F32, ROT_PLAIN>(a.wo, a.wl, rows, a.splits, nullptr, rs, a.out, st, a.lse);
     if (a.ot == F16) return launch_merge_splits<D, F16, ROT_PLAIN>(a.wo, a.wl, rows, a.splits, nullptr, rs, a.out, st, a.lse);
     return launch_merge_splits<D, BF16, ROT_PLAIN>(a.wo, a.wl, rows, a.splits, nullptr, rs, a.out, st, a.lse);
@@ -1081,6 +1273,7 @@ extern "C" int ftq_v1_store(const void* key, const void* value, int dtype, int64
   FTQ_REQUIRE(n_tokens >= 0 && num_kv_heads > 0 && num_blocks >= 0 && block_size > 0,
               "bad token / head / block counts");
   FTQ_REQUIRE(dtype >= F32 && dtype <= BF16, "dtype must be FTQ_F32, FTQ_F16 or FTQ_BF16");
+  FTQ_REQUIRE(v_rotate >= 0 && v_rotate <= 3, "v_rotate: bit 0 = rotate V, bit 1 = Lloyd-Max V codes");
   const V1Geom g = v1_geom(d, key_bits, value_bits);
   FTQ_REQUIRE(stride_head >= g.raw, "stride_head is smaller than the slot bytes (see ftq_v1_slot_bytes)");
   FTQ_REQUIRE(stride_pos >= stride_head * num_kv_heads && stride_block >= stride_pos * block_size,
@@ -1094,11 +1287,11 @@ extern "C" int ftq_v1_store(const void* key, const void* value, int dtype, int64
   hipStream_t st = (hipStream_t)stream;
   hipError_t e;
   if (d == 64)
-    e = v1_launch_store<64>(key, value, dtype, n_tokens, num_kv_heads, midpoints, key_bits, value_bits, v_rotate != 0, slot_mapping, kv_cache, num_blocks, block_size, stride_block, stride_pos, stride_head, st);
+    e = v1_launch_store<64>(key, value, dtype, n_tokens, num_kv_heads, midpoints, key_bits, value_bits, v_rotate, slot_mapping, kv_cache, num_blocks, block_size, stride_block, stride_pos, stride_head, st);
   else if (d == 128)
-    e = v1_launch_store<128>(key, value, dtype, n_tokens, num_kv_heads, midpoints, key_bits, value_bits, v_rotate != 0, slot_mapping, kv_cache, num_blocks, block_size, stride_block, stride_pos, stride_head, st);
+    e = v1_launch_store<128>(key, value, dtype, n_tokens, num_kv_heads, midpoints, key_bits, value_bits, v_rotate, slot_mapping, kv_cache, num_blocks, block_size, stride_block, stride_pos, stride_head, st);
   else
-    e = v1_launch_store<256>(key, value, dtype, n_tokens, num_kv_heads, midpoints, key_bits, value_bits, v_rotate != 0, slot_mapping, kv_cache, num_blocks, block_size, stride_block, stride_pos, stride_head, st);
+    e = v1_launch_store<256>(key, value, dtype, n_tokens, num_kv_heads, midpoints, key_bits, value_bits, v_rotate, slot_mapping, kv_cache, num_blocks, block_size, stride_block, stride_pos, stride_head, st);
   return hip_status(e);
 }
 
@@ -1119,6 +1312,7 @@ extern "C" int ftq_v1_decode_attention_lse(
     int value_bits, float scale, int v_rotate, int num_splits, void* workspace,
     int64_t workspace_bytes, void* out, int out_dtype, float* lse_out, void* stream) {
   FTQ_REQUIRE(d == 128, "v1 decode attention: head_dim must be 128");
+  FTQ_REQUIRE(v_rotate >= 0 && v_rotate <= 3, "v_rotate: bit 0 = un-rotate V, bit 1 = Lloyd-Max V codes");
   FTQ_REQUIRE(key_bits >= 2 && key_bits <= 4 && value_bits >= 2 && value_bits <= 4,
               "v1 decode attention: key_bits and value_bits must be 2, 3 or 4");
   FTQ_REQUIRE(block_size >= 16 && block_size <= 4096 && (block_size & (block_size - 1)) == 0,
@@ -1154,7 +1348,7 @@ extern "C" int ftq_v1_decode_attention_lse(
   a.nb = num_blocks; a.sblk = stride_block; a.spos = stride_pos; a.shead = stride_head;
   a.cent = centroids;
   a.qscale = fwht_scale(d) * scale * 1.4426950408889634f;
-  a.splits = num_splits; a.vrot = v_rotate != 0;
+  a.splits = num_splits; a.vrot = v_rotate;
   a.wo = static_cast<float*>(workspace);
   a.wl = a.wo + (int64_t)batch * num_q_heads * num_splits * d;
   a.out = out; a.ot = out_dtype; a.lse = lse_out;

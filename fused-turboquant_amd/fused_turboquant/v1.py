@@ -128,11 +128,19 @@ def _strides(kv_cache: torch.Tensor):
     return kv_cache.stride(0), kv_cache.stride(1), kv_cache.stride(2)
 
 
+def _v_flags(v_rotate: bool, v_lloyd_max: bool) -> int:
+    # the C ABI's v_rotate word: bit 0 rotates V, bit 1 selects Lloyd-Max V codes
+    return (1 if (v_rotate or v_lloyd_max) else 0) | (2 if v_lloyd_max else 0)
+
+
 def v1_store(key: torch.Tensor, value: torch.Tensor, kv_cache: torch.Tensor,
              slot_mapping: torch.Tensor, midpoints: torch.Tensor, key_bits: int,
-             value_bits: int, v_rotate: bool = False) -> None:
+             value_bits: int, v_rotate: bool = False, v_lloyd_max: bool = False) -> None:
     """Quantise ``key``/``value`` [n, Hkv, d] into their slots (``slot_mapping`` [n]
-    int64; negative entries are skipped)."""
+    int64; negative entries are skipped).  ``v_lloyd_max`` (implies
+    ``v_rotate``): 4-bit V takes Lloyd-Max codes against the K midpoints and its
+    norm in the scale field (reference ``triton_inkernel_store.py:159-200``);
+    other V widths keep the uniform codes."""
     n, hkv, d = key.shape
     _check_bits(d, key_bits, value_bits)
     if value.shape != key.shape:
@@ -156,7 +164,7 @@ def v1_store(key: torch.Tensor, value: torch.Tensor, kv_cache: torch.Tensor,
     L = _bind()
     _lib.check(L.ftq_v1_store(
         k.data_ptr(), v.data_ptr(), _lib.dtype_code(k.dtype), n, hkv, d, mids.data_ptr(),
-        key_bits, value_bits, int(bool(v_rotate)), slot_mapping.contiguous().data_ptr(),
+        key_bits, value_bits, _v_flags(v_rotate, v_lloyd_max), slot_mapping.contiguous().data_ptr(),
         kv_cache.data_ptr(), nb, bs, sb, sp, sh, _lib.stream_ptr(dev)))
 
 
@@ -171,6 +179,7 @@ def workspace_bytes(batch: int, num_q_heads: int, head_dim: int, num_splits: int
 def v1_decode_attention(query: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.Tensor,
                         seq_lens: torch.Tensor, centroids: torch.Tensor, key_bits: int,
                         value_bits: int, scale: float | None = None, v_rotate: bool = False,
+                        v_lloyd_max: bool = False,
                         kv_start: torch.Tensor | None = None, num_splits: int | None = None,
                         max_seq_len: int | None = None, out: torch.Tensor | None = None,
                         workspace: torch.Tensor | None = None, lse: torch.Tensor | None = None) -> torch.Tensor:
@@ -225,7 +234,7 @@ def v1_decode_attention(query: torch.Tensor, kv_cache: torch.Tensor, block_table
     args = (q.data_ptr(), _lib.dtype_code(q.dtype), kv_cache.data_ptr(), nb, bs, sb, sp, sh,
             bt.data_ptr(), bt.shape[1], seq_lens.contiguous().data_ptr(),
             ks.data_ptr() if ks is not None else None, B, hq, hkv, d, cent.data_ptr(), key_bits,
-            value_bits, float(scale), int(bool(v_rotate)), int(num_splits), workspace.data_ptr(),
+            value_bits, float(scale), _v_flags(v_rotate, v_lloyd_max), int(num_splits), workspace.data_ptr(),
             workspace.numel(), out.data_ptr(), _lib.dtype_code(out.dtype))
     if lse is None:
         _lib.check(L.ftq_v1_decode_attention(*args, _lib.stream_ptr(dev)))
@@ -240,12 +249,13 @@ class TurboQuantV1Layer:
     V-rotation switch (``TURBOQUANT_V_ROTATE``, ``v1_backend.py:733-740``)."""
 
     def __init__(self, head_dim: int, key_bits: int, value_bits: int, v_rotate: bool = False,
-                 centroids: torch.Tensor | None = None, device="cuda"):
+                 centroids: torch.Tensor | None = None, device="cuda", v_lloyd_max: bool = False):
         _check_bits(head_dim, key_bits, value_bits)
         self.head_dim = head_dim
         self.key_bits = key_bits
         self.value_bits = value_bits
-        self.v_rotate = bool(v_rotate)
+        self.v_lloyd_max = bool(v_lloyd_max)
+        self.v_rotate = bool(v_rotate) or self.v_lloyd_max
         c = centroids if centroids is not None else default_centroids(head_dim, key_bits)
         if c.numel() != (1 << key_bits):
             raise ValueError("centroids must have 2^key_bits entries")
@@ -258,11 +268,12 @@ class TurboQuantV1Layer:
 
     def store(self, key, value, kv_cache, slot_mapping) -> None:
         v1_store(key, value, kv_cache, slot_mapping, self.midpoints, self.key_bits,
-                 self.value_bits, self.v_rotate)
+                 self.value_bits, self.v_rotate, self.v_lloyd_max)
 
     def decode(self, query, kv_cache, block_table, seq_lens, **kw) -> torch.Tensor:
         return v1_decode_attention(query, kv_cache, block_table, seq_lens, self.centroids,
-                                   self.key_bits, self.value_bits, v_rotate=self.v_rotate, **kw)
+                                   self.key_bits, self.value_bits, v_rotate=self.v_rotate,
+                                   v_lloyd_max=self.v_lloyd_max, **kw)
 
 
 # --------------------------------------------------------------------------

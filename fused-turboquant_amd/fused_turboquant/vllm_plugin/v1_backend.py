@@ -212,8 +212,8 @@ class FusedTurboQuantV1Impl(_ImplBase):
         self.v_rotate = not self._is_raw and (env_flag("TURBOQUANT_V_ROTATE") or env_flag("TURBOQUANT_V_LLOYD_MAX"))
         self.defer_prefill = not self._is_raw and env_flag("TURBOQUANT_DEFER_PREFILL")
         self._prefix_capacity = _defer_capacity() if self.defer_prefill else 0
-        if env_flag("TURBOQUANT_V_LLOYD_MAX") and not self._is_raw:
-            raise NotImplementedError("TURBOQUANT_V_LLOYD_MAX (Lloyd-Max V codes) is not part of this build")
+        # Lloyd-Max V codes (4-bit V; other widths stay uniform but rotated, as in the reference)
+        self.v_lloyd_max = not self._is_raw and env_flag("TURBOQUANT_V_LLOYD_MAX")
 
     # -- per-layer state ---------------------------------------------------
     def _state(self, layer, device) -> V1.TurboQuantV1Layer:
@@ -223,7 +223,8 @@ class FusedTurboQuantV1Impl(_ImplBase):
             if cent is not None and cent.numel() != (1 << self.key_bits):
                 cent = None
             st = V1.TurboQuantV1Layer(self.head_size, self.key_bits, self.value_bits,
-                                      v_rotate=self.v_rotate, centroids=cent, device=device)
+                                      v_rotate=self.v_rotate, centroids=cent, device=device,
+                                      v_lloyd_max=self.v_lloyd_max)
             layer._fused_tq_state = st
         return st
 
@@ -322,7 +323,8 @@ class FusedTurboQuantV1Impl(_ImplBase):
         o2 = torch.empty(B, hq, d, dtype=torch.float32, device=dev)
         l2 = torch.empty(B, hq, dtype=torch.float32, device=dev)
         V1.v1_decode_attention(q, kv_cache, bt, sl, st.centroids, self.key_bits, self.value_bits,
-                               scale=self.scale, v_rotate=self.v_rotate, kv_start=plen.expand(B).contiguous(),
+                               scale=self.scale, v_rotate=self.v_rotate, v_lloyd_max=self.v_lloyd_max,
+                               kv_start=plen.expand(B).contiguous(),
                                max_seq_len=msl, out=o2, lse=l2)
         # merge (a row empty in both phases stays 0)
         m = torch.maximum(l1, l2)
@@ -338,7 +340,8 @@ class FusedTurboQuantV1Impl(_ImplBase):
         if self._is_raw:
             return RAW.raw_decode_attention(q, kv_cache, bt, sl, scale=self.scale, max_seq_len=msl)
         return V1.v1_decode_attention(q, kv_cache, bt, sl, st.centroids, self.key_bits, self.value_bits,
-                                      scale=self.scale, v_rotate=self.v_rotate, max_seq_len=msl)
+                                      scale=self.scale, v_rotate=self.v_rotate, v_lloyd_max=self.v_lloyd_max,
+                                      max_seq_len=msl)
 
     def _prefill(self, q, k, v, kv_cache, md, nd, ndt, st):
         """Prefill sequences nd.. of the batch (tokens ndt..N)."""

@@ -172,6 +172,11 @@ int64_t ftq_v1_slot_bytes(int d, int key_bits, int value_bits);
  * against `midpoints` (2^key_bits - 1 sorted float32; code = number of
  * midpoints <= y), norm stored fp16; V (rotated first and rounded back to
  * dtype when v_rotate) quantised uniformly between its min and max.
+ * v_rotate is a bit set: bit 0 rotates V; bit 1 (value_bits 4 only, with
+ * bit 0) stores V as Lloyd-Max codes instead (TURBOQUANT_V_LLOYD_MAX): the
+ * rotated V is normalised and coded against `midpoints` like K, its fp16 norm
+ * goes to the scale field and 0 to the min field (v1_backend.py:736-749,
+ * triton_inkernel_store.py:159-200).
  * slot_mapping[i] < 0 skips token i.  Replaces _launch_rht / _fused_store_rht
  * (vllm_plugin/triton_inkernel_store.py:376-440, 554-616) and the V
  * pre-rotation of _launch_store (v1_backend.py:712-749).  One launch.
@@ -193,7 +198,9 @@ int ftq_v1_default_splits(int batch, int num_kv_heads, int max_seq_len);
  * NULL = 0), kv head = h / (Hq/Hkv); scores use the rotated query q H/sqrt(d)
  * against the norm-corrected centroids (2^key_bits sorted float32) times the
  * fp16 K norm; V = code * scale + min; with v_rotate the output is multiplied
- * by H/sqrt(d).  Rows with no positions give 0.  Replaces the stage-1 kernel
+ * by H/sqrt(d).  v_rotate bit 1 (as in ftq_v1_store) reads Lloyd-Max V
+ * codes: V = c[code] * ||v|| / ||c[codes]|| (triton_decode_offset.py:399-419).
+ * Rows with no positions give 0.  Replaces the stage-1 kernel
  * _tq_decode_stage1_offset (vllm_plugin/triton_decode_offset.py:42-442), the
  * stage-2 merge, the un-rotation and the output cast of
  * _decode_attention_offset_only (v1_backend.py:975-1093).  Head dim 128.

@@ -441,13 +441,28 @@ def v1_round_dtype(x: np.ndarray, dtype: str) -> np.ndarray:
     raise ValueError(dtype)
 
 
+def v1_quantize_v_lloyd(v: np.ndarray, midpoints: np.ndarray):
+    """Lloyd-Max V codes (TURBOQUANT_V_LLOYD_MAX, 4-bit V;
+    triton_inkernel_store.py:159-200): norm = sqrt(sum v^2 + 1e-16),
+    u = v / (norm + 1e-8), code = the K midpoint search on u (``>=`` going up).
+    Returns (codes u8, norm f32, u f32)."""
+    v = np.asarray(v, np.float32)
+    v64 = v.astype(np.float64)
+    norm = np.sqrt(np.sum(v64 * v64, axis=-1) + 1e-16).astype(np.float32)
+    u = (v / (norm[..., None] + np.float32(1e-8))).astype(np.float32)
+    return v1_quantize_k(u, midpoints), norm, u
+
+
 def v1_store(key: np.ndarray, value: np.ndarray, slot_mapping: np.ndarray, kv_cache: np.ndarray,
              midpoints: np.ndarray, kb: int, vb: int, v_rotate: bool = False,
-             value_dtype: str = "f32"):
+             value_dtype: str = "f32", v_lloyd_max: bool = False):
     """Write [N, H, d] float32 K/V (already converted from their dtype) into
     ``kv_cache`` uint8[nb, bs, H, slot] in place.  Negative slots are skipped
     (triton_inkernel_store.py:394-395).  With ``v_rotate`` V is first rotated
     by M = H/sqrt(d) and rounded back to the value dtype (v1_backend.py:736-740).
+    With ``v_lloyd_max`` and 4-bit V, V takes Lloyd-Max codes against the K
+    midpoints, its norm goes in the scale field and the min field is 0
+    (triton_inkernel_store.py:159-200); other V widths keep the uniform codes.
 
     Returns a dict of per-(token, head) intermediates for tie accounting.
     """
@@ -461,7 +476,11 @@ def v1_store(key: np.ndarray, value: np.ndarray, slot_mapping: np.ndarray, kv_ca
     kcodes = v1_quantize_k(y, midpoints)
     if v_rotate:
         value = v1_round_dtype((fwht_unscaled(value) * fwht_scale(d)).astype(np.float32), value_dtype)
-    vq, sc, mn, t = v1_quantize_v(value, vb)
+    if v_lloyd_max and vb == 4:
+        vq, sc, t = v1_quantize_v_lloyd(value, midpoints)
+        mn = np.zeros_like(sc)
+    else:
+        vq, sc, mn, t = v1_quantize_v(value, vb)
     kp = pack(kcodes, kb)
     vp = pack(vq, vb)
     n16 = norm.astype(np.float16).view(np.uint8).reshape(N, H, 2)
@@ -495,15 +514,23 @@ def v1_unpack(kv_cache: np.ndarray, d: int, kb: int, vb: int):
 
 
 def v1_dequant(kv_cache: np.ndarray, d: int, kb: int, vb: int, centroids: np.ndarray,
-               norm_correction: bool = True):
+               norm_correction: bool = True, v_lloyd_max: bool = False):
     """Per-slot reconstructions in the rotated domain (float64):
     K^ = ||k||_16 * c / sqrt(sum c^2 + 1e-16)  (triton_decode_offset.py:210-242),
-    V^ = q * scale_16 + zero_16               (:256-428)."""
+    V^ = q * scale_16 + zero_16               (:256-428), or with
+    ``v_lloyd_max`` and 4-bit V V^ = ||v||_16 * c_v / sqrt(sum c_v^2 + 1e-16)
+    (:399-419; the scale field holds ||v||, the K centroids are shared)."""
     kc, kn, vc, sc, zr = v1_unpack(kv_cache, d, kb, vb)
-    c = np.sort(np.asarray(centroids, np.float32)).astype(np.float64)[kc]
+    cs = np.sort(np.asarray(centroids, np.float32)).astype(np.float64)
+    c = cs[kc]
     if norm_correction:
         c = c / np.sqrt(np.sum(c * c, axis=-1, keepdims=True) + 1e-16)
     k_hat = c * kn.astype(np.float64)[..., None]
+    if v_lloyd_max and vb == 4:
+        cv = cs[np.minimum(vc, cs.size - 1)]
+        if norm_correction:
+            cv = cv / np.sqrt(np.sum(cv * cv, axis=-1, keepdims=True) + 1e-16)
+        return k_hat, cv * sc.astype(np.float64)[..., None]
     v_hat = vc.astype(np.float64) * sc.astype(np.float64)[..., None] + zr.astype(np.float64)[..., None]
     return k_hat, v_hat
 
@@ -511,7 +538,7 @@ def v1_dequant(kv_cache: np.ndarray, d: int, kb: int, vb: int, centroids: np.nda
 def v1_decode_attention(q: np.ndarray, kv_cache: np.ndarray, block_table: np.ndarray,
                         seq_lens: np.ndarray, centroids: np.ndarray, kb: int, vb: int,
                         scale: float, kv_start=None, v_rotate: bool = False,
-                        norm_correction: bool = True):
+                        norm_correction: bool = True, v_lloyd_max: bool = False):
     """Decode attention over the v1 slot cache, float64.
 
     q [B, Hq, d] (float32 values of the query); q_rot = q @ M with
@@ -527,7 +554,7 @@ def v1_decode_attention(q: np.ndarray, kv_cache: np.ndarray, block_table: np.nda
     G = Hq // Hkv
     M = sylvester(d) / math.sqrt(d)
     q_rot = q @ M
-    k_hat, v_hat = v1_dequant(kv_cache, d, kb, vb, centroids, norm_correction)
+    k_hat, v_hat = v1_dequant(kv_cache, d, kb, vb, centroids, norm_correction, v_lloyd_max)
     out = np.zeros((B, Hq, d))
     for b in range(B):
         L = int(seq_lens[b])

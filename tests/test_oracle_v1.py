@@ -230,3 +230,58 @@ def test_hybrid_equals_two_phase_lse_merge(v_rotate):
     assert np.allclose(got, want, atol=1e-10)
     # sequence 1 sees no prefix: exactly the kv_start decode
     assert np.allclose(got[1], o2[1], atol=1e-12)
+
+
+def test_v_lloyd_max_store_fields_and_codes():
+    """TURBOQUANT_V_LLOYD_MAX (triton_inkernel_store.py:159-200): codes by brute
+    force (#{K midpoints m : m <= v / (||v|| + 1e-8)}), the norm in the scale
+    field, a zero min field; and 2/3-bit V fall through to the uniform codes."""
+    rng = np.random.default_rng(31)
+    d, kb, H, N = 128, 4, 2, 24
+    c = O.lloyd_max_codebook(d, kb)[1].astype(np.float32)
+    mids = O.v1_midpoints(c)
+    g = O.v1_geometry(d, kb, 4)
+    k = rng.standard_normal((N, H, d)).astype(np.float32)
+    v = (rng.standard_normal((N, H, d)) * 3).astype(np.float32)
+    cache = np.zeros((4, 8, H, g["slot"]), np.uint8)
+    st = O.v1_store(k, v, np.arange(N), cache, mids, kb, 4, v_rotate=True, v_lloyd_max=True)
+    vv = st["value"]  # rotated, as stored
+    for i in range(0, N, 5):
+        for h in range(H):
+            x = vv[i, h].astype(np.float64)
+            nrm = np.float32(np.sqrt((x * x).sum() + 1e-16))
+            u = (vv[i, h] / (nrm + np.float32(1e-8))).astype(np.float32)
+            want = np.array([sum(1 for m in mids if m <= e) for e in u])
+            assert np.array_equal(st["vcodes"][i, h], want)
+    kc, kn, vc, sc, zr = O.v1_unpack(cache, d, kb, 4)
+    blk, off = np.arange(N) // 8, np.arange(N) % 8
+    assert np.array_equal(sc[blk, off], st["vscale"].astype(np.float16))
+    assert not zr[blk, off].any()
+    # 3-bit V ignores the flag (uniform codes, as the reference's VQB == 4 test)
+    g3 = O.v1_geometry(d, kb, 3)
+    a = np.zeros((4, 8, H, g3["slot"]), np.uint8)
+    b = np.zeros_like(a)
+    O.v1_store(k, v, np.arange(N), a, mids, kb, 3, v_rotate=True)
+    O.v1_store(k, v, np.arange(N), b, mids, kb, 3, v_rotate=True, v_lloyd_max=True)
+    assert np.array_equal(a, b)
+
+
+def test_v_lloyd_max_dequant_norm_and_quality():
+    """Dequantised Lloyd-Max V (triton_decode_offset.py:399-419): the norm
+    correction makes ||V^|| equal the stored fp16 norm, and V^ taken back by
+    M^T tracks the original V (4-bit Lloyd-Max on unit directions)."""
+    rng = np.random.default_rng(32)
+    d, kb, H, N = 128, 4, 2, 40
+    c = O.lloyd_max_codebook(d, kb)[1].astype(np.float32)
+    g = O.v1_geometry(d, kb, 4)
+    k = rng.standard_normal((N, H, d)).astype(np.float32)
+    v = rng.standard_normal((N, H, d)).astype(np.float32)
+    cache = np.zeros((5, 8, H, g["slot"]), np.uint8)
+    O.v1_store(k, v, np.arange(N), cache, O.v1_midpoints(c), kb, 4, v_rotate=True, v_lloyd_max=True)
+    _, v_hat = O.v1_dequant(cache, d, kb, 4, c, v_lloyd_max=True)
+    _, _, _, sc, _ = O.v1_unpack(cache, d, kb, 4)
+    assert np.allclose(np.linalg.norm(v_hat, axis=-1), sc.astype(np.float64), rtol=1e-12)
+    M = O.sylvester(d) / math.sqrt(d)
+    rec = v_hat.reshape(-1, H, d)[:N] @ M.T
+    cos = np.sum(rec * v, axis=-1) / (np.linalg.norm(rec, axis=-1) * np.linalg.norm(v, axis=-1))
+    assert cos.min() > 0.98

@@ -84,7 +84,7 @@ def test_store_parity(cuda, d, kb, vb, vrot):
     print(f"[v1 store d={d} kb={kb} vb={vb} vrot={vrot} {dtn}] K code ties={ties} of {wk.size}")
 
 
-def _oracle_cache(g, nb, bs, h, d, kb, vb, n_tok, vrot, dtype="bf16", outliers=False):
+def _oracle_cache(g, nb, bs, h, d, kb, vb, n_tok, vrot, dtype="bf16", outliers=False, lloyd=False):
     """Cache bytes written by the oracle (the decode tests do not depend on the GPU store)."""
     from fused_turboquant import v1
     slot = max(v1.slot_size(d, kb, vb), 128)
@@ -93,7 +93,7 @@ def _oracle_cache(g, nb, bs, h, d, kb, vb, n_tok, vrot, dtype="bf16", outliers=F
     c = v1.default_centroids(d, kb).numpy()
     slots = torch.randperm(nb * bs, generator=g)[:n_tok].numpy()
     O.v1_store(k.float().numpy(), v.float().numpy(), slots, cache, O.v1_midpoints(c), kb, vb,
-               v_rotate=vrot, value_dtype=dtype)
+               v_rotate=vrot or lloyd, value_dtype=dtype, v_lloyd_max=lloyd)
     return cache, c
 
 
@@ -236,3 +236,113 @@ def test_config4_full_size(cuda):
                                      layer.centroids.cpu().numpy(), kb, vb, 1 / math.sqrt(d),
                                      v_rotate=True)
         _check_attn(o1[b:b + 1, kvh * 4:kvh * 4 + 4], want, f"config4 b={b} kvh={kvh} ctx={L}")
+
+
+@pytest.mark.parametrize("kb", [2, 3, 4])
+def test_store_parity_v_lloyd_max(cuda, kb):
+    """TURBOQUANT_V_LLOYD_MAX store (reference triton_inkernel_store.py:159-200):
+    V rotated and rounded to bf16, Lloyd-Max codes of v / (||v|| + 1e-8) against
+    the K midpoints, ||v|| in the scale field, 0 in the min field.  Codes equal
+    the oracle's except at midpoint ties (the norms are float reductions whose
+    order differs); both norms within 1e-3; every other byte exact."""
+    from fused_turboquant import v1
+    d, vb, nb, bs, h = 128, 4, 5, 16, 3
+    g = torch.Generator().manual_seed(700 + kb)
+    layer = v1.TurboQuantV1Layer(d, kb, vb, device=cuda, v_lloyd_max=True)
+    assert layer.v_rotate
+    slot = max(v1.slot_size(d, kb, vb), 128)
+    cache = torch.full((nb, bs, h, slot), 0xAB, dtype=torch.uint8, device=cuda)
+    n = nb * bs - 5
+    slots = torch.randperm(nb * bs, generator=g)[:n]
+    slots[3] = -1
+    k, v = _kv(g, n, h, d, torch.bfloat16, outliers=True)
+    layer.store(k.to(cuda), v.to(cuda), cache, slots.to(cuda))
+    got = cache.cpu().numpy()
+    want = np.full(got.shape, 0xAB, np.uint8)
+    mids = layer.midpoints.cpu().numpy()
+    st = O.v1_store(k.float().numpy(), v.float().numpy(), slots.numpy(), want, mids, kb, vb,
+                    v_rotate=True, value_dtype="bf16", v_lloyd_max=True)
+    geo = O.v1_geometry(d, kb, vb)
+    sl = slots.numpy()
+    ok = sl >= 0
+    blk, off = sl[ok] // bs, sl[ok] % bs
+    # padding, min field, unmapped slots: exact
+    assert np.array_equal(got[..., geo["raw"]:], want[..., geo["raw"]:])
+    assert np.array_equal(got[..., geo["kps"] + geo["vdb"] + 2:geo["raw"]],
+                          want[..., geo["kps"] + geo["vdb"] + 2:geo["raw"]])
+    unmapped = np.ones((nb, bs), bool)
+    unmapped[blk, off] = False
+    assert np.array_equal(got[unmapped], want[unmapped])
+    gk, gkn, gv, gsc, gzr = O.v1_unpack(got, d, kb, vb)
+    wk, wkn, wv, wsc, wzr = O.v1_unpack(want, d, kb, vb)
+    assert not gzr[blk, off].any()
+    for name, gn, wn in (("K norm", gkn, wkn), ("V norm", gsc, wsc)):
+        a, b = gn[blk, off].astype(np.float32), wn[blk, off].astype(np.float32)
+        assert np.all(np.abs(a - b) <= 1e-3 * np.abs(b)), name
+    m64 = mids.astype(np.float64)
+    for name, gc, wc, u in (("K", gk, wk, st["y"]), ("V", gv, wv, st["vt"])):
+        a, b = gc[blk, off], wc[blk, off]
+        diff = a != b
+        if diff.any():
+            uu = u[ok][diff].astype(np.float64)
+            assert np.min(np.abs(uu[:, None] - m64[None, :]), axis=1).max() < TIE, name
+            assert np.all(np.abs(a[diff].astype(int) - b[diff].astype(int)) == 1), name
+        print(f"[v1 store lloyd kb={kb}] {name} code ties={int(diff.sum())} of {a.size}")
+
+
+@pytest.mark.parametrize("kb,vb", [(2, 2), (2, 4), (3, 3), (4, 2)])
+@pytest.mark.parametrize("hq,hkv", [(16, 4), (32, 4)])  # the GQA-4 kernel and the general one
+@pytest.mark.parametrize("splits", [1, 5])
+def test_decode_parity_outlier_keys(cuda, kb, vb, hq, hkv, splits):
+    """Keys and values 8x the typical norm on 2% of tokens: large, spread-out
+    scores, where a relative error in q.c / ||c|| of the centroid table's f16
+    rounding (up to 2^-12, per centroid value) moves softmax weights by ~0.5%
+    and the outputs by more than 2e-2.  Against the oracle's float64 attention."""
+    from fused_turboquant import v1
+    d, bs, nb = 128, 16, 48
+    g = torch.Generator().manual_seed(700 + kb * 10 + vb + hq + splits)
+    cache, c = _oracle_cache(g, nb, bs, hkv, d, kb, vb, nb * bs, (kb + vb) % 2 == 0, outliers=True)
+    lens = [0, 1, 17, 100, 257, 64]
+    starts = [0, 0, 5, 40, 0, 63]
+    B = len(lens)
+    bt = torch.randint(0, nb, (B, 20), generator=g, dtype=torch.int32)
+    q = torch.randn(B, hq, d, generator=g).to(torch.bfloat16)
+    sl = torch.tensor(lens, dtype=torch.int32)
+    ks = torch.tensor(starts, dtype=torch.int32)
+    vrot = (kb + vb) % 2 == 0
+    out = v1.v1_decode_attention(q.to(cuda), torch.from_numpy(cache).to(cuda), bt.to(cuda), sl.to(cuda),
+                                 torch.from_numpy(c).to(cuda), kb, vb, v_rotate=vrot, kv_start=ks.to(cuda),
+                                 num_splits=splits)
+    want = O.v1_decode_attention(q.float().numpy(), cache, bt.numpy(), sl.numpy(), c, kb, vb,
+                                 1 / math.sqrt(d), kv_start=ks.numpy(), v_rotate=vrot)
+    got = out.float().cpu().numpy()
+    assert not got[0].any()
+    _check_attn(got, want, f"v1 outlier keys kb={kb} vb={vb} hq={hq} hkv={hkv} S={splits}")
+
+
+@pytest.mark.parametrize("kb", [2, 3, 4])
+@pytest.mark.parametrize("hq,hkv", [(8, 2), (16, 4), (4, 4)])
+@pytest.mark.parametrize("splits", [1, 5])
+def test_decode_parity_v_lloyd_max(cuda, kb, hq, hkv, splits):
+    """TURBOQUANT_V_LLOYD_MAX decode (reference triton_decode_offset.py:399-419):
+    V = c[code] ||v||_16 / ||c[codes]||, un-rotated; against the oracle's float64
+    attention over the same cache bytes, with kv_start on two rows."""
+    from fused_turboquant import v1
+    d, vb, bs, nb = 128, 4, 16, 48
+    g = torch.Generator().manual_seed(900 + kb * 10 + hq + splits)
+    cache, c = _oracle_cache(g, nb, bs, hkv, d, kb, vb, nb * bs, True, outliers=True, lloyd=True)
+    lens = [0, 1, 17, 100, 257, 64]
+    starts = [0, 0, 5, 40, 0, 63]
+    B = len(lens)
+    bt = torch.randint(0, nb, (B, 20), generator=g, dtype=torch.int32)
+    q = torch.randn(B, hq, d, generator=g).to(torch.bfloat16)
+    sl = torch.tensor(lens, dtype=torch.int32)
+    ks = torch.tensor(starts, dtype=torch.int32)
+    out = v1.v1_decode_attention(q.to(cuda), torch.from_numpy(cache).to(cuda), bt.to(cuda), sl.to(cuda),
+                                 torch.from_numpy(c).to(cuda), kb, vb, v_rotate=True, v_lloyd_max=True,
+                                 kv_start=ks.to(cuda), num_splits=splits)
+    want = O.v1_decode_attention(q.float().numpy(), cache, bt.numpy(), sl.numpy(), c, kb, vb,
+                                 1 / math.sqrt(d), kv_start=ks.numpy(), v_rotate=True, v_lloyd_max=True)
+    got = out.float().cpu().numpy()
+    assert not got[0].any()
+    _check_attn(got, want, f"v1 lloyd kb={kb} hq={hq} hkv={hkv} S={splits}")

@@ -45,12 +45,13 @@ def _causal_ref(q, k, v, scale):
     return out
 
 
-def _run_step(cuda, seqs, dtype_str, hq, hkv, vrot, monkeypatch, seed, bs=16, protect="0"):
+def _run_step(cuda, seqs, dtype_str, hq, hkv, vrot, monkeypatch, seed, bs=16, protect="0", lloyd=False):
     """seqs: list of (cached_len, query_len), decodes (query_len 1, cached > 0) first.
     Stores the cached tokens in earlier update calls, then runs one step."""
     from fused_turboquant import vllm_plugin as vp
     monkeypatch.setenv("TURBOQUANT_BOUNDARY_PROTECT", protect)
     monkeypatch.setenv("TURBOQUANT_V_ROTATE", "1" if vrot else "0")
+    monkeypatch.setenv("TURBOQUANT_V_LLOYD_MAX", "1" if lloyd else "0")
     g = torch.Generator().manual_seed(seed)
     Bk = vp.FusedTurboQuantV1Backend
     impl = vp.FusedTurboQuantV1Impl(hq, D, 1 / math.sqrt(D), hkv, kv_cache_dtype=dtype_str)
@@ -121,7 +122,7 @@ def _run_step(cuda, seqs, dtype_str, hq, hkv, vrot, monkeypatch, seed, bs=16, pr
                 want = O.raw_decode_attention(qs[i].float().numpy(), cache_np, btr, sl, 1 / math.sqrt(D))
             else:
                 want = O.v1_decode_attention(qs[i].float().numpy(), cache_np, btr, sl, cent, kb, vb,
-                                             1 / math.sqrt(D), v_rotate=vrot)
+                                             1 / math.sqrt(D), v_rotate=vrot or lloyd, v_lloyd_max=lloyd)
         kind = "prefill" if c == 0 else ("decode" if q == 1 else "continuation")
         _check(got[a:a + q], want, f"{dtype_str} vrot={vrot} seq{i} {kind} cached={c} q={q}")
 
@@ -232,3 +233,13 @@ def test_deferred_prefill_hybrid_decode(cuda, monkeypatch, dtype_str, vrot):
         store1(P + t, torch.randn(hkv, D, generator=g).to(torch.bfloat16),
                torch.randn(hkv, D, generator=g).to(torch.bfloat16))
         decode(P + t + 1, pk, pv, P, f"{dtype_str} vrot={vrot} step {t}")
+
+
+@pytest.mark.parametrize("dtype_str", ["turboquant_4bit_nc", "turboquant_k3v4_nc", "turboquant_k4v2_nc"])
+def test_v_lloyd_max_step(cuda, monkeypatch, dtype_str):
+    """TURBOQUANT_V_LLOYD_MAX=1 through the Impl (reference v1_backend.py:728-740,
+    1086-1092): 4-bit V stores Lloyd-Max codes and decodes them with the norm
+    correction; 2-bit V (K4V2) stays uniform but rotated.  Decode, fresh
+    prefill and continuation in one mixed step."""
+    _run_step(cuda, [(40, 1), (700, 1), (0, 33), (129, 9)], dtype_str, 32, 8, False, monkeypatch,
+              seed=7, lloyd=True)
