@@ -380,7 +380,7 @@ template <int D, int BK, int BV, bool SHARE, int NW>
 __host__ __device__ constexpr int paged_attn_lds(int G) {
   const int lut = CodeLut<BK>::BYTES + (SHARE ? 0 : CodeLut<BV>::BYTES);
   const int red = NW * G * (D + 1) * 4;
-  const int qs = G * (D + 8) * 2;
+  const int qs = G * (D + 4) * 4;
   const int m = lut > red ? lut : red;
   return m > qs ? m : qs;
 }
@@ -414,8 +414,11 @@ __device__ __forceinline__ void finish_row(float (&y)[D / 64], float L, const fl
 //     of 4 waves per SIMD (<= 128 VGPRs).  The waves merge in LDS and the
 //     workgroup writes the output itself (inverse RHT, output dtype): no
 //     workspace and no second launch.
-template <int D, int BK, int BV, int QT, bool SHARE, int NW>
-__global__ __launch_bounds__(NW * 64, NW == 16 ? 1 : (D == 128 ? 4 : 2)) void paged_attn_kernel(
+//   QL (more than 8 query heads per kv head, no spare MFMA columns): the
+//     query's f16 remainder is a second B operand with an MFMA of its own
+//     (16 more registers: 3 workgroups per CU at d = 128).
+template <int D, int BK, int BV, int QT, bool SHARE, int NW, bool QL = false>
+__global__ __launch_bounds__(NW * 64, NW == 16 ? 1 : (D == 128 ? (QL ? 3 : 4) : 2)) void paged_attn_kernel(
     const void* __restrict__ query, const uint8_t* __restrict__ cache,
     const int32_t* __restrict__ block_table, const int32_t* __restrict__ seq_lens, int hq, int hkv,
     int page_size, int max_blocks, int64_t num_blocks, const float* __restrict__ ksigns,
@@ -423,6 +426,7 @@ __global__ __launch_bounds__(NW * 64, NW == 16 ? 1 : (D == 128 ? 4 : 2)) void pa
     float* __restrict__ ws_o, float* __restrict__ ws_lse, const float* __restrict__ vsigns, float vscale,
     void* __restrict__ out, int ot) {
   static_assert(NW == 4 || (NW == 16 && D == 128), "4 waves, or 16 waves at d = 128");
+  static_assert(!QL || NW == 4, "the 16-wave form takes at most 4 query heads per kv head");
   using Gm = PagedGeom<D, BK, BV>;
   constexpr int NS = Gm::NS, NB = Gm::NB;
   constexpr int E = D / 16;
@@ -437,56 +441,15 @@ __global__ __launch_bounds__(NW * 64, NW == 16 ? 1 : (D == 128 ? 4 : 2)) void pa
   constexpr int LUTK_BYTES = CodeLut<BK>::BYTES;
   extern __shared__ __attribute__((aligned(16))) uint8_t pool[];
   __shared__ float red_m[NW][16], red_l[NW][16];
-  __shared__ uint16_t lev16[2][16];  // fp16 K / V levels
-  _Float16 (*qs)[D + 8] = reinterpret_cast<_Float16 (*)[D + 8]>(pool);
+  __shared__ uint16_t lev16[2][16];  // f16(sigma level), K / V
+  __shared__ float tab_inv[2];       // 1 / (sigma (1 + rmid)), K / V
+  float (*qs)[D + 4] = reinterpret_cast<float (*)[D + 4]>(pool);
   float* red_o = reinterpret_cast<float*>(pool);  // [NW waves][G heads][D + 1]
   uint8_t* lutK = pool;
   uint8_t* lutV = SHARE ? pool : pool + LUTK_BYTES;
 
-  if (tid < (1 << BK)) lev16[0][tid] = (uint16_t)f32_to_f16_bits(klev[tid]);
-  if (tid >= 64 && tid - 64 < (1 << BV)) lev16[1][tid - 64] = (uint16_t)f32_to_f16_bits(vlev[tid - 64]);
-
-  // rotate the G query heads of this kv head: one head per 16 lanes
-  {
-    const int g = tid >> 4, l16 = tid & 15;
-    if (g < G) {
-      float y[E], sg[E];
-      load_elems<QT, E>(query, ((int64_t)b * hq + kvh * G + g) * D + l16 * E, y);
-#pragma unroll
-      for (int i = 0; i < E; ++i) {
-        sg[i] = ksigns[l16 * E + i];
-        y[i] *= sg[i];
-      }
-      fwht_lanes<E, 16>(y, l16);
-      const float sc = (float)(1.0 / __builtin_sqrt((double)D)) * qscale;
-#pragma unroll
-      for (int i = 0; i < E; ++i) qs[g][l16 * E + i] = (_Float16)(y[i] * sc);
-    }
-  }
-  __syncthreads();
-
-  // B operand of the Q.K MFMAs: lane (h, q), MFMA s -> Q[h][q*D/4 + 8s + j]
-  Op8 qb[NS];
-#pragma unroll
-  for (int s = 0; s < NS; ++s) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      uint32_t w = 0;
-      if (h < G) {
-        const _Float16 a0 = qs[h][q * (D / 4) + 8 * s + 2 * j];
-        const _Float16 a1 = qs[h][q * (D / 4) + 8 * s + 2 * j + 1];
-        w = (uint32_t)__builtin_bit_cast(uint16_t, a0) | ((uint32_t)__builtin_bit_cast(uint16_t, a1) << 16);
-      }
-      qb[s].u[j] = w;
-    }
-  }
-  __syncthreads();  // qs is dead from here on; its LDS holds the code tables
-  build_code_lut<BK>(lutK, lev16[0], tid, NW * 64);
-  if (!SHARE) build_code_lut<BV>(lutV, lev16[1], tid, NW * 64);
-  __syncthreads();
-  const uint32_t tabK = lut_lane_base<BK>(lane, lds_addr(lutK));
-  const uint32_t tabV = lut_lane_base<BV>(lane, lds_addr(lutV));
-
+  // tile range and the first tile's loads, issued before the prologue so that
+  // their latency overlaps it
   const int seq_len = seq_lens[b];
   const int n_tiles = (seq_len + 31) >> 5;
   const int tps = (n_tiles + num_splits - 1) / num_splits;
@@ -504,6 +467,94 @@ __global__ __launch_bounds__(NW * 64, NW == 16 ? 1 : (D == 128 ? 4 : 2)) void pa
       const_cast<int32_t*>(block_table + (int64_t)b * max_blocks), (short)0,
       (int)min((int64_t)max_blocks * 4, (int64_t)0x7ffffffc), 0x00020000);
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);  // wave-uniform -> scalar tile math
+  TileRegs<D, BK, BV> ra, rb;
+  int tile = t_begin + wave_u;
+  auto bt_of = [&](int t) __attribute__((always_inline)) {
+    return fetch_bt(bt_rs, t, t < t_end, seq_subs, sd, (uint32_t)lane);
+  };
+  TileOff lo;
+  lo.k = (uint32_t)h * Gm::KTOK + (uint32_t)q * Gm::KLANE;
+  lo.v = (uint32_t)Gm::KSEC + (uint32_t)lane * Gm::VLANE;
+  lo.n = (uint32_t)Gm::KNORM + (uint32_t)q * 8u;
+  auto load = [&](TileRegs<D, BK, BV>& r, int btv, int t) __attribute__((always_inline)) {
+    load_tile(r, cache, btv, t, sd, blk_stride, kvh_off, nb32, lo);
+  };
+  int btv = 0;
+  if (tile < t_end) {
+    load(ra, bt_of(tile), tile);
+    btv = bt_of(tile + NW);
+  }
+
+  float y[E];  // this lane's query elements, loaded before the level-table work
+  if ((tid >> 4) < G) load_elems<QT, E>(query, ((int64_t)b * hq + kvh * G + (tid >> 4)) * D + (tid & 15) * E, y);
+
+  // f16 level tables f16(sigma level) with sigma chosen to equalise the
+  // relative rounding errors; the scores and the output are divided by
+  // sigma (1 + rmid), which leaves an error of at most half the spread.
+  // Wave 0 sizes the K table, wave 1 the V table (none for a shared table:
+  // one codebook array for K and V takes the K scale).
+  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+  if (wave_s == 0) {
+    const TableScale t = table_scale<1 << BK>(klev, false);
+    if (lane < (1 << BK)) lev16[0][lane] = (uint16_t)f32_to_f16_bits(t.sigma * klev[lane]);
+    if (lane == 0) tab_inv[0] = 1.f / (t.sigma * (1.f + t.rmid));
+  } else if (wave_s == 1 && !SHARE) {
+    const TableScale t = table_scale<1 << BV>(vlev, false);
+    if (lane < (1 << BV)) lev16[1][lane] = (uint16_t)f32_to_f16_bits(t.sigma * vlev[lane]);
+    if (lane == 0) tab_inv[1] = 1.f / (t.sigma * (1.f + t.rmid));
+  }
+
+  // rotate the G query heads of this kv head: one head per 16 lanes
+  {
+    const int g = tid >> 4, l16 = tid & 15;
+    if (g < G) {
+      float sg[E];
+#pragma unroll
+      for (int i = 0; i < E; ++i) {
+        sg[i] = ksigns[l16 * E + i];
+        y[i] *= sg[i];
+      }
+      fwht_lanes<E, 16>(y, l16);
+      const float sc = (float)(1.0 / __builtin_sqrt((double)D)) * qscale;
+#pragma unroll
+      for (int i = 0; i < E; ++i) qs[g][l16 * E + i] = y[i] * sc;
+    }
+  }
+  __syncthreads();
+
+  // B operand of the Q.K MFMAs: lane (h, q), MFMA s -> Q[h][q*D/4 + 8s + j] as
+  // f16; the remainder q - f16(q) goes to column 8 + h when G <= 8 (summed into
+  // column h after the K loop, no extra MFMA), else (QL) to a second operand
+  const bool qrem = !QL && G <= 8;
+  const float kinv = tab_inv[0];
+  Op8 qb[NS], ql[QL ? NS : 1];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      uint32_t w = 0, wl = 0;
+      const int hh = (qrem && h >= 8) ? h - 8 : h;
+      if (hh < G) {
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const float x = qs[hh][q * (D / 4) + 8 * s + 2 * j + e] * kinv;
+          const _Float16 hi = (_Float16)x;
+          const _Float16 lo = (_Float16)(x - (float)hi);
+          w |= (uint32_t)__builtin_bit_cast(uint16_t, hh == h ? hi : lo) << (16 * e);
+          wl |= (uint32_t)__builtin_bit_cast(uint16_t, lo) << (16 * e);
+        }
+      }
+      qb[s].u[j] = w;
+      if constexpr (QL) ql[s].u[j] = wl;
+    }
+  }
+  __syncthreads();  // qs is dead from here on; its LDS holds the code tables
+  build_code_lut<BK>(lutK, lev16[0], tid, NW * 64);
+  if (!SHARE) build_code_lut<BV>(lutV, lev16[1], tid, NW * 64);
+  __syncthreads();
+  const uint32_t tabK = lut_lane_base<BK>(lane, lds_addr(lutK));
+  const uint32_t tabV = lut_lane_base<BV>(lane, lds_addr(lutV));
+
 
   float m_run = -INFINITY, l_run = 0.f;
   floatx4 acc[NB];
@@ -528,6 +579,7 @@ __global__ __launch_bounds__(NW * 64, NW == 16 ? 1 : (D == 128 ? 4 : 2)) void pa
         const uint2 c23 = lut_quad<BK>(cur.k[sb], (8 * st + 4) * BK, tabK);
         a.u[0] = c01.x; a.u[1] = c01.y; a.u[2] = c23.x; a.u[3] = c23.y;
         c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a.h, qb[st].h, c, 0, 0, 0);
+        if constexpr (QL) c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a.h, ql[st].h, c, 0, 0, 0);
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -536,6 +588,12 @@ __global__ __launch_bounds__(NW * 64, NW == 16 ? 1 : (D == 128 ? 4 : 2)) void pa
       }
     }
     if constexpr (BK <= 3 && BV <= 3) sched_lds_mfma<2 * NS, 4>();  // (4-bit tables: registers run out)
+    // add the q remainder's column h + 8 (the same token, so the same K norm)
+    if (qrem)
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s[sb][i] += dpp_xor8(s[sb][i]);
     if (tile * 32 + 32 > seq_len) {  // only the last tile of a sequence is partial
 #pragma unroll
       for (int sb = 0; sb < 2; ++sb)
@@ -592,23 +650,8 @@ __global__ __launch_bounds__(NW * 64, NW == 16 ? 1 : (D == 128 ? 4 : 2)) void pa
 
   // ping-pong over two register sets so the next tile's loads overlap this tile's math
   // and the block-table entries one tile further ahead
-  TileRegs<D, BK, BV> ra, rb;
-  int tile = t_begin + wave_u;
-  auto bt_of = [&](int t) __attribute__((always_inline)) {
-    return fetch_bt(bt_rs, t, t < t_end, seq_subs, sd, (uint32_t)lane);
-  };
-  TileOff lo;
-  lo.k = (uint32_t)h * Gm::KTOK + (uint32_t)q * Gm::KLANE;
-  lo.v = (uint32_t)Gm::KSEC + (uint32_t)lane * Gm::VLANE;
-  lo.n = (uint32_t)Gm::KNORM + (uint32_t)q * 8u;
-  auto load = [&](TileRegs<D, BK, BV>& r, int btv, int t) __attribute__((always_inline)) {
-    load_tile(r, cache, btv, t, sd, blk_stride, kvh_off, nb32, lo);
-  };
-  int btv = 0;
-  if (tile < t_end) {
-    load(ra, bt_of(tile), tile);
-    btv = bt_of(tile + NW);
-  }
+  // ping-pong over two register sets so the next tile's loads overlap this tile's math
+  // and the block-table entries one tile further ahead
   while (tile < t_end) {
     int btn = bt_of(tile + 2 * NW);
     load(rb, btv, tile + NW);
@@ -622,9 +665,10 @@ __global__ __launch_bounds__(NW * 64, NW == 16 ? 1 : (D == 128 ? 4 : 2)) void pa
     process(rb, tile);
     tile += NW;
   }
-  // undo the P' pre-scale
+  // undo the P' pre-scale and the V table scale
+  const float osc = 512.f * tab_inv[SHARE ? 0 : 1];
 #pragma unroll
-  for (int bb = 0; bb < NB; ++bb) acc[bb] *= 512.f;
+  for (int bb = 0; bb < NB; ++bb) acc[bb] *= osc;
 
   // ---- merge the 4 waves through LDS (the code tables' LDS is reused) ----
   __syncthreads();
@@ -753,17 +797,17 @@ static bool fused_form(int d, int hq, int hkv, int splits) {
   return d == 128 && hq / hkv <= 4 && splits == 1;
 }
 
-template <int D, int BK, int BV, bool SHARE, int NW>
+template <int D, int BK, int BV, bool SHARE, int NW, bool QL = false>
 static void launch_attn_nw(const AttnArgs& a, hipStream_t st) {
   dim3 grid(a.splits, a.hkv, a.B), block(NW * 64);
   const size_t lds = (size_t)paged_attn_lds<D, BK, BV, SHARE, NW>(a.hq / a.hkv);
   const float sc = fwht_scale(D);
   if (a.qt == F32)
-    paged_attn_kernel<D, BK, BV, F32, SHARE, NW><<<grid, block, lds, st>>>(a.q, a.cache, a.bt, a.sl, a.hq, a.hkv, a.page_size, a.max_blocks, a.num_blocks, a.ks, a.kl, a.vl, a.qscale, a.splits, a.wo, a.wl, a.vs, sc, a.out, a.ot);
+    paged_attn_kernel<D, BK, BV, F32, SHARE, NW, QL><<<grid, block, lds, st>>>(a.q, a.cache, a.bt, a.sl, a.hq, a.hkv, a.page_size, a.max_blocks, a.num_blocks, a.ks, a.kl, a.vl, a.qscale, a.splits, a.wo, a.wl, a.vs, sc, a.out, a.ot);
   else if (a.qt == F16)
-    paged_attn_kernel<D, BK, BV, F16, SHARE, NW><<<grid, block, lds, st>>>(a.q, a.cache, a.bt, a.sl, a.hq, a.hkv, a.page_size, a.max_blocks, a.num_blocks, a.ks, a.kl, a.vl, a.qscale, a.splits, a.wo, a.wl, a.vs, sc, a.out, a.ot);
+    paged_attn_kernel<D, BK, BV, F16, SHARE, NW, QL><<<grid, block, lds, st>>>(a.q, a.cache, a.bt, a.sl, a.hq, a.hkv, a.page_size, a.max_blocks, a.num_blocks, a.ks, a.kl, a.vl, a.qscale, a.splits, a.wo, a.wl, a.vs, sc, a.out, a.ot);
   else
-    paged_attn_kernel<D, BK, BV, BF16, SHARE, NW><<<grid, block, lds, st>>>(a.q, a.cache, a.bt, a.sl, a.hq, a.hkv, a.page_size, a.max_blocks, a.num_blocks, a.ks, a.kl, a.vl, a.qscale, a.splits, a.wo, a.wl, a.vs, sc, a.out, a.ot);
+    paged_attn_kernel<D, BK, BV, BF16, SHARE, NW, QL><<<grid, block, lds, st>>>(a.q, a.cache, a.bt, a.sl, a.hq, a.hkv, a.page_size, a.max_blocks, a.num_blocks, a.ks, a.kl, a.vl, a.qscale, a.splits, a.wo, a.wl, a.vs, sc, a.out, a.ot);
 }
 
 template <int D, int BK, int BV, bool SHARE>
@@ -774,7 +818,8 @@ static void launch_attn_kernel(const AttnArgs& a, hipStream_t st) {
       return;
     }
   }
-  launch_attn_nw<D, BK, BV, SHARE, 4>(a, st);
+  if (a.hq / a.hkv > 8) launch_attn_nw<D, BK, BV, SHARE, 4, true>(a, st);
+  else launch_attn_nw<D, BK, BV, SHARE, 4>(a, st);
 }
 
 template <int D, int BK, int BV>

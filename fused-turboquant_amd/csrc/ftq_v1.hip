@@ -364,51 +364,6 @@ __device__ __forceinline__ void wave_lds_fence() {
   __asm__ volatile("" ::: "memory");
 }
 
-// Scale of the centroid tables behind the f16 MFMA operands.  A centroid c
-// enters the Q.K MFMAs as f16(sigma c); the scores divide by the norm of the
-// same f16 values (the norm correction), so any error common to all
-// centroids cancels and only the spread of the relative rounding errors
-// (f16(x) - x) / x across the table moves q.c / ||c||.  f16(c) itself has a
-// spread of up to 2^-11, which with keys 8x the typical norm shifts softmax
-// weights by about 0.5%.  sigma = 2^k (1 + j/256), 2^k putting the largest |c|
-// in [512, 1024): every thread tries one j, the workgroup keeps the j with the
-// smallest spread (lowest j on ties; the same on every workgroup).  For the
-// Lloyd-Max tables of 2-, 3- and 4-bit codes the spread drops to about 1e-7,
-// 3e-5 and 2e-4.  Called by all threads; c[0, n) in LDS; red[8] LDS scratch.
-__device__ float cent_scale(const float* c, int n, int tid, float* red) {
-  float mx = 0.f;
-  for (int i = 0; i < n; ++i) mx = fmaxf(mx, fabsf(c[i]));
-  if (!(mx > 0.f) || !(mx < INFINITY)) return 1.f;  // same branch in every thread
-  const int e = (int)((__float_as_uint(mx) >> 23) & 255u);  // mx in [2^(e-127), 2^(e-126))
-  const float p2 = __uint_as_float((uint32_t)min(max(263 - e, 1), 254) << 23);  // 2^(136 - e)
-  const float sg = p2 * (1.f + (float)(tid & 255) * (1.f / 256.f));
-  float rlo = 0.f, rhi = 0.f;
-  for (int i = 0; i < n; ++i) {
-    const float x = sg * c[i];
-    const float r = x != 0.f ? (f16_bits_to_f32(f32_to_f16_bits(x)) - x) / x : 0.f;
-    rlo = fminf(rlo, r);
-    rhi = fmaxf(rhi, r);
-  }
-  // argmin over the workgroup of (spread, j): spread >= 0, so its bits order as the value
-  uint64_t key = ((uint64_t)__float_as_uint(rhi - rlo) << 32) | (uint32_t)(tid & 255);
-  for (int o = 32; o >= 1; o >>= 1) {
-    const uint64_t other = ((uint64_t)(uint32_t)__shfl_xor((int)(key >> 32), o) << 32) |
-                           (uint32_t)__shfl_xor((int)(uint32_t)key, o);
-    key = other < key ? other : key;
-  }
-  uint32_t* r32 = reinterpret_cast<uint32_t*>(red);
-  if ((tid & 63) == 0) {
-    r32[2 * (tid >> 6)] = (uint32_t)(key >> 32);
-    r32[2 * (tid >> 6) + 1] = (uint32_t)key;
-  }
-  __syncthreads();
-  uint64_t best = ~0ull;
-  for (int w = 0; w < 4; ++w) {
-    const uint64_t k = ((uint64_t)r32[2 * w] << 32) | r32[2 * w + 1];
-    best = k < best ? k : best;
-  }
-  return p2 * (1.f + (float)(uint32_t)best * (1.f / 256.f));
-}
 // f16 pairs (a, b): hi | hi << 16 and lo | lo << 16, lo = f16(x - f16(x))
 __device__ __forceinline__ uint2 cent_hilo_pair(float a, float b) {
   const uint32_t ha = f32_to_f16_bits(a), hb = f32_to_f16_bits(b);
@@ -495,7 +450,7 @@ __global__ __launch_bounds__(256, 2) void v1_attn_kernel(
     }
   }
   __syncthreads();  // qs is dead; its LDS now holds the pair table
-  const float csc = cent_scale(centl, 1 << KB, tid, &red_m[0][0]);
+  const float csc = table_scale<1 << KB>(cent, true).sigma;
   const float vk = csc * (1.f / 256.f), vinv = 256.f / csc;  // Lloyd-Max V: P' scale and its inverse
   for (int e = tid; e < (1 << (2 * KB)); e += 256)
     reinterpret_cast<uint32_t*>(lut)[e] = cent_hilo_pair(csc * centl[e & ((1 << KB) - 1)], csc * centl[e >> KB]).x;
@@ -893,7 +848,7 @@ __global__ __launch_bounds__(256, VB == 2 ? 4 : 2) void v1_attn_g4_kernel(
   }
   __syncthreads();
   {
-    const float csc = cent_scale(centl, 1 << KB, tid, &red_m[0][0]);
+    const float csc = table_scale<1 << KB>(cent, true).sigma;
     for (int e = tid; e < (1 << (2 * KB)); e += 256)
       reinterpret_cast<uint32_t*>(lut)[e] = cent_hilo_pair(csc * centl[e & ((1 << KB) - 1)], csc * centl[e >> KB]).x;
   }

@@ -21,12 +21,17 @@ def _quants(cache):
     return cache.k_quant, cache.v_quant
 
 
-def _fill(cache, lens, bt, hkv, d, g, dev, dtype=torch.bfloat16):
+def _fill(cache, lens, bt, hkv, d, g, dev, dtype=torch.bfloat16, outliers=False):
     page = cache.page_size
     ks, vs = [], []
     for b, L in enumerate(lens):
-        k = torch.randn(L, hkv, d, generator=g).to(dtype)
-        v = torch.randn(L, hkv, d, generator=g).to(dtype)
+        k = torch.randn(L, hkv, d, generator=g)
+        v = torch.randn(L, hkv, d, generator=g)
+        if outliers:  # 2% of tokens at 8x the typical norm
+            sel = torch.rand(L, generator=g) < 0.02
+            k[sel] *= 8
+            v[sel] *= 8
+        k, v = k.to(dtype), v.to(dtype)
         if L:
             pos = torch.arange(L)
             slots = bt[b].long()[pos // page] * page + pos % page
@@ -108,6 +113,42 @@ def test_decode_attention_parity(cuda, bk, bv, hq, hkv):
         out32 = cache.decode_attention(q.to(cuda), bt.to(cuda), sl, num_splits=splits,
                                        out=torch.empty(B, hq, d, device=cuda)).cpu().numpy()
         assert np.abs(out32 - ref).max() <= 2e-2
+
+
+@pytest.mark.parametrize("bk,bv", [(3, 3), (4, 2), (2, 4)])
+@pytest.mark.parametrize("hq,hkv", [(16, 4), (32, 4), (32, 2)])
+def test_decode_attention_outlier_keys(cuda, bk, bv, hq, hkv):
+    """Keys and values 8x the typical norm on 2% of tokens: large, spread-out
+    scores, where a relative error in the scores (the f16 level table, the
+    f16 query) moves softmax weights and outputs visibly.  Against float64
+    attention over the oracle's decode; the bound grows with |want| by one
+    bf16 ulp, as rounding the exact answer to bf16 alone errs by half of that."""
+    from fused_turboquant.paged import PagedTurboQuantCache
+    d, page = 128, 16
+    lens = [1, 17, 100, 515, 1000]
+    B = len(lens)
+    maxp = max((L + page - 1) // page for L in lens)
+    g = torch.Generator().manual_seed(500 + bk * 100 + bv * 10 + hq + hkv)
+    nblk = B * maxp + 3
+    cache = PagedTurboQuantCache(nblk, page, hkv, d, bk, bv, device=cuda)
+    bt = torch.randperm(nblk, generator=g)[: B * maxp].view(B, maxp).to(torch.int32)
+    ks, vs = _fill(cache, lens, bt, hkv, d, g, cuda, outliers=True)
+    q = torch.randn(B, hq, d, generator=g).to(torch.bfloat16)
+    S = max(lens)
+    Kd = np.zeros((B, hkv, S, d))
+    Vd = np.zeros((B, hkv, S, d))
+    for b, L in enumerate(lens):
+        Kd[b, :, :L] = _decoded(cache.k_quant, ks[b].reshape(-1, d), bk, d)[0].reshape(L, hkv, d).transpose(1, 0, 2)
+        Vd[b, :, :L] = _decoded(cache.v_quant, vs[b].reshape(-1, d), bv, d)[0].reshape(L, hkv, d).transpose(1, 0, 2)
+    ref = O.dense_decode_attention(q.float().numpy(), Kd, Vd, lens, 1 / math.sqrt(d))
+    sl = torch.tensor(lens, dtype=torch.int32, device=cuda)
+    bound = 2e-2 + 2.0 ** -8 * np.abs(ref)
+    for splits in (1, 3):
+        out = cache.decode_attention(q.to(cuda), bt.to(cuda), sl, num_splits=splits).float().cpu().numpy()
+        err = np.abs(out - ref)
+        print(f"[attn outliers bk={bk} bv={bv} hq={hq} hkv={hkv} splits={splits}] max={err.max():.2e} "
+              f"mean={err.mean():.2e} (|ref| max {np.abs(ref).max():.1f}) worst/bound {(err / bound).max():.2f}")
+        assert (err <= bound).all() and err.mean() <= 2e-3 * max(1.0, float(np.abs(ref).mean()))
 
 
 def test_decode_attention_page32_and_zero_len(cuda):
