@@ -37,8 +37,8 @@ HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, AMD published
 # (FETCH x2.0, WRITE x1.0); the summaries are in profiles/hbm_traffic_counters.md.
 # Keyed by roofline entry; None where no counter run covers the kernel.
 TRAFFIC_BYTES: dict = {
-    "encode_d128_3bit": 80344854, "encode_d256_3bit": 160168819, "decode_d128_3bit_f32": 149010595,
-    "paged_attn_config3": 219911850, "v1_attn_config4": 406642033, "raw_attn_boundary": 1081617368,
+    "encode_d128_3bit": 80336620, "encode_d256_3bit": 160154623, "decode_d128_3bit_f32": 149011545,
+    "paged_attn_config3": 219810032, "v1_attn_config4": 406670855, "raw_attn_boundary": 1081506403,
 }
 
 
