@@ -7,6 +7,8 @@
 // output transform of the cache format:
 //   ROT_SIGNS  o <- (H o) * scale * signs   inverse RHT of library-format V
 //   ROT_PLAIN  o <- (H o) * scale            un-rotation of v1 V (v_rotate)
+//   ROT_MATRIX o <- o M^T, M = signs (row-major D x D fp32): un-rotation of v1 V
+//              rotated by a matrix strategy (x M)
 //   ROT_NONE   o unchanged
 // A row with every split empty (lse = -inf) is written as zeros.  With
 // lse_out, the row's natural-log log-sum-exp of the scaled scores goes there
@@ -22,7 +24,7 @@
 
 namespace ftq {
 
-enum MergeRot : int { ROT_NONE = 0, ROT_PLAIN = 1, ROT_SIGNS = 2 };
+enum MergeRot : int { ROT_NONE = 0, ROT_PLAIN = 1, ROT_SIGNS = 2, ROT_MATRIX = 3 };
 
 __device__ __forceinline__ float wave_max64(float x) {
 #pragma unroll
@@ -168,7 +170,23 @@ __global__ __launch_bounds__(256) void merge_splits_kernel(const float* __restri
   const float inv = (W > 0.f) ? 1.f / W : 0.f;
 #pragma unroll
   for (int i = 0; i < E; ++i) y[i] *= inv;
-  if constexpr (ROT != ROT_NONE) {
+  if constexpr (ROT == ROT_MATRIX) {
+    __shared__ float mrow[4][D];  // this wave's row; a wave's LDS accesses run in order
+    const int w = (int)(threadIdx.x >> 6);
+#pragma unroll
+    for (int i = 0; i < E; ++i) mrow[w][lane * E + i] = y[i];
+    __asm__ volatile("" ::: "memory");
+    float z[E];
+#pragma unroll
+    for (int i = 0; i < E; ++i) z[i] = 0.f;
+    for (int j = 0; j < D; ++j) {
+      const float oj = mrow[w][j];
+#pragma unroll
+      for (int i = 0; i < E; ++i) z[i] = __builtin_fmaf(oj, signs[(int64_t)(lane * E + i) * D + j], z[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < E; ++i) y[i] = z[i];
+  } else if constexpr (ROT != ROT_NONE) {
     fwht_wave64<E>(y, lane);
 #pragma unroll
     for (int i = 0; i < E; ++i) {

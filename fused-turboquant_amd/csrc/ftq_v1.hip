@@ -85,16 +85,42 @@ __device__ __forceinline__ float round_to_dtype(float x) {
   else return x;
 }
 
+// x <- x M for a vector spread over 16 lanes, E contiguous elements per lane
+// (M row-major D x D fp32, the rotation of a matrix strategy: planar, rotor,
+// iso or a caller's own).  The vector goes through `row` (D floats of LDS
+// private to this 16-lane group, which lies inside one wave), and each lane
+// forms its E columns.
+template <int D, int E>
+__device__ __forceinline__ void rot_matrix_lanes(float (&x)[E], const float* __restrict__ M, float* row, int lane) {
+#pragma unroll
+  for (int i = 0; i < E; ++i) row[lane * E + i] = x[i];
+  __asm__ volatile("" ::: "memory");  // a wave's LDS accesses run in order
+  float y[E];
+#pragma unroll
+  for (int i = 0; i < E; ++i) y[i] = 0.f;
+  for (int k = 0; k < D; ++k) {
+    const float xk = row[k];
+#pragma unroll
+    for (int i = 0; i < E; ++i) y[i] = __builtin_fmaf(xk, M[(int64_t)k * D + lane * E + i], y[i]);
+  }
+  __asm__ volatile("" ::: "memory");
+#pragma unroll
+  for (int i = 0; i < E; ++i) x[i] = y[i];
+}
+
 // One (token, kv head) per 16 lanes, D/16 contiguous elements per lane.
-template <int D, int DT>
+// ROTM: K (and V when rotated) rotated by the matrix rot instead of H/sqrt(D).
+template <int D, int DT, bool ROTM = false>
 __global__ __launch_bounds__(256) void v1_store_kernel(
     const void* __restrict__ key, const void* __restrict__ value, int64_t n_tokens, int hkv,
     const float* __restrict__ mid_g, int kb, int vb, int v_rotate,
     const int64_t* __restrict__ slot_mapping, uint8_t* __restrict__ cache, int64_t num_blocks,
-    int block_size, int64_t s_blk, int64_t s_pos, int64_t s_head, float rscale) {
+    int block_size, int64_t s_blk, int64_t s_pos, int64_t s_head, float rscale,
+    const float* __restrict__ rot) {
   constexpr int E = D / 16;
   __shared__ uint8_t kc[16][D];
   __shared__ uint8_t vc[16][D];
+  __shared__ float xs[ROTM ? 16 : 1][ROTM ? D : 1];  // ROTM: the group's vector for the matrix product
   __shared__ float mids[16];
   const int lane = threadIdx.x & 15, grp = threadIdx.x >> 4;
   const int nmid = (1 << kb) - 1;
@@ -125,7 +151,8 @@ __global__ __launch_bounds__(256) void v1_store_kernel(
       const float den = nrm + 1e-8f;
 #pragma unroll
       for (int i = 0; i < E; ++i) x[i] = x[i] / den;
-      fwht_lanes<E, 16>(x, lane);
+      if constexpr (ROTM) rot_matrix_lanes<D, E>(x, rot, &xs[grp][0], lane);
+      else fwht_lanes<E, 16>(x, lane);
 #pragma unroll
       for (int i = 0; i < E; ++i) {
         const float y = x[i] * rscale;
@@ -138,7 +165,8 @@ __global__ __launch_bounds__(256) void v1_store_kernel(
       float v[E];
       load_elems<DT, E>(value, vi * D + lane * E, v);
       if (v_rotate & 1) {
-        fwht_lanes<E, 16>(v, lane);
+        if constexpr (ROTM) rot_matrix_lanes<D, E>(v, rot, &xs[grp][0], lane);
+        else fwht_lanes<E, 16>(v, lane);
 #pragma unroll
         for (int i = 0; i < E; ++i) v[i] = round_to_dtype<DT>(v[i] * rscale);
       }
@@ -387,7 +415,7 @@ __global__ __launch_bounds__(256, 2) void v1_attn_kernel(
     const int32_t* __restrict__ kv_start, int hq, int hkv, int lbs, int max_blocks,
     int64_t num_blocks, int64_t s_blk, int64_t s_pos, int64_t s_head,
     const float* __restrict__ cent, float qscale, int num_splits, float* __restrict__ ws_o,
-    float* __restrict__ ws_lse) {
+    float* __restrict__ ws_lse, const float* __restrict__ rot) {
   using A = V1A<D, KB, VB>;
   constexpr int NS = A::NS, NB = A::NB, E = D / 16;
   const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
@@ -422,7 +450,8 @@ __global__ __launch_bounds__(256, 2) void v1_attn_kernel(
     if (gg < G) {
       float y[E];
       load_elems<QT, E>(query, ((int64_t)b * hq + kvh * G + gg) * D + l16 * E, y);
-      fwht_lanes<E, 16>(y, l16);
+      if (rot != nullptr) rot_matrix_lanes<D, E>(y, rot, &qs[gg][0], l16);  // q M (matrix strategies)
+      else fwht_lanes<E, 16>(y, l16);
 #pragma unroll
       for (int i = 0; i < E; ++i) qs[gg][l16 * E + i] = y[i] * qscale;
     }
@@ -789,7 +818,7 @@ __global__ __launch_bounds__(256, VB == 2 ? 4 : 2) void v1_attn_g4_kernel(
     const int32_t* __restrict__ kv_start, int hq, int hkv, int lbs, int max_blocks,
     int64_t num_blocks, int64_t s_blk, int64_t s_pos, int64_t s_head,
     const float* __restrict__ cent, float qscale, int num_splits, float* __restrict__ ws_o,
-    float* __restrict__ ws_lse) {
+    float* __restrict__ ws_lse, const float* __restrict__ rot) {
   using A = V1A<D, KB, VB>;
   constexpr int NS = A::NS, NB = A::NB, E = D / 16;
   constexpr int G = 4;
@@ -818,7 +847,8 @@ __global__ __launch_bounds__(256, VB == 2 ? 4 : 2) void v1_attn_g4_kernel(
     if (gg < G) {
       float y[E];
       load_elems<QT, E>(query, ((int64_t)b * hq + kvh * G + gg) * D + l16 * E, y);
-      fwht_lanes<E, 16>(y, l16);
+      if (rot != nullptr) rot_matrix_lanes<D, E>(y, rot, &qs[gg][0], l16);  // q M (matrix strategies)
+      else fwht_lanes<E, 16>(y, l16);
 #pragma unroll
       for (int i = 0; i < E; ++i) qs[gg][l16 * E + i] = y[i] * qscale;
     }
@@ -1124,18 +1154,21 @@ template <int D>
 static hipError_t v1_launch_store(const void* k, const void* v, int dt, int64_t n, int hkv,
                                   const float* mids, int kb, int vb, int vrot, const int64_t* slots,
                                   uint8_t* cache, int64_t nb, int bs, int64_t sb, int64_t sp,
-                                  int64_t sh, hipStream_t st) {
+                                  int64_t sh, const float* rot, hipStream_t st) {
   const int64_t nvec = n * hkv;
   int64_t gsz = (nvec + 15) / 16;
   if (gsz > 256 * 16) gsz = 256 * 16;
   const float rs = fwht_scale(D);
   dim3 grid((unsigned)gsz), block(256);
   if (dt == F32)
-    v1_store_kernel<D, F32><<<grid, block, 0, st>>>(k, v, n, hkv, mids, kb, vb, vrot, slots, cache, nb, bs, sb, sp, sh, rs);
+    { if (rot) v1_store_kernel<D, F32, true><<<grid, block, 0, st>>>(k, v, n, hkv, mids, kb, vb, vrot, slots, cache, nb, bs, sb, sp, sh, 1.f, rot);
+      else v1_store_kernel<D, F32><<<grid, block, 0, st>>>(k, v, n, hkv, mids, kb, vb, vrot, slots, cache, nb, bs, sb, sp, sh, rs, nullptr); }
   else if (dt == F16)
-    v1_store_kernel<D, F16><<<grid, block, 0, st>>>(k, v, n, hkv, mids, kb, vb, vrot, slots, cache, nb, bs, sb, sp, sh, rs);
+    { if (rot) v1_store_kernel<D, F16, true><<<grid, block, 0, st>>>(k, v, n, hkv, mids, kb, vb, vrot, slots, cache, nb, bs, sb, sp, sh, 1.f, rot);
+      else v1_store_kernel<D, F16><<<grid, block, 0, st>>>(k, v, n, hkv, mids, kb, vb, vrot, slots, cache, nb, bs, sb, sp, sh, rs, nullptr); }
   else
-    v1_store_kernel<D, BF16><<<grid, block, 0, st>>>(k, v, n, hkv, mids, kb, vb, vrot, slots, cache, nb, bs, sb, sp, sh, rs);
+    { if (rot) v1_store_kernel<D, BF16, true><<<grid, block, 0, st>>>(k, v, n, hkv, mids, kb, vb, vrot, slots, cache, nb, bs, sb, sp, sh, 1.f, rot);
+      else v1_store_kernel<D, BF16><<<grid, block, 0, st>>>(k, v, n, hkv, mids, kb, vb, vrot, slots, cache, nb, bs, sb, sp, sh, rs, nullptr); }
   return hipGetLastError();
 }
 
@@ -1153,6 +1186,7 @@ struct V1Args {
   void* out;
   int ot;
   float* lse;  // optional per-row natural-log LSE (B*Hq floats)
+  const float* rot;  // rotation matrix (D x D fp32, x M), or null for H/sqrt(D)
 };
 
 template <int D, int KB, int VB>
@@ -1161,32 +1195,37 @@ static hipError_t v1_launch_attn3(const V1Args& a, hipStream_t st) {
   if constexpr (VB == 4) {
     if (a.vrot & 2) {  // Lloyd-Max V codes
       if (a.qt == F32)
-        v1_attn_kernel<D, KB, VB, F32, true><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.ks, a.hq, a.hkv, a.lbs, a.max_blocks, a.nb, a.sblk, a.spos, a.shead, a.cent, a.qscale, a.splits, a.wo, a.wl);
+        v1_attn_kernel<D, KB, VB, F32, true><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.ks, a.hq, a.hkv, a.lbs, a.max_blocks, a.nb, a.sblk, a.spos, a.shead, a.cent, a.qscale, a.splits, a.wo, a.wl, a.rot);
       else if (a.qt == F16)
-        v1_attn_kernel<D, KB, VB, F16, true><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.ks, a.hq, a.hkv, a.lbs, a.max_blocks, a.nb, a.sblk, a.spos, a.shead, a.cent, a.qscale, a.splits, a.wo, a.wl);
+        v1_attn_kernel<D, KB, VB, F16, true><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.ks, a.hq, a.hkv, a.lbs, a.max_blocks, a.nb, a.sblk, a.spos, a.shead, a.cent, a.qscale, a.splits, a.wo, a.wl, a.rot);
       else
-        v1_attn_kernel<D, KB, VB, BF16, true><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.ks, a.hq, a.hkv, a.lbs, a.max_blocks, a.nb, a.sblk, a.spos, a.shead, a.cent, a.qscale, a.splits, a.wo, a.wl);
+        v1_attn_kernel<D, KB, VB, BF16, true><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.ks, a.hq, a.hkv, a.lbs, a.max_blocks, a.nb, a.sblk, a.spos, a.shead, a.cent, a.qscale, a.splits, a.wo, a.wl, a.rot);
       goto merge;
     }
   }
   if (a.hq == 4 * a.hkv) {
     if (a.qt == F32)
-      v1_attn_g4_kernel<D, KB, VB, F32><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.ks, a.hq, a.hkv, a.lbs, a.max_blocks, a.nb, a.sblk, a.spos, a.shead, a.cent, a.qscale, a.splits, a.wo, a.wl);
+      v1_attn_g4_kernel<D, KB, VB, F32><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.ks, a.hq, a.hkv, a.lbs, a.max_blocks, a.nb, a.sblk, a.spos, a.shead, a.cent, a.qscale, a.splits, a.wo, a.wl, a.rot);
     else if (a.qt == F16)
-      v1_attn_g4_kernel<D, KB, VB, F16><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.ks, a.hq, a.hkv, a.lbs, a.max_blocks, a.nb, a.sblk, a.spos, a.shead, a.cent, a.qscale, a.splits, a.wo, a.wl);
+      v1_attn_g4_kernel<D, KB, VB, F16><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.ks, a.hq, a.hkv, a.lbs, a.max_blocks, a.nb, a.sblk, a.spos, a.shead, a.cent, a.qscale, a.splits, a.wo, a.wl, a.rot);
     else
-      v1_attn_g4_kernel<D, KB, VB, BF16><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.ks, a.hq, a.hkv, a.lbs, a.max_blocks, a.nb, a.sblk, a.spos, a.shead, a.cent, a.qscale, a.splits, a.wo, a.wl);
+      v1_attn_g4_kernel<D, KB, VB, BF16><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.ks, a.hq, a.hkv, a.lbs, a.max_blocks, a.nb, a.sblk, a.spos, a.shead, a.cent, a.qscale, a.splits, a.wo, a.wl, a.rot);
   } else if (a.qt == F32)
-    v1_attn_kernel<D, KB, VB, F32><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.ks, a.hq, a.hkv, a.lbs, a.max_blocks, a.nb, a.sblk, a.spos, a.shead, a.cent, a.qscale, a.splits, a.wo, a.wl);
+    v1_attn_kernel<D, KB, VB, F32><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.ks, a.hq, a.hkv, a.lbs, a.max_blocks, a.nb, a.sblk, a.spos, a.shead, a.cent, a.qscale, a.splits, a.wo, a.wl, a.rot);
   else if (a.qt == F16)
-    v1_attn_kernel<D, KB, VB, F16><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.ks, a.hq, a.hkv, a.lbs, a.max_blocks, a.nb, a.sblk, a.spos, a.shead, a.cent, a.qscale, a.splits, a.wo, a.wl);
+    v1_attn_kernel<D, KB, VB, F16><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.ks, a.hq, a.hkv, a.lbs, a.max_blocks, a.nb, a.sblk, a.spos, a.shead, a.cent, a.qscale, a.splits, a.wo, a.wl, a.rot);
   else
-    v1_attn_kernel<D, KB, VB, BF16><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.ks, a.hq, a.hkv, a.lbs, a.max_blocks, a.nb, a.sblk, a.spos, a.shead, a.cent, a.qscale, a.splits, a.wo, a.wl);
+    v1_attn_kernel<D, KB, VB, BF16><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.ks, a.hq, a.hkv, a.lbs, a.max_blocks, a.nb, a.sblk, a.spos, a.shead, a.cent, a.qscale, a.splits, a.wo, a.wl, a.rot);
 merge:
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int64_t rows = (int64_t)a.B * a.hq;
   const float rs = fwht_scale(D);
+  if ((a.vrot & 1) && a.rot != nullptr) {  // o M^T
+    if (a.ot == F32) return launch_merge_splits<D, F32, ROT_MATRIX>(a.wo, a.wl, rows, a.splits, a.rot, 1.f, a.out, st, a.lse);
+    if (a.ot == F16) return launch_merge_splits<D, F16, ROT_MATRIX>(a.wo, a.wl, rows, a.splits, a.rot, 1.f, a.out, st, a.lse);
+    return launch_merge_splits<D, BF16, ROT_MATRIX>(a.wo, a.wl, rows, a.splits, a.rot, 1.f, a.out, st, a.lse);
+  }
   if (a.vrot & 1) {
     if (a.ot == F32) return launch_merge_splits<D, F32, ROT_PLAIN>(a.wo, a.wl, rows, a.splits, nullptr, rs, a.out, st, a.lse);
     if (a.ot == F16) return launch_merge_splits<D, F16, ROT_PLAIN>(a.wo, a.wl, rows, a.splits, nullptr, rs, a.out, st, a.lse);
@@ -1216,12 +1255,12 @@ extern "C" int64_t ftq_v1_slot_bytes(int d, int key_bits, int value_bits) {
   return v1_geom(d, key_bits, value_bits).raw;
 }
 
-extern "C" int ftq_v1_store(const void* key, const void* value, int dtype, int64_t n_tokens,
+extern "C" int ftq_v1_store_rot(const void* key, const void* value, int dtype, int64_t n_tokens,
                             int num_kv_heads, int d, const float* midpoints, int key_bits,
                             int value_bits, int v_rotate, const int64_t* slot_mapping,
                             uint8_t* kv_cache, int64_t num_blocks, int block_size,
                             int64_t stride_block, int64_t stride_pos, int64_t stride_head,
-                            void* stream) {
+                            const float* rotation, void* stream) {
   FTQ_REQUIRE(d == 64 || d == 128 || d == 256, "v1 store: head_dim must be 64, 128 or 256");
   FTQ_REQUIRE(key_bits >= 2 && key_bits <= 4 && value_bits >= 2 && value_bits <= 4,
               "v1 store: key_bits and value_bits must be 2, 3 or 4");
@@ -1229,6 +1268,7 @@ extern "C" int ftq_v1_store(const void* key, const void* value, int dtype, int64
               "bad token / head / block counts");
   FTQ_REQUIRE(dtype >= F32 && dtype <= BF16, "dtype must be FTQ_F32, FTQ_F16 or FTQ_BF16");
   FTQ_REQUIRE(v_rotate >= 0 && v_rotate <= 3, "v_rotate: bit 0 = rotate V, bit 1 = Lloyd-Max V codes");
+  FTQ_REQUIRE(rotation == nullptr || aligned4(rotation), "rotation must be 4-byte aligned");
   const V1Geom g = v1_geom(d, key_bits, value_bits);
   FTQ_REQUIRE(stride_head >= g.raw, "stride_head is smaller than the slot bytes (see ftq_v1_slot_bytes)");
   FTQ_REQUIRE(stride_pos >= stride_head * num_kv_heads && stride_block >= stride_pos * block_size,
@@ -1242,12 +1282,21 @@ extern "C" int ftq_v1_store(const void* key, const void* value, int dtype, int64
   hipStream_t st = (hipStream_t)stream;
   hipError_t e;
   if (d == 64)
-    e = v1_launch_store<64>(key, value, dtype, n_tokens, num_kv_heads, midpoints, key_bits, value_bits, v_rotate, slot_mapping, kv_cache, num_blocks, block_size, stride_block, stride_pos, stride_head, st);
+    e = v1_launch_store<64>(key, value, dtype, n_tokens, num_kv_heads, midpoints, key_bits, value_bits, v_rotate, slot_mapping, kv_cache, num_blocks, block_size, stride_block, stride_pos, stride_head, rotation, st);
   else if (d == 128)
-    e = v1_launch_store<128>(key, value, dtype, n_tokens, num_kv_heads, midpoints, key_bits, value_bits, v_rotate, slot_mapping, kv_cache, num_blocks, block_size, stride_block, stride_pos, stride_head, st);
+    e = v1_launch_store<128>(key, value, dtype, n_tokens, num_kv_heads, midpoints, key_bits, value_bits, v_rotate, slot_mapping, kv_cache, num_blocks, block_size, stride_block, stride_pos, stride_head, rotation, st);
   else
-    e = v1_launch_store<256>(key, value, dtype, n_tokens, num_kv_heads, midpoints, key_bits, value_bits, v_rotate, slot_mapping, kv_cache, num_blocks, block_size, stride_block, stride_pos, stride_head, st);
+    e = v1_launch_store<256>(key, value, dtype, n_tokens, num_kv_heads, midpoints, key_bits, value_bits, v_rotate, slot_mapping, kv_cache, num_blocks, block_size, stride_block, stride_pos, stride_head, rotation, st);
   return hip_status(e);
+}
+
+extern "C" int ftq_v1_store(const void* key, const void* value, int dtype, int64_t n_tokens,
+                            int num_kv_heads, int d, const float* midpoints, int key_bits,
+                            int value_bits, int v_rotate, const int64_t* slot_mapping,
+                            uint8_t* kv_cache, int64_t num_blocks, int block_size,
+                            int64_t stride_block, int64_t stride_pos, int64_t stride_head,
+                            void* stream) {
+  return ftq_v1_store_rot(key, value, dtype, n_tokens, num_kv_heads, d, midpoints, key_bits, value_bits, v_rotate, slot_mapping, kv_cache, num_blocks, block_size, stride_block, stride_pos, stride_head, nullptr, stream);
 }
 
 extern "C" int64_t ftq_v1_workspace_bytes(int batch, int num_q_heads, int d, int num_splits) {
@@ -1259,15 +1308,17 @@ extern "C" int ftq_v1_default_splits(int batch, int num_kv_heads, int max_seq_le
   return auto_splits(batch, num_kv_heads, max_seq_len, 1024);
 }
 
-extern "C" int ftq_v1_decode_attention_lse(
+extern "C" int ftq_v1_decode_attention_rot(
     const void* query, int q_dtype, const uint8_t* kv_cache, int64_t num_blocks, int block_size,
     int64_t stride_block, int64_t stride_pos, int64_t stride_head, const int32_t* block_table,
     int max_blocks_per_seq, const int32_t* seq_lens, const int32_t* kv_start, int batch,
     int num_q_heads, int num_kv_heads, int d, const float* centroids, int key_bits,
     int value_bits, float scale, int v_rotate, int num_splits, void* workspace,
-    int64_t workspace_bytes, void* out, int out_dtype, float* lse_out, void* stream) {
+    int64_t workspace_bytes, void* out, int out_dtype, float* lse_out, const float* rotation,
+    void* stream) {
   FTQ_REQUIRE(d == 128, "v1 decode attention: head_dim must be 128");
   FTQ_REQUIRE(v_rotate >= 0 && v_rotate <= 3, "v_rotate: bit 0 = un-rotate V, bit 1 = Lloyd-Max V codes");
+  FTQ_REQUIRE(rotation == nullptr || aligned4(rotation), "rotation must be 4-byte aligned");
   FTQ_REQUIRE(key_bits >= 2 && key_bits <= 4 && value_bits >= 2 && value_bits <= 4,
               "v1 decode attention: key_bits and value_bits must be 2, 3 or 4");
   FTQ_REQUIRE(block_size >= 16 && block_size <= 4096 && (block_size & (block_size - 1)) == 0,
@@ -1302,7 +1353,8 @@ extern "C" int ftq_v1_decode_attention_lse(
   while ((1 << a.lbs) < block_size) ++a.lbs;
   a.nb = num_blocks; a.sblk = stride_block; a.spos = stride_pos; a.shead = stride_head;
   a.cent = centroids;
-  a.qscale = fwht_scale(d) * scale * 1.4426950408889634f;
+  a.qscale = (rotation != nullptr ? 1.f : fwht_scale(d)) * scale * 1.4426950408889634f;
+  a.rot = rotation;
   a.splits = num_splits; a.vrot = v_rotate;
   a.wo = static_cast<float*>(workspace);
   a.wl = a.wo + (int64_t)batch * num_q_heads * num_splits * d;
@@ -1313,6 +1365,16 @@ extern "C" int ftq_v1_decode_attention_lse(
   else if (key_bits == 3) e = v1_launch_attn2<128, 3>(value_bits, a, st);
   else e = v1_launch_attn2<128, 4>(value_bits, a, st);
   return hip_status(e);
+}
+
+extern "C" int ftq_v1_decode_attention_lse(
+    const void* query, int q_dtype, const uint8_t* kv_cache, int64_t num_blocks, int block_size,
+    int64_t stride_block, int64_t stride_pos, int64_t stride_head, const int32_t* block_table,
+    int max_blocks_per_seq, const int32_t* seq_lens, const int32_t* kv_start, int batch,
+    int num_q_heads, int num_kv_heads, int d, const float* centroids, int key_bits,
+    int value_bits, float scale, int v_rotate, int num_splits, void* workspace,
+    int64_t workspace_bytes, void* out, int out_dtype, float* lse_out, void* stream) {
+  return ftq_v1_decode_attention_rot(query, q_dtype, kv_cache, num_blocks, block_size, stride_block, stride_pos, stride_head, block_table, max_blocks_per_seq, seq_lens, kv_start, batch, num_q_heads, num_kv_heads, d, centroids, key_bits, value_bits, scale, v_rotate, num_splits, workspace, workspace_bytes, out, out_dtype, lse_out, nullptr, stream);
 }
 
 extern "C" int ftq_v1_decode_attention(

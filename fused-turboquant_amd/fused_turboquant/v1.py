@@ -43,6 +43,11 @@ _SIG = {
     "ftq_v1_decode_attention_lse": ["vp", "i32", "vp", "i64", "i32", "i64", "i64", "i64", "vp", "i32",
                                     "vp", "vp", "i32", "i32", "i32", "i32", "vp", "i32", "i32", "f32",
                                     "i32", "i32", "vp", "i64", "vp", "i32", "vp", "vp"],
+    "ftq_v1_store_rot": ["vp", "vp", "i32", "i64", "i32", "i32", "vp", "i32", "i32", "i32", "vp", "vp",
+                         "i64", "i32", "i64", "i64", "i64", "vp", "vp"],
+    "ftq_v1_decode_attention_rot": ["vp", "i32", "vp", "i64", "i32", "i64", "i64", "i64", "vp", "i32",
+                                    "vp", "vp", "i32", "i32", "i32", "i32", "vp", "i32", "i32", "f32",
+                                    "i32", "i32", "vp", "i64", "vp", "i32", "vp", "vp", "vp"],
 }
 
 
@@ -133,9 +138,38 @@ def _v_flags(v_rotate: bool, v_lloyd_max: bool) -> int:
     return (1 if (v_rotate or v_lloyd_max) else 0) | (2 if v_lloyd_max else 0)
 
 
+def planar_rotation(head_dim: int, seed: int = 42, device="cpu") -> torch.Tensor:
+    """Rotation matrix M (x M, float32 [d, d]) of the planar strategy
+    (reference ``vllm_plugin/rotation/planar.py:32-67``,
+    ``core/planar.py:48-68``): pair p of coordinates (2p, 2p + 1) is turned by
+    an angle theta_p = 2 pi U[0, 1) from a CPU ``torch.Generator`` seeded
+    ``seed``; block p of M is [[cos, sin], [-sin, cos]], so
+    x M = [cos x0 - sin x1, sin x0 + cos x1] per pair."""
+    if head_dim % 2:
+        raise ValueError("planar rotation needs an even head_dim")
+    n = head_dim // 2
+    gen = torch.Generator(device="cpu").manual_seed(seed)
+    theta = torch.rand(n, generator=gen, device="cpu") * (2.0 * math.pi)
+    c, sn = theta.cos().to(torch.float32), theta.sin().to(torch.float32)
+    m = torch.zeros(head_dim, head_dim, dtype=torch.float32)
+    i = torch.arange(n)
+    m[2 * i, 2 * i] = c
+    m[2 * i, 2 * i + 1] = sn
+    m[2 * i + 1, 2 * i] = -sn
+    m[2 * i + 1, 2 * i + 1] = c
+    return m.to(device)
+
+
+def _rotation_arg(rotation: torch.Tensor, d: int, dev) -> torch.Tensor:
+    if rotation.shape != (d, d):
+        raise ValueError("rotation must be a [head_dim, head_dim] matrix")
+    return rotation.to(device=dev, dtype=torch.float32).contiguous()
+
+
 def v1_store(key: torch.Tensor, value: torch.Tensor, kv_cache: torch.Tensor,
              slot_mapping: torch.Tensor, midpoints: torch.Tensor, key_bits: int,
-             value_bits: int, v_rotate: bool = False, v_lloyd_max: bool = False) -> None:
+             value_bits: int, v_rotate: bool = False, v_lloyd_max: bool = False,
+             rotation: torch.Tensor | None = None) -> None:
     """Quantise ``key``/``value`` [n, Hkv, d] into their slots (``slot_mapping`` [n]
     int64; negative entries are skipped).  ``v_lloyd_max`` (implies
     ``v_rotate``): 4-bit V takes Lloyd-Max codes against the K midpoints and its
@@ -162,10 +196,14 @@ def v1_store(key: torch.Tensor, value: torch.Tensor, kv_cache: torch.Tensor,
     sb, sp, sh = _strides(kv_cache)
     mids = midpoints.to(torch.float32).contiguous()
     L = _bind()
-    _lib.check(L.ftq_v1_store(
-        k.data_ptr(), v.data_ptr(), _lib.dtype_code(k.dtype), n, hkv, d, mids.data_ptr(),
-        key_bits, value_bits, _v_flags(v_rotate, v_lloyd_max), slot_mapping.contiguous().data_ptr(),
-        kv_cache.data_ptr(), nb, bs, sb, sp, sh, _lib.stream_ptr(dev)))
+    args = (k.data_ptr(), v.data_ptr(), _lib.dtype_code(k.dtype), n, hkv, d, mids.data_ptr(),
+            key_bits, value_bits, _v_flags(v_rotate, v_lloyd_max), slot_mapping.contiguous().data_ptr(),
+            kv_cache.data_ptr(), nb, bs, sb, sp, sh)
+    if rotation is None:
+        _lib.check(L.ftq_v1_store(*args, _lib.stream_ptr(dev)))
+    else:  # a matrix strategy (planar, rotor, iso): x M in the kernel
+        rot = _rotation_arg(rotation, d, dev)
+        _lib.check(L.ftq_v1_store_rot(*args, rot.data_ptr(), _lib.stream_ptr(dev)))
 
 
 def default_splits(batch: int, num_kv_heads: int, max_seq_len: int) -> int:
@@ -182,7 +220,8 @@ def v1_decode_attention(query: torch.Tensor, kv_cache: torch.Tensor, block_table
                         v_lloyd_max: bool = False,
                         kv_start: torch.Tensor | None = None, num_splits: int | None = None,
                         max_seq_len: int | None = None, out: torch.Tensor | None = None,
-                        workspace: torch.Tensor | None = None, lse: torch.Tensor | None = None) -> torch.Tensor:
+                        workspace: torch.Tensor | None = None, lse: torch.Tensor | None = None,
+                        rotation: torch.Tensor | None = None) -> torch.Tensor:
     """query [B, Hq, d] -> [B, Hq, d] (query dtype unless ``out`` is given).
 
     Attends positions [kv_start[b], seq_lens[b]) of block-table row b
@@ -236,7 +275,11 @@ def v1_decode_attention(query: torch.Tensor, kv_cache: torch.Tensor, block_table
             ks.data_ptr() if ks is not None else None, B, hq, hkv, d, cent.data_ptr(), key_bits,
             value_bits, float(scale), _v_flags(v_rotate, v_lloyd_max), int(num_splits), workspace.data_ptr(),
             workspace.numel(), out.data_ptr(), _lib.dtype_code(out.dtype))
-    if lse is None:
+    if rotation is not None:  # a matrix strategy: q M, and o M^T with v_rotate
+        rot = _rotation_arg(rotation, d, dev)
+        _lib.check(L.ftq_v1_decode_attention_rot(*args, lse.data_ptr() if lse is not None else None,
+                                                 rot.data_ptr(), _lib.stream_ptr(dev)))
+    elif lse is None:
         _lib.check(L.ftq_v1_decode_attention(*args, _lib.stream_ptr(dev)))
     else:
         _lib.check(L.ftq_v1_decode_attention_lse(*args, lse.data_ptr(), _lib.stream_ptr(dev)))
@@ -249,7 +292,8 @@ class TurboQuantV1Layer:
     V-rotation switch (``TURBOQUANT_V_ROTATE``, ``v1_backend.py:733-740``)."""
 
     def __init__(self, head_dim: int, key_bits: int, value_bits: int, v_rotate: bool = False,
-                 centroids: torch.Tensor | None = None, device="cuda", v_lloyd_max: bool = False):
+                 centroids: torch.Tensor | None = None, device="cuda", v_lloyd_max: bool = False,
+                 kind: str = "rht", rotation: torch.Tensor | None = None):
         _check_bits(head_dim, key_bits, value_bits)
         self.head_dim = head_dim
         self.key_bits = key_bits
@@ -261,6 +305,17 @@ class TurboQuantV1Layer:
             raise ValueError("centroids must have 2^key_bits entries")
         self.centroids = torch.sort(c.to(torch.float32)).values.to(device)
         self.midpoints = midpoints_of(self.centroids)
+        # rotation strategy (TURBOQUANT_KIND): rht = the kernels' own H/sqrt(d);
+        # planar = a matrix x M applied in the kernels; a caller's matrix the same
+        self.kind = kind
+        if rotation is not None:
+            self.rotation = rotation.to(device=device, dtype=torch.float32).contiguous()
+        elif kind == "rht":
+            self.rotation = None
+        elif kind == "planar":
+            self.rotation = planar_rotation(head_dim, device=device)
+        else:
+            raise NotImplementedError(f"rotation kind {kind!r}: rht, planar or an explicit matrix")
 
     def kv_cache_shape(self, num_blocks: int, block_size: int, num_kv_heads: int) -> tuple:
         return get_kv_cache_shape(num_blocks, block_size, num_kv_heads, self.head_dim,
@@ -268,12 +323,12 @@ class TurboQuantV1Layer:
 
     def store(self, key, value, kv_cache, slot_mapping) -> None:
         v1_store(key, value, kv_cache, slot_mapping, self.midpoints, self.key_bits,
-                 self.value_bits, self.v_rotate, self.v_lloyd_max)
+                 self.value_bits, self.v_rotate, self.v_lloyd_max, rotation=self.rotation)
 
     def decode(self, query, kv_cache, block_table, seq_lens, **kw) -> torch.Tensor:
         return v1_decode_attention(query, kv_cache, block_table, seq_lens, self.centroids,
                                    self.key_bits, self.value_bits, v_rotate=self.v_rotate,
-                                   v_lloyd_max=self.v_lloyd_max, **kw)
+                                   v_lloyd_max=self.v_lloyd_max, rotation=self.rotation, **kw)
 
 
 # --------------------------------------------------------------------------

@@ -186,6 +186,20 @@ int ftq_v1_store(const void* key, const void* value, int dtype, int64_t n_tokens
                  int v_rotate, const int64_t* slot_mapping, uint8_t* kv_cache,
                  int64_t num_blocks, int block_size, int64_t stride_block, int64_t stride_pos,
                  int64_t stride_head, void* stream);
+/*
+ * ftq_v1_store with the rotation of a matrix strategy: K (and V when
+ * v_rotate) rotated by x M, `rotation` = M row-major d x d float32 on the
+ * device (NULL = the unsigned Hadamard H/sqrt(d)).  Replaces the in-kernel
+ * (D, D) and block-diagonal rotations of _fused_store_matrix /
+ * _fused_store_block_diag (vllm_plugin/triton_inkernel_store.py:459-541,
+ * 649-744) behind MatrixRotationStrategy.launch_store
+ * (vllm_plugin/rotation/matrix.py:50-70): planar, rotor, iso.
+ */
+int ftq_v1_store_rot(const void* key, const void* value, int dtype, int64_t n_tokens,
+                     int num_kv_heads, int d, const float* midpoints, int key_bits, int value_bits,
+                     int v_rotate, const int64_t* slot_mapping, uint8_t* kv_cache,
+                     int64_t num_blocks, int block_size, int64_t stride_block, int64_t stride_pos,
+                     int64_t stride_head, const float* rotation, void* stream);
 
 /* Workspace bytes ftq_v1_decode_attention needs: batch*Hq*splits*(d+1)*4. */
 int64_t ftq_v1_workspace_bytes(int batch, int num_q_heads, int d, int num_splits);
@@ -230,6 +244,22 @@ int ftq_v1_decode_attention_lse(const void* query, int q_dtype, const uint8_t* k
                                 float scale, int v_rotate, int num_splits, void* workspace,
                                 int64_t workspace_bytes, void* out, int out_dtype, float* lse_out,
                                 void* stream);
+/*
+ * ftq_v1_decode_attention_lse for a matrix strategy: the query is rotated
+ * by q M and, with v_rotate, the output by o M^T, `rotation` = M row-major
+ * d x d float32 on the device (NULL = H/sqrt(d)).  Replaces
+ * rotate_for_decode's q @ M (vllm_plugin/rotation/matrix.py:47-48) and the
+ * o @ M^T un-rotation (v1_backend.py:1086-1092) around stage 1.
+ */
+int ftq_v1_decode_attention_rot(const void* query, int q_dtype, const uint8_t* kv_cache,
+                                int64_t num_blocks, int block_size, int64_t stride_block,
+                                int64_t stride_pos, int64_t stride_head, const int32_t* block_table,
+                                int max_blocks_per_seq, const int32_t* seq_lens,
+                                const int32_t* kv_start, int batch, int num_q_heads, int num_kv_heads,
+                                int d, const float* centroids, int key_bits, int value_bits,
+                                float scale, int v_rotate, int num_splits, void* workspace,
+                                int64_t workspace_bytes, void* out, int out_dtype, float* lse_out,
+                                const float* rotation, void* stream);
 
 /* ---------------------------------------------------------------------------
  * Raw fp16 slots of the boundary-protection layers (TURBOQUANT_BOUNDARY_PROTECT

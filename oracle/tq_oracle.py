@@ -392,7 +392,7 @@ def v1_quantize_k(y: np.ndarray, midpoints: np.ndarray) -> np.ndarray:
     return np.searchsorted(m, np.asarray(y, np.float32), side="right").astype(np.uint8)
 
 
-def v1_k_rotate(k: np.ndarray):
+def v1_k_rotate(k: np.ndarray, rotation=None):
     """K path before the quantiser (triton_inkernel_store.py:406-430):
     norm = sqrt(sum k^2 + 1e-16); x = k / (norm + 1e-8); y = H x / sqrt(d)
     (Sylvester butterflies, no random signs).  Returns (y f32, norm f32)."""
@@ -401,7 +401,10 @@ def v1_k_rotate(k: np.ndarray):
     k64 = k.astype(np.float64)
     norm = np.sqrt(np.sum(k64 * k64, axis=-1) + 1e-16).astype(np.float32)
     x = (k / (norm[..., None] + np.float32(1e-8))).astype(np.float32)
-    y = (fwht_unscaled(x) * fwht_scale(d)).astype(np.float32)
+    if rotation is None:
+        y = (fwht_unscaled(x) * fwht_scale(d)).astype(np.float32)
+    else:  # a matrix strategy: x M (MatrixRotationStrategy.rotate_for_store, rotation/matrix.py:44-45)
+        y = (x.astype(np.float64) @ np.asarray(rotation, np.float64)).astype(np.float32)
     return y, norm
 
 
@@ -455,7 +458,7 @@ def v1_quantize_v_lloyd(v: np.ndarray, midpoints: np.ndarray):
 
 def v1_store(key: np.ndarray, value: np.ndarray, slot_mapping: np.ndarray, kv_cache: np.ndarray,
              midpoints: np.ndarray, kb: int, vb: int, v_rotate: bool = False,
-             value_dtype: str = "f32", v_lloyd_max: bool = False):
+             value_dtype: str = "f32", v_lloyd_max: bool = False, rotation=None):
     """Write [N, H, d] float32 K/V (already converted from their dtype) into
     ``kv_cache`` uint8[nb, bs, H, slot] in place.  Negative slots are skipped
     (triton_inkernel_store.py:394-395).  With ``v_rotate`` V is first rotated
@@ -472,10 +475,12 @@ def v1_store(key: np.ndarray, value: np.ndarray, slot_mapping: np.ndarray, kv_ca
     nb, bs, Hc, slot = kv_cache.shape
     assert Hc == H
     g = v1_geometry(d, kb, vb)
-    y, norm = v1_k_rotate(key)
+    y, norm = v1_k_rotate(key, rotation)
     kcodes = v1_quantize_k(y, midpoints)
     if v_rotate:
-        value = v1_round_dtype((fwht_unscaled(value) * fwht_scale(d)).astype(np.float32), value_dtype)
+        vr = (fwht_unscaled(value) * fwht_scale(d)) if rotation is None else \
+            np.asarray(value, np.float64) @ np.asarray(rotation, np.float64)
+        value = v1_round_dtype(vr.astype(np.float32), value_dtype)
     if v_lloyd_max and vb == 4:
         vq, sc, t = v1_quantize_v_lloyd(value, midpoints)
         mn = np.zeros_like(sc)
@@ -538,7 +543,8 @@ def v1_dequant(kv_cache: np.ndarray, d: int, kb: int, vb: int, centroids: np.nda
 def v1_decode_attention(q: np.ndarray, kv_cache: np.ndarray, block_table: np.ndarray,
                         seq_lens: np.ndarray, centroids: np.ndarray, kb: int, vb: int,
                         scale: float, kv_start=None, v_rotate: bool = False,
-                        norm_correction: bool = True, v_lloyd_max: bool = False):
+                        norm_correction: bool = True, v_lloyd_max: bool = False,
+                        rotation=None):
     """Decode attention over the v1 slot cache, float64.
 
     q [B, Hq, d] (float32 values of the query); q_rot = q @ M with
@@ -552,7 +558,7 @@ def v1_decode_attention(q: np.ndarray, kv_cache: np.ndarray, block_table: np.nda
     B, Hq, d = q.shape
     nb, bs, Hkv, slot = kv_cache.shape
     G = Hq // Hkv
-    M = sylvester(d) / math.sqrt(d)
+    M = sylvester(d) / math.sqrt(d) if rotation is None else np.asarray(rotation, np.float64)
     q_rot = q @ M
     k_hat, v_hat = v1_dequant(kv_cache, d, kb, vb, centroids, norm_correction, v_lloyd_max)
     out = np.zeros((B, Hq, d))

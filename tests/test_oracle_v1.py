@@ -285,3 +285,35 @@ def test_v_lloyd_max_dequant_norm_and_quality():
     rec = v_hat.reshape(-1, H, d)[:N] @ M.T
     cos = np.sum(rec * v, axis=-1) / (np.linalg.norm(rec, axis=-1) * np.linalg.norm(v, axis=-1))
     assert cos.min() > 0.98
+
+
+def test_planar_rotation_matrix():
+    """The planar strategy's M (x M): orthogonal with determinant 1, nonzero
+    only on the 2x2 diagonal blocks, and x M turns each coordinate pair by
+    +theta_p: e_{2p} M = (cos, sin) on (2p, 2p+1), e_{2p+1} M = (-sin, cos)
+    (the row-vector form of the reference's block [[c, s], [-s, c]],
+    rotation/planar.py:32-52); the angles are 2 pi U[0, 1) from the seeded
+    CPU generator, so every rank builds the same matrix."""
+    import math as _m
+    import torch
+    from fused_turboquant import v1
+    d = 128
+    M = v1.planar_rotation(d).double().numpy()
+    assert np.abs(M @ M.T - np.eye(d)).max() < 1e-6
+    assert abs(np.linalg.det(M) - 1.0) < 1e-5
+    blockmask = np.kron(np.eye(d // 2), np.ones((2, 2))).astype(bool)
+    assert not M[~blockmask].any()
+    theta = torch.rand(d // 2, generator=torch.Generator().manual_seed(42)).double().numpy() * 2 * _m.pi
+    e = np.eye(d)
+    for p in (0, 1, 17, 63):
+        r0, r1 = e[2 * p] @ M, e[2 * p + 1] @ M
+        assert np.allclose(r0[2 * p:2 * p + 2], [np.cos(theta[p]), np.sin(theta[p])], atol=1e-6)
+        assert np.allclose(r1[2 * p:2 * p + 2], [-np.sin(theta[p]), np.cos(theta[p])], atol=1e-6)
+    assert np.array_equal(v1.planar_rotation(d).numpy(), v1.planar_rotation(d).numpy())
+    # the oracle's matrix path with M = H / sqrt(d) reproduces its Hadamard path
+    rng = np.random.default_rng(0)
+    k = rng.standard_normal((5, 2, d)).astype(np.float32)
+    H = O.sylvester(d) / _m.sqrt(d)
+    y0, n0 = O.v1_k_rotate(k)
+    y1, n1 = O.v1_k_rotate(k, H)
+    assert np.abs(y0 - y1).max() < 1e-6 and np.array_equal(n0, n1)

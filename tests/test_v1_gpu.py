@@ -346,3 +346,79 @@ def test_decode_parity_v_lloyd_max(cuda, kb, hq, hkv, splits):
     got = out.float().cpu().numpy()
     assert not got[0].any()
     _check_attn(got, want, f"v1 lloyd kb={kb} hq={hq} hkv={hkv} S={splits}")
+
+
+@pytest.mark.parametrize("kb,vb", [(4, 2), (3, 3)])
+def test_store_parity_planar_matrix(cuda, kb, vb):
+    """Matrix-strategy store (planar, x M in the kernel; reference
+    triton_inkernel_store.py:459-541 behind rotation/matrix.py:50-70) against
+    the oracle's x M in float64: K codes equal except where the rotated unit
+    vector sits within 1e-5 of a midpoint (the kernel's fp32 product is
+    rounded differently), K norms within 1e-3, V (rotated by M, rounded to
+    bf16, min/max coded) within one code step."""
+    from fused_turboquant import v1
+    d, bs, hkv, nb = 128, 16, 4, 8
+    n = nb * bs
+    g = torch.Generator().manual_seed(41 + kb)
+    layer = v1.TurboQuantV1Layer(d, kb, vb, v_rotate=True, kind="planar", device=cuda)
+    M = layer.rotation.cpu().numpy()
+    k, v = _kv(g, n, hkv, d, torch.bfloat16)
+    slots = torch.randperm(nb * bs, generator=g)[:n]
+    cache = torch.zeros(layer.kv_cache_shape(nb, bs, hkv), dtype=torch.uint8, device=cuda)
+    layer.store(k.to(cuda), v.to(cuda), cache, slots.to(cuda))
+    got = cache.cpu().numpy()
+    want = np.zeros_like(got)
+    mids = layer.midpoints.cpu().numpy()
+    O.v1_store(k.float().numpy(), v.float().numpy(), slots.numpy(), want, mids, kb, vb,
+               v_rotate=True, value_dtype="bf16", rotation=M)
+    kg, kng, vg, scg, zg = O.v1_unpack(got, d, kb, vb)
+    kw, knw, vw, scw, zw = O.v1_unpack(want, d, kb, vb)
+    y, _ = O.v1_k_rotate(k.float().numpy(), M)
+    blk, off = slots.numpy() // bs, slots.numpy() % bs
+    dk = kg[blk, off].astype(int) - kw[blk, off].astype(int)
+    near = np.min(np.abs(y[..., None] - mids[None, None, None, :]), axis=-1) < 1e-5
+    bad = (dk != 0) & ~((np.abs(dk) == 1) & near)
+    print(f"[v1 planar store kb={kb} vb={vb}] K code ties={(dk != 0).sum()} of {dk.size}")
+    assert not bad.any()
+    kn_g, kn_w = kng[blk, off].astype(np.float64), knw[blk, off].astype(np.float64)
+    assert np.abs(kn_g - kn_w).max() <= 1e-3 * np.abs(kn_w).max()
+    vhg = vg[blk, off] * scg[blk, off][..., None].astype(np.float64) + zg[blk, off][..., None].astype(np.float64)
+    vhw = vw[blk, off] * scw[blk, off][..., None].astype(np.float64) + zw[blk, off][..., None].astype(np.float64)
+    step = np.maximum(scg[blk, off], scw[blk, off]).astype(np.float64)[..., None]
+    assert (np.abs(vhg - vhw) <= 1.01 * step + 1e-3).all()
+
+
+@pytest.mark.parametrize("kb,vb", [(4, 2), (3, 3), (2, 4)])
+@pytest.mark.parametrize("hq,hkv", [(16, 4), (8, 1)])
+def test_decode_parity_planar_matrix(cuda, kb, vb, hq, hkv):
+    """Matrix-strategy decode: q M in the kernel prologue and o M^T in the merge
+    (reference rotation/matrix.py:47-48, v1_backend.py:1086-1092) against the
+    oracle's float64 attention over the same cache bytes (written by the
+    oracle with the same M)."""
+    from fused_turboquant import v1
+    d, bs, nb = 128, 16, 48
+    g = torch.Generator().manual_seed(300 + kb * 10 + vb + hq)
+    M = v1.planar_rotation(d).numpy()
+    slot = max(v1.slot_size(d, kb, vb), 128)
+    cache = np.zeros((nb, bs, hkv, slot), np.uint8)
+    k, v = _kv(g, nb * bs, hkv, d, torch.bfloat16, outliers=True)
+    c = v1.default_centroids(d, kb).numpy()
+    slots = torch.randperm(nb * bs, generator=g).numpy()
+    O.v1_store(k.float().numpy(), v.float().numpy(), slots, cache, O.v1_midpoints(c), kb, vb,
+               v_rotate=True, value_dtype="bf16", rotation=M)
+    lens = [0, 1, 17, 100, 257, 64]
+    starts = [0, 0, 5, 40, 0, 63]
+    B = len(lens)
+    bt = torch.randint(0, nb, (B, 20), generator=g, dtype=torch.int32)
+    q = torch.randn(B, hq, d, generator=g).to(torch.bfloat16)
+    sl = torch.tensor(lens, dtype=torch.int32)
+    ks = torch.tensor(starts, dtype=torch.int32)
+    for splits in (1, 5):
+        out = v1.v1_decode_attention(q.to(cuda), torch.from_numpy(cache).to(cuda), bt.to(cuda), sl.to(cuda),
+                                     torch.from_numpy(c).to(cuda), kb, vb, v_rotate=True, kv_start=ks.to(cuda),
+                                     num_splits=splits, rotation=torch.from_numpy(M).to(cuda))
+        want = O.v1_decode_attention(q.float().numpy(), cache, bt.numpy(), sl.numpy(), c, kb, vb,
+                                     1 / math.sqrt(d), kv_start=ks.numpy(), v_rotate=True, rotation=M)
+        got = out.float().cpu().numpy()
+        assert not got[0].any()
+        _check_attn(got, want, f"v1 planar kb={kb} vb={vb} hq={hq} hkv={hkv} S={splits}")
