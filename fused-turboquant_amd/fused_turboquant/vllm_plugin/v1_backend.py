@@ -214,6 +214,12 @@ class FusedTurboQuantV1Impl(_ImplBase):
         self._prefix_capacity = _defer_capacity() if self.defer_prefill else 0
         # Lloyd-Max V codes (4-bit V; other widths stay uniform but rotated, as in the reference)
         self.v_lloyd_max = not self._is_raw and env_flag("TURBOQUANT_V_LLOYD_MAX")
+        # rotation strategy (reference v1_backend.py:516-523): rht, or planar as a
+        # rotation matrix applied inside the store / decode / merge kernels
+        self.kind = os.environ.get("TURBOQUANT_KIND", "rht").strip().lower() or "rht"
+        if not self._is_raw and self.kind not in ("rht", "planar"):
+            raise NotImplementedError(f"TURBOQUANT_KIND={self.kind!r}: rht and planar are supported "
+                                      "(rotor and iso are not)")
 
     # -- per-layer state ---------------------------------------------------
     def _state(self, layer, device) -> V1.TurboQuantV1Layer:
@@ -224,7 +230,7 @@ class FusedTurboQuantV1Impl(_ImplBase):
                 cent = None
             st = V1.TurboQuantV1Layer(self.head_size, self.key_bits, self.value_bits,
                                       v_rotate=self.v_rotate, centroids=cent, device=device,
-                                      v_lloyd_max=self.v_lloyd_max)
+                                      v_lloyd_max=self.v_lloyd_max, kind=self.kind)
             layer._fused_tq_state = st
         return st
 
@@ -325,7 +331,7 @@ class FusedTurboQuantV1Impl(_ImplBase):
         V1.v1_decode_attention(q, kv_cache, bt, sl, st.centroids, self.key_bits, self.value_bits,
                                scale=self.scale, v_rotate=self.v_rotate, v_lloyd_max=self.v_lloyd_max,
                                kv_start=plen.expand(B).contiguous(),
-                               max_seq_len=msl, out=o2, lse=l2)
+                               max_seq_len=msl, out=o2, lse=l2, rotation=st.rotation)
         # merge (a row empty in both phases stays 0)
         m = torch.maximum(l1, l2)
         m = torch.where(torch.isneginf(m), torch.zeros_like(m), m)
@@ -341,7 +347,7 @@ class FusedTurboQuantV1Impl(_ImplBase):
             return RAW.raw_decode_attention(q, kv_cache, bt, sl, scale=self.scale, max_seq_len=msl)
         return V1.v1_decode_attention(q, kv_cache, bt, sl, st.centroids, self.key_bits, self.value_bits,
                                       scale=self.scale, v_rotate=self.v_rotate, v_lloyd_max=self.v_lloyd_max,
-                                      max_seq_len=msl)
+                                      max_seq_len=msl, rotation=st.rotation)
 
     def _prefill(self, q, k, v, kv_cache, md, nd, ndt, st):
         """Prefill sequences nd.. of the batch (tokens ndt..N)."""

@@ -45,13 +45,15 @@ def _causal_ref(q, k, v, scale):
     return out
 
 
-def _run_step(cuda, seqs, dtype_str, hq, hkv, vrot, monkeypatch, seed, bs=16, protect="0", lloyd=False):
+def _run_step(cuda, seqs, dtype_str, hq, hkv, vrot, monkeypatch, seed, bs=16, protect="0", lloyd=False,
+              kind="rht"):
     """seqs: list of (cached_len, query_len), decodes (query_len 1, cached > 0) first.
     Stores the cached tokens in earlier update calls, then runs one step."""
     from fused_turboquant import vllm_plugin as vp
     monkeypatch.setenv("TURBOQUANT_BOUNDARY_PROTECT", protect)
     monkeypatch.setenv("TURBOQUANT_V_ROTATE", "1" if vrot else "0")
     monkeypatch.setenv("TURBOQUANT_V_LLOYD_MAX", "1" if lloyd else "0")
+    monkeypatch.setenv("TURBOQUANT_KIND", kind)
     g = torch.Generator().manual_seed(seed)
     Bk = vp.FusedTurboQuantV1Backend
     impl = vp.FusedTurboQuantV1Impl(hq, D, 1 / math.sqrt(D), hkv, kv_cache_dtype=dtype_str)
@@ -109,6 +111,7 @@ def _run_step(cuda, seqs, dtype_str, hq, hkv, vrot, monkeypatch, seed, bs=16, pr
     cache_np = cache.view(torch.uint8).cpu().numpy()
     raw = impl._is_raw
     cent = None if raw else layer._fused_tq_state.centroids.cpu().numpy()
+    rot = None if raw or layer._fused_tq_state.rotation is None else layer._fused_tq_state.rotation.cpu().numpy()
     kb, vb = impl.key_bits, impl.value_bits
     for i, (c, q) in enumerate(seqs):
         a = int(qsl[i])
@@ -122,7 +125,8 @@ def _run_step(cuda, seqs, dtype_str, hq, hkv, vrot, monkeypatch, seed, bs=16, pr
                 want = O.raw_decode_attention(qs[i].float().numpy(), cache_np, btr, sl, 1 / math.sqrt(D))
             else:
                 want = O.v1_decode_attention(qs[i].float().numpy(), cache_np, btr, sl, cent, kb, vb,
-                                             1 / math.sqrt(D), v_rotate=vrot or lloyd, v_lloyd_max=lloyd)
+                                             1 / math.sqrt(D), v_rotate=vrot or lloyd, v_lloyd_max=lloyd,
+                                             rotation=rot)
         kind = "prefill" if c == 0 else ("decode" if q == 1 else "continuation")
         _check(got[a:a + q], want, f"{dtype_str} vrot={vrot} seq{i} {kind} cached={c} q={q}")
 
@@ -243,3 +247,13 @@ def test_v_lloyd_max_step(cuda, monkeypatch, dtype_str):
     prefill and continuation in one mixed step."""
     _run_step(cuda, [(40, 1), (700, 1), (0, 33), (129, 9)], dtype_str, 32, 8, False, monkeypatch,
               seed=7, lloyd=True)
+
+
+@pytest.mark.parametrize("vrot", [False, True])
+def test_planar_kind_step(cuda, monkeypatch, vrot):
+    """TURBOQUANT_KIND=planar through the Impl (reference v1_backend.py:516-523,
+    rotation/planar.py): the store, decode and merge kernels rotate by the
+    planar matrix.  Decode, fresh prefill and continuation in one mixed step,
+    against the oracle with the same matrix."""
+    _run_step(cuda, [(40, 1), (700, 1), (0, 33), (129, 9)], "turboquant_k4v2_nc", 32, 8, vrot, monkeypatch,
+              seed=11, kind="planar")

@@ -174,3 +174,16 @@ def test_additional_config_maps_defer_and_lloyd_keys():
     from fused_turboquant.vllm_plugin import plugin
     assert plugin.TQ_CONFIG_ENV_MAP["defer_prefill"] == "TURBOQUANT_DEFER_PREFILL"
     assert plugin.TQ_CONFIG_ENV_MAP["v_lloyd_max"] == "TURBOQUANT_V_LLOYD_MAX"
+
+
+def test_kind_env_planar_and_unsupported(monkeypatch):
+    """TURBOQUANT_KIND: rht (default) and planar build; rotor / iso raise at
+    Impl construction (reference v1_backend.py:516-523 registry lookup)."""
+    from fused_turboquant import vllm_plugin as vp
+    monkeypatch.setenv("TURBOQUANT_KIND", "planar")
+    impl = vp.FusedTurboQuantV1Impl(32, 128, 128 ** -0.5, 8, kv_cache_dtype="turboquant_k4v2_nc")
+    assert impl.kind == "planar"
+    for k in ("rotor", "iso"):
+        monkeypatch.setenv("TURBOQUANT_KIND", k)
+        with pytest.raises(NotImplementedError):
+            vp.FusedTurboQuantV1Impl(32, 128, 128 ** -0.5, 8, kv_cache_dtype="turboquant_k4v2_nc")
