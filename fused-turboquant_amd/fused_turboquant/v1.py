@@ -160,6 +160,47 @@ def planar_rotation(head_dim: int, seed: int = 42, device="cpu") -> torch.Tensor
     return m.to(device)
 
 
+def rotor_rotation(head_dim: int, seed: int = 42, device="cpu") -> torch.Tensor:
+    """Rotation matrix M (x M, float32 [d, d]) of the rotor strategy (reference
+    ``vllm_plugin/rotation/rotor.py:60-166``): coordinates in groups of 3, each
+    turned by the 3x3 matrix of a Cl(3,0) rotor (s, p12, p13, p23) =
+    (cos(a/2), sin(a/2) b) with b a unit vector from ``randn`` and a = 2 pi
+    U[0, 1), both drawn for ceil(d/3) groups from a CPU generator seeded
+    ``seed``; d mod 3 = 2 trailing coordinates take a Givens turn by a third
+    draw, 1 is left alone.  Blocks are built in column form and M is their
+    transpose."""
+    D = head_dim
+    n, r = D // 3, D % 3
+    npad = (D + 2) // 3
+    gen = torch.Generator(device="cpu").manual_seed(seed)
+    m = torch.zeros(D, D, dtype=torch.float32)
+    if n > 0:
+        b = torch.randn(npad, 3, generator=gen, dtype=torch.float32)[:n]
+        b = b / b.norm(dim=-1, keepdim=True).clamp(min=1e-8)
+        a = (torch.rand(npad, generator=gen, dtype=torch.float32) * (2.0 * math.pi))[:n]
+        h = a / 2
+        sc = torch.cos(h)
+        sh = torch.sin(h)
+        p12, p13, p23 = sh * b[:, 0], sh * b[:, 1], sh * b[:, 2]
+        s2, q12, q13, q23 = sc * sc, p12 * p12, p13 * p13, p23 * p23
+        rows = [
+            [s2 - q12 - q13 + q23, 2 * sc * p12 - 2 * p13 * p23, 2 * sc * p13 + 2 * p12 * p23],
+            [-2 * sc * p12 - 2 * p13 * p23, s2 - q12 + q13 - q23, 2 * sc * p23 - 2 * p12 * p13],
+            [-2 * sc * p13 + 2 * p12 * p23, -2 * sc * p23 - 2 * p12 * p13, s2 + q12 - q13 - q23],
+        ]
+        for i in range(3):
+            for j in range(3):
+                m[3 * torch.arange(n) + i, 3 * torch.arange(n) + j] = rows[i][j]
+    t = 3 * n
+    if r == 1:
+        m[t, t] = 1.0
+    elif r == 2:
+        th = torch.rand(1, generator=gen, dtype=torch.float32).item() * (2.0 * math.pi)
+        c, sn = math.cos(th), math.sin(th)
+        m[t, t], m[t, t + 1], m[t + 1, t], m[t + 1, t + 1] = c, -sn, sn, c
+    return m.T.contiguous().to(device)
+
+
 def _rotation_arg(rotation: torch.Tensor, d: int, dev) -> torch.Tensor:
     if rotation.shape != (d, d):
         raise ValueError("rotation must be a [head_dim, head_dim] matrix")
@@ -314,8 +355,10 @@ class TurboQuantV1Layer:
             self.rotation = None
         elif kind == "planar":
             self.rotation = planar_rotation(head_dim, device=device)
+        elif kind == "rotor":
+            self.rotation = rotor_rotation(head_dim, device=device)
         else:
-            raise NotImplementedError(f"rotation kind {kind!r}: rht, planar or an explicit matrix")
+            raise NotImplementedError(f"rotation kind {kind!r}: rht, planar, rotor or an explicit matrix")
 
     def kv_cache_shape(self, num_blocks: int, block_size: int, num_kv_heads: int) -> tuple:
         return get_kv_cache_shape(num_blocks, block_size, num_kv_heads, self.head_dim,

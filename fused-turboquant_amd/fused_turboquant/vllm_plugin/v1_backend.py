@@ -214,12 +214,12 @@ class FusedTurboQuantV1Impl(_ImplBase):
         self._prefix_capacity = _defer_capacity() if self.defer_prefill else 0
         # Lloyd-Max V codes (4-bit V; other widths stay uniform but rotated, as in the reference)
         self.v_lloyd_max = not self._is_raw and env_flag("TURBOQUANT_V_LLOYD_MAX")
-        # rotation strategy (reference v1_backend.py:516-523): rht, or planar as a
+        # rotation strategy (reference v1_backend.py:516-523): rht, or planar / rotor as a
         # rotation matrix applied inside the store / decode / merge kernels
         self.kind = os.environ.get("TURBOQUANT_KIND", "rht").strip().lower() or "rht"
-        if not self._is_raw and self.kind not in ("rht", "planar"):
-            raise NotImplementedError(f"TURBOQUANT_KIND={self.kind!r}: rht and planar are supported "
-                                      "(rotor and iso are not)")
+        if not self._is_raw and self.kind not in ("rht", "planar", "rotor"):
+            raise NotImplementedError(f"TURBOQUANT_KIND={self.kind!r}: rht, planar and rotor are supported "
+                                      "(iso is not)")
 
     # -- per-layer state ---------------------------------------------------
     def _state(self, layer, device) -> V1.TurboQuantV1Layer:

@@ -317,3 +317,32 @@ def test_planar_rotation_matrix():
     y0, n0 = O.v1_k_rotate(k)
     y1, n1 = O.v1_k_rotate(k, H)
     assert np.abs(y0 - y1).max() < 1e-6 and np.array_equal(n0, n1)
+
+
+
+def test_rotor_rotation_matrix():
+    """The rotor strategy's M (x M) at d = 128: orthogonal with determinant 1,
+    3x3 blocks on the diagonal for coordinates 0..125 and a 2x2 Givens block
+    on 126..127; each 3x3 block is the rotor sandwich's matrix: its trace is
+    1 + 2 cos(a) and it leaves fixed the axis dual to the rotor's bivector,
+    (b3, -b2, b1) (the closed form of the reference's rotor.py:96-124 entries)."""
+    import torch
+    from fused_turboquant import v1
+    d = 128
+    M = v1.rotor_rotation(d).double().numpy()
+    assert np.abs(M @ M.T - np.eye(d)).max() < 1e-5
+    assert abs(np.linalg.det(M) - 1.0) < 1e-4
+    mask = np.zeros((d, d), bool)
+    for g in range(42):
+        mask[3 * g:3 * g + 3, 3 * g:3 * g + 3] = True
+    mask[126:128, 126:128] = True
+    assert not M[~mask].any()
+    gen = torch.Generator().manual_seed(42)
+    b = torch.randn(43, 3, generator=gen, dtype=torch.float32)[:42].double().numpy()
+    b /= np.linalg.norm(b, axis=1, keepdims=True)
+    a = torch.rand(43, generator=gen, dtype=torch.float32).double().numpy()[:42] * 2 * np.pi
+    for g in (0, 7, 41):
+        blk = M[3 * g:3 * g + 3, 3 * g:3 * g + 3]
+        assert abs(np.trace(blk) - (1 + 2 * np.cos(a[g]))) < 1e-5
+        axis = np.array([b[g, 2], -b[g, 1], b[g, 0]])  # dual of p12 e12 + p13 e13 + p23 e23
+        assert np.allclose(axis @ blk, axis, atol=1e-5)

@@ -348,8 +348,9 @@ def test_decode_parity_v_lloyd_max(cuda, kb, hq, hkv, splits):
     _check_attn(got, want, f"v1 lloyd kb={kb} hq={hq} hkv={hkv} S={splits}")
 
 
+@pytest.mark.parametrize("kind", ["planar", "rotor"])
 @pytest.mark.parametrize("kb,vb", [(4, 2), (3, 3)])
-def test_store_parity_planar_matrix(cuda, kb, vb):
+def test_store_parity_planar_matrix(cuda, kb, vb, kind):
     """Matrix-strategy store (planar, x M in the kernel; reference
     triton_inkernel_store.py:459-541 behind rotation/matrix.py:50-70) against
     the oracle's x M in float64: K codes equal except where the rotated unit
@@ -360,7 +361,7 @@ def test_store_parity_planar_matrix(cuda, kb, vb):
     d, bs, hkv, nb = 128, 16, 4, 8
     n = nb * bs
     g = torch.Generator().manual_seed(41 + kb)
-    layer = v1.TurboQuantV1Layer(d, kb, vb, v_rotate=True, kind="planar", device=cuda)
+    layer = v1.TurboQuantV1Layer(d, kb, vb, v_rotate=True, kind=kind, device=cuda)
     M = layer.rotation.cpu().numpy()
     k, v = _kv(g, n, hkv, d, torch.bfloat16)
     slots = torch.randperm(nb * bs, generator=g)[:n]
@@ -378,7 +379,7 @@ def test_store_parity_planar_matrix(cuda, kb, vb):
     dk = kg[blk, off].astype(int) - kw[blk, off].astype(int)
     near = np.min(np.abs(y[..., None] - mids[None, None, None, :]), axis=-1) < 1e-5
     bad = (dk != 0) & ~((np.abs(dk) == 1) & near)
-    print(f"[v1 planar store kb={kb} vb={vb}] K code ties={(dk != 0).sum()} of {dk.size}")
+    print(f"[v1 {kind} store kb={kb} vb={vb}] K code ties={(dk != 0).sum()} of {dk.size}")
     assert not bad.any()
     kn_g, kn_w = kng[blk, off].astype(np.float64), knw[blk, off].astype(np.float64)
     assert np.abs(kn_g - kn_w).max() <= 1e-3 * np.abs(kn_w).max()
@@ -388,9 +389,10 @@ def test_store_parity_planar_matrix(cuda, kb, vb):
     assert (np.abs(vhg - vhw) <= 1.01 * step + 1e-3).all()
 
 
+@pytest.mark.parametrize("kind", ["planar", "rotor"])
 @pytest.mark.parametrize("kb,vb", [(4, 2), (3, 3), (2, 4)])
 @pytest.mark.parametrize("hq,hkv", [(16, 4), (8, 1)])
-def test_decode_parity_planar_matrix(cuda, kb, vb, hq, hkv):
+def test_decode_parity_planar_matrix(cuda, kb, vb, hq, hkv, kind):
     """Matrix-strategy decode: q M in the kernel prologue and o M^T in the merge
     (reference rotation/matrix.py:47-48, v1_backend.py:1086-1092) against the
     oracle's float64 attention over the same cache bytes (written by the
@@ -398,7 +400,7 @@ def test_decode_parity_planar_matrix(cuda, kb, vb, hq, hkv):
     from fused_turboquant import v1
     d, bs, nb = 128, 16, 48
     g = torch.Generator().manual_seed(300 + kb * 10 + vb + hq)
-    M = v1.planar_rotation(d).numpy()
+    M = (v1.planar_rotation(d) if kind == "planar" else v1.rotor_rotation(d)).numpy()
     slot = max(v1.slot_size(d, kb, vb), 128)
     cache = np.zeros((nb, bs, hkv, slot), np.uint8)
     k, v = _kv(g, nb * bs, hkv, d, torch.bfloat16, outliers=True)
@@ -421,4 +423,4 @@ def test_decode_parity_planar_matrix(cuda, kb, vb, hq, hkv):
                                      1 / math.sqrt(d), kv_start=ks.numpy(), v_rotate=True, rotation=M)
         got = out.float().cpu().numpy()
         assert not got[0].any()
-        _check_attn(got, want, f"v1 planar kb={kb} vb={vb} hq={hq} hkv={hkv} S={splits}")
+        _check_attn(got, want, f"v1 {kind} kb={kb} vb={vb} hq={hq} hkv={hkv} S={splits}")

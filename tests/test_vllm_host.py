@@ -177,13 +177,15 @@ def test_additional_config_maps_defer_and_lloyd_keys():
 
 
 def test_kind_env_planar_and_unsupported(monkeypatch):
-    """TURBOQUANT_KIND: rht (default) and planar build; rotor / iso raise at
+    """TURBOQUANT_KIND: rht (default), planar and rotor build; iso raises at
     Impl construction (reference v1_backend.py:516-523 registry lookup)."""
     from fused_turboquant import vllm_plugin as vp
     monkeypatch.setenv("TURBOQUANT_KIND", "planar")
     impl = vp.FusedTurboQuantV1Impl(32, 128, 128 ** -0.5, 8, kv_cache_dtype="turboquant_k4v2_nc")
     assert impl.kind == "planar"
-    for k in ("rotor", "iso"):
+    monkeypatch.setenv("TURBOQUANT_KIND", "rotor")
+    assert vp.FusedTurboQuantV1Impl(32, 128, 128 ** -0.5, 8, kv_cache_dtype="turboquant_k4v2_nc").kind == "rotor"
+    for k in ("iso", "bogus"):
         monkeypatch.setenv("TURBOQUANT_KIND", k)
         with pytest.raises(NotImplementedError):
             vp.FusedTurboQuantV1Impl(32, 128, 128 ** -0.5, 8, kv_cache_dtype="turboquant_k4v2_nc")
