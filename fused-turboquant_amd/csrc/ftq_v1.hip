@@ -45,6 +45,7 @@
 #include "ftq_internal.h"
 
 #include <cmath>
+#include <mutex>
 
 namespace ftq {
 
@@ -1389,4 +1390,74 @@ extern "C" int ftq_v1_decode_attention(
                                      num_q_heads, num_kv_heads, d, centroids, key_bits, value_bits, scale,
                                      v_rotate, num_splits, workspace, workspace_bytes, out, out_dtype, nullptr,
                                      stream);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free decode attention.  The split-K partials (per (row, split):
+// D floats of output and one log2-sum-exp) go to `scratch`, a file-scope
+// device array, instead of a caller's workspace.  Every stage-1 workgroup
+// writes all of its partials (zeros and -inf for an empty split) before the
+// merge reads them, so nothing in the array has to start at zero and the
+// contents a previous call left behind are never read.
+// All calls on one GPU share that GPU's copy of the array: calls that overlap
+// on one GPU (two host threads, or two streams without an ordering between
+// them) race on it.
+// ---------------------------------------------------------------------------
+namespace {
+constexpr int64_t kV1ScratchBytes = (int64_t)16 << 20;  // 16 MiB per device
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) float scratch[kV1ScratchBytes / 4];
+
+std::mutex g_scratch_mu;
+void* g_scratch_dev[kMaxDevices] = {};  // device address of `scratch`, per device
+
+// Device address of this device's `scratch`, looked up once per device (the
+// array's host-side name is not a device address).
+int current_scratch(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return ftq::hip_status(e);
+  FTQ_REQUIRE(dev >= 0 && dev < kMaxDevices, "device ordinal beyond the scratch table (64 devices)");
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (g_scratch_dev[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return ftq::hip_status(e);
+    FTQ_REQUIRE(p != nullptr, "hipGetSymbolAddress returned no address for the scratch array");
+    g_scratch_dev[dev] = p;
+  }
+  *out = g_scratch_dev[dev];
+  return FTQ_OK;
+}
+}  // namespace
+
+extern "C" int64_t ftq_v1_scratch_bytes(void) { return kV1ScratchBytes; }
+
+extern "C" int ftq_v1_decode_attention_noalloc(
+    const void* query, int q_dtype, const uint8_t* kv_cache, int64_t num_blocks, int block_size,
+    int64_t stride_block, int64_t stride_pos, int64_t stride_head, const int32_t* block_table,
+    int max_blocks_per_seq, const int32_t* seq_lens, const int32_t* kv_start, int batch,
+    int num_q_heads, int num_kv_heads, int d, const float* centroids, int key_bits,
+    int value_bits, float scale, int v_rotate, int num_splits, void* out, int out_dtype,
+    void* stream) {
+  const int64_t need = ftq_v1_workspace_bytes(batch, num_q_heads, d, num_splits);
+  FTQ_REQUIRE(need >= 0, "bad batch / head / split counts");
+  FTQ_REQUIRE(need <= kV1ScratchBytes,
+              "batch * num_q_heads * num_splits * (head_dim + 1) * 4 exceeds the 16 MiB scratch of "
+              "ftq_v1_decode_attention_noalloc: lower num_splits or the batch");
+  if (batch == 0) return FTQ_OK;
+  if (stream != nullptr) {  // the scratch address is per device: the stream must be the current device's
+    int cur = -1, sdev = -1;
+    hipError_t e = hipGetDevice(&cur);
+    if (e == hipSuccess) e = hipStreamGetDevice((hipStream_t)stream, &sdev);
+    if (e != hipSuccess) return hip_status(e);
+    FTQ_REQUIRE(cur == sdev, "stream belongs to another device than the current one");
+  }
+  void* ws = nullptr;
+  const int rc = current_scratch(&ws);
+  if (rc != FTQ_OK) return rc;
+  return ftq_v1_decode_attention(query, q_dtype, kv_cache, num_blocks, block_size, stride_block, stride_pos,
+                                 stride_head, block_table, max_blocks_per_seq, seq_lens, kv_start, batch,
+                                 num_q_heads, num_kv_heads, d, centroids, key_bits, value_bits, scale,
+                                 v_rotate, num_splits, ws, kV1ScratchBytes, out, out_dtype, stream);
 }

@@ -261,6 +261,32 @@ int ftq_v1_decode_attention_rot(const void* query, int q_dtype, const uint8_t* k
                                 int64_t workspace_bytes, void* out, int out_dtype, float* lse_out,
                                 const float* rotation, void* stream);
 
+/* Bytes of the device scratch array ftq_v1_decode_attention_noalloc uses in
+ * place of a workspace (16 MiB per device). */
+int64_t ftq_v1_scratch_bytes(void);
+/*
+ * ftq_v1_decode_attention without the workspace argument: allocates nothing
+ * and takes no workspace.  The split-K partials go to a file-scope device
+ * array of ftq_v1_scratch_bytes() bytes, which each GPU the library runs on
+ * holds until the process ends; its device address is looked up once per
+ * device on the first call there.  Rejects (FTQ_ERR_ARG) a shape whose
+ * ftq_v1_workspace_bytes exceeds that size, and a stream of another device
+ * than the current one.  All calls on one GPU share its array: calls that
+ * overlap on one GPU race.  Results equal ftq_v1_decode_attention's.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).
+ */
+int ftq_v1_decode_attention_noalloc(const void* query, int q_dtype, const uint8_t* kv_cache,
+                                    int64_t num_blocks, int block_size, int64_t stride_block,
+                                    int64_t stride_pos, int64_t stride_head,
+                                    const int32_t* block_table, int max_blocks_per_seq,
+                                    const int32_t* seq_lens, const int32_t* kv_start, int batch,
+                                    int num_q_heads, int num_kv_heads, int d,
+                                    const float* centroids, int key_bits, int value_bits,
+                                    float scale, int v_rotate, int num_splits, void* out,
+                                    int out_dtype, void* stream);
+
 /* ---------------------------------------------------------------------------
  * Raw fp16 slots of the boundary-protection layers (TURBOQUANT_BOUNDARY_PROTECT
  * = fp16): the same [num_blocks][block_size][Hkv][slot] byte cache, per
