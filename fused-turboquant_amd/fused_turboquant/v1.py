@@ -201,6 +201,81 @@ def rotor_rotation(head_dim: int, seed: int = 42, device="cpu") -> torch.Tensor:
     return m.T.contiguous().to(device)
 
 
+def _unit_quaternions(n: int, seed: int) -> torch.Tensor:
+    """n unit quaternions (w, x, y, z): ``randn(n, 4)`` from a CPU generator
+    seeded ``seed``, each divided by max(norm, 1e-8)."""
+    gen = torch.Generator(device="cpu").manual_seed(seed)
+    q = torch.randn(n, 4, generator=gen, dtype=torch.float32)
+    return q / q.norm(dim=-1, keepdim=True).clamp(min=1e-8)
+
+
+def _quat_mat(q: torch.Tensor, right: bool) -> torch.Tensor:
+    """[n, 4, 4] column-form matrices of v -> q v (right=False) or v -> v q
+    (right=True) under the Hamilton product, components (w, x, y, z)."""
+    w, x, y, z = q.unbind(-1)
+    if right:
+        rows = ((w, -x, -y, -z), (x, w, z, -y), (y, -z, w, x), (z, y, -x, w))
+    else:
+        rows = ((w, -x, -y, -z), (x, w, -z, y), (y, z, w, -x), (z, -y, x, w))
+    return torch.stack([torch.stack(r, dim=-1) for r in rows], dim=-2)
+
+
+def iso_rotation(head_dim: int, full: bool = False, seed: int = 42, device="cpu") -> torch.Tensor:
+    """Rotation matrix M (x M, float32 [d, d]) of the IsoQuant strategies
+    (reference ``vllm_plugin/rotation/iso.py:65-158``): coordinates in groups
+    of 4, each group a quaternion v turned to q_L v (``iso_fast``) or
+    q_L v conj(q_R) (``iso_full``), q_L drawn with ``seed`` and q_R with
+    ``seed + 10000``; d is padded to a multiple of 4 and M cropped back.
+    Blocks are built in column form and M is their transpose."""
+    D = head_dim
+    dp = (D + 3) // 4 * 4
+    n = dp // 4
+    blk = _quat_mat(_unit_quaternions(n, seed), right=False)
+    if full:
+        qr = _unit_quaternions(n, seed + 10000) * torch.tensor([1.0, -1.0, -1.0, -1.0])
+        r = _quat_mat(qr, right=True)
+        # the 4x4 block product L R, summed k = 0..3 in order in fp32 (no fused
+        # multiply-add), so the result does not depend on the host's BLAS
+        acc = blk[:, :, 0, None] * r[:, None, 0, :]
+        for k in range(1, 4):
+            acc = acc + blk[:, :, k, None] * r[:, None, k, :]
+        blk = acc
+    m = torch.zeros(dp, dp, dtype=torch.float32)
+    g = torch.arange(n)
+    for i in range(4):
+        for j in range(4):
+            m[4 * g + i, 4 * g + j] = blk[:, i, j]
+    return m.T[:D, :D].contiguous().to(device)
+
+
+# block size of each block-diagonal strategy (reference rotation/*.py block_size)
+BLOCK_SIZES = {"planar": 2, "rotor": 3, "iso_fast": 4, "iso_full": 4}
+
+
+def rotation_matrix(kind: str, head_dim: int, device="cpu") -> torch.Tensor:
+    """M of a registered matrix strategy (``TURBOQUANT_KIND``) at head_dim."""
+    if kind == "planar":
+        return planar_rotation(head_dim, device=device)
+    if kind == "rotor":
+        return rotor_rotation(head_dim, device=device)
+    if kind in ("iso_fast", "iso_full"):
+        return iso_rotation(head_dim, full=(kind == "iso_full"), device=device)
+    raise ValueError(f"no rotation matrix for kind {kind!r}")
+
+
+def block_coeffs(m: torch.Tensor, block: int) -> torch.Tensor:
+    """[B, D] coefficients of a block-diagonal M with B x B blocks:
+    coeffs[k][d] = M[(d // B) B + k][d], 0 where that row is past D, so
+    (x M)[d] = sum_k x[(d // B) B + k] coeffs[k][d] (reference
+    ``rotation/matrix.py:104-124``)."""
+    D = m.shape[-1]
+    d = torch.arange(D, device=m.device)
+    src = (d // block * block)[None, :] + torch.arange(block, device=m.device)[:, None]
+    ok = src < D
+    c = m[torch.where(ok, src, torch.zeros_like(src)), d[None, :].expand(block, D)]
+    return (c * ok.to(m.dtype)).contiguous()
+
+
 def _rotation_arg(rotation: torch.Tensor, d: int, dev) -> torch.Tensor:
     if rotation.shape != (d, d):
         raise ValueError("rotation must be a [head_dim, head_dim] matrix")
@@ -353,12 +428,11 @@ class TurboQuantV1Layer:
             self.rotation = rotation.to(device=device, dtype=torch.float32).contiguous()
         elif kind == "rht":
             self.rotation = None
-        elif kind == "planar":
-            self.rotation = planar_rotation(head_dim, device=device)
-        elif kind == "rotor":
-            self.rotation = rotor_rotation(head_dim, device=device)
+        elif kind in BLOCK_SIZES:
+            self.rotation = rotation_matrix(kind, head_dim, device=device)
         else:
-            raise NotImplementedError(f"rotation kind {kind!r}: rht, planar, rotor or an explicit matrix")
+            raise ValueError(f"rotation kind {kind!r}: rht, planar, rotor, iso_fast, iso_full "
+                             "or an explicit matrix")
 
     def kv_cache_shape(self, num_blocks: int, block_size: int, num_kv_heads: int) -> tuple:
         return get_kv_cache_shape(num_blocks, block_size, num_kv_heads, self.head_dim,

@@ -61,6 +61,9 @@ from .. import raw as RAW
 from .. import v1 as V1
 from .plugin import TQ_PRESETS, boundary_protect_enabled, boundary_protect_mode, env_flag, host_preset
 
+# TURBOQUANT_KIND values the reference registers (vllm_plugin/rotation/*.py register_rotation)
+ROTATION_KINDS = ("rht", "planar", "rotor", "iso_fast", "iso_full")
+
 try:  # vLLM's base classes when present (not installed in every environment)
     from vllm.attention.backends.abstract import AttentionBackend as _BackendBase  # type: ignore
     from vllm.attention.backends.abstract import AttentionImpl as _ImplBase  # type: ignore
@@ -214,12 +217,13 @@ class FusedTurboQuantV1Impl(_ImplBase):
         self._prefix_capacity = _defer_capacity() if self.defer_prefill else 0
         # Lloyd-Max V codes (4-bit V; other widths stay uniform but rotated, as in the reference)
         self.v_lloyd_max = not self._is_raw and env_flag("TURBOQUANT_V_LLOYD_MAX")
-        # rotation strategy (reference v1_backend.py:516-523): rht, or planar / rotor as a
-        # rotation matrix applied inside the store / decode / merge kernels
-        self.kind = os.environ.get("TURBOQUANT_KIND", "rht").strip().lower() or "rht"
-        if not self._is_raw and self.kind not in ("rht", "planar", "rotor"):
-            raise NotImplementedError(f"TURBOQUANT_KIND={self.kind!r}: rht, planar and rotor are supported "
-                                      "(iso is not)")
+        # rotation strategy (reference v1_backend.py:516-523): rht, or one of the block-diagonal
+        # strategies (planar, rotor, iso_fast, iso_full) applied inside the store / decode /
+        # merge kernels.  Names are matched as given, like the reference's registry lookup.
+        self.kind = os.environ.get("TURBOQUANT_KIND", "rht")
+        if not self._is_raw and self.kind not in ROTATION_KINDS:
+            raise ValueError(f"TURBOQUANT_KIND={self.kind!r} not registered. Pick one of "
+                             f"{', '.join(ROTATION_KINDS)}")
 
     # -- per-layer state ---------------------------------------------------
     def _state(self, layer, device) -> V1.TurboQuantV1Layer:

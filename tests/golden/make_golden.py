@@ -20,6 +20,15 @@ its outputs as data:
   coordinates so tie cases can be identified.
 * ``fwht.npz``       -- ``fwht`` of a few seeded float32 inputs
   (reference ``core/hadamard.py:23-48``).
+* ``rotations.npz``  -- the (D, D) matrices M (``x @ M``) the vLLM rotation
+  strategies build: ``planar`` (``vllm_plugin/rotation/planar.py:32-64``),
+  ``rotor`` (``rotation/rotor.py:60-166``), ``iso_fast`` and ``iso_full``
+  (``rotation/iso.py:65-158``), for D in {64, 128, 256} (rotor also 129 and
+  130, the tail cases D mod 3 = 0 and 1), and each strategy's ``[B, D]``
+  block coefficients (``rotation/matrix.py:104-124``).
+
+``python tests/golden/make_golden.py [ref_src] rotations`` writes only
+``rotations.npz``.
 
 The fixture files are inputs and expected outputs only.
 """
@@ -100,5 +109,28 @@ def main(ref_src: str) -> None:
     print("wrote fixtures to", OUT)
 
 
+def rotations(ref_src: str) -> None:
+    """Record the reference's seeded rotation matrices (pure torch on the CPU;
+    the strategies' modules import no vLLM)."""
+    sys.path.insert(0, ref_src)
+    from fused_turboquant.vllm_plugin.rotation import get_rotation
+
+    rot = {}
+    for kind, dims in (("planar", (64, 128, 256)), ("rotor", (64, 128, 129, 130, 256)),
+                       ("iso_fast", (64, 128, 256)), ("iso_full", (64, 128, 256))):
+        strat = get_rotation(kind)
+        for d in dims:
+            m = strat.build_matrix(d, "cpu").to(torch.float32)
+            rot[f"{kind}_{d}"] = m.numpy()
+            rot[f"{kind}_{d}_coeffs"] = strat.compute_coeffs(m, strat.block_size).numpy()
+    np.savez_compressed(os.path.join(OUT, "rotations.npz"), **rot)
+    print("wrote rotations.npz to", OUT)
+
+
 if __name__ == "__main__":
-    main(sys.argv[1] if len(sys.argv) > 1 else "/root/reference/src")
+    src = sys.argv[1] if len(sys.argv) > 1 else "/root/reference/src"
+    if len(sys.argv) > 2 and sys.argv[2] == "rotations":
+        rotations(src)
+    else:
+        main(src)
+        rotations(src)

@@ -9,6 +9,7 @@ import math
 
 import numpy as np
 import pytest
+import torch
 
 from oracle import tq_oracle as O
 
@@ -346,3 +347,77 @@ def test_rotor_rotation_matrix():
         assert abs(np.trace(blk) - (1 + 2 * np.cos(a[g]))) < 1e-5
         axis = np.array([b[g, 2], -b[g, 1], b[g, 0]])  # dual of p12 e12 + p13 e13 + p23 e23
         assert np.allclose(axis @ blk, axis, atol=1e-5)
+
+
+# ---- pins of the oracle's dtype rounding, the uniform V rounding and the
+# ---- seeded rotation matrices
+
+
+def _round_cases():
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal(4096).astype(np.float32) * np.float32(3)
+    bits = x.view(np.uint32).copy()
+    # exact bf16 ties (low half 0x8000) with even and odd kept halves, and one ulp either side
+    tie = (bits[:512] & np.uint32(0xFFFF0000)) | np.uint32(0x8000)
+    extra = np.concatenate([tie, tie + np.uint32(1), tie - np.uint32(1),
+                            tie ^ np.uint32(0x10000)]).view(np.float32)
+    special = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 3.4028235e38, -3.4028235e38,
+                        1e-40, -1e-40, 65504.0, 65520.0, 65519.996, 6e-8, 2.9e-8, 1e-45],
+                       np.float32)
+    # f16 ties: values exactly halfway between two f16 numbers
+    h = rng.standard_normal(512).astype(np.float16)
+    nxt = np.nextafter(h, np.float16(np.inf))
+    htie = ((h.astype(np.float64) + nxt.astype(np.float64)) / 2).astype(np.float32)
+    return np.concatenate([x, extra, special, htie[np.isfinite(htie)]])
+
+
+@pytest.mark.parametrize("dt,tdt", [("bf16", torch.bfloat16), ("f16", torch.float16)])
+def test_round_dtype_matches_torch_conversion(dt, tdt):
+    """v1_round_dtype (the value dtype round trip of the V pre-rotation) equals
+    torch's own float32 -> bf16 / f16 -> float32 conversion bit for bit, on
+    exact ties, ±inf, NaN, overflow, subnormals and signed zero."""
+    x = _round_cases()
+    got = O.v1_round_dtype(x, dt)
+    want = torch.from_numpy(x).to(tdt).float().numpy()
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+@pytest.mark.parametrize("vb", [1, 2, 3, 4])
+@pytest.mark.parametrize("step", [1.0, 2.0, 0.25])
+def test_quantize_v_rounds_half_up_at_exact_halves(vb, step):
+    """Uniform V codes are trunc((v - min) / scale + 0.5)
+    (triton_inkernel_store.py:210, 235): a value exactly halfway between codes
+    k and k + 1 takes k + 1 for every k (round half to even would take the even
+    one).  min = 0 and max = top * step make the scale exactly `step`."""
+    top = (1 << vb) - 1
+    halves = (np.arange(top) + 0.5) * step
+    v = np.zeros((1, 64), np.float32)
+    v[0, 0] = 0.0
+    v[0, 1] = top * step
+    v[0, 2:2 + top] = halves
+    q, sc, mn, _ = O.v1_quantize_v(v, vb)
+    assert sc[0] == np.float32(step) and mn[0] == 0.0
+    assert q[0, 0] == 0 and q[0, 1] == top
+    assert list(q[0, 2:2 + top]) == list(range(1, top + 1))
+
+
+@pytest.mark.parametrize("kind", ["planar", "rotor", "iso_fast", "iso_full"])
+def test_rotation_matrices_equal_the_reference(kind):
+    """The seeded matrices of the block-diagonal strategies and their [B, D]
+    coefficients equal the reference's own (tests/golden/rotations.npz,
+    written from vllm_plugin/rotation/*.py build_matrix / compute_coeffs)."""
+    import os
+    from conftest import GOLDEN
+    from fused_turboquant import v1
+    z = np.load(os.path.join(GOLDEN, "rotations.npz"))
+    keys = [k for k in z.files if k.startswith(kind + "_") and not k.endswith("_coeffs")
+            and k[len(kind) + 1:].isdigit()]
+    assert keys
+    for k in keys:
+        d = int(k[len(kind) + 1:])
+        m = v1.rotation_matrix(kind, d)
+        assert np.array_equal(m.numpy(), z[k]), k
+        c = v1.block_coeffs(m, v1.BLOCK_SIZES[kind])
+        assert np.array_equal(c.numpy(), z[k + "_coeffs"]), k

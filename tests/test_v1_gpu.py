@@ -348,7 +348,7 @@ def test_decode_parity_v_lloyd_max(cuda, kb, hq, hkv, splits):
     _check_attn(got, want, f"v1 lloyd kb={kb} hq={hq} hkv={hkv} S={splits}")
 
 
-@pytest.mark.parametrize("kind", ["planar", "rotor"])
+@pytest.mark.parametrize("kind", ["planar", "rotor", "iso_fast", "iso_full"])
 @pytest.mark.parametrize("kb,vb", [(4, 2), (3, 3)])
 def test_store_parity_planar_matrix(cuda, kb, vb, kind):
     """Matrix-strategy store (planar, x M in the kernel; reference
@@ -389,7 +389,7 @@ def test_store_parity_planar_matrix(cuda, kb, vb, kind):
     assert (np.abs(vhg - vhw) <= 1.01 * step + 1e-3).all()
 
 
-@pytest.mark.parametrize("kind", ["planar", "rotor"])
+@pytest.mark.parametrize("kind", ["planar", "rotor", "iso_fast", "iso_full"])
 @pytest.mark.parametrize("kb,vb", [(4, 2), (3, 3), (2, 4)])
 @pytest.mark.parametrize("hq,hkv", [(16, 4), (8, 1)])
 def test_decode_parity_planar_matrix(cuda, kb, vb, hq, hkv, kind):
@@ -400,7 +400,7 @@ def test_decode_parity_planar_matrix(cuda, kb, vb, hq, hkv, kind):
     from fused_turboquant import v1
     d, bs, nb = 128, 16, 48
     g = torch.Generator().manual_seed(300 + kb * 10 + vb + hq)
-    M = (v1.planar_rotation(d) if kind == "planar" else v1.rotor_rotation(d)).numpy()
+    M = v1.rotation_matrix(kind, d).numpy()
     slot = max(v1.slot_size(d, kb, vb), 128)
     cache = np.zeros((nb, bs, hkv, slot), np.uint8)
     k, v = _kv(g, nb * bs, hkv, d, torch.bfloat16, outliers=True)

@@ -176,16 +176,16 @@ def test_additional_config_maps_defer_and_lloyd_keys():
     assert plugin.TQ_CONFIG_ENV_MAP["v_lloyd_max"] == "TURBOQUANT_V_LLOYD_MAX"
 
 
-def test_kind_env_planar_and_unsupported(monkeypatch):
-    """TURBOQUANT_KIND: rht (default), planar and rotor build; iso raises at
-    Impl construction (reference v1_backend.py:516-523 registry lookup)."""
+def test_kind_env_registered_and_unknown(monkeypatch):
+    """TURBOQUANT_KIND: every name the reference registers builds (rht,
+    planar, rotor, iso_fast, iso_full); others raise ValueError as the
+    reference's registry lookup does (v1_backend.py:516-523), matched as given
+    (no case folding)."""
     from fused_turboquant import vllm_plugin as vp
-    monkeypatch.setenv("TURBOQUANT_KIND", "planar")
-    impl = vp.FusedTurboQuantV1Impl(32, 128, 128 ** -0.5, 8, kv_cache_dtype="turboquant_k4v2_nc")
-    assert impl.kind == "planar"
-    monkeypatch.setenv("TURBOQUANT_KIND", "rotor")
-    assert vp.FusedTurboQuantV1Impl(32, 128, 128 ** -0.5, 8, kv_cache_dtype="turboquant_k4v2_nc").kind == "rotor"
-    for k in ("iso", "bogus"):
+    for k in ("planar", "rotor", "iso_fast", "iso_full", "rht"):
         monkeypatch.setenv("TURBOQUANT_KIND", k)
-        with pytest.raises(NotImplementedError):
+        assert vp.FusedTurboQuantV1Impl(32, 128, 128 ** -0.5, 8, kv_cache_dtype="turboquant_k4v2_nc").kind == k
+    for k in ("iso", "bogus", "Planar", "RHT"):
+        monkeypatch.setenv("TURBOQUANT_KIND", k)
+        with pytest.raises(ValueError, match="not registered"):
             vp.FusedTurboQuantV1Impl(32, 128, 128 ** -0.5, 8, kv_cache_dtype="turboquant_k4v2_nc")
