@@ -7,20 +7,35 @@ One step = the BASELINE headline workload on one GPU, inputs resident in HBM:
     library-format cache (B=32, Hq=32, Hkv=8, d=128, ctx 8192, page 16).
 ``value`` is the encode throughput in GB/s of bf16 input consumed.
 
-Also timed (not part of the step): the d=256 encode and the d=128 decode of
-config 2, config 4 (vLLM v1 slot format, K4V2, v_rotate, B=4, contexts
-U[65536, 131072]) and the boundary-layer raw fp16 decode attention at the
-config-3 shape (512-byte K|V slots, 1.07 GB).  Every kernel gets a roofline entry: algorithmic bytes per
-launch / launch time, from HIP events on the stream the library launches on
+Also timed (not part of the step), each with a roofline entry:
+  * the d=256 encode and the d=128 decode of config 2;
+  * config 3 through the fp32-operand VALU kernel (the reference's arithmetic)
+    beside the default f16-operand matrix-core kernel;
+  * config 4 (vLLM v1 slot format, K4V2, v_rotate, B=4, contexts
+    U[65536, 131072]);
+  * the boundary-layer raw fp16 decode attention at the config-3 shape;
+  * the stores: the v1 slot store (rht, and the block-diagonal rotations) at
+    the reference's published shapes (1024 tokens x 8 kv heads and 1 token x 8
+    kv heads, D = 128 / 256) and at a config-4 prefill chunk, and the paged
+    library-format store of a config-3 chunk.
+Kernel times come from HIP events on the stream the library launches on
 (torch's current stream), in steady state: 20 untimed launches, then the
-median of three windows of back-to-back launches.
+median of three windows of back-to-back launches.  roofline.achieved =
+algorithmic bytes per launch / launch time.
+
+The CPU baseline (rank 0, N=1) times the torch restatement of the reference's
+unfused path (oracle/torch_ref.py) on the host cores: config 1, config-2
+encode and decode at d = 128 and 256, and decode attention of one config-3
+sequence.
 
 Prints ONE JSON line.
 """
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
+import math
 import os
 import platform
 import sys
@@ -40,6 +55,9 @@ TRAFFIC_BYTES: dict = {
     "encode_d128_3bit": 80336620, "encode_d256_3bit": 160154623, "decode_d128_3bit_f32": 149011545,
     "paged_attn_config3": 219810032, "v1_attn_config4": 406670855, "raw_attn_boundary": 1081506403,
 }
+
+# config-1 outlier channels (x10), fixed here so the CPU baseline's input is reproducible
+CONFIG1_OUTLIER_CHANNELS = (3, 37, 70, 111)
 
 
 def log(msg):
@@ -66,20 +84,31 @@ def time_launches(fn, iters, torch, warm=20, windows=3):
     return sorted(per)[len(per) // 2]
 
 
-def lean_launch(fn, keep, *args):
+def lean_launch(fn, *args):
     """A C-ABI launch with its ctypes arguments converted once: host time per
     call stays well under a kernel's, so back-to-back launches leave no gaps.
-    The arguments hold raw device pointers, so the tensors behind them (`keep`)
-    stay referenced by the launcher.  Statuses are checked after the timed
-    region (check_lean)."""
-    import ctypes
-    conv = tuple(ctypes.c_void_p(a) if isinstance(a, int) and abs(a) > 2 ** 40 else a for a in args)
+    Tensor arguments are passed as their data pointers and held by the
+    launcher (``keep``) for as long as it lives, so no launch can read or
+    write memory that was handed to another allocation.  Statuses are checked
+    after the timed region (check_lean)."""
+    import torch
+    keep, conv = [], []
+    for a in args:
+        if isinstance(a, torch.Tensor):
+            keep.append(a)
+            conv.append(ctypes.c_void_p(a.data_ptr()))
+        elif isinstance(a, int) and abs(a) > 2 ** 40:  # a raw pointer (the stream)
+            conv.append(ctypes.c_void_p(a))
+        else:
+            conv.append(a)
+    conv = tuple(conv)
     status = []
 
     def call():
         status.append(fn(*conv))
     call.status = status
     call.keep = tuple(keep)
+    call.args = conv
     return call
 
 
@@ -91,27 +120,6 @@ def check_lean(*calls):
         c.status.clear()
 
 
-def cpu_baseline_encode(n_vec=65536, d=128, bits=3):
-    """Oracle (numpy restatement of the reference's unfused path) encode on the host."""
-    import numpy as np
-    import torch
-    from oracle import tq_oracle as O
-    from fused_turboquant.core.hadamard import generate_rht_signs
-    from fused_turboquant.core.lloyd_max import compute_lloyd_max_codebook
-    g = torch.Generator().manual_seed(0)
-    x = torch.randn(n_vec, d, generator=g).to(torch.bfloat16).float().numpy()
-    s = generate_rht_signs(d, 42).numpy()
-    bnd = compute_lloyd_max_codebook(d, bits)[0].astype(np.float32)
-    O.encode(x[:1024], s, bnd, bits)
-    ts = []
-    for _ in range(5):
-        t0 = time.perf_counter()
-        O.encode(x, s, bnd, bits)
-        ts.append(time.perf_counter() - t0)
-    t = sorted(ts)[len(ts) // 2]
-    return n_vec * d * 2 / t / 1e9, f"{n_vec} vectors x d={d} bf16, 3-bit encode, median of 5"
-
-
 def roof(name, alg_bytes, t_us):
     gbs = alg_bytes / (t_us * 1e-6) / 1e9
     tr = TRAFFIC_BYTES.get(name)
@@ -120,12 +128,349 @@ def roof(name, alg_bytes, t_us):
             "algorithmic_bytes": alg_bytes}
 
 
+# ---------------------------------------------------------------------------
+# workloads
+# ---------------------------------------------------------------------------
+
+
+def config2_tensors(d, seed, T=32768, H=8):
+    """Config 2: [T, H, d] bf16, channel c ~ N(0, 1) * s_c, s_c ~ lognormal(0, 0.5)."""
+    import torch
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    sc = torch.exp(0.5 * torch.randn(d, generator=torch.Generator().manual_seed(seed + 1)))
+    k = (torch.randn(T, H, d, generator=g) * sc).to(torch.bfloat16)
+    v = (torch.randn(T, H, d, generator=g) * sc).to(torch.bfloat16)
+    return k, v
+
+
+def encode_setup(dev, d, seed, bits=3):
+    import torch
+    from fused_turboquant import TurboQuantMSE, _lib
+    L = _lib.lib()
+    k_cpu, v_cpu = config2_tensors(d, seed)
+    k, v = k_cpu.to(dev), v_cpu.to(dev)
+    n = k.shape[0] * k.shape[1]
+    tq = TurboQuantMSE(d, bits=bits, seed=42, device=dev)
+    ck, cv = tq.encode(k), tq.encode(v)
+    signs, bnd = tq.rotation.signs, tq.quantizer.boundaries
+    cls = tq.quantizer.codebook_class  # symmetric at d = 128: the |t|-search kernel
+    sp = _lib.stream_ptr(dev)
+
+    def enc(x, c):
+        return lean_launch(L.ftq_encode_cb, x, 2, n, d, signs, bnd, bits, cls, c.indices, c.norms, sp)
+    return {"tq": tq, "ck": ck, "enc_k": enc(k, ck), "enc_v": enc(v, cv), "k_cpu": k_cpu, "n": n}
+
+
+def make_config3(dev, B=32, hq=32, hkv=8, d=128, ctx=8192, page=16, bits=3, seed=0, keep_first=False):
+    """Config 3: B sequences of ctx tokens in the library-format paged cache,
+    block table = a seeded random permutation of the pages.  keep_first: also
+    return sequence 0's K / V (CPU bf16, [ctx, Hkv, d]) for the CPU baseline."""
+    import torch
+    from fused_turboquant.paged import PagedTurboQuantCache
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    pages_per_seq = (ctx + page - 1) // page
+    nblocks = B * pages_per_seq
+    cache = PagedTurboQuantCache(nblocks, page, hkv, d, bits, bits, seed=42, device=dev)
+    perm = torch.randperm(nblocks, generator=g).to(torch.int32)
+    block_table = perm.view(B, pages_per_seq).to(dev)
+    pos = torch.arange(ctx, dtype=torch.int64)
+    slots = (block_table.cpu().long()[:, pos // page] * page + (pos % page)).reshape(-1).to(dev)
+    chunk = 1 << 16
+    n = B * ctx
+    first = None
+    for s in range(0, n, chunk):
+        e = min(n, s + chunk)
+        k = torch.randn(e - s, hkv, d, generator=g).to(torch.bfloat16)
+        v = torch.randn(e - s, hkv, d, generator=g).to(torch.bfloat16)
+        if keep_first and s == 0:
+            first = (k[:ctx].clone(), v[:ctx].clone())
+        cache.store(k.to(dev), v.to(dev), slots[s:e])
+    q = torch.randn(B, hq, d, generator=g).to(torch.bfloat16).to(dev)
+    seq_lens = torch.full((B,), ctx, dtype=torch.int32, device=dev)
+    if keep_first:
+        return cache, q, block_table, seq_lens, first
+    return cache, q, block_table, seq_lens
+
+
+def paged_setup(dev, cfg3, operands):
+    """One C-ABI launch per step of the config-3 decode; operands "f16" (the
+    default matrix-core kernel) or "fp32" (the VALU kernel)."""
+    import torch
+    from fused_turboquant import _lib
+    from fused_turboquant import paged as P
+    cache, q, bt, sl = cfg3[:4]
+    B, hq, d = q.shape
+    hkv = cache.num_kv_heads
+    ctx = int(sl[0])
+    splits = P.default_splits(B, hkv, ctx, hq, d) if operands == "f16" else P.default_splits(B, hkv, ctx)
+    out = torch.empty(B, hq, d, dtype=torch.bfloat16, device=dev)
+    ws = torch.empty(max(P.workspace_bytes(B, hq, d, splits), 16), dtype=torch.uint8, device=dev)
+    P.paged_decode_attention(q, cache.kv_cache, bt, sl, cache.k_quant, cache.v_quant,
+                             num_splits=splits, out=out, workspace=ws, operands=operands)
+    L = P._bind()
+    kv = cache.kv_cache
+    nb, _, nsub, _ = kv.shape
+    kq, vq = cache.k_quant, cache.v_quant
+    klev = kq.quantizer.levels
+    kp, vp = P._levels_pair(kq, vq)
+    vlev = klev if kp == vp else vq.quantizer.levels  # equal codebooks: one shared table
+    fn = L.ftq_paged_decode_attention if operands == "f16" else L.ftq_paged_decode_attention_valu
+    run = lean_launch(fn, q, _lib.dtype_code(q.dtype), kv, bt, sl, B, hq, hkv, d, nsub * 16, bt.shape[1], nb,
+                      kq.rotation.signs, vq.rotation.signs, klev, vlev, kq.bits, vq.bits,
+                      1.0 / math.sqrt(d), splits, ws, ws.numel(), out, _lib.dtype_code(out.dtype),
+                      _lib.stream_ptr(dev))
+    kv_bytes = B * ctx * hkv * (P.subblock_bytes(d, 3, 3) // 16)
+    total = kv_bytes + q.numel() * 2 + out.numel() * 2 + bt.numel() * 4 + sl.numel() * 4
+    return {"run": run, "kv_bytes": kv_bytes, "total_bytes": total, "splits": splits}
+
+
+def make_config4(dev, seed=4):
+    """Config 4: K4V2, v_rotate, B=4, 32 q / 8 kv heads, d=128, page 16;
+    ctx_i ~ U[65536, 131072]; K/V N(0,1) bf16 with 2% of tokens x8; block
+    table a seeded permutation of the physical pages."""
+    import torch
+    from fused_turboquant import v1 as V1
+    d, bs, hkv, hq, kb, vb, B = 128, 16, 8, 32, 4, 2, 4
+    g = torch.Generator().manual_seed(seed)
+    lens = torch.randint(65536, 131073, (B,), generator=g).tolist()
+    layer = V1.TurboQuantV1Layer(d, kb, vb, v_rotate=True, device=dev)
+    pages = [(n + bs - 1) // bs for n in lens]
+    nb = sum(pages)
+    cache = torch.zeros(layer.kv_cache_shape(nb, bs, hkv), dtype=torch.uint8, device=dev)
+    perm = torch.randperm(nb, generator=g).to(torch.int32)
+    bt = torch.zeros(B, max(pages), dtype=torch.int32)
+    used = 0
+    gd = torch.Generator(device=dev).manual_seed(seed + 1)
+    for b, n in enumerate(lens):
+        bt[b, :pages[b]] = perm[used:used + pages[b]]
+        used += pages[b]
+        btd = bt[b].to(dev).long()
+        for s0 in range(0, n, 32768):
+            m = min(32768, n - s0)
+            k = torch.randn(m, hkv, d, generator=gd, device=dev)
+            v = torch.randn(m, hkv, d, generator=gd, device=dev)
+            sel = torch.rand(m, generator=gd, device=dev) < 0.02
+            k[sel] *= 8
+            v[sel] *= 8
+            pos = torch.arange(s0, s0 + m, device=dev)
+            layer.store(k.to(torch.bfloat16), v.to(torch.bfloat16), cache, btd[pos // bs] * bs + pos % bs)
+    q = torch.randn(B, hq, d, generator=g).to(torch.bfloat16).to(dev)
+    sl = torch.tensor(lens, dtype=torch.int32, device=dev)
+    return layer, cache, q, bt.to(dev), sl, lens
+
+
+def v1_setup(dev):
+    import torch
+    from fused_turboquant import _lib
+    from fused_turboquant import v1 as V1
+    layer, cache, q, bt, sl, lens = make_config4(dev)
+    B, hq, d = q.shape
+    hkv = cache.shape[2]
+    splits = V1.default_splits(B, hkv, max(lens))
+    out = torch.empty(B, hq, d, dtype=torch.bfloat16, device=dev)
+    ws = torch.empty(V1.workspace_bytes(B, hq, d, splits), dtype=torch.uint8, device=dev)
+    V1.v1_decode_attention(q, cache, bt, sl, layer.centroids, layer.key_bits, layer.value_bits,
+                           v_rotate=True, num_splits=splits, out=out, workspace=ws)
+    L = V1._bind()
+    sb, sp, sh = cache.stride(0), cache.stride(1), cache.stride(2)
+    nb, bs = cache.shape[0], cache.shape[1]
+    run = lean_launch(L.ftq_v1_decode_attention, q, _lib.dtype_code(q.dtype), cache, nb, bs, sb, sp, sh,
+                      bt, bt.shape[1], sl, None, B, hq, hkv, d, layer.centroids, layer.key_bits,
+                      layer.value_bits, 1.0 / math.sqrt(d), 1, splits, ws, ws.numel(), out,
+                      _lib.dtype_code(out.dtype), _lib.stream_ptr(dev))
+    per_tok = V1.slot_bytes(d, layer.key_bits, layer.value_bits)  # 66 B of K + 36 B of V
+    kv_bytes = sum(lens) * hkv * per_tok
+    total = kv_bytes + q.numel() * 2 + out.numel() * 2 + sum((n + 15) // 16 for n in lens) * 4 + B * 4
+    return {"run": run, "kv_bytes": kv_bytes, "total_bytes": total, "splits": splits, "lens": lens}
+
+
+def raw_setup(dev, B=32, hq=32, hkv=8, d=128, ctx=8192, bs=16, seed=5):
+    """Raw fp16 boundary-layer cache at the config-3 shape (slot 512 B, pages a
+    seeded permutation), filled by raw_store."""
+    import torch
+    from fused_turboquant import _lib
+    from fused_turboquant import raw as R
+    g = torch.Generator().manual_seed(seed)
+    gd = torch.Generator(device=dev).manual_seed(seed)
+    pages = ctx // bs
+    nb = B * pages
+    cache = torch.zeros(nb, bs, hkv, 4 * d, dtype=torch.uint8, device=dev)
+    bt = torch.randperm(nb, generator=g).to(torch.int32).view(B, pages).to(dev)
+    pos = torch.arange(ctx, device=dev)
+    for b in range(B):
+        k = torch.randn(ctx, hkv, d, generator=gd, device=dev).to(torch.bfloat16)
+        v = torch.randn(ctx, hkv, d, generator=gd, device=dev).to(torch.bfloat16)
+        R.raw_store(k, v, cache, bt[b].long()[pos // bs] * bs + pos % bs)
+    q = torch.randn(B, hq, d, generator=g).to(torch.bfloat16).to(dev)
+    sl = torch.full((B,), ctx, dtype=torch.int32, device=dev)
+    splits = R.default_splits(B, hkv, ctx)
+    out = torch.empty(B, hq, d, dtype=torch.bfloat16, device=dev)
+    ws = torch.empty(R.workspace_bytes(B, hq, d, splits), dtype=torch.uint8, device=dev)
+    R.raw_decode_attention(q, cache, bt, sl, num_splits=splits, out=out, workspace=ws)
+    L = R._bind()
+    run = lean_launch(L.ftq_raw_decode_attention, q, _lib.dtype_code(q.dtype), cache, nb, bs,
+                      cache.stride(0), cache.stride(1), cache.stride(2), bt, bt.shape[1], sl, None, B, hq,
+                      hkv, d, 1.0 / math.sqrt(d), splits, ws, ws.numel(), out, _lib.dtype_code(out.dtype),
+                      _lib.stream_ptr(dev))
+    kv_bytes = B * ctx * hkv * R.raw_slot_bytes(d)
+    total = kv_bytes + q.numel() * 2 + out.numel() * 2 + bt.numel() * 4 + sl.numel() * 4
+    return {"run": run, "kv_bytes": kv_bytes, "total_bytes": total, "splits": splits,
+            "cache": cache, "q": q, "bt": bt, "sl": sl, "out": out}
+
+
+def v1_store_setup(dev, n_tokens, d, kb, vb, kind="rht", v_rotate=False, hkv=8, bs=16, seed=11):
+    """One v1 store launch: n_tokens x hkv K/V (bf16) into slots of a
+    seeded permutation of the pages.  Algorithmic bytes: K and V read (2 d
+    bytes each per (token, head)), the slot's used bytes written, the slot
+    mapping read."""
+    import torch
+    from fused_turboquant import _lib
+    from fused_turboquant import v1 as V1
+    g = torch.Generator().manual_seed(seed)
+    layer = V1.TurboQuantV1Layer(d, kb, vb, v_rotate=v_rotate, kind=kind, device=dev)
+    nb = (n_tokens + bs - 1) // bs + 1
+    cache = torch.zeros(layer.kv_cache_shape(nb, bs, hkv), dtype=torch.uint8, device=dev)
+    k = torch.randn(n_tokens, hkv, d, generator=g).to(torch.bfloat16).to(dev)
+    v = torch.randn(n_tokens, hkv, d, generator=g).to(torch.bfloat16).to(dev)
+    slots = torch.randperm(nb * bs, generator=g)[:n_tokens].to(dev)
+    layer.store(k, v, cache, slots)
+    L = V1._bind()
+    vflags = (1 if layer.v_rotate else 0) | (2 if layer.v_lloyd_max else 0)
+    args = [k, v, _lib.BF16, n_tokens, hkv, d, layer.midpoints, kb, vb, vflags, slots, cache, nb, bs,
+            cache.stride(0), cache.stride(1), cache.stride(2)]
+    if layer.rotation is None:
+        run = lean_launch(L.ftq_v1_store, *args, _lib.stream_ptr(dev))
+    else:
+        run = lean_launch(L.ftq_v1_store_rot, *args, layer.rotation, _lib.stream_ptr(dev))
+    total = n_tokens * hkv * (4 * d + V1.slot_bytes(d, kb, vb)) + n_tokens * 8
+    return {"run": run, "total_bytes": total}
+
+
+def paged_store_setup(dev, n_tokens=65536, hkv=8, d=128, bits=3, page=16, seed=12):
+    """One library-format paged store launch of a config-3 chunk (K3V3)."""
+    import torch
+    from fused_turboquant import _lib
+    from fused_turboquant import paged as P
+    g = torch.Generator().manual_seed(seed)
+    nb = n_tokens // page
+    cache = P.PagedTurboQuantCache(nb, page, hkv, d, bits, bits, device=dev)
+    k = torch.randn(n_tokens, hkv, d, generator=g).to(torch.bfloat16).to(dev)
+    v = torch.randn(n_tokens, hkv, d, generator=g).to(torch.bfloat16).to(dev)
+    slots = torch.randperm(nb, generator=g).repeat_interleave(page).to(dev) * page + \
+        torch.arange(n_tokens, device=dev) % page
+    cache.store(k, v, slots)
+    L = P._bind()
+    kq, vq = cache.k_quant, cache.v_quant
+    run = lean_launch(L.ftq_paged_store, k, v, _lib.BF16, n_tokens, hkv, d, kq.rotation.signs,
+                      vq.rotation.signs, kq.quantizer.boundaries, vq.quantizer.boundaries, bits, bits, slots,
+                      cache.kv_cache, page, nb, _lib.stream_ptr(dev))
+    total = n_tokens * hkv * (4 * d + P.subblock_bytes(d, bits, bits) // 16) + n_tokens * 8
+    return {"run": run, "total_bytes": total}
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline: the torch restatement of the reference's unfused path
+# ---------------------------------------------------------------------------
+
+
+def cpu_time(fn, runs=5):
+    """1 warmup, then the median of `runs` wall times (s)."""
+    fn()
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return sorted(ts)[len(ts) // 2]
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
+def cpu_baseline(k128, k256, cfg3_first, cfg3_q0):
+    """Config 1, config-2 encode / decode at d = 128 and 256 (one tensor each)
+    and one config-3 sequence's decode attention, timed on the host cores."""
+    import numpy as np
+    import torch
+    from fused_turboquant.core.hadamard import generate_rht_signs
+    from fused_turboquant.core.lloyd_max import compute_lloyd_max_codebook
+    from oracle import torch_ref as T
+    torch.set_num_threads(os.cpu_count() or 1)
+    res = {"threads": torch.get_num_threads(), "os_cpu_count": os.cpu_count(), "cpu_model": cpu_model()}
+
+    def cb(d, bits):
+        b, lv = compute_lloyd_max_codebook(d, bits)
+        return torch.as_tensor(np.asarray(b, np.float32)), torch.as_tensor(np.asarray(lv, np.float32))
+
+    # config 1: 4-bit, [1, 8, 4096, 128], N(0,1) with 4 channels x10, data and signs from seed 0
+    g = torch.Generator().manual_seed(0)
+    x1 = torch.randn(1, 8, 4096, 128, generator=g)
+    x1[..., list(CONFIG1_OUTLIER_CHANNELS)] *= 10
+    x1 = x1.to(torch.bfloat16)
+    s0 = generate_rht_signs(128, 0)
+    b4, l4 = cb(128, 4)
+    p1, n1 = T.encode(x1, s0, b4, 4)
+    y1 = T.decode(p1, n1, l4, s0, 4, 128)
+    xf = x1.float()
+    xn = torch.linalg.vector_norm(xf, dim=-1)
+    t1 = cpu_time(lambda: T.decode(*T.encode(x1, s0, b4, 4), l4, s0, 4, 128))
+    res["config1"] = {
+        "packed_bytes": p1.numel() + n1.numel() * 2,
+        "roundtrip_mse": float(((y1 - xf) ** 2).mean()),
+        "roundtrip_rel_mse": float(((y1 - xf) ** 2).sum() / (xf ** 2).sum()),
+        "norm_rel_err_max": float(((n1.float() - xn).abs() / xn).max()),
+        "norm_rel_err_mean": float(((n1.float() - xn).abs() / xn).mean()),
+        "decoded_norm_rel_err_mean": float(((torch.linalg.vector_norm(y1, dim=-1) - xn).abs() / xn).mean()),
+        "encode_decode_s": round(t1, 4),
+    }
+    # config 2: one tensor each, 3-bit, seed-42 signs
+    for d, x in ((128, k128), (256, k256)):
+        s42 = generate_rht_signs(d, 42)
+        bnd, lev = cb(d, 3)
+        t_enc = cpu_time(lambda: T.encode(x, s42, bnd, 3))
+        p, nrm = T.encode(x, s42, bnd, 3)
+        t_dec = cpu_time(lambda: T.decode(p, nrm, lev, s42, 3, d))
+        nbytes = x.numel() * 2
+        res[f"config2_d{d}"] = {"encode_s": round(t_enc, 4), "encode_gbs": round(nbytes / t_enc / 1e9, 4),
+                                "decode_s": round(t_dec, 4),
+                                "decode_gbs_out": round(x.numel() * 4 / t_dec / 1e9, 4)}
+    # config 3, sequence 0 (B = 1): decode its K and V, then dense attention
+    k3, v3 = cfg3_first
+    s42 = generate_rht_signs(128, 42)
+    bnd, lev = cb(128, 3)
+    pk, nk = T.encode(k3, s42, bnd, 3)
+    pv, nv = T.encode(v3, s42, bnd, 3)
+    q0 = cfg3_q0.float()
+
+    def attn():
+        K = T.decode(pk, nk, lev, s42, 3, 128).permute(1, 0, 2)[None]
+        V = T.decode(pv, nv, lev, s42, 3, 128).permute(1, 0, 2)[None]
+        return T.dense_attention(q0, K, V, 128 ** -0.5)
+    t3 = cpu_time(attn)
+    res["config3_b1"] = {"decode_attention_s": round(t3, 4), "ctx": int(k3.shape[0]),
+                         "kv_compressed_gbs": round(k3.shape[0] * 8 * 100 / t3 / 1e9, 4)}
+    return res
+
+
+# ---------------------------------------------------------------------------
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--only", default="",
+                    help="comma list of roofline entries to time (profiling runs); the step still runs")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run one 256 MiB device-to-device copy (calibrates rocprof byte counters)")
     args = ap.parse_args()
@@ -135,50 +480,54 @@ def main():
         sys.exit(2)
 
     import torch
-    from fused_turboquant import TurboQuantMSE, _lib
-    from fused_turboquant import paged as P
-    from fused_turboquant import raw as R
-    from fused_turboquant import v1 as V1
-
+    from fused_turboquant import _lib
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     L = _lib.lib()
     sp = _lib.stream_ptr(dev)
-    bits, T, H = 3, 32768, 8
-    n = T * H
+    only = set(x for x in args.only.split(",") if x)
 
-    def codec_setup(d, seed):
-        g = torch.Generator(device="cpu").manual_seed(seed)
-        sc = torch.exp(0.5 * torch.randn(d, generator=torch.Generator().manual_seed(seed + 1)))
-        k = (torch.randn(T, H, d, generator=g) * sc).to(torch.bfloat16).to(dev)
-        v = (torch.randn(T, H, d, generator=g) * sc).to(torch.bfloat16).to(dev)
-        tq = TurboQuantMSE(d, bits=bits, seed=42, device=dev)
-        ck, cv = tq.encode(k), tq.encode(v)
-        signs, bnd = tq.rotation.signs, tq.quantizer.boundaries
+    def want(name):
+        return not only or name in only
 
-        cls = tq.quantizer.codebook_class  # symmetric at d=128: the |t|-search kernel
-
-        def enc(x, c):
-            return lean_launch(L.ftq_encode_cb, (x, c, signs, bnd), x.data_ptr(), 2, n, d, signs.data_ptr(),
-                               bnd.data_ptr(), bits, cls, c.indices.data_ptr(), c.norms.data_ptr(), sp)
-        return tq, ck, enc(k, ck), enc(v, cv)
-
-    log(f"[bench] config2 encode: [{T},{H},128] and [{T},{H},256] bf16 3-bit, K and V")
-    tq128, ck128, enc_k, enc_v = codec_setup(128, 0)
-    _, _, enc_k256, _ = codec_setup(256, 10)
-    dec_out = torch.empty(T, H, 128, dtype=torch.float32, device=dev)
-    lev, sg = tq128.quantizer.levels, tq128.rotation.signs
-
-    dec_k = lean_launch(L.ftq_decode, (ck128, lev, sg, dec_out), ck128.indices.data_ptr(), ck128.norms.data_ptr(),
-                        n, 128, lev.data_ptr(), sg.data_ptr(), bits, dec_out.data_ptr(), 0, sp)
+    log("[bench] config2 encode: [32768,8,128] and [32768,8,256] bf16 3-bit, K and V")
+    e128 = encode_setup(dev, 128, 0)
+    e256 = encode_setup(dev, 256, 10) if want("encode_d256_3bit") else None
+    n = e128["n"]
+    ck = e128["ck"]
+    lev, sg = e128["tq"].quantizer.levels, e128["tq"].rotation.signs
+    dec_out = torch.empty(32768, 8, 128, dtype=torch.float32, device=dev)
+    dec_k = lean_launch(L.ftq_decode, ck.indices, ck.norms, n, 128, lev, sg, 3, dec_out, 0, sp)
 
     log("[bench] config3 paged cache (B=32 ctx=8192 K3V3)")
-    attn3 = P.bench_setup(dev)
-    log("[bench] config4 v1 cache (B=4 ctx~U[64K,128K] K4V2 v_rotate)")
-    attn4 = V1.bench_setup(dev)
-    log("[bench] boundary-layer raw fp16 cache (config3 shape, 512 B slots)")
-    attnr = R.bench_setup(dev)
+    cfg3 = make_config3(dev, keep_first=not args.no_cpu)
+    attn3 = paged_setup(dev, cfg3, "f16")
+    attn3v = paged_setup(dev, cfg3, "fp32") if want("paged_attn_config3_fp32_valu") else None
+    attn4 = attnr = None
+    if want("v1_attn_config4"):
+        log("[bench] config4 v1 cache (B=4 ctx~U[64K,128K] K4V2 v_rotate)")
+        attn4 = v1_setup(dev)
+    if want("raw_attn_boundary"):
+        log("[bench] boundary-layer raw fp16 cache (config3 shape, 512 B slots)")
+        attnr = raw_setup(dev)
+    stores = {}
+    store_cases = [("v1_store_rht_1024x8_d128", 1024, 128, 3, 3, "rht", False),
+                   ("v1_store_rht_1024x8_d256", 1024, 256, 3, 3, "rht", False),
+                   ("v1_store_rht_1x8_d128", 1, 128, 3, 3, "rht", False),
+                   ("v1_store_rht_1x8_d256", 1, 256, 3, 3, "rht", False),
+                   ("v1_store_planar_1024x8_d128", 1024, 128, 3, 3, "planar", False),
+                   ("v1_store_rotor_1024x8_d128", 1024, 128, 3, 3, "rotor", False),
+                   ("v1_store_iso_full_1024x8_d128", 1024, 128, 3, 3, "iso_full", False),
+                   ("v1_store_planar_1024x8_d256", 1024, 256, 3, 3, "planar", False),
+                   ("v1_store_config4_chunk", 32768, 128, 4, 2, "rht", True)]
+    for name, nt, d, kb, vb, kind, vrot in store_cases:
+        if want(name):
+            stores[name] = v1_store_setup(dev, nt, d, kb, vb, kind, vrot)
+    if want("paged_store_config3_chunk"):
+        stores["paged_store_config3_chunk"] = paged_store_setup(dev)
     torch.cuda.synchronize()
+
+    enc_k, enc_v = e128["enc_k"], e128["enc_v"]
 
     def step():
         enc_k()
@@ -195,7 +544,7 @@ def main():
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    check_lean(enc_k, enc_v)
+    check_lean(enc_k, enc_v, attn3["run"])
     t0 = time.perf_counter()
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
@@ -204,45 +553,70 @@ def main():
         step()
     e1.record()
     torch.cuda.synchronize()
-    check_lean(enc_k, enc_v)
+    check_lean(enc_k, enc_v, attn3["run"])
     wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
     ms_step = e0.elapsed_time(e1) / args.steps
     log(f"[bench] {args.steps} steps: {ms_step * 1e3:.1f} us/step (event), {wall_ms * 1e3:.1f} us/step (wall)")
 
     it = max(args.steps, 20)
-    t_enc = time_launches(enc_k, it, torch)
-    t_enc256 = time_launches(enc_k256, it, torch)
-    t_dec = time_launches(dec_k, it, torch)
-    t_a3 = time_launches(attn3["run"], it, torch)
-    t_a4 = time_launches(attn4["run"], it, torch)
-    t_ar = time_launches(attnr["run"], it, torch)
-    check_lean(enc_k, enc_k256, dec_k)
+    enc_bytes = n * 128 * 2 + n * (128 * 3 // 8) + n * 2
+    rl = {}
+    timed = []
 
-    enc_bytes = n * 128 * 2 + n * (128 * bits // 8) + n * 2
-    enc256_bytes = n * 256 * 2 + n * (256 * bits // 8) + n * 2
-    dec_bytes = n * (128 * bits // 8) + n * 2 + n * 128 * 4
-    rl = {
-        "encode_d128_3bit": roof("encode_d128_3bit", enc_bytes, t_enc),
-        "encode_d256_3bit": roof("encode_d256_3bit", enc256_bytes, t_enc256),
-        "decode_d128_3bit_f32": roof("decode_d128_3bit_f32", dec_bytes, t_dec),
-        "paged_attn_config3": roof("paged_attn_config3", attn3["total_bytes"], t_a3),
-        "v1_attn_config4": roof("v1_attn_config4", attn4["total_bytes"], t_a4),
-        "raw_attn_boundary": roof("raw_attn_boundary", attnr["total_bytes"], t_ar),
-    }
+    def entry(name, fn, alg_bytes, iters=it):
+        if want(name):
+            rl[name] = roof(name, alg_bytes, time_launches(fn, iters, torch))
+            timed.append(fn)
+
+    entry("encode_d128_3bit", enc_k, enc_bytes)
+    if e256 is not None:
+        entry("encode_d256_3bit", e256["enc_k"], n * 256 * 2 + n * (256 * 3 // 8) + n * 2)
+    entry("decode_d128_3bit_f32", dec_k, n * (128 * 3 // 8) + n * 2 + n * 128 * 4)
+    entry("paged_attn_config3", attn3["run"], attn3["total_bytes"])
+    if attn3v is not None:
+        entry("paged_attn_config3_fp32_valu", attn3v["run"], attn3v["total_bytes"])
+    if attn4 is not None:
+        entry("v1_attn_config4", attn4["run"], attn4["total_bytes"])
+    if attnr is not None:
+        entry("raw_attn_boundary", attnr["run"], attnr["total_bytes"])
+    for name, st in stores.items():
+        entry(name, st["run"], st["total_bytes"], iters=max(it, 100))
+    check_lean(*timed)
     for k, r in rl.items():
         log(f"[bench] {k}: {r['kernel_us']} us  {r['achieved']} GB/s  frac {r['frac']}")
+    t_enc = rl["encode_d128_3bit"]["kernel_us"] if "encode_d128_3bit" in rl else ms_step * 1e3
+    t_a3 = rl["paged_attn_config3"]["kernel_us"] if "paged_attn_config3" in rl else float("nan")
     enc_in_gbs = n * 128 * 2 / (t_enc * 1e-6) / 1e9
 
     cpu = None
     if not args.no_cpu:
-        log("[bench] cpu baseline (oracle encode on host cores)")
-        cv_gbs, sample = cpu_baseline_encode()
-        cpu = {"value": round(cv_gbs, 4), "unit": "GB/s (bf16 in)", "cores": 1, "kind": "port",
-               "sample": sample + f"; host {platform.processor() or platform.machine()}, "
-                                  f"os.cpu_count()={os.cpu_count()}, numpy single thread"}
+        log("[bench] cpu baseline (torch restatement of the unfused reference path, host cores)")
+        k256_cpu = e256["k_cpu"] if e256 is not None else config2_tensors(256, 10)[0]
+        res = cpu_baseline(e128["k_cpu"], k256_cpu, cfg3[4], cfg3[1][:1].cpu())
+        cpu = {"value": res["config2_d128"]["encode_gbs"], "unit": "GB/s (bf16 in, 3-bit d=128 encode)",
+               "cores": res["threads"], "kind": "port",
+               "sample": "oracle/torch_ref.py (torch restatement of the reference's unfused CPU path) at "
+                         f"torch.set_num_threads({res['os_cpu_count']}): config-2 encode/decode of one full "
+                         "[32768,8,d] tensor at d=128 and 256, config 1 (4-bit [1,8,4096,128], outlier "
+                         "channels x10) encode+decode, config-3 sequence 0 (B=1, ctx 8192) decode K/V + dense "
+                         f"attention; 1 warmup, median of 5; host {res['cpu_model']}",
+               "detail": res}
 
-    main_roof = dict(rl["encode_d128_3bit"])
+    main_roof = dict(rl.get("encode_d128_3bit", {}))
     main_roof["kernel"] = "ftq::encode_mfma_kernel<128,3,bf16,sym>"
+    cfg = {"workload": "config2 encode K+V [32768,8,128] bf16 3-bit + config3 paged decode "
+                       "attention B=32 Hq=32 Hkv=8 d=128 ctx=8192 page=16 K3V3",
+           "encode_us": round(t_enc, 2),
+           "attn_us_per_step": round(t_a3, 2),
+           "attn_kv_gbs": round(attn3["kv_bytes"] / (t_a3 * 1e-6) / 1e9, 1),
+           "attn_splits": attn3["splits"],
+           "attn_operands": "f16 MFMA operands (sigma-scaled level tables, query f16 hi+lo), fp32 accumulate "
+                            "and softmax; paged_attn_config3_fp32_valu = fp32 products on the VALU"}
+    if attn4 is not None and "v1_attn_config4" in rl:
+        t_a4 = rl["v1_attn_config4"]["kernel_us"]
+        cfg.update({"config4_attn_us_per_step": round(t_a4, 2),
+                    "config4_kv_gbs": round(attn4["kv_bytes"] / (t_a4 * 1e-6) / 1e9, 1),
+                    "config4_ctx": attn4["lens"], "config4_splits": attn4["splits"]})
     out = {
         "metric": "3-bit d128 encode GB/s + paged decode-attn us/step @8K ctx; % of HBM peak",
         "value": round(enc_in_gbs, 1),
@@ -250,16 +624,9 @@ def main():
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms_step, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "bf16 in / fp32 math / u8 codes", "data": "synthetic",
-        "config": {"workload": "config2 encode K+V [32768,8,128] bf16 3-bit + config3 paged decode "
-                               "attention B=32 Hq=32 Hkv=8 d=128 ctx=8192 page=16 K3V3",
-                   "encode_us": round(t_enc, 2),
-                   "attn_us_per_step": round(t_a3, 2),
-                   "attn_kv_gbs": round(attn3["kv_bytes"] / (t_a3 * 1e-6) / 1e9, 1),
-                   "attn_splits": attn3["splits"],
-                   "config4_attn_us_per_step": round(t_a4, 2),
-                   "config4_kv_gbs": round(attn4["kv_bytes"] / (t_a4 * 1e-6) / 1e9, 1),
-                   "config4_ctx": attn4["lens"], "config4_splits": attn4["splits"]},
+        "dtype": "bf16 in / fp32 math / u8 codes (encode); attention: f16 MFMA operands, fp32 accumulate",
+        "data": "synthetic",
+        "config": cfg,
         "roofline": main_roof,
         "rooflines": rl,
         "cpu_baseline": cpu,

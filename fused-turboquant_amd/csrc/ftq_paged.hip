@@ -732,6 +732,345 @@ __global__ __launch_bounds__(NW * 64, NW == 16 ? 1 : (D == 128 ? (QL ? 3 : 4) : 
 }
 
 // ---------------------------------------------------------------------------
+// decode attention with fp32 operands on the VALU (the reference's arithmetic:
+// fp32 products of the rotated query with the fp32 K levels, fp32 softmax
+// weights times the fp32 V norms and levels), kept beside the MFMA kernel
+// above to measure what the f16 matrix-core operands buy.  Split form only
+// (4 waves per (split, kv head, batch), partials merged by merge_splits_kernel),
+// d = 128, at most 4 query heads per kv head.
+//
+// Lane (m, g) = (lane & 15, lane >> 4) of a wave, per 16-token sub-block:
+//   Q.K: token m, dims [32 g, 32 g + 32): 16 pair lookups of fp32 levels and
+//        4 heads x 32 FMAs against the rotated query read from LDS (one
+//        16-byte read gives the 4 heads of one dim); the four quarter sums of
+//        a token are added over lanes m, m + 16, m + 32, m + 48.
+//   P.V: the lane-major V chunk of lane (g, m) -- tokens 4g..4g+3, dims
+//        16 b + m, b = 0..7 -- into acc[b][h] (fp32), summed over g after the
+//        last tile.  The softmax weights move from the score layout (lane
+//        (m, g) holds head g of token m) to the chunk layout through 512
+//        bytes of LDS per wave.
+// ---------------------------------------------------------------------------
+template <int B>
+struct CodeLut32 {  // fp32 pair tables: entry = (level[c0], level[c1]), 8 bytes
+  static constexpr int ENTRIES = 1 << (2 * B);
+  static constexpr int LOG_COPIES = (B <= 3) ? 4 : 0;  // 16 copies: a 16-lane phase of 8-byte reads
+  static constexpr int COPIES = 1 << LOG_COPIES;
+  static constexpr int BYTES = ENTRIES * 8 * COPIES;
+};
+
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) const f32x2 lds_f2;
+typedef __attribute__((address_space(3))) const f32x4 lds_f4;
+
+template <int B>
+__device__ void build_code_lut32(uint8_t* lut, const float* __restrict__ lev, int tid, int nthreads) {
+  using C = CodeLut32<B>;
+  for (int k = tid; k < C::ENTRIES * C::COPIES; k += nthreads) {
+    const int e = k >> C::LOG_COPIES;
+    reinterpret_cast<f32x2*>(lut)[k] = f32x2{lev[e & ((1 << B) - 1)], lev[e >> B]};
+  }
+}
+
+// the fp32 levels of the 2 codes at bits [P, P + 2B) of the code words
+template <int B, int N>
+__device__ __forceinline__ f32x2 lut32_pair(const uint32_t (&w)[N], int P, uint32_t base) {
+  using C = CodeLut32<B>;
+  return *(lds_f2*)(uintptr_t)lut_entry_off<3 + C::LOG_COPIES, 2 * B>(w, P, base);
+}
+
+template <int D, int BK, int BV>
+struct ValuTile {
+  using Gm = PagedGeom<D, BK, BV>;
+  uint32_t k[2][Gm::KLANE / 4];  // token m, K bytes [g KLANE, (g + 1) KLANE)
+  uint32_t v[2][Gm::VLANE / 4];  // V chunk of lane (g, m)
+  uint32_t kn[2];                // K norm of token m (f16 bits, low half)
+  uint32_t vn[2][2];             // V norms of tokens 4g..4g+3
+  bool ok[2];
+};
+
+template <int D, int BK, int BV>
+__device__ __forceinline__ void load_tile_valu(ValuTile<D, BK, BV>& r, const uint8_t* __restrict__ cache, int btv,
+                                               int tile, const SubDiv& sd, int64_t blk_stride, int64_t kvh_off,
+                                               int nb32, uint32_t ok_off, uint32_t ov_off, uint32_t okn, uint32_t ovn) {
+  using Gm = PagedGeom<D, BK, BV>;
+#pragma unroll
+  for (int sb = 0; sb < 2; ++sb) {
+    int phys = __builtin_amdgcn_readlane(btv, sb);
+    const bool valid = (uint32_t)phys < (uint32_t)nb32;
+    const int j = 2 * tile + sb;
+    const int sub = valid ? j - sd.page(j) * sd.nsub : 0;
+    if (!valid) phys = 0;
+    const uint8_t* base = cache + ((int64_t)phys * blk_stride + kvh_off + (int64_t)sub * Gm::SUB);
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(base), (short)0, Gm::SUB, 0x00020000);
+    buf_dwords(rs, ok_off, r.k[sb]);
+    buf_dwords(rs, ov_off, r.v[sb]);
+    r.kn[sb] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, okn, 0, 0);
+    buf_dwords(rs, ovn, r.vn[sb]);
+    r.ok[sb] = valid;
+  }
+}
+
+template <int D, int BK, int BV, int QT, bool SHARE>
+__global__ __launch_bounds__(256, 2) void paged_attn_valu_kernel(
+    const void* __restrict__ query, const uint8_t* __restrict__ cache,
+    const int32_t* __restrict__ block_table, const int32_t* __restrict__ seq_lens, int hq, int hkv,
+    int page_size, int max_blocks, int64_t num_blocks, const float* __restrict__ ksigns,
+    const float* __restrict__ klev, const float* __restrict__ vlev, float qscale, int num_splits,
+    float* __restrict__ ws_o, float* __restrict__ ws_lse) {
+  static_assert(D == 128, "laid out for head_dim 128");
+  using Gm = PagedGeom<D, BK, BV>;
+  constexpr int NW = 4, GM = 4;  // waves, query heads per kv head (at most)
+  constexpr int E = D / 16;
+  constexpr int QG = 32 * GM + 4;  // floats per quarter of the query block (padded: conflict-free reads)
+  constexpr int LK = CodeLut32<BK>::BYTES, LV = SHARE ? 0 : CodeLut32<BV>::BYTES;
+  const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int G = hq / hkv;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int m = lane & 15, g = lane >> 4;
+
+  // LDS: code tables | rotated query [4 quarters][32 dims][4 heads] | per-wave
+  // softmax weights [2 sub-blocks][16 tokens][4 heads]; the tables' bytes are
+  // reused for the wave merge at the end
+  extern __shared__ __attribute__((aligned(16))) uint8_t pool[];
+  __shared__ float red_m[NW][GM], red_l[NW][GM];
+  uint8_t* lutK = pool;
+  uint8_t* lutV = SHARE ? pool : pool + LK;
+  float* qv = reinterpret_cast<float*>(pool + LK + LV);
+  float* pw = qv + 4 * QG + wave * 128;
+  float* red_o = reinterpret_cast<float*>(pool);
+
+  const int seq_len = seq_lens[b];
+  const int n_tiles = (seq_len + 31) >> 5;
+  const int tps = (n_tiles + num_splits - 1) / num_splits;
+  const int t_begin = split * tps;
+  const int t_end = min(t_begin + tps, n_tiles);
+  SubDiv sd;
+  sd.nsub = page_size >> 4;
+  sd.m = (0x80000000u + (uint32_t)sd.nsub - 1u) / (uint32_t)sd.nsub;
+  sd.j_cap = (int)min((int64_t)max_blocks * sd.nsub, (int64_t)0x7fffffff);
+  const int seq_subs = (int)(((int64_t)seq_len + 15) >> 4);
+  const int nb32 = (int)min(num_blocks, (int64_t)0x7fffffff);
+  const int64_t blk_stride = (int64_t)hkv * sd.nsub * Gm::SUB;
+  const int64_t kvh_off = (int64_t)kvh * sd.nsub * Gm::SUB;
+  const __amdgpu_buffer_rsrc_t bt_rs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<int32_t*>(block_table + (int64_t)b * max_blocks), (short)0,
+      (int)min((int64_t)max_blocks * 4, (int64_t)0x7ffffffc), 0x00020000);
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  const uint32_t ok_off = (uint32_t)m * Gm::KTOK + (uint32_t)g * Gm::KLANE;
+  const uint32_t ov_off = (uint32_t)Gm::KSEC + (uint32_t)lane * Gm::VLANE;
+  const uint32_t okn = (uint32_t)Gm::KNORM + 2u * (uint32_t)m;
+  const uint32_t ovn = (uint32_t)Gm::VNORM + 8u * (uint32_t)g;
+  ValuTile<D, BK, BV> ra, rb;
+  int tile = t_begin + wave_u;
+  auto bt_of = [&](int t) __attribute__((always_inline)) {
+    return fetch_bt(bt_rs, t, t < t_end, seq_subs, sd, (uint32_t)lane);
+  };
+  auto load = [&](ValuTile<D, BK, BV>& r, int btv, int t) __attribute__((always_inline)) {
+    load_tile_valu(r, cache, btv, t, sd, blk_stride, kvh_off, nb32, ok_off, ov_off, okn, ovn);
+  };
+  int btv = 0;
+  if (tile < t_end) {
+    load(ra, bt_of(tile), tile);
+    btv = bt_of(tile + NW);
+  }
+
+  // prologue: fp32 pair tables, rotated and scaled query (one head per 16 lanes)
+  build_code_lut32<BK>(lutK, klev, tid, NW * 64);
+  if (!SHARE) build_code_lut32<BV>(lutV, vlev, tid, NW * 64);
+  {
+    const int hh = tid >> 4, l16 = tid & 15;
+    if (hh < GM) {
+      float y[E];
+      if (hh < G) {
+        load_elems<QT, E>(query, ((int64_t)b * hq + kvh * G + hh) * D + l16 * E, y);
+#pragma unroll
+        for (int i = 0; i < E; ++i) y[i] *= ksigns[l16 * E + i];
+      } else {
+#pragma unroll
+        for (int i = 0; i < E; ++i) y[i] = 0.f;
+      }
+      fwht_lanes<E, 16>(y, l16);
+      const float sc = (float)(1.0 / __builtin_sqrt((double)D)) * qscale;
+#pragma unroll
+      for (int i = 0; i < E; ++i) {
+        const int dd = l16 * E + i;
+        qv[(dd >> 5) * QG + (dd & 31) * GM + hh] = y[i] * sc;
+      }
+    }
+  }
+  __syncthreads();
+  const uint32_t tabK = lds_addr(lutK) + (((uint32_t)lane & (CodeLut32<BK>::COPIES - 1u)) << 3);
+  const uint32_t tabV = lds_addr(lutV) + (((uint32_t)lane & (CodeLut32<BV>::COPIES - 1u)) << 3);
+  const uint32_t qaddr = lds_addr(qv) + (uint32_t)g * QG * 4u;
+  const uint32_t pw_addr = lds_addr(pw);
+
+  float m_run[GM], l_run = 0.f;
+  float acc[8][GM];
+#pragma unroll
+  for (int h = 0; h < GM; ++h) m_run[h] = -INFINITY;
+#pragma unroll
+  for (int bb = 0; bb < 8; ++bb)
+#pragma unroll
+    for (int h = 0; h < GM; ++h) acc[bb][h] = 0.f;
+
+  constexpr float TAU = 8.f;
+  auto process = [&](const ValuTile<D, BK, BV>& cur, int tile) __attribute__((always_inline)) {
+    float s[2][GM];
+#pragma unroll
+    for (int sb = 0; sb < 2; ++sb) {
+      float sq[GM];
+#pragma unroll
+      for (int h = 0; h < GM; ++h) sq[h] = 0.f;
+#pragma unroll
+      for (int j = 0; j < 32; j += 2) {
+        const f32x2 lv = lut32_pair<BK>(cur.k[sb], j * BK, tabK);
+        const f32x4 q0 = *(lds_f4*)(uintptr_t)(qaddr + 16u * (uint32_t)j);
+        const f32x4 q1 = *(lds_f4*)(uintptr_t)(qaddr + 16u * (uint32_t)(j + 1));
+        sq[0] = __builtin_fmaf(q0.x, lv.x, sq[0]);
+        sq[1] = __builtin_fmaf(q0.y, lv.x, sq[1]);
+        sq[2] = __builtin_fmaf(q0.z, lv.x, sq[2]);
+        sq[3] = __builtin_fmaf(q0.w, lv.x, sq[3]);
+        sq[0] = __builtin_fmaf(q1.x, lv.y, sq[0]);
+        sq[1] = __builtin_fmaf(q1.y, lv.y, sq[1]);
+        sq[2] = __builtin_fmaf(q1.z, lv.y, sq[2]);
+        sq[3] = __builtin_fmaf(q1.w, lv.y, sq[3]);
+      }
+      const float kn = (float)__builtin_bit_cast(_Float16, (uint16_t)cur.kn[sb]);
+      const bool live = tile * 32 + sb * 16 + m < seq_len;
+#pragma unroll
+      for (int h = 0; h < GM; ++h) {
+        const float t = warp_sum_q(sq[h]) * kn;
+        s[sb][h] = live ? t : -INFINITY;
+      }
+    }
+    float tmax[GM];
+    bool raise = false;
+#pragma unroll
+    for (int h = 0; h < GM; ++h) {
+      float x = vmax(s[0][h], s[1][h]);
+      x = vmax(x, lane_xor<1>(x));
+      x = vmax(x, lane_xor<2>(x));
+      x = vmax(x, lane_xor<4>(x));
+      tmax[h] = vmax(x, lane_xor<8>(x));
+      raise = raise || (tmax[h] > m_run[h] + TAU);
+    }
+    if (__builtin_amdgcn_ballot_w64(raise) != 0) {  // wave-uniform, rare
+      float al[GM];
+#pragma unroll
+      for (int h = 0; h < GM; ++h) {
+        const float m_new = fmaxf(m_run[h], tmax[h]);
+        al[h] = __builtin_amdgcn_exp2f(m_run[h] - m_new);
+        m_run[h] = m_new;
+#pragma unroll
+        for (int bb = 0; bb < 8; ++bb) acc[bb][h] *= al[h];
+      }
+      l_run *= g == 0 ? al[0] : g == 1 ? al[1] : g == 2 ? al[2] : al[3];
+    }
+    // softmax weights of head g for token m of both sub-blocks
+    const float mg = g == 0 ? m_run[0] : g == 1 ? m_run[1] : g == 2 ? m_run[2] : m_run[3];
+#pragma unroll
+    for (int sb = 0; sb < 2; ++sb) {
+      const float sg = g == 0 ? s[sb][0] : g == 1 ? s[sb][1] : g == 2 ? s[sb][2] : s[sb][3];
+      const float p = __builtin_amdgcn_exp2f(sg - mg);
+      l_run += p;
+      pw[(sb * 16 + m) * GM + g] = p;
+    }
+    __asm__ volatile("" ::: "memory");  // a wave's LDS accesses run in order
+#pragma unroll
+    for (int sb = 0; sb < 2; ++sb) {
+      float pv[4][GM];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const f32x4 pp = *(lds_f4*)(uintptr_t)(pw_addr + 16u * (uint32_t)(sb * 16 + 4 * g + i));
+        const uint32_t vw = cur.vn[sb][i >> 1];
+        const float vn = cur.ok[sb] ? (float)__builtin_bit_cast(_Float16, (uint16_t)(vw >> (16 * (i & 1)))) : 0.f;
+        pv[i][0] = pp.x * vn;
+        pv[i][1] = pp.y * vn;
+        pv[i][2] = pp.z * vn;
+        pv[i][3] = pp.w * vn;
+      }
+#pragma unroll
+      for (int bb = 0; bb < 8; ++bb) {
+#pragma unroll
+        for (int pr = 0; pr < 2; ++pr) {
+          const f32x2 lv = lut32_pair<BV>(cur.v[sb], (4 * bb + 2 * pr) * BV, tabV);
+#pragma unroll
+          for (int h = 0; h < GM; ++h) {
+            acc[bb][h] = __builtin_fmaf(pv[2 * pr][h], lv.x, acc[bb][h]);
+            acc[bb][h] = __builtin_fmaf(pv[2 * pr + 1][h], lv.y, acc[bb][h]);
+          }
+        }
+      }
+    }
+    __asm__ volatile("" ::: "memory");
+  };
+
+  while (tile < t_end) {
+    int btn = bt_of(tile + 2 * NW);
+    load(rb, btv, tile + NW);
+    btv = btn;
+    process(ra, tile);
+    tile += NW;
+    if (tile >= t_end) break;
+    btn = bt_of(tile + 2 * NW);
+    load(ra, btv, tile + NW);
+    btv = btn;
+    process(rb, tile);
+    tile += NW;
+  }
+
+  // ---- wave totals, then the 4 waves merged through LDS ----
+  const float l_tot = group_sum<16>(l_run);  // head g, over the 16 tokens of a row
+#pragma unroll
+  for (int bb = 0; bb < 8; ++bb)
+#pragma unroll
+    for (int h = 0; h < GM; ++h) acc[bb][h] = warp_sum_q(acc[bb][h]);
+  __syncthreads();  // the code tables are dead: their LDS takes the merge buffer
+  if (lane == 0) {
+#pragma unroll
+    for (int h = 0; h < GM; ++h) red_m[wave][h] = m_run[h];
+  }
+  if (m == 0) red_l[wave][g] = l_tot;
+  if (g == 0) {
+#pragma unroll
+    for (int h = 0; h < GM; ++h)
+      if (h < G)
+#pragma unroll
+        for (int bb = 0; bb < 8; ++bb) red_o[(wave * G + h) * (D + 1) + 16 * bb + m] = acc[bb][h];
+  }
+  __syncthreads();
+  const int64_t row0 = ((int64_t)b * hq + kvh * G) * num_splits + split;
+  for (int idx = tid; idx < G * D; idx += NW * 64) {
+    const int gg = idx / D, d = idx % D;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) M = fmaxf(M, red_m[w][gg]);
+    float L = 0.f, o = 0.f;
+    if (M != -INFINITY) {
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        const float f = __builtin_amdgcn_exp2f(red_m[w][gg] - M);
+        L += f * red_l[w][gg];
+        o += f * red_o[(w * G + gg) * (D + 1) + d];
+      }
+    }
+    const int64_t row = row0 + (int64_t)gg * num_splits;
+    ws_o[row * D + d] = (L > 0.f) ? o / L : 0.f;
+    if (d == 0) ws_lse[row] = (L > 0.f) ? M + __builtin_log2f(L) : -INFINITY;
+  }
+}
+
+template <int D, int BK, int BV, bool SHARE>
+__host__ constexpr int paged_attn_valu_lds() {
+  const int tabs = CodeLut32<BK>::BYTES + (SHARE ? 0 : CodeLut32<BV>::BYTES);
+  const int front = tabs + (4 * (32 * 4 + 4) + 4 * 128) * 4;
+  const int red = 4 * 4 * (D + 1) * 4;
+  return front > red ? front : red;
+}
+
+// ---------------------------------------------------------------------------
 // host launchers (stage 2 -- merge of the splits, inverse RHT of V, output
 // cast -- is merge_splits_kernel in ftq_merge.h)
 // ---------------------------------------------------------------------------
@@ -855,6 +1194,52 @@ static hipError_t launch_attn1(int bk, int bv, const AttnArgs& a, hipStream_t st
   return launch_attn2<D, 4>(bv, a, st);
 }
 
+// merge of the split partials: inverse RHT of V, output dtype
+static hipError_t launch_attn_merge(const AttnArgs& a, int d, hipStream_t st) {
+  const int64_t rows = (int64_t)a.B * a.hq;
+  const float sc = fwht_scale(d);
+  if (d == 256) {
+    if (a.ot == F32) return launch_merge_splits<256, F32, ROT_SIGNS>(a.wo, a.wl, rows, a.splits, a.vs, sc, a.out, st);
+    if (a.ot == F16) return launch_merge_splits<256, F16, ROT_SIGNS>(a.wo, a.wl, rows, a.splits, a.vs, sc, a.out, st);
+    return launch_merge_splits<256, BF16, ROT_SIGNS>(a.wo, a.wl, rows, a.splits, a.vs, sc, a.out, st);
+  }
+  if (a.ot == F32) return launch_merge_splits<128, F32, ROT_SIGNS>(a.wo, a.wl, rows, a.splits, a.vs, sc, a.out, st);
+  if (a.ot == F16) return launch_merge_splits<128, F16, ROT_SIGNS>(a.wo, a.wl, rows, a.splits, a.vs, sc, a.out, st);
+  return launch_merge_splits<128, BF16, ROT_SIGNS>(a.wo, a.wl, rows, a.splits, a.vs, sc, a.out, st);
+}
+
+template <int D, int BK, int BV, bool SHARE>
+static void launch_attn_valu_kernel(const AttnArgs& a, hipStream_t st) {
+  dim3 grid(a.splits, a.hkv, a.B), block(256);
+  constexpr size_t lds = (size_t)paged_attn_valu_lds<D, BK, BV, SHARE>();
+  if (a.qt == F32)
+    paged_attn_valu_kernel<D, BK, BV, F32, SHARE><<<grid, block, lds, st>>>(a.q, a.cache, a.bt, a.sl, a.hq, a.hkv, a.page_size, a.max_blocks, a.num_blocks, a.ks, a.kl, a.vl, a.qscale, a.splits, a.wo, a.wl);
+  else if (a.qt == F16)
+    paged_attn_valu_kernel<D, BK, BV, F16, SHARE><<<grid, block, lds, st>>>(a.q, a.cache, a.bt, a.sl, a.hq, a.hkv, a.page_size, a.max_blocks, a.num_blocks, a.ks, a.kl, a.vl, a.qscale, a.splits, a.wo, a.wl);
+  else
+    paged_attn_valu_kernel<D, BK, BV, BF16, SHARE><<<grid, block, lds, st>>>(a.q, a.cache, a.bt, a.sl, a.hq, a.hkv, a.page_size, a.max_blocks, a.num_blocks, a.ks, a.kl, a.vl, a.qscale, a.splits, a.wo, a.wl);
+}
+
+template <int BK, int BV>
+static hipError_t launch_attn_valu(const AttnArgs& a, hipStream_t st) {
+  if constexpr (BK == BV) {
+    if (a.kl == a.vl) launch_attn_valu_kernel<128, BK, BV, true>(a, st);
+    else launch_attn_valu_kernel<128, BK, BV, false>(a, st);
+  } else {
+    launch_attn_valu_kernel<128, BK, BV, false>(a, st);
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  return launch_attn_merge(a, 128, st);
+}
+
+template <int BK>
+static hipError_t launch_attn_valu2(int bv, const AttnArgs& a, hipStream_t st) {
+  if (bv == 2) return launch_attn_valu<BK, 2>(a, st);
+  if (bv == 3) return launch_attn_valu<BK, 3>(a, st);
+  return launch_attn_valu<BK, 4>(a, st);
+}
+
 int auto_splits(int batch, int hkv, int seq_hint, int target_wgs) {
   // aim for target_wgs workgroups with at least 8 tiles per wave
   const int units = batch * hkv;
@@ -923,12 +1308,13 @@ extern "C" int ftq_paged_store(const void* key, const void* value, int dtype, in
   return hip_status(e);
 }
 
-extern "C" int ftq_paged_decode_attention(
-    const void* query, int q_dtype, const uint8_t* kv_cache, const int32_t* block_table,
-    const int32_t* seq_lens, int batch, int num_q_heads, int num_kv_heads, int d, int page_size,
-    int max_blocks_per_seq, int64_t num_blocks, const float* k_signs, const float* v_signs, const float* k_levels,
-    const float* v_levels, int bits_k, int bits_v, float scale, int num_splits, void* workspace,
-    int64_t workspace_bytes, void* out, int out_dtype, void* stream) {
+// Argument checks and launch arguments shared by the two decode entry points.
+static int paged_attn_args(AttnArgs& a, const void* query, int q_dtype, const uint8_t* kv_cache,
+                           const int32_t* block_table, const int32_t* seq_lens, int batch, int num_q_heads,
+                           int num_kv_heads, int d, int page_size, int max_blocks_per_seq, int64_t num_blocks,
+                           const float* k_signs, const float* v_signs, const float* k_levels,
+                           const float* v_levels, int bits_k, int bits_v, float scale, int num_splits,
+                           void* workspace, int64_t workspace_bytes, void* out, int out_dtype) {
   FTQ_REQUIRE(d == 128 || d == 256, "paged attention: head_dim must be 128 or 256");
   FTQ_REQUIRE(bits_k >= 2 && bits_k <= 4 && bits_v >= 2 && bits_v <= 4, "bits must be 2, 3, or 4");
   FTQ_REQUIRE(page_size >= 16 && page_size % 16 == 0, "page_size must be a multiple of 16");
@@ -952,7 +1338,6 @@ extern "C" int ftq_paged_decode_attention(
               "workspace too small (see ftq_paged_workspace_bytes)");
   FTQ_REQUIRE(aligned16(query) && aligned16(out) && aligned16(workspace) && aligned16(kv_cache),
               "query, out, workspace and kv_cache must be 16-byte aligned");
-  AttnArgs a;
   a.q = query; a.qt = q_dtype; a.cache = kv_cache; a.bt = block_table; a.sl = seq_lens;
   a.B = batch; a.hq = num_q_heads; a.hkv = num_kv_heads; a.page_size = page_size;
   a.max_blocks = max_blocks_per_seq; a.num_blocks = num_blocks; a.ks = k_signs; a.vs = v_signs; a.kl = k_levels; a.vl = v_levels;
@@ -961,7 +1346,45 @@ extern "C" int ftq_paged_decode_attention(
   a.wo = static_cast<float*>(workspace);
   a.wl = a.wo + (int64_t)batch * num_q_heads * num_splits * d;
   a.out = out; a.ot = out_dtype;
+  return FTQ_OK;
+}
+
+extern "C" int ftq_paged_decode_attention(
+    const void* query, int q_dtype, const uint8_t* kv_cache, const int32_t* block_table,
+    const int32_t* seq_lens, int batch, int num_q_heads, int num_kv_heads, int d, int page_size,
+    int max_blocks_per_seq, int64_t num_blocks, const float* k_signs, const float* v_signs, const float* k_levels,
+    const float* v_levels, int bits_k, int bits_v, float scale, int num_splits, void* workspace,
+    int64_t workspace_bytes, void* out, int out_dtype, void* stream) {
+  AttnArgs a;
+  const int rc = paged_attn_args(a, query, q_dtype, kv_cache, block_table, seq_lens, batch, num_q_heads,
+                                 num_kv_heads, d, page_size, max_blocks_per_seq, num_blocks, k_signs, v_signs,
+                                 k_levels, v_levels, bits_k, bits_v, scale, num_splits, workspace,
+                                 workspace_bytes, out, out_dtype);
+  if (rc != FTQ_OK || batch == 0) return rc;
   hipStream_t st = (hipStream_t)stream;
   hipError_t e = (d == 128) ? launch_attn1<128>(bits_k, bits_v, a, st) : launch_attn1<256>(bits_k, bits_v, a, st);
+  return hip_status(e);
+}
+
+extern "C" int ftq_paged_decode_attention_valu(
+    const void* query, int q_dtype, const uint8_t* kv_cache, const int32_t* block_table,
+    const int32_t* seq_lens, int batch, int num_q_heads, int num_kv_heads, int d, int page_size,
+    int max_blocks_per_seq, int64_t num_blocks, const float* k_signs, const float* v_signs, const float* k_levels,
+    const float* v_levels, int bits_k, int bits_v, float scale, int num_splits, void* workspace,
+    int64_t workspace_bytes, void* out, int out_dtype, void* stream) {
+  FTQ_REQUIRE(d == 128, "fp32 VALU paged attention: head_dim must be 128");
+  FTQ_REQUIRE(num_kv_heads > 0 && num_q_heads % num_kv_heads == 0 && num_q_heads / num_kv_heads <= 4,
+              "fp32 VALU paged attention: at most 4 query heads per kv head");
+  AttnArgs a;
+  const int rc = paged_attn_args(a, query, q_dtype, kv_cache, block_table, seq_lens, batch, num_q_heads,
+                                 num_kv_heads, d, page_size, max_blocks_per_seq, num_blocks, k_signs, v_signs,
+                                 k_levels, v_levels, bits_k, bits_v, scale, num_splits, workspace,
+                                 workspace_bytes, out, out_dtype);
+  if (rc != FTQ_OK || batch == 0) return rc;
+  hipStream_t st = (hipStream_t)stream;
+  hipError_t e;
+  if (bits_k == 2) e = launch_attn_valu2<2>(bits_v, a, st);
+  else if (bits_k == 3) e = launch_attn_valu2<3>(bits_v, a, st);
+  else e = launch_attn_valu2<4>(bits_v, a, st);
   return hip_status(e);
 }

@@ -35,6 +35,7 @@ _SIG = {
                                    "i32", "i64", "vp", "vp", "vp", "vp", "i32", "i32", "f32", "i32",
                                    "vp", "i64", "vp", "i32", "vp"],
 }
+_SIG["ftq_paged_decode_attention_valu"] = _SIG["ftq_paged_decode_attention"]
 
 
 def _bind():
@@ -126,14 +127,20 @@ def paged_decode_attention(query: torch.Tensor, kv_cache: torch.Tensor, block_ta
                            seq_lens: torch.Tensor, k_quant: TurboQuantMSE, v_quant: TurboQuantMSE,
                            scale: float | None = None, num_splits: int | None = None,
                            max_seq_len: int | None = None, out: torch.Tensor | None = None,
-                           workspace: torch.Tensor | None = None) -> torch.Tensor:
+                           workspace: torch.Tensor | None = None, operands: str = "f16") -> torch.Tensor:
     """query [B, Hq, d] -> attention output [B, Hq, d] (query dtype unless ``out`` given).
 
     ``num_splits`` (split-K factor over the context) defaults to a value that
     fills the GPU; pass ``max_seq_len`` to size it without a device sync.
     ``workspace`` (uint8, >= ``workspace_bytes``) may be preallocated for
-    graph capture.
+    graph capture.  ``operands``: ``"f16"`` (default) takes the scores and
+    P.V on the matrix cores with f16 operands (scaled level tables, query as
+    f16 hi + lo, fp32 accumulation); ``"fp32"`` takes every product in fp32
+    on the VALU, the reference's arithmetic (d = 128, GQA group <= 4, split
+    form only).
     """
+    if operands not in ("f16", "fp32"):
+        raise ValueError("operands must be 'f16' or 'fp32'")
     B, hq, d = query.shape
     nb, hkv, nsub, sub = kv_cache.shape
     if sub != subblock_bytes(d, k_quant.bits, v_quant.bits):
@@ -150,7 +157,7 @@ def paged_decode_attention(query: torch.Tensor, kv_cache: torch.Tensor, block_ta
         scale = 1.0 / math.sqrt(d)
     if num_splits is None:
         msl = max_seq_len if max_seq_len is not None else block_table.shape[1] * nsub * 16
-        num_splits = default_splits(B, hkv, msl, hq, d)
+        num_splits = default_splits(B, hkv, msl, hq, d) if operands == "f16" else default_splits(B, hkv, msl)
     if out is None:
         out = torch.empty(B, hq, d, dtype=q.dtype, device=dev)
     need = workspace_bytes(B, hq, d, num_splits)
@@ -158,7 +165,8 @@ def paged_decode_attention(query: torch.Tensor, kv_cache: torch.Tensor, block_ta
         workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=dev)
     bt = block_table.contiguous()
     L = _bind()
-    _lib.check(L.ftq_paged_decode_attention(
+    fn = L.ftq_paged_decode_attention if operands == "f16" else L.ftq_paged_decode_attention_valu
+    _lib.check(fn(
         q.data_ptr(), _lib.dtype_code(q.dtype), kv_cache.data_ptr(), bt.data_ptr(),
         seq_lens.contiguous().data_ptr(), B, hq, hkv, d, nsub * 16, bt.shape[1], nb,
         k_quant.rotation.signs.data_ptr(), v_quant.rotation.signs.data_ptr(),
@@ -245,100 +253,3 @@ class PagedTurboQuantCache:
     def decode_attention(self, query, block_table, seq_lens, **kw) -> torch.Tensor:
         return paged_decode_attention(query, self.kv_cache, block_table, seq_lens,
                                       self.k_quant, self.v_quant, **kw)
-
-
-# --------------------------------------------------------------------------
-# benchmark / smoke helpers (config 3 of the benchmark plan)
-# --------------------------------------------------------------------------
-
-
-def make_config3(dev, B=32, hq=32, hkv=8, d=128, ctx=8192, page=16, bits=3, seed=0):
-    """B sequences of ctx tokens, block table = seeded random permutation of the pages."""
-    g = torch.Generator(device="cpu").manual_seed(seed)
-    pages_per_seq = (ctx + page - 1) // page
-    nblocks = B * pages_per_seq
-    cache = PagedTurboQuantCache(nblocks, page, hkv, d, bits, bits, seed=42, device=dev)
-    perm = torch.randperm(nblocks, generator=g).to(torch.int32)
-    block_table = perm.view(B, pages_per_seq).to(dev)
-    # slots of every (sequence, position) in order
-    pos = torch.arange(ctx, dtype=torch.int64)
-    slots = (block_table.cpu().long()[:, pos // page] * page + (pos % page)).reshape(-1).to(dev)
-    chunk = 1 << 16
-    n = B * ctx
-    for s in range(0, n, chunk):
-        e = min(n, s + chunk)
-        k = torch.randn(e - s, hkv, d, generator=g).to(torch.bfloat16).to(dev)
-        v = torch.randn(e - s, hkv, d, generator=g).to(torch.bfloat16).to(dev)
-        cache.store(k, v, slots[s:e])
-    q = torch.randn(B, hq, d, generator=g).to(torch.bfloat16).to(dev)
-    seq_lens = torch.full((B,), ctx, dtype=torch.int32, device=dev)
-    return cache, q, block_table, seq_lens
-
-
-def bench_setup(dev):
-    B, hq, hkv, d, ctx, page = 32, 32, 8, 128, 8192, 16
-    cache, q, bt, sl = make_config3(dev, B, hq, hkv, d, ctx, page)
-    splits = default_splits(B, hkv, ctx, hq, d)
-    out = torch.empty(B, hq, d, dtype=torch.bfloat16, device=dev)
-    ws = torch.empty(workspace_bytes(B, hq, d, splits), dtype=torch.uint8, device=dev)
-
-    # one C-ABI launch per step (the wrapper's checks ran once above); the
-    # launch holds raw pointers, so the tensors behind them stay with it
-    paged_decode_attention(q, cache.kv_cache, bt, sl, cache.k_quant, cache.v_quant,
-                           num_splits=splits, out=out, workspace=ws)
-    L = _bind()
-    kv = cache.kv_cache
-    nb, _, nsub, _ = kv.shape
-    kq, vq = cache.k_quant, cache.v_quant
-    args = (q.data_ptr(), _lib.dtype_code(q.dtype), kv.data_ptr(), bt.data_ptr(), sl.data_ptr(), B, hq, hkv,
-            d, nsub * 16, bt.shape[1], nb, kq.rotation.signs.data_ptr(), vq.rotation.signs.data_ptr(),
-            *_levels_pair(kq, vq), kq.bits, vq.bits,
-            1.0 / math.sqrt(d), splits, ws.data_ptr(), ws.numel(), out.data_ptr(), _lib.dtype_code(out.dtype),
-            _lib.stream_ptr(dev))
-    keep = (cache, q, bt, sl, ws, out)
-
-    def run():
-        _lib.check(L.ftq_paged_decode_attention(*args))
-    run.keep = keep
-
-    kv_bytes = B * ctx * hkv * (subblock_bytes(d, 3, 3) // 16)
-    total = kv_bytes + q.numel() * 2 + out.numel() * 2 + bt.numel() * 4 + sl.numel() * 4
-    return {"run": run, "kv_bytes": kv_bytes, "total_bytes": total, "splits": splits,
-            "cache": cache, "q": q, "bt": bt, "sl": sl, "out": out}
-
-
-def smoke_paged(dev):
-    """Tiny paged store + decode attention checked against the CPU oracle."""
-    import numpy as np
-    from oracle import tq_oracle as O
-    B, hq, hkv, d, page = 2, 8, 2, 128, 16
-    lens = [37, 70]
-    g = torch.Generator().manual_seed(3)
-    nblk = 12
-    cache = PagedTurboQuantCache(nblk, page, hkv, d, 3, 3, device=dev)
-    bt = torch.randperm(nblk, generator=g)[: B * 6].view(B, 6).to(torch.int32)
-    ks, vs = [], []
-    for b in range(B):
-        k = torch.randn(lens[b], hkv, d, generator=g).to(torch.bfloat16)
-        v = torch.randn(lens[b], hkv, d, generator=g).to(torch.bfloat16)
-        pos = torch.arange(lens[b])
-        slots = (bt[b].long()[pos // page] * page + pos % page)
-        cache.store(k.to(dev), v.to(dev), slots.to(dev))
-        ks.append(k)
-        vs.append(v)
-    q = torch.randn(B, hq, d, generator=g).to(torch.bfloat16)
-    out = cache.decode_attention(q.to(dev), bt.to(dev), torch.tensor(lens, dtype=torch.int32, device=dev),
-                                 num_splits=2).float().cpu().numpy()
-    kq, vq = cache.k_quant, cache.v_quant
-    S = max(lens)
-    Kd = np.zeros((B, hkv, S, d))
-    Vd = np.zeros((B, hkv, S, d))
-    for b in range(B):
-        for src, dst, tq in ((ks[b], Kd, kq), (vs[b], Vd, vq)):
-            p, n16, _, _ = O.encode(src.float().numpy(), tq.rotation.signs.cpu().numpy(),
-                                    tq.quantizer.boundaries.cpu().numpy(), 3)
-            dec = O.decode(p, n16, tq.quantizer.levels.cpu().numpy(), tq.rotation.signs.cpu().numpy(), 3, d)
-            dst[b, :, : lens[b]] = dec.transpose(1, 0, 2)
-    ref = O.dense_decode_attention(q.float().numpy(), Kd, Vd, lens, 1.0 / math.sqrt(d))
-    err = np.abs(out - ref)
-    assert err.max() <= 2e-2 and err.mean() <= 2e-3, (err.max(), err.mean())

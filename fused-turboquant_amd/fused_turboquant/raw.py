@@ -161,39 +161,3 @@ def raw_decode_attention(query: torch.Tensor, kv_cache: torch.Tensor, block_tabl
     else:
         _lib.check(L.ftq_raw_decode_attention_lse(*args, lse.data_ptr(), _lib.stream_ptr(dev)))
     return out
-
-
-# --------------------------------------------------------------------------
-# benchmark helper: the config-3 shape over raw fp16 slots (512 B per token)
-# --------------------------------------------------------------------------
-
-
-def bench_setup(dev, B=32, hq=32, hkv=8, d=128, ctx=8192, bs=16, seed=5):
-    """Raw fp16 cache of B sequences of ``ctx`` tokens (slot 512 B, pages a
-    seeded permutation), filled by ``raw_store``; returns a launcher and the
-    algorithmic bytes of one decode step."""
-    g = torch.Generator().manual_seed(seed)
-    gd = torch.Generator(device=dev).manual_seed(seed)  # bulk K/V drawn on the device
-    pages = ctx // bs
-    nb = B * pages
-    cache = torch.zeros(nb, bs, hkv, 4 * d, dtype=torch.uint8, device=dev)
-    bt = torch.randperm(nb, generator=g).to(torch.int32).view(B, pages).to(dev)
-    pos = torch.arange(ctx, device=dev)
-    for b in range(B):
-        k = torch.randn(ctx, hkv, d, generator=gd, device=dev).to(torch.bfloat16)
-        v = torch.randn(ctx, hkv, d, generator=gd, device=dev).to(torch.bfloat16)
-        slots = bt[b].long()[pos // bs] * bs + pos % bs
-        raw_store(k, v, cache, slots)
-    q = torch.randn(B, hq, d, generator=g).to(torch.bfloat16).to(dev)
-    sl = torch.full((B,), ctx, dtype=torch.int32, device=dev)
-    splits = default_splits(B, hkv, ctx)
-    out = torch.empty(B, hq, d, dtype=torch.bfloat16, device=dev)
-    ws = torch.empty(workspace_bytes(B, hq, d, splits), dtype=torch.uint8, device=dev)
-
-    def run():
-        raw_decode_attention(q, cache, bt, sl, num_splits=splits, out=out, workspace=ws)
-
-    kv_bytes = B * ctx * hkv * raw_slot_bytes(d)
-    total = kv_bytes + q.numel() * 2 + out.numel() * 2 + bt.numel() * 4 + sl.numel() * 4
-    return {"run": run, "kv_bytes": kv_bytes, "total_bytes": total, "splits": splits,
-            "cache": cache, "q": q, "bt": bt, "sl": sl, "out": out, "ws": ws}

@@ -446,75 +446,3 @@ class TurboQuantV1Layer:
         return v1_decode_attention(query, kv_cache, block_table, seq_lens, self.centroids,
                                    self.key_bits, self.value_bits, v_rotate=self.v_rotate,
                                    v_lloyd_max=self.v_lloyd_max, rotation=self.rotation, **kw)
-
-
-# --------------------------------------------------------------------------
-# benchmark helper (config 4 of the benchmark plan)
-# --------------------------------------------------------------------------
-
-
-def make_config4(dev, seed=4):
-    """Mixed-bit long-context decode: K4V2, v_rotate on, B=4, 32 q / 8 kv heads,
-    d=128, page 16; ctx_i ~ U[65536, 131072]; K/V N(0,1) bf16 with 2% of tokens
-    x8; block table a seeded permutation of the physical pages."""
-    d, bs, hkv, hq, kb, vb, B = 128, 16, 8, 32, 4, 2, 4
-    g = torch.Generator().manual_seed(seed)
-    lens = torch.randint(65536, 131073, (B,), generator=g).tolist()
-    layer = TurboQuantV1Layer(d, kb, vb, v_rotate=True, device=dev)
-    pages = [(L + bs - 1) // bs for L in lens]
-    nb = sum(pages)
-    cache = torch.zeros(layer.kv_cache_shape(nb, bs, hkv), dtype=torch.uint8, device=dev)
-    perm = torch.randperm(nb, generator=g).to(torch.int32)
-    bt = torch.zeros(B, max(pages), dtype=torch.int32)
-    used = 0
-    gd = torch.Generator(device=dev).manual_seed(seed + 1)
-    for b, L in enumerate(lens):
-        bt[b, :pages[b]] = perm[used:used + pages[b]]
-        used += pages[b]
-        btd = bt[b].to(dev).long()
-        for s0 in range(0, L, 32768):
-            n = min(32768, L - s0)
-            k = torch.randn(n, hkv, d, generator=gd, device=dev)
-            v = torch.randn(n, hkv, d, generator=gd, device=dev)
-            sel = torch.rand(n, generator=gd, device=dev) < 0.02
-            k[sel] *= 8
-            v[sel] *= 8
-            pos = torch.arange(s0, s0 + n, device=dev)
-            layer.store(k.to(torch.bfloat16), v.to(torch.bfloat16), cache, btd[pos // bs] * bs + pos % bs)
-    q = torch.randn(B, hq, d, generator=g).to(torch.bfloat16).to(dev)
-    sl = torch.tensor(lens, dtype=torch.int32, device=dev)
-    return layer, cache, q, bt.to(dev), sl, lens
-
-
-def bench_setup(dev):
-    layer, cache, q, bt, sl, lens = make_config4(dev)
-    B, hq, d = q.shape
-    hkv = cache.shape[2]
-    splits = default_splits(B, hkv, max(lens))
-    out = torch.empty(B, hq, d, dtype=torch.bfloat16, device=dev)
-    ws = torch.empty(workspace_bytes(B, hq, d, splits), dtype=torch.uint8, device=dev)
-
-    # one C-ABI launch per step: the wrapper's validation and centroid sort stay outside
-    v1_decode_attention(q, cache, bt, sl, layer.centroids, layer.key_bits, layer.value_bits,
-                        v_rotate=True, num_splits=splits, out=out, workspace=ws)
-    L = _bind()
-    sb, sp, sh = _strides(cache)
-    nb, bs = cache.shape[0], cache.shape[1]
-    args = (q.data_ptr(), _lib.dtype_code(q.dtype), cache.data_ptr(), nb, bs, sb, sp, sh,
-            bt.data_ptr(), bt.shape[1], sl.data_ptr(), None, B, hq, hkv, d,
-            layer.centroids.data_ptr(), layer.key_bits, layer.value_bits, 1.0 / math.sqrt(d), 1,
-            splits, ws.data_ptr(), ws.numel(), out.data_ptr(), _lib.dtype_code(out.dtype),
-            _lib.stream_ptr(dev))
-
-    # the launch holds raw pointers: keep every tensor behind them alive with it
-    keep = (layer, cache, q, bt, sl, ws, out)
-
-    def run():
-        _lib.check(L.ftq_v1_decode_attention(*args))
-    run.keep = keep
-
-    per_tok = slot_bytes(d, layer.key_bits, layer.value_bits)  # 66 B of K + 36 B of V
-    kv_bytes = sum(lens) * hkv * per_tok
-    total = kv_bytes + q.numel() * 2 + out.numel() * 2 + sum((L + 15) // 16 for L in lens) * 4 + B * 4
-    return {"run": run, "kv_bytes": kv_bytes, "total_bytes": total, "splits": splits,
-            "lens": lens, "out": out}

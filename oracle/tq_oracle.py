@@ -258,6 +258,17 @@ def decode(packed: np.ndarray, norms16: np.ndarray, levels: np.ndarray, signs: n
     return inverse_rht(r, signs)
 
 
+def tie_ulps(u: np.ndarray, cuts: np.ndarray, d: int) -> np.ndarray:
+    """Distance of u to the nearest of `cuts` (float32 values: interior
+    boundaries or midpoints), in float32 ulps of max(|cut|, d**-0.5): the
+    rounding of the rotated coordinate (a sum of d terms of size ~d**-0.5 in
+    normalised units) is measured against that scale, also at a cut near 0."""
+    c = np.asarray(cuts, np.float32)
+    scale = np.spacing(np.maximum(np.abs(c), np.float32(d ** -0.5)).astype(np.float32)).astype(np.float64)
+    uu = np.asarray(u, np.float64)[..., None]
+    return np.min(np.abs(uu - c.astype(np.float64)) / scale, axis=-1)
+
+
 def boundary_distance(u: np.ndarray, boundaries: np.ndarray) -> np.ndarray:
     """|u - nearest interior boundary| (float64), for tie accounting."""
     b = np.asarray(boundaries, np.float32).astype(np.float64)[1:-1]

@@ -41,10 +41,13 @@ def _check_arrays(x_cpu, s, bnd, packed, norms, bits, d, label):
     codes_ref = O.unpack(p_ref.reshape(-1, d * bits // 8), bits, d)
     diff = codes != codes_ref
     ties = int(diff.sum())
+    worst = 0.0
     if ties:
         dist = O.boundary_distance(u_ref.reshape(-1, d), bnd)[diff]
+        worst = float(O.tie_ulps(u_ref.reshape(-1, d)[diff], np.asarray(bnd)[1:-1], d).max())
         assert dist.max() < TIE, f"{label}: code mismatch {dist.max():.3g} away from a boundary"
         assert np.all(np.abs(codes.astype(int) - codes_ref.astype(int))[diff] == 1)
+    print(f"[{label}] tie distance max {worst:.2f} ulp")
     nn = norms.reshape(-1).astype(np.float32)
     nr = n_ref.reshape(-1).astype(np.float32)
     assert np.all(np.abs(nn - nr) <= 1e-3 * np.abs(nr) + 1e-7), f"{label}: norm mismatch"

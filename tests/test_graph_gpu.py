@@ -11,6 +11,8 @@ with that eager result, bit for bit (same kernels, same inputs).
 import math
 
 import pytest
+
+import bench
 import torch
 
 pytestmark = pytest.mark.gpu
@@ -61,7 +63,7 @@ def test_encode_under_graph(cuda):
 def test_paged_decode_under_graph(cuda, splits):
     from fused_turboquant import paged as P
     B, hq, hkv, d, ctx, page = 4, 16, 4, 128, 700, 16
-    cache, q, bt, sl = P.make_config3(cuda, B, hq, hkv, d, ctx, page)
+    cache, q, bt, sl = bench.make_config3(cuda, B, hq, hkv, d, ctx, page)
     out_g = torch.empty(B, hq, d, dtype=torch.bfloat16, device=cuda)
     ws = torch.empty(P.workspace_bytes(B, hq, d, splits), dtype=torch.uint8, device=cuda)
     g = _capture(lambda: P.paged_decode_attention(q, cache.kv_cache, bt, sl, cache.k_quant, cache.v_quant,

@@ -141,3 +141,46 @@ def test_lse_merge_equals_single_softmax():
         parts_o.append((pp / pp.sum()) @ v[a:b]); parts_l.append(m + np.log(pp.sum()))
     o, _ = O.lse_merge(np.array(parts_o), np.array(parts_l))
     assert np.allclose(o, full, atol=1e-12)
+
+
+# ---- the torch restatement timed as bench.py's CPU baseline -----------------
+
+
+@pytest.mark.parametrize("d", [64, 128, 256])
+@pytest.mark.parametrize("bits", [2, 3, 4])
+def test_torch_ref_matches_reference(golden, d, bits):
+    """oracle/torch_ref.py reproduces the reference's unfused encode / decode
+    outputs (tests/golden/encode.npz) byte for byte."""
+    import torch
+    from oracle import torch_ref as T
+    enc, cb = golden["encode"], golden["codebooks"]
+    key = f"{d}_{bits}"
+    x = torch.from_numpy(enc["x_" + key].view(np.int16)).view(torch.bfloat16)
+    s = torch.from_numpy(golden["signs"][f"s_{d}_42"])
+    bnd = torch.from_numpy(cb[f"b_{d}_{bits}"].astype(np.float32))
+    lev = torch.from_numpy(cb[f"l_{d}_{bits}"].astype(np.float32))
+    p, n16 = T.encode(x, s, bnd, bits)
+    assert np.array_equal(p.numpy(), enc["packed_" + key])
+    assert np.array_equal(n16.view(torch.int16).numpy().view(np.uint16), enc["norms_" + key])
+    dec = T.decode(p, n16, lev, s, bits, d)
+    assert np.array_equal(dec.numpy(), enc["dec_" + key])
+
+
+def test_torch_ref_config1_and_attention(golden):
+    """Config-1 fixture (4-bit, outlier channels) byte for byte, and the dense
+    attention against the numpy oracle's float64 attention."""
+    import torch
+    from oracle import torch_ref as T
+    enc, cb = golden["encode"], golden["codebooks"]
+    x = torch.from_numpy(enc["x_cfg1"].view(np.int16)).view(torch.bfloat16)
+    s = torch.from_numpy(golden["signs"]["s_128_0"])
+    p, n16 = T.encode(x, s, torch.from_numpy(cb["b_128_4"].astype(np.float32)), 4)
+    assert np.array_equal(p.numpy(), enc["packed_cfg1"])
+    assert np.array_equal(n16.view(torch.int16).numpy().view(np.uint16), enc["norms_cfg1"])
+    g = torch.Generator().manual_seed(3)
+    q = torch.randn(2, 8, 128, generator=g)
+    k = torch.randn(2, 2, 50, 128, generator=g)
+    v = torch.randn(2, 2, 50, 128, generator=g)
+    got = T.dense_attention(q, k, v, 128 ** -0.5).numpy()
+    want = O.dense_decode_attention(q.numpy(), k.numpy(), v.numpy(), [50, 50], 128 ** -0.5)
+    assert np.abs(got - want).max() < 1e-5

@@ -9,6 +9,8 @@ import math
 
 import numpy as np
 import pytest
+
+import bench
 import torch
 
 from oracle import tq_oracle as O
@@ -181,7 +183,7 @@ def test_config3_full_size(cuda):
     through the agreement of the default (the single-launch form: B * Hkv = 256
     workgroups of 16 waves) with the split form (4 splits + merge launch)."""
     from fused_turboquant import paged as P
-    cache, q, bt, sl = P.make_config3(cuda)
+    cache, q, bt, sl = bench.make_config3(cuda)
     B, hq, d = q.shape
     assert P.default_splits(B, cache.num_kv_heads, int(sl[0]), hq, d) == 1
     out = P.paged_decode_attention(q, cache.kv_cache, bt, sl, cache.k_quant, cache.v_quant)
@@ -209,3 +211,75 @@ def test_config3_full_size(cuda):
         err = np.abs(a[bsel] - ref[0])
         print(f"[config3 seq {bsel}] max={err.max():.2e} mean={err.mean():.2e}")
         assert err.max() <= 2e-2 and err.mean() <= 2e-3
+
+
+# ---- fp32-operand VALU form (ftq_paged_decode_attention_valu) ----------------
+
+
+def _dense_ref(cache, lens, bt, q, bk, bv, d):
+    """float64 attention over the oracle's decode of the codes and norms the
+    GPU store wrote (read back from the pages), so store ties do not enter."""
+    full = cache.kv_cache.cpu().numpy()
+    kq, vq = cache.k_quant, cache.v_quant
+    B = len(lens)
+    hkv = full.shape[1]
+    S = max(lens)
+    Kd = np.zeros((B, hkv, S, d))
+    Vd = np.zeros((B, hkv, S, d))
+    for b, L in enumerate(lens):
+        if not L:
+            continue
+        kc, vc, kn, vn = O.paged_unpack(full[bt[b].numpy()], d, bk, bv)
+        for h in range(hkv):
+            Kd[b, h, :L] = O.decode(O.pack(kc[:, h].reshape(-1, d)[:L], bk), kn[:, h].reshape(-1)[:L],
+                                    kq.quantizer.levels.cpu().numpy(), kq.rotation.signs.cpu().numpy(), bk, d)
+            Vd[b, h, :L] = O.decode(O.pack(vc[:, h].reshape(-1, d)[:L], bv), vn[:, h].reshape(-1)[:L],
+                                    vq.quantizer.levels.cpu().numpy(), vq.rotation.signs.cpu().numpy(), bv, d)
+    return O.dense_decode_attention(q.float().numpy(), Kd, Vd, lens, 1 / math.sqrt(d))
+
+
+@pytest.mark.parametrize("bk,bv", [(3, 3), (4, 2), (2, 4), (4, 4), (2, 2)])
+@pytest.mark.parametrize("hq,hkv", [(32, 8), (8, 8), (12, 4)])
+@pytest.mark.parametrize("outliers", [False, True])
+def test_decode_attention_fp32_operands(cuda, bk, bv, hq, hkv, outliers):
+    """The fp32 VALU form takes every product in fp32, like the reference, so
+    with a float32 output it matches float64 attention over the oracle's
+    decode of the stored codes to fp32 rounding -- also with keys and values
+    8x the typical norm on 2% of tokens, where the f16-operand kernel needs
+    the bf16-ulp allowance."""
+    from fused_turboquant.paged import PagedTurboQuantCache
+    d, page = 128, 16
+    lens = [0, 1, 17, 33, 100, 515, 1000]
+    B = len(lens)
+    maxp = max((L + page - 1) // page for L in lens)
+    g = torch.Generator().manual_seed(1300 + bk * 100 + bv * 10 + hq + outliers)
+    nblk = B * maxp + 3
+    cache = PagedTurboQuantCache(nblk, page, hkv, d, bk, bv, device=cuda)
+    bt = torch.randperm(nblk, generator=g)[: B * maxp].view(B, maxp).to(torch.int32)
+    _fill(cache, lens, bt, hkv, d, g, cuda, outliers=outliers)
+    q = torch.randn(B, hq, d, generator=g).to(torch.bfloat16)
+    ref = _dense_ref(cache, lens, bt, q, bk, bv, d)
+    sl = torch.tensor(lens, dtype=torch.int32, device=cuda)
+    for splits in (1, 3, 8):
+        out = cache.decode_attention(q.to(cuda), bt.to(cuda), sl, num_splits=splits, operands="fp32",
+                                     out=torch.empty(B, hq, d, device=cuda)).cpu().numpy()
+        err = np.abs(out - ref)
+        print(f"[attn fp32 operands bk={bk} bv={bv} hq={hq} hkv={hkv} outliers={outliers} S={splits}] "
+              f"max={err.max():.2e} mean={err.mean():.2e} (|ref| max {np.abs(ref).max():.1f})")
+        assert np.all(out[0] == 0)
+        assert (err <= 1e-4 + 1e-5 * np.abs(ref)).all()
+        # bf16 output: only the output's rounding (at most 2^-8 of |x|) is added
+        outb = cache.decode_attention(q.to(cuda), bt.to(cuda), sl, num_splits=splits,
+                                      operands="fp32").float().cpu().numpy()
+        errb = np.abs(outb - ref)
+        assert (errb <= 1e-4 + 2.0 ** -8 * np.abs(ref)).all()
+
+
+def test_fp32_operands_rejects_unsupported_shapes(cuda):
+    from fused_turboquant.paged import PagedTurboQuantCache
+    cache = PagedTurboQuantCache(4, 16, 2, 128, 3, 3, device=cuda)
+    q = torch.zeros(1, 16, 128, dtype=torch.bfloat16, device=cuda)  # GQA 8
+    bt = torch.zeros(1, 2, dtype=torch.int32, device=cuda)
+    sl = torch.ones(1, dtype=torch.int32, device=cuda)
+    with pytest.raises(ValueError, match="at most 4 query heads"):
+        cache.decode_attention(q, bt, sl, operands="fp32")

@@ -12,6 +12,8 @@ import math
 
 import numpy as np
 import pytest
+
+import bench
 import torch
 
 from oracle import tq_oracle as O
@@ -141,8 +143,9 @@ def test_bench_shape_full_size(cuda):
     """The benchmark's shape (B=32, Hq=32, Hkv=8, ctx 8192, 512-byte slots,
     1.07 GB of K/V): oracle on two sequences, split-count invariance over all."""
     from fused_turboquant import raw
-    setup = raw.bench_setup(cuda)
+    setup = bench.raw_setup(cuda)
     setup["run"]()
+    bench.check_lean(setup["run"])
     out = setup["out"].float().cpu().numpy()
     cache, bt, sl, q = setup["cache"], setup["bt"], setup["sl"], setup["q"]
     for b in (0, 31):

@@ -75,6 +75,8 @@ def test_store_parity(cuda, d, kb, vb, vrot):
         y = st["y"][ok][diff].astype(np.float64)
         mids = layer.midpoints.cpu().numpy().astype(np.float64)
         dist = np.min(np.abs(y[:, None] - mids[None, :]), axis=1)
+        print(f"[v1 store d={d} kb={kb} vb={vb}] K ties={ties} max "
+              f"{O.tie_ulps(y, mids.astype(np.float32), d).max():.2f} ulp")
         assert dist.max() < TIE
         assert np.all(np.abs(gk[diff].astype(int) - wk[diff].astype(int)) == 1)
     # K norm fp16
