@@ -184,3 +184,13 @@ def test_torch_ref_config1_and_attention(golden):
     got = T.dense_attention(q, k, v, 128 ** -0.5).numpy()
     want = O.dense_decode_attention(q.numpy(), k.numpy(), v.numpy(), [50, 50], 128 ** -0.5)
     assert np.abs(got - want).max() < 1e-5
+
+
+def test_tie_ulps_counts_float32_steps():
+    """tie_ulps measures |u - cut| in float32 ulps of max(|cut|, d^-1/2)."""
+    d = 128
+    cuts = np.array([-0.2, 0.0, 0.15], np.float32)
+    u = np.array([np.float32(0.15) + 3 * np.spacing(np.float32(0.15)),
+                  np.float32(-0.2) - 2 * np.spacing(np.float32(0.2)),
+                  5 * np.spacing(np.float32(d ** -0.5))], np.float64)
+    assert np.allclose(O.tie_ulps(u, cuts, d), [3.0, 2.0, 5.0])

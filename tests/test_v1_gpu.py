@@ -18,7 +18,7 @@ import torch
 from oracle import tq_oracle as O
 
 pytestmark = pytest.mark.gpu
-TIE = 2e-6
+TIE_ULPS = 4  # a code may differ only within 4 float32 ulps of a midpoint (oracle.tie_ulps)
 DT = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}
 
 
@@ -72,12 +72,11 @@ def test_store_parity(cuda, d, kb, vb, vrot):
     diff = gk != wk
     ties = int(diff.sum())
     if ties:
-        y = st["y"][ok][diff].astype(np.float64)
-        mids = layer.midpoints.cpu().numpy().astype(np.float64)
-        dist = np.min(np.abs(y[:, None] - mids[None, :]), axis=1)
-        print(f"[v1 store d={d} kb={kb} vb={vb}] K ties={ties} max "
-              f"{O.tie_ulps(y, mids.astype(np.float32), d).max():.2f} ulp")
-        assert dist.max() < TIE
+        y = st["y"][ok][diff]
+        mids = layer.midpoints.cpu().numpy()
+        worst = O.tie_ulps(y, mids, d).max()
+        print(f"[v1 store d={d} kb={kb} vb={vb}] K ties={ties} max {worst:.2f} ulp")
+        assert worst <= TIE_ULPS
         assert np.all(np.abs(gk[diff].astype(int) - wk[diff].astype(int)) == 1)
     # K norm fp16
     gn = got[blk, off, :, mse:mse + 2].copy().view(np.float16)[..., 0].astype(np.float32)
@@ -286,8 +285,7 @@ def test_store_parity_v_lloyd_max(cuda, kb):
         a, b = gc[blk, off], wc[blk, off]
         diff = a != b
         if diff.any():
-            uu = u[ok][diff].astype(np.float64)
-            assert np.min(np.abs(uu[:, None] - m64[None, :]), axis=1).max() < TIE, name
+            assert O.tie_ulps(u[ok][diff], mids, d).max() <= TIE_ULPS, name
             assert np.all(np.abs(a[diff].astype(int) - b[diff].astype(int)) == 1), name
         print(f"[v1 store lloyd kb={kb}] {name} code ties={int(diff.sum())} of {a.size}")
 
