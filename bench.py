@@ -338,7 +338,10 @@ def v1_store_setup(dev, n_tokens, d, kb, vb, kind="rht", v_rotate=False, hkv=8, 
     vflags = (1 if layer.v_rotate else 0) | (2 if layer.v_lloyd_max else 0)
     args = [k, v, _lib.BF16, n_tokens, hkv, d, layer.midpoints, kb, vb, vflags, slots, cache, nb, bs,
             cache.stride(0), cache.stride(1), cache.stride(2)]
-    if layer.rotation is None:
+    if layer.coeffs is not None:  # block-diagonal strategies: O(B d) per vector
+        run = lean_launch(L.ftq_v1_store_blockdiag, *args, layer.coeffs, layer.coeffs.shape[0],
+                          _lib.stream_ptr(dev))
+    elif layer.rotation is None:
         run = lean_launch(L.ftq_v1_store, *args, _lib.stream_ptr(dev))
     else:
         run = lean_launch(L.ftq_v1_store_rot, *args, layer.rotation, _lib.stream_ptr(dev))
@@ -519,6 +522,7 @@ def main():
                    ("v1_store_rotor_1024x8_d128", 1024, 128, 3, 3, "rotor", False),
                    ("v1_store_iso_full_1024x8_d128", 1024, 128, 3, 3, "iso_full", False),
                    ("v1_store_planar_1024x8_d256", 1024, 256, 3, 3, "planar", False),
+                   ("v1_store_iso_full_1024x8_d256", 1024, 256, 3, 3, "iso_full", False),
                    ("v1_store_config4_chunk", 32768, 128, 4, 2, "rht", True)]
     for name, nt, d, kb, vb, kind, vrot in store_cases:
         if want(name):

@@ -43,6 +43,7 @@
 #include "ftq_merge.h"
 #include "ftq_codec_dev.h"
 #include "ftq_internal.h"
+#include "ftq_v1_dev.h"
 
 #include <cmath>
 #include <mutex>
@@ -53,12 +54,6 @@ float fwht_scale(int d);
 
 typedef unsigned short us2 __attribute__((ext_vector_type(2)));
 
-struct V1Geom {
-  int mse, kps, vdb, raw;
-};
-__host__ __device__ constexpr V1Geom v1_geom(int d, int kb, int vb) {
-  return V1Geom{d * kb / 8, d * kb / 8 + 2, d * vb / 8, d * kb / 8 + 2 + d * vb / 8 + 4};
-}
 
 // ---------------------------------------------------------------------------
 // store
@@ -79,12 +74,6 @@ __device__ __forceinline__ uint32_t packed_bits(const uint8_t* c, int B, int pos
   return n == 32 ? r : (r & ((1u << n) - 1u));
 }
 
-template <int DT>
-__device__ __forceinline__ float round_to_dtype(float x) {
-  if constexpr (DT == BF16) return bf16_bits_to_f32(f32_to_bf16_bits(x));
-  else if constexpr (DT == F16) return f16_bits_to_f32(f32_to_f16_bits(x));
-  else return x;
-}
 
 // x <- x M for a vector spread over 16 lanes, E contiguous elements per lane
 // (M row-major D x D fp32, the rotation of a matrix strategy: planar, rotor,
@@ -1151,25 +1140,22 @@ __global__ __launch_bounds__(256, VB == 2 ? 4 : 2) void v1_attn_g4_kernel(
 // merge_splits_kernel in ftq_merge.h)
 // ---------------------------------------------------------------------------
 
+// dense matrix rotation (a caller's own M): x M through a per-group LDS row
 template <int D>
-static hipError_t v1_launch_store(const void* k, const void* v, int dt, int64_t n, int hkv,
-                                  const float* mids, int kb, int vb, int vrot, const int64_t* slots,
-                                  uint8_t* cache, int64_t nb, int bs, int64_t sb, int64_t sp,
-                                  int64_t sh, const float* rot, hipStream_t st) {
+static hipError_t v1_launch_store_dense(const void* k, const void* v, int dt, int64_t n, int hkv,
+                                        const float* mids, int kb, int vb, int vrot, const int64_t* slots,
+                                        uint8_t* cache, int64_t nb, int bs, int64_t sb, int64_t sp,
+                                        int64_t sh, const float* rot, hipStream_t st) {
   const int64_t nvec = n * hkv;
   int64_t gsz = (nvec + 15) / 16;
   if (gsz > 256 * 16) gsz = 256 * 16;
-  const float rs = fwht_scale(D);
   dim3 grid((unsigned)gsz), block(256);
   if (dt == F32)
-    { if (rot) v1_store_kernel<D, F32, true><<<grid, block, 0, st>>>(k, v, n, hkv, mids, kb, vb, vrot, slots, cache, nb, bs, sb, sp, sh, 1.f, rot);
-      else v1_store_kernel<D, F32><<<grid, block, 0, st>>>(k, v, n, hkv, mids, kb, vb, vrot, slots, cache, nb, bs, sb, sp, sh, rs, nullptr); }
+    v1_store_kernel<D, F32, true><<<grid, block, 0, st>>>(k, v, n, hkv, mids, kb, vb, vrot, slots, cache, nb, bs, sb, sp, sh, 1.f, rot);
   else if (dt == F16)
-    { if (rot) v1_store_kernel<D, F16, true><<<grid, block, 0, st>>>(k, v, n, hkv, mids, kb, vb, vrot, slots, cache, nb, bs, sb, sp, sh, 1.f, rot);
-      else v1_store_kernel<D, F16><<<grid, block, 0, st>>>(k, v, n, hkv, mids, kb, vb, vrot, slots, cache, nb, bs, sb, sp, sh, rs, nullptr); }
+    v1_store_kernel<D, F16, true><<<grid, block, 0, st>>>(k, v, n, hkv, mids, kb, vb, vrot, slots, cache, nb, bs, sb, sp, sh, 1.f, rot);
   else
-    { if (rot) v1_store_kernel<D, BF16, true><<<grid, block, 0, st>>>(k, v, n, hkv, mids, kb, vb, vrot, slots, cache, nb, bs, sb, sp, sh, 1.f, rot);
-      else v1_store_kernel<D, BF16><<<grid, block, 0, st>>>(k, v, n, hkv, mids, kb, vb, vrot, slots, cache, nb, bs, sb, sp, sh, rs, nullptr); }
+    v1_store_kernel<D, BF16, true><<<grid, block, 0, st>>>(k, v, n, hkv, mids, kb, vb, vrot, slots, cache, nb, bs, sb, sp, sh, 1.f, rot);
   return hipGetLastError();
 }
 
@@ -1256,26 +1242,25 @@ extern "C" int64_t ftq_v1_slot_bytes(int d, int key_bits, int value_bits) {
   return v1_geom(d, key_bits, value_bits).raw;
 }
 
+namespace ftq {
+int v1_store_checks(int d, int key_bits, int value_bits, int64_t n_tokens, int num_kv_heads, int64_t num_blocks,
+                    int block_size, int dtype, int v_rotate, int64_t stride_block, int64_t stride_pos,
+                    int64_t stride_head);
+}
+
 extern "C" int ftq_v1_store_rot(const void* key, const void* value, int dtype, int64_t n_tokens,
                             int num_kv_heads, int d, const float* midpoints, int key_bits,
                             int value_bits, int v_rotate, const int64_t* slot_mapping,
                             uint8_t* kv_cache, int64_t num_blocks, int block_size,
                             int64_t stride_block, int64_t stride_pos, int64_t stride_head,
                             const float* rotation, void* stream) {
-  FTQ_REQUIRE(d == 64 || d == 128 || d == 256, "v1 store: head_dim must be 64, 128 or 256");
-  FTQ_REQUIRE(key_bits >= 2 && key_bits <= 4 && value_bits >= 2 && value_bits <= 4,
-              "v1 store: key_bits and value_bits must be 2, 3 or 4");
-  FTQ_REQUIRE(n_tokens >= 0 && num_kv_heads > 0 && num_blocks >= 0 && block_size > 0,
-              "bad token / head / block counts");
-  FTQ_REQUIRE(dtype >= F32 && dtype <= BF16, "dtype must be FTQ_F32, FTQ_F16 or FTQ_BF16");
-  FTQ_REQUIRE(v_rotate >= 0 && v_rotate <= 3, "v_rotate: bit 0 = rotate V, bit 1 = Lloyd-Max V codes");
-  FTQ_REQUIRE(rotation == nullptr || aligned4(rotation), "rotation must be 4-byte aligned");
-  const V1Geom g = v1_geom(d, key_bits, value_bits);
-  FTQ_REQUIRE(stride_head >= g.raw, "stride_head is smaller than the slot bytes (see ftq_v1_slot_bytes)");
-  FTQ_REQUIRE(stride_pos >= stride_head * num_kv_heads && stride_block >= stride_pos * block_size,
-              "kv_cache strides must describe [num_blocks][block_size][num_kv_heads][slot]");
-  FTQ_REQUIRE(stride_head % 4 == 0 && stride_pos % 4 == 0 && stride_block % 4 == 0,
-              "kv_cache strides must be multiples of 4 bytes");
+  if (rotation == nullptr)
+    return ftq_v1_store(key, value, dtype, n_tokens, num_kv_heads, d, midpoints, key_bits, value_bits, v_rotate,
+                        slot_mapping, kv_cache, num_blocks, block_size, stride_block, stride_pos, stride_head, stream);
+  const int rc = v1_store_checks(d, key_bits, value_bits, n_tokens, num_kv_heads, num_blocks, block_size, dtype,
+                                 v_rotate, stride_block, stride_pos, stride_head);
+  if (rc != FTQ_OK) return rc;
+  FTQ_REQUIRE(aligned4(rotation), "rotation must be 4-byte aligned");
   if (n_tokens == 0) return FTQ_OK;
   FTQ_REQUIRE(key && value && midpoints && slot_mapping && kv_cache, "null pointer argument");
   FTQ_REQUIRE(aligned16(key) && aligned16(value), "key/value must be 16-byte aligned");
@@ -1283,21 +1268,12 @@ extern "C" int ftq_v1_store_rot(const void* key, const void* value, int dtype, i
   hipStream_t st = (hipStream_t)stream;
   hipError_t e;
   if (d == 64)
-    e = v1_launch_store<64>(key, value, dtype, n_tokens, num_kv_heads, midpoints, key_bits, value_bits, v_rotate, slot_mapping, kv_cache, num_blocks, block_size, stride_block, stride_pos, stride_head, rotation, st);
+    e = v1_launch_store_dense<64>(key, value, dtype, n_tokens, num_kv_heads, midpoints, key_bits, value_bits, v_rotate, slot_mapping, kv_cache, num_blocks, block_size, stride_block, stride_pos, stride_head, rotation, st);
   else if (d == 128)
-    e = v1_launch_store<128>(key, value, dtype, n_tokens, num_kv_heads, midpoints, key_bits, value_bits, v_rotate, slot_mapping, kv_cache, num_blocks, block_size, stride_block, stride_pos, stride_head, rotation, st);
+    e = v1_launch_store_dense<128>(key, value, dtype, n_tokens, num_kv_heads, midpoints, key_bits, value_bits, v_rotate, slot_mapping, kv_cache, num_blocks, block_size, stride_block, stride_pos, stride_head, rotation, st);
   else
-    e = v1_launch_store<256>(key, value, dtype, n_tokens, num_kv_heads, midpoints, key_bits, value_bits, v_rotate, slot_mapping, kv_cache, num_blocks, block_size, stride_block, stride_pos, stride_head, rotation, st);
+    e = v1_launch_store_dense<256>(key, value, dtype, n_tokens, num_kv_heads, midpoints, key_bits, value_bits, v_rotate, slot_mapping, kv_cache, num_blocks, block_size, stride_block, stride_pos, stride_head, rotation, st);
   return hip_status(e);
-}
-
-extern "C" int ftq_v1_store(const void* key, const void* value, int dtype, int64_t n_tokens,
-                            int num_kv_heads, int d, const float* midpoints, int key_bits,
-                            int value_bits, int v_rotate, const int64_t* slot_mapping,
-                            uint8_t* kv_cache, int64_t num_blocks, int block_size,
-                            int64_t stride_block, int64_t stride_pos, int64_t stride_head,
-                            void* stream) {
-  return ftq_v1_store_rot(key, value, dtype, n_tokens, num_kv_heads, d, midpoints, key_bits, value_bits, v_rotate, slot_mapping, kv_cache, num_blocks, block_size, stride_block, stride_pos, stride_head, nullptr, stream);
 }
 
 extern "C" int64_t ftq_v1_workspace_bytes(int batch, int num_q_heads, int d, int num_splits) {

@@ -45,6 +45,8 @@ _SIG = {
                                     "i32", "i32", "vp", "i64", "vp", "i32", "vp", "vp"],
     "ftq_v1_store_rot": ["vp", "vp", "i32", "i64", "i32", "i32", "vp", "i32", "i32", "i32", "vp", "vp",
                          "i64", "i32", "i64", "i64", "i64", "vp", "vp"],
+    "ftq_v1_store_blockdiag": ["vp", "vp", "i32", "i64", "i32", "i32", "vp", "i32", "i32", "i32", "vp", "vp",
+                               "i64", "i32", "i64", "i64", "i64", "vp", "i32", "vp"],
     "ftq_v1_decode_attention_rot": ["vp", "i32", "vp", "i64", "i32", "i64", "i64", "i64", "vp", "i32",
                                     "vp", "vp", "i32", "i32", "i32", "i32", "vp", "i32", "i32", "f32",
                                     "i32", "i32", "vp", "i64", "vp", "i32", "vp", "vp", "vp"],
@@ -285,12 +287,15 @@ def _rotation_arg(rotation: torch.Tensor, d: int, dev) -> torch.Tensor:
 def v1_store(key: torch.Tensor, value: torch.Tensor, kv_cache: torch.Tensor,
              slot_mapping: torch.Tensor, midpoints: torch.Tensor, key_bits: int,
              value_bits: int, v_rotate: bool = False, v_lloyd_max: bool = False,
-             rotation: torch.Tensor | None = None) -> None:
+             rotation: torch.Tensor | None = None, coeffs: torch.Tensor | None = None) -> None:
     """Quantise ``key``/``value`` [n, Hkv, d] into their slots (``slot_mapping`` [n]
     int64; negative entries are skipped).  ``v_lloyd_max`` (implies
     ``v_rotate``): 4-bit V takes Lloyd-Max codes against the K midpoints and its
     norm in the scale field (reference ``triton_inkernel_store.py:159-200``);
-    other V widths keep the uniform codes."""
+    other V widths keep the uniform codes.  ``coeffs`` ([B, d] float32, B in
+    2/3/4): a block-diagonal rotation given by its block coefficients
+    (``block_coeffs``), O(B d) per vector (reference ``_fused_store_block_diag``,
+    ``triton_inkernel_store.py:649-860``); ``rotation``: any d x d matrix, O(d^2)."""
     n, hkv, d = key.shape
     _check_bits(d, key_bits, value_bits)
     if value.shape != key.shape:
@@ -315,9 +320,14 @@ def v1_store(key: torch.Tensor, value: torch.Tensor, kv_cache: torch.Tensor,
     args = (k.data_ptr(), v.data_ptr(), _lib.dtype_code(k.dtype), n, hkv, d, mids.data_ptr(),
             key_bits, value_bits, _v_flags(v_rotate, v_lloyd_max), slot_mapping.contiguous().data_ptr(),
             kv_cache.data_ptr(), nb, bs, sb, sp, sh)
-    if rotation is None:
+    if coeffs is not None:  # block-diagonal strategy: planar (B=2), rotor (3), iso (4)
+        if coeffs.dim() != 2 or coeffs.shape[1] != d or coeffs.shape[0] not in (2, 3, 4):
+            raise ValueError("coeffs must be [B, head_dim] with B in 2, 3, 4")
+        cf = coeffs.to(device=dev, dtype=torch.float32).contiguous()
+        _lib.check(L.ftq_v1_store_blockdiag(*args, cf.data_ptr(), cf.shape[0], _lib.stream_ptr(dev)))
+    elif rotation is None:
         _lib.check(L.ftq_v1_store(*args, _lib.stream_ptr(dev)))
-    else:  # a matrix strategy (planar, rotor, iso): x M in the kernel
+    else:  # any d x d matrix: x M in the kernel
         rot = _rotation_arg(rotation, d, dev)
         _lib.check(L.ftq_v1_store_rot(*args, rot.data_ptr(), _lib.stream_ptr(dev)))
 
@@ -424,12 +434,15 @@ class TurboQuantV1Layer:
         # rotation strategy (TURBOQUANT_KIND): rht = the kernels' own H/sqrt(d);
         # planar = a matrix x M applied in the kernels; a caller's matrix the same
         self.kind = kind
+        self.coeffs = None  # [B, d] block coefficients of a block-diagonal strategy (the store's form)
         if rotation is not None:
             self.rotation = rotation.to(device=device, dtype=torch.float32).contiguous()
         elif kind == "rht":
             self.rotation = None
         elif kind in BLOCK_SIZES:
-            self.rotation = rotation_matrix(kind, head_dim, device=device)
+            m = rotation_matrix(kind, head_dim)
+            self.rotation = m.to(device)
+            self.coeffs = block_coeffs(m, BLOCK_SIZES[kind]).to(device)
         else:
             raise ValueError(f"rotation kind {kind!r}: rht, planar, rotor, iso_fast, iso_full "
                              "or an explicit matrix")
@@ -440,7 +453,8 @@ class TurboQuantV1Layer:
 
     def store(self, key, value, kv_cache, slot_mapping) -> None:
         v1_store(key, value, kv_cache, slot_mapping, self.midpoints, self.key_bits,
-                 self.value_bits, self.v_rotate, self.v_lloyd_max, rotation=self.rotation)
+                 self.value_bits, self.v_rotate, self.v_lloyd_max,
+                 rotation=self.rotation if self.coeffs is None else None, coeffs=self.coeffs)
 
     def decode(self, query, kv_cache, block_table, seq_lens, **kw) -> torch.Tensor:
         return v1_decode_attention(query, kv_cache, block_table, seq_lens, self.centroids,

@@ -152,6 +152,24 @@ int ftq_paged_decode_attention(const void* query, int q_dtype, const uint8_t* kv
                                int bits_k, int bits_v, float scale, int num_splits, void* workspace,
                                int64_t workspace_bytes, void* out, int out_dtype, void* stream);
 
+/*
+ * ftq_paged_decode_attention with every product in fp32 on the VALU (fp32
+ * level tables, fp32 rotated query, fp32 weights times norms), the
+ * arithmetic of the reference's flash_decode_compressed
+ * (kernels/triton_flash_decode.py:66-221); same arguments and semantics.
+ * Always the split form (stage 1 into the workspace, then the merge + inverse
+ * RHT launch).  d = 128 and at most 4 query heads per kv head.  About 2.3x the
+ * time of the default matrix-core form at BASELINE config 3.
+ */
+int ftq_paged_decode_attention_valu(const void* query, int q_dtype, const uint8_t* kv_cache,
+                                    const int32_t* block_table, const int32_t* seq_lens, int batch,
+                                    int num_q_heads, int num_kv_heads, int d, int page_size,
+                                    int max_blocks_per_seq, int64_t num_blocks, const float* k_signs,
+                                    const float* v_signs, const float* k_levels,
+                                    const float* v_levels, int bits_k, int bits_v, float scale,
+                                    int num_splits, void* workspace, int64_t workspace_bytes, void* out,
+                                    int out_dtype, void* stream);
+
 /* ---- vLLM v1 TURBOQUANT slot format ------------------------------------
  * kv_cache uint8 [num_blocks][block_size][num_kv_heads][slot] (strides in
  * bytes); per (token, kv head) slot:
@@ -200,6 +218,26 @@ int ftq_v1_store_rot(const void* key, const void* value, int dtype, int64_t n_to
                      int v_rotate, const int64_t* slot_mapping, uint8_t* kv_cache,
                      int64_t num_blocks, int block_size, int64_t stride_block, int64_t stride_pos,
                      int64_t stride_head, const float* rotation, void* stream);
+
+/*
+ * ftq_v1_store for the block-diagonal rotation strategies (planar B = 2,
+ * rotor B = 3, iso_fast / iso_full B = 4): K (and V when v_rotate) rotated
+ * by x M with M given by its coefficients coeffs[B][d] (float32, device),
+ * coeffs[j][e] = M[(e / B) B + j][e] (0 where that row is past d); K is
+ * normalised by multiplying with 1 / (norm + 1e-8) and y[e] =
+ * sum_j x[(e / B) B + j] coeffs[j][e] is formed by fused multiply-adds in
+ * j order.  O(B d) work per vector.  Replaces _launch_block_diag /
+ * _fused_store_block_diag (vllm_plugin/triton_inkernel_store.py:649-860)
+ * behind BlockDiagonalRotationStrategy.launch_store
+ * (vllm_plugin/rotation/matrix.py:126-148) and the V pre-rotation of
+ * _launch_store (v1_backend.py:736-740).
+ */
+int ftq_v1_store_blockdiag(const void* key, const void* value, int dtype, int64_t n_tokens,
+                           int num_kv_heads, int d, const float* midpoints, int key_bits,
+                           int value_bits, int v_rotate, const int64_t* slot_mapping,
+                           uint8_t* kv_cache, int64_t num_blocks, int block_size,
+                           int64_t stride_block, int64_t stride_pos, int64_t stride_head,
+                           const float* coeffs, int block, void* stream);
 
 /* Workspace bytes ftq_v1_decode_attention needs: batch*Hq*splits*(d+1)*4. */
 int64_t ftq_v1_workspace_bytes(int batch, int num_q_heads, int d, int num_splits);

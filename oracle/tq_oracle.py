@@ -403,7 +403,27 @@ def v1_quantize_k(y: np.ndarray, midpoints: np.ndarray) -> np.ndarray:
     return np.searchsorted(m, np.asarray(y, np.float32), side="right").astype(np.uint8)
 
 
-def v1_k_rotate(k: np.ndarray, rotation=None):
+def v1_blockdiag_rotate(x: np.ndarray, coeffs: np.ndarray, B: int) -> np.ndarray:
+    """x M for a block-diagonal M given by coeffs[j][e] = M[(e // B) B + j][e]:
+    y[e] = fma(x_{B-1}, c_{B-1}, ... fma(x_1, c_1, x_0 c_0)) in float32 with
+    x_j = x[(e // B) B + j] (reference _fused_store_block_diag,
+    triton_inkernel_store.py:727-742).  Each fused step is the exact product
+    plus the sum formed in float64, then rounded to float32."""
+    x = np.asarray(x, np.float32)
+    c = np.asarray(coeffs, np.float32)
+    d = x.shape[-1]
+    e = np.arange(d)
+    y = None
+    for j in range(B):
+        src = (e // B) * B + j
+        ok = src < d
+        xp = np.where(ok, x[..., np.minimum(src, d - 1)], np.float32(0)).astype(np.float64)
+        prod = xp * c[j].astype(np.float64)
+        y = prod.astype(np.float32) if j == 0 else (prod + y.astype(np.float64)).astype(np.float32)
+    return y
+
+
+def v1_k_rotate(k: np.ndarray, rotation=None, blockdiag=None):
     """K path before the quantiser (triton_inkernel_store.py:406-430):
     norm = sqrt(sum k^2 + 1e-16); x = k / (norm + 1e-8); y = H x / sqrt(d)
     (Sylvester butterflies, no random signs).  Returns (y f32, norm f32)."""
@@ -412,7 +432,11 @@ def v1_k_rotate(k: np.ndarray, rotation=None):
     k64 = k.astype(np.float64)
     norm = np.sqrt(np.sum(k64 * k64, axis=-1) + 1e-16).astype(np.float32)
     x = (k / (norm[..., None] + np.float32(1e-8))).astype(np.float32)
-    if rotation is None:
+    if blockdiag is not None:  # k * (1 / (norm + 1e-8)), then the block products (:718-742)
+        inv = (np.float32(1.0) / (norm + np.float32(1e-8))).astype(np.float32)
+        x = (k * inv[..., None]).astype(np.float32)
+        y = v1_blockdiag_rotate(x, *blockdiag)
+    elif rotation is None:
         y = (fwht_unscaled(x) * fwht_scale(d)).astype(np.float32)
     else:  # a matrix strategy: x M (MatrixRotationStrategy.rotate_for_store, rotation/matrix.py:44-45)
         y = (x.astype(np.float64) @ np.asarray(rotation, np.float64)).astype(np.float32)
@@ -469,7 +493,7 @@ def v1_quantize_v_lloyd(v: np.ndarray, midpoints: np.ndarray):
 
 def v1_store(key: np.ndarray, value: np.ndarray, slot_mapping: np.ndarray, kv_cache: np.ndarray,
              midpoints: np.ndarray, kb: int, vb: int, v_rotate: bool = False,
-             value_dtype: str = "f32", v_lloyd_max: bool = False, rotation=None):
+             value_dtype: str = "f32", v_lloyd_max: bool = False, rotation=None, blockdiag=None):
     """Write [N, H, d] float32 K/V (already converted from their dtype) into
     ``kv_cache`` uint8[nb, bs, H, slot] in place.  Negative slots are skipped
     (triton_inkernel_store.py:394-395).  With ``v_rotate`` V is first rotated
@@ -477,6 +501,8 @@ def v1_store(key: np.ndarray, value: np.ndarray, slot_mapping: np.ndarray, kv_ca
     With ``v_lloyd_max`` and 4-bit V, V takes Lloyd-Max codes against the K
     midpoints, its norm goes in the scale field and the min field is 0
     (triton_inkernel_store.py:159-200); other V widths keep the uniform codes.
+    ``blockdiag`` = (coeffs [B, d], B): a block-diagonal strategy, K and the
+    rotated V formed by v1_blockdiag_rotate.
 
     Returns a dict of per-(token, head) intermediates for tie accounting.
     """
@@ -486,11 +512,15 @@ def v1_store(key: np.ndarray, value: np.ndarray, slot_mapping: np.ndarray, kv_ca
     nb, bs, Hc, slot = kv_cache.shape
     assert Hc == H
     g = v1_geometry(d, kb, vb)
-    y, norm = v1_k_rotate(key, rotation)
+    y, norm = v1_k_rotate(key, rotation, blockdiag)
     kcodes = v1_quantize_k(y, midpoints)
     if v_rotate:
-        vr = (fwht_unscaled(value) * fwht_scale(d)) if rotation is None else \
-            np.asarray(value, np.float64) @ np.asarray(rotation, np.float64)
+        if blockdiag is not None:
+            vr = v1_blockdiag_rotate(value, *blockdiag)
+        elif rotation is None:
+            vr = fwht_unscaled(value) * fwht_scale(d)
+        else:
+            vr = np.asarray(value, np.float64) @ np.asarray(rotation, np.float64)
         value = v1_round_dtype(vr.astype(np.float32), value_dtype)
     if v_lloyd_max and vb == 4:
         vq, sc, t = v1_quantize_v_lloyd(value, midpoints)

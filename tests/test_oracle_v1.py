@@ -421,3 +421,26 @@ def test_rotation_matrices_equal_the_reference(kind):
         assert np.array_equal(m.numpy(), z[k]), k
         c = v1.block_coeffs(m, v1.BLOCK_SIZES[kind])
         assert np.array_equal(c.numpy(), z[k + "_coeffs"]), k
+
+
+@pytest.mark.parametrize("kind", ["planar", "rotor", "iso_fast", "iso_full"])
+def test_blockdiag_rotate_equals_matrix_product(kind):
+    """v1_blockdiag_rotate (the block coefficients' fused multiply-add chain)
+    equals x M of the dense matrix to within 2 float32 ulps of the result's
+    scale, and exactly where a block holds a single nonzero per column."""
+    from fused_turboquant import v1
+    rng = np.random.default_rng(7)
+    for d in (64, 128, 256):
+        m = v1.rotation_matrix(kind, d)
+        B = v1.BLOCK_SIZES[kind]
+        cf = v1.block_coeffs(m, B).numpy()
+        x = rng.standard_normal((40, d)).astype(np.float32)
+        got = O.v1_blockdiag_rotate(x, cf, B)
+        want = x.astype(np.float64) @ m.numpy().astype(np.float64)
+        scale = np.abs(x).max(axis=-1, keepdims=True) * B
+        assert np.all(np.abs(got - want) <= 2 * np.spacing(scale.astype(np.float32)))
+    cf = np.zeros((3, 12), np.float32)  # the identity with 3x3 blocks: coefficient 1 at j = e mod 3
+    for e in range(12):
+        cf[e % 3, e] = 1.0
+    x = rng.standard_normal((5, 12)).astype(np.float32)
+    assert np.array_equal(O.v1_blockdiag_rotate(x, cf, 3), x)

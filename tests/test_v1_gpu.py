@@ -349,20 +349,62 @@ def test_decode_parity_v_lloyd_max(cuda, kb, hq, hkv, splits):
 
 
 @pytest.mark.parametrize("kind", ["planar", "rotor", "iso_fast", "iso_full"])
+@pytest.mark.parametrize("d", [64, 128, 256])
+@pytest.mark.parametrize("kb,vb", [(4, 2), (3, 3), (2, 4)])
+def test_store_parity_blockdiag(cuda, kind, d, kb, vb):
+    """Block-diagonal store (planar / rotor / iso through their [B, d]
+    coefficients; reference _fused_store_block_diag,
+    triton_inkernel_store.py:649-860) against the oracle's restatement of the
+    same fp32 arithmetic: K codes equal except within 4 ulps of a midpoint, K
+    norms within 1e-3, V (rotated by the same blocks, rounded to bf16, min/max
+    coded) byte for byte."""
+    from fused_turboquant import v1
+    bs, hkv, nb = 16, 4, 8
+    n = nb * bs - 3
+    g = torch.Generator().manual_seed(41 + kb + d)
+    layer = v1.TurboQuantV1Layer(d, kb, vb, v_rotate=True, kind=kind, device=cuda)
+    B = v1.BLOCK_SIZES[kind]
+    cf = layer.coeffs.cpu().numpy()
+    k, v = _kv(g, n, hkv, d, torch.bfloat16, outliers=True)
+    slots = torch.randperm(nb * bs, generator=g)[:n]
+    slots[5] = -1
+    cache = torch.zeros(layer.kv_cache_shape(nb, bs, hkv), dtype=torch.uint8, device=cuda)
+    layer.store(k.to(cuda), v.to(cuda), cache, slots.to(cuda))
+    got = cache.cpu().numpy()
+    want = np.zeros_like(got)
+    mids = layer.midpoints.cpu().numpy()
+    st = O.v1_store(k.float().numpy(), v.float().numpy(), slots.numpy(), want, mids, kb, vb,
+                    v_rotate=True, value_dtype="bf16", blockdiag=(cf, B))
+    geo = O.v1_geometry(d, kb, vb)
+    sl = slots.numpy()
+    ok = sl >= 0
+    blk, off = sl[ok] // bs, sl[ok] % bs
+    assert np.array_equal(got[..., geo["kps"]:], want[..., geo["kps"]:])  # V codes, scale, min, padding
+    gk = O.unpack(got[blk, off, :, :geo["mse"]], kb, d)
+    wk = st["kcodes"][ok]
+    diff = gk != wk
+    worst = O.tie_ulps(st["y"][ok][diff], mids, d).max() if diff.any() else 0.0
+    print(f"[v1 {kind} store d={d} kb={kb} vb={vb}] K ties={int(diff.sum())} max {worst:.2f} ulp")
+    assert worst <= TIE_ULPS
+    assert np.all(np.abs(gk[diff].astype(int) - wk[diff].astype(int)) == 1)
+    gn = got[blk, off, :, geo["mse"]:geo["kps"]].copy().view(np.float16)[..., 0].astype(np.float32)
+    wn = want[blk, off, :, geo["mse"]:geo["kps"]].copy().view(np.float16)[..., 0].astype(np.float32)
+    assert np.all(np.abs(gn - wn) <= 1e-3 * np.abs(wn))
+
+
 @pytest.mark.parametrize("kb,vb", [(4, 2), (3, 3)])
-def test_store_parity_planar_matrix(cuda, kb, vb, kind):
-    """Matrix-strategy store (planar, x M in the kernel; reference
-    triton_inkernel_store.py:459-541 behind rotation/matrix.py:50-70) against
-    the oracle's x M in float64: K codes equal except where the rotated unit
-    vector sits within 1e-5 of a midpoint (the kernel's fp32 product is
-    rounded differently), K norms within 1e-3, V (rotated by M, rounded to
-    bf16, min/max coded) within one code step."""
+def test_store_parity_dense_matrix(cuda, kb, vb):
+    """A caller's own d x d rotation (a seeded random orthogonal matrix) through
+    the dense in-kernel product (ftq_v1_store_rot) against the oracle's x M in
+    float64: K codes equal except where the rotated unit vector sits within
+    1e-5 of a midpoint (the kernel's fp32 sum of d products is rounded
+    differently), K norms within 1e-3, V within one code step."""
     from fused_turboquant import v1
     d, bs, hkv, nb = 128, 16, 4, 8
     n = nb * bs
-    g = torch.Generator().manual_seed(41 + kb)
-    layer = v1.TurboQuantV1Layer(d, kb, vb, v_rotate=True, kind=kind, device=cuda)
-    M = layer.rotation.cpu().numpy()
+    g = torch.Generator().manual_seed(45 + kb)
+    M = torch.linalg.qr(torch.randn(d, d, generator=g, dtype=torch.float64))[0].to(torch.float32)
+    layer = v1.TurboQuantV1Layer(d, kb, vb, v_rotate=True, rotation=M, device=cuda)
     k, v = _kv(g, n, hkv, d, torch.bfloat16)
     slots = torch.randperm(nb * bs, generator=g)[:n]
     cache = torch.zeros(layer.kv_cache_shape(nb, bs, hkv), dtype=torch.uint8, device=cuda)
@@ -371,15 +413,15 @@ def test_store_parity_planar_matrix(cuda, kb, vb, kind):
     want = np.zeros_like(got)
     mids = layer.midpoints.cpu().numpy()
     O.v1_store(k.float().numpy(), v.float().numpy(), slots.numpy(), want, mids, kb, vb,
-               v_rotate=True, value_dtype="bf16", rotation=M)
+               v_rotate=True, value_dtype="bf16", rotation=M.numpy())
     kg, kng, vg, scg, zg = O.v1_unpack(got, d, kb, vb)
     kw, knw, vw, scw, zw = O.v1_unpack(want, d, kb, vb)
-    y, _ = O.v1_k_rotate(k.float().numpy(), M)
+    y, _ = O.v1_k_rotate(k.float().numpy(), M.numpy())
     blk, off = slots.numpy() // bs, slots.numpy() % bs
     dk = kg[blk, off].astype(int) - kw[blk, off].astype(int)
     near = np.min(np.abs(y[..., None] - mids[None, None, None, :]), axis=-1) < 1e-5
     bad = (dk != 0) & ~((np.abs(dk) == 1) & near)
-    print(f"[v1 {kind} store kb={kb} vb={vb}] K code ties={(dk != 0).sum()} of {dk.size}")
+    print(f"[v1 dense store kb={kb} vb={vb}] K code ties={(dk != 0).sum()} of {dk.size}")
     assert not bad.any()
     kn_g, kn_w = kng[blk, off].astype(np.float64), knw[blk, off].astype(np.float64)
     assert np.abs(kn_g - kn_w).max() <= 1e-3 * np.abs(kn_w).max()
@@ -415,7 +457,7 @@ def test_decode_parity_planar_matrix(cuda, kb, vb, hq, hkv, kind):
     q = torch.randn(B, hq, d, generator=g).to(torch.bfloat16)
     sl = torch.tensor(lens, dtype=torch.int32)
     ks = torch.tensor(starts, dtype=torch.int32)
-    for splits in (1, 5):
+    for splits in (1, 5, 16):  # 16: the 4-wave-per-row merge with the o M^T un-rotation
         out = v1.v1_decode_attention(q.to(cuda), torch.from_numpy(cache).to(cuda), bt.to(cuda), sl.to(cuda),
                                      torch.from_numpy(c).to(cuda), kb, vb, v_rotate=True, kv_start=ks.to(cuda),
                                      num_splits=splits, rotation=torch.from_numpy(M).to(cuda))
@@ -424,3 +466,41 @@ def test_decode_parity_planar_matrix(cuda, kb, vb, hq, hkv, kind):
         got = out.float().cpu().numpy()
         assert not got[0].any()
         _check_attn(got, want, f"v1 {kind} kb={kb} vb={vb} hq={hq} hkv={hkv} S={splits}")
+
+
+@pytest.mark.parametrize("kind", ["planar", "rotor", "iso_full"])
+@pytest.mark.parametrize("hq,hkv", [(16, 4), (8, 1)])
+def test_decode_parity_v_lloyd_max_matrix(cuda, kind, hq, hkv):
+    """Lloyd-Max V with a matrix strategy: the general kernel's VLM form with
+    q M in its prologue and o M^T in the merge, against the oracle's float64
+    attention over the same cache bytes (written by the oracle with the same
+    M), 1, 5 and 16 splits."""
+    from fused_turboquant import v1
+    d, kb, vb, bs, nb = 128, 4, 4, 16, 48
+    g = torch.Generator().manual_seed(950 + hq + hkv)
+    M = v1.rotation_matrix(kind, d).numpy()
+    slot = max(v1.slot_size(d, kb, vb), 128)
+    cache = np.zeros((nb, bs, hkv, slot), np.uint8)
+    k, v = _kv(g, nb * bs, hkv, d, torch.bfloat16, outliers=True)
+    c = v1.default_centroids(d, kb).numpy()
+    slots = torch.randperm(nb * bs, generator=g).numpy()
+    O.v1_store(k.float().numpy(), v.float().numpy(), slots, cache, O.v1_midpoints(c), kb, vb,
+               v_rotate=True, value_dtype="bf16", v_lloyd_max=True, rotation=M)
+    lens = [0, 1, 17, 100, 257, 700]
+    starts = [0, 0, 5, 40, 0, 63]
+    B = len(lens)
+    bt = torch.randint(0, nb, (B, 48), generator=g, dtype=torch.int32)
+    q = torch.randn(B, hq, d, generator=g).to(torch.bfloat16)
+    sl = torch.tensor(lens, dtype=torch.int32)
+    ks = torch.tensor(starts, dtype=torch.int32)
+    want = O.v1_decode_attention(q.float().numpy(), cache, bt.numpy(), sl.numpy(), c, kb, vb,
+                                 1 / math.sqrt(d), kv_start=ks.numpy(), v_rotate=True, v_lloyd_max=True,
+                                 rotation=M)
+    for splits in (1, 5, 16):
+        out = v1.v1_decode_attention(q.to(cuda), torch.from_numpy(cache).to(cuda), bt.to(cuda), sl.to(cuda),
+                                     torch.from_numpy(c).to(cuda), kb, vb, v_rotate=True, v_lloyd_max=True,
+                                     kv_start=ks.to(cuda), num_splits=splits,
+                                     rotation=torch.from_numpy(M).to(cuda))
+        got = out.float().cpu().numpy()
+        assert not got[0].any()
+        _check_attn(got, want, f"v1 lloyd {kind} hq={hq} hkv={hkv} S={splits}")
