@@ -61,7 +61,18 @@ int64_t paged_sub_bytes(int d, int bk, int bv) {
 }
 
 // ---------------------------------------------------------------------------
-// store: encode K and V of n tokens x Hkv heads and scatter into the pages
+// store: encode K and V of n tokens x Hkv heads and scatter into the pages.
+// One wave per (group of 16 consecutive input tokens, kv head); a vector is
+// encoded by 16 lanes, 4 at a time.  K codes, K and V norms are per token and
+// written directly.  V codes go to the lane-major chunks, where 4 tokens share
+// each chunk's words:
+//   * a group whose 16 tokens fill one whole 16-token sub-block in order (a
+//     prefill: slot_mapping[16 g + j] = S + j, S a multiple of 16) stages the
+//     16 tokens' V codes in LDS and writes every chunk whole, with plain
+//     stores;
+//   * any other group (decode steps, ragged tails, scattered slots) merges
+//     each token's bits into the chunk words with atomic and / or, which is
+//     correct for any slot mapping.
 // ---------------------------------------------------------------------------
 template <int D, int BK, int BV, int DT>
 __global__ __launch_bounds__(256) void paged_store_kernel(
@@ -72,9 +83,10 @@ __global__ __launch_bounds__(256) void paged_store_kernel(
     int64_t num_blocks, float scale) {
   using Gm = PagedGeom<D, BK, BV>;
   constexpr int E = D / 16, LPV = 16;
-  __shared__ uint8_t vcode[16][D];
-  const int lane = threadIdx.x & 15;
-  const int grp = threadIdx.x >> 4;
+  constexpr int NDW = Gm::VLANE / 4;  // dwords of one lane chunk
+  __shared__ uint8_t vcode[4][16][D];  // per wave: the V codes of its group's 16 tokens
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int l16 = lane & 15, sub = lane >> 4;
 
   float kb[(1 << BK) - 1], vb[(1 << BV) - 1];
 #pragma unroll
@@ -84,82 +96,106 @@ __global__ __launch_bounds__(256) void paged_store_kernel(
   float ks[E], vs[E];
 #pragma unroll
   for (int i = 0; i < E; ++i) {
-    ks[i] = ksigns[lane * E + i];
-    vs[i] = vsigns[lane * E + i];
+    ks[i] = ksigns[l16 * E + i];
+    vs[i] = vsigns[l16 * E + i];
   }
   const int nsub = page_size / 16;
-  const int64_t nvec = n_tokens * hkv * 2;  // (token, head, K|V)
+  const int64_t n_groups = (n_tokens + 15) / 16;
+  const int64_t items = n_groups * hkv;
 
-  for (int64_t base = (int64_t)blockIdx.x * 16; base < nvec; base += (int64_t)gridDim.x * 16) {
-    const int64_t gv = base + grp;
-    bool active = gv < nvec;
-    const bool is_v = (gv & 1) != 0;
-    const int64_t th = gv >> 1;
-    const int64_t tok = active ? th / hkv : 0;
-    const int head = active ? (int)(th % hkv) : 0;
-    const int64_t slot = active ? slot_mapping[tok] : -1;
-    active = active && slot >= 0 && slot / page_size < num_blocks;
-    uint8_t* sb = nullptr;
-    int tt = 0;
-    if (active) {
-      const int64_t blk = slot / page_size;
-      const int off = (int)(slot % page_size);
-      tt = off & 15;
-      sb = cache + (((blk * hkv + head) * nsub) + (off >> 4)) * (int64_t)Gm::SUB;
-      float y[E];
-      uint32_t c[E];
-      const int64_t eoff = (tok * hkv + head) * D + lane * E;
-      if (!is_v) {
+  for (int64_t item = (int64_t)blockIdx.x * 4 + wave; item < items; item += (int64_t)gridDim.x * 4) {
+    const int64_t grp = item / hkv;
+    const int head = (int)(item - grp * hkv);
+    const int64_t t0 = grp * 16;
+    // whole-sub-block group?  (lanes l, l + 16, l + 32, l + 48 check token t0 + l)
+    const int64_t sl = (t0 + l16 < n_tokens) ? slot_mapping[t0 + l16] : -1;
+    const int64_t s0 = ((int64_t)__builtin_amdgcn_readfirstlane((int)(sl >> 32)) << 32) |
+                       (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)sl);
+    const bool lane_ok = s0 >= 0 && (s0 & 15) == 0 && sl == s0 + l16 && s0 / page_size < num_blocks;
+    const bool whole = __builtin_amdgcn_ballot_w64(lane_ok) == ~0ull;
+
+#pragma unroll 1
+    for (int p = 0; p < 4; ++p) {
+      const int tt = 4 * p + sub;  // token of the group this 16-lane vector encodes
+      const int64_t tok = t0 + tt;
+      const int64_t slot = tok < n_tokens ? slot_mapping[tok] : -1;
+      const bool active = slot >= 0 && slot / page_size < num_blocks;
+      if (active) {  // uniform over the vector's 16 lanes
+        const int64_t blk = slot / page_size;
+        const int off = (int)(slot - blk * page_size);
+        const int ts = off & 15;
+        uint8_t* sbp = cache + (((blk * hkv + head) * nsub) + (off >> 4)) * (int64_t)Gm::SUB;
+        const int64_t eoff = (tok * hkv + head) * D + l16 * E;
+        float y[E];
+        uint32_t c[E];
         load_elems<DT, E>(key, eoff, y);
-        const float nrm = encode_core<E, LPV, BK>(y, ks, kb, scale, lane, c);
-        pack_store<E, BK>(c, sb + tt * Gm::KTOK, lane);
-        if (lane == 0)
-          reinterpret_cast<uint16_t*>(sb + Gm::KNORM)[tt] = (uint16_t)f32_to_f16_bits(nrm);
-      } else {
+        const float kn = encode_core<E, LPV, BK>(y, ks, kb, scale, l16, c);
+        pack_store<E, BK>(c, sbp + ts * Gm::KTOK, l16);
         load_elems<DT, E>(value, eoff, y);
-        const float nrm = encode_core<E, LPV, BV>(y, vs, vb, scale, lane, c);
+        const float vn = encode_core<E, LPV, BV>(y, vs, vb, scale, l16, c);
+        if (l16 == 0) {
+          reinterpret_cast<uint16_t*>(sbp + Gm::KNORM)[ts] = (uint16_t)f32_to_f16_bits(kn);
+          reinterpret_cast<uint16_t*>(sbp + Gm::VNORM)[ts] = (uint16_t)f32_to_f16_bits(vn);
+        }
 #pragma unroll
-        for (int i = 0; i < E; ++i) vcode[grp][lane * E + i] = (uint8_t)c[i];
-        if (lane == 0)
-          reinterpret_cast<uint16_t*>(sb + Gm::VNORM)[tt] = (uint16_t)f32_to_f16_bits(nrm);
-      }
-    }
-    __syncthreads();
-    if (active && is_v) {
-      // lane r owns chunk (q = tt/4, r): this token's code for d = 16b + r sits at
-      // bit (4b + tt%4) * BV.  Other tokens share the chunk's dwords, so clear and
-      // set only this token's bits with atomics (correct for any slot mapping).
-      constexpr int NDW = Gm::VLANE / 4;
-      uint32_t v0[NDW], m0[NDW];  // this token's bits as if it were token 0 of its quad
+        for (int i = 0; i < E; ++i) vcode[wave][tt][l16 * E + i] = (uint8_t)c[i];
+        __asm__ volatile("" ::: "memory");  // a wave's LDS accesses run in order
+        if (!whole) {
+          // lane r owns chunk (ts / 4, r): this token's code for d = 16 b + r sits
+          // at bit (4 b + ts % 4) BV; other tokens share the chunk's words, so
+          // clear and set only this token's bits
+          uint32_t v0[NDW], m0[NDW];  // this token's bits as if it were token 0 of its quad
 #pragma unroll
-      for (int w = 0; w < NDW; ++w) { v0[w] = 0; m0[w] = 0; }
+          for (int w = 0; w < NDW; ++w) { v0[w] = 0; m0[w] = 0; }
 #pragma unroll
-      for (int b = 0; b < D / 16; ++b) {
-        const uint32_t code = vcode[grp][16 * b + lane];
-        const int P = 4 * b * BV;  // compile-time after unrolling; fields never straddle here
-        v0[P >> 5] |= code << (P & 31);
-        m0[P >> 5] |= ((1u << BV) - 1u) << (P & 31);
-      }
-      // move to token (tt % 4): shift the whole chunk left by (tt % 4) * BV bits
-      const int sh = (tt & 3) * BV;
-      uint32_t val[NDW], msk[NDW];
+          for (int b = 0; b < D / 16; ++b) {
+            const uint32_t code = vcode[wave][tt][16 * b + l16];
+            const int P = 4 * b * BV;  // compile-time after unrolling; fields never straddle here
+            v0[P >> 5] |= code << (P & 31);
+            m0[P >> 5] |= ((1u << BV) - 1u) << (P & 31);
+          }
+          const int sh = (ts & 3) * BV;
+          uint32_t* chunk = reinterpret_cast<uint32_t*>(sbp + Gm::KSEC + ((ts >> 2) * 16 + l16) * Gm::VLANE);
 #pragma unroll
-      for (int w = 0; w < NDW; ++w) {
-        const uint64_t vv = ((uint64_t)v0[w] << 32) | (w ? v0[w - 1] : 0u);
-        const uint64_t mm = ((uint64_t)m0[w] << 32) | (w ? m0[w - 1] : 0u);
-        val[w] = (uint32_t)((vv << sh) >> 32);
-        msk[w] = (uint32_t)((mm << sh) >> 32);
-      }
-      uint32_t* chunk = reinterpret_cast<uint32_t*>(sb + Gm::KSEC + ((tt >> 2) * 16 + lane) * Gm::VLANE);
-#pragma unroll
-      for (int w = 0; w < NDW; ++w) {
-        if (msk[w]) {
-          atomicAnd(chunk + w, ~msk[w]);
-          atomicOr(chunk + w, val[w]);
+          for (int w = 0; w < NDW; ++w) {
+            const uint64_t vv = ((uint64_t)v0[w] << 32) | (w ? v0[w - 1] : 0u);
+            const uint64_t mm = ((uint64_t)m0[w] << 32) | (w ? m0[w - 1] : 0u);
+            const uint32_t val = (uint32_t)((vv << sh) >> 32), msk = (uint32_t)((mm << sh) >> 32);
+            if (msk) {
+              atomicAnd(chunk + w, ~msk);
+              atomicOr(chunk + w, val);
+            }
+          }
         }
       }
     }
-    __syncthreads();
+    if (whole) {  // wave-uniform: every chunk of the sub-block, written whole
+      __asm__ volatile("" ::: "memory");
+      const int64_t blk = s0 / page_size;
+      const int off = (int)(s0 - blk * page_size);
+      uint8_t* sbp = cache + (((blk * hkv + head) * nsub) + (off >> 4)) * (int64_t)Gm::SUB;
+      // lane (q, r) = (lane >> 4, lane & 15): tokens 4q..4q+3 at d = 16 b + r
+      uint32_t w[NDW];
+#pragma unroll
+      for (int k = 0; k < NDW; ++k) w[k] = 0;
+#pragma unroll
+      for (int b = 0; b < D / 16; ++b)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int P = (4 * b + i) * BV;  // compile-time; a field never straddles a word (BV | 32 or 3 * 4 fits)
+          const uint32_t code = vcode[wave][4 * sub + i][16 * b + l16];
+          if ((P & 31) + BV <= 32) {
+            w[P >> 5] |= code << (P & 31);
+          } else {
+            w[P >> 5] |= code << (P & 31);
+            w[(P >> 5) + 1] |= code >> (32 - (P & 31));
+          }
+        }
+      uint32_t* chunk = reinterpret_cast<uint32_t*>(sbp + Gm::KSEC + lane * Gm::VLANE);
+#pragma unroll
+      for (int k = 0; k < NDW; ++k) chunk[k] = w[k];
+    }
+    __asm__ volatile("" ::: "memory");
   }
 }
 
@@ -1081,8 +1117,8 @@ static hipError_t launch_store3(const void* k, const void* v, int dt, int64_t n,
                                 const float* ks, const float* vs, const float* kb, const float* vb,
                                 const int64_t* slots, uint8_t* cache, int page_size,
                                 int64_t num_blocks, hipStream_t st) {
-  const int64_t nvec = n * hkv * 2;
-  int64_t g = (nvec + 15) / 16;
+  const int64_t items = (n + 15) / 16 * hkv;  // (16-token group, kv head), 4 per workgroup
+  int64_t g = (items + 3) / 4;
   if (g > 256 * 8) g = 256 * 8;
   const float sc = fwht_scale(D);
   dim3 grid((unsigned)g), block(256);
