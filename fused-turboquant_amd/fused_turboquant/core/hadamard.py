@@ -12,7 +12,7 @@ from __future__ import annotations
 import torch
 import torch.nn as nn
 
-from .. import _lib
+from .. import _lib, _ops
 
 
 def _validate_power_of_two(d: int, name: str = "d") -> None:
@@ -45,22 +45,21 @@ def _ones(d: int, device: torch.device) -> torch.Tensor:
 
 def rht_apply(x: torch.Tensor, signs: torch.Tensor, inverse: bool,
               out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
-    """Launch ``ftq_rht`` on the rows of ``x`` (last dim = d)."""
+    """The RHT of the rows of ``x`` (last dim = d) through ``torch.ops.fused_tq.rht``
+    (the ``ftq_rht`` kernel)."""
     d = x.shape[-1]
     _validate_power_of_two(d)
     dev = _lib.require_device(x, signs)
     if signs.dtype != torch.float32 or signs.numel() != d:
         raise ValueError("signs must be a float32 vector of length d")
+    del dev
     xf = x.contiguous()
     if xf.dtype not in (torch.float32, torch.float16, torch.bfloat16):
         xf = xf.float()
-    n = xf.numel() // d
-    out = torch.empty(xf.shape, dtype=out_dtype, device=dev)
-    L = _lib.lib()
-    _lib.check(L.ftq_rht(xf.data_ptr(), _lib.dtype_code(xf.dtype), n, d, signs.contiguous().data_ptr(),
-                         1 if inverse else 0, out.data_ptr(), _lib.dtype_code(out_dtype),
-                         _lib.stream_ptr(dev)))
-    return out
+    _lib.dtype_code(out_dtype)
+    if d not in (64, 128, 256):
+        raise ValueError(f"head_dim must be 64, 128 or 256 for the gfx950 kernels, got {d}")
+    return _ops.ops().rht(xf, signs.contiguous(), bool(inverse), out_dtype)
 
 
 def fwht(x: torch.Tensor) -> torch.Tensor:

@@ -4,7 +4,8 @@ Mirrors reference ``core/quantizer.py``: ``CompressedTensor`` (:36-51) and
 ``TurboQuantMSE`` (:54-216).  ``encode`` and ``decode`` are single HIP kernel
 launches (``ftq_encode`` / ``ftq_decode``) with the numerics of the
 reference's unfused path (:137-160, :191-205): packed codes, fp16 norms of
-the rotated vector, float32 reconstruction.  Device tensors only.
+the rotated vector, float32 reconstruction.  Device tensors only; the
+launches go through the ``torch.ops.fused_tq.encode`` / ``decode`` operators.
 """
 from __future__ import annotations
 
@@ -12,7 +13,7 @@ from dataclasses import dataclass
 
 import torch
 
-from .. import _lib
+from .. import _lib, _ops
 from .hadamard import RHTRotation
 from .lloyd_max import LloydMaxQuantizer
 
@@ -73,15 +74,9 @@ class TurboQuantMSE:
         xc = x.contiguous()
         if xc.dtype not in (torch.float32, torch.float16, torch.bfloat16):
             xc = xc.float()
-        lead = tuple(x.shape[:-1])
-        n = xc.numel() // self.head_dim
-        packed = torch.empty(lead + (packed_dim(self.head_dim, self.bits),), dtype=torch.uint8, device=dev)
-        norms = torch.empty(lead, dtype=torch.float16, device=dev)
-        L = _lib.lib()
-        _lib.check(L.ftq_encode_cb(xc.data_ptr(), _lib.dtype_code(xc.dtype), n, self.head_dim,
-                                   self.rotation.signs.data_ptr(), self.quantizer.boundaries.data_ptr(),
-                                   self.bits, self.quantizer.codebook_class, packed.data_ptr(),
-                                   norms.data_ptr(), _lib.stream_ptr(dev)))
+        del dev
+        packed, norms = _ops.ops().encode(xc, self.rotation.signs, self.quantizer.boundaries, self.bits,
+                                          self.quantizer.codebook_class)
         return CompressedTensor(indices=packed, norms=norms, original_dim=self.head_dim, bits=self.bits)
 
     # -- decode ------------------------------------------------------------
@@ -95,13 +90,9 @@ class TurboQuantMSE:
             raise ValueError("indices must be uint8 with last dim d*bits/8")
         if nr.dtype != torch.float16 or tuple(nr.shape) != tuple(pk.shape[:-1]):
             raise ValueError("norms must be float16 with the leading shape of indices")
-        dev = _lib.require_device(pk, nr, self.quantizer.levels)
-        out = torch.empty(tuple(nr.shape) + (d,), dtype=out_dtype, device=dev)
-        L = _lib.lib()
-        _lib.check(L.ftq_decode(pk.data_ptr(), nr.data_ptr(), nr.numel(), d,
-                                self.quantizer.levels.data_ptr(), self.rotation.signs.data_ptr(), bits,
-                                out.data_ptr(), _lib.dtype_code(out_dtype), _lib.stream_ptr(dev)))
-        return out
+        _lib.require_device(pk, nr, self.quantizer.levels)
+        _lib.dtype_code(out_dtype)
+        return _ops.ops().decode(pk, nr, self.quantizer.levels, self.rotation.signs, bits, d, out_dtype)
 
     def roundtrip(self, x: torch.Tensor) -> torch.Tensor:
         return self.decode(self.encode(x))

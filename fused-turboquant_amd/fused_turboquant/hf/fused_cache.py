@@ -267,6 +267,34 @@ def _keep_from_mask(attention_mask, q_len: int) -> Optional[torch.Tensor]:
     return None if bool(keep.all()) else keep
 
 
+def _continuation_mask(lens_before, past_len: int, q_len: int, keep, attention_mask, compress_v, device):
+    """[B, 1, q, past_len + q] bool mask of a chunk of q new tokens over the
+    decoded past of each sequence and the chunk itself.
+
+    V-compressed layers store only a sequence's real tokens, so sequence b's
+    past is the first lens_before[b] decoded positions: beyond them the rows
+    hold this chunk's own tokens (stored before decoding) or zeros, and are
+    hidden.  Within the chunk the mask is causal and hides padding tokens
+    (``keep`` False) from every row but their own, so no row is empty.
+    K-only layers keep every position in step with the base cache's V, so
+    their past is masked by the model's own 4-D attention mask when it has
+    one."""
+    B = len(lens_before)
+    causal = torch.ones(q_len, q_len, dtype=torch.bool, device=device).tril()
+    if not compress_v:
+        if attention_mask is not None and attention_mask.dim() == 4 and attention_mask.shape[-1] >= past_len + q_len:
+            m = attention_mask[:, :, -q_len:, -(past_len + q_len):]
+            return m if m.dtype == torch.bool else (m == 0)
+        return torch.cat([torch.ones(q_len, past_len, dtype=torch.bool, device=device), causal], dim=1)
+    lb = torch.tensor(lens_before, device=device)
+    past_ok = (torch.arange(past_len, device=device)[None, :] < lb[:, None])[:, None, :].expand(B, q_len, past_len)
+    new_ok = causal[None].expand(B, q_len, q_len)
+    if keep is not None:
+        eye = torch.eye(q_len, dtype=torch.bool, device=device)[None]
+        new_ok = new_ok & (keep[:, None, :].to(torch.bool) | eye)
+    return torch.cat([past_ok, new_ok], dim=2)[:, None]
+
+
 def _probe_attention_module(module, config) -> dict:
     return {
         "is_cross_attention": bool(getattr(module, "is_cross_attention", False)),
@@ -321,8 +349,9 @@ def make_fused_attention_forward(attn_module, cache: CompressedKVCache, quantize
             cos, sin = position_embeddings
             q, k = _apply_rotary_pos_emb(q, k, cos, sin)
 
-        had_past = bool(cache.seq_lens(layer_idx))
-        past_len = max(cache.seq_lens(layer_idx)) if had_past else 0
+        lens_before = cache.seq_lens(layer_idx)  # per sequence, before this chunk is stored
+        had_past = bool(lens_before) and max(lens_before) > 0
+        past_len = max(lens_before) if had_past else 0
         # V-compressed layers drop masked-out (padding) tokens so each sequence's
         # pages hold only its own tokens; K-only layers keep every position so K
         # lines up with the full-precision V of the base cache, and mask instead
@@ -358,9 +387,9 @@ def make_fused_attention_forward(attn_module, cache: CompressedKVCache, quantize
                   else raw_v[:, :, :past_len])
             kk = torch.cat([kd, k], dim=2)
             vv = torch.cat([vd, v], dim=2)
-            causal = torch.ones(q_len, past_len + q_len, dtype=torch.bool, device=q.device).tril(past_len)
+            mask = _continuation_mask(lens_before, past_len, q_len, keep, attention_mask, compress_v, q.device)
             out = F.scaled_dot_product_attention(q, _repeat_kv(kk, n_rep), _repeat_kv(vv, n_rep),
-                                                 attn_mask=causal, scale=scale)
+                                                 attn_mask=mask, scale=scale)
         out = out.transpose(1, 2).reshape(bsz, q_len, -1)
         o_proj = getattr(attn_module, "o_proj", None) or getattr(attn_module, "out_proj", None)
         return o_proj(out), None

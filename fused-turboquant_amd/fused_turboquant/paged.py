@@ -25,7 +25,7 @@ import math
 import numpy as np
 import torch
 
-from . import _lib
+from . import _lib, _ops
 from .core.quantizer import TurboQuantMSE
 
 _SIG = {
@@ -91,13 +91,10 @@ def paged_store(key: torch.Tensor, value: torch.Tensor, kv_cache: torch.Tensor,
     v = value.to(k.dtype).contiguous()
     if k.dtype not in (torch.float32, torch.float16, torch.bfloat16):
         k, v = k.float(), v.float()
-    L = _bind()
-    _lib.check(L.ftq_paged_store(
-        k.data_ptr(), v.data_ptr(), _lib.dtype_code(k.dtype), n, hkv, d,
-        k_quant.rotation.signs.data_ptr(), v_quant.rotation.signs.data_ptr(),
-        k_quant.quantizer.boundaries.data_ptr(), v_quant.quantizer.boundaries.data_ptr(),
-        k_quant.bits, v_quant.bits, slot_mapping.contiguous().data_ptr(), kv_cache.data_ptr(),
-        nsub * 16, nb, _lib.stream_ptr(dev)))
+    del dev
+    _ops.ops().paged_store(k, v, kv_cache, slot_mapping.contiguous(), k_quant.rotation.signs,
+                           v_quant.rotation.signs, k_quant.quantizer.boundaries, v_quant.quantizer.boundaries,
+                           k_quant.bits, v_quant.bits, nsub * 16)
 
 
 def default_splits(batch: int, num_kv_heads: int, max_seq_len: int, num_q_heads: int | None = None,
@@ -117,6 +114,14 @@ def _levels_pair(k_quant: TurboQuantMSE, v_quant: TurboQuantMSE):
     if kq is vq or (kq.bits == vq.bits and np.array_equal(kq.levels_host, vq.levels_host)):
         return kq.levels.data_ptr(), kq.levels.data_ptr()
     return kq.levels.data_ptr(), vq.levels.data_ptr()
+
+
+def _levels_tensors(k_quant: TurboQuantMSE, v_quant: TurboQuantMSE):
+    """The K and V level tensors; the K tensor for both when the codebooks are
+    equal (the kernel then builds one shared code table)."""
+    kp, vp = _levels_pair(k_quant, v_quant)
+    kl = k_quant.quantizer.levels
+    return kl, (kl if kp == vp else v_quant.quantizer.levels)
 
 
 def workspace_bytes(batch: int, num_q_heads: int, head_dim: int, num_splits: int) -> int:
@@ -164,15 +169,12 @@ def paged_decode_attention(query: torch.Tensor, kv_cache: torch.Tensor, block_ta
     if workspace is None or workspace.numel() < need:
         workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=dev)
     bt = block_table.contiguous()
-    L = _bind()
-    fn = L.ftq_paged_decode_attention if operands == "f16" else L.ftq_paged_decode_attention_valu
-    _lib.check(fn(
-        q.data_ptr(), _lib.dtype_code(q.dtype), kv_cache.data_ptr(), bt.data_ptr(),
-        seq_lens.contiguous().data_ptr(), B, hq, hkv, d, nsub * 16, bt.shape[1], nb,
-        k_quant.rotation.signs.data_ptr(), v_quant.rotation.signs.data_ptr(),
-        *_levels_pair(k_quant, v_quant),
-        k_quant.bits, v_quant.bits, float(scale), int(num_splits), workspace.data_ptr(),
-        workspace.numel(), out.data_ptr(), _lib.dtype_code(out.dtype), _lib.stream_ptr(dev)))
+    if operands == "fp32" and (d != 128 or hq // hkv > 4):
+        raise ValueError("fp32 operands: head_dim 128 and at most 4 query heads per kv head")
+    _ops.ops().paged_decode_attention(
+        q, kv_cache, bt, seq_lens.contiguous(), k_quant.rotation.signs, v_quant.rotation.signs,
+        *_levels_tensors(k_quant, v_quant), k_quant.bits, v_quant.bits, nsub * 16, float(scale),
+        int(num_splits), workspace, out, operands == "fp32")
     return out
 
 

@@ -19,7 +19,7 @@ import math
 
 import torch
 
-from . import _lib
+from . import _lib, _ops
 
 _SIG = {
     "ftq_raw_store": ["vp", "vp", "i32", "i64", "i32", "i32", "vp", "vp", "i64", "i32", "i64", "i64",
@@ -87,11 +87,9 @@ def raw_store(key: torch.Tensor, value: torch.Tensor, kv_cache: torch.Tensor,
     if k.dtype not in (torch.float32, torch.float16, torch.bfloat16):
         k = k.float()
     v = value.to(k.dtype).contiguous()
-    sb, sp, sh = _strides(kv_cache)
-    L = _bind()
-    _lib.check(L.ftq_raw_store(k.data_ptr(), v.data_ptr(), _lib.dtype_code(k.dtype), n, hkv, d,
-                               slot_mapping.contiguous().data_ptr(), kv_cache.data_ptr(), nb, bs, sb, sp, sh,
-                               _lib.stream_ptr(dev)))
+    _strides(kv_cache)
+    del dev
+    _ops.ops().raw_store(k, v, kv_cache, slot_mapping.contiguous())
 
 
 def default_splits(batch: int, num_kv_heads: int, max_seq_len: int) -> int:
@@ -148,16 +146,8 @@ def raw_decode_attention(query: torch.Tensor, kv_cache: torch.Tensor, block_tabl
     need = workspace_bytes(B, hq, d, num_splits)
     if workspace is None or workspace.numel() < need:
         workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=dev)
-    sb, sp, sh = _strides(kv_cache)
-    bt = block_table.contiguous()
+    _strides(kv_cache)
     ks = kv_start.contiguous() if kv_start is not None else None
-    L = _bind()
-    args = (q.data_ptr(), _lib.dtype_code(q.dtype), kv_cache.data_ptr(), nb, bs, sb, sp, sh,
-            bt.data_ptr(), bt.shape[1], seq_lens.contiguous().data_ptr(),
-            ks.data_ptr() if ks is not None else None, B, hq, hkv, d, float(scale), int(num_splits),
-            workspace.data_ptr(), workspace.numel(), out.data_ptr(), _lib.dtype_code(out.dtype))
-    if lse is None:
-        _lib.check(L.ftq_raw_decode_attention(*args, _lib.stream_ptr(dev)))
-    else:
-        _lib.check(L.ftq_raw_decode_attention_lse(*args, lse.data_ptr(), _lib.stream_ptr(dev)))
+    _ops.ops().raw_decode_attention(q, kv_cache, block_table.contiguous(), seq_lens.contiguous(), ks,
+                                    float(scale), int(num_splits), workspace, out, lse)
     return out

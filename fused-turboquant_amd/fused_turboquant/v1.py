@@ -31,7 +31,7 @@ import math
 
 import torch
 
-from . import _lib
+from . import _lib, _ops
 from .core.lloyd_max import compute_lloyd_max_codebook
 
 _SIG = {
@@ -314,22 +314,17 @@ def v1_store(key: torch.Tensor, value: torch.Tensor, kv_cache: torch.Tensor,
     if k.dtype not in (torch.float32, torch.float16, torch.bfloat16):
         k = k.float()
     v = value.to(k.dtype).contiguous()
-    sb, sp, sh = _strides(kv_cache)
+    _strides(kv_cache)
     mids = midpoints.to(torch.float32).contiguous()
-    L = _bind()
-    args = (k.data_ptr(), v.data_ptr(), _lib.dtype_code(k.dtype), n, hkv, d, mids.data_ptr(),
-            key_bits, value_bits, _v_flags(v_rotate, v_lloyd_max), slot_mapping.contiguous().data_ptr(),
-            kv_cache.data_ptr(), nb, bs, sb, sp, sh)
+    cf = rot = None
     if coeffs is not None:  # block-diagonal strategy: planar (B=2), rotor (3), iso (4)
         if coeffs.dim() != 2 or coeffs.shape[1] != d or coeffs.shape[0] not in (2, 3, 4):
             raise ValueError("coeffs must be [B, head_dim] with B in 2, 3, 4")
         cf = coeffs.to(device=dev, dtype=torch.float32).contiguous()
-        _lib.check(L.ftq_v1_store_blockdiag(*args, cf.data_ptr(), cf.shape[0], _lib.stream_ptr(dev)))
-    elif rotation is None:
-        _lib.check(L.ftq_v1_store(*args, _lib.stream_ptr(dev)))
-    else:  # any d x d matrix: x M in the kernel
+    elif rotation is not None:  # any d x d matrix: x M in the kernel
         rot = _rotation_arg(rotation, d, dev)
-        _lib.check(L.ftq_v1_store_rot(*args, rot.data_ptr(), _lib.stream_ptr(dev)))
+    _ops.ops().v1_store(k, v, kv_cache, slot_mapping.contiguous(), mids, key_bits, value_bits,
+                        _v_flags(v_rotate, v_lloyd_max), rot, cf)
 
 
 def default_splits(batch: int, num_kv_heads: int, max_seq_len: int) -> int:
@@ -347,7 +342,7 @@ def v1_decode_attention(query: torch.Tensor, kv_cache: torch.Tensor, block_table
                         kv_start: torch.Tensor | None = None, num_splits: int | None = None,
                         max_seq_len: int | None = None, out: torch.Tensor | None = None,
                         workspace: torch.Tensor | None = None, lse: torch.Tensor | None = None,
-                        rotation: torch.Tensor | None = None) -> torch.Tensor:
+                        rotation: torch.Tensor | None = None, sorted_centroids: bool = False) -> torch.Tensor:
     """query [B, Hq, d] -> [B, Hq, d] (query dtype unless ``out`` is given).
 
     Attends positions [kv_start[b], seq_lens[b]) of block-table row b
@@ -356,7 +351,8 @@ def v1_decode_attention(query: torch.Tensor, kv_cache: torch.Tensor, block_table
     to size it without reading ``block_table``'s width); ``workspace`` (uint8,
     >= ``workspace_bytes``) may be preallocated for graph capture.  ``lse``
     (float32 [B, Hq]) receives each row's natural-log log-sum-exp of the
-    scaled scores (-inf for a row with no positions).
+    scaled scores (-inf for a row with no positions).  ``sorted_centroids``:
+    the table is already sorted (skips the sort, e.g. for graph capture).
     """
     B, hq, d = query.shape
     _check_bits(d, key_bits, value_bits)
@@ -391,24 +387,15 @@ def v1_decode_attention(query: torch.Tensor, kv_cache: torch.Tensor, block_table
     need = workspace_bytes(B, hq, d, num_splits)
     if workspace is None or workspace.numel() < need:
         workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=dev)
-    sb, sp, sh = _strides(kv_cache)
-    bt = block_table.contiguous()
-    cent = torch.sort(centroids.to(torch.float32)).values.contiguous()
+    _strides(kv_cache)
+    cent = centroids.to(torch.float32)
+    if not sorted_centroids:
+        cent = torch.sort(cent).values
     ks = kv_start.contiguous() if kv_start is not None else None
-    L = _bind()
-    args = (q.data_ptr(), _lib.dtype_code(q.dtype), kv_cache.data_ptr(), nb, bs, sb, sp, sh,
-            bt.data_ptr(), bt.shape[1], seq_lens.contiguous().data_ptr(),
-            ks.data_ptr() if ks is not None else None, B, hq, hkv, d, cent.data_ptr(), key_bits,
-            value_bits, float(scale), _v_flags(v_rotate, v_lloyd_max), int(num_splits), workspace.data_ptr(),
-            workspace.numel(), out.data_ptr(), _lib.dtype_code(out.dtype))
-    if rotation is not None:  # a matrix strategy: q M, and o M^T with v_rotate
-        rot = _rotation_arg(rotation, d, dev)
-        _lib.check(L.ftq_v1_decode_attention_rot(*args, lse.data_ptr() if lse is not None else None,
-                                                 rot.data_ptr(), _lib.stream_ptr(dev)))
-    elif lse is None:
-        _lib.check(L.ftq_v1_decode_attention(*args, _lib.stream_ptr(dev)))
-    else:
-        _lib.check(L.ftq_v1_decode_attention_lse(*args, lse.data_ptr(), _lib.stream_ptr(dev)))
+    rot = _rotation_arg(rotation, d, dev) if rotation is not None else None  # q M, and o M^T with v_rotate
+    _ops.ops().v1_decode_attention(q, kv_cache, block_table.contiguous(), seq_lens.contiguous(), ks,
+                                   cent.contiguous(), key_bits, value_bits, float(scale),
+                                   _v_flags(v_rotate, v_lloyd_max), int(num_splits), workspace, out, lse, rot)
     return out
 
 
@@ -459,4 +446,5 @@ class TurboQuantV1Layer:
     def decode(self, query, kv_cache, block_table, seq_lens, **kw) -> torch.Tensor:
         return v1_decode_attention(query, kv_cache, block_table, seq_lens, self.centroids,
                                    self.key_bits, self.value_bits, v_rotate=self.v_rotate,
-                                   v_lloyd_max=self.v_lloyd_max, rotation=self.rotation, **kw)
+                                   v_lloyd_max=self.v_lloyd_max, rotation=self.rotation,
+                                   sorted_centroids=True, **kw)

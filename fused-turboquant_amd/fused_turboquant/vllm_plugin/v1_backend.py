@@ -72,6 +72,43 @@ except Exception:  # pragma: no cover - depends on the environment
     _ImplBase = object
 
 
+def _max_kv_splits() -> int:
+    """Split-K factor of decode steps under CUDA/HIP graph capture, fixed so
+    the captured launches and buffers do not depend on the step's context
+    length: vLLM's attention_config.tq_max_kv_splits_for_cuda_graph
+    (reference :569-574), else TURBOQUANT_MAX_KV_SPLITS (default 32)."""
+    try:
+        from vllm.config import get_current_vllm_config  # type: ignore
+        v = int(get_current_vllm_config().attention_config.tq_max_kv_splits_for_cuda_graph)
+    except Exception:
+        v = int(os.environ.get("TURBOQUANT_MAX_KV_SPLITS", "32"))
+    if not 1 <= v <= 1024:
+        raise ValueError("the maximum KV split count must be in [1, 1024]")
+    return v
+
+
+def _buf(layer, name: str, shape: tuple, dtype, device) -> torch.Tensor:
+    """A per-layer scratch tensor cached on the layer (reference
+    _get_or_alloc_buf, v1_backend.py:1851-1866): allocated when first needed
+    or when a larger one is, else the same storage, so decode steps allocate
+    nothing after warm-up and captured graphs keep their addresses."""
+    bufs = getattr(layer, "_fused_tq_bufs", None)
+    if bufs is None:
+        bufs = {}
+        try:
+            layer._fused_tq_bufs = bufs
+        except AttributeError:  # a layer object that takes no attributes: cache on the Impl's side
+            bufs = _buf.__dict__.setdefault("_fallback", {}).setdefault(id(layer), {})
+    n = 1
+    for x in shape:
+        n *= int(x)
+    t = bufs.get(name)
+    if t is None or t.numel() < n or t.dtype != dtype or t.device != torch.device(device):
+        t = torch.empty(max(n, 1), dtype=dtype, device=device)
+        bufs[name] = t
+    return t[:n].view(shape)
+
+
 def _defer_capacity() -> int:
     """Positions of the deferred-prefill buffer: vLLM's max(max_model_len,
     max_num_batched_tokens) (reference :575-585), else
@@ -148,7 +185,7 @@ class FusedTurboQuantV1Backend(_BackendBase):
 
     @classmethod
     def supports_head_size(cls, head_size: int) -> bool:
-        return head_size in (64, 128, 256)
+        return head_size == 128
 
     @classmethod
     def supports_compute_capability(cls, capability) -> bool:
@@ -215,6 +252,7 @@ class FusedTurboQuantV1Impl(_ImplBase):
         self.v_rotate = not self._is_raw and (env_flag("TURBOQUANT_V_ROTATE") or env_flag("TURBOQUANT_V_LLOYD_MAX"))
         self.defer_prefill = not self._is_raw and env_flag("TURBOQUANT_DEFER_PREFILL")
         self._prefix_capacity = _defer_capacity() if self.defer_prefill else 0
+        self.max_kv_splits = _max_kv_splits()
         # Lloyd-Max V codes (4-bit V; other widths stay uniform but rotated, as in the reference)
         self.v_lloyd_max = not self._is_raw and env_flag("TURBOQUANT_V_LLOYD_MAX")
         # rotation strategy (reference v1_backend.py:516-523): rht, or one of the block-diagonal
@@ -295,9 +333,17 @@ class FusedTurboQuantV1Impl(_ImplBase):
         q = query[:N].view(N, self.num_heads, self.head_size)
         nd = attn_metadata.num_decodes
         ndt = attn_metadata.num_decode_tokens
-        out = torch.empty(N, self.num_heads, self.head_size, dtype=query.dtype, device=query.device)
         if not attn_metadata.is_prefill:
             nd, ndt = attn_metadata.seq_lens.shape[0], N
+            # decode-only step: straight into vLLM's output buffer, per-layer
+            # scratch, no host reads -- capturable in a CUDA/HIP graph
+            o3 = output[:N].view(N, self.num_heads, self.head_size)
+            if output.dtype == query.dtype and o3.is_contiguous():
+                dec = self._decode_hybrid if self.defer_prefill else self._decode
+                dec(q, kv_cache, attn_metadata.block_table[:nd], attn_metadata.seq_lens[:nd], st,
+                    max_seq_len=getattr(attn_metadata, "max_seq_len", None), layer=layer, out=o3)
+                return output
+        out = torch.empty(N, self.num_heads, self.head_size, dtype=query.dtype, device=query.device)
         if ndt > 0:
             dec = self._decode_hybrid if self.defer_prefill else self._decode
             out[:ndt] = dec(q[:ndt], kv_cache, attn_metadata.block_table[:nd], attn_metadata.seq_lens[:nd], st,
@@ -312,10 +358,19 @@ class FusedTurboQuantV1Impl(_ImplBase):
             output[:N] = out.reshape(N, -1).to(output.dtype)
         return output
 
-    def _decode_hybrid(self, q, kv_cache, block_table, seq_lens, st, max_seq_len=None, layer=None):
+    def _splits(self, B: int, max_seq_len: int) -> int:
+        """The decode's split-K factor: fixed (max_kv_splits) while a graph is
+        being captured, else sized to the step's context, capped by it."""
+        if torch.cuda.is_current_stream_capturing():
+            return self.max_kv_splits
+        fn = RAW.default_splits if self._is_raw else V1.default_splits
+        return max(1, min(self.max_kv_splits, fn(B, self.num_kv_heads, max_seq_len)))
+
+    def _decode_hybrid(self, q, kv_cache, block_table, seq_lens, st, max_seq_len=None, layer=None, out=None):
         """Deferred-prefill decode (reference _decode_attention_hybrid,
         :1095-1277): fp16 prefix attention for sequence 0, quantised attention
-        over [P, seq_len) for every sequence, merged by log-sum-exp."""
+        over [P, seq_len) for every sequence, merged by log-sum-exp.  Every
+        intermediate is per-layer scratch (no allocation after warm-up)."""
         B, hq, d = q.shape
         dev = q.device
         pcache, plen, row = self._prefix(layer, dev)
@@ -323,35 +378,58 @@ class FusedTurboQuantV1Impl(_ImplBase):
         sl = seq_lens if seq_lens.dtype == torch.int32 else seq_lens.to(torch.int32)
         msl = max_seq_len if max_seq_len is not None else bt.shape[1] * kv_cache.shape[1]
         # phase 1: the prefix, sequence 0 only (the others get no positions)
-        sl_p = torch.zeros(B, dtype=torch.int32, device=dev)
+        sl_p = _buf(layer, "sl_p", (B,), torch.int32, dev)
+        sl_p.zero_()
         sl_p[:1].copy_(plen)
-        o1 = torch.empty(B, hq, d, dtype=torch.float32, device=dev)
-        l1 = torch.empty(B, hq, dtype=torch.float32, device=dev)
-        RAW.raw_decode_attention(q, pcache, row.expand(B, -1).contiguous(), sl_p, scale=self.scale,
-                                 max_seq_len=self._prefix_capacity, out=o1, lse=l1)
+        rows = _buf(layer, "prefix_rows", (B, row.shape[0]), torch.int32, dev)
+        rows.copy_(row.expand(B, -1))
+        o1 = _buf(layer, "o1", (B, hq, d), torch.float32, dev)
+        l1 = _buf(layer, "l1", (B, hq), torch.float32, dev)
+        s1 = RAW.default_splits(B, self.num_kv_heads, self._prefix_capacity)
+        ws1 = _buf(layer, "ws1", (RAW.workspace_bytes(B, hq, d, s1),), torch.uint8, dev)
+        RAW.raw_decode_attention(q, pcache, rows, sl_p, scale=self.scale, num_splits=s1, out=o1, lse=l1,
+                                 workspace=ws1)
         # phase 2: the quantised positions [P, seq_len)
-        o2 = torch.empty(B, hq, d, dtype=torch.float32, device=dev)
-        l2 = torch.empty(B, hq, dtype=torch.float32, device=dev)
+        o2 = _buf(layer, "o2", (B, hq, d), torch.float32, dev)
+        l2 = _buf(layer, "l2", (B, hq), torch.float32, dev)
+        ks = _buf(layer, "kv_start", (B,), torch.int32, dev)
+        ks.copy_(plen.expand(B))
+        s2 = self._splits(B, msl)
+        ws2 = _buf(layer, "ws", (V1.workspace_bytes(B, hq, d, self.max_kv_splits),), torch.uint8, dev)
         V1.v1_decode_attention(q, kv_cache, bt, sl, st.centroids, self.key_bits, self.value_bits,
                                scale=self.scale, v_rotate=self.v_rotate, v_lloyd_max=self.v_lloyd_max,
-                               kv_start=plen.expand(B).contiguous(),
-                               max_seq_len=msl, out=o2, lse=l2, rotation=st.rotation)
+                               kv_start=ks, num_splits=s2, out=o2, lse=l2, rotation=st.rotation,
+                               workspace=ws2, sorted_centroids=True)
         # merge (a row empty in both phases stays 0)
         m = torch.maximum(l1, l2)
         m = torch.where(torch.isneginf(m), torch.zeros_like(m), m)
         w1, w2 = torch.exp(l1 - m), torch.exp(l2 - m)
         tot = (w1 + w2).clamp(min=1e-20)
-        return ((o1 * w1.unsqueeze(-1) + o2 * w2.unsqueeze(-1)) / tot.unsqueeze(-1)).to(q.dtype)
+        res = (o1 * w1.unsqueeze(-1) + o2 * w2.unsqueeze(-1)) / tot.unsqueeze(-1)
+        if out is None:
+            return res.to(q.dtype)
+        out.copy_(res)
+        return out
 
-    def _decode(self, q, kv_cache, block_table, seq_lens, st, max_seq_len=None, layer=None):
+    def _decode(self, q, kv_cache, block_table, seq_lens, st, max_seq_len=None, layer=None, out=None):
+        B, hq, d = q.shape
+        dev = q.device
         bt = block_table if block_table.dtype == torch.int32 else block_table.to(torch.int32)
         sl = seq_lens if seq_lens.dtype == torch.int32 else seq_lens.to(torch.int32)
         msl = max_seq_len if max_seq_len is not None else bt.shape[1] * kv_cache.shape[1]
+        splits = self._splits(B, msl)
+        if layer is not None:
+            wsb = (RAW.workspace_bytes if self._is_raw else V1.workspace_bytes)(B, hq, d, self.max_kv_splits)
+            ws = _buf(layer, "ws", (wsb,), torch.uint8, dev)
+        else:
+            ws = None
         if self._is_raw:
-            return RAW.raw_decode_attention(q, kv_cache, bt, sl, scale=self.scale, max_seq_len=msl)
+            return RAW.raw_decode_attention(q, kv_cache, bt, sl, scale=self.scale, num_splits=splits, out=out,
+                                            workspace=ws)
         return V1.v1_decode_attention(q, kv_cache, bt, sl, st.centroids, self.key_bits, self.value_bits,
                                       scale=self.scale, v_rotate=self.v_rotate, v_lloyd_max=self.v_lloyd_max,
-                                      max_seq_len=msl, rotation=st.rotation)
+                                      num_splits=splits, rotation=st.rotation, out=out, workspace=ws,
+                                      sorted_centroids=True)
 
     def _prefill(self, q, k, v, kv_cache, md, nd, ndt, st):
         """Prefill sequences nd.. of the batch (tokens ndt..N)."""

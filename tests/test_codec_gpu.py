@@ -203,3 +203,20 @@ def test_config2_full_size_parity(cuda, d):
     ct2 = tq.encode(dec)
     same = (ct2.indices == ct.indices).float().mean().item()
     assert same > 0.99
+
+
+def test_encode_decode_under_torch_compile(cuda):
+    """TurboQuantMSE.encode / decode go through torch.ops.fused_tq with fake
+    implementations: torch.compile traces them in one graph (no breaks) and
+    the compiled function returns the eager results bit for bit."""
+    from fused_turboquant import TurboQuantMSE
+    tq = TurboQuantMSE(128, bits=3, seed=42, device=cuda)
+
+    def roundtrip(x):
+        ct = tq.encode(x)
+        return ct.indices, ct.norms, tq.decode(ct)
+
+    compiled = torch.compile(roundtrip, fullgraph=True)
+    x = torch.randn(300, 8, 128, generator=torch.Generator().manual_seed(6)).to(torch.bfloat16).to(cuda)
+    for got, want in zip(compiled(x), roundtrip(x)):
+        assert torch.equal(got, want)

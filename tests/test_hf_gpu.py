@@ -125,3 +125,43 @@ def test_k_only_layers(cuda, compress_v):
         _, got = _gen(model, ids, torch.ones_like(ids), cache, 3)
     cos = torch.nn.functional.cosine_similarity(got.reshape(-1, got.shape[-1]), ref.reshape(-1, ref.shape[-1]), dim=-1)
     assert torch.isfinite(got).all() and cos.min() > 0.98, cos.min()
+
+
+def test_padded_batch_continuation_chunk(cuda):
+    """A left-padded batch prefilled, then a 3-token chunk of new tokens per
+    sequence (a multi-token continuation over the compressed past), against
+    each sequence run alone through the same steps."""
+    from fused_turboquant.hf import patch_model
+    model = _tiny_llama(cuda)
+    cache = patch_model(model, bits=4, verify=False)
+    g = torch.Generator().manual_seed(8)
+    a = torch.randint(1, 320, (1, 4), generator=g)
+    b = torch.randint(1, 320, (1, 10), generator=g)
+    ca = torch.randint(1, 320, (1, 3), generator=g)
+    cb = torch.randint(1, 320, (1, 3), generator=g)
+    ids = torch.zeros(2, 10, dtype=torch.long)
+    mask = torch.zeros(2, 10, dtype=torch.long)
+    ids[0, 6:], mask[0, 6:] = a[0], 1
+    ids[1], mask[1] = b[0], 1
+
+    def two_steps(p_ids, p_mask, c_ids):
+        # positions counted over each sequence's real tokens (as generate() does), so a
+        # left-padded sequence's keys are rotated exactly as when it runs alone
+        pos = (p_mask.cumsum(-1) - 1).clamp(min=0)
+        cpos = p_mask.sum(-1, keepdim=True) + torch.arange(c_ids.shape[1])[None]
+        with torch.inference_mode():
+            model(input_ids=p_ids.to(cuda), attention_mask=p_mask.to(cuda), position_ids=pos.to(cuda),
+                  past_key_values=cache, use_cache=True)
+            m2 = torch.cat([p_mask, torch.ones(p_mask.shape[0], c_ids.shape[1], dtype=torch.long)], 1)
+            out = model(input_ids=c_ids.to(cuda), attention_mask=m2.to(cuda), position_ids=cpos.to(cuda),
+                        past_key_values=cache, use_cache=True)
+        cache.reset()
+        return out.logits.float()
+
+    lb = two_steps(ids, mask, torch.cat([ca, cb], 0))
+    la = two_steps(a, torch.ones_like(a), ca)
+    l1 = two_steps(b, torch.ones_like(b), cb)
+    for got, want, tag in ((lb[0], la[0], "seq a"), (lb[1], l1[0], "seq b")):
+        diff = (got - want).abs().max().item()
+        print(f"[hf padded continuation {tag}] max logit diff {diff:.3e} (|logit| max {want.abs().max().item():.2f})")
+        assert diff <= 2e-2 * max(1.0, want.abs().max().item())

@@ -257,3 +257,69 @@ def test_planar_kind_step(cuda, monkeypatch, vrot):
     against the oracle with the same matrix."""
     _run_step(cuda, [(40, 1), (700, 1), (0, 33), (129, 9)], "turboquant_k4v2_nc", 32, 8, vrot, monkeypatch,
               seed=11, kind="planar")
+
+
+@pytest.mark.parametrize("defer", [False, True])
+def test_impl_decode_under_graph_capture(cuda, monkeypatch, defer):
+    """A decode-only step of FusedTurboQuantV1Impl.forward captured in a HIP
+    graph (per-layer scratch, output written in place, the split count fixed
+    at TURBOQUANT_MAX_KV_SPLITS): three replays with new queries, an eager step
+    between them, each replay bit-identical to the eager forward of the same
+    inputs (the eager step picks the same split count here)."""
+    from fused_turboquant import vllm_plugin as vp
+    monkeypatch.setenv("TURBOQUANT_BOUNDARY_PROTECT", "0")
+    monkeypatch.setenv("TURBOQUANT_V_ROTATE", "1")
+    monkeypatch.setenv("TURBOQUANT_V_LLOYD_MAX", "0")
+    monkeypatch.setenv("TURBOQUANT_KIND", "rht")
+    monkeypatch.setenv("TURBOQUANT_MAX_KV_SPLITS", "4")
+    monkeypatch.setenv("TURBOQUANT_DEFER_PREFILL", "1" if defer else "0")
+    monkeypatch.setenv("TURBOQUANT_DEFER_PREFILL_CAPACITY", "256")
+    hq, hkv, bs = 8, 2, 16
+    lens = [8100, 8192, 7000]
+    B = len(lens)
+    impl = vp.FusedTurboQuantV1Impl(hq, D, 1 / math.sqrt(D), hkv, kv_cache_dtype="turboquant_k4v2_nc")
+    layer = SimpleNamespace()
+    g = torch.Generator().manual_seed(77)
+    pages = [(n + bs - 1) // bs for n in lens]
+    nb = sum(pages)
+    cache = torch.zeros(vp.FusedTurboQuantV1Backend.get_kv_cache_shape(nb, bs, hkv, D, "turboquant_k4v2_nc"),
+                        dtype=torch.uint8, device=cuda)
+    perm = torch.randperm(nb, generator=g).to(torch.int32)
+    bt = torch.zeros(B, max(pages), dtype=torch.int32)
+    used = 0
+    for i, n in enumerate(lens):
+        bt[i, :pages[i]] = perm[used:used + pages[i]]
+        used += pages[i]
+        k = torch.randn(n, hkv * D, generator=g).to(torch.bfloat16).to(cuda)
+        v = torch.randn(n, hkv * D, generator=g).to(torch.bfloat16).to(cuda)
+        pos = torch.arange(n)
+        impl.do_kv_cache_update(layer, k, v, cache, (bt[i].long()[pos // bs] * bs + pos % bs).to(cuda))
+    md = SimpleNamespace(seq_lens=torch.tensor(lens, dtype=torch.int32, device=cuda), block_table=bt.to(cuda),
+                         query_start_loc=torch.arange(B + 1, dtype=torch.int32, device=cuda), num_actual_tokens=B,
+                         max_query_len=1, max_seq_len=max(lens), is_prefill=False, num_decodes=B,
+                         num_decode_tokens=B)
+    q = torch.empty(B, hq * D, dtype=torch.bfloat16, device=cuda)
+    kv = torch.zeros(B, hkv * D, dtype=torch.bfloat16, device=cuda)
+    out_g = torch.empty(B, hq * D, dtype=torch.bfloat16, device=cuda)
+
+    def new_q(rep):
+        q.copy_(torch.randn(B, hq * D, generator=torch.Generator().manual_seed(100 + rep)).to(torch.bfloat16))
+
+    new_q(0)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):  # warm-up: per-layer scratch allocated before the capture
+        impl.forward(layer, q, kv, kv, cache, md, output=out_g)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        impl.forward(layer, q, kv, kv, cache, md, output=out_g)
+    for rep in range(1, 4):
+        new_q(rep)
+        graph.replay()
+        torch.cuda.synchronize()
+        got = out_g.clone()
+        want = impl.forward(layer, q, kv, kv, cache, md, output=torch.empty_like(out_g))
+        torch.cuda.synchronize()
+        assert torch.isfinite(got.float()).all()
+        assert torch.equal(got, want), rep
