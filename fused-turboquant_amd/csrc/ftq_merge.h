@@ -63,11 +63,13 @@ __device__ __forceinline__ void fwht_wave64(float (&y)[E], int lane) {
   }
 }
 
-// E = 2 or 4 contiguous fp32 loads / dtype stores (8 or 16 bytes per lane)
+// E = 1, 2 or 4 contiguous fp32 loads / dtype stores (4, 8 or 16 bytes per lane)
 template <int E>
 __device__ __forceinline__ void load_f32_small(const float* p, float (&x)[E]) {
-  static_assert(E == 2 || E == 4, "2 or 4 elements");
-  if constexpr (E == 2) {
+  static_assert(E == 1 || E == 2 || E == 4, "1, 2 or 4 elements");
+  if constexpr (E == 1) {
+    x[0] = *p;
+  } else if constexpr (E == 2) {
     const float2 v = *reinterpret_cast<const float2*>(p);
     x[0] = v.x; x[1] = v.y;
   } else {
@@ -79,8 +81,11 @@ template <int OT, int E>
 __device__ __forceinline__ void store_small(void* base, int64_t off, const float (&y)[E]) {
   if constexpr (OT == F32) {
     float* p = static_cast<float*>(base) + off;
-    if constexpr (E == 2) *reinterpret_cast<float2*>(p) = make_float2(y[0], y[1]);
+    if constexpr (E == 1) *p = y[0];
+    else if constexpr (E == 2) *reinterpret_cast<float2*>(p) = make_float2(y[0], y[1]);
     else *reinterpret_cast<float4*>(p) = make_float4(y[0], y[1], y[2], y[3]);
+  } else if constexpr (E == 1) {
+    *(static_cast<uint16_t*>(base) + off) = (uint16_t)f32_to_half_bits(OT, y[0]);
   } else {
     uint32_t w[E / 2];
 #pragma unroll

@@ -237,11 +237,6 @@ __device__ void build_code_lut(uint8_t* lut, const uint16_t* single, int tid, in
 
 typedef __attribute__((address_space(3))) const uint32_t lds_u32;
 
-// LDS address of a __shared__ object
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
-}
-
 // LDS address of this lane's copy of a code table
 template <int B>
 __device__ __forceinline__ uint32_t lut_lane_base(int lane, uint32_t table_addr) {

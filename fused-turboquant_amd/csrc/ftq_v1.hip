@@ -75,29 +75,6 @@ __device__ __forceinline__ uint32_t packed_bits(const uint8_t* c, int B, int pos
 }
 
 
-// x <- x M for a vector spread over 16 lanes, E contiguous elements per lane
-// (M row-major D x D fp32, the rotation of a matrix strategy: planar, rotor,
-// iso or a caller's own).  The vector goes through `row` (D floats of LDS
-// private to this 16-lane group, which lies inside one wave), and each lane
-// forms its E columns.
-template <int D, int E>
-__device__ __forceinline__ void rot_matrix_lanes(float (&x)[E], const float* __restrict__ M, float* row, int lane) {
-#pragma unroll
-  for (int i = 0; i < E; ++i) row[lane * E + i] = x[i];
-  __asm__ volatile("" ::: "memory");  // a wave's LDS accesses run in order
-  float y[E];
-#pragma unroll
-  for (int i = 0; i < E; ++i) y[i] = 0.f;
-  for (int k = 0; k < D; ++k) {
-    const float xk = row[k];
-#pragma unroll
-    for (int i = 0; i < E; ++i) y[i] = __builtin_fmaf(xk, M[(int64_t)k * D + lane * E + i], y[i]);
-  }
-  __asm__ volatile("" ::: "memory");
-#pragma unroll
-  for (int i = 0; i < E; ++i) x[i] = y[i];
-}
-
 // One (token, kv head) per 16 lanes, D/16 contiguous elements per lane.
 // ROTM: K (and V when rotated) rotated by the matrix rot instead of H/sqrt(D).
 template <int D, int DT, bool ROTM = false>
@@ -1159,22 +1136,7 @@ static hipError_t v1_launch_store_dense(const void* k, const void* v, int dt, in
   return hipGetLastError();
 }
 
-struct V1Args {
-  const void* q;
-  int qt;
-  const uint8_t* cache;
-  const int32_t *bt, *sl, *ks;
-  int B, hq, hkv, lbs, max_blocks;
-  int64_t nb, sblk, spos, shead;
-  const float* cent;
-  float qscale;
-  int splits, vrot;
-  float *wo, *wl;
-  void* out;
-  int ot;
-  float* lse;  // optional per-row natural-log LSE (B*Hq floats)
-  const float* rot;  // rotation matrix (D x D fp32, x M), or null for H/sqrt(D)
-};
+
 
 template <int D, int KB, int VB>
 static hipError_t v1_launch_attn3(const V1Args& a, hipStream_t st) {
@@ -1236,10 +1198,13 @@ int auto_splits(int batch, int hkv, int seq_hint, int target_wgs);
 
 using namespace ftq;
 
+extern "C" int64_t ftq_v1_slot_bytes_flags(int d, int key_bits, int value_bits, int v_flags) {
+  if (!(d == 64 || d == 128 || d == 256) || !v1_widths_ok(key_bits, value_bits, v_flags)) return -1;
+  return v1_geom(d, key_bits, value_bits, (v_flags & V1F_KFP8) != 0).raw;
+}
+
 extern "C" int64_t ftq_v1_slot_bytes(int d, int key_bits, int value_bits) {
-  if (!(d == 64 || d == 128 || d == 256) || key_bits < 2 || key_bits > 4 || value_bits < 2 || value_bits > 4)
-    return -1;
-  return v1_geom(d, key_bits, value_bits).raw;
+  return ftq_v1_slot_bytes_flags(d, key_bits, value_bits, 0);
 }
 
 namespace ftq {
@@ -1260,6 +1225,8 @@ extern "C" int ftq_v1_store_rot(const void* key, const void* value, int dtype, i
   const int rc = v1_store_checks(d, key_bits, value_bits, n_tokens, num_kv_heads, num_blocks, block_size, dtype,
                                  v_rotate, stride_block, stride_pos, stride_head);
   if (rc != FTQ_OK) return rc;
+  FTQ_REQUIRE(key_bits <= 4 && value_bits <= 4 && (v_rotate & V1F_KFP8) == 0,
+              "dense-matrix store: key_bits and value_bits in 1..4, no fp8 keys");
   FTQ_REQUIRE(aligned4(rotation), "rotation must be 4-byte aligned");
   if (n_tokens == 0) return FTQ_OK;
   FTQ_REQUIRE(key && value && midpoints && slot_mapping && kv_cache, "null pointer argument");
@@ -1293,11 +1260,12 @@ extern "C" int ftq_v1_decode_attention_rot(
     int value_bits, float scale, int v_rotate, int num_splits, void* workspace,
     int64_t workspace_bytes, void* out, int out_dtype, float* lse_out, const float* rotation,
     void* stream) {
-  FTQ_REQUIRE(d == 128, "v1 decode attention: head_dim must be 128");
-  FTQ_REQUIRE(v_rotate >= 0 && v_rotate <= 3, "v_rotate: bit 0 = un-rotate V, bit 1 = Lloyd-Max V codes");
+  FTQ_REQUIRE(d == 64 || d == 128 || d == 256, "v1 decode attention: head_dim must be 64, 128 or 256");
+  FTQ_REQUIRE(v_rotate >= 0 && v_rotate <= 15,
+              "v_flags: bit 0 = un-rotate V, bit 1 = Lloyd-Max V codes, bit 2 = fp8 keys, bit 3 = fp32 products");
   FTQ_REQUIRE(rotation == nullptr || aligned4(rotation), "rotation must be 4-byte aligned");
-  FTQ_REQUIRE(key_bits >= 2 && key_bits <= 4 && value_bits >= 2 && value_bits <= 4,
-              "v1 decode attention: key_bits and value_bits must be 2, 3 or 4");
+  FTQ_REQUIRE(v1_widths_ok(key_bits, value_bits, v_rotate),
+              "v1 decode attention: key_bits and value_bits must both be in 1..4, or both 8 (fp8 keys: both 8)");
   FTQ_REQUIRE(block_size >= 16 && block_size <= 4096 && (block_size & (block_size - 1)) == 0,
               "block_size must be a power of two in [16, 4096]");
   FTQ_REQUIRE(batch >= 0 && num_kv_heads > 0 && num_q_heads > 0 && num_blocks >= 0,
@@ -1308,7 +1276,8 @@ extern "C" int ftq_v1_decode_attention_rot(
   FTQ_REQUIRE(max_blocks_per_seq >= 0, "max_blocks_per_seq must be >= 0");
   FTQ_REQUIRE(q_dtype >= F32 && q_dtype <= BF16 && out_dtype >= F32 && out_dtype <= BF16,
               "dtype must be FTQ_F32, FTQ_F16 or FTQ_BF16");
-  const V1Geom g = v1_geom(d, key_bits, value_bits);
+  const bool kf8 = (v_rotate & V1F_KFP8) != 0;
+  const V1Geom g = v1_geom(d, key_bits, value_bits, kf8);
   FTQ_REQUIRE(stride_head >= g.raw, "stride_head is smaller than the slot bytes (see ftq_v1_slot_bytes)");
   FTQ_REQUIRE(stride_pos >= stride_head * num_kv_heads && stride_block >= stride_pos * block_size,
               "kv_cache strides must describe [num_blocks][block_size][num_kv_heads][slot]");
@@ -1317,8 +1286,8 @@ extern "C" int ftq_v1_decode_attention_rot(
   FTQ_REQUIRE(stride_pos * 16 < ((int64_t)1 << 31), "stride_pos too large");
   if (batch == 0) return FTQ_OK;
   FTQ_REQUIRE(num_blocks >= 1, "kv_cache must hold at least one block");
-  FTQ_REQUIRE(query && kv_cache && block_table && seq_lens && centroids && workspace && out,
-              "null pointer argument");
+  FTQ_REQUIRE(query && kv_cache && block_table && seq_lens && workspace && out, "null pointer argument");
+  FTQ_REQUIRE(centroids != nullptr || kf8, "null centroids");
   FTQ_REQUIRE(workspace_bytes >= ftq_v1_workspace_bytes(batch, num_q_heads, d, num_splits),
               "workspace too small (see ftq_v1_workspace_bytes)");
   FTQ_REQUIRE(aligned16(query) && aligned16(out) && aligned16(workspace) && aligned4(kv_cache),
@@ -1338,7 +1307,12 @@ extern "C" int ftq_v1_decode_attention_rot(
   a.out = out; a.ot = out_dtype; a.lse = lse_out;
   hipStream_t st = (hipStream_t)stream;
   hipError_t e;
-  if (key_bits == 2) e = v1_launch_attn2<128, 2>(value_bits, a, st);
+  // the matrix-core kernels: head_dim 128, 2-4 bit codes, f16 operands; every
+  // other format, and fp32 products on request, on the VALU kernel
+  const bool mfma = d == 128 && !kf8 && (v_rotate & V1F_FP32) == 0 && key_bits >= 2 && key_bits <= 4 &&
+                    value_bits >= 2 && value_bits <= 4;
+  if (!mfma) e = v1_valu_launch(a, d, key_bits, value_bits, v_rotate, st);
+  else if (key_bits == 2) e = v1_launch_attn2<128, 2>(value_bits, a, st);
   else if (key_bits == 3) e = v1_launch_attn2<128, 3>(value_bits, a, st);
   else e = v1_launch_attn2<128, 4>(value_bits, a, st);
   return hip_status(e);

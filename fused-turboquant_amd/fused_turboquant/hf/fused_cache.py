@@ -480,24 +480,57 @@ def _resolve_compress_v(compress_v, layer_idx: int, n_layers: int) -> bool:
     raise ValueError(f"compress_v must be a bool, 'boundary' or a callable, got {compress_v!r}")
 
 
-def _smoke_test(model, cache: CompressedKVCache, config) -> None:
-    """One prompt + one decode step through the patched model; the decode
-    logits must be finite (reference :883-962 compares against the unpatched
-    model, which needs the original forwards; here a non-finite result or an
-    exception is the failure signal)."""
+SMOKE_MIN_COSINE = 0.8  # reference hf/fused_cache.py:947
+
+
+def _swap_forwards(model, forwards: dict) -> dict:
+    """Install ``forwards`` (module name -> forward) and return the ones they replace."""
+    replaced = {}
+    for name, module in model.named_modules():
+        if name in forwards:
+            replaced[name] = module.forward
+            module.forward = forwards[name]
+    return replaced
+
+
+def _smoke_test(model, cache: CompressedKVCache, originals: dict, config) -> float:
+    """Verify the patched model against the unpatched one (reference
+    ``hf/fused_cache.py:883-961``): a 4-token prompt and one decode step
+    through the patched model (the step reads the compressed pages through
+    the fused decode attention), then the same 5 tokens through the original
+    forwards with no cache.  The cosine similarity of the two last-position
+    logit vectors must reach 0.8, as in the reference; a fused forward that
+    raises is reported the same way.  Returns the similarity; the model is
+    left patched with an empty cache."""
     device = next(model.parameters()).device
     vocab = getattr(config, "vocab_size", 32000)
-    ids = torch.randint(0, vocab, (1, 4), device=device)
+    ids = torch.randint(0, vocab, (1, 5), device=device)
     try:
         with torch.inference_mode():
-            out = model(ids, past_key_values=cache, use_cache=True)
-            out = model(ids[:, -1:], past_key_values=cache, use_cache=True)
+            model(ids[:, :4], past_key_values=cache, use_cache=True)
+            fused = model(ids[:, 4:], past_key_values=cache, use_cache=True).logits[0, -1].float()
     except Exception as exc:  # report as the reference does
         cache.reset()
-        raise RuntimeError(f"Smoke test failed: fused forward raised {type(exc).__name__}: {exc}") from exc
-    if not torch.isfinite(out.logits).all():
-        cache.reset()
-        raise RuntimeError("Smoke test failed: non-finite logits from the patched model")
+        raise RuntimeError(f"Smoke test failed: fused forward raised {type(exc).__name__}: {exc}. "
+                           "This model architecture may not be compatible with fused-turboquant; "
+                           "see check_model_compatibility(model)") from exc
+    cache.reset()
+    patched = _swap_forwards(model, originals)
+    try:
+        with torch.inference_mode():
+            ref = model(ids, use_cache=False).logits[0, -1].float()
+    except Exception:  # the reference skips the check when its own forward fails
+        logger.debug("Smoke test skipped: the unpatched forward failed")
+        return float("nan")
+    finally:
+        _swap_forwards(model, patched)
+    cos = torch.nn.functional.cosine_similarity(fused[None], ref[None]).item()
+    if not math.isfinite(cos) or cos < SMOKE_MIN_COSINE:
+        raise RuntimeError(f"Smoke test failed: cosine similarity between fused and reference logits is "
+                           f"{cos:.4f} (threshold {SMOKE_MIN_COSINE}); the fused attention path is wrong "
+                           f"for {type(model).__name__}. Pass verify=False to skip this check.")
+    logger.info("Smoke test passed: logit cosine similarity = %.4f", cos)
+    return cos
 
 
 def patch_model(model, bits: int = 4, head_dim: int | None = None, verify: bool = True,
@@ -561,7 +594,7 @@ def patch_model(model, bits: int = 4, head_dim: int | None = None, verify: bool 
     if not originals:
         logger.warning("No attention layers were patched; see check_model_compatibility(model)")
     elif verify:
-        _smoke_test(model, cache, config)
+        _smoke_test(model, cache, originals, config)
         cache.reset()
     return cache
 

@@ -73,18 +73,28 @@ def _bind():
     return L
 
 
-def _check_bits(head_dim: int, key_bits: int, value_bits: int) -> None:
+def _check_bits(head_dim: int, key_bits: int, value_bits: int, key_fp8: bool = False) -> None:
+    """Widths with a store and a decode: K and V both in 1..4 (the
+    ``turboquant_k{K}v{V}_nc`` presets and aliases, reference
+    ``vllm_plugin/plugin.py:322``), or both 8 -- 8-bit Lloyd-Max keys, or fp8
+    keys (``key_fp8``), with 8-bit uniform values (the 8-bit / fp8 boundary
+    layers, ``boundary_tq_config.py``)."""
     if head_dim not in (64, 128, 256):
         raise ValueError(f"head_dim must be 64, 128 or 256, got {head_dim}")
-    if not (2 <= key_bits <= 4) or not (2 <= value_bits <= 4):
-        raise ValueError("key_bits and value_bits must be 2, 3 or 4")
+    if key_fp8 or key_bits == 8 or value_bits == 8:
+        if key_bits != 8 or value_bits != 8:
+            raise ValueError("8-bit (and fp8) keys pair with 8-bit values: key_bits = value_bits = 8")
+    elif not (1 <= key_bits <= 4) or not (1 <= value_bits <= 4):
+        raise ValueError("key_bits and value_bits must be in 1..4 (or both 8)")
 
 
-def slot_bytes(head_dim: int, key_bits: int, value_bits: int) -> int:
+def slot_bytes(head_dim: int, key_bits: int, value_bits: int, key_fp8: bool = False) -> int:
     """Bytes of a slot that hold data: key_packed_size + value bytes + 4
-    (reference ``boundary_tq_config.py:66-81``)."""
-    _check_bits(head_dim, key_bits, value_bits)
-    return (head_dim * key_bits // 8 + 2) + (head_dim * value_bits // 8) + 4
+    (reference ``boundary_tq_config.py:66-81``); fp8 keys take head_dim bytes
+    and no norm."""
+    _check_bits(head_dim, key_bits, value_bits, key_fp8)
+    kps = head_dim if key_fp8 else head_dim * key_bits // 8 + 2
+    return kps + head_dim * value_bits // 8 + 4
 
 
 def host_preset_bits(key_bits: int, value_bits: int) -> tuple:
@@ -135,9 +145,16 @@ def _strides(kv_cache: torch.Tensor):
     return kv_cache.stride(0), kv_cache.stride(1), kv_cache.stride(2)
 
 
-def _v_flags(v_rotate: bool, v_lloyd_max: bool) -> int:
-    # the C ABI's v_rotate word: bit 0 rotates V, bit 1 selects Lloyd-Max V codes
-    return (1 if (v_rotate or v_lloyd_max) else 0) | (2 if v_lloyd_max else 0)
+# bits of the C ABI's v_rotate / v_flags word (FTQ_V1_* in fused_tq.h)
+VROT, VLLOYD, KFP8, FP32 = 1, 2, 4, 8
+
+
+def _v_flags(v_rotate: bool, v_lloyd_max: bool, key_fp8: bool = False, fp32: bool = False) -> int:
+    return ((VROT if (v_rotate or v_lloyd_max) else 0) | (VLLOYD if v_lloyd_max else 0)
+            | (KFP8 if key_fp8 else 0) | (FP32 if fp32 else 0))
+
+
+_OPERANDS = ("f16", "fp32")
 
 
 def planar_rotation(head_dim: int, seed: int = 42, device="cpu") -> torch.Tensor:
@@ -287,9 +304,12 @@ def _rotation_arg(rotation: torch.Tensor, d: int, dev) -> torch.Tensor:
 def v1_store(key: torch.Tensor, value: torch.Tensor, kv_cache: torch.Tensor,
              slot_mapping: torch.Tensor, midpoints: torch.Tensor, key_bits: int,
              value_bits: int, v_rotate: bool = False, v_lloyd_max: bool = False,
-             rotation: torch.Tensor | None = None, coeffs: torch.Tensor | None = None) -> None:
+             rotation: torch.Tensor | None = None, coeffs: torch.Tensor | None = None,
+             key_fp8: bool = False) -> None:
     """Quantise ``key``/``value`` [n, Hkv, d] into their slots (``slot_mapping`` [n]
-    int64; negative entries are skipped).  ``v_lloyd_max`` (implies
+    int64; negative entries are skipped).  ``key_fp8`` (key_bits = value_bits
+    = 8): K stored as fp8 e4m3fn, no norm, ``midpoints`` unused (reference
+    ``triton_inkernel_store.py:59-83``).  ``v_lloyd_max`` (implies
     ``v_rotate``): 4-bit V takes Lloyd-Max codes against the K midpoints and its
     norm in the scale field (reference ``triton_inkernel_store.py:159-200``);
     other V widths keep the uniform codes.  ``coeffs`` ([B, d] float32, B in
@@ -297,17 +317,19 @@ def v1_store(key: torch.Tensor, value: torch.Tensor, kv_cache: torch.Tensor,
     (``block_coeffs``), O(B d) per vector (reference ``_fused_store_block_diag``,
     ``triton_inkernel_store.py:649-860``); ``rotation``: any d x d matrix, O(d^2)."""
     n, hkv, d = key.shape
-    _check_bits(d, key_bits, value_bits)
+    _check_bits(d, key_bits, value_bits, key_fp8)
     if value.shape != key.shape:
         raise ValueError("key and value shapes differ")
     nb, bs, hk2, slot = kv_cache.shape
     if hk2 != hkv:
         raise ValueError("kv_cache num_kv_heads does not match key")
-    if slot < slot_bytes(d, key_bits, value_bits):
+    if slot < slot_bytes(d, key_bits, value_bits, key_fp8):
         raise ValueError("kv_cache slot is smaller than the slot bytes for these bits")
     if slot_mapping.dtype != torch.int64 or slot_mapping.numel() != n:
         raise ValueError("slot_mapping must be int64 with one entry per token")
-    if midpoints.numel() != (1 << key_bits) - 1:
+    if midpoints is None or key_fp8:
+        midpoints = torch.zeros(1, dtype=torch.float32, device=key.device)
+    elif midpoints.numel() != (1 << key_bits) - 1:
         raise ValueError("midpoints must have 2^key_bits - 1 entries")
     dev = _lib.require_device(key, value, kv_cache, slot_mapping, midpoints)
     k = key.contiguous()
@@ -324,7 +346,7 @@ def v1_store(key: torch.Tensor, value: torch.Tensor, kv_cache: torch.Tensor,
     elif rotation is not None:  # any d x d matrix: x M in the kernel
         rot = _rotation_arg(rotation, d, dev)
     _ops.ops().v1_store(k, v, kv_cache, slot_mapping.contiguous(), mids, key_bits, value_bits,
-                        _v_flags(v_rotate, v_lloyd_max), rot, cf)
+                        _v_flags(v_rotate, v_lloyd_max, key_fp8), rot, cf)
 
 
 def default_splits(batch: int, num_kv_heads: int, max_seq_len: int) -> int:
@@ -342,7 +364,8 @@ def v1_decode_attention(query: torch.Tensor, kv_cache: torch.Tensor, block_table
                         kv_start: torch.Tensor | None = None, num_splits: int | None = None,
                         max_seq_len: int | None = None, out: torch.Tensor | None = None,
                         workspace: torch.Tensor | None = None, lse: torch.Tensor | None = None,
-                        rotation: torch.Tensor | None = None, sorted_centroids: bool = False) -> torch.Tensor:
+                        rotation: torch.Tensor | None = None, sorted_centroids: bool = False,
+                        key_fp8: bool = False, operands: str = "f16") -> torch.Tensor:
     """query [B, Hq, d] -> [B, Hq, d] (query dtype unless ``out`` is given).
 
     Attends positions [kv_start[b], seq_lens[b]) of block-table row b
@@ -353,13 +376,19 @@ def v1_decode_attention(query: torch.Tensor, kv_cache: torch.Tensor, block_table
     (float32 [B, Hq]) receives each row's natural-log log-sum-exp of the
     scaled scores (-inf for a row with no positions).  ``sorted_centroids``:
     the table is already sorted (skips the sort, e.g. for graph capture).
+    ``key_fp8``: the keys are fp8 e4m3fn (``centroids`` unused).
+    ``operands``: ``"f16"`` (default) runs head_dim 128 with 2-4 bit codes on
+    the matrix-core kernels (f16 operands, fp32 accumulation); ``"fp32"``
+    keeps every product in fp32 on the VALU, the reference's arithmetic.
+    Head dims 64 and 256, 1- and 8-bit codes and fp8 keys always take the
+    fp32 kernel.
     """
     B, hq, d = query.shape
-    _check_bits(d, key_bits, value_bits)
-    if d != 128:
-        raise ValueError("v1 decode attention supports head_dim 128")
+    _check_bits(d, key_bits, value_bits, key_fp8)
+    if operands not in _OPERANDS:
+        raise ValueError(f"operands must be one of {_OPERANDS}, got {operands!r}")
     nb, bs, hkv, slot = kv_cache.shape
-    if slot < slot_bytes(d, key_bits, value_bits):
+    if slot < slot_bytes(d, key_bits, value_bits, key_fp8):
         raise ValueError("kv_cache slot is smaller than the slot bytes for these bits")
     if block_table.dtype != torch.int32 or seq_lens.dtype != torch.int32:
         raise ValueError("block_table and seq_lens must be int32")
@@ -367,7 +396,10 @@ def v1_decode_attention(query: torch.Tensor, kv_cache: torch.Tensor, block_table
         raise ValueError("block_table must be [B, max_blocks] and seq_lens [B]")
     if kv_start is not None and (kv_start.dtype != torch.int32 or kv_start.numel() != B):
         raise ValueError("kv_start must be int32 [B]")
-    if centroids.numel() != (1 << key_bits):
+    if centroids is None or key_fp8:
+        centroids = torch.zeros(1, dtype=torch.float32, device=query.device)
+        sorted_centroids = True
+    elif centroids.numel() != (1 << key_bits):
         raise ValueError("centroids must have 2^key_bits entries")
     if lse is not None and (lse.dtype != torch.float32 or lse.numel() != B * hq or not lse.is_contiguous()):
         raise ValueError("lse must be a contiguous float32 tensor of B * num_q_heads entries")
@@ -395,7 +427,8 @@ def v1_decode_attention(query: torch.Tensor, kv_cache: torch.Tensor, block_table
     rot = _rotation_arg(rotation, d, dev) if rotation is not None else None  # q M, and o M^T with v_rotate
     _ops.ops().v1_decode_attention(q, kv_cache, block_table.contiguous(), seq_lens.contiguous(), ks,
                                    cent.contiguous(), key_bits, value_bits, float(scale),
-                                   _v_flags(v_rotate, v_lloyd_max), int(num_splits), workspace, out, lse, rot)
+                                   _v_flags(v_rotate, v_lloyd_max, key_fp8, operands == "fp32"),
+                                   int(num_splits), workspace, out, lse, rot)
     return out
 
 
@@ -406,18 +439,27 @@ class TurboQuantV1Layer:
 
     def __init__(self, head_dim: int, key_bits: int, value_bits: int, v_rotate: bool = False,
                  centroids: torch.Tensor | None = None, device="cuda", v_lloyd_max: bool = False,
-                 kind: str = "rht", rotation: torch.Tensor | None = None):
-        _check_bits(head_dim, key_bits, value_bits)
+                 kind: str = "rht", rotation: torch.Tensor | None = None, key_fp8: bool = False,
+                 operands: str = "f16"):
+        _check_bits(head_dim, key_bits, value_bits, key_fp8)
+        if operands not in _OPERANDS:
+            raise ValueError(f"operands must be one of {_OPERANDS}, got {operands!r}")
         self.head_dim = head_dim
         self.key_bits = key_bits
         self.value_bits = value_bits
+        self.key_fp8 = bool(key_fp8)
+        self.operands = operands
         self.v_lloyd_max = bool(v_lloyd_max)
         self.v_rotate = bool(v_rotate) or self.v_lloyd_max
-        c = centroids if centroids is not None else default_centroids(head_dim, key_bits)
-        if c.numel() != (1 << key_bits):
-            raise ValueError("centroids must have 2^key_bits entries")
-        self.centroids = torch.sort(c.to(torch.float32)).values.to(device)
-        self.midpoints = midpoints_of(self.centroids)
+        if self.key_fp8:  # fp8 keys: no codebook (the 8-bit V is uniform)
+            self.centroids = torch.zeros(1, dtype=torch.float32, device=device)
+            self.midpoints = self.centroids
+        else:
+            c = centroids if centroids is not None else default_centroids(head_dim, key_bits)
+            if c.numel() != (1 << key_bits):
+                raise ValueError("centroids must have 2^key_bits entries")
+            self.centroids = torch.sort(c.to(torch.float32)).values.to(device)
+            self.midpoints = midpoints_of(self.centroids)
         # rotation strategy (TURBOQUANT_KIND): rht = the kernels' own H/sqrt(d);
         # planar = a matrix x M applied in the kernels; a caller's matrix the same
         self.kind = kind
@@ -435,16 +477,21 @@ class TurboQuantV1Layer:
                              "or an explicit matrix")
 
     def kv_cache_shape(self, num_blocks: int, block_size: int, num_kv_heads: int) -> tuple:
+        if self.key_bits == 8:  # 8-bit formats live in boundary-layer slots: the raw bytes, rounded up
+            raw = slot_bytes(self.head_dim, 8, 8, self.key_fp8)
+            return (num_blocks, block_size, num_kv_heads, 1 << (raw - 1).bit_length())
         return get_kv_cache_shape(num_blocks, block_size, num_kv_heads, self.head_dim,
                                   self.key_bits, self.value_bits)
 
     def store(self, key, value, kv_cache, slot_mapping) -> None:
         v1_store(key, value, kv_cache, slot_mapping, self.midpoints, self.key_bits,
                  self.value_bits, self.v_rotate, self.v_lloyd_max,
-                 rotation=self.rotation if self.coeffs is None else None, coeffs=self.coeffs)
+                 rotation=self.rotation if self.coeffs is None else None, coeffs=self.coeffs,
+                 key_fp8=self.key_fp8)
 
     def decode(self, query, kv_cache, block_table, seq_lens, **kw) -> torch.Tensor:
         return v1_decode_attention(query, kv_cache, block_table, seq_lens, self.centroids,
                                    self.key_bits, self.value_bits, v_rotate=self.v_rotate,
                                    v_lloyd_max=self.v_lloyd_max, rotation=self.rotation,
-                                   sorted_centroids=True, **kw)
+                                   sorted_centroids=True, key_fp8=self.key_fp8,
+                                   **{"operands": self.operands, **kw})

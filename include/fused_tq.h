@@ -175,14 +175,28 @@ int ftq_paged_decode_attention_valu(const void* query, int q_dtype, const uint8_
  * bytes); per (token, kv head) slot:
  *   [K codes d*kb/8][K norm f16][V codes d*vb/8][V scale f16][V min f16][pad]
  * (reference vllm_plugin/triton_inkernel_store.py:38-330,
- * boundary_tq_config.py:66-81, v1_backend.py:171-220).
+ * boundary_tq_config.py:66-81, v1_backend.py:171-220).  Code widths: K and V
+ * both in 1..4, or both 8 (the 8-bit boundary layers: 256 Lloyd-Max
+ * centroids for K, 8-bit uniform V).  FP8 keys (v_flags bit 2, key_bits 8):
+ * d bytes of fp8 e4m3fn K, no K norm: [K fp8 d][V codes][V scale][V min].
+ * The int v_rotate argument of the store and decode entry points is this
+ * bit set (FTQ_V1_*): bit 0 V rotated, bit 1 Lloyd-Max V codes (4-bit V),
+ * bit 2 fp8 keys, bit 3 (decode only) fp32 products on the VALU.
  */
+#define FTQ_V1_VROT 1
+#define FTQ_V1_VLLOYD 2
+#define FTQ_V1_KFP8 4
+#define FTQ_V1_FP32 8
 
 /* Bytes of a slot that hold data (key_packed_size + value bytes + 4), or -1
  * for an unsupported shape.  Replaces BoundaryTurboQuantConfig.key_packed_size /
  * value_data_bytes (boundary_tq_config.py:66-81); the slot stride itself is the
  * caller's (v1_backend.py:171-209 rounds it up to a power of two). */
 int64_t ftq_v1_slot_bytes(int d, int key_bits, int value_bits);
+/* ftq_v1_slot_bytes for a v_flags bit set: with FTQ_V1_KFP8 the key part is d
+ * bytes of fp8 and no norm (BoundaryTurboQuantConfig.key_packed_size with
+ * key_fp8, boundary_tq_config.py:66-73). */
+int64_t ftq_v1_slot_bytes_flags(int d, int key_bits, int value_bits, int v_flags);
 
 /*
  * Store n_tokens x num_kv_heads K/V vectors ([n][Hkv][d], dtype) into their
@@ -194,7 +208,11 @@ int64_t ftq_v1_slot_bytes(int d, int key_bits, int value_bits);
  * bit 0) stores V as Lloyd-Max codes instead (TURBOQUANT_V_LLOYD_MAX): the
  * rotated V is normalised and coded against `midpoints` like K, its fp16 norm
  * goes to the scale field and 0 to the min field (v1_backend.py:736-749,
- * triton_inkernel_store.py:159-200).
+ * triton_inkernel_store.py:159-200); bit 2 stores K as fp8 e4m3fn
+ * (key_bits 8; y * norm rounded to nearest even, saturating at +-448; no
+ * norm; `midpoints` unused, triton_inkernel_store.py:59-83).  1-bit codes
+ * (:138-146, :205-229) and 8-bit K / V (:132-137, 8-bit V :202-330) as the
+ * reference packs them.
  * slot_mapping[i] < 0 skips token i.  Replaces _launch_rht / _fused_store_rht
  * (vllm_plugin/triton_inkernel_store.py:376-440, 554-616) and the V
  * pre-rotation of _launch_store (v1_backend.py:712-749).  One launch.
@@ -251,12 +269,16 @@ int ftq_v1_default_splits(int batch, int num_kv_heads, int max_seq_len);
  * against the norm-corrected centroids (2^key_bits sorted float32) times the
  * fp16 K norm; V = code * scale + min; with v_rotate the output is multiplied
  * by H/sqrt(d).  v_rotate bit 1 (as in ftq_v1_store) reads Lloyd-Max V
- * codes: V = c[code] * ||v|| / ||c[codes]|| (triton_decode_offset.py:399-419).
- * Rows with no positions give 0.  Replaces the stage-1 kernel
+ * codes: V = c[code] * ||v|| / ||c[codes]|| (triton_decode_offset.py:399-419);
+ * bit 2 reads fp8 keys (scores q_rot . k_fp8, :174-192; `centroids` unused
+ * then).  Rows with no positions give 0.  Replaces the stage-1 kernel
  * _tq_decode_stage1_offset (vllm_plugin/triton_decode_offset.py:42-442), the
  * stage-2 merge, the un-rotation and the output cast of
- * _decode_attention_offset_only (v1_backend.py:975-1093).  Head dim 128.
- * Two launches on `stream`: split-K stage 1, then merge.
+ * _decode_attention_offset_only (v1_backend.py:975-1093).  Head dim 64, 128
+ * or 256.  Two launches on `stream`: split-K stage 1, then merge.  Head dim
+ * 128 with 2-4 bit codes runs the matrix-core kernels (f16 operands, fp32
+ * accumulation); every other format, or v_rotate bit 3, runs a kernel with
+ * every product in fp32 on the VALU (the reference's arithmetic).
  */
 int ftq_v1_decode_attention(const void* query, int q_dtype, const uint8_t* kv_cache,
                             int64_t num_blocks, int block_size, int64_t stride_block,

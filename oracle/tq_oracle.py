@@ -373,16 +373,17 @@ def paged_unpack(cache: np.ndarray, d: int, bk: int, bv: int):
 # --------------------------------------------------------------------------
 
 
-def v1_geometry(d: int, kb: int, vb: int) -> dict:
+def v1_geometry(d: int, kb: int, vb: int, key_fp8: bool = False) -> dict:
     """Byte offsets inside one (token, kv head) slot.
 
     ``[K codes: mse][K norm f16][V codes: vdb][V scale f16][V zero f16][pad]``;
-    key_packed_size = mse + 2 (boundary_tq_config.py:66-75), value data bytes =
-    ceil(d * vb / 8) (:77-81), raw = kps + vdb + 4, slot = next power of 2
-    (v1_backend.py:206-209, boundary protection off).
+    key_packed_size = mse + 2 (boundary_tq_config.py:66-75), or d with fp8
+    keys and no norm (:66-73); value data bytes = ceil(d * vb / 8), d at 8 bits
+    (:77-81); raw = kps + vdb + 4, slot = next power of 2 (v1_backend.py:206-209,
+    boundary protection off).
     """
-    mse = -(-d * kb // 8)
-    kps = mse + 2
+    mse = d if key_fp8 else -(-d * kb // 8)
+    kps = mse if key_fp8 else mse + 2
     vdb = d if vb == 8 else -(-d * vb // 8)
     raw = kps + vdb + 4
     slot = 1 << (raw - 1).bit_length()
@@ -443,6 +444,41 @@ def v1_k_rotate(k: np.ndarray, rotation=None, blockdiag=None):
     return y, norm
 
 
+def f32_to_e4m3(x: np.ndarray) -> np.ndarray:
+    """float32 -> fp8 e4m3fn bytes (bias 7, 3 mantissa bits, no infinities,
+    0x7f / 0xff NaN), rounding to nearest even and saturating at +-448 --
+    the reference's ``y.to(tl.float8e4nv)`` of the fp8-key store
+    (triton_inkernel_store.py:76-82), whose out-of-range behaviour
+    (saturation) is parity unpinned: torch's own e4m3fn conversion gives NaN
+    there, and the two agree below 464.  Each byte is the encoding whose value
+    is nearest in float64 (ties to the even mantissa)."""
+    x = np.asarray(x, np.float32)
+    codes = np.arange(256, dtype=np.uint32)
+    vals = e4m3_to_f32(codes).astype(np.float64)
+    pos = codes[:127][np.argsort(vals[:127])]  # 0x00 .. 0x7e: +0 .. 448, increasing
+    pv = vals[pos]
+    a = np.abs(x.astype(np.float64))
+    i = np.clip(np.searchsorted(pv, a, side="left"), 1, pos.size - 1)
+    lo, hi = pv[i - 1], pv[i]
+    take_hi = (a - lo > hi - a) | ((a - lo == hi - a) & ((pos[i] & 1) == 0))
+    out = np.where(take_hi, pos[i], pos[i - 1])
+    out = np.where(a >= 448.0, 0x7E, out)  # saturate (infinities included)
+    out = np.where(np.isnan(x), 0x7F, out)
+    sign = (x.view(np.uint32) >> 24) & 0x80
+    return (out | sign).astype(np.uint8)
+
+
+def e4m3_to_f32(b: np.ndarray) -> np.ndarray:
+    """fp8 e4m3fn bytes -> float32: (-1)^s 2^(e-7) (1 + m/8) for e > 0,
+    (-1)^s m 2^-9 for e = 0, NaN for 0x7f / 0xff."""
+    b = np.asarray(b).astype(np.uint32)
+    e = (b >> 3) & 15
+    m = b & 7
+    v = np.where(e == 0, m * 2.0 ** -9, (1.0 + m / 8.0) * np.exp2(e.astype(np.float64) - 7.0))
+    v = np.where((e == 15) & (m == 7), np.nan, v)
+    return np.where(b & 0x80, -v, v).astype(np.float32)
+
+
 def v1_quantize_v(v: np.ndarray, vb: int):
     """Per-vector uniform min/max quantiser (triton_inkernel_store.py:202-330).
 
@@ -493,7 +529,8 @@ def v1_quantize_v_lloyd(v: np.ndarray, midpoints: np.ndarray):
 
 def v1_store(key: np.ndarray, value: np.ndarray, slot_mapping: np.ndarray, kv_cache: np.ndarray,
              midpoints: np.ndarray, kb: int, vb: int, v_rotate: bool = False,
-             value_dtype: str = "f32", v_lloyd_max: bool = False, rotation=None, blockdiag=None):
+             value_dtype: str = "f32", v_lloyd_max: bool = False, rotation=None, blockdiag=None,
+             key_fp8: bool = False):
     """Write [N, H, d] float32 K/V (already converted from their dtype) into
     ``kv_cache`` uint8[nb, bs, H, slot] in place.  Negative slots are skipped
     (triton_inkernel_store.py:394-395).  With ``v_rotate`` V is first rotated
@@ -502,7 +539,9 @@ def v1_store(key: np.ndarray, value: np.ndarray, slot_mapping: np.ndarray, kv_ca
     midpoints, its norm goes in the scale field and the min field is 0
     (triton_inkernel_store.py:159-200); other V widths keep the uniform codes.
     ``blockdiag`` = (coeffs [B, d], B): a block-diagonal strategy, K and the
-    rotated V formed by v1_blockdiag_rotate.
+    rotated V formed by v1_blockdiag_rotate.  With ``key_fp8`` (key bits 8) K
+    is stored as fp8 e4m3fn bytes of y * norm and no norm
+    (triton_inkernel_store.py:59-83).
 
     Returns a dict of per-(token, head) intermediates for tie accounting.
     """
@@ -511,9 +550,12 @@ def v1_store(key: np.ndarray, value: np.ndarray, slot_mapping: np.ndarray, kv_ca
     N, H, d = key.shape
     nb, bs, Hc, slot = kv_cache.shape
     assert Hc == H
-    g = v1_geometry(d, kb, vb)
+    g = v1_geometry(d, kb, vb, key_fp8)
     y, norm = v1_k_rotate(key, rotation, blockdiag)
-    kcodes = v1_quantize_k(y, midpoints)
+    if key_fp8:
+        kcodes = f32_to_e4m3((y * norm[..., None]).astype(np.float32))
+    else:
+        kcodes = v1_quantize_k(y, midpoints)
     if v_rotate:
         if blockdiag is not None:
             vr = v1_blockdiag_rotate(value, *blockdiag)
@@ -527,7 +569,7 @@ def v1_store(key: np.ndarray, value: np.ndarray, slot_mapping: np.ndarray, kv_ca
         mn = np.zeros_like(sc)
     else:
         vq, sc, mn, t = v1_quantize_v(value, vb)
-    kp = pack(kcodes, kb)
+    kp = kcodes if key_fp8 else pack(kcodes, kb)
     vp = pack(vq, vb)
     n16 = norm.astype(np.float16).view(np.uint8).reshape(N, H, 2)
     sc16 = sc.astype(np.float16).view(np.uint8).reshape(N, H, 2)
@@ -539,20 +581,26 @@ def v1_store(key: np.ndarray, value: np.ndarray, slot_mapping: np.ndarray, kv_ca
         blk, off = divmod(s, bs)
         row = kv_cache[blk, off]
         row[:, 0:g["mse"]] = kp[i]
-        row[:, g["mse"]:g["kps"]] = n16[i]
+        if not key_fp8:
+            row[:, g["mse"]:g["kps"]] = n16[i]
         row[:, g["kps"]:g["kps"] + g["vdb"]] = vp[i]
         row[:, g["kps"] + g["vdb"]:g["kps"] + g["vdb"] + 2] = sc16[i]
         row[:, g["kps"] + g["vdb"] + 2:g["raw"]] = mn16[i]
     return dict(y=y, norm=norm, kcodes=kcodes, vcodes=vq, vscale=sc, vmin=mn, vt=t, value=value)
 
 
-def v1_unpack(kv_cache: np.ndarray, d: int, kb: int, vb: int):
+def v1_unpack(kv_cache: np.ndarray, d: int, kb: int, vb: int, key_fp8: bool = False):
     """uint8[nb, bs, H, slot] -> (K codes, K norm f16, V codes, V scale f16,
-    V zero f16), codes [nb, bs, H, d]."""
-    g = v1_geometry(d, kb, vb)
+    V zero f16), codes [nb, bs, H, d].  With ``key_fp8`` the K "codes" are the
+    fp8 bytes and the K norm is None."""
+    g = v1_geometry(d, kb, vb, key_fp8)
     c = np.asarray(kv_cache)
-    kc = unpack(c[..., :g["mse"]], kb, d)
-    kn = c[..., g["mse"]:g["kps"]].copy().view(np.float16)[..., 0]
+    if key_fp8:
+        kc = c[..., :d].copy()
+        kn = None
+    else:
+        kc = unpack(c[..., :g["mse"]], kb, d)
+        kn = c[..., g["mse"]:g["kps"]].copy().view(np.float16)[..., 0]
     vc = unpack(c[..., g["kps"]:g["kps"] + g["vdb"]], vb, d)
     sc = c[..., g["kps"] + g["vdb"]:g["kps"] + g["vdb"] + 2].copy().view(np.float16)[..., 0]
     zr = c[..., g["kps"] + g["vdb"] + 2:g["raw"]].copy().view(np.float16)[..., 0]
@@ -560,18 +608,22 @@ def v1_unpack(kv_cache: np.ndarray, d: int, kb: int, vb: int):
 
 
 def v1_dequant(kv_cache: np.ndarray, d: int, kb: int, vb: int, centroids: np.ndarray,
-               norm_correction: bool = True, v_lloyd_max: bool = False):
+               norm_correction: bool = True, v_lloyd_max: bool = False, key_fp8: bool = False):
     """Per-slot reconstructions in the rotated domain (float64):
     K^ = ||k||_16 * c / sqrt(sum c^2 + 1e-16)  (triton_decode_offset.py:210-242),
     V^ = q * scale_16 + zero_16               (:256-428), or with
     ``v_lloyd_max`` and 4-bit V V^ = ||v||_16 * c_v / sqrt(sum c_v^2 + 1e-16)
-    (:399-419; the scale field holds ||v||, the K centroids are shared)."""
-    kc, kn, vc, sc, zr = v1_unpack(kv_cache, d, kb, vb)
-    cs = np.sort(np.asarray(centroids, np.float32)).astype(np.float64)
-    c = cs[kc]
-    if norm_correction:
-        c = c / np.sqrt(np.sum(c * c, axis=-1, keepdims=True) + 1e-16)
-    k_hat = c * kn.astype(np.float64)[..., None]
+    (:399-419; the scale field holds ||v||, the K centroids are shared).
+    fp8 keys: K^ = the fp8 values themselves (:174-192)."""
+    kc, kn, vc, sc, zr = v1_unpack(kv_cache, d, kb, vb, key_fp8)
+    cs = np.sort(np.asarray(centroids, np.float32)).astype(np.float64) if centroids is not None else None
+    if key_fp8:
+        k_hat = e4m3_to_f32(kc).astype(np.float64)
+    else:
+        c = cs[kc]
+        if norm_correction:
+            c = c / np.sqrt(np.sum(c * c, axis=-1, keepdims=True) + 1e-16)
+        k_hat = c * kn.astype(np.float64)[..., None]
     if v_lloyd_max and vb == 4:
         cv = cs[np.minimum(vc, cs.size - 1)]
         if norm_correction:
@@ -585,7 +637,7 @@ def v1_decode_attention(q: np.ndarray, kv_cache: np.ndarray, block_table: np.nda
                         seq_lens: np.ndarray, centroids: np.ndarray, kb: int, vb: int,
                         scale: float, kv_start=None, v_rotate: bool = False,
                         norm_correction: bool = True, v_lloyd_max: bool = False,
-                        rotation=None):
+                        rotation=None, key_fp8: bool = False):
     """Decode attention over the v1 slot cache, float64.
 
     q [B, Hq, d] (float32 values of the query); q_rot = q @ M with
@@ -601,7 +653,7 @@ def v1_decode_attention(q: np.ndarray, kv_cache: np.ndarray, block_table: np.nda
     G = Hq // Hkv
     M = sylvester(d) / math.sqrt(d) if rotation is None else np.asarray(rotation, np.float64)
     q_rot = q @ M
-    k_hat, v_hat = v1_dequant(kv_cache, d, kb, vb, centroids, norm_correction, v_lloyd_max)
+    k_hat, v_hat = v1_dequant(kv_cache, d, kb, vb, centroids, norm_correction, v_lloyd_max, key_fp8)
     out = np.zeros((B, Hq, d))
     for b in range(B):
         L = int(seq_lens[b])

@@ -71,3 +71,57 @@ def test_quantizer_routing():
     cache.set_layer_quantizer_v(0, v_tq)
     assert cache.get_layer_quantizer(0) is k_tq and cache.get_layer_quantizer_v(0) is v_tq
     assert cache.get_layer_quantizer(7) is k_tq  # unregistered layer -> default
+
+
+class _ResettableCache:
+    """A transformers DynamicCache with the ``reset()`` the smoke test calls."""
+
+    def __new__(cls):
+        from transformers import DynamicCache
+
+        class _C(DynamicCache):
+            def reset(self):
+                self.__init__()
+        return _C()
+
+
+def _swap_attention(model, make):
+    """Replace every self-attention forward by make(original); returns the originals."""
+    originals = {}
+    for name, module in model.named_modules():
+        if name.endswith("self_attn"):
+            originals[name] = module.forward
+            module.forward = make(module.forward)
+    return originals
+
+
+def test_smoke_test_compares_against_unpatched_logits():
+    """The verify step runs prompt + decode through the patched forwards and
+    the same tokens through the originals, and passes on identical paths
+    (cosine 1), leaving the patched forwards installed."""
+    from fused_turboquant.hf import fused_cache as FC
+    model = _tiny_llama().eval()
+    originals = _swap_attention(model, lambda f: (lambda *a, **k: f(*a, **k)))
+    patched = {n: m.forward for n, m in model.named_modules() if n in originals}
+    cos = FC._smoke_test(model, _ResettableCache(), originals, model.config)
+    assert cos == pytest.approx(1.0, abs=1e-5)
+    assert all(m.forward is patched[n] for n, m in model.named_modules() if n in originals)
+
+
+def test_smoke_test_rejects_a_wrong_attention_path():
+    """A patched attention that returns the wrong output (negated here, on the
+    CPU) drives the logit cosine below 0.8 and fails the verify step; the
+    patched forwards are still the installed ones afterwards."""
+    from fused_turboquant.hf import fused_cache as FC
+    model = _tiny_llama().eval()
+
+    def wrong(f):
+        def fwd(*a, **k):
+            out = f(*a, **k)
+            return (-4.0 * out[0],) + tuple(out[1:])
+        return fwd
+    originals = _swap_attention(model, wrong)
+    patched = {n: m.forward for n, m in model.named_modules() if n in originals}
+    with pytest.raises(RuntimeError, match="cosine similarity"):
+        FC._smoke_test(model, _ResettableCache(), originals, model.config)
+    assert all(m.forward is patched[n] for n, m in model.named_modules() if n in originals)

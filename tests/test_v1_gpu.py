@@ -237,6 +237,12 @@ def test_config4_full_size(cuda):
                                      layer.centroids.cpu().numpy(), kb, vb, 1 / math.sqrt(d),
                                      v_rotate=True)
         _check_attn(o1[b:b + 1, kvh * 4:kvh * 4 + 4], want, f"config4 b={b} kvh={kvh} ctx={L}")
+        # the north-star bound itself (max <= 2e-2, mean <= 2e-3, no widening)
+        # on the fp32 outputs, where no output rounding is added
+        for s, o32 in zip((8, 64), f32):
+            err = np.abs(o32[b:b + 1, kvh * 4:kvh * 4 + 4].astype(np.float64) - want)
+            print(f"[config4 fp32 out S={s} b={b} kvh={kvh}] max {err.max():.2e} mean {err.mean():.2e}")
+            assert err.max() <= 2e-2 and err.mean() <= 2e-3, (s, b, kvh)
 
 
 @pytest.mark.parametrize("kb", [2, 3, 4])
