@@ -27,6 +27,7 @@
 #include "ftq_device.h"
 #include "ftq_internal.h"
 #include "ftq_merge.h"
+#include "ftq_v1_dev.h"
 
 namespace ftq {
 
@@ -453,13 +454,14 @@ extern "C" int ftq_raw_decode_attention_lse(
     int max_blocks_per_seq, const int32_t* seq_lens, const int32_t* kv_start, int batch,
     int num_q_heads, int num_kv_heads, int d, float scale, int num_splits, void* workspace,
     int64_t workspace_bytes, void* out, int out_dtype, float* lse_out, void* stream) {
-  FTQ_REQUIRE(d == 128, "raw decode attention: head_dim must be 128");
+  FTQ_REQUIRE(d == 64 || d == 128 || d == 256, "raw decode attention: head_dim must be 64, 128 or 256");
   FTQ_REQUIRE(block_size >= 16 && block_size <= 4096 && (block_size & (block_size - 1)) == 0,
               "block_size must be a power of two in [16, 4096]");
   FTQ_REQUIRE(batch >= 0 && num_kv_heads > 0 && num_q_heads > 0 && num_blocks >= 0,
               "bad batch / head / block counts");
   FTQ_REQUIRE(num_q_heads % num_kv_heads == 0, "num_q_heads must be a multiple of num_kv_heads");
-  FTQ_REQUIRE(num_q_heads / num_kv_heads <= 8, "raw decode attention: GQA group must be <= 8");
+  FTQ_REQUIRE(num_q_heads / num_kv_heads <= (d == 128 ? 8 : 16),
+              "raw decode attention: GQA group must be <= 8 at head_dim 128, <= 16 otherwise");
   FTQ_REQUIRE(num_splits >= 1 && num_splits <= 1024, "num_splits must be in [1, 1024]");
   FTQ_REQUIRE(max_blocks_per_seq >= 0, "max_blocks_per_seq must be >= 0");
   FTQ_REQUIRE(q_dtype >= F32 && q_dtype <= BF16 && out_dtype >= F32 && out_dtype <= BF16,
@@ -477,6 +479,19 @@ extern "C" int ftq_raw_decode_attention_lse(
               "workspace too small (see ftq_raw_workspace_bytes)");
   FTQ_REQUIRE(aligned16(query) && aligned16(out) && aligned16(workspace) && aligned16(kv_cache),
               "query, out, workspace and kv_cache must be 16-byte aligned");
+  if (d != 128) {  // head_dim 64 / 256: the fp32 VALU kernel over the same slots
+    V1Args v;
+    v.q = query; v.qt = q_dtype; v.cache = kv_cache; v.bt = block_table; v.sl = seq_lens; v.ks = kv_start;
+    v.B = batch; v.hq = num_q_heads; v.hkv = num_kv_heads; v.max_blocks = max_blocks_per_seq;
+    v.lbs = 0;
+    while ((1 << v.lbs) < block_size) ++v.lbs;
+    v.nb = num_blocks; v.sblk = stride_block; v.spos = stride_pos; v.shead = stride_head;
+    v.cent = nullptr; v.qscale = scale * 1.4426950408889634f; v.splits = num_splits; v.vrot = 0;
+    v.wo = static_cast<float*>(workspace);
+    v.wl = v.wo + (int64_t)batch * num_q_heads * num_splits * d;
+    v.out = out; v.ot = out_dtype; v.lse = lse_out; v.rot = nullptr;
+    return hip_status(raw_valu_launch(v, d, (hipStream_t)stream));
+  }
   RawArgs a;
   a.q = query; a.qt = q_dtype; a.cache = kv_cache; a.bt = block_table; a.sl = seq_lens; a.ks = kv_start;
   a.B = batch; a.hq = num_q_heads; a.hkv = num_kv_heads; a.max_blocks = max_blocks_per_seq;

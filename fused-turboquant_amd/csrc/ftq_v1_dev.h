@@ -80,5 +80,8 @@ bool v1_widths_ok(int kb, int vb, int flags);
 // The fp32 VALU decode (any head_dim of 64, 128, 256; every code width);
 // defined in ftq_v1_valu.hip.
 hipError_t v1_valu_launch(const V1Args& a, int d, int kb, int vb, int flags, hipStream_t st);
+// The same kernel over raw fp16 [K | V] slots (boundary layers; a.vrot = 0,
+// a.rot = null, a.qscale = scale * log2 e).
+hipError_t raw_valu_launch(const V1Args& a, int d, hipStream_t st);
 
 }  // namespace ftq

@@ -5,7 +5,10 @@
 // e4m3fn keys; V codes of 1, 2, 3, 4 or 8 bits, uniform or Lloyd-Max (4-bit).
 // The matrix-core kernels of ftq_v1.hip cover head_dim 128 with 2-4 bit codes
 // at f16 operand precision; this kernel is the path for everything else, and
-// for callers that ask for fp32 products.
+// for callers that ask for fp32 products.  The same kernel reads the raw fp16
+// [K | V] slots of the boundary layers (KB = VB = 16: no codes, no norms, no
+// rotation; reference triton_boundary_attn.py:28-219) at head_dim 64 and 256,
+// where ftq_raw.hip's matrix-core kernel covers 128.
 //
 // Per split (one workgroup of 4 waves per (batch, kv head, group of <= 4 query
 // heads, split)); a wave takes every 4th 16-token S-tile of the split.
@@ -105,7 +108,9 @@ __device__ __forceinline__ void load_bytes(__amdgpu_buffer_rsrc_t rs, uint32_t o
 
 template <int D, int KB, int VB, bool KF8, bool VLM>
 struct VGeo {
-  static constexpr V1Geom G = v1_geom(D, KB, VB, KF8);
+  static constexpr bool RAW = KB == 16;      // raw fp16 K and V: [K 2D bytes][V 2D bytes]
+  static constexpr V1Geom G = RAW ? V1Geom{2 * D, 2 * D, 2 * D, 4 * D} : v1_geom(D, KB, VB, KF8);
+  static constexpr bool VA4 = RAW;           // V chunks at 4-byte aligned offsets
   static constexpr int KQ = D * KB / 32;     // K bytes of one quarter of a vector
   static constexpr int KQW = (KQ + 3) / 4;
   static constexpr int DG = D / 8;           // P.V dim groups (8 dims each)
@@ -114,7 +119,7 @@ struct VGeo {
   static constexpr int VW = (VB * 8 + 31) / 32;  // dwords of one token's 8 V codes
   static constexpr int VTB = D / 8;          // Lloyd-Max V: V code bytes of one quarter (4-bit codes)
   static constexpr int VTW = VLM ? (VTB + 3) / 4 : 1;
-  static constexpr int KTB = KF8 ? 8 : KB;   // bits of a K table index
+  static constexpr int KTB = RAW ? 0 : KF8 ? 8 : KB;  // bits of a K table index (no table for raw K)
   static constexpr int QG = D + 4;           // floats per query quarter (4 heads x D/4 dims, padded)
 };
 
@@ -141,14 +146,18 @@ __device__ __forceinline__ void vtile_load(VTile<D, KB, VB, KF8, VLM>& r, const 
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(bst), (short)0, (int)(16u * s_pos), 0x00020000);
   const uint32_t row = (uint32_t)m * s_pos;
   load_bytes<Q::KQ, true>(rs, row + (uint32_t)(g * Q::KQ), r.k);
-  r.kn = KF8 ? 0u : (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, row + Q::G.mse, 0, 0);
-  r.vs = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, row + Q::G.kps + Q::G.vdb, 0, 0);
-  r.vm = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, row + Q::G.kps + Q::G.vdb + 2, 0, 0);
+  if constexpr (Q::RAW) {
+    r.kn = r.vs = r.vm = 0u;
+  } else {
+    r.kn = KF8 ? 0u : (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, row + Q::G.mse, 0, 0);
+    r.vs = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, row + Q::G.kps + Q::G.vdb, 0, 0);
+    r.vm = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, row + Q::G.kps + Q::G.vdb + 2, 0, 0);
+  }
   if constexpr (VLM) load_bytes<Q::VTB, false>(rs, row + Q::G.kps + (uint32_t)(g * Q::VTB), r.vt);
 #pragma unroll
   for (int i = 0; i < Q::TPL; ++i) {
     const uint32_t t = (uint32_t)(tg * Q::TPL + i);
-    load_bytes<VB, false>(rs, t * s_pos + Q::G.kps + (uint32_t)(dg * VB), r.v[i]);
+    load_bytes<VB, Q::VA4>(rs, t * s_pos + Q::G.kps + (uint32_t)(dg * VB), r.v[i]);
   }
   r.ok = ok;
 }
@@ -164,7 +173,7 @@ __global__ __launch_bounds__(256, 2) void v1_attn_valu_kernel(
   constexpr int E16 = D / 16;                 // query elements per lane in the prologue
   // K table entries; Lloyd-Max V reads it with 4-bit codes, and codes at or
   // above 2^KB (never stored) read the top centroid
-  constexpr int NK = (VLM && Q::KTB < 4) ? 16 : 1 << Q::KTB;
+  constexpr int NK = Q::RAW ? 0 : (VLM && Q::KTB < 4) ? 16 : 1 << Q::KTB;
   constexpr int TAB_BYTES = NK * 32 * 4;
   constexpr int RED_BYTES = NW * GM * (D + 1) * 4;
   constexpr int ROT_BYTES = GM * D * 4;
@@ -198,8 +207,10 @@ __global__ __launch_bounds__(256, 2) void v1_attn_valu_kernel(
 #pragma unroll
       for (int i = 0; i < E16; ++i) y[i] = 0.f;
     }
-    if (rot != nullptr) rot_matrix_lanes<D, E16>(y, rot, reinterpret_cast<float*>(pool) + hh * D, l16);
-    else fwht_lanes<E16, 16>(y, l16);
+    if constexpr (!Q::RAW) {  // raw K is not rotated
+      if (rot != nullptr) rot_matrix_lanes<D, E16>(y, rot, reinterpret_cast<float*>(pool) + hh * D, l16);
+      else fwht_lanes<E16, 16>(y, l16);
+    }
 #pragma unroll
     for (int i = 0; i < E16; ++i) {
       const int d = l16 * E16 + i, qq = d / (D / 4), di = d % (D / 4);
@@ -208,11 +219,13 @@ __global__ __launch_bounds__(256, 2) void v1_attn_valu_kernel(
   }
   __syncthreads();  // the prologue rows are dead: the pool takes the K table
   float* ktab = reinterpret_cast<float*>(pool);
-  for (int e = tid; e < NK * 32; e += NW * 64) {
-    const int c = e >> 5;
-    ktab[e] = KF8 ? e4m3_to_f32((uint32_t)c) : cent[c < (1 << KB) ? c : (1 << KB) - 1];
+  if constexpr (!Q::RAW) {
+    for (int e = tid; e < NK * 32; e += NW * 64) {
+      const int c = e >> 5;
+      ktab[e] = KF8 ? e4m3_to_f32((uint32_t)c) : cent[c < (1 << KB) ? c : (1 << KB) - 1];
+    }
+    __syncthreads();
   }
-  __syncthreads();
   const uint32_t tab = lds_addr(ktab) + 4u * (uint32_t)(lane & 31);
   auto tabv = [&](uint32_t c) __attribute__((always_inline)) {
     return *(__attribute__((address_space(3))) const float*)(uintptr_t)(tab + (c << 7));
@@ -258,18 +271,20 @@ __global__ __launch_bounds__(256, 2) void v1_attn_valu_kernel(
     float csq = 0.f;
 #pragma unroll
     for (int i = 0; i < D / 4; ++i) {
-      const float c = tabv(code_at<Q::KTB>(cur.k, i));
+      float c;
+      if constexpr (Q::RAW) c = (float)__builtin_bit_cast(_Float16, (uint16_t)code_at<16>(cur.k, i));
+      else c = tabv(code_at<Q::KTB>(cur.k, i));
       const f32x4 q4 = *(__attribute__((address_space(3))) const f32x4*)(uintptr_t)(qaddr + 16u * (uint32_t)i);
       dot[0] = __builtin_fmaf(q4.x, c, dot[0]);
       dot[1] = __builtin_fmaf(q4.y, c, dot[1]);
       dot[2] = __builtin_fmaf(q4.z, c, dot[2]);
       dot[3] = __builtin_fmaf(q4.w, c, dot[3]);
-      if constexpr (!KF8) csq = __builtin_fmaf(c, c, csq);
+      if constexpr (!KF8 && !Q::RAW) csq = __builtin_fmaf(c, c, csq);
     }
     const int pos = j * 16 + m;
     const bool live = cur.ok && pos >= k0 && pos < seq_len;
     float kf = 1.f;
-    if constexpr (!KF8) {
+    if constexpr (!KF8 && !Q::RAW) {
       const float kn = (float)__builtin_bit_cast(_Float16, (uint16_t)cur.kn);
       kf = kn / __builtin_sqrtf(warp_sum_q(csq) + 1e-16f);
     }
@@ -283,7 +298,9 @@ __global__ __launch_bounds__(256, 2) void v1_attn_valu_kernel(
     // that are not attended, whose fields may hold anything
     float wf, zm = 0.f;
     const float vs = (float)__builtin_bit_cast(_Float16, (uint16_t)cur.vs);
-    if constexpr (VLM) {
+    if constexpr (Q::RAW) {
+      wf = 1.f;
+    } else if constexpr (VLM) {
       float vsq = 0.f;
 #pragma unroll
       for (int i = 0; i < D / 4; ++i) {
@@ -339,7 +356,9 @@ __global__ __launch_bounds__(256, 2) void v1_attn_valu_kernel(
 #pragma unroll
       for (int jj = 0; jj < 8; ++jj) {
         const uint32_t cd = code_at<VB>(cur.v[i], jj);
-        const float val = VLM ? tabv(cd) : (float)cd;
+        float val;
+        if constexpr (Q::RAW) val = (float)__builtin_bit_cast(_Float16, (uint16_t)cd);
+        else val = VLM ? tabv(cd) : (float)cd;
         acc[jj][0] = __builtin_fmaf(w4.x, val, acc[jj][0]);
         acc[jj][1] = __builtin_fmaf(w4.y, val, acc[jj][1]);
         acc[jj][2] = __builtin_fmaf(w4.z, val, acc[jj][2]);
@@ -474,6 +493,17 @@ hipError_t merge_d(const V1Args& a, hipStream_t st) {
 }
 
 }  // namespace
+
+hipError_t raw_valu_launch(const V1Args& a, int d, hipStream_t st) {
+  hipError_t e;
+  if (d == 64) e = launch_valu<64, 16, 16, false, false>(a, st);
+  else if (d == 128) e = launch_valu<128, 16, 16, false, false>(a, st);
+  else e = launch_valu<256, 16, 16, false, false>(a, st);
+  if (e != hipSuccess) return e;
+  if (d == 64) return merge_d<64>(a, st);
+  if (d == 128) return merge_d<128>(a, st);
+  return merge_d<256>(a, st);
+}
 
 hipError_t v1_valu_launch(const V1Args& a, int d, int kb, int vb, int flags, hipStream_t st) {
   const bool kf8 = (flags & V1F_KFP8) != 0, vlm = (flags & V1F_VLM) != 0;

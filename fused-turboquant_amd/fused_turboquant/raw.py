@@ -108,20 +108,20 @@ def raw_decode_attention(query: torch.Tensor, kv_cache: torch.Tensor, block_tabl
     """query [B, Hq, d] -> [B, Hq, d] (query dtype unless ``out`` is given).
 
     Attends positions [kv_start[b], seq_lens[b]) of block-table row b over the
-    raw fp16 slots.  ``num_splits`` defaults to a value that fills the GPU
+    raw fp16 slots.  Head dim 128 runs the matrix-core kernel (GQA group <= 8);
+    64 and 256 the fp32 VALU kernel (group <= 16).  ``num_splits`` defaults to a value that fills the GPU
     (pass ``max_seq_len`` to size it without reading ``block_table``'s width);
     ``workspace`` (uint8, >= ``workspace_bytes``) may be preallocated.
     ``lse`` (float32 [B, Hq]) receives each row's natural-log log-sum-exp of
     the scaled scores (-inf for a row with no positions).
     """
     B, hq, d = query.shape
-    if d != 128:
-        raise ValueError("raw decode attention supports head_dim 128")
     nb, bs, hkv, slot = kv_cache.shape
     if slot < raw_slot_bytes(d):
         raise ValueError("kv_cache slot is smaller than 4 * head_dim bytes")
-    if hq % hkv != 0 or hq // hkv > 8:
-        raise ValueError("num_q_heads must be a multiple of num_kv_heads with a group of at most 8")
+    gmax = 8 if d == 128 else 16
+    if hq % hkv != 0 or hq // hkv > gmax:
+        raise ValueError(f"num_q_heads must be a multiple of num_kv_heads with a group of at most {gmax}")
     if block_table.dtype != torch.int32 or seq_lens.dtype != torch.int32:
         raise ValueError("block_table and seq_lens must be int32")
     if block_table.dim() != 2 or block_table.shape[0] != B or seq_lens.numel() != B:

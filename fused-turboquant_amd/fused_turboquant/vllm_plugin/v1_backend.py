@@ -27,8 +27,14 @@ Boundary-protection layers (a plain cache dtype such as ``"auto"``; reference
 ``:335-366``) follow ``TURBOQUANT_BOUNDARY_PROTECT``: ``fp16`` stores raw fp16
 K|V slots (``ftq_raw_store``, the reference's ``_store_raw_kv``, ``:1449-1505``)
 and decodes them with ``ftq_raw_decode_attention`` (the reference's
-``boundary_fp16_decode_attention``, ``triton_boundary_attn.py:28-219``); 2/3/4
-run the TurboQuant path at that width inside the fp16-sized slot.
+``boundary_fp16_decode_attention``, ``triton_boundary_attn.py:28-219``); 2/3/4/8
+run the TurboQuant path at that width inside the fp16-sized slot (8: 256
+Lloyd-Max centroids for K, 8-bit uniform V), and ``fp8`` stores fp8 e4m3fn
+keys with 8-bit uniform values (``boundary_tq_config.py``).
+
+Head sizes 64, 128 and 256.  At 128 with 2-4 bit codes decode runs on the
+matrix-core kernels; every other head size and width (1-bit, 8-bit, fp8
+keys) runs the fp32 decode kernel.
 
 Deferred prefill (``TURBOQUANT_DEFER_PREFILL=1``, TurboQuant layers; reference
 ``:331-332``, ``:673-686``, ``:1095-1277``): a prefill store of 1 < N <=
@@ -185,7 +191,9 @@ class FusedTurboQuantV1Backend(_BackendBase):
 
     @classmethod
     def supports_head_size(cls, head_size: int) -> bool:
-        return head_size == 128
+        # 128: matrix-core decode for 2-4 bit codes; 64 and 256 (and every
+        # other width): the fp32 decode kernel
+        return head_size in (64, 128, 256)
 
     @classmethod
     def supports_compute_capability(cls, capability) -> bool:
@@ -224,23 +232,27 @@ class FusedTurboQuantV1Impl(_ImplBase):
         is_boundary = not (isinstance(kv_cache_dtype, str) and kv_cache_dtype.startswith("turboquant_"))
         mode = boundary_protect_mode()
         self._is_raw = False
+        self.key_fp8 = False
         if is_boundary:
             if mode == "fp16":
                 self._is_raw = True
                 self.preset, self.key_bits, self.value_bits = "raw_fp16", 16, 16
-            elif mode in (2, 3, 4):
+            elif mode in (2, 3, 4, 8):
+                # N-bit Lloyd-Max keys and N-bit uniform values in the fp16-sized slot
+                # (reference BoundaryTurboQuantConfig, boundary_tq_config.py)
                 self.preset, self.key_bits, self.value_bits = f"boundary_{mode}bit", mode, mode
-            elif mode in ("fp8", 8):
-                raise NotImplementedError("8-bit / FP8 boundary layers (TURBOQUANT_BOUNDARY_PROTECT=8 or fp8) "
-                                          "are not part of this build; use 1/fp16 or 2/3/4")
+            elif mode == "fp8":
+                # fp8 e4m3fn keys (no codebook, no norm) and 8-bit uniform values
+                self.preset, self.key_bits, self.value_bits = "boundary_fp8", 8, 8
+                self.key_fp8 = True
             else:
                 raise NotImplementedError(f"kv_cache_dtype={kv_cache_dtype!r} needs a turboquant_* cache dtype "
                                           "when TURBOQUANT_BOUNDARY_PROTECT is off")
         else:
             self.preset, self.key_bits, self.value_bits = host_preset(kv_cache_dtype)
-        if head_size != 128:
-            raise NotImplementedError("the gfx950 decode kernels support head_size 128")
-        group_limit = 8 if self._is_raw else 16
+        if head_size not in (64, 128, 256):
+            raise NotImplementedError("the gfx950 kernels support head_size 64, 128 and 256")
+        group_limit = 8 if (self._is_raw and head_size == 128) else 16
         if num_heads % num_kv_heads != 0 or num_heads // num_kv_heads > group_limit:
             raise ValueError(f"num_heads must be a multiple of num_kv_heads with a group of at most {group_limit}")
         self.num_heads = num_heads
@@ -272,7 +284,7 @@ class FusedTurboQuantV1Impl(_ImplBase):
                 cent = None
             st = V1.TurboQuantV1Layer(self.head_size, self.key_bits, self.value_bits,
                                       v_rotate=self.v_rotate, centroids=cent, device=device,
-                                      v_lloyd_max=self.v_lloyd_max, kind=self.kind)
+                                      v_lloyd_max=self.v_lloyd_max, kind=self.kind, key_fp8=self.key_fp8)
             layer._fused_tq_state = st
         return st
 
@@ -399,7 +411,7 @@ class FusedTurboQuantV1Impl(_ImplBase):
         V1.v1_decode_attention(q, kv_cache, bt, sl, st.centroids, self.key_bits, self.value_bits,
                                scale=self.scale, v_rotate=self.v_rotate, v_lloyd_max=self.v_lloyd_max,
                                kv_start=ks, num_splits=s2, out=o2, lse=l2, rotation=st.rotation,
-                               workspace=ws2, sorted_centroids=True)
+                               workspace=ws2, sorted_centroids=True, key_fp8=self.key_fp8)
         # merge (a row empty in both phases stays 0)
         m = torch.maximum(l1, l2)
         m = torch.where(torch.isneginf(m), torch.zeros_like(m), m)
@@ -429,7 +441,7 @@ class FusedTurboQuantV1Impl(_ImplBase):
         return V1.v1_decode_attention(q, kv_cache, bt, sl, st.centroids, self.key_bits, self.value_bits,
                                       scale=self.scale, v_rotate=self.v_rotate, v_lloyd_max=self.v_lloyd_max,
                                       num_splits=splits, rotation=st.rotation, out=out, workspace=ws,
-                                      sorted_centroids=True)
+                                      sorted_centroids=True, key_fp8=self.key_fp8)
 
     def _prefill(self, q, k, v, kv_cache, md, nd, ndt, st):
         """Prefill sequences nd.. of the batch (tokens ndt..N)."""

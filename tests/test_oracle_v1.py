@@ -444,3 +444,79 @@ def test_blockdiag_rotate_equals_matrix_product(kind):
         cf[e % 3, e] = 1.0
     x = rng.standard_normal((5, 12)).astype(np.float32)
     assert np.array_equal(O.v1_blockdiag_rotate(x, cf, 3), x)
+
+
+def test_fp8_e4m3_matches_torch_in_range_and_saturates():
+    """The fp8-key conversion (reference triton_inkernel_store.py:76-82) is
+    IEEE-style round to nearest even onto e4m3fn: equal to torch's own
+    float8_e4m3fn cast for every value below 464 (subnormals, exact midpoints,
+    powers of two), +-448 above (the reference's saturating cast), and the
+    decode table equals torch's for all 256 bytes."""
+    rng = np.random.default_rng(8)
+    x = np.concatenate([rng.standard_normal(40000).astype(np.float32) * s for s in (1e-3, 3e-2, 1, 40, 300)])
+    vals = O.e4m3_to_f32(np.arange(127))
+    mids = ((vals[:-1].astype(np.float64) + vals[1:]) / 2).astype(np.float32)  # exact ties
+    x = np.concatenate([x, mids, -mids, vals, np.float32([0.0, -0.0, 2.0 ** -10, 463.5, 2.0 ** -6])])
+    got = O.f32_to_e4m3(x)
+    want = torch.from_numpy(x).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    inr = np.abs(x) < 464
+    assert np.array_equal(got[inr], want[inr])
+    big = np.float32([464.0, 1e4, np.inf, -np.inf, -500.0])
+    assert np.array_equal(O.f32_to_e4m3(big), np.uint8([0x7E, 0x7E, 0x7E, 0xFE, 0xFE]))
+    assert O.f32_to_e4m3(np.float32([np.nan]))[0] & 0x7F == 0x7F
+    table = torch.arange(256, dtype=torch.uint8).view(torch.float8_e4m3fn).float().numpy()
+    mine = O.e4m3_to_f32(np.arange(256))
+    assert np.array_equal(np.isnan(mine), np.isnan(table))
+    assert np.array_equal(mine[~np.isnan(mine)], table[~np.isnan(table)])
+
+
+@pytest.mark.parametrize("d", [64, 128, 256])
+def test_fp8_key_store_round_trip(d):
+    """fp8 keys: the stored bytes decode to y * norm within half an fp8 step
+    (3 mantissa bits: 2^-4 relative), no norm field, V region as for MSE keys."""
+    rng = np.random.default_rng(d)
+    k = rng.standard_normal((9, 2, d)).astype(np.float32) * 2
+    v = rng.standard_normal((9, 2, d)).astype(np.float32)
+    g = O.v1_geometry(d, 8, 8, key_fp8=True)
+    assert g["kps"] == g["mse"] == d and g["raw"] == 2 * d + 4
+    cache = np.zeros((2, 8, 2, g["slot"]), np.uint8)
+    st = O.v1_store(k, v, np.arange(9), cache, np.zeros(1, np.float32), 8, 8, key_fp8=True)
+    kc, kn, vc, sc, zr = O.v1_unpack(cache, d, 8, 8, key_fp8=True)
+    assert kn is None
+    x = (st["y"] * st["norm"][..., None]).astype(np.float64)
+    back = O.e4m3_to_f32(kc.reshape(-1, 2, d)[:9]).astype(np.float64)
+    assert np.all(np.abs(back - x) <= 2.0 ** -4 * np.abs(x) + 2.0 ** -10)
+    # y * norm is the rotated key itself: H k / sqrt(d) up to the 1e-8 in the normalisation
+    hk = k.astype(np.float64) @ O.sylvester(d) / math.sqrt(d)
+    assert np.abs(x - hk).max() <= 1e-5 * np.abs(hk).max()
+
+
+@pytest.mark.parametrize("kb,vb,fp8", [(1, 1, False), (1, 4, False), (4, 1, False), (3, 2, False),
+                                       (8, 8, False), (8, 8, True)])
+@pytest.mark.parametrize("d", [64, 128, 256])
+def test_slot_bytes_agree_everywhere(d, kb, vb, fp8):
+    """C ABI (ftq_v1_slot_bytes_flags), Python (v1.slot_bytes) and the oracle
+    give the same slot bytes for every supported width."""
+    import ctypes
+    from fused_turboquant import _lib
+    from fused_turboquant import v1
+    L = _lib.lib()
+    L.ftq_v1_slot_bytes_flags.restype = ctypes.c_int64
+    L.ftq_v1_slot_bytes_flags.argtypes = [ctypes.c_int] * 4
+    want = O.v1_geometry(d, kb, vb, key_fp8=fp8)["raw"]
+    assert v1.slot_bytes(d, kb, vb, key_fp8=fp8) == want
+    assert L.ftq_v1_slot_bytes_flags(d, kb, vb, 4 if fp8 else 0) == want
+
+
+@pytest.mark.parametrize("kb,vb,fp8", [(0, 2, False), (5, 4, False), (8, 4, False), (4, 8, False),
+                                       (4, 4, True), (2, 2, True)])
+def test_unsupported_widths_rejected(kb, vb, fp8):
+    import ctypes
+    from fused_turboquant import _lib
+    from fused_turboquant import v1
+    L = _lib.lib()
+    L.ftq_v1_slot_bytes_flags.restype = ctypes.c_int64
+    L.ftq_v1_slot_bytes_flags.argtypes = [ctypes.c_int] * 4
+    assert L.ftq_v1_slot_bytes_flags(128, kb, vb, 4 if fp8 else 0) == -1
+    with pytest.raises(ValueError):
+        v1.slot_bytes(128, kb, vb, key_fp8=fp8)

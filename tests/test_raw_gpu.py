@@ -156,3 +156,31 @@ def test_bench_shape_full_size(cuda):
         _check(out[b:b + 1], want, torch.bfloat16, f"raw bench shape b={b}")
     other = raw.raw_decode_attention(q, cache, bt, sl, num_splits=1).float().cpu().numpy()
     _check(other, out.astype(np.float64), torch.bfloat16, "raw split invariance")
+
+
+@pytest.mark.parametrize("d", [64, 256])
+@pytest.mark.parametrize("hq,hkv", [(8, 2), (16, 1), (6, 3)])
+def test_decode_parity_head_dims_64_256(cuda, d, hq, hkv):
+    """Head dims 64 and 256 run the fp32 VALU kernel over the same raw slots
+    (fp32 products: the reference's boundary_fp16_decode_attention arithmetic),
+    with kv_start, empty rows and GQA groups up to 16; same bounds."""
+    from fused_turboquant import raw
+    bs, nb = 16, 48
+    g = torch.Generator().manual_seed(d + hq)
+    cache = _oracle_cache(g, nb, bs, hkv, d, nb * bs)
+    lens = [0, 1, 15, 17, 100, 257, 16, 300]
+    starts = [0, 0, 3, 17, 40, 0, 1, 256]
+    B = len(lens)
+    bt = torch.randint(0, nb, (B, 20), generator=g, dtype=torch.int32)
+    q = torch.randn(B, hq, d, generator=g).to(torch.bfloat16)
+    sl = torch.tensor(lens, dtype=torch.int32)
+    ks = torch.tensor(starts, dtype=torch.int32)
+    want = O.raw_decode_attention(q.float().numpy(), cache, bt.numpy(), sl.numpy(), 1 / math.sqrt(d),
+                                  kv_start=ks.numpy())
+    for odt, splits in ((torch.bfloat16, 3), (torch.float32, 16)):
+        out = torch.empty(B, hq, d, dtype=odt, device=cuda)
+        raw.raw_decode_attention(q.to(cuda), torch.from_numpy(cache).to(cuda), bt.to(cuda), sl.to(cuda),
+                                 kv_start=ks.to(cuda), num_splits=splits, out=out)
+        got = out.float().cpu().numpy()
+        assert not got[0].any() and not got[3].any()  # empty row, kv_start == seq_len
+        _check(got, want, odt, f"raw d={d} hq={hq} hkv={hkv} S={splits} out={odt}")

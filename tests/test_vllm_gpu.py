@@ -46,7 +46,7 @@ def _causal_ref(q, k, v, scale):
 
 
 def _run_step(cuda, seqs, dtype_str, hq, hkv, vrot, monkeypatch, seed, bs=16, protect="0", lloyd=False,
-              kind="rht"):
+              kind="rht", D=D):
     """seqs: list of (cached_len, query_len), decodes (query_len 1, cached > 0) first.
     Stores the cached tokens in earlier update calls, then runs one step."""
     from fused_turboquant import vllm_plugin as vp
@@ -124,9 +124,10 @@ def _run_step(cuda, seqs, dtype_str, hq, hkv, vrot, monkeypatch, seed, bs=16, pr
             if raw:
                 want = O.raw_decode_attention(qs[i].float().numpy(), cache_np, btr, sl, 1 / math.sqrt(D))
             else:
-                want = O.v1_decode_attention(qs[i].float().numpy(), cache_np, btr, sl, cent, kb, vb,
+                want = O.v1_decode_attention(qs[i].float().numpy(), cache_np, btr, sl,
+                                             None if impl.key_fp8 else cent, kb, vb,
                                              1 / math.sqrt(D), v_rotate=vrot or lloyd, v_lloyd_max=lloyd,
-                                             rotation=rot)
+                                             rotation=rot, key_fp8=impl.key_fp8)
         kind = "prefill" if c == 0 else ("decode" if q == 1 else "continuation")
         _check(got[a:a + q], want, f"{dtype_str} vrot={vrot} seq{i} {kind} cached={c} q={q}")
 
@@ -160,7 +161,7 @@ def test_no_metadata_zeroes_output(cuda):
     assert not out.any()
 
 
-@pytest.mark.parametrize("protect", ["1", "3"])
+@pytest.mark.parametrize("protect", ["1", "3", "8", "fp8"])
 def test_boundary_layer_mixed_batch(cuda, monkeypatch, protect):
     """A boundary-protection layer (cache dtype "auto", vLLM's bf16 allocation):
     raw fp16 slots by default, 3-bit TurboQuant codes in the fp16-sized slot
@@ -323,3 +324,20 @@ def test_impl_decode_under_graph_capture(cuda, monkeypatch, defer):
         torch.cuda.synchronize()
         assert torch.isfinite(got.float()).all()
         assert torch.equal(got, want), rep
+
+
+@pytest.mark.parametrize("d", [64, 256])
+@pytest.mark.parametrize("dtype_str,protect", [("turboquant_3bit_nc", "0"), ("turboquant_k4v2_nc", "0"),
+                                               ("auto", "1"), ("auto", "fp8")])
+def test_head_sizes_64_256(cuda, monkeypatch, d, dtype_str, protect):
+    """Head sizes 64 and 256 (the fp32 decode kernel; raw fp16 boundary slots
+    likewise): decode, fresh prefill and continuation in one step."""
+    _run_step(cuda, [(40, 1), (700, 1), (0, 21), (129, 9)], dtype_str, 16, 4, d == 256, monkeypatch,
+              seed=d + len(dtype_str), protect=protect, D=d)
+
+
+@pytest.mark.parametrize("dtype_str", ["turboquant_k1v2_nc", "turboquant_k4v1_nc", "turboquant_k1v1_nc"])
+def test_one_bit_aliases(cuda, monkeypatch, dtype_str):
+    """The 1-bit turboquant_k{K}v{V}_nc aliases (reference plugin.py:322): the
+    host preset's slot, 1-bit codes, decode on the fp32 kernel."""
+    _run_step(cuda, [(64, 1), (900, 1), (33, 5)], dtype_str, 32, 8, True, monkeypatch, seed=9)

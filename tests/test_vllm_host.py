@@ -25,6 +25,10 @@ def _clean_env(monkeypatch):
     ("turboquant_k2v4_nc", ("turboquant_k3v4_nc", 2, 4)),
     ("turboquant_k2v2_nc", ("turboquant_3bit_nc", 2, 2)),
     ("turboquant_k3v3_nc", ("turboquant_3bit_nc", 3, 3)),
+    ("turboquant_k1v2_nc", ("turboquant_3bit_nc", 1, 2)),
+    ("turboquant_k1v4_nc", ("turboquant_k3v4_nc", 1, 4)),
+    ("turboquant_k4v1_nc", ("turboquant_4bit_nc", 4, 1)),
+    ("turboquant_k1v1_nc", ("turboquant_3bit_nc", 1, 1)),
 ])
 def test_host_preset(dt, want):
     assert vp.host_preset(dt) == want
@@ -39,7 +43,7 @@ def test_host_preset_env_override(monkeypatch):
         vp.host_preset("turboquant_3bit_nc")
 
 
-@pytest.mark.parametrize("dt", ["fp8", "turboquant_5bit_nc", "turboquant_k1v2_nc", "auto"])
+@pytest.mark.parametrize("dt", ["fp8", "turboquant_5bit_nc", "turboquant_k5v2_nc", "turboquant_k0v2_nc", "auto"])
 def test_host_preset_rejects(dt):
     with pytest.raises(ValueError):
         vp.host_preset(dt)
@@ -72,7 +76,8 @@ def test_backend_surface():
     assert B.supports_kv_cache_dtype("turboquant_k4v2_nc")
     assert B.supports_kv_cache_dtype("turboquant_3bit_nc")
     assert not B.supports_kv_cache_dtype("fp8_e4m3")
-    assert B.supports_head_size(128) and not B.supports_head_size(96)
+    assert B.supports_head_size(128) and B.supports_head_size(64) and B.supports_head_size(256)
+    assert not B.supports_head_size(96)
 
 
 def test_impl_init_and_refusals(monkeypatch):
@@ -88,7 +93,8 @@ def test_impl_init_and_refusals(monkeypatch):
     with pytest.raises(NotImplementedError):
         mk(sliding_window=128)
     with pytest.raises(NotImplementedError):
-        mk(head_size=64)
+        mk(head_size=96)
+    assert mk(head_size=64).head_size == 64 and mk(head_size=256).head_size == 256
     with pytest.raises(ValueError):
         mk(num_heads=8, num_kv_heads=3)
     with pytest.raises(ValueError):
@@ -139,10 +145,18 @@ def test_boundary_layer_impl_modes(monkeypatch):
     monkeypatch.setenv("TURBOQUANT_BOUNDARY_PROTECT", "3")   # TurboQuant codes at 3 bits in the fp16 slot
     im = mk()
     assert not im._is_raw and (im.key_bits, im.value_bits) == (3, 3)
-    for m in ("fp8", "8", "0"):
-        monkeypatch.setenv("TURBOQUANT_BOUNDARY_PROTECT", m)
-        with pytest.raises(NotImplementedError):
-            mk()
+    monkeypatch.setenv("TURBOQUANT_BOUNDARY_PROTECT", "8")   # 8-bit Lloyd-Max K, 8-bit V
+    im = mk()
+    assert (im.key_bits, im.value_bits, im.key_fp8, im.preset) == (8, 8, False, "boundary_8bit")
+    monkeypatch.setenv("TURBOQUANT_BOUNDARY_PROTECT", "fp8")  # fp8 keys, 8-bit V
+    im = mk()
+    assert (im.key_bits, im.value_bits, im.key_fp8, im.preset) == (8, 8, True, "boundary_fp8")
+    # both fit the fp16-sized slot vLLM gives boundary layers (reference README: 262 bytes at d=128)
+    from fused_turboquant import v1
+    assert v1.slot_bytes(128, 8, 8) == 262 and v1.slot_bytes(128, 8, 8, key_fp8=True) == 260 <= 4 * 128
+    monkeypatch.setenv("TURBOQUANT_BOUNDARY_PROTECT", "0")
+    with pytest.raises(NotImplementedError):
+        mk()
     monkeypatch.setenv("TURBOQUANT_BOUNDARY_PROTECT", "fp16")
     with pytest.raises(ValueError):  # raw decode kernel: GQA group <= 8
         vp.FusedTurboQuantV1Impl(32, 128, 0.1, 2, kv_cache_dtype="bfloat16")
