@@ -156,6 +156,15 @@ __global__ __launch_bounds__(256) void rht_kernel(const void* __restrict__ x, in
 // host side
 // ---------------------------------------------------------------------------
 
+// power-of-two head dims without a tuned kernel (ftq_codec_any.hip)
+bool codec_any_dim(int d);
+hipError_t codec_any_encode(int d, const void* x, int dt, int64_t n, const float* signs, const float* boundaries,
+                            int bits, uint8_t* packed, uint16_t* norms, hipStream_t st);
+hipError_t codec_any_decode(int d, const uint8_t* packed, const uint16_t* norms, int64_t n, const float* levels,
+                            const float* signs, int bits, void* out, int ot, hipStream_t st);
+hipError_t codec_any_rht(int d, const void* x, int it, int64_t n, const float* signs, int inverse, void* out,
+                         int ot, hipStream_t st);
+
 float fwht_scale(int d) { return (float)std::pow((double)d, -0.5); }
 
 // Workgroups (256 threads) that fit on the device at once for kernel k.
@@ -286,7 +295,7 @@ extern "C" int ftq_encode_cb(const void* x, int x_dtype, int64_t n, int d, const
                              const float* boundaries, int bits, int codebook_class,
                              uint8_t* packed_out, uint16_t* norms_out, void* stream) {
   FTQ_REQUIRE(n >= 0, "n must be >= 0");
-  FTQ_REQUIRE(d == 64 || d == 128 || d == 256, "head_dim must be 64, 128 or 256");
+  FTQ_REQUIRE(d == 64 || d == 128 || d == 256 || codec_any_dim(d), "head_dim must be a power of two in [8, 4096]");
   FTQ_REQUIRE(bits >= 2 && bits <= 4, "bits must be 2, 3, or 4");
   FTQ_REQUIRE(x_dtype >= F32 && x_dtype <= BF16, "x_dtype must be FTQ_F32, FTQ_F16 or FTQ_BF16");
   FTQ_REQUIRE(codebook_class == FTQ_CB_ANY || codebook_class == FTQ_CB_SYMMETRIC,
@@ -294,10 +303,11 @@ extern "C" int ftq_encode_cb(const void* x, int x_dtype, int64_t n, int d, const
   if (n == 0) return FTQ_OK;
   FTQ_REQUIRE(x && signs && boundaries && packed_out && norms_out, "null pointer argument");
   FTQ_REQUIRE(aligned16(x), "x must be 16-byte aligned");
-  FTQ_REQUIRE(aligned4(packed_out), "packed_out must be 4-byte aligned");
+  FTQ_REQUIRE(codec_any_dim(d) || aligned4(packed_out), "packed_out must be 4-byte aligned");
   hipStream_t st = (hipStream_t)stream;
   hipError_t e;
-  if (d == 64) e = launch_encode_d<64>(x, x_dtype, n, signs, boundaries, bits, codebook_class, packed_out, norms_out, st);
+  if (codec_any_dim(d)) e = codec_any_encode(d, x, x_dtype, n, signs, boundaries, bits, packed_out, norms_out, st);
+  else if (d == 64) e = launch_encode_d<64>(x, x_dtype, n, signs, boundaries, bits, codebook_class, packed_out, norms_out, st);
   else if (d == 128) e = launch_encode_d<128>(x, x_dtype, n, signs, boundaries, bits, codebook_class, packed_out, norms_out, st);
   else e = launch_encode_d<256>(x, x_dtype, n, signs, boundaries, bits, codebook_class, packed_out, norms_out, st);
   return hip_status(e);
@@ -313,16 +323,17 @@ extern "C" int ftq_decode(const uint8_t* packed, const uint16_t* norms, int64_t 
                           const float* levels, const float* signs, int bits, void* out,
                           int out_dtype, void* stream) {
   FTQ_REQUIRE(n >= 0, "n must be >= 0");
-  FTQ_REQUIRE(d == 64 || d == 128 || d == 256, "head_dim must be 64, 128 or 256");
+  FTQ_REQUIRE(d == 64 || d == 128 || d == 256 || codec_any_dim(d), "head_dim must be a power of two in [8, 4096]");
   FTQ_REQUIRE(bits >= 2 && bits <= 4, "bits must be 2, 3, or 4");
   FTQ_REQUIRE(out_dtype >= F32 && out_dtype <= BF16, "out_dtype must be FTQ_F32, FTQ_F16 or FTQ_BF16");
   if (n == 0) return FTQ_OK;
   FTQ_REQUIRE(packed && norms && levels && signs && out, "null pointer argument");
   FTQ_REQUIRE(aligned16(out), "out must be 16-byte aligned");
-  FTQ_REQUIRE(aligned4(packed), "packed must be 4-byte aligned");
+  FTQ_REQUIRE(codec_any_dim(d) || aligned4(packed), "packed must be 4-byte aligned");
   hipStream_t st = (hipStream_t)stream;
   hipError_t e;
-  if (d == 64) e = launch_decode_d<64>(packed, norms, n, levels, signs, bits, out, out_dtype, st);
+  if (codec_any_dim(d)) e = codec_any_decode(d, packed, norms, n, levels, signs, bits, out, out_dtype, st);
+  else if (d == 64) e = launch_decode_d<64>(packed, norms, n, levels, signs, bits, out, out_dtype, st);
   else if (d == 128) e = launch_decode_d<128>(packed, norms, n, levels, signs, bits, out, out_dtype, st);
   else e = launch_decode_d<256>(packed, norms, n, levels, signs, bits, out, out_dtype, st);
   return hip_status(e);
@@ -331,7 +342,7 @@ extern "C" int ftq_decode(const uint8_t* packed, const uint16_t* norms, int64_t 
 extern "C" int ftq_rht(const void* x, int x_dtype, int64_t n, int d, const float* signs,
                        int inverse, void* out, int out_dtype, void* stream) {
   FTQ_REQUIRE(n >= 0, "n must be >= 0");
-  FTQ_REQUIRE(d == 64 || d == 128 || d == 256, "head_dim must be 64, 128 or 256");
+  FTQ_REQUIRE(d == 64 || d == 128 || d == 256 || codec_any_dim(d), "head_dim must be a power of two in [8, 4096]");
   FTQ_REQUIRE(x_dtype >= F32 && x_dtype <= BF16 && out_dtype >= F32 && out_dtype <= BF16,
               "dtype must be FTQ_F32, FTQ_F16 or FTQ_BF16");
   if (n == 0) return FTQ_OK;
@@ -339,7 +350,8 @@ extern "C" int ftq_rht(const void* x, int x_dtype, int64_t n, int d, const float
   FTQ_REQUIRE(aligned16(x) && aligned16(out), "x and out must be 16-byte aligned");
   hipStream_t st = (hipStream_t)stream;
   hipError_t e;
-  if (d == 64) e = launch_rht_d<64>(x, x_dtype, n, signs, inverse, out, out_dtype, st);
+  if (codec_any_dim(d)) e = codec_any_rht(d, x, x_dtype, n, signs, inverse, out, out_dtype, st);
+  else if (d == 64) e = launch_rht_d<64>(x, x_dtype, n, signs, inverse, out, out_dtype, st);
   else if (d == 128) e = launch_rht_d<128>(x, x_dtype, n, signs, inverse, out, out_dtype, st);
   else e = launch_rht_d<256>(x, x_dtype, n, signs, inverse, out, out_dtype, st);
   return hip_status(e);

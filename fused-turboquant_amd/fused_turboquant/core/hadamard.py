@@ -57,8 +57,8 @@ def rht_apply(x: torch.Tensor, signs: torch.Tensor, inverse: bool,
     if xf.dtype not in (torch.float32, torch.float16, torch.bfloat16):
         xf = xf.float()
     _lib.dtype_code(out_dtype)
-    if d not in (64, 128, 256):
-        raise ValueError(f"head_dim must be 64, 128 or 256 for the gfx950 kernels, got {d}")
+    if not 8 <= d <= 4096:
+        raise ValueError(f"head_dim must be a power of two in [8, 4096] for the gfx950 kernels, got {d}")
     return _ops.ops().rht(xf, signs.contiguous(), bool(inverse), out_dtype)
 
 

@@ -56,8 +56,10 @@ class TurboQuantMSE:
             raise ValueError(f"head_dim must be a power of 2, got {head_dim}")
         if bits not in (2, 3, 4):
             raise ValueError(f"bits must be 2, 3, or 4, got {bits}")
-        if head_dim not in (64, 128, 256):
-            raise ValueError(f"head_dim must be 64, 128 or 256 for the gfx950 kernels, got {head_dim}")
+        if not 8 <= head_dim <= 4096:
+            # 64 / 128 / 256 run tuned kernels; the other powers of two a generic one
+            raise ValueError(f"head_dim must be a power of two in [8, 4096] for the gfx950 kernels, "
+                             f"got {head_dim}")
         self.head_dim = head_dim
         self.bits = bits
         self.device = device

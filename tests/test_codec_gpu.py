@@ -220,3 +220,31 @@ def test_encode_decode_under_torch_compile(cuda):
     x = torch.randn(300, 8, 128, generator=torch.Generator().manual_seed(6)).to(torch.bfloat16).to(cuda)
     for got, want in zip(compiled(x), roundtrip(x)):
         assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("d", [8, 16, 32, 512, 1024, 2048])
+@pytest.mark.parametrize("bits", [2, 3, 4])
+def test_other_power_of_two_head_dims(cuda, d, bits):
+    """TurboQuantMSE at the power-of-two head dims without a tuned kernel
+    (reference core/quantizer.py:77-80 accepts any): codes equal the oracle's
+    except at counted boundary ties, fp16 norms within 1e-3, decode and both
+    RHT directions bit-identical to the oracle."""
+    from fused_turboquant import TurboQuantMSE
+    from fused_turboquant.core.hadamard import randomized_hadamard, inverse_randomized_hadamard
+    tq = TurboQuantMSE(head_dim=d, bits=bits, device=cuda)
+    n = max(4, 16384 // d) + 3
+    for dtype in (torch.bfloat16, torch.float32):
+        x = _mk(n, d, dtype, seed=d + bits)
+        ct = tq.encode(x.to(cuda))
+        assert ct.indices.shape == (n, d * bits // 8) and ct.norms.shape == (n,)
+        _check_encode(tq, x, ct, bits, d, f"any d={d} b={bits} {dtype}")
+        got = tq.decode(ct).cpu().numpy()
+        want = O.decode(ct.indices.cpu().numpy(), ct.norms.cpu().numpy(), tq.quantizer.levels.cpu().numpy(),
+                        tq.rotation.signs.cpu().numpy(), bits, d)
+        assert np.array_equal(got, want), f"decode d={d} b={bits}"
+    s = tq.rotation.signs
+    x = _mk(n, d, torch.float32, seed=d).to(cuda)
+    y = randomized_hadamard(x, s)
+    assert np.array_equal(y.cpu().numpy(), O.rht(x.cpu().numpy(), s.cpu().numpy()))
+    z = inverse_randomized_hadamard(y, s)
+    assert np.array_equal(z.cpu().numpy(), O.inverse_rht(y.cpu().numpy(), s.cpu().numpy()))
