@@ -25,6 +25,16 @@ decode steps append one token per sequence.
 Layers whose V is kept uncompressed (``compress_v=False`` / ``"boundary"`` /
 a callable) keep K in pages and V in full precision; their decode step
 dequantises K with the decode kernel and attends with torch ops.
+
+Head dims: 128 and 256 use the paged format and the fused paged decode
+attention; any other power of two (Gemma 4's 512-wide global layers, for
+example) keeps the reference's flat per-sequence rows of codes + fp16 norms,
+encoded and decoded by the codec kernels, and attends with torch ops over
+the decoded K / V -- as do sliding-window layers, whose decode step masks all
+but the last ``sliding_window`` positions and the first ``sink_tokens``
+(reference ``:600-611``).  Gemma 4's K = V layers (no ``v_proj``: V is the
+k_proj output through ``v_norm``) and per-layer head dims are handled;
+layers that share another layer's KV are refused (reference ``:421-426``).
 """
 from __future__ import annotations
 
@@ -133,6 +143,64 @@ class _LayerPages:
         return fold(kp), fold(kn), fold(vp), fold(vn)
 
 
+class _LayerFlat:
+    """Compressed K / V of one layer whose head dim has no paged kernel: per
+    sequence a row of ``cap`` positions of codes [Hkv, cap, d * bits / 8] and
+    fp16 norms [Hkv, cap] (the reference's flat CompressedTensor layout,
+    ``hf/fused_cache.py:195-222``), grown by doubling; token i of sequence b
+    sits at position i of row b."""
+
+    def __init__(self, batch: int, hkv: int, d: int, k_tq: TurboQuantMSE, v_tq: TurboQuantMSE, device):
+        self.B, self.hkv, self.d = batch, hkv, d
+        self.k_tq, self.v_tq = k_tq, v_tq
+        self.cap = 0
+        self.kp = self.kn = self.vp = self.vn = None
+        self.lens = [0] * batch
+        self.lens_dev = torch.zeros(batch, dtype=torch.int32, device=device)
+        self.device = device
+
+    def _ensure(self, need: int) -> None:
+        if need <= self.cap:
+            return
+        new = max(need, 2 * self.cap, 64)
+
+        def grow(t, tail, dtype):
+            fresh = torch.zeros(self.B, self.hkv, new, *tail, dtype=dtype, device=self.device)
+            if t is not None:
+                fresh[:, :, :self.cap] = t
+            return fresh
+        self.kp = grow(self.kp, (self.d * self.k_tq.bits // 8,), torch.uint8)
+        self.kn = grow(self.kn, (), torch.float16)
+        self.vp = grow(self.vp, (self.d * self.v_tq.bits // 8,), torch.uint8)
+        self.vn = grow(self.vn, (), torch.float16)
+        self.cap = new
+
+    def append(self, key: torch.Tensor, value: torch.Tensor, keep: Optional[torch.Tensor]) -> None:
+        B, hkv, q, d = key.shape
+        ck, cv = self.k_tq.encode(key), self.v_tq.encode(value)
+        if keep is None:
+            counts = [q] * B
+            pos = torch.tensor(self.lens, device=self.device).view(-1, 1) + torch.arange(q, device=self.device)
+            sel = torch.ones(B, q, dtype=torch.bool, device=self.device)
+        else:
+            sel = keep.to(torch.bool)
+            counts = sel.sum(dim=1).tolist()
+            pos = torch.tensor(self.lens, device=self.device).view(-1, 1) + sel.long().cumsum(dim=1) - 1
+        self._ensure(max(L + c for L, c in zip(self.lens, counts)))
+        b_idx = torch.arange(B, device=self.device).view(-1, 1).expand(B, q)[sel]
+        p_idx = pos[sel]
+        self.kp[b_idx, :, p_idx] = ck.indices.permute(0, 2, 1, 3)[sel]
+        self.kn[b_idx, :, p_idx] = ck.norms.permute(0, 2, 1)[sel]
+        self.vp[b_idx, :, p_idx] = cv.indices.permute(0, 2, 1, 3)[sel]
+        self.vn[b_idx, :, p_idx] = cv.norms.permute(0, 2, 1)[sel]
+        self.lens = [L + c for L, c in zip(self.lens, counts)]
+        self.lens_dev.copy_(torch.tensor(self.lens, dtype=torch.int32))
+
+    def flat(self):
+        L = max(self.lens) if self.lens else 0
+        return self.kp[:, :, :L], self.kn[:, :, :L], self.vp[:, :, :L], self.vn[:, :, :L]
+
+
 class CompressedKVCache(DynamicCache):
     """KV cache holding TurboQuant-compressed K (and V) per patched layer.
 
@@ -167,12 +235,13 @@ class CompressedKVCache(DynamicCache):
         return self._layer_tq.get(layer_idx, self.tq)
 
     # -- storage -------------------------------------------------------------
-    def _layer(self, layer_idx: int, like: torch.Tensor) -> _LayerPages:
+    def _layer(self, layer_idx: int, like: torch.Tensor):
         lp = self._pages.get(layer_idx)
         if lp is None:
             B, hkv, _, d = like.shape
-            lp = _LayerPages(B, hkv, d, self.get_layer_quantizer(layer_idx),
-                             self.get_layer_quantizer_v(layer_idx), like.device)
+            kind = _LayerPages if d in (128, 256) else _LayerFlat  # the paged kernels take 128 and 256
+            lp = kind(B, hkv, d, self.get_layer_quantizer(layer_idx), self.get_layer_quantizer_v(layer_idx),
+                      like.device)
             self._pages[layer_idx] = lp
         return lp
 
@@ -224,11 +293,33 @@ class CompressedKVCache(DynamicCache):
         e = self._entry(layer_idx, "v")
         return tq.decode(CompressedTensor(e["packed_indices"], e["norms"], tq.head_dim, tq.bits))
 
-    def decode_attention(self, query: torch.Tensor, layer_idx: int, scale: float) -> torch.Tensor:
-        """query [B, Hq, d] -> [B, Hq, d] (query dtype), fused over the pages."""
+    def decode_attention(self, query: torch.Tensor, layer_idx: int, scale: float,
+                         sliding_window: Optional[int] = None, sink_tokens: int = 0) -> torch.Tensor:
+        """query [B, Hq, d] -> [B, Hq, d] (query dtype): the fused paged decode
+        attention; for flat (non-paged) layers and sliding windows, softmax
+        attention in fp32 over the decoded K / V of each sequence's positions
+        (with a window: the last ``sliding_window`` and the first
+        ``sink_tokens``, reference ``hf/fused_cache.py:600-611``)."""
         lp = self._pages[layer_idx]
-        return P.paged_decode_attention(query, lp.kv_cache, lp.block_table, lp.lens_dev, lp.k_tq, lp.v_tq,
-                                        scale=scale, max_seq_len=max(lp.lens))
+        if isinstance(lp, _LayerPages) and sliding_window is None:
+            return P.paged_decode_attention(query, lp.kv_cache, lp.block_table, lp.lens_dev, lp.k_tq, lp.v_tq,
+                                            scale=scale, max_seq_len=max(lp.lens))
+        kd = self.decode_keys(layer_idx)
+        vd = self.decode_values(layer_idx)
+        B, hq, d = query.shape
+        n_rep = hq // kd.shape[1]
+        S = kd.shape[2]
+        scores = torch.matmul(query.float().unsqueeze(2), _repeat_kv(kd, n_rep).transpose(-1, -2).contiguous())
+        scores = scores * scale  # [B, Hq, 1, S]
+        pos = torch.arange(S, device=query.device).view(1, -1)
+        lens = lp.lens_dev.view(-1, 1).to(torch.int64)
+        ok = pos < lens
+        if sliding_window is not None:
+            ok = ok & ((pos >= lens - sliding_window) | (pos < sink_tokens))
+        scores = scores.masked_fill(~ok[:, None, None, :], float("-inf"))
+        w = torch.softmax(scores, dim=-1)
+        w = torch.nan_to_num(w, nan=0.0)  # a sequence with no positions gives 0
+        return torch.matmul(w, _repeat_kv(vd, n_rep)).squeeze(2).to(query.dtype)
 
     def reset(self):
         """Drop every layer so the object can serve a new prompt (reference :350-360)."""
@@ -257,17 +348,23 @@ def _repeat_kv(x: torch.Tensor, n_rep: int) -> torch.Tensor:
     return x[:, :, None].expand(b, h, n_rep, s, d).reshape(b, h * n_rep, s, d)
 
 
-def _keep_from_mask(attention_mask, q_len: int) -> Optional[torch.Tensor]:
-    """[B, q] bool of the new tokens a sequence attends to from its last
-    query row (False = padding), or None when nothing is masked."""
+def _keep_from_mask(attention_mask, q_len: int, window: Optional[int] = None) -> Optional[torch.Tensor]:
+    """[B, q] bool of the new tokens that are not padding, or None when none
+    is.  Token j is read from query row r_j = min(j + window - 1, q - 1), the
+    last row whose window still holds it (the last row without a window):
+    a real token is visible there, a padding token is not."""
     if attention_mask is None or attention_mask.dim() != 4:
         return None
-    last = attention_mask[:, 0, -1, -q_len:]
-    keep = last if last.dtype == torch.bool else (last == 0)
+    m = attention_mask[:, 0, -q_len:, -q_len:]
+    vis = m if m.dtype == torch.bool else (m == 0)
+    j = torch.arange(q_len, device=vis.device)
+    r = torch.full_like(j, q_len - 1) if window is None else torch.clamp(j + window - 1, max=q_len - 1)
+    keep = vis[:, r, j]
     return None if bool(keep.all()) else keep
 
 
-def _continuation_mask(lens_before, past_len: int, q_len: int, keep, attention_mask, compress_v, device):
+def _continuation_mask(lens_before, past_len: int, q_len: int, keep, attention_mask, compress_v, device,
+                       window: Optional[int] = None):
     """[B, 1, q, past_len + q] bool mask of a chunk of q new tokens over the
     decoded past of each sequence and the chunk itself.
 
@@ -292,59 +389,106 @@ def _continuation_mask(lens_before, past_len: int, q_len: int, keep, attention_m
     if keep is not None:
         eye = torch.eye(q_len, dtype=torch.bool, device=device)[None]
         new_ok = new_ok & (keep[:, None, :].to(torch.bool) | eye)
+    if window is not None:
+        # row i of sequence b sits at position lens_before[b] + (its index among
+        # the kept tokens); it sees the positions within `window` of itself
+        kept = (keep.to(torch.long) if keep is not None else torch.ones(B, q_len, dtype=torch.long, device=device))
+        row_pos = lb[:, None] + kept.cumsum(dim=1) - 1                             # [B, q]
+        past_pos = torch.arange(past_len, device=device)[None, None, :]
+        past_ok = past_ok & (past_pos > row_pos[:, :, None] - window)
+        new_pos = lb[:, None] + kept.cumsum(dim=1) - 1
+        new_ok = new_ok & (new_pos[:, None, :] > row_pos[:, :, None] - window)
     return torch.cat([past_ok, new_ok], dim=2)[:, None]
 
 
+def _module_k_eq_v(module) -> bool:
+    """Gemma 4 full-attention layers (``attention_k_eq_v``): no ``v_proj``, V
+    is the k_proj output through ``v_norm`` (reference ``:89-105``)."""
+    has_qk = getattr(module, "q_proj", None) is not None and getattr(module, "k_proj", None) is not None
+    if not has_qk or getattr(module, "v_proj", "missing") is not None:
+        return False
+    return bool(getattr(module, "use_alternative_attention", False)) or bool(
+        getattr(getattr(module, "config", None), "attention_k_eq_v", False))
+
+
+def _module_is_kv_shared(module) -> bool:
+    """Gemma 4 layers that reuse another layer's K / V (reference ``:108-110``)."""
+    return bool(getattr(module, "is_kv_shared_layer", False))
+
+
+def _layer_sliding_window(module, config) -> Optional[int]:
+    """The module's own window when it declares one (None on Gemma's full
+    layers), else the config's."""
+    if hasattr(module, "sliding_window"):
+        return getattr(module, "sliding_window")
+    return _cfg(config, "sliding_window", None) if config is not None else None
+
+
 def _probe_attention_module(module, config) -> dict:
+    k_eq_v = _module_k_eq_v(module)
+    has_qkv = (getattr(module, "q_proj", None) is not None and getattr(module, "k_proj", None) is not None
+               and (getattr(module, "v_proj", None) is not None or k_eq_v))
     return {
         "is_cross_attention": bool(getattr(module, "is_cross_attention", False)),
         "has_fused_qkv": hasattr(module, "qkv_proj") or hasattr(module, "c_attn"),
-        "has_separate_qkv": all(getattr(module, p, None) is not None for p in ("q_proj", "k_proj", "v_proj")),
-        "sliding_window": getattr(module, "sliding_window", None) or getattr(config, "sliding_window", None),
-        "attn_logit_softcapping": getattr(config, "attn_logit_softcapping", None),
+        "has_separate_qkv": has_qkv,
+        "k_eq_v": k_eq_v,
+        "is_kv_shared": _module_is_kv_shared(module),
+        "sliding_window": _layer_sliding_window(module, config),
+        "attn_logit_softcapping": _cfg(config, "attn_logit_softcapping", None),
         "rope_expected": _config_uses_rope(config),
     }
 
 
 def _config_uses_rope(config) -> bool:
     for attr in ("rope_theta", "rope_scaling", "rope_parameters", "rotary_emb_base"):
-        if getattr(config, attr, None) is not None:
+        if _cfg(config, attr, None) is not None:
             return True
-    return getattr(config, "position_embedding_type", "rope") in ("rope", "rotary")
+    return _cfg(config, "position_embedding_type", "rope") in ("rope", "rotary")
 
 
 def make_fused_attention_forward(attn_module, cache: CompressedKVCache, quantizer: TurboQuantMSE,
                                  layer_idx: int, config=None, compress_v: bool = True):
     """Replacement forward for one decoder self-attention layer (reference
     ``hf/fused_cache.py:386-682``)."""
+    k_eq_v = _module_k_eq_v(attn_module)
+    window = _layer_sliding_window(attn_module, config)
     if config is not None:
         probe = _probe_attention_module(attn_module, config)
         if probe["is_cross_attention"]:
             raise ValueError(f"Layer {layer_idx}: cross-attention layers cannot be patched")
+        if probe["is_kv_shared"]:
+            raise ValueError(f"Layer {layer_idx}: a KV-shared layer (is_kv_shared_layer=True) reuses another "
+                             "layer's K/V and cannot be patched")
         if probe["has_fused_qkv"] and not probe["has_separate_qkv"]:
             raise ValueError(f"Layer {layer_idx}: fused QKV projections are not supported")
         if probe["attn_logit_softcapping"] is not None:
             raise ValueError(f"Layer {layer_idx}: attention logit softcapping is not supported")
-        if probe["sliding_window"] is not None:
-            raise ValueError(f"Layer {layer_idx}: sliding-window attention is not supported")
     head_dim = quantizer.head_dim
-    scale = float(getattr(attn_module, "scaling", None) or 1.0 / math.sqrt(head_dim))
+    scaling = getattr(attn_module, "scaling", None)  # Gemma sets 1.0 (Q and K are RMS-normalised)
+    scale = float(scaling) if scaling is not None else 1.0 / math.sqrt(head_dim)
     n_heads = attn_module.q_proj.out_features // head_dim
     n_kv_heads = attn_module.k_proj.out_features // head_dim
     n_rep = n_heads // n_kv_heads
     q_norm = getattr(attn_module, "q_norm", None)
     k_norm = getattr(attn_module, "k_norm", None)
+    v_norm = getattr(attn_module, "v_norm", None)
+    n_sink = int(_cfg(config, "sink_tokens", 4) or 0) if config is not None else 4
 
     def fused_forward(hidden_states, position_embeddings=None, attention_mask=None,
                       past_key_values=None, cache_position=None, **kwargs):
         bsz, q_len, _ = hidden_states.size()
         q = attn_module.q_proj(hidden_states).view(bsz, q_len, n_heads, head_dim).transpose(1, 2)
-        k = attn_module.k_proj(hidden_states).view(bsz, q_len, n_kv_heads, head_dim).transpose(1, 2)
-        v = attn_module.v_proj(hidden_states).view(bsz, q_len, n_kv_heads, head_dim).transpose(1, 2)
+        k_out = attn_module.k_proj(hidden_states)
+        v_out = k_out if (k_eq_v or getattr(attn_module, "v_proj", None) is None) else attn_module.v_proj(hidden_states)
+        k = k_out.view(bsz, q_len, n_kv_heads, head_dim).transpose(1, 2)
+        v = v_out.view(bsz, q_len, n_kv_heads, head_dim).transpose(1, 2)
         if q_norm is not None:
             q = q_norm(q)
         if k_norm is not None:
             k = k_norm(k)
+        if v_norm is not None:  # V takes no RoPE; Gemma normalises it on its own
+            v = v_norm(v)
         if position_embeddings is not None:
             cos, sin = position_embeddings
             q, k = _apply_rotary_pos_emb(q, k, cos, sin)
@@ -355,7 +499,7 @@ def make_fused_attention_forward(attn_module, cache: CompressedKVCache, quantize
         # V-compressed layers drop masked-out (padding) tokens so each sequence's
         # pages hold only its own tokens; K-only layers keep every position so K
         # lines up with the full-precision V of the base cache, and mask instead
-        keep = _keep_from_mask(attention_mask, q_len) if compress_v else None
+        keep = _keep_from_mask(attention_mask, q_len, window) if compress_v else None
         cache.store_compressed_kv(k, v, layer_idx, keep=keep)
         # sequence-length bookkeeping of the base class (one element per token)
         if compress_v:
@@ -365,7 +509,8 @@ def make_fused_attention_forward(attn_module, cache: CompressedKVCache, quantize
             _, raw_v = cache.update(k[..., :1], v, layer_idx)
 
         if q_len == 1 and compress_v:
-            out = cache.decode_attention(q[:, :, 0], layer_idx, scale).unsqueeze(2)
+            out = cache.decode_attention(q[:, :, 0], layer_idx, scale, sliding_window=window,
+                                         sink_tokens=n_sink).unsqueeze(2)
         elif q_len == 1:
             # K-only layer (reference :591-624 with V uncompressed)
             kd = cache.decode_keys(layer_idx).to(q.dtype)
@@ -378,6 +523,9 @@ def make_fused_attention_forward(attn_module, cache: CompressedKVCache, quantize
             out = torch.matmul(w, _repeat_kv(raw_v[:, :, -S:], n_rep))
         elif not had_past:
             mask = attention_mask[:, :, :q_len, :q_len] if attention_mask is not None and attention_mask.dim() == 4 else None
+            if mask is None and window is not None and q_len > window:  # causal within the window
+                i = torch.arange(q_len, device=q.device)
+                mask = (i[None, :] <= i[:, None]) & (i[None, :] > i[:, None] - window)
             out = F.scaled_dot_product_attention(q, _repeat_kv(k, n_rep), _repeat_kv(v, n_rep),
                                                  attn_mask=mask, scale=scale, is_causal=mask is None)
         else:
@@ -387,7 +535,8 @@ def make_fused_attention_forward(attn_module, cache: CompressedKVCache, quantize
                   else raw_v[:, :, :past_len])
             kk = torch.cat([kd, k], dim=2)
             vv = torch.cat([vd, v], dim=2)
-            mask = _continuation_mask(lens_before, past_len, q_len, keep, attention_mask, compress_v, q.device)
+            mask = _continuation_mask(lens_before, past_len, q_len, keep, attention_mask, compress_v, q.device,
+                                      window)
             out = F.scaled_dot_product_attention(q, _repeat_kv(kk, n_rep), _repeat_kv(vv, n_rep),
                                                  attn_mask=mask, scale=scale)
         out = out.transpose(1, 2).reshape(bsz, q_len, -1)
@@ -401,70 +550,115 @@ def make_fused_attention_forward(attn_module, cache: CompressedKVCache, quantize
 # model-level entry points
 # --------------------------------------------------------------------------
 
+def _cfg(config, name: str, default=None):
+    """A config attribute, or ``default`` when it is missing or, on a
+    heterogeneous (per-layer) config such as Gemma 4's, not defined globally."""
+    try:
+        return getattr(config, name, default)
+    except Exception:  # transformers refuses global reads of per-layer attributes
+        return default
+
+
 def _resolve_config(model):
     config = model.config
-    return getattr(config, "text_config", config)
+    return _cfg(config, "text_config", config)
 
 
 def _resolve_head_dim(config) -> int:
-    hd = getattr(config, "head_dim", None)
+    hd = _cfg(config, "head_dim", None)
     if hd:
         return hd
-    hs, nh = getattr(config, "hidden_size", None), getattr(config, "num_attention_heads", None)
+    hs, nh = _cfg(config, "hidden_size", None), _cfg(config, "num_attention_heads", None)
     return hs // nh if hs and nh else 0
 
 
+def _resolve_layer_head_dim(module, config) -> int:
+    """The layer's own head_dim when the module declares one (Gemma 4: 256 on
+    sliding layers, 512 on full ones), else the config's (reference
+    ``:728-740``)."""
+    hd = getattr(module, "head_dim", None)
+    return hd if isinstance(hd, int) and hd > 0 else _resolve_head_dim(config)
+
+
 def _is_full_attention_layer(module, name: str = "") -> bool:
-    if getattr(module, "is_cross_attention", False):
+    """A decoder self-attention module this library can patch: separate q / k
+    projections, a v projection or K = V (Gemma 4), an output projection; not
+    cross-attention, not a vision tower, not a KV-shared layer (reference
+    ``:686-707``)."""
+    if getattr(module, "is_cross_attention", False) or _module_is_kv_shared(module):
         return False
     if any(kw in name.lower() for kw in _SKIP_NAME_KEYWORDS):
         return False
-    has_qkv = all(getattr(module, p, None) is not None for p in ("q_proj", "k_proj", "v_proj"))
-    return has_qkv and (hasattr(module, "o_proj") or hasattr(module, "out_proj"))
+    has_qk = all(getattr(module, p, None) is not None for p in ("q_proj", "k_proj"))
+    has_v = getattr(module, "v_proj", None) is not None or _module_k_eq_v(module)
+    return has_qk and has_v and (hasattr(module, "o_proj") or hasattr(module, "out_proj"))
+
+
+def _head_dim_ok(hd: int) -> bool:
+    return 8 <= hd <= 4096 and (hd & (hd - 1)) == 0
 
 
 def check_model_compatibility(model) -> dict:
-    """Whether ``patch_model`` can patch this model (reference :750-880)."""
+    """Whether ``patch_model`` can patch this model (reference :750-880).
+
+    Per-layer head dims are read from the attention modules; each must be a
+    power of two in [8, 4096] (128 and 256 take the fused paged decode, the
+    others torch attention over the decoded cache).  Sliding-window layers
+    are supported; logit soft-capping and KV-shared layers are not."""
     config = _resolve_config(model)
     head_dim = _resolve_head_dim(config)
-    n_q = getattr(config, "num_attention_heads", 0)
-    n_kv = getattr(config, "num_key_value_heads", n_q)
+    n_q = _cfg(config, "num_attention_heads", 0)
+    n_kv = _cfg(config, "num_key_value_heads", n_q) or n_q
     issues, unsupported = [], []
-    eligible = total = fused_qkv = cross = 0
+    eligible = total = fused_qkv = cross = kv_shared = k_eq_v = 0
+    layer_hds = []
     for name, module in model.named_modules():
         total += 1
         if getattr(module, "is_cross_attention", False):
             cross += 1
+            continue
+        if _module_is_kv_shared(module):
+            kv_shared += 1
             continue
         if (hasattr(module, "qkv_proj") or hasattr(module, "c_attn")) and not all(
                 hasattr(module, p) for p in ("q_proj", "k_proj", "v_proj")):
             fused_qkv += 1
         if _is_full_attention_layer(module, name):
             eligible += 1
-    if head_dim not in (128, 256):
-        issues.append(f"head_dim {head_dim} is not supported by the gfx950 paged kernels (128 or 256)")
+            k_eq_v += int(_module_k_eq_v(module))
+            hd_l = _resolve_layer_head_dim(module, config)
+            layer_hds.append(hd_l)
+            if hd_l > 0:
+                nq_l, nkv_l = module.q_proj.out_features // hd_l, module.k_proj.out_features // hd_l
+                if nkv_l <= 0 or nq_l % nkv_l or nq_l // nkv_l > 16:
+                    issues.append(f"{name}: {nq_l} query heads over {nkv_l} kv heads (need a group of <= 16)")
+    hds = sorted(set(layer_hds)) or ([head_dim] if head_dim else [])
+    bad = [hd for hd in hds if not _head_dim_ok(hd)]
+    if bad:
+        issues.append(f"head_dim {bad} is not a power of two in [8, 4096]")
     if n_kv > 0 and n_q % n_kv != 0:
         issues.append(f"n_q_heads ({n_q}) is not divisible by n_kv_heads ({n_kv})")
     elif n_kv > 0 and n_q // n_kv > 16:
         issues.append(f"GQA group {n_q // n_kv} exceeds 16")
     if eligible == 0:
         issues.append("No compatible attention layers found (need separate q/k/v and o projections)")
+    if kv_shared:
+        issues.append(f"{kv_shared} KV-shared layers reuse another layer's K/V; they cannot be patched")
     if not _config_uses_rope(config):
         issues.append("Model config does not indicate RoPE usage")
-    if getattr(config, "attn_logit_softcapping", None) is not None:
+    if _cfg(config, "attn_logit_softcapping", None) is not None:
         unsupported.append("logit_softcapping")
-    if getattr(config, "sliding_window", None) is not None:
-        unsupported.append("sliding_window")
     if unsupported:
         issues.append(f"Unsupported attention features: {', '.join(unsupported)}")
     arch = type(model).__name__
     return {
-        "compatible": not issues, "head_dim_valid": head_dim in (128, 256), "head_dim": head_dim,
+        "compatible": not issues, "head_dim_valid": not bad, "head_dim": hds[0] if hds else head_dim,
+        "head_dims": hds, "paged_head_dims": [hd for hd in hds if hd in (128, 256)],
         "n_q_heads": n_q, "n_kv_heads": n_kv, "eligible_layers": eligible, "total_layers": total,
         "issues": issues, "rope_detected": _config_uses_rope(config),
-        "sliding_window": getattr(config, "sliding_window", None), "unsupported_features": unsupported,
-        "fused_qkv_layers": fused_qkv, "cross_attention_layers": cross, "architecture": arch,
-        "known_compatible": arch in KNOWN_COMPATIBLE,
+        "sliding_window": _cfg(config, "sliding_window", None), "unsupported_features": unsupported,
+        "fused_qkv_layers": fused_qkv, "cross_attention_layers": cross, "kv_shared_layers": kv_shared,
+        "k_eq_v_layers": k_eq_v, "architecture": arch, "known_compatible": arch in KNOWN_COMPATIBLE,
     }
 
 
@@ -561,20 +755,28 @@ def patch_model(model, bits: int = 4, head_dim: int | None = None, verify: bool 
 
     config = _resolve_config(model)
     device = next(model.parameters()).device
-    hd = head_dim if head_dim is not None else _resolve_head_dim(config)
-    if hd not in (128, 256):
-        raise ValueError(f"head_dim={hd}: the gfx950 paged kernels support head_dim 128 or 256")
+    shared = [n for n, m in model.named_modules() if _module_is_kv_shared(m)]
+    if shared:
+        raise ValueError(f"{len(shared)} KV-shared layers (e.g. {shared[0]}) reuse another layer's K/V, which "
+                         "this cache keeps compressed; models with num_kv_shared_layers=0 can be patched")
     eligible = [(n, m) for n, m in model.named_modules() if _is_full_attention_layer(m, n)]
     n_layers = len(eligible)
+    layer_hd = {n: (head_dim if head_dim is not None else _resolve_layer_head_dim(m, config)) for n, m in eligible}
+    for n, hd in layer_hd.items():
+        if not _head_dim_ok(hd):
+            raise ValueError(f"head_dim={hd} ({n}): the gfx950 kernels take powers of two in [8, 4096]")
     tqs: dict = {}
 
-    def get_tq(b: int) -> TurboQuantMSE:
-        if b not in tqs:
-            tqs[b] = TurboQuantMSE(head_dim=hd, bits=b, device=device, max_iterations=max_iterations,
-                                   num_grid_points=num_grid_points)
-        return tqs[b]
+    def get_tq(hd: int, b: int) -> TurboQuantMSE:
+        if (hd, b) not in tqs:
+            tqs[hd, b] = TurboQuantMSE(head_dim=hd, bits=b, device=device, max_iterations=max_iterations,
+                                       num_grid_points=num_grid_points)
+        return tqs[hd, b]
 
-    cache = CompressedKVCache(get_tq(bits), compress_v=compress_v is not False)
+    hd0 = layer_hd[eligible[0][0]] if eligible else (head_dim or _resolve_head_dim(config))
+    if not _head_dim_ok(hd0):
+        raise ValueError(f"head_dim={hd0}: the gfx950 kernels take powers of two in [8, 4096]")
+    cache = CompressedKVCache(get_tq(hd0, bits), compress_v=compress_v is not False)
     n_boundary = min(boundary_protect, n_layers // 2)
     skip = set(range(n_boundary)) | set(range(n_layers - n_boundary, n_layers)) if n_boundary else set()
     originals = {}
@@ -582,10 +784,10 @@ def patch_model(model, bits: int = 4, head_dim: int | None = None, verify: bool 
         if pos in skip:
             continue
         layer_idx = getattr(module, "layer_idx", pos)  # the index the base cache sees
-        tq = get_tq(bits)
+        tq = get_tq(layer_hd[name], bits)
         cache.set_layer_quantizer(layer_idx, tq)
         if v_bits != bits:
-            cache.set_layer_quantizer_v(layer_idx, get_tq(v_bits))
+            cache.set_layer_quantizer_v(layer_idx, get_tq(layer_hd[name], v_bits))
         originals[name] = module.forward
         module.forward = make_fused_attention_forward(
             module, cache, tq, layer_idx, config=config,

@@ -165,3 +165,126 @@ def test_padded_batch_continuation_chunk(cuda):
         diff = (got - want).abs().max().item()
         print(f"[hf padded continuation {tag}] max logit diff {diff:.3e} (|logit| max {want.abs().max().item():.2f})")
         assert diff <= 2e-2 * max(1.0, want.abs().max().item())
+
+
+def _tiny_gemma4(cuda, window=8, sinks=0):
+    """A random-init Gemma 4 text model: sliding layers at head_dim 64 (flat
+    rows, window attention), full layers at head_dim 128 with K = V (no
+    v_proj) and one kv head (paged decode), scaling 1.0, q/k/v norms."""
+    from transformers import Gemma4TextConfig
+    from transformers.models.gemma4.modeling_gemma4 import Gemma4ForCausalLM
+    cfg = Gemma4TextConfig(vocab_size=320, hidden_size=256, intermediate_size=512, num_hidden_layers=4,
+                           num_attention_heads=4, num_key_value_heads=2, head_dim=64, global_head_dim=128,
+                           sliding_window=window,
+                           layer_types=["sliding_attention", "full_attention", "sliding_attention", "full_attention"],
+                           attention_k_eq_v=True, num_global_key_value_heads=1, vocab_size_per_layer_input=320,
+                           hidden_size_per_layer_input=16, max_position_embeddings=512)
+    cfg.sink_tokens = sinks
+    torch.manual_seed(0)
+    model = Gemma4ForCausalLM(cfg)
+    # Gemma scores with scaling 1.0 over RMS-normalised q and k: at random init
+    # (norm weights 1) the scores have std sqrt(head_dim) and every softmax is
+    # near one-hot, so any K error flips it.  Trained models are far smoother;
+    # shrinking the query norm weights gives this one softmaxes of that kind.
+    with torch.no_grad():
+        for n, mod in model.named_modules():
+            if n.endswith("self_attn"):
+                mod.q_norm.weight.mul_(0.1)
+    return model.to(device=cuda, dtype=torch.bfloat16).eval()
+
+
+def _teacher_forced(model, ids, steps, cache):
+    """Logits of a prompt prefill and then of each token of `steps` fed one at a time."""
+    out = [model(ids, past_key_values=cache, use_cache=True).logits[:, -1].float()]
+    for t in range(steps.shape[1]):
+        out.append(model(steps[:, t:t + 1], past_key_values=cache, use_cache=True).logits[:, -1].float())
+    return torch.stack(out, 1)
+
+
+def test_gemma4_patched_close_to_unpatched(cuda):
+    """Gemma 4 (per-layer head dims, K = V layers, sliding windows shorter than
+    the prompt): fed the same tokens, the patched model's decode logits follow
+    the unpatched model's to quantisation accuracy, and unpatching restores it
+    exactly."""
+    from transformers import DynamicCache
+    from fused_turboquant.hf import check_model_compatibility, patch_model, unpatch_model
+    model = _tiny_gemma4(cuda)
+    rep = check_model_compatibility(model)
+    assert rep["compatible"] and rep["head_dims"] == [64, 128] and rep["k_eq_v_layers"] == 2, rep
+    g = torch.Generator().manual_seed(4)
+    ids = torch.randint(1, 320, (1, 30), generator=g).to(cuda)
+    steps = torch.randint(1, 320, (1, 12), generator=g).to(cuda)
+    with torch.inference_mode():
+        ref = _teacher_forced(model, ids, steps, DynamicCache(config=model.config))
+        cache = patch_model(model, bits=4, verify=True)
+        got = _teacher_forced(model, ids, steps, cache)
+        kinds = {i: type(lp).__name__ for i, lp in cache._pages.items()}
+        unpatch_model(model)
+        again = _teacher_forced(model, ids, steps, DynamicCache(config=model.config))
+    assert kinds == {0: "_LayerFlat", 1: "_LayerPages", 2: "_LayerFlat", 3: "_LayerPages"}, kinds
+    d0 = (got[:, 0] - ref[:, 0]).abs().max().item()
+    print(f"[gemma4 patched vs unpatched] prefill logits max diff {d0:.3e}")
+    assert torch.allclose(got[:, 0], ref[:, 0], atol=2e-2, rtol=2e-2)  # prefill: full precision
+    cos = torch.nn.functional.cosine_similarity(got[0, 1:], ref[0, 1:], dim=-1)
+    print(f"[gemma4 patched vs unpatched] decode logits cos per step {[round(c, 4) for c in cos.tolist()]}")
+    assert cos.min() > 0.95 and cos.mean() > 0.975
+    assert torch.equal(again, ref)
+
+
+def test_flat_layer_decode_matches_dense(cuda):
+    """A head dim without a paged kernel (64): the flat rows decode to the
+    oracle's dequantised vectors and the decode attention equals float64
+    softmax attention over them, per sequence length; with a window, only the
+    last `window` positions and the first `sinks` are attended."""
+    from fused_turboquant import TurboQuantMSE
+    from fused_turboquant.hf import CompressedKVCache
+    d, B, hkv, hq = 64, 2, 2, 8
+    tq = TurboQuantMSE(d, bits=3, device=cuda)
+    cache = CompressedKVCache(tq)
+    cache.set_layer_quantizer(0, tq)
+    g = torch.Generator().manual_seed(6)
+    k = torch.randn(B, hkv, 21, d, generator=g).to(torch.bfloat16).to(cuda)
+    v = torch.randn(B, hkv, 21, d, generator=g).to(torch.bfloat16).to(cuda)
+    keep = torch.ones(B, 21, dtype=torch.bool)
+    keep[1, :4] = False  # left padding of sequence 1
+    cache.store_compressed_kv(k, v, 0, keep=keep.to(cuda))
+    for _ in range(3):
+        cache.store_compressed_kv(k[:, :, :1] * 0.5, v[:, :, :1] * 2, 0)
+    assert cache.seq_lens(0) == [24, 20]
+    q = torch.randn(B, hq, d, generator=g).to(torch.bfloat16).to(cuda)
+    kd = cache.decode_keys(0).double().cpu().numpy()
+    vd = cache.decode_values(0).double().cpu().numpy()
+    for window, sinks in ((None, 0), (6, 2)):
+        got = cache.decode_attention(q, 0, 0.125, sliding_window=window, sink_tokens=sinks).float().cpu().numpy()
+        for b, L in enumerate((24, 20)):
+            pos = np.arange(L)
+            if window is not None:
+                pos = pos[(pos >= L - window) | (pos < sinks)]
+            for h in range(hq):
+                s = kd[b, h // 4, pos] @ q[b, h].double().cpu().numpy() * 0.125
+                p = np.exp(s - s.max())
+                want = (p / p.sum()) @ vd[b, h // 4, pos]
+                err = np.abs(got[b, h] - want).max()
+                assert err <= 1e-2 + 2 ** -8 * np.abs(want).max(), (window, b, h, err)
+
+
+def test_chunked_prefill_matches_one_pass(cuda):
+    """chunked_prefill (reference hf/chunked_prefill.py:35-95): the next-token
+    logits after a prompt prefilled in chunks of 7 follow a one-pass prefill
+    of the same prompt to quantisation accuracy (each chunk attends over the
+    compressed earlier chunks), and decode continues from the chunked cache."""
+    from fused_turboquant.hf import patch_model, unpatch_model
+    from fused_turboquant.hf.chunked_prefill import chunked_prefill
+    model = _tiny_llama(cuda)
+    ids = torch.randint(1, 320, (1, 40), generator=torch.Generator().manual_seed(8)).to(cuda)
+    cache = patch_model(model, bits=4, verify=False)
+    with torch.inference_mode():
+        one = model(ids, past_key_values=cache, use_cache=True).logits[:, -1].float()
+        cache.reset()
+        chunked = chunked_prefill(model, ids, cache, chunk_size=7)[:, -1].float()
+        assert cache.seq_lens(0) == [40]
+        nxt = model(chunked.argmax(-1, keepdim=True), past_key_values=cache, use_cache=True).logits
+    unpatch_model(model)
+    cos = torch.nn.functional.cosine_similarity(one, chunked, dim=-1).min().item()
+    print(f"[chunked prefill] last-token logits cos {cos:.4f}")
+    assert cos > 0.98 and torch.isfinite(nxt).all()

@@ -56,8 +56,10 @@ def test_check_model_compatibility():
     r = check_model_compatibility(_tiny_llama())
     assert r["compatible"] and r["eligible_layers"] == 2 and r["head_dim"] == 128
     assert r["n_q_heads"] == 4 and r["n_kv_heads"] == 2 and r["known_compatible"]
-    r64 = check_model_compatibility(_tiny_llama(head_dim=64))
-    assert not r64["compatible"] and any("head_dim" in i for i in r64["issues"])
+    r64 = check_model_compatibility(_tiny_llama(head_dim=64))  # flat rows + torch attention
+    assert r64["compatible"] and r64["head_dims"] == [64] and r64["paged_head_dims"] == []
+    r96 = check_model_compatibility(_tiny_llama(head_dim=96))
+    assert not r96["compatible"] and any("head_dim" in i for i in r96["issues"])
 
 
 def test_quantizer_routing():
@@ -125,3 +127,57 @@ def test_smoke_test_rejects_a_wrong_attention_path():
     with pytest.raises(RuntimeError, match="cosine similarity"):
         FC._smoke_test(model, _ResettableCache(), originals, model.config)
     assert all(m.forward is patched[n] for n, m in model.named_modules() if n in originals)
+
+
+def _tiny_gemma4(shared=0):
+    from transformers import Gemma4TextConfig
+    from transformers.models.gemma4.modeling_gemma4 import Gemma4ForCausalLM
+    cfg = Gemma4TextConfig(vocab_size=320, hidden_size=256, intermediate_size=512, num_hidden_layers=4,
+                           num_attention_heads=4, num_key_value_heads=2, head_dim=64, global_head_dim=128,
+                           sliding_window=8,
+                           layer_types=["sliding_attention", "full_attention", "sliding_attention", "full_attention"],
+                           attention_k_eq_v=True, num_global_key_value_heads=1, vocab_size_per_layer_input=320,
+                           hidden_size_per_layer_input=16, max_position_embeddings=512, num_kv_shared_layers=shared)
+    torch.manual_seed(0)
+    return Gemma4ForCausalLM(cfg)
+
+
+def test_gemma4_compatibility_report():
+    """Gemma 4: per-layer head dims (64 sliding, 128 full), K = V full layers,
+    sliding windows, scaling 1.0 -- reported compatible; KV-shared layers are
+    reported and refused by patch_model (reference hf/fused_cache.py:421-426)."""
+    from fused_turboquant.hf import check_model_compatibility, patch_model
+    from fused_turboquant.hf import fused_cache as FC
+    m = _tiny_gemma4()
+    r = check_model_compatibility(m)
+    assert r["compatible"], r["issues"]
+    assert r["head_dims"] == [64, 128] and r["paged_head_dims"] == [128] and r["k_eq_v_layers"] == 2
+    attn = [mod for n, mod in m.named_modules() if n.endswith("self_attn")]
+    assert [FC._resolve_layer_head_dim(a, m.config) for a in attn] == [64, 128, 64, 128]
+    assert [FC._layer_sliding_window(a, m.config) for a in attn] == [8, None, 8, None]
+    assert [FC._module_k_eq_v(a) for a in attn] == [False, True, False, True]
+    s = _tiny_gemma4(shared=2)
+    r = check_model_compatibility(s)
+    assert not r["compatible"] and r["kv_shared_layers"] == 2
+    with pytest.raises(ValueError, match="KV-shared"):
+        patch_model(s, bits=4)
+
+
+def test_keep_and_window_masks():
+    """Padding detection reads each token from the last query row whose
+    window holds it; the continuation mask limits rows to their window."""
+    from fused_turboquant.hf import fused_cache as FC
+    q, W = 6, 3
+    i = torch.arange(q)
+    vis = (i[None, :] <= i[:, None]) & (i[None, :] > i[:, None] - W)   # sliding causal
+    vis = vis[None, None].repeat(2, 1, 1, 1)
+    vis[1, :, :, :2] = False                                          # sequence 1: two padding tokens
+    keep = FC._keep_from_mask(vis, q, W)
+    assert keep.tolist() == [[True] * 6, [False, False, True, True, True, True]]
+    assert FC._keep_from_mask(vis[:1], q, W) is None
+    m = FC._continuation_mask([5, 2], 5, 3, None, None, True, "cpu", window=4)[:, 0]
+    # sequence 0: rows at positions 5, 6, 7 see positions > p - 4 of its 5 past + itself causally
+    assert m[0, 0].tolist() == [False, False, True, True, True, True, False, False]
+    assert m[0, 2].tolist() == [False, False, False, False, True, True, True, True]
+    # sequence 1: 2 past positions (2..4 of the decoded past are not its own)
+    assert m[1, 0].tolist() == [True, True, False, False, False, True, False, False]
