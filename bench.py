@@ -259,29 +259,33 @@ def make_config4(dev, seed=4):
     return layer, cache, q, bt.to(dev), sl, lens
 
 
-def v1_setup(dev):
+def v1_setup(dev, cfg4=None, operands="f16"):
+    """The config-4 v1 decode; operands "fp32" = the fp32-product VALU kernel
+    (v_flags bit 3) over the same cache."""
     import torch
     from fused_turboquant import _lib
     from fused_turboquant import v1 as V1
-    layer, cache, q, bt, sl, lens = make_config4(dev)
+    layer, cache, q, bt, sl, lens = cfg4 if cfg4 is not None else make_config4(dev)
+    flags = V1.VROT | (V1.FP32 if operands == "fp32" else 0)
     B, hq, d = q.shape
     hkv = cache.shape[2]
     splits = V1.default_splits(B, hkv, max(lens))
     out = torch.empty(B, hq, d, dtype=torch.bfloat16, device=dev)
     ws = torch.empty(V1.workspace_bytes(B, hq, d, splits), dtype=torch.uint8, device=dev)
     V1.v1_decode_attention(q, cache, bt, sl, layer.centroids, layer.key_bits, layer.value_bits,
-                           v_rotate=True, num_splits=splits, out=out, workspace=ws)
+                           v_rotate=True, num_splits=splits, out=out, workspace=ws, operands=operands)
     L = V1._bind()
     sb, sp, sh = cache.stride(0), cache.stride(1), cache.stride(2)
     nb, bs = cache.shape[0], cache.shape[1]
     run = lean_launch(L.ftq_v1_decode_attention, q, _lib.dtype_code(q.dtype), cache, nb, bs, sb, sp, sh,
                       bt, bt.shape[1], sl, None, B, hq, hkv, d, layer.centroids, layer.key_bits,
-                      layer.value_bits, 1.0 / math.sqrt(d), 1, splits, ws, ws.numel(), out,
+                      layer.value_bits, 1.0 / math.sqrt(d), flags, splits, ws, ws.numel(), out,
                       _lib.dtype_code(out.dtype), _lib.stream_ptr(dev))
     per_tok = V1.slot_bytes(d, layer.key_bits, layer.value_bits)  # 66 B of K + 36 B of V
     kv_bytes = sum(lens) * hkv * per_tok
     total = kv_bytes + q.numel() * 2 + out.numel() * 2 + sum((n + 15) // 16 for n in lens) * 4 + B * 4
-    return {"run": run, "kv_bytes": kv_bytes, "total_bytes": total, "splits": splits, "lens": lens}
+    return {"run": run, "kv_bytes": kv_bytes, "total_bytes": total, "splits": splits, "lens": lens,
+            "cfg4": (layer, cache, q, bt, sl, lens)}
 
 
 def raw_setup(dev, B=32, hq=32, hkv=8, d=128, ctx=8192, bs=16, seed=5):
@@ -506,10 +510,12 @@ def main():
     cfg3 = make_config3(dev, keep_first=not args.no_cpu)
     attn3 = paged_setup(dev, cfg3, "f16")
     attn3v = paged_setup(dev, cfg3, "fp32") if want("paged_attn_config3_fp32_valu") else None
-    attn4 = attnr = None
-    if want("v1_attn_config4"):
+    attn4 = attn4v = attnr = None
+    if want("v1_attn_config4") or want("v1_attn_config4_fp32_valu"):
         log("[bench] config4 v1 cache (B=4 ctx~U[64K,128K] K4V2 v_rotate)")
         attn4 = v1_setup(dev)
+        if want("v1_attn_config4_fp32_valu"):
+            attn4v = v1_setup(dev, attn4["cfg4"], "fp32")
     if want("raw_attn_boundary"):
         log("[bench] boundary-layer raw fp16 cache (config3 shape, 512 B slots)")
         attnr = raw_setup(dev)
@@ -581,6 +587,8 @@ def main():
         entry("paged_attn_config3_fp32_valu", attn3v["run"], attn3v["total_bytes"])
     if attn4 is not None:
         entry("v1_attn_config4", attn4["run"], attn4["total_bytes"])
+    if attn4v is not None:
+        entry("v1_attn_config4_fp32_valu", attn4v["run"], attn4v["total_bytes"])
     if attnr is not None:
         entry("raw_attn_boundary", attnr["run"], attnr["total_bytes"])
     for name, st in stores.items():

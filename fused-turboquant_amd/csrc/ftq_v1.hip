@@ -392,7 +392,11 @@ __global__ __launch_bounds__(256, 2) void v1_attn_kernel(
 
   // LDS pool, reused in three phases: rotated queries (prologue), the K code
   // pair table (tile loop), the wave-merge buffer (epilogue)
-  constexpr int LUT_BYTES = 4 << (2 * KB);  // f16 pair f16(sigma c[e & mask]) | f16(sigma c[e >> KB]) << 16
+  // K pair table: entry e = f16(sigma c[e & mask]) | f16(sigma c[e >> KB]) << 16, in LUT_C
+  // interleaved copies (lane l reads copy l % LUT_C), so the random lookups of
+  // a 32-lane LDS phase spread over the banks
+  constexpr int LUT_LOGC = 5;
+  constexpr int LUT_BYTES = (4 << (2 * KB)) << LUT_LOGC;
   constexpr int RED_BYTES = 4 * 16 * (D + 1) * 4;
   constexpr int QS_BYTES = 16 * (D + 4) * 4;
   constexpr int POOL0 = LUT_BYTES > RED_BYTES ? LUT_BYTES : RED_BYTES;
@@ -408,6 +412,7 @@ __global__ __launch_bounds__(256, 2) void v1_attn_kernel(
   float (*qs)[D + 4] = reinterpret_cast<float (*)[D + 4]>(pool);
   float (*red_o)[16][D + 1] = reinterpret_cast<float (*)[16][D + 1]>(pool);
   uint8_t* lut = pool;
+  const uint8_t* lutl = pool + 4 * (lane & ((1 << LUT_LOGC) - 1));  // this lane's copy of the K pair table
 
   if (tid < (1 << KB)) centl[tid] = cent[tid];
   // q_rot = q H / sqrt(D) for the G query heads of this kv head (one per 16 lanes),
@@ -448,8 +453,10 @@ __global__ __launch_bounds__(256, 2) void v1_attn_kernel(
   __syncthreads();  // qs is dead; its LDS now holds the pair table
   const float csc = table_scale<1 << KB>(cent, true).sigma;
   const float vk = csc * (1.f / 256.f), vinv = 256.f / csc;  // Lloyd-Max V: P' scale and its inverse
-  for (int e = tid; e < (1 << (2 * KB)); e += 256)
-    reinterpret_cast<uint32_t*>(lut)[e] = cent_hilo_pair(csc * centl[e & ((1 << KB) - 1)], csc * centl[e >> KB]).x;
+  for (int k = tid; k < ((1 << (2 * KB)) << LUT_LOGC); k += 256) {
+    const int e = k >> LUT_LOGC;
+    reinterpret_cast<uint32_t*>(lut)[k] = cent_hilo_pair(csc * centl[e & ((1 << KB) - 1)], csc * centl[e >> KB]).x;
+  }
   if constexpr (VLM) {
     constexpr int NC = 1 << KB;  // codes >= NC do not occur; they read the top centroid
     const int c0 = tid & 15, c1 = tid >> 4;
@@ -512,7 +519,7 @@ __global__ __launch_bounds__(256, 2) void v1_attn_kernel(
         Op8 a;
 #pragma unroll
         for (int p = 0; p < 4; ++p)
-          a.u[p] = *reinterpret_cast<const uint32_t*>(lut + field_off<2>(cur.k[st], (8 * s + 2 * p) * KB, 2 * KB));
+          a.u[p] = *reinterpret_cast<const uint32_t*>(lutl + field_off<2 + LUT_LOGC>(cur.k[st], (8 * s + 2 * p) * KB, 2 * KB));
         sacc[st] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a.h, qb[s].h, sacc[st], 0, 0, 0);
         sacc[st] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a.h, ql[s].h, sacc[st], 0, 0, 0);
         gacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a.h, a.h, gacc, 0, 0, 0);
@@ -794,7 +801,11 @@ __global__ __launch_bounds__(256, VB == 2 ? 4 : 2) void v1_attn_g4_kernel(
   const int m = lane & 15, g = lane >> 4;      // MFMA layout: row / column m, k-group g
   const int ci = (lane >> 2) & 3;  // compact layout: head lane & 3, token 4g + ci
 
-  constexpr int LUT_BYTES = 4 << (2 * KB);  // f16 pair f16(sigma c[e & mask]) | f16(sigma c[e >> KB]) << 16
+  // K pair table in LUT_C interleaved copies (lane l reads copy l % LUT_C):
+  // 32 for 2- and 3-bit keys; 16 for 4-bit (16 KB, so that 4 workgroups still
+  // fit a CU's LDS)
+  constexpr int LUT_LOGC = KB == 4 ? 4 : 5;
+  constexpr int LUT_BYTES = (4 << (2 * KB)) << LUT_LOGC;
   constexpr int RED_BYTES = 4 * G * (D + 1) * 4;
   constexpr int QS_BYTES = G * (D + 4) * 4;
   constexpr int POOL0 = LUT_BYTES > RED_BYTES ? LUT_BYTES : RED_BYTES;
@@ -807,6 +818,7 @@ __global__ __launch_bounds__(256, VB == 2 ? 4 : 2) void v1_attn_g4_kernel(
   float (*qs)[D + 4] = reinterpret_cast<float (*)[D + 4]>(pool);
   float (*red_o)[G][D + 1] = reinterpret_cast<float (*)[G][D + 1]>(pool);
   uint8_t* lut = pool;
+  const uint8_t* lutl = pool + 4 * (lane & ((1 << LUT_LOGC) - 1));  // this lane's copy of the K pair table
 
   if (tid < (1 << KB)) centl[tid] = cent[tid];
   {
@@ -846,8 +858,10 @@ __global__ __launch_bounds__(256, VB == 2 ? 4 : 2) void v1_attn_g4_kernel(
   __syncthreads();
   {
     const float csc = table_scale<1 << KB>(cent, true).sigma;
-    for (int e = tid; e < (1 << (2 * KB)); e += 256)
-      reinterpret_cast<uint32_t*>(lut)[e] = cent_hilo_pair(csc * centl[e & ((1 << KB) - 1)], csc * centl[e >> KB]).x;
+    for (int k = tid; k < ((1 << (2 * KB)) << LUT_LOGC); k += 256) {
+      const int e = k >> LUT_LOGC;
+      reinterpret_cast<uint32_t*>(lut)[k] = cent_hilo_pair(csc * centl[e & ((1 << KB) - 1)], csc * centl[e >> KB]).x;
+    }
   }
   __syncthreads();
 
@@ -902,7 +916,7 @@ __global__ __launch_bounds__(256, VB == 2 ? 4 : 2) void v1_attn_g4_kernel(
         Op8 a;
 #pragma unroll
         for (int p = 0; p < 4; ++p)
-          a.u[p] = *reinterpret_cast<const uint32_t*>(lut + field_off<2>(cur.k[st], (8 * s + 2 * p) * KB, 2 * KB));
+          a.u[p] = *reinterpret_cast<const uint32_t*>(lutl + field_off<2 + LUT_LOGC>(cur.k[st], (8 * s + 2 * p) * KB, 2 * KB));
         sacc[st] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a.h, qb[s].h, sacc[st], 0, 0, 0);
         gacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a.h, a.h, gacc, 0, 0, 0);
       }
