@@ -188,13 +188,42 @@ int codec_grid(int64_t n, int gpb) {
 }
 
 template <int D, int BITS, int DT, bool SYM>
-static void launch_encode_mfma(const void* x, int64_t n, const float* signs, const float* bnd,
-                               float sc, double rsc, uint8_t* packed, uint16_t* norms, hipStream_t st) {
+static void launch_encode_mfma(const EncodeSegs& io, int64_t n, const float* signs, const float* bnd,
+                               float sc, double rsc, hipStream_t st) {
   // one pass of resident workgroups, each wave looping over groups of 16 vectors
   static const int cap = resident_workgroups(encode_mfma_kernel<D, BITS, DT, SYM>);
-  const int64_t want = (n + 63) / 64;
+  const int64_t want = ((n + 15) / 16 * io.nseg + 3) / 4;
   encode_mfma_kernel<D, BITS, DT, SYM><<<dim3((unsigned)(want < cap ? want : cap)), dim3(256), 0, st>>>(
-      x, n, signs, bnd, sc, rsc, packed, norms);
+      io, n, signs, bnd, sc, rsc);
+}
+
+// The matrix-core encoder takes this input: d = 128 / 256, 16-bit elements.
+static bool encode_mfma_ok(int d, int dt) { return (d == 128 || d == 256) && dt != F32; }
+
+template <int D, int BITS>
+static void launch_encode_mfma_db(const EncodeSegs& io, int dt, int64_t n, const float* signs,
+                                  const float* bnd, int cb_class, hipStream_t st) {
+  if constexpr (D == 128 || D == 256) {
+    const float sc = fwht_scale(D);
+    const double rsc = 1.0 / (double)sc;
+    const bool sym = cb_class == FTQ_CB_SYMMETRIC;
+    if (dt == F16) {
+      if (sym) launch_encode_mfma<D, BITS, F16, true>(io, n, signs, bnd, sc, rsc, st);
+      else launch_encode_mfma<D, BITS, F16, false>(io, n, signs, bnd, sc, rsc, st);
+    } else {
+      if (sym) launch_encode_mfma<D, BITS, BF16, true>(io, n, signs, bnd, sc, rsc, st);
+      else launch_encode_mfma<D, BITS, BF16, false>(io, n, signs, bnd, sc, rsc, st);
+    }
+  }
+}
+
+template <int D>
+static hipError_t launch_encode_mfma_d(const EncodeSegs& io, int dt, int64_t n, const float* signs,
+                                       const float* bnd, int bits, int cb_class, hipStream_t st) {
+  if (bits == 2) launch_encode_mfma_db<D, 2>(io, dt, n, signs, bnd, cb_class, st);
+  else if (bits == 3) launch_encode_mfma_db<D, 3>(io, dt, n, signs, bnd, cb_class, st);
+  else launch_encode_mfma_db<D, 4>(io, dt, n, signs, bnd, cb_class, st);
+  return hipGetLastError();
 }
 
 template <int D, int BITS>
@@ -203,18 +232,10 @@ static hipError_t launch_encode_db(const void* x, int dt, int64_t n, const float
                                    hipStream_t st) {
   const float sc = fwht_scale(D);
   const double rsc = 1.0 / (double)sc;
-  if constexpr (D == 128 || D == 256) {
-    if (dt != F32) {  // 16-bit inputs: Hadamard transform on the matrix cores
-      const bool sym = cb_class == FTQ_CB_SYMMETRIC;
-      if (dt == F16) {
-        if (sym) launch_encode_mfma<D, BITS, F16, true>(x, n, signs, bnd, sc, rsc, packed, norms, st);
-        else launch_encode_mfma<D, BITS, F16, false>(x, n, signs, bnd, sc, rsc, packed, norms, st);
-      } else {
-        if (sym) launch_encode_mfma<D, BITS, BF16, true>(x, n, signs, bnd, sc, rsc, packed, norms, st);
-        else launch_encode_mfma<D, BITS, BF16, false>(x, n, signs, bnd, sc, rsc, packed, norms, st);
-      }
-      return hipGetLastError();
-    }
+  if (encode_mfma_ok(D, dt)) {  // 16-bit inputs: Hadamard transform on the matrix cores
+    const EncodeSegs io{x, nullptr, packed, nullptr, norms, nullptr, 1};
+    launch_encode_mfma_db<D, BITS>(io, dt, n, signs, bnd, cb_class, st);
+    return hipGetLastError();
   }
   constexpr int VPB = 256 / FastShape<D>::LPV;
   dim3 grid(codec_grid(n, VPB)), block(256);
@@ -310,6 +331,35 @@ extern "C" int ftq_encode_cb(const void* x, int x_dtype, int64_t n, int d, const
   else if (d == 64) e = launch_encode_d<64>(x, x_dtype, n, signs, boundaries, bits, codebook_class, packed_out, norms_out, st);
   else if (d == 128) e = launch_encode_d<128>(x, x_dtype, n, signs, boundaries, bits, codebook_class, packed_out, norms_out, st);
   else e = launch_encode_d<256>(x, x_dtype, n, signs, boundaries, bits, codebook_class, packed_out, norms_out, st);
+  return hip_status(e);
+}
+
+extern "C" int ftq_encode_kv(const void* k, const void* v, int x_dtype, int64_t n, int d,
+                             const float* signs, const float* boundaries, int bits, int codebook_class,
+                             uint8_t* k_packed_out, uint16_t* k_norms_out, uint8_t* v_packed_out,
+                             uint16_t* v_norms_out, void* stream) {
+  FTQ_REQUIRE(n >= 0, "n must be >= 0");
+  FTQ_REQUIRE(d == 64 || d == 128 || d == 256 || codec_any_dim(d), "head_dim must be a power of two in [8, 4096]");
+  FTQ_REQUIRE(bits >= 2 && bits <= 4, "bits must be 2, 3, or 4");
+  FTQ_REQUIRE(x_dtype >= F32 && x_dtype <= BF16, "x_dtype must be FTQ_F32, FTQ_F16 or FTQ_BF16");
+  FTQ_REQUIRE(codebook_class == FTQ_CB_ANY || codebook_class == FTQ_CB_SYMMETRIC,
+              "codebook_class must be FTQ_CB_ANY or FTQ_CB_SYMMETRIC");
+  if (n == 0) return FTQ_OK;
+  FTQ_REQUIRE(k && v && signs && boundaries && k_packed_out && k_norms_out && v_packed_out && v_norms_out,
+              "null pointer argument");
+  if (!encode_mfma_ok(d, x_dtype)) {  // no fused kernel for this input: one launch per tensor
+    const int e = ftq_encode_cb(k, x_dtype, n, d, signs, boundaries, bits, codebook_class, k_packed_out,
+                                k_norms_out, stream);
+    if (e != FTQ_OK) return e;
+    return ftq_encode_cb(v, x_dtype, n, d, signs, boundaries, bits, codebook_class, v_packed_out,
+                         v_norms_out, stream);
+  }
+  FTQ_REQUIRE(aligned16(k) && aligned16(v), "k and v must be 16-byte aligned");
+  FTQ_REQUIRE(aligned4(k_packed_out) && aligned4(v_packed_out), "packed outputs must be 4-byte aligned");
+  const EncodeSegs io{k, v, k_packed_out, v_packed_out, k_norms_out, v_norms_out, 2};
+  hipStream_t st = (hipStream_t)stream;
+  hipError_t e = d == 128 ? launch_encode_mfma_d<128>(io, x_dtype, n, signs, boundaries, bits, codebook_class, st)
+                          : launch_encode_mfma_d<256>(io, x_dtype, n, signs, boundaries, bits, codebook_class, st);
   return hip_status(e);
 }
 

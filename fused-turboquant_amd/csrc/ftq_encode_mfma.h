@@ -22,7 +22,10 @@
 // from its copy of the codebook: one loop per kernel keeps the register count
 // at 126 (4 waves per SIMD) at d = 128.
 //
-// Transform.  A wave encodes 16 vectors at a time.  The input, sign-flipped,
+// Transform.  A wave encodes 16 vectors (a group) at a time.  A launch may
+// cover two tensors of the same shape (K and V of one store): the groups of
+// the second follow those of the first in one numbering, so the waves stream
+// both without a second launch.  The input, sign-flipped,
 // is the B operand of v_mfma_f32_16x16x32_{bf16,f16} (K = input element,
 // N = vector) and the Hadamard matrix is the A operand (M = output element),
 // with its rows and columns permuted so that every lane needs only four
@@ -52,6 +55,18 @@ namespace ftq {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+// The tensors one launch encodes: nseg (1 or 2) segments of n vectors each,
+// segment 1 being the V of a fused K + V store.  Unused pointers may be null.
+struct EncodeSegs {
+  const void* x0;
+  const void* x1;
+  uint8_t* packed0;
+  uint8_t* packed1;
+  uint16_t* norms0;
+  uint16_t* norms1;
+  int nseg;
+};
 
 union Op16x8 {
   uint32_t u[4];
@@ -205,12 +220,10 @@ __device__ __forceinline__ void quantize_pack_sym(const float (&x)[E], float Tm,
 }
 
 template <int D, int BITS, int DT, bool SYM>
-__global__ __launch_bounds__(256) void encode_mfma_kernel(const void* __restrict__ x, int64_t n,
+__global__ __launch_bounds__(256) void encode_mfma_kernel(EncodeSegs io, int64_t n,
                                                           const float* __restrict__ signs,
                                                           const float* __restrict__ boundaries,
-                                                          float c, double rc,
-                                                          uint8_t* __restrict__ packed,
-                                                          uint16_t* __restrict__ norms) {
+                                                          float c, double rc) {
   static_assert(D == 128 || D == 256, "MFMA encoder covers d = 128 and 256");
   static_assert(DT == BF16 || DT == F16, "MFMA encoder takes 16-bit inputs");
   constexpr int EL = D / 4;   // outputs (and inputs) per lane
@@ -259,8 +272,10 @@ __global__ __launch_bounds__(256) void encode_mfma_kernel(const void* __restrict
   const int diag_src = (((j >> 2) << 4) | j) << 2;  // ds_bpermute byte address
 
   const int64_t wave = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int64_t wstride = (int64_t)gridDim.x * 4 * 16;
-  const uint16_t* xb = static_cast<const uint16_t*>(x);
+  const int64_t gstride = (int64_t)gridDim.x * 4;
+  // groups of 16 vectors, numbered over the segments one after the other
+  const int64_t gps = (n + 15) >> 4;
+  const int64_t ngroups = gps * io.nseg;
 
   // interior boundaries (wave-uniform)
   float Bv[NT];
@@ -271,7 +286,18 @@ __global__ __launch_bounds__(256) void encode_mfma_kernel(const void* __restrict
   // groups of 16 vectors; the next group's input is loaded while the current
   // one is encoded.  Past the end the load repeats the last vector, so every
   // iteration issues the same loads and the wait counts stay static.
-  auto load_group = [&](int64_t g0, Op16x8 (&dst)[KS]) {
+  // group g (clamped to the last one, so a prefetch past the end stays in
+  // bounds): its segment and the index of its first vector there
+  auto locate = [&](int64_t g, int& seg, int64_t& g0) {
+    g = g < ngroups ? g : ngroups - 1;
+    seg = g >= gps ? 1 : 0;
+    g0 = (g - (seg ? gps : 0)) << 4;
+  };
+  auto load_group = [&](int64_t g, Op16x8 (&dst)[KS]) {
+    int seg;
+    int64_t g0;
+    locate(g, seg, g0);
+    const uint16_t* xb = static_cast<const uint16_t*>(seg ? io.x1 : io.x0);
     const int64_t vv = g0 + j < n ? g0 + j : n - 1;
     const uint4* src = reinterpret_cast<const uint4*>(xb + vv * D + EL * q);
 #pragma unroll
@@ -295,7 +321,7 @@ __global__ __launch_bounds__(256) void encode_mfma_kernel(const void* __restrict
     nrm = sqrt_rn(xx * (float)D) * c;
     return (nrm + 1e-8f) * rcf;
   };
-  auto encode_group = [&](Op16x8 (&cur)[KS], int64_t g0) {
+  auto encode_group = [&](Op16x8 (&cur)[KS], int64_t g) {
     flip_signs(cur);
     f32x4_t acc[MB];
 #pragma unroll
@@ -329,6 +355,11 @@ __global__ __launch_bounds__(256) void encode_mfma_kernel(const void* __restrict
       for (int k = 0; k < NT; ++k) T[k] = Bv[k] * sv;
       quantize_pack<BITS, EL>(t, T, w);
     }
+    int seg;
+    int64_t g0;
+    locate(g, seg, g0);
+    uint8_t* packed = seg ? io.packed1 : io.packed0;
+    uint16_t* norms = seg ? io.norms1 : io.norms0;
     const int64_t v = g0 + j;
     if (v < n) {
       uint32_t* dst = reinterpret_cast<uint32_t*>(packed + v * PD) + NW * q;
@@ -344,20 +375,20 @@ __global__ __launch_bounds__(256) void encode_mfma_kernel(const void* __restrict
       if (q == 0) norms[v] = (uint16_t)f32_to_f16_bits(nrm);
     }
   };
-  if (wave * 16 >= n) return;
+  if (wave >= ngroups) return;
   // two register sets alternate, so no copies between iterations
-  int64_t v0 = wave * 16;
+  int64_t g = wave;
   Op16x8 b0[KS], b1[KS];
-  load_group(v0, b0);
+  load_group(g, b0);
   for (;;) {
-    load_group(v0 + wstride, b1);
-    encode_group(b0, v0);
-    v0 += wstride;
-    if (v0 >= n) break;
-    load_group(v0 + wstride, b0);
-    encode_group(b1, v0);
-    v0 += wstride;
-    if (v0 >= n) break;
+    load_group(g + gstride, b1);
+    encode_group(b0, g);
+    g += gstride;
+    if (g >= ngroups) break;
+    load_group(g + gstride, b0);
+    encode_group(b1, g);
+    g += gstride;
+    if (g >= ngroups) break;
   }
 }
 

@@ -75,6 +75,33 @@ std::tuple<at::Tensor, at::Tensor> encode(const at::Tensor& x, const at::Tensor&
   return {packed, norms};
 }
 
+std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> encode_kv(const at::Tensor& k, const at::Tensor& v,
+                                                                     const at::Tensor& signs,
+                                                                     const at::Tensor& boundaries, int64_t bits,
+                                                                     int64_t codebook_class) {
+  contig(k, "k");
+  contig(v, "v");
+  contig(signs, "signs");
+  contig(boundaries, "boundaries");
+  TORCH_CHECK(k.sizes() == v.sizes() && k.scalar_type() == v.scalar_type() && k.device() == v.device(),
+              "fused_tq: k and v must agree in shape, dtype and device");
+  const c10::DeviceGuard g(k.device());
+  const int64_t d = k.size(-1);
+  const int64_t n = d > 0 ? k.numel() / d : 0;
+  auto sizes = k.sizes().vec();
+  sizes.back() = d * bits / 8;
+  at::Tensor kp = at::empty(sizes, k.options().dtype(at::kByte));
+  at::Tensor vp = at::empty(sizes, k.options().dtype(at::kByte));
+  sizes.pop_back();
+  at::Tensor kn = at::empty(sizes, k.options().dtype(at::kHalf));
+  at::Tensor vn = at::empty(sizes, k.options().dtype(at::kHalf));
+  check_rc(ftq_encode_kv(k.data_ptr(), v.data_ptr(), dt(k), n, (int)d, signs.data_ptr<float>(),
+                         boundaries.data_ptr<float>(), (int)bits, (int)codebook_class, kp.data_ptr<uint8_t>(),
+                         reinterpret_cast<uint16_t*>(kn.data_ptr()), vp.data_ptr<uint8_t>(),
+                         reinterpret_cast<uint16_t*>(vn.data_ptr()), stream_of(k)));
+  return {kp, kn, vp, vn};
+}
+
 at::Tensor decode(const at::Tensor& packed, const at::Tensor& norms, const at::Tensor& levels, const at::Tensor& signs,
                   int64_t bits, int64_t d, c10::ScalarType out_dtype) {
   contig(packed, "packed");
@@ -260,6 +287,8 @@ void raw_decode_attention(const at::Tensor& query, const at::Tensor& kv_cache, c
 
 TORCH_LIBRARY(fused_tq, m) {
   m.def("encode(Tensor x, Tensor signs, Tensor boundaries, int bits, int codebook_class) -> (Tensor, Tensor)");
+  m.def("encode_kv(Tensor k, Tensor v, Tensor signs, Tensor boundaries, int bits, int codebook_class) -> "
+        "(Tensor, Tensor, Tensor, Tensor)");
   m.def("decode(Tensor packed, Tensor norms, Tensor levels, Tensor signs, int bits, int d, ScalarType out_dtype) -> Tensor");
   m.def("rht(Tensor x, Tensor signs, bool inverse, ScalarType out_dtype) -> Tensor");
   m.def("paged_store(Tensor key, Tensor value, Tensor(a!) kv_cache, Tensor slot_mapping, Tensor k_signs, "
@@ -280,6 +309,7 @@ TORCH_LIBRARY(fused_tq, m) {
 
 TORCH_LIBRARY_IMPL(fused_tq, CUDA, m) {
   m.impl("encode", &encode);
+  m.impl("encode_kv", &encode_kv);
   m.impl("decode", &decode);
   m.impl("rht", &rht);
   m.impl("paged_store", &paged_store);

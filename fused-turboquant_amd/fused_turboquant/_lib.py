@@ -29,6 +29,7 @@ _i64 = ctypes.c_int64
 SIGNATURES = {
     "ftq_encode": [_vp, _i32, _i64, _i32, _vp, _vp, _i32, _vp, _vp, _vp],
     "ftq_encode_cb": [_vp, _i32, _i64, _i32, _vp, _vp, _i32, _i32, _vp, _vp, _vp],
+    "ftq_encode_kv": [_vp, _vp, _i32, _i64, _i32, _vp, _vp, _i32, _i32, _vp, _vp, _vp, _vp, _vp],
     "ftq_codebook_class": [_vp, _i32],
     "ftq_decode": [_vp, _vp, _i64, _i32, _vp, _vp, _i32, _vp, _i32, _vp],
     "ftq_rht": [_vp, _i32, _i64, _i32, _vp, _i32, _vp, _i32, _vp],

@@ -81,6 +81,24 @@ class TurboQuantMSE:
                                           self.quantizer.codebook_class)
         return CompressedTensor(indices=packed, norms=norms, original_dim=self.head_dim, bits=self.bits)
 
+    def encode_kv(self, k: torch.Tensor, v: torch.Tensor) -> tuple[CompressedTensor, CompressedTensor]:
+        """``(encode(k), encode(v))`` of two tensors of one shape and dtype, in
+        one kernel launch for 16-bit input at d = 128 / 256 -- the stacked
+        K + V encode of ``FusedTurboQuantCache.store_compressed_kv``
+        (reference ``hf/fused_cache.py:274-330``) without the stack copy."""
+        if k.shape != v.shape or k.dtype != v.dtype:
+            raise ValueError(f"k {tuple(k.shape)} {k.dtype} and v {tuple(v.shape)} {v.dtype} must agree")
+        if k.shape[-1] != self.head_dim:
+            raise ValueError(f"last dim {k.shape[-1]} != head_dim {self.head_dim}")
+        _lib.require_device(k, v, self.rotation.signs, self.quantizer.boundaries)
+        kc, vc = k.contiguous(), v.contiguous()
+        if kc.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+            kc, vc = kc.float(), vc.float()
+        kp, kn, vp, vn = _ops.ops().encode_kv(kc, vc, self.rotation.signs, self.quantizer.boundaries, self.bits,
+                                              self.quantizer.codebook_class)
+        return (CompressedTensor(indices=kp, norms=kn, original_dim=self.head_dim, bits=self.bits),
+                CompressedTensor(indices=vp, norms=vn, original_dim=self.head_dim, bits=self.bits))
+
     # -- decode ------------------------------------------------------------
     def decode(self, compressed: CompressedTensor, out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
         d, bits = compressed.original_dim, compressed.bits

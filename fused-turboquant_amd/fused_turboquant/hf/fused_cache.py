@@ -177,7 +177,10 @@ class _LayerFlat:
 
     def append(self, key: torch.Tensor, value: torch.Tensor, keep: Optional[torch.Tensor]) -> None:
         B, hkv, q, d = key.shape
-        ck, cv = self.k_tq.encode(key), self.v_tq.encode(value)
+        if self.k_tq is self.v_tq and key.shape == value.shape and key.dtype == value.dtype:
+            ck, cv = self.k_tq.encode_kv(key, value)  # one launch for K and V
+        else:
+            ck, cv = self.k_tq.encode(key), self.v_tq.encode(value)
         if keep is None:
             counts = [q] * B
             pos = torch.tensor(self.lens, device=self.device).view(-1, 1) + torch.arange(q, device=self.device)

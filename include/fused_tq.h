@@ -74,6 +74,21 @@ int ftq_encode_cb(const void* x, int x_dtype, int64_t n, int d, const float* sig
                   uint16_t* norms_out, void* stream);
 
 /*
+ * ftq_encode_cb of two tensors of the same shape with one codebook, K and V
+ * of one store: k, v [n, d] (x_dtype) to k_packed_out / v_packed_out
+ * [n, d*bits/8] and k_norms_out / v_norms_out [n].  For 16-bit input at
+ * d = 128 / 256 one kernel launch streams both tensors (2n vectors); other
+ * inputs are encoded one tensor after the other on the stream.  Outputs are
+ * those of two ftq_encode_cb calls.
+ * Replaces the stacked single-launch encode of
+ * FusedTurboQuantCache.store_compressed_kv (reference hf/fused_cache.py:274-330),
+ * which encodes torch.stack([k, v]) with one TurboQuantMSE.encode.
+ */
+int ftq_encode_kv(const void* k, const void* v, int x_dtype, int64_t n, int d, const float* signs,
+                  const float* boundaries, int bits, int codebook_class, uint8_t* k_packed_out,
+                  uint16_t* k_norms_out, uint8_t* v_packed_out, uint16_t* v_norms_out, void* stream);
+
+/*
  * Fused library-format decode: unpack, levels[code] * norm, FWHT, * d^-1/2,
  * * signs.  out [n, d] in out_dtype (FTQ_F32 matches the reference).
  * Replaces triton_fused_decode (reference kernels/triton_decode.py:104-155)

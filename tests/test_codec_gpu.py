@@ -248,3 +248,78 @@ def test_other_power_of_two_head_dims(cuda, d, bits):
     assert np.array_equal(y.cpu().numpy(), O.rht(x.cpu().numpy(), s.cpu().numpy()))
     z = inverse_randomized_hadamard(y, s)
     assert np.array_equal(z.cpu().numpy(), O.inverse_rht(y.cpu().numpy(), s.cpu().numpy()))
+
+
+@pytest.mark.parametrize("d", [64, 128, 256, 512])
+@pytest.mark.parametrize("bits", [2, 3, 4])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_encode_kv_matches_two_encodes(cuda, d, bits, dtype):
+    """ftq_encode_kv (one launch over K and V for 16-bit input at d = 128 / 256,
+    two launches otherwise) returns exactly what two ftq_encode_cb calls return,
+    at vector counts that end mid-group (16 vectors a group) and on both sides of
+    one grid pass; the V half is also checked against the oracle."""
+    from fused_turboquant import TurboQuantMSE
+    tq = TurboQuantMSE(d, bits=bits, seed=42, device=cuda)
+    for n in (1, 15, 17, 2053, 70001 if d <= 256 else 3001):
+        k = _mk(n, d, dtype, seed=n + bits).to(cuda)
+        v = _mk(n, d, dtype, seed=n + bits + 1, outliers=True).to(cuda)
+        ck, cv = tq.encode_kv(k, v)
+        rk, rv = tq.encode(k), tq.encode(v)
+        label = f"d={d} bits={bits} {dtype} n={n}"
+        print(f"[encode_kv {label}]", flush=True)
+        for got, ref in ((ck, rk), (cv, rv)):
+            assert torch.equal(got.indices, ref.indices), label
+            assert torch.equal(got.norms.view(torch.int16), ref.norms.view(torch.int16)), label
+        if n == 2053:
+            _check_encode(tq, v.cpu(), cv, bits, d, label + " V")
+
+
+def test_encode_kv_c_abi(cuda):
+    """The C entry point: outputs of K and V land in their own buffers, shape
+    checks and the n = 0 no-op."""
+    from fused_turboquant import TurboQuantMSE, _lib
+    L = _lib.lib()
+    tq = TurboQuantMSE(128, bits=3, seed=42, device=cuda)
+    n = 333
+    k = _mk(n, 128, torch.bfloat16, seed=1).to(cuda)
+    v = _mk(n, 128, torch.bfloat16, seed=2).to(cuda)
+    kp = torch.full((n, 48), 0xAB, dtype=torch.uint8, device=cuda)
+    vp = torch.full((n, 48), 0xAB, dtype=torch.uint8, device=cuda)
+    kn = torch.zeros(n, dtype=torch.float16, device=cuda)
+    vn = torch.zeros(n, dtype=torch.float16, device=cuda)
+    sp = _lib.stream_ptr(cuda)
+    args = (tq.rotation.signs.data_ptr(), tq.quantizer.boundaries.data_ptr(), 3, tq.quantizer.codebook_class,
+            kp.data_ptr(), kn.data_ptr(), vp.data_ptr(), vn.data_ptr(), sp)
+    _lib.check(L.ftq_encode_kv(k.data_ptr(), v.data_ptr(), 2, n, 128, *args))
+    pk, nk = _encode_c(k, tq.rotation.signs, tq.quantizer.boundaries, 3, tq.quantizer.codebook_class, cuda)
+    pv, nv = _encode_c(v, tq.rotation.signs, tq.quantizer.boundaries, 3, tq.quantizer.codebook_class, cuda)
+    assert torch.equal(kp, pk) and torch.equal(vp, pv)
+    assert torch.equal(kn.view(torch.int16), nk.view(torch.int16)) and torch.equal(vn.view(torch.int16),
+                                                                                    nv.view(torch.int16))
+    before = kp.clone()
+    _lib.check(L.ftq_encode_kv(k.data_ptr(), v.data_ptr(), 2, 0, 128, *args))
+    torch.cuda.synchronize()
+    assert torch.equal(kp, before)
+    assert L.ftq_encode_kv(k.data_ptr(), None, 2, n, 128, *args) == -1
+    assert L.ftq_encode_kv(k.data_ptr(), v.data_ptr(), 2, n, 96, *args) == -1
+
+
+def test_encode_kv_past_2gib(cuda):
+    """K and V of more than 2^31 bytes each (byte offsets past 32 bits): the
+    codes and norms equal those of the two pieces encoded separately."""
+    from fused_turboquant import TurboQuantMSE
+    d = 128
+    chunk = (1 << 31) // (d * 2) - 16  # the first piece: just under 2^31 bytes
+    n = chunk + 1000
+    tq = TurboQuantMSE(d, bits=3, seed=42, device=cuda)
+    g = torch.Generator(device=cuda).manual_seed(5)
+    k = torch.randn(n, d, generator=g, device=cuda).to(torch.bfloat16)
+    v = torch.randn(n, d, generator=g, device=cuda).to(torch.bfloat16)
+    ck, cv = tq.encode_kv(k, v)
+    for x, c in ((k, ck), (v, cv)):
+        head, tail = tq.encode(x[:chunk]), tq.encode(x[chunk:].contiguous())
+        assert torch.equal(c.indices[:chunk], head.indices) and torch.equal(c.indices[chunk:], tail.indices)
+        assert torch.equal(c.norms[:chunk].view(torch.int16), head.norms.view(torch.int16))
+        assert torch.equal(c.norms[chunk:].view(torch.int16), tail.norms.view(torch.int16))
+    del k, v, ck, cv
+    torch.cuda.empty_cache()

@@ -95,6 +95,18 @@ def test_encode_cb_rejects_unknown_class():
     assert rc == -1 and b"codebook_class" in L.ftq_last_error()
 
 
+def test_encode_kv_validates_before_launch():
+    """ftq_encode_kv's argument checks run on the host (no device needed)."""
+    L = _built_lib().lib()
+    assert L.ftq_encode_kv(None, None, 2, 4, 128, None, None, 3, 7, None, None, None, None, None) == -1
+    assert b"codebook_class" in L.ftq_last_error()
+    assert L.ftq_encode_kv(None, None, 2, 4, 96, None, None, 3, 0, None, None, None, None, None) == -1
+    assert b"head_dim" in L.ftq_last_error()
+    assert L.ftq_encode_kv(None, None, 2, 4, 128, None, None, 3, 0, None, None, None, None, None) == -1
+    assert b"null" in L.ftq_last_error()
+    assert L.ftq_encode_kv(None, None, 2, 0, 128, None, None, 3, 0, None, None, None, None, None) == 0
+
+
 @pytest.mark.parametrize("d", [64, 128, 256])
 @pytest.mark.parametrize("bits", [1, 2, 3, 4])
 def test_product_codebook_matches_reference(golden, d, bits):
