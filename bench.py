@@ -52,10 +52,13 @@ RAMP_S = 0.3  # untimed seconds of back-to-back steps before any timing (clock r
 # HBM bytes per launch from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs of this
 # script, each scaled by the factor a 256 MiB device-to-device copy reads
 # (FETCH x2.0, WRITE x1.0); the summaries are in profiles/hbm_traffic_counters.md.
-# Keyed by roofline entry; None where no counter run covers the kernel.
+# Keyed by roofline entry; None where no counter run covers the kernel (the
+# small v1 stores, whose counts stay below the copy calibration's resolution).
 TRAFFIC_BYTES: dict = {
-    "encode_d128_3bit": 80336620, "encode_d256_3bit": 160154623, "decode_d128_3bit_f32": 149011545,
-    "paged_attn_config3": 219810032, "v1_attn_config4": 406670855, "raw_attn_boundary": 1081506403,
+    "encode_kv_d128_3bit": 160610070, "encode_kv_d128_3bit_same_input": 160589283,
+    "encode_d128_3bit": 80381460, "encode_d256_3bit": 160236278, "decode_d128_3bit_f32": 149002410,
+    "paged_attn_config3": 219807611, "v1_attn_config4": 406670855, "raw_attn_boundary": 1081506403,
+    "v1_store_config4_chunk": 170110042, "paged_store_config3_chunk": 323967432,
 }
 
 # config-1 outlier channels (x10), fixed here so the CPU baseline's input is reproducible
