@@ -21,8 +21,10 @@ Also timed (not part of the step), each with a roofline entry:
     library-format store of a config-3 chunk.
 Kernel times come from HIP events on the stream the library launches on
 (torch's current stream), in steady state: 20 untimed launches, then the
-median of three windows of back-to-back launches.  roofline.achieved =
-algorithmic bytes per launch / launch time.
+median of three windows of back-to-back launches.  The stores at the
+reference's small shapes take a few us, less than one launch from Python:
+they are recorded 50 to a HIP graph and timed per replay / 50.
+roofline.achieved = algorithmic bytes per launch / launch time.
 
 The CPU baseline (rank 0, N=1) times the torch restatement of the reference's
 unfused path (oracle/torch_ref.py) on the host cores: config 1, config-2
@@ -114,7 +116,41 @@ def lean_launch(fn, *args):
     call.status = status
     call.keep = tuple(keep)
     call.args = conv
+    call.fn = fn
     return call
+
+
+GRAPH_LAUNCHES = 50  # launches per HIP graph for the kernels shorter than a Python launch
+
+
+def graph_launcher(call, torch):
+    """The launches of a lean_launch call (its last argument is the stream)
+    recorded K = GRAPH_LAUNCHES times into one HIP graph on a stream of its own:
+    replaying it runs K back-to-back kernels without Python between them, so a
+    kernel shorter than one host launch (~14 us from Python) is timed by the
+    GPU, not by the host.  Returns replay(), whose time / K is one launch."""
+    s = torch.cuda.Stream()
+    conv = call.args[:-1] + (ctypes.c_void_p(s.cuda_stream),)
+    status = []
+
+    def on_s():
+        status.append(call.fn(*conv))
+    on_s.status = status
+    on_s.keep = call.keep
+    with torch.cuda.stream(s):
+        on_s()  # eager first: one-time host set-up of the launch path
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        for _ in range(GRAPH_LAUNCHES):
+            on_s()
+
+    def replay():
+        g.replay()
+    replay.parts = (on_s,)
+    replay.status = []
+    replay.graph = g
+    return replay
 
 
 def rotating(calls):
@@ -570,6 +606,7 @@ def main():
     for name, nt, d, kb, vb, kind, vrot in store_cases:
         if want(name):
             stores[name] = v1_store_setup(dev, nt, d, kb, vb, kind, vrot)
+            stores[name]["graph"] = nt <= 1024  # a few us: shorter than a launch from Python
     if want("paged_store_config3_chunk"):
         stores["paged_store_config3_chunk"] = paged_store_setup(dev)
     torch.cuda.synchronize()
@@ -616,9 +653,9 @@ def main():
     rl = {}
     timed = []
 
-    def entry(name, fn, alg_bytes, iters=it):
+    def entry(name, fn, alg_bytes, iters=it, per=1):
         if want(name):
-            rl[name] = roof(name, alg_bytes, time_launches(fn, iters, torch))
+            rl[name] = roof(name, alg_bytes, time_launches(fn, iters, torch) / per)
             timed.append(fn)
 
     entry("encode_kv_d128_3bit", enc_kv, 2 * enc_bytes)
@@ -637,7 +674,10 @@ def main():
     if attnr is not None:
         entry("raw_attn_boundary", attnr["run"], attnr["total_bytes"])
     for name, st in stores.items():
-        entry(name, st["run"], st["total_bytes"], iters=max(it, 100))
+        if st.get("graph"):  # shorter than a Python launch: K launches per HIP graph replay
+            entry(name, graph_launcher(st["run"], torch), st["total_bytes"], iters=4, per=GRAPH_LAUNCHES)
+        else:
+            entry(name, st["run"], st["total_bytes"], iters=max(it, 100))
     check_lean(*timed)
     for k, r in rl.items():
         log(f"[bench] {k}: {r['kernel_us']} us  {r['achieved']} GB/s  frac {r['frac']}")
