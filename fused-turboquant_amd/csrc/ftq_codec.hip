@@ -197,8 +197,12 @@ static void launch_encode_mfma(const EncodeSegs& io, int64_t n, const float* sig
       io, n, signs, bnd, sc, rsc);
 }
 
-// The matrix-core encoder takes this input: d = 128 / 256, 16-bit elements.
-static bool encode_mfma_ok(int d, int dt) { return (d == 128 || d == 256) && dt != F32; }
+// The matrix-core encoder takes this input: d = 128 / 256, 16-bit elements,
+// nseg tensors of n vectors in fewer than 2^31 - 2^20 groups of 16 (its
+// 32-bit group numbering; 2^35 vectors, far beyond device memory).
+static bool encode_mfma_ok(int d, int dt, int64_t n, int nseg) {
+  return (d == 128 || d == 256) && dt != F32 && (n + 15) / 16 * nseg < ((int64_t)1 << 31) - (1 << 20);
+}
 
 template <int D, int BITS>
 static void launch_encode_mfma_db(const EncodeSegs& io, int dt, int64_t n, const float* signs,
@@ -232,7 +236,7 @@ static hipError_t launch_encode_db(const void* x, int dt, int64_t n, const float
                                    hipStream_t st) {
   const float sc = fwht_scale(D);
   const double rsc = 1.0 / (double)sc;
-  if (encode_mfma_ok(D, dt)) {  // 16-bit inputs: Hadamard transform on the matrix cores
+  if (encode_mfma_ok(D, dt, n, 1)) {  // 16-bit inputs: Hadamard transform on the matrix cores
     const EncodeSegs io{x, nullptr, packed, nullptr, norms, nullptr, 1};
     launch_encode_mfma_db<D, BITS>(io, dt, n, signs, bnd, cb_class, st);
     return hipGetLastError();
@@ -347,7 +351,7 @@ extern "C" int ftq_encode_kv(const void* k, const void* v, int x_dtype, int64_t 
   if (n == 0) return FTQ_OK;
   FTQ_REQUIRE(k && v && signs && boundaries && k_packed_out && k_norms_out && v_packed_out && v_norms_out,
               "null pointer argument");
-  if (!encode_mfma_ok(d, x_dtype)) {  // no fused kernel for this input: one launch per tensor
+  if (!encode_mfma_ok(d, x_dtype, n, 2)) {  // no fused kernel for this input: one launch per tensor
     const int e = ftq_encode_cb(k, x_dtype, n, d, signs, boundaries, bits, codebook_class, k_packed_out,
                                 k_norms_out, stream);
     if (e != FTQ_OK) return e;

@@ -20,26 +20,33 @@
 // 3 compares, 1 select and 3 carry-adds per 3-bit element instead of 3, 4, 3.
 // The symmetric form is a separate instantiation (SYM), chosen by the host
 // from its copy of the codebook: one loop per kernel keeps the register count
-// at 126 (4 waves per SIMD) at d = 128.
+// at 100 (5 waves per SIMD) at d = 128 and 149 (3 waves) at d = 256.
 //
 // Transform.  A wave encodes 16 vectors (a group) at a time.  A launch may
 // cover two tensors of the same shape (K and V of one store): the groups of
 // the second follow those of the first in one numbering, so the waves stream
-// both without a second launch.  The input, sign-flipped,
-// is the B operand of v_mfma_f32_16x16x32_{bf16,f16} (K = input element,
-// N = vector) and the Hadamard matrix is the A operand (M = output element),
-// with its rows and columns permuted so that every lane needs only four
-// operand registers and ends up holding contiguous outputs:
+// both without a second launch.  The transform runs in 128-element blocks:
+// H_256 = [[H_128, H_128], [H_128, -H_128]] (the top index bit of the
+// Sylvester matrix contributes (-1)^(o7 e7)), so at d = 256 each half of the
+// input goes through the 128-point transform on the matrix cores and one fp32
+// add and subtract per output pair finish it: half the matrix-core work of the
+// dense 256 x 256 product, for one VALU operation per element.
+//
+// The 128-point transform: the input block, sign-flipped, is the B operand of
+// v_mfma_f32_16x16x32_{bf16,f16} (K = input element, N = vector) and the
+// Hadamard matrix is the A operand (M = output element), with its rows and
+// columns permuted so that every lane needs only four operand registers and
+// ends up holding contiguous outputs:
 //   lane l = 16 q + j  (q = l / 16, j = l % 16 = vector of the group)
-//   B operand, K step s: input elements e = EL q + 8 s + t, t = 0..7
-//   A operand, M block mb: row i = 4 q' + r holds output o = EL q' + 4 mb + r
+//   B operand, K step s: block elements e = 32 q + 8 s + t, t = 0..7
+//   A operand, M block mb: row i = 4 q' + r holds output o = 32 q' + 4 mb + r
 //   H[o][e] = (-1)^popc(o & e) = (-1)^(popc(r & t) + mb0 t2 + popc((mb >> 1) & s) + popc(q' & q))
-// (EL = d/4; o and e split into bit fields r|mb|q' and t|s|q that line up).
+// (o and e split into bit fields r|mb|q' and t|s|q that line up).
 // So A(mb, s) = (-1)^popc((mb >> 1) & s) * P_{mb & 1}, a compile-time sign
 // times one of two per-lane patterns, and the accumulator of M block mb in
-// lane (q, j) holds outputs EL q + 4 mb + 0..3 of vector j: lane q owns the
-// contiguous elements [EL q, EL q + EL) and stores their codes with one
-// EL*bits/8-byte write.
+// lane (q, j) holds outputs 32 q + 4 mb + 0..3 of vector j: lane q owns the
+// contiguous outputs [32 q, 32 q + 32) of every 128-element block and stores
+// their codes with one 4*bits-byte write per block.
 //
 // Products with +-1 are exact; the fp32 sums follow the matrix core's
 // accumulation order instead of the reference's butterfly order, so t can
@@ -154,8 +161,7 @@ __device__ __forceinline__ void quantize_pack(const float (&x)[E], const float (
 // sqrt rounded to nearest: the hardware estimate r, then r - ulp or r + ulp
 // when the residual a - r' r (one fma, sign exact) shows the true root lies
 // nearer to it.  No rescaling for inputs below 2^-96 (norms that small store
-// as fp16 zero either way); fewer registers than the library sqrt, which
-// keeps the d = 128 encoder at 4 waves per SIMD.
+// as fp16 zero either way); fewer registers than the library sqrt.
 __device__ __forceinline__ float sqrt_rn(float a) {
   float r = __builtin_amdgcn_sqrtf(a);
   const float rd = __int_as_float(__float_as_int(r) - 1);
@@ -226,9 +232,10 @@ __global__ __launch_bounds__(256) void encode_mfma_kernel(EncodeSegs io, int64_t
                                                           float c, double rc) {
   static_assert(D == 128 || D == 256, "MFMA encoder covers d = 128 and 256");
   static_assert(DT == BF16 || DT == F16, "MFMA encoder takes 16-bit inputs");
-  constexpr int EL = D / 4;   // outputs (and inputs) per lane
-  constexpr int KS = D / 32;  // K steps
-  constexpr int MB = D / 16;  // M blocks
+  constexpr int NB = D / 128;  // 128-element transform blocks
+  constexpr int EL = D / 4;    // outputs (and inputs) per lane, 32 per block
+  constexpr int KS = D / 32;   // K steps, 4 per block
+  constexpr int MB = D / 16;   // M blocks, 8 per block
   constexpr int NT = (1 << BITS) - 1;
   constexpr int MID = 1 << (BITS - 1);  // boundaries[MID] is the middle one
   constexpr int NH = MID - 1;
@@ -256,26 +263,41 @@ __global__ __launch_bounds__(256) void encode_mfma_kernel(EncodeSegs io, int64_t
     N0.u[w] = p0 ^ 0x80008000u;
     N1.u[w] = p1 ^ 0x80008000u;
   }
-  // RHT sign flips of this lane's input elements EL q + 8 s + t, as xor masks
-  uint32_t sm[KS][4];
-#pragma unroll
-  for (int s = 0; s < KS; ++s) {
+  // RHT sign flips of input elements 128 b + 32 q + 8 s + t (K step 4 b + s)
+  // as xor masks, smt[q KS + 4 b + s] for the lanes of quarter q.  The table
+  // sits in LDS and is read once per group (16 lanes share each entry): held
+  // in registers it would take KS * 4 VGPRs for the kernel's lifetime, which
+  // at d = 256 is the difference between 2 and 3 waves per SIMD.
+  __shared__ uint4 smt[4 * KS];
+  if (threadIdx.x < 4 * KS) {
+    const int qq = threadIdx.x / KS, s = threadIdx.x % KS;
+    uint32_t m[4];
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
-      const int e = EL * q + 8 * s + 2 * w;
-      sm[s][w] = (signs[e] < 0.f ? 0x8000u : 0u) | (signs[e + 1] < 0.f ? 0x80000000u : 0u);
+      const int e = 128 * (s >> 2) + 32 * qq + 8 * (s & 3) + 2 * w;
+      m[w] = (signs[e] < 0.f ? 0x8000u : 0u) | (signs[e + 1] < 0.f ? 0x80000000u : 0u);
     }
+    smt[threadIdx.x] = make_uint4(m[0], m[1], m[2], m[3]);
   }
+  __syncthreads();
   // G[j][j] of the Gram MFMA sits in lane (j / 4, j), accumulator j % 4:
   // every lane picks accumulator j % 4 and reads lane (j / 4, j)'s pick
-  const bool jr_hi = (j & 2) != 0, jr_lo = (j & 1) != 0;
+  // as all-ones / all-zero lane masks for bit selects (the empty asm keeps
+  // the compiler from turning them back into compares inside the loop)
+  uint32_t jr_hi = (j & 2) ? ~0u : 0u, jr_lo = (j & 1) ? ~0u : 0u;
+  asm volatile("" : "+v"(jr_hi), "+v"(jr_lo));
+  auto bsel = [](uint32_t m, float a, float b) {
+    return __uint_as_float((__float_as_uint(a) & m) | (__float_as_uint(b) & ~m));
+  };
   const int diag_src = (((j >> 2) << 4) | j) << 2;  // ds_bpermute byte address
 
-  const int64_t wave = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int64_t gstride = (int64_t)gridDim.x * 4;
-  // groups of 16 vectors, numbered over the segments one after the other
-  const int64_t gps = (n + 15) >> 4;
-  const int64_t ngroups = gps * io.nseg;
+  // wave-uniform, so the group bookkeeping below stays on the scalar unit
+  const int wave = (int)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int gstride = (int)gridDim.x * 4;
+  // groups of 16 vectors, numbered over the segments one after the other (the
+  // host keeps their count below 2^31 - 2^20, so g + gstride cannot overflow)
+  const int gps = (int)((n + 15) >> 4);
+  const int ngroups = gps * io.nseg;
 
   // interior boundaries (wave-uniform)
   float Bv[NT];
@@ -288,26 +310,35 @@ __global__ __launch_bounds__(256) void encode_mfma_kernel(EncodeSegs io, int64_t
   // iteration issues the same loads and the wait counts stay static.
   // group g (clamped to the last one, so a prefetch past the end stays in
   // bounds): its segment and the index of its first vector there
-  auto locate = [&](int64_t g, int& seg, int64_t& g0) {
+  auto locate = [&](int g, int& seg, int64_t& g0) {
     g = g < ngroups ? g : ngroups - 1;
     seg = g >= gps ? 1 : 0;
-    g0 = (g - (seg ? gps : 0)) << 4;
+    g0 = (int64_t)(g - (seg ? gps : 0)) << 4;
   };
-  auto load_group = [&](int64_t g, Op16x8 (&dst)[KS]) {
+  auto load_group = [&](int g, Op16x8 (&dst)[KS]) {
     int seg;
     int64_t g0;
     locate(g, seg, g0);
-    const uint16_t* xb = static_cast<const uint16_t*>(seg ? io.x1 : io.x0);
-    const int64_t vv = g0 + j < n ? g0 + j : n - 1;
-    const uint4* src = reinterpret_cast<const uint4*>(xb + vv * D + EL * q);
+    // wave-uniform group base plus a 32-bit lane offset; rows past the end
+    // read the last row (the lane's row within the group, clamped)
+    const uint16_t* xb = static_cast<const uint16_t*>(seg ? io.x1 : io.x0) + g0 * D;
+    const int last = (int)(n - 1 - g0 < 15 ? n - 1 - g0 : 15);
+    const int jj = j < last ? j : last;
+    const uint4* src = reinterpret_cast<const uint4*>(xb + (jj * D + 32 * q));
 #pragma unroll
-    for (int s = 0; s < KS; ++s) dst[s].v = src[s];
+    for (int s = 0; s < KS; ++s) dst[s].v = src[16 * (s >> 2) + (s & 3)];
   };
-  auto flip_signs = [&](Op16x8 (&v)[KS]) {
+  // z is an opaque zero: the table reads stay inside the loop instead of
+  // being hoisted out of it into registers
+  auto flip_signs = [&](Op16x8 (&v)[KS], int z) {
 #pragma unroll
-    for (int s = 0; s < KS; ++s)
-#pragma unroll
-      for (int w = 0; w < 4; ++w) v[s].u[w] ^= sm[s][w];
+    for (int s = 0; s < KS; ++s) {
+      const uint4 m = smt[q * KS + s + z];
+      v[s].u[0] ^= m.x;
+      v[s].u[1] ^= m.y;
+      v[s].u[2] ^= m.z;
+      v[s].u[3] ^= m.w;
+    }
   };
   // t domain scale of the thresholds, RN((norm + 1e-8) / c), of the group held
   // (sign-flipped) in v; the norm itself goes to nrm
@@ -315,35 +346,58 @@ __global__ __launch_bounds__(256) void encode_mfma_kernel(EncodeSegs io, int64_t
     f32x4_t gram = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < KS; ++s) gram = mfma_16x16x32<DT>(v[s], v[s], gram);
-    const float pick = jr_hi ? (jr_lo ? gram[3] : gram[2]) : (jr_lo ? gram[1] : gram[0]);
+    const float pick = bsel(jr_hi, bsel(jr_lo, gram[3], gram[2]), bsel(jr_lo, gram[1], gram[0]));
     const float xx = __int_as_float(__builtin_amdgcn_ds_bpermute(diag_src, __float_as_int(pick)));
     // ||t||^2 = D ||x||^2 (Parseval for the unnormalised transform)
     nrm = sqrt_rn(xx * (float)D) * c;
     return (nrm + 1e-8f) * rcf;
   };
-  auto encode_group = [&](Op16x8 (&cur)[KS], int64_t g) {
-    flip_signs(cur);
+  // encodes group g held in cur, and reloads cur with group gnext once the
+  // transform and the norm no longer need it
+  auto encode_group = [&](Op16x8 (&cur)[KS], int g, int gnext) {
+    int z = 0;
+    asm volatile("" : "+s"(z));
+    flip_signs(cur, z);
     f32x4_t acc[MB];
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    // block b's transform into acc[8 b .. 8 b + 7]
 #pragma unroll
-    for (int s = 0; s < KS; ++s) {
+    for (int s = 0; s < 4; ++s) {
 #pragma unroll
-      for (int mb = 0; mb < MB; ++mb) {
-        const bool neg = (__builtin_popcount((mb >> 1) & s) & 1) != 0;
-        const Op16x8& a = (mb & 1) ? (neg ? N1 : P1) : (neg ? N0 : P0);
-        acc[mb] = mfma_16x16x32<DT>(a, cur[s], acc[mb]);
+      for (int b = 0; b < NB; ++b) {
+#pragma unroll
+        for (int mb = 0; mb < 8; ++mb) {
+          const bool neg = (__builtin_popcount((mb >> 1) & s) & 1) != 0;
+          const Op16x8& a = (mb & 1) ? (neg ? N1 : P1) : (neg ? N0 : P0);
+          acc[8 * b + mb] = mfma_16x16x32<DT>(a, cur[4 * b + s], acc[8 * b + mb]);
+        }
       }
     }
+    // t[32 b + 4 mb + i] = output 128 b + 32 q + 4 mb + i
     float t[EL];
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
+    for (int mb = 0; mb < 8; ++mb)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) t[4 * mb + i] = acc[mb][i];
+      for (int i = 0; i < 4; ++i) {
+        if constexpr (NB == 1) {
+          t[4 * mb + i] = acc[mb][i];
+        } else {
+          const float z0 = acc[mb][i], z1 = acc[8 + mb][i];
+          t[4 * mb + i] = z0 + z1;
+          t[32 + 4 * mb + i] = z0 - z1;
+        }
+      }
     constexpr int NW = EL * BITS / 32;
     uint32_t w[NW];
     float nrm;
     const float sv = norm_scale(cur, nrm);
+    // the next group's loads go out here, ahead of the quantiser (whose VALU
+    // work covers their latency), and no earlier: before this point the
+    // registers hold the current group
+    __builtin_amdgcn_sched_barrier(0);
+    load_group(gnext, cur);
+    __builtin_amdgcn_sched_barrier(0);
     if constexpr (SYM) {
       float P[NH];
 #pragma unroll
@@ -358,35 +412,37 @@ __global__ __launch_bounds__(256) void encode_mfma_kernel(EncodeSegs io, int64_t
     int seg;
     int64_t g0;
     locate(g, seg, g0);
-    uint8_t* packed = seg ? io.packed1 : io.packed0;
-    uint16_t* norms = seg ? io.norms1 : io.norms0;
-    const int64_t v = g0 + j;
-    if (v < n) {
-      uint32_t* dst = reinterpret_cast<uint32_t*>(packed + v * PD) + NW * q;
-      if constexpr (NW == 2) {
-        *reinterpret_cast<uint2*>(dst) = make_uint2(w[0], w[1]);
-      } else if constexpr (NW % 4 == 0) {
+    uint8_t* packed = (seg ? io.packed1 : io.packed0) + g0 * PD;
+    uint16_t* norms = (seg ? io.norms1 : io.norms0) + g0;
+    const int rows = (int)(n - g0 < 16 ? n - g0 : 16);
+    if (j < rows) {
+      // block b's codes: BITS words at word BITS (4 b + q) of the row
 #pragma unroll
-        for (int k = 0; k < NW; k += 4) *reinterpret_cast<uint4*>(dst + k) = make_uint4(w[k], w[k + 1], w[k + 2], w[k + 3]);
-      } else {
+      for (int b = 0; b < NB; ++b) {
+        uint32_t* dst = reinterpret_cast<uint32_t*>(packed + j * PD) + BITS * (4 * b + q);
+        const uint32_t* wb = w + BITS * b;
+        if constexpr (BITS == 2) {
+          *reinterpret_cast<uint2*>(dst) = make_uint2(wb[0], wb[1]);
+        } else if constexpr (BITS == 4) {
+          *reinterpret_cast<uint4*>(dst) = make_uint4(wb[0], wb[1], wb[2], wb[3]);
+        } else {
 #pragma unroll
-        for (int k = 0; k < NW; ++k) dst[k] = w[k];
+          for (int k = 0; k < BITS; ++k) dst[k] = wb[k];
+        }
       }
-      if (q == 0) norms[v] = (uint16_t)f32_to_f16_bits(nrm);
+      if (q == 0) norms[j] = (uint16_t)f32_to_f16_bits(nrm);
     }
   };
   if (wave >= ngroups) return;
-  // two register sets alternate, so no copies between iterations
-  int64_t g = wave;
-  Op16x8 b0[KS], b1[KS];
-  load_group(g, b0);
+  // one register set: group g + gstride is loaded into it while group g is
+  // quantised.  (Two alternating sets, loaded a whole group ahead, cost KS * 4
+  // more VGPRs: 3 waves per SIMD instead of 2 at d = 256, and no faster at
+  // d = 128.)
+  int g = wave;
+  Op16x8 cur[KS];
+  load_group(g, cur);
   for (;;) {
-    load_group(g + gstride, b1);
-    encode_group(b0, g);
-    g += gstride;
-    if (g >= ngroups) break;
-    load_group(g + gstride, b0);
-    encode_group(b1, g);
+    encode_group(cur, g, g + gstride);
     g += gstride;
     if (g >= ngroups) break;
   }
