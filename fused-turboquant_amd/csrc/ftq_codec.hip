@@ -167,18 +167,6 @@ hipError_t codec_any_rht(int d, const void* x, int it, int64_t n, const float* s
 
 float fwht_scale(int d) { return (float)std::pow((double)d, -0.5); }
 
-// Workgroups (256 threads) that fit on the device at once for kernel k.
-template <typename K>
-static int resident_workgroups(K k) {
-  int dev = 0, cus = 0, per_cu = 0;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, 256, 0) != hipSuccess || cus <= 0 ||
-      per_cu <= 0)
-    return 512;
-  return cus * per_cu;
-}
-
 int codec_grid(int64_t n, int gpb) {
   int64_t want = (n + gpb - 1) / gpb;
   const int64_t cap = 256 * 16;  // 16 workgroups per CU on 256 CUs

@@ -20,7 +20,7 @@
 // 3 compares, 1 select and 3 carry-adds per 3-bit element instead of 3, 4, 3.
 // The symmetric form is a separate instantiation (SYM), chosen by the host
 // from its copy of the codebook: one loop per kernel keeps the register count
-// at 100 (5 waves per SIMD) at d = 128 and 149 (3 waves) at d = 256.
+// at 100 (4 waves per SIMD) at d = 128 and 149 (3 waves) at d = 256.
 //
 // Transform.  A wave encodes 16 vectors (a group) at a time.  A launch may
 // cover two tensors of the same shape (K and V of one store): the groups of
@@ -100,19 +100,24 @@ __device__ __forceinline__ uint32_t shift_in(uint32_t w, bool bit) {
 
 // Codes of E elements, code = #{k : a > V_k} over NT = 2^BITS - 1 sorted
 // thresholds by binary search, packed little-endian (element e at bits
-// [BITS e, BITS e + BITS)) into E*BITS/32 words.  Bits are shifted in from
-// the highest position down; four elements per step keep independent
-// compares queued behind each select.  Strict, like the reference's
-// bucketize(right=False): a value on a threshold takes the lower code.
-template <int BITS, int E>
-__device__ __forceinline__ void quantize_pack(const float (&x)[E], const float (&V)[(1 << BITS) - 1],
+// [BITS e, BITS e + BITS)) into E*BITS/32 words.  Element e is compared with
+// threshold set e % NS (NS = 4: four vectors interleaved element by element).
+// Bits are shifted in from the highest position down; four elements per step
+// keep independent compares queued behind each select.  Strict, like the
+// reference's bucketize(right=False): a value on a threshold takes the lower
+// code.
+template <int BITS, int E, int NS = 1>
+__device__ __forceinline__ void quantize_pack(const float (&x)[E], const float (&VS)[NS][(1 << BITS) - 1],
                                               uint32_t (&w)[E * BITS / 32]) {
   static_assert((E * BITS) % 32 == 0, "whole words per lane");
+  static_assert(NS == 1 || NS == 2 || NS == 4, "threshold sets repeat every 4 elements");
 #pragma unroll
   for (int k = 0; k < E * BITS / 32; ++k) w[k] = 0;
 #pragma unroll
   for (int i0 = E - 4; i0 >= 0; i0 -= 4) {
     bool s[4][BITS];
+    // element i0 + u takes threshold set u % NS (i0 is a multiple of 4)
+#define V VS[u % NS]
     if constexpr (BITS == 2) {
 #pragma unroll
       for (int u = 0; u < 4; ++u) s[u][1] = x[i0 + u] > V[1];
@@ -147,6 +152,7 @@ __device__ __forceinline__ void quantize_pack(const float (&x)[E], const float (
         s[u][0] = x[i0 + u] > (s[u][2] ? hi : lo);
       }
     }
+#undef V
 #pragma unroll
     for (int u = 3; u >= 0; --u) {
 #pragma unroll
@@ -225,6 +231,113 @@ __device__ __forceinline__ void quantize_pack_sym(const float (&x)[E], float Tm,
   }
 }
 
+// Per-lane constants of the 128-point Hadamard transform on the matrix cores
+// (layout above) and of the Gram-diagonal norm.
+template <int DT>
+struct Rht128 {
+  Op16x8 P0, P1, N0, N1;  // A operand patterns, +-
+  uint32_t jr_hi, jr_lo;  // bits 1 and 0 of j as all-ones / all-zero masks
+  int diag_src;           // ds_bpermute byte address of lane (j / 4, j)
+
+  __device__ __forceinline__ void init(int lane) {
+    const int q = lane >> 4, j = lane & 15;
+    const int qp = (lane >> 2) & 3, r = lane & 3;
+    // A patterns: P0[t] = (-1)^(popc(r & t) + popc(q' & q)), P1[t] = P0[t] (-1)^(t >> 2)
+    const uint32_t one = (DT == BF16) ? 0x3F80u : 0x3C00u;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      uint32_t p0 = 0, p1 = 0;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int t = 2 * w + h;
+        const uint32_t s0 = (uint32_t)(__popc(r & t) + __popc(qp & q)) & 1u;
+        const uint32_t s1 = s0 ^ (uint32_t)(t >> 2);
+        p0 |= (one | (s0 << 15)) << (16 * h);
+        p1 |= (one | (s1 << 15)) << (16 * h);
+      }
+      P0.u[w] = p0;
+      P1.u[w] = p1;
+      N0.u[w] = p0 ^ 0x80008000u;
+      N1.u[w] = p1 ^ 0x80008000u;
+    }
+    // G[j][j] of the Gram MFMA sits in lane (j / 4, j), accumulator j % 4:
+    // every lane picks accumulator j % 4 and reads lane (j / 4, j)'s pick.
+    // The empty asm keeps the compiler from turning the masks back into
+    // compares inside the caller's loop.
+    jr_hi = (j & 2) ? ~0u : 0u;
+    jr_lo = (j & 1) ? ~0u : 0u;
+    asm volatile("" : "+v"(jr_hi), "+v"(jr_lo));
+    diag_src = (((j >> 2) << 4) | j) << 2;
+  }
+
+  // acc[8 b + mb] = H_128 x (block b of the group in cur, K steps 4 b .. 4 b + 3)
+  template <int NB>
+  __device__ __forceinline__ void transform(const Op16x8 (&cur)[4 * NB], f32x4_t (&acc)[8 * NB]) const {
+#pragma unroll
+    for (int mb = 0; mb < 8 * NB; ++mb) acc[mb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+#pragma unroll
+        for (int mb = 0; mb < 8; ++mb) {
+          const bool neg = (__builtin_popcount((mb >> 1) & s) & 1) != 0;
+          const Op16x8& a = (mb & 1) ? (neg ? N1 : P1) : (neg ? N0 : P0);
+          acc[8 * b + mb] = mfma_16x16x32<DT>(a, cur[4 * b + s], acc[8 * b + mb]);
+        }
+      }
+    }
+  }
+
+  // sum of squares of vector j (the Gram diagonal), in every lane of vector j
+  template <int KS>
+  __device__ __forceinline__ float sumsq(const Op16x8 (&cur)[KS]) const {
+    f32x4_t gram = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < KS; ++s) gram = mfma_16x16x32<DT>(cur[s], cur[s], gram);
+    auto bsel = [](uint32_t m, float a, float b) {
+      return __uint_as_float((__float_as_uint(a) & m) | (__float_as_uint(b) & ~m));
+    };
+    const float pick = bsel(jr_hi, bsel(jr_lo, gram[3], gram[2]), bsel(jr_lo, gram[1], gram[0]));
+    return __int_as_float(__builtin_amdgcn_ds_bpermute(diag_src, __float_as_int(pick)));
+  }
+};
+
+// RHT sign flips of input elements 128 b + 32 q + 8 s + t (K step 4 b + s) as
+// xor masks, table[q KS + 4 b + s] for the lanes of quarter q.  The table sits
+// in LDS and is read once per group (16 lanes share each entry): held in
+// registers it would take KS * 4 VGPRs for the kernel's lifetime, which at
+// d = 256 is the difference between 2 and 3 waves per SIMD.  Filled by the
+// threads with tid in [0, 4 KS); the caller synchronises.
+template <int KS>
+__device__ __forceinline__ void fill_sign_table(uint4* table, const float* __restrict__ signs, int tid) {
+  if (tid >= 0 && tid < 4 * KS) {
+    const int qq = tid / KS, s = tid % KS;
+    uint32_t m[4];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const int e = 128 * (s >> 2) + 32 * qq + 8 * (s & 3) + 2 * w;
+      m[w] = (signs[e] < 0.f ? 0x8000u : 0u) | (signs[e + 1] < 0.f ? 0x80000000u : 0u);
+    }
+    table[tid] = make_uint4(m[0], m[1], m[2], m[3]);
+  }
+}
+
+// z is an opaque zero (an empty asm result inside the caller's loop): the
+// table reads stay inside the loop instead of being hoisted out of it into
+// registers
+template <int KS>
+__device__ __forceinline__ void flip_signs(Op16x8 (&v)[KS], const uint4* table, int q, int z) {
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    const uint4 m = table[q * KS + s + z];
+    v[s].u[0] ^= m.x;
+    v[s].u[1] ^= m.y;
+    v[s].u[2] ^= m.z;
+    v[s].u[3] ^= m.w;
+  }
+}
+
 template <int D, int BITS, int DT, bool SYM>
 __global__ __launch_bounds__(256) void encode_mfma_kernel(EncodeSegs io, int64_t n,
                                                           const float* __restrict__ signs,
@@ -243,53 +356,11 @@ __global__ __launch_bounds__(256) void encode_mfma_kernel(EncodeSegs io, int64_t
 
   const int lane = threadIdx.x & 63;
   const int q = lane >> 4, j = lane & 15;
-  const int qp = (lane >> 2) & 3, r = lane & 3;
-  // A patterns: P0[t] = (-1)^(popc(r & t) + popc(q' & q)), P1[t] = P0[t] (-1)^(t >> 2)
-  const uint32_t one = (DT == BF16) ? 0x3F80u : 0x3C00u;
-  Op16x8 P0, P1, N0, N1;
-#pragma unroll
-  for (int w = 0; w < 4; ++w) {
-    uint32_t p0 = 0, p1 = 0;
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int t = 2 * w + h;
-      const uint32_t s0 = (uint32_t)(__popc(r & t) + __popc(qp & q)) & 1u;
-      const uint32_t s1 = s0 ^ (uint32_t)(t >> 2);
-      p0 |= (one | (s0 << 15)) << (16 * h);
-      p1 |= (one | (s1 << 15)) << (16 * h);
-    }
-    P0.u[w] = p0;
-    P1.u[w] = p1;
-    N0.u[w] = p0 ^ 0x80008000u;
-    N1.u[w] = p1 ^ 0x80008000u;
-  }
-  // RHT sign flips of input elements 128 b + 32 q + 8 s + t (K step 4 b + s)
-  // as xor masks, smt[q KS + 4 b + s] for the lanes of quarter q.  The table
-  // sits in LDS and is read once per group (16 lanes share each entry): held
-  // in registers it would take KS * 4 VGPRs for the kernel's lifetime, which
-  // at d = 256 is the difference between 2 and 3 waves per SIMD.
+  Rht128<DT> H;
+  H.init(lane);
   __shared__ uint4 smt[4 * KS];
-  if (threadIdx.x < 4 * KS) {
-    const int qq = threadIdx.x / KS, s = threadIdx.x % KS;
-    uint32_t m[4];
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const int e = 128 * (s >> 2) + 32 * qq + 8 * (s & 3) + 2 * w;
-      m[w] = (signs[e] < 0.f ? 0x8000u : 0u) | (signs[e + 1] < 0.f ? 0x80000000u : 0u);
-    }
-    smt[threadIdx.x] = make_uint4(m[0], m[1], m[2], m[3]);
-  }
+  fill_sign_table<KS>(smt, signs, (int)threadIdx.x);
   __syncthreads();
-  // G[j][j] of the Gram MFMA sits in lane (j / 4, j), accumulator j % 4:
-  // every lane picks accumulator j % 4 and reads lane (j / 4, j)'s pick
-  // as all-ones / all-zero lane masks for bit selects (the empty asm keeps
-  // the compiler from turning them back into compares inside the loop)
-  uint32_t jr_hi = (j & 2) ? ~0u : 0u, jr_lo = (j & 1) ? ~0u : 0u;
-  asm volatile("" : "+v"(jr_hi), "+v"(jr_lo));
-  auto bsel = [](uint32_t m, float a, float b) {
-    return __uint_as_float((__float_as_uint(a) & m) | (__float_as_uint(b) & ~m));
-  };
-  const int diag_src = (((j >> 2) << 4) | j) << 2;  // ds_bpermute byte address
 
   // wave-uniform, so the group bookkeeping below stays on the scalar unit
   const int wave = (int)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -328,26 +399,10 @@ __global__ __launch_bounds__(256) void encode_mfma_kernel(EncodeSegs io, int64_t
 #pragma unroll
     for (int s = 0; s < KS; ++s) dst[s].v = src[16 * (s >> 2) + (s & 3)];
   };
-  // z is an opaque zero: the table reads stay inside the loop instead of
-  // being hoisted out of it into registers
-  auto flip_signs = [&](Op16x8 (&v)[KS], int z) {
-#pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      const uint4 m = smt[q * KS + s + z];
-      v[s].u[0] ^= m.x;
-      v[s].u[1] ^= m.y;
-      v[s].u[2] ^= m.z;
-      v[s].u[3] ^= m.w;
-    }
-  };
   // t domain scale of the thresholds, RN((norm + 1e-8) / c), of the group held
   // (sign-flipped) in v; the norm itself goes to nrm
   auto norm_scale = [&](const Op16x8 (&v)[KS], float& nrm) {
-    f32x4_t gram = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s = 0; s < KS; ++s) gram = mfma_16x16x32<DT>(v[s], v[s], gram);
-    const float pick = bsel(jr_hi, bsel(jr_lo, gram[3], gram[2]), bsel(jr_lo, gram[1], gram[0]));
-    const float xx = __int_as_float(__builtin_amdgcn_ds_bpermute(diag_src, __float_as_int(pick)));
+    const float xx = H.sumsq(v);
     // ||t||^2 = D ||x||^2 (Parseval for the unnormalised transform)
     nrm = sqrt_rn(xx * (float)D) * c;
     return (nrm + 1e-8f) * rcf;
@@ -357,23 +412,9 @@ __global__ __launch_bounds__(256) void encode_mfma_kernel(EncodeSegs io, int64_t
   auto encode_group = [&](Op16x8 (&cur)[KS], int g, int gnext) {
     int z = 0;
     asm volatile("" : "+s"(z));
-    flip_signs(cur, z);
+    flip_signs<KS>(cur, smt, q, z);
     f32x4_t acc[MB];
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    // block b's transform into acc[8 b .. 8 b + 7]
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-#pragma unroll
-      for (int b = 0; b < NB; ++b) {
-#pragma unroll
-        for (int mb = 0; mb < 8; ++mb) {
-          const bool neg = (__builtin_popcount((mb >> 1) & s) & 1) != 0;
-          const Op16x8& a = (mb & 1) ? (neg ? N1 : P1) : (neg ? N0 : P0);
-          acc[8 * b + mb] = mfma_16x16x32<DT>(a, cur[4 * b + s], acc[8 * b + mb]);
-        }
-      }
-    }
+    H.template transform<NB>(cur, acc);
     // t[32 b + 4 mb + i] = output 128 b + 32 q + 4 mb + i
     float t[EL];
 #pragma unroll
@@ -404,9 +445,9 @@ __global__ __launch_bounds__(256) void encode_mfma_kernel(EncodeSegs io, int64_t
       for (int k = 0; k < NH; ++k) P[k] = Bv[MID + k] * sv;
       quantize_pack_sym<BITS, EL>(t, Bv[MID - 1] * sv, P, w);
     } else {
-      float T[NT];
+      float T[1][NT];
 #pragma unroll
-      for (int k = 0; k < NT; ++k) T[k] = Bv[k] * sv;
+      for (int k = 0; k < NT; ++k) T[0][k] = Bv[k] * sv;
       quantize_pack<BITS, EL>(t, T, w);
     }
     int seg;

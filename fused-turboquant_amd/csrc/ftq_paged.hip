@@ -36,6 +36,7 @@
 #include "ftq_attn_dev.h"
 #include "ftq_merge.h"
 #include "ftq_codec_dev.h"
+#include "ftq_encode_mfma.h"
 #include "ftq_internal.h"
 
 #include <cmath>
@@ -73,6 +74,8 @@ int64_t paged_sub_bytes(int d, int bk, int bv) {
 //   * any other group (decode steps, ragged tails, scattered slots) merges
 //     each token's bits into the chunk words with atomic and / or, which is
 //     correct for any slot mapping.
+// With skip_whole set, whole-sub-block groups are left to
+// paged_store_mfma_kernel (below), launched beside this one.
 // ---------------------------------------------------------------------------
 template <int D, int BK, int BV, int DT>
 __global__ __launch_bounds__(256) void paged_store_kernel(
@@ -80,7 +83,7 @@ __global__ __launch_bounds__(256) void paged_store_kernel(
     const float* __restrict__ ksigns, const float* __restrict__ vsigns,
     const float* __restrict__ kbnd_g, const float* __restrict__ vbnd_g,
     const int64_t* __restrict__ slot_mapping, uint8_t* __restrict__ cache, int page_size,
-    int64_t num_blocks, float scale) {
+    int64_t num_blocks, float scale, int skip_whole) {
   using Gm = PagedGeom<D, BK, BV>;
   constexpr int E = D / 16, LPV = 16;
   constexpr int NDW = Gm::VLANE / 4;  // dwords of one lane chunk
@@ -113,6 +116,7 @@ __global__ __launch_bounds__(256) void paged_store_kernel(
                        (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)sl);
     const bool lane_ok = s0 >= 0 && (s0 & 15) == 0 && sl == s0 + l16 && s0 / page_size < num_blocks;
     const bool whole = __builtin_amdgcn_ballot_w64(lane_ok) == ~0ull;
+    if (whole && skip_whole) continue;
 
 #pragma unroll 1
     for (int p = 0; p < 4; ++p) {
@@ -196,6 +200,149 @@ __global__ __launch_bounds__(256) void paged_store_kernel(
       for (int k = 0; k < NDW; ++k) chunk[k] = w[k];
     }
     __asm__ volatile("" ::: "memory");
+  }
+}
+
+// ---------------------------------------------------------------------------
+// store of whole sub-blocks on the matrix cores (d = 128, 16-bit input).
+// A group is 16 consecutive input tokens of one kv head whose slots are one
+// whole 16-token sub-block in order (slot_mapping[16 g + j] = S + j, S a
+// multiple of 16): a prefill chunk.  Every other group is left to
+// paged_store_kernel.  The 16 vectors of K (then V) go through the encoder's
+// 128-point Hadamard transform and norm on the matrix cores (Rht128,
+// ftq_encode_mfma.h), lane (q, j) ending up with outputs 32 q .. 32 q + 31 of
+// token j, so K's codes (per token, reference bit layout) and both norms are
+// written straight from there.  V's codes go to the lane-major chunks: chunk
+// (q', r) holds tokens 4 q' .. 4 q' + 3 at d = 16 b + r, which sit in 16
+// different lanes.  The rotated V values therefore go through LDS (fp32, one
+// 8 KB [dim][token] tile per wave) and each lane quantises its own chunk's 32
+// values, element 4 b + i against token 4 q' + i's thresholds, and writes the
+// chunk whole.  The quantiser is the general one (any codebook), as the
+// encoder's general instantiation.
+// LDS tile, dword address of (dim, token): row dim ^ (dim >> 5 & 1) (the two
+// 32-dim quarters of one write phase land in opposite bank halves), token
+// xor 4 ((row >> 1) & 3) (the 8 rows of one 128-byte read phase land in
+// distinct 4-bank groups): conflict-free for both the per-token writes and
+// the 4-token reads.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int pstore_row(int dim) { return dim ^ ((dim >> 5) & 1); }
+__device__ __forceinline__ int pstore_addr(int dim, int token) {
+  const int row = pstore_row(dim);
+  return row * 16 + (token ^ (((row >> 1) & 3) << 2));
+}
+
+template <int BK, int BV, int DT>
+__global__ __launch_bounds__(256) void paged_store_mfma_kernel(
+    const void* __restrict__ key, const void* __restrict__ value, int64_t n_tokens, int hkv,
+    const float* __restrict__ ksigns, const float* __restrict__ vsigns,
+    const float* __restrict__ kbnd_g, const float* __restrict__ vbnd_g,
+    const int64_t* __restrict__ slot_mapping, uint8_t* __restrict__ cache, int page_size,
+    int64_t num_blocks, float c, double rc) {
+  constexpr int D = 128, KS = 4;
+  using Gm = PagedGeom<D, BK, BV>;
+  constexpr int NTK = (1 << BK) - 1, NTV = (1 << BV) - 1;
+  const int lane = threadIdx.x & 63, q = lane >> 4, j = lane & 15;
+  const int wv = threadIdx.x >> 6;
+  Rht128<DT> H;
+  H.init(lane);
+  __shared__ uint4 ksm[4 * KS], vsm[4 * KS];
+  __shared__ __align__(16) float tile[4][D * 16];  // per wave: V's rotated values
+  __shared__ __align__(16) float vsc[4][16];       // per wave: V's threshold scale per token
+  fill_sign_table<KS>(ksm, ksigns, (int)threadIdx.x);
+  fill_sign_table<KS>(vsm, vsigns, (int)threadIdx.x - 64);  // threads 64 .. 64 + 4 KS - 1
+  __syncthreads();
+  float kb[NTK], vb[NTV];  // interior boundaries (wave-uniform)
+#pragma unroll
+  for (int k = 0; k < NTK; ++k) kb[k] = kbnd_g[1 + k];
+#pragma unroll
+  for (int k = 0; k < NTV; ++k) vb[k] = vbnd_g[1 + k];
+  const float rcf = (float)rc;
+  const int nsub = page_size / 16;
+  const int64_t items = n_tokens / 16 * hkv;  // only whole groups of 16 can fill a sub-block
+  float* tw = tile[wv];
+
+  // 16 vectors of one tensor: lane (q, j) gets outputs 32 q .. 32 q + 31 of
+  // token t0 + j in t and the norm in nrm; returns the threshold scale
+  auto rotate = [&](const void* x, int64_t t0, int head, const uint4* signs, float (&t)[32], float& nrm) {
+    const uint16_t* src = static_cast<const uint16_t*>(x) + ((t0 + j) * hkv + head) * D + 32 * q;
+    Op16x8 cur[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) cur[s].v = reinterpret_cast<const uint4*>(src)[s];
+    int z = 0;
+    asm volatile("" : "+s"(z));
+    flip_signs<KS>(cur, signs, q, z);
+    f32x4_t acc[8];
+    H.template transform<1>(cur, acc);
+#pragma unroll
+    for (int mb = 0; mb < 8; ++mb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) t[4 * mb + i] = acc[mb][i];
+    nrm = sqrt_rn(H.sumsq(cur) * (float)D) * c;
+    return (nrm + 1e-8f) * rcf;
+  };
+
+  for (int64_t item = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(wv); item < items;
+       item += (int64_t)gridDim.x * 4) {
+    const int64_t grp = item / hkv;
+    const int head = (int)(item - grp * hkv);
+    const int64_t t0 = grp * 16;
+    const int64_t sl = slot_mapping[t0 + j];
+    const int64_t s0 = ((int64_t)__builtin_amdgcn_readfirstlane((int)(sl >> 32)) << 32) |
+                       (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)sl);
+    const bool lane_ok = s0 >= 0 && (s0 & 15) == 0 && sl == s0 + j && s0 / page_size < num_blocks;
+    if (__builtin_amdgcn_ballot_w64(lane_ok) != ~0ull) continue;  // paged_store_kernel's
+    const int64_t blk = s0 / page_size;
+    const int off = (int)(s0 - blk * page_size);
+    uint8_t* sbp = cache + (((blk * hkv + head) * nsub) + (off >> 4)) * (int64_t)Gm::SUB;
+
+    float t[32];
+    float nrm;
+    {  // K: codes per token, BK words of token j at word BK q of its row
+      const float sv = rotate(key, t0, head, ksm, t, nrm);
+      float T[1][NTK];
+#pragma unroll
+      for (int k = 0; k < NTK; ++k) T[0][k] = kb[k] * sv;
+      uint32_t w[BK];
+      quantize_pack<BK, 32>(t, T, w);
+      uint32_t* dst = reinterpret_cast<uint32_t*>(sbp + j * Gm::KTOK) + BK * q;
+#pragma unroll
+      for (int k = 0; k < BK; ++k) dst[k] = w[k];
+      if (q == 0) reinterpret_cast<uint16_t*>(sbp + Gm::KNORM)[j] = (uint16_t)f32_to_f16_bits(nrm);
+    }
+    {  // V: through the LDS tile into lane-major chunks
+      const float sv = rotate(value, t0, head, vsm, t, nrm);
+      if (q == 0) {
+        reinterpret_cast<uint16_t*>(sbp + Gm::VNORM)[j] = (uint16_t)f32_to_f16_bits(nrm);
+        vsc[wv][j] = sv;
+      }
+#pragma unroll
+      for (int e = 0; e < 32; ++e) tw[pstore_addr(32 * q + e, j)] = t[e];
+      __asm__ volatile("" ::: "memory");  // a wave's LDS accesses run in order
+      // this lane now owns chunk (q, j): tokens 4 q + i at d = 16 b + j
+      const float4 s4 = *reinterpret_cast<const float4*>(&vsc[wv][4 * q]);
+      float T[4][NTV];
+#pragma unroll
+      for (int k = 0; k < NTV; ++k) {
+        T[0][k] = vb[k] * s4.x;
+        T[1][k] = vb[k] * s4.y;
+        T[2][k] = vb[k] * s4.z;
+        T[3][k] = vb[k] * s4.w;
+      }
+#pragma unroll
+      for (int b = 0; b < 8; ++b) {
+        const float4 x4 = *reinterpret_cast<const float4*>(&tw[pstore_addr(16 * b + j, 4 * q)]);
+        t[4 * b] = x4.x;
+        t[4 * b + 1] = x4.y;
+        t[4 * b + 2] = x4.z;
+        t[4 * b + 3] = x4.w;
+      }
+      uint32_t w[BV];
+      quantize_pack<BV, 32, 4>(t, T, w);
+      uint32_t* chunk = reinterpret_cast<uint32_t*>(sbp + Gm::KSEC + lane * Gm::VLANE);
+#pragma unroll
+      for (int k = 0; k < BV; ++k) chunk[k] = w[k];
+      __asm__ volatile("" ::: "memory");  // the tile is rewritten by the next group
+    }
   }
 }
 
@@ -1117,12 +1264,29 @@ static hipError_t launch_store3(const void* k, const void* v, int dt, int64_t n,
   if (g > 256 * 8) g = 256 * 8;
   const float sc = fwht_scale(D);
   dim3 grid((unsigned)g), block(256);
+  // whole sub-blocks (only possible with 16 or more tokens) go to the matrix-core
+  // kernel when it takes the input, the rest to paged_store_kernel
+  const int mfma = D == 128 && dt != F32 && n >= 16;
+  if (mfma) {
+    const int64_t witems = n / 16 * hkv;
+    int64_t wg = (witems + 3) / 4;
+    const double rsc = 1.0 / (double)sc;
+    if (dt == F16) {
+      static const int cap = resident_workgroups(paged_store_mfma_kernel<BK, BV, F16>);
+      paged_store_mfma_kernel<BK, BV, F16><<<dim3((unsigned)(wg < cap ? wg : cap)), block, 0, st>>>(
+          k, v, n, hkv, ks, vs, kb, vb, slots, cache, page_size, num_blocks, sc, rsc);
+    } else {
+      static const int cap = resident_workgroups(paged_store_mfma_kernel<BK, BV, BF16>);
+      paged_store_mfma_kernel<BK, BV, BF16><<<dim3((unsigned)(wg < cap ? wg : cap)), block, 0, st>>>(
+          k, v, n, hkv, ks, vs, kb, vb, slots, cache, page_size, num_blocks, sc, rsc);
+    }
+  }
   if (dt == F32)
-    paged_store_kernel<D, BK, BV, F32><<<grid, block, 0, st>>>(k, v, n, hkv, ks, vs, kb, vb, slots, cache, page_size, num_blocks, sc);
+    paged_store_kernel<D, BK, BV, F32><<<grid, block, 0, st>>>(k, v, n, hkv, ks, vs, kb, vb, slots, cache, page_size, num_blocks, sc, 0);
   else if (dt == F16)
-    paged_store_kernel<D, BK, BV, F16><<<grid, block, 0, st>>>(k, v, n, hkv, ks, vs, kb, vb, slots, cache, page_size, num_blocks, sc);
+    paged_store_kernel<D, BK, BV, F16><<<grid, block, 0, st>>>(k, v, n, hkv, ks, vs, kb, vb, slots, cache, page_size, num_blocks, sc, mfma);
   else
-    paged_store_kernel<D, BK, BV, BF16><<<grid, block, 0, st>>>(k, v, n, hkv, ks, vs, kb, vb, slots, cache, page_size, num_blocks, sc);
+    paged_store_kernel<D, BK, BV, BF16><<<grid, block, 0, st>>>(k, v, n, hkv, ks, vs, kb, vb, slots, cache, page_size, num_blocks, sc, mfma);
   return hipGetLastError();
 }
 

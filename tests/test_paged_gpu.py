@@ -49,19 +49,10 @@ def _decoded(tq, x, bits, d):
     return O.decode(p, n16, tq.quantizer.levels.cpu().numpy(), s, bits, d), p, n16, u
 
 
-@pytest.mark.parametrize("bk,bv", [(3, 3), (4, 2), (2, 4), (4, 4), (2, 2)])
-@pytest.mark.parametrize("page", [16, 32])
-def test_store_layout_parity(cuda, bk, bv, page):
-    from fused_turboquant.paged import PagedTurboQuantCache
-    d, hkv, nblk = 128, 2, 6
-    g = torch.Generator().manual_seed(bk * 10 + bv + page)
-    cache = PagedTurboQuantCache(nblk, page, hkv, d, bk, bv, device=cuda)
-    n = nblk * page - 5  # leave a few slots untouched
-    slots = torch.randperm(nblk * page, generator=g)[:n]
-    slots[3] = -1  # skipped slot
-    k = torch.randn(n, hkv, d, generator=g).to(torch.bfloat16)
-    v = torch.randn(n, hkv, d, generator=g).to(torch.bfloat16)
-    cache.store(k.to(cuda), v.to(cuda), slots.to(cuda))
+def _check_store(cache, k, v, slots, d, bk, bv, page, tag):
+    """Codes and norms read back from the pages against the oracle's encode of
+    the same K / V (ties within TIE_ULPS of a boundary allowed)."""
+    n, hkv = k.shape[0], k.shape[1]
     kc, vc, kn, vn = O.paged_unpack(cache.kv_cache.cpu().numpy(), d, bk, bv)
     ties = 0
     for src, codes, norms, tq, bits in ((k, kc, kn, cache.k_quant, bk), (v, vc, vn, cache.v_quant, bv)):
@@ -81,7 +72,51 @@ def test_store_layout_parity(cuda, bk, bv, page):
         gn = norms[blk, :, off].astype(np.float32)
         wn = n16[ok].astype(np.float32)
         assert np.all(np.abs(gn - wn) <= 1e-3 * np.abs(wn) + 1e-7)
-    print(f"[store bk={bk} bv={bv} page={page}] ties={ties}")
+    print(f"[store {tag} bk={bk} bv={bv} page={page}] ties={ties}")
+
+
+@pytest.mark.parametrize("bk,bv", [(3, 3), (4, 2), (2, 4), (4, 4), (2, 2)])
+@pytest.mark.parametrize("page", [16, 32])
+def test_store_layout_parity(cuda, bk, bv, page):
+    """Scattered slots: every group takes the per-token store."""
+    from fused_turboquant.paged import PagedTurboQuantCache
+    d, hkv, nblk = 128, 2, 6
+    g = torch.Generator().manual_seed(bk * 10 + bv + page)
+    cache = PagedTurboQuantCache(nblk, page, hkv, d, bk, bv, device=cuda)
+    n = nblk * page - 5  # leave a few slots untouched
+    slots = torch.randperm(nblk * page, generator=g)[:n]
+    slots[3] = -1  # skipped slot
+    k = torch.randn(n, hkv, d, generator=g).to(torch.bfloat16)
+    v = torch.randn(n, hkv, d, generator=g).to(torch.bfloat16)
+    cache.store(k.to(cuda), v.to(cuda), slots.to(cuda))
+    _check_store(cache, k, v, slots, d, bk, bv, page, "scattered")
+
+
+@pytest.mark.parametrize("bk,bv", [(3, 3), (4, 2), (2, 4), (4, 4), (2, 2), (3, 4), (4, 3), (2, 3)])
+@pytest.mark.parametrize("page", [16, 48])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_store_prefill_parity(cuda, bk, bv, page, dtype):
+    """A prefill: tokens in slot order over pages taken in a seeded order, so
+    every full group of 16 fills one sub-block whole (the matrix-core store).
+    Mixed in, in the same call: a group with a skipped slot, a group shifted
+    off the sub-block boundary, and a ragged tail (the per-token store)."""
+    from fused_turboquant.paged import PagedTurboQuantCache
+    d, hkv, nblk = 128, 3, 7
+    g = torch.Generator().manual_seed(100 + bk * 10 + bv + page)
+    cache = PagedTurboQuantCache(nblk, page, hkv, d, bk, bv, device=cuda)
+    pages = torch.randperm(nblk, generator=g)
+    slots = (pages[:, None] * page + torch.arange(page)[None, :]).reshape(-1)
+    slots[16 * 2 + 5] = -1  # group 2: one skipped slot
+    grp = slots[16 * 4:16 * 5].clone()  # group 4: one slot past the sub-block's start
+    slots[16 * 4:16 * 5] = torch.cat([grp[1:], grp[:1]])
+    n = slots.numel() - 7  # ragged tail
+    slots = slots[:n]
+    k = torch.randn(n, hkv, d, generator=g)
+    v = torch.randn(n, hkv, d, generator=g)
+    k[::37] *= 8  # a few outlier tokens
+    k, v = k.to(dtype), v.to(dtype)
+    cache.store(k.to(cuda), v.to(cuda), slots.to(cuda))
+    _check_store(cache, k, v, slots, d, bk, bv, page, "prefill")
 
 
 @pytest.mark.parametrize("bk,bv", [(3, 3), (4, 2), (2, 4), (4, 4)])
