@@ -36,12 +36,24 @@ def _kv(g, n, h, d, dtype, outliers=False):
 @pytest.mark.parametrize("kb,vb", [(4, 2), (3, 3), (2, 4), (4, 4), (2, 2)])
 @pytest.mark.parametrize("vrot", [False, True])
 def test_store_parity(cuda, d, kb, vb, vrot):
-    from fused_turboquant import v1
     dtn = "bf16" if (d + kb) % 2 == 0 else "f16"
     if d == 128 and kb == 3:
         dtn = "f32"
-    nb, bs, h = 5, 16, 3
-    g = torch.Generator().manual_seed(d * 100 + kb * 10 + vb + vrot)
+    _check_v1_store(cuda, d, kb, vb, vrot, dtn, 5, 16, 3, d * 100 + kb * 10 + vb + vrot)
+
+
+@pytest.mark.parametrize("kb,vb", [(a, b) for a in (2, 3, 4) for b in (2, 3, 4)])
+@pytest.mark.parametrize("dtn", ["bf16", "f16"])
+@pytest.mark.parametrize("vrot", [False, True])
+def test_store_parity_16bit_d128(cuda, kb, vb, dtn, vrot):
+    """Every K, V width pair at d = 128 with bf16 and fp16 input, V rotated or
+    not: 5 heads over 7 blocks of 16, skipped slots and outlier keys mixed in."""
+    _check_v1_store(cuda, 128, kb, vb, vrot, dtn, 7, 16, 5, 900 + kb * 10 + vb + 2 * vrot, outliers=True)
+
+
+def _check_v1_store(cuda, d, kb, vb, vrot, dtn, nb, bs, h, seed, outliers=False):
+    from fused_turboquant import v1
+    g = torch.Generator().manual_seed(seed)
     layer = v1.TurboQuantV1Layer(d, kb, vb, v_rotate=vrot, device=cuda)
     slot = max(v1.slot_size(d, kb, vb), 128)
     cache = torch.full((nb, bs, h, slot), 0xAB, dtype=torch.uint8, device=cuda)
@@ -49,7 +61,7 @@ def test_store_parity(cuda, d, kb, vb, vrot):
     slots = torch.randperm(nb * bs, generator=g)[:n]
     slots[4] = -1
     slots[9] = -5
-    k, v = _kv(g, n, h, d, DT[dtn])
+    k, v = _kv(g, n, h, d, DT[dtn], outliers=outliers)
     layer.store(k.to(cuda), v.to(cuda), cache, slots.to(cuda))
     got = cache.cpu().numpy()
 
