@@ -63,34 +63,38 @@ int64_t paged_sub_bytes(int d, int bk, int bv) {
 
 // ---------------------------------------------------------------------------
 // store: encode K and V of n tokens x Hkv heads and scatter into the pages.
-// One wave per (group of 16 consecutive input tokens, kv head); a vector is
-// encoded by 16 lanes, 4 at a time.  K codes, K and V norms are per token and
-// written directly.  V codes go to the lane-major chunks, where 4 tokens share
-// each chunk's words:
+// One wave per (group of 16 consecutive input tokens, kv head).  K codes, K
+// and V norms are per token and written directly.  V codes go to the
+// lane-major chunks, where 4 tokens share each chunk's words:
 //   * a group whose 16 tokens fill one whole 16-token sub-block in order (a
-//     prefill: slot_mapping[16 g + j] = S + j, S a multiple of 16) stages the
-//     16 tokens' V codes in LDS and writes every chunk whole, with plain
-//     stores;
+//     prefill: slot_mapping[16 g + j] = S + j, S a multiple of 16) writes
+//     every chunk whole, with plain stores;
 //   * any other group (decode steps, ragged tails, scattered slots) merges
 //     each token's bits into the chunk words with atomic and / or, which is
 //     correct for any slot mapping.
-// With skip_whole set, whole-sub-block groups are left to
-// paged_store_mfma_kernel (below), launched beside this one.
+// paged_store_mfma_kernel (d = 128, 16-bit input) encodes whole groups on the
+// matrix cores and the others token by token (paged_store_tokens);
+// paged_store_kernel (fp32 input, d = 256) does every group token by token.
 // ---------------------------------------------------------------------------
+
+// The tokens of group t0 .. t0 + 15 (one kv head), 4 at a time, 16 lanes each
+// (row `sub` of the wave takes token t0 + 4 p + sub): K codes, both norms and,
+// for a group that is not a whole sub-block, V's bits merged into the shared
+// chunk words with atomic and / or.  Each token's V codes are also staged in
+// vcode[token][d] (this wave's LDS), from which a whole group's chunks are
+// written by the caller.
 template <int D, int BK, int BV, int DT>
-__global__ __launch_bounds__(256) void paged_store_kernel(
+__device__ __forceinline__ void paged_store_tokens(
     const void* __restrict__ key, const void* __restrict__ value, int64_t n_tokens, int hkv,
-    const float* __restrict__ ksigns, const float* __restrict__ vsigns,
-    const float* __restrict__ kbnd_g, const float* __restrict__ vbnd_g,
-    const int64_t* __restrict__ slot_mapping, uint8_t* __restrict__ cache, int page_size,
-    int64_t num_blocks, float scale, int skip_whole) {
+    const float* __restrict__ ksigns, const float* __restrict__ vsigns, const float* __restrict__ kbnd_g,
+    const float* __restrict__ vbnd_g, const int64_t* __restrict__ slot_mapping, uint8_t* __restrict__ cache,
+    int page_size, int64_t num_blocks, float scale, int64_t t0, int head, bool whole, uint8_t (*vcode)[D]) {
   using Gm = PagedGeom<D, BK, BV>;
   constexpr int E = D / 16, LPV = 16;
   constexpr int NDW = Gm::VLANE / 4;  // dwords of one lane chunk
-  __shared__ uint8_t vcode[4][16][D];  // per wave: the V codes of its group's 16 tokens
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int lane = threadIdx.x & 63;
   const int l16 = lane & 15, sub = lane >> 4;
-
+  const int nsub = page_size / 16;
   float kb[(1 << BK) - 1], vb[(1 << BV) - 1];
 #pragma unroll
   for (int j = 0; j < (1 << BK) - 1; ++j) kb[j] = kbnd_g[j + 1];
@@ -102,6 +106,77 @@ __global__ __launch_bounds__(256) void paged_store_kernel(
     ks[i] = ksigns[l16 * E + i];
     vs[i] = vsigns[l16 * E + i];
   }
+#pragma unroll 1
+  for (int p = 0; p < 4; ++p) {
+    const int tt = 4 * p + sub;  // token of the group this 16-lane vector encodes
+    const int64_t tok = t0 + tt;
+    const int64_t slot = tok < n_tokens ? slot_mapping[tok] : -1;
+    const bool active = slot >= 0 && slot / page_size < num_blocks;
+    if (active) {  // uniform over the vector's 16 lanes
+      const int64_t blk = slot / page_size;
+      const int off = (int)(slot - blk * page_size);
+      const int ts = off & 15;
+      uint8_t* sbp = cache + (((blk * hkv + head) * nsub) + (off >> 4)) * (int64_t)Gm::SUB;
+      const int64_t eoff = (tok * hkv + head) * D + l16 * E;
+      float y[E];
+      uint32_t c[E];
+      load_elems<DT, E>(key, eoff, y);
+      const float kn = encode_core<E, LPV, BK>(y, ks, kb, scale, l16, c);
+      pack_store<E, BK>(c, sbp + ts * Gm::KTOK, l16);
+      load_elems<DT, E>(value, eoff, y);
+      const float vn = encode_core<E, LPV, BV>(y, vs, vb, scale, l16, c);
+      if (l16 == 0) {
+        reinterpret_cast<uint16_t*>(sbp + Gm::KNORM)[ts] = (uint16_t)f32_to_f16_bits(kn);
+        reinterpret_cast<uint16_t*>(sbp + Gm::VNORM)[ts] = (uint16_t)f32_to_f16_bits(vn);
+      }
+#pragma unroll
+      for (int i = 0; i < E; ++i) vcode[tt][l16 * E + i] = (uint8_t)c[i];
+      __asm__ volatile("" ::: "memory");  // a wave's LDS accesses run in order
+      if (!whole) {
+        // lane r owns chunk (ts / 4, r): this token's code for d = 16 b + r sits
+        // at bit (4 b + ts % 4) BV; other tokens share the chunk's words, so
+        // clear and set only this token's bits
+        uint32_t v0[NDW], m0[NDW];  // this token's bits as if it were token 0 of its quad
+#pragma unroll
+        for (int w = 0; w < NDW; ++w) { v0[w] = 0; m0[w] = 0; }
+#pragma unroll
+        for (int b = 0; b < D / 16; ++b) {
+          const uint32_t code = vcode[tt][16 * b + l16];
+          const int P = 4 * b * BV;  // compile-time after unrolling; fields never straddle here
+          v0[P >> 5] |= code << (P & 31);
+          m0[P >> 5] |= ((1u << BV) - 1u) << (P & 31);
+        }
+        const int sh = (ts & 3) * BV;
+        uint32_t* chunk = reinterpret_cast<uint32_t*>(sbp + Gm::KSEC + ((ts >> 2) * 16 + l16) * Gm::VLANE);
+#pragma unroll
+        for (int w = 0; w < NDW; ++w) {
+          const uint64_t vv = ((uint64_t)v0[w] << 32) | (w ? v0[w - 1] : 0u);
+          const uint64_t mm = ((uint64_t)m0[w] << 32) | (w ? m0[w - 1] : 0u);
+          const uint32_t val = (uint32_t)((vv << sh) >> 32), msk = (uint32_t)((mm << sh) >> 32);
+          if (msk) {
+            atomicAnd(chunk + w, ~msk);
+            atomicOr(chunk + w, val);
+          }
+        }
+      }
+    }
+  }
+}
+
+// The VALU store: every group, for the inputs the matrix-core kernel below
+// does not take (fp32, d = 256).
+template <int D, int BK, int BV, int DT>
+__global__ __launch_bounds__(256) void paged_store_kernel(
+    const void* __restrict__ key, const void* __restrict__ value, int64_t n_tokens, int hkv,
+    const float* __restrict__ ksigns, const float* __restrict__ vsigns,
+    const float* __restrict__ kbnd_g, const float* __restrict__ vbnd_g,
+    const int64_t* __restrict__ slot_mapping, uint8_t* __restrict__ cache, int page_size,
+    int64_t num_blocks, float scale) {
+  using Gm = PagedGeom<D, BK, BV>;
+  constexpr int NDW = Gm::VLANE / 4;  // dwords of one lane chunk
+  __shared__ uint8_t vcode[4][16][D];  // per wave: the V codes of its group's 16 tokens
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int l16 = lane & 15, sub = lane >> 4;
   const int nsub = page_size / 16;
   const int64_t n_groups = (n_tokens + 15) / 16;
   const int64_t items = n_groups * hkv;
@@ -116,63 +191,8 @@ __global__ __launch_bounds__(256) void paged_store_kernel(
                        (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)sl);
     const bool lane_ok = s0 >= 0 && (s0 & 15) == 0 && sl == s0 + l16 && s0 / page_size < num_blocks;
     const bool whole = __builtin_amdgcn_ballot_w64(lane_ok) == ~0ull;
-    if (whole && skip_whole) continue;
-
-#pragma unroll 1
-    for (int p = 0; p < 4; ++p) {
-      const int tt = 4 * p + sub;  // token of the group this 16-lane vector encodes
-      const int64_t tok = t0 + tt;
-      const int64_t slot = tok < n_tokens ? slot_mapping[tok] : -1;
-      const bool active = slot >= 0 && slot / page_size < num_blocks;
-      if (active) {  // uniform over the vector's 16 lanes
-        const int64_t blk = slot / page_size;
-        const int off = (int)(slot - blk * page_size);
-        const int ts = off & 15;
-        uint8_t* sbp = cache + (((blk * hkv + head) * nsub) + (off >> 4)) * (int64_t)Gm::SUB;
-        const int64_t eoff = (tok * hkv + head) * D + l16 * E;
-        float y[E];
-        uint32_t c[E];
-        load_elems<DT, E>(key, eoff, y);
-        const float kn = encode_core<E, LPV, BK>(y, ks, kb, scale, l16, c);
-        pack_store<E, BK>(c, sbp + ts * Gm::KTOK, l16);
-        load_elems<DT, E>(value, eoff, y);
-        const float vn = encode_core<E, LPV, BV>(y, vs, vb, scale, l16, c);
-        if (l16 == 0) {
-          reinterpret_cast<uint16_t*>(sbp + Gm::KNORM)[ts] = (uint16_t)f32_to_f16_bits(kn);
-          reinterpret_cast<uint16_t*>(sbp + Gm::VNORM)[ts] = (uint16_t)f32_to_f16_bits(vn);
-        }
-#pragma unroll
-        for (int i = 0; i < E; ++i) vcode[wave][tt][l16 * E + i] = (uint8_t)c[i];
-        __asm__ volatile("" ::: "memory");  // a wave's LDS accesses run in order
-        if (!whole) {
-          // lane r owns chunk (ts / 4, r): this token's code for d = 16 b + r sits
-          // at bit (4 b + ts % 4) BV; other tokens share the chunk's words, so
-          // clear and set only this token's bits
-          uint32_t v0[NDW], m0[NDW];  // this token's bits as if it were token 0 of its quad
-#pragma unroll
-          for (int w = 0; w < NDW; ++w) { v0[w] = 0; m0[w] = 0; }
-#pragma unroll
-          for (int b = 0; b < D / 16; ++b) {
-            const uint32_t code = vcode[wave][tt][16 * b + l16];
-            const int P = 4 * b * BV;  // compile-time after unrolling; fields never straddle here
-            v0[P >> 5] |= code << (P & 31);
-            m0[P >> 5] |= ((1u << BV) - 1u) << (P & 31);
-          }
-          const int sh = (ts & 3) * BV;
-          uint32_t* chunk = reinterpret_cast<uint32_t*>(sbp + Gm::KSEC + ((ts >> 2) * 16 + l16) * Gm::VLANE);
-#pragma unroll
-          for (int w = 0; w < NDW; ++w) {
-            const uint64_t vv = ((uint64_t)v0[w] << 32) | (w ? v0[w - 1] : 0u);
-            const uint64_t mm = ((uint64_t)m0[w] << 32) | (w ? m0[w - 1] : 0u);
-            const uint32_t val = (uint32_t)((vv << sh) >> 32), msk = (uint32_t)((mm << sh) >> 32);
-            if (msk) {
-              atomicAnd(chunk + w, ~msk);
-              atomicOr(chunk + w, val);
-            }
-          }
-        }
-      }
-    }
+    paged_store_tokens<D, BK, BV, DT>(key, value, n_tokens, hkv, ksigns, vsigns, kbnd_g, vbnd_g, slot_mapping,
+                                      cache, page_size, num_blocks, scale, t0, head, whole, vcode[wave]);
     if (whole) {  // wave-uniform: every chunk of the sub-block, written whole
       __asm__ volatile("" ::: "memory");
       const int64_t blk = s0 / page_size;
@@ -204,11 +224,10 @@ __global__ __launch_bounds__(256) void paged_store_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// store of whole sub-blocks on the matrix cores (d = 128, 16-bit input).
-// A group is 16 consecutive input tokens of one kv head whose slots are one
-// whole 16-token sub-block in order (slot_mapping[16 g + j] = S + j, S a
-// multiple of 16): a prefill chunk.  Every other group is left to
-// paged_store_kernel.  The 16 vectors of K (then V) go through the encoder's
+// store on the matrix cores (d = 128, 16-bit input).  A group whose slots are
+// one whole 16-token sub-block in order (a prefill chunk) is encoded here;
+// every other group goes token by token through paged_store_tokens, with this
+// wave's LDS tile as its staging area.  The 16 vectors of K (then V) go through the encoder's
 // 128-point Hadamard transform and norm on the matrix cores (Rht128,
 // ftq_encode_mfma.h), lane (q, j) ending up with outputs 32 q .. 32 q + 31 of
 // token j, so K's codes (per token, reference bit layout) and both norms are
@@ -258,7 +277,7 @@ __global__ __launch_bounds__(256) void paged_store_mfma_kernel(
   for (int k = 0; k < NTV; ++k) vb[k] = vbnd_g[1 + k];
   const float rcf = (float)rc;
   const int nsub = page_size / 16;
-  const int64_t items = n_tokens / 16 * hkv;  // only whole groups of 16 can fill a sub-block
+  const int64_t items = (n_tokens + 15) / 16 * hkv;
   float* tw = tile[wv];
 
   // 16 vectors of one tensor: lane (q, j) gets outputs 32 q .. 32 q + 31 of
@@ -286,11 +305,17 @@ __global__ __launch_bounds__(256) void paged_store_mfma_kernel(
     const int64_t grp = item / hkv;
     const int head = (int)(item - grp * hkv);
     const int64_t t0 = grp * 16;
-    const int64_t sl = slot_mapping[t0 + j];
+    const int64_t sl = t0 + j < n_tokens ? slot_mapping[t0 + j] : -1;
     const int64_t s0 = ((int64_t)__builtin_amdgcn_readfirstlane((int)(sl >> 32)) << 32) |
                        (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)sl);
     const bool lane_ok = s0 >= 0 && (s0 & 15) == 0 && sl == s0 + j && s0 / page_size < num_blocks;
-    if (__builtin_amdgcn_ballot_w64(lane_ok) != ~0ull) continue;  // paged_store_kernel's
+    if (__builtin_amdgcn_ballot_w64(lane_ok) != ~0ull) {  // wave-uniform
+      paged_store_tokens<D, BK, BV, DT>(key, value, n_tokens, hkv, ksigns, vsigns, kbnd_g, vbnd_g, slot_mapping,
+                                        cache, page_size, num_blocks, c, t0, head, false,
+                                        reinterpret_cast<uint8_t(*)[D]>(tw));
+      __asm__ volatile("" ::: "memory");  // the tile is rewritten by the next group
+      continue;
+    }
     const int64_t blk = s0 / page_size;
     const int off = (int)(s0 - blk * page_size);
     uint8_t* sbp = cache + (((blk * hkv + head) * nsub) + (off >> 4)) * (int64_t)Gm::SUB;
@@ -1264,29 +1289,24 @@ static hipError_t launch_store3(const void* k, const void* v, int dt, int64_t n,
   if (g > 256 * 8) g = 256 * 8;
   const float sc = fwht_scale(D);
   dim3 grid((unsigned)g), block(256);
-  // whole sub-blocks (only possible with 16 or more tokens) go to the matrix-core
-  // kernel when it takes the input, the rest to paged_store_kernel
-  const int mfma = D == 128 && dt != F32 && n >= 16;
-  if (mfma) {
-    const int64_t witems = n / 16 * hkv;
-    int64_t wg = (witems + 3) / 4;
+  if (dt == F32) {
+    paged_store_kernel<D, BK, BV, F32><<<grid, block, 0, st>>>(k, v, n, hkv, ks, vs, kb, vb, slots, cache, page_size, num_blocks, sc);
+  } else if constexpr (D == 128) {  // one launch: whole sub-blocks on the matrix cores, the rest per token
     const double rsc = 1.0 / (double)sc;
     if (dt == F16) {
       static const int cap = resident_workgroups(paged_store_mfma_kernel<BK, BV, F16>);
-      paged_store_mfma_kernel<BK, BV, F16><<<dim3((unsigned)(wg < cap ? wg : cap)), block, 0, st>>>(
+      paged_store_mfma_kernel<BK, BV, F16><<<dim3((unsigned)(g < cap ? g : cap)), block, 0, st>>>(
           k, v, n, hkv, ks, vs, kb, vb, slots, cache, page_size, num_blocks, sc, rsc);
     } else {
       static const int cap = resident_workgroups(paged_store_mfma_kernel<BK, BV, BF16>);
-      paged_store_mfma_kernel<BK, BV, BF16><<<dim3((unsigned)(wg < cap ? wg : cap)), block, 0, st>>>(
+      paged_store_mfma_kernel<BK, BV, BF16><<<dim3((unsigned)(g < cap ? g : cap)), block, 0, st>>>(
           k, v, n, hkv, ks, vs, kb, vb, slots, cache, page_size, num_blocks, sc, rsc);
     }
+  } else if (dt == F16) {
+    paged_store_kernel<D, BK, BV, F16><<<grid, block, 0, st>>>(k, v, n, hkv, ks, vs, kb, vb, slots, cache, page_size, num_blocks, sc);
+  } else {
+    paged_store_kernel<D, BK, BV, BF16><<<grid, block, 0, st>>>(k, v, n, hkv, ks, vs, kb, vb, slots, cache, page_size, num_blocks, sc);
   }
-  if (dt == F32)
-    paged_store_kernel<D, BK, BV, F32><<<grid, block, 0, st>>>(k, v, n, hkv, ks, vs, kb, vb, slots, cache, page_size, num_blocks, sc, 0);
-  else if (dt == F16)
-    paged_store_kernel<D, BK, BV, F16><<<grid, block, 0, st>>>(k, v, n, hkv, ks, vs, kb, vb, slots, cache, page_size, num_blocks, sc, mfma);
-  else
-    paged_store_kernel<D, BK, BV, BF16><<<grid, block, 0, st>>>(k, v, n, hkv, ks, vs, kb, vb, slots, cache, page_size, num_blocks, sc, mfma);
   return hipGetLastError();
 }
 
