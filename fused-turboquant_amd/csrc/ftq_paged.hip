@@ -72,9 +72,9 @@ int64_t paged_sub_bytes(int d, int bk, int bv) {
 //   * any other group (decode steps, ragged tails, scattered slots) merges
 //     each token's bits into the chunk words with atomic and / or, which is
 //     correct for any slot mapping.
-// paged_store_mfma_kernel (d = 128, 16-bit input) encodes whole groups on the
-// matrix cores and the others token by token (paged_store_tokens);
-// paged_store_kernel (fp32 input, d = 256) does every group token by token.
+// paged_store_mfma_kernel (16-bit input) encodes whole groups on the matrix
+// cores and the others token by token (paged_store_tokens); paged_store_kernel
+// (fp32 input) does every group token by token.
 // ---------------------------------------------------------------------------
 
 // The tokens of group t0 .. t0 + 15 (one kv head), 4 at a time, 16 lanes each
@@ -163,8 +163,8 @@ __device__ __forceinline__ void paged_store_tokens(
   }
 }
 
-// The VALU store: every group, for the inputs the matrix-core kernel below
-// does not take (fp32, d = 256).
+// The VALU store: every group, for the input the matrix-core kernel below
+// does not take (fp32).
 template <int D, int BK, int BV, int DT>
 __global__ __launch_bounds__(256) void paged_store_kernel(
     const void* __restrict__ key, const void* __restrict__ value, int64_t n_tokens, int hkv,
@@ -224,7 +224,7 @@ __global__ __launch_bounds__(256) void paged_store_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// store on the matrix cores (d = 128, 16-bit input).  A group whose slots are
+// store on the matrix cores (d = 128 and 256, 16-bit input).  A group whose slots are
 // one whole 16-token sub-block in order (a prefill chunk) is encoded here;
 // every other group goes token by token through paged_store_tokens, with this
 // wave's LDS tile as its staging area.  The 16 vectors of K (then V) go through the encoder's
@@ -250,14 +250,16 @@ __device__ __forceinline__ int pstore_addr(int dim, int token) {
   return row * 16 + (token ^ (((row >> 1) & 3) << 2));
 }
 
-template <int BK, int BV, int DT>
+template <int D, int BK, int BV, int DT>
 __global__ __launch_bounds__(256) void paged_store_mfma_kernel(
     const void* __restrict__ key, const void* __restrict__ value, int64_t n_tokens, int hkv,
     const float* __restrict__ ksigns, const float* __restrict__ vsigns,
     const float* __restrict__ kbnd_g, const float* __restrict__ vbnd_g,
     const int64_t* __restrict__ slot_mapping, uint8_t* __restrict__ cache, int page_size,
     int64_t num_blocks, float c, double rc) {
-  constexpr int D = 128, KS = 4;
+  static_assert(D == 128 || D == 256, "the matrix-core store covers d = 128 and 256");
+  constexpr int KS = D / 32;   // K steps of the transform, 4 per 128-element block
+  constexpr int NB = D / 128;  // 128-element blocks (the encoder's factored d = 256)
   using Gm = PagedGeom<D, BK, BV>;
   constexpr int NTK = (1 << BK) - 1, NTV = (1 << BV) - 1;
   const int lane = threadIdx.x & 63, q = lane >> 4, j = lane & 15;
@@ -265,7 +267,7 @@ __global__ __launch_bounds__(256) void paged_store_mfma_kernel(
   Rht128<DT> H;
   H.init(lane);
   __shared__ uint4 ksm[4 * KS], vsm[4 * KS];
-  __shared__ __align__(16) float tile[4][D * 16];  // per wave: V's rotated values
+  __shared__ __align__(16) float tile[4][128 * 16];  // per wave: 128 of V's rotated dims
   __shared__ __align__(16) float vsc[4][16];       // per wave: V's threshold scale per token
   fill_sign_table<KS>(ksm, ksigns, (int)threadIdx.x);
   fill_sign_table<KS>(vsm, vsigns, (int)threadIdx.x - 64);  // threads 64 .. 64 + 4 KS - 1
@@ -280,22 +282,33 @@ __global__ __launch_bounds__(256) void paged_store_mfma_kernel(
   const int64_t items = (n_tokens + 15) / 16 * hkv;
   float* tw = tile[wv];
 
-  // 16 vectors of one tensor: lane (q, j) gets outputs 32 q .. 32 q + 31 of
-  // token t0 + j in t and the norm in nrm; returns the threshold scale
-  auto rotate = [&](const void* x, int64_t t0, int head, const uint4* signs, float (&t)[32], float& nrm) {
+  // 16 vectors of one tensor: lane (q, j) gets outputs 128 b + 32 q .. 128 b +
+  // 32 q + 31 of token t0 + j in t[32 b ..] (at d = 256 the two 128-point
+  // transforms and their butterfly, as the encoder) and the norm in nrm;
+  // returns the threshold scale
+  auto rotate = [&](const void* x, int64_t t0, int head, const uint4* signs, float (&t)[32 * NB],
+                    float& nrm) {
     const uint16_t* src = static_cast<const uint16_t*>(x) + ((t0 + j) * hkv + head) * D + 32 * q;
     Op16x8 cur[KS];
 #pragma unroll
-    for (int s = 0; s < KS; ++s) cur[s].v = reinterpret_cast<const uint4*>(src)[s];
+    for (int s = 0; s < KS; ++s) cur[s].v = reinterpret_cast<const uint4*>(src)[16 * (s >> 2) + (s & 3)];
     int z = 0;
     asm volatile("" : "+s"(z));
     flip_signs<KS>(cur, signs, q, z);
-    f32x4_t acc[8];
-    H.template transform<1>(cur, acc);
+    f32x4_t acc[8 * NB];
+    H.template transform<NB>(cur, acc);
 #pragma unroll
     for (int mb = 0; mb < 8; ++mb)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) t[4 * mb + i] = acc[mb][i];
+      for (int i = 0; i < 4; ++i) {
+        if constexpr (NB == 1) {
+          t[4 * mb + i] = acc[mb][i];
+        } else {
+          const float z0 = acc[mb][i], z1 = acc[8 + mb][i];
+          t[4 * mb + i] = z0 + z1;
+          t[32 + 4 * mb + i] = z0 - z1;
+        }
+      }
     nrm = sqrt_rn(H.sumsq(cur) * (float)D) * c;
     return (nrm + 1e-8f) * rcf;
   };
@@ -320,30 +333,31 @@ __global__ __launch_bounds__(256) void paged_store_mfma_kernel(
     const int off = (int)(s0 - blk * page_size);
     uint8_t* sbp = cache + (((blk * hkv + head) * nsub) + (off >> 4)) * (int64_t)Gm::SUB;
 
-    float t[32];
+    float t[32 * NB];
     float nrm;
-    {  // K: codes per token, BK words of token j at word BK q of its row
+    {  // K: codes per token, block b's BK words of token j at word BK (4 b + q) of its row
       const float sv = rotate(key, t0, head, ksm, t, nrm);
       float T[1][NTK];
 #pragma unroll
       for (int k = 0; k < NTK; ++k) T[0][k] = kb[k] * sv;
-      uint32_t w[BK];
-      quantize_pack<BK, 32>(t, T, w);
-      uint32_t* dst = reinterpret_cast<uint32_t*>(sbp + j * Gm::KTOK) + BK * q;
+      uint32_t w[BK * NB];
+      quantize_pack<BK, 32 * NB>(t, T, w);
 #pragma unroll
-      for (int k = 0; k < BK; ++k) dst[k] = w[k];
+      for (int b = 0; b < NB; ++b) {
+        uint32_t* dst = reinterpret_cast<uint32_t*>(sbp + j * Gm::KTOK) + BK * (4 * b + q);
+#pragma unroll
+        for (int k = 0; k < BK; ++k) dst[k] = w[BK * b + k];
+      }
       if (q == 0) reinterpret_cast<uint16_t*>(sbp + Gm::KNORM)[j] = (uint16_t)f32_to_f16_bits(nrm);
     }
-    {  // V: through the LDS tile into lane-major chunks
+    {  // V: through the LDS tile into lane-major chunks, 128 dims at a time
       const float sv = rotate(value, t0, head, vsm, t, nrm);
       if (q == 0) {
         reinterpret_cast<uint16_t*>(sbp + Gm::VNORM)[j] = (uint16_t)f32_to_f16_bits(nrm);
         vsc[wv][j] = sv;
       }
-#pragma unroll
-      for (int e = 0; e < 32; ++e) tw[pstore_addr(32 * q + e, j)] = t[e];
-      __asm__ volatile("" ::: "memory");  // a wave's LDS accesses run in order
-      // this lane now owns chunk (q, j): tokens 4 q + i at d = 16 b + j
+      __asm__ volatile("" ::: "memory");
+      // this lane owns chunk (q, j): tokens 4 q + i at d = 16 b + j
       const float4 s4 = *reinterpret_cast<const float4*>(&vsc[wv][4 * q]);
       float T[4][NTV];
 #pragma unroll
@@ -353,20 +367,27 @@ __global__ __launch_bounds__(256) void paged_store_mfma_kernel(
         T[2][k] = vb[k] * s4.z;
         T[3][k] = vb[k] * s4.w;
       }
-#pragma unroll
-      for (int b = 0; b < 8; ++b) {
-        const float4 x4 = *reinterpret_cast<const float4*>(&tw[pstore_addr(16 * b + j, 4 * q)]);
-        t[4 * b] = x4.x;
-        t[4 * b + 1] = x4.y;
-        t[4 * b + 2] = x4.z;
-        t[4 * b + 3] = x4.w;
-      }
-      uint32_t w[BV];
-      quantize_pack<BV, 32, 4>(t, T, w);
       uint32_t* chunk = reinterpret_cast<uint32_t*>(sbp + Gm::KSEC + lane * Gm::VLANE);
 #pragma unroll
-      for (int k = 0; k < BV; ++k) chunk[k] = w[k];
-      __asm__ volatile("" ::: "memory");  // the tile is rewritten by the next group
+      for (int hb = 0; hb < NB; ++hb) {  // dims 128 hb ..: d-blocks 8 hb .. 8 hb + 7, chunk words BV hb ..
+#pragma unroll
+        for (int e = 0; e < 32; ++e) tw[pstore_addr(32 * q + e, j)] = t[32 * hb + e];
+        __asm__ volatile("" ::: "memory");  // a wave's LDS accesses run in order
+        float x[32];
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+          const float4 x4 = *reinterpret_cast<const float4*>(&tw[pstore_addr(16 * b + j, 4 * q)]);
+          x[4 * b] = x4.x;
+          x[4 * b + 1] = x4.y;
+          x[4 * b + 2] = x4.z;
+          x[4 * b + 3] = x4.w;
+        }
+        uint32_t w[BV];
+        quantize_pack<BV, 32, 4>(x, T, w);
+#pragma unroll
+        for (int k = 0; k < BV; ++k) chunk[BV * hb + k] = w[k];
+        __asm__ volatile("" ::: "memory");  // the tile is rewritten next
+      }
     }
   }
 }
@@ -1291,21 +1312,17 @@ static hipError_t launch_store3(const void* k, const void* v, int dt, int64_t n,
   dim3 grid((unsigned)g), block(256);
   if (dt == F32) {
     paged_store_kernel<D, BK, BV, F32><<<grid, block, 0, st>>>(k, v, n, hkv, ks, vs, kb, vb, slots, cache, page_size, num_blocks, sc);
-  } else if constexpr (D == 128) {  // one launch: whole sub-blocks on the matrix cores, the rest per token
+  } else {  // one launch: whole sub-blocks on the matrix cores, the rest per token
     const double rsc = 1.0 / (double)sc;
     if (dt == F16) {
-      static const int cap = resident_workgroups(paged_store_mfma_kernel<BK, BV, F16>);
-      paged_store_mfma_kernel<BK, BV, F16><<<dim3((unsigned)(g < cap ? g : cap)), block, 0, st>>>(
+      static const int cap = resident_workgroups(paged_store_mfma_kernel<D, BK, BV, F16>);
+      paged_store_mfma_kernel<D, BK, BV, F16><<<dim3((unsigned)(g < cap ? g : cap)), block, 0, st>>>(
           k, v, n, hkv, ks, vs, kb, vb, slots, cache, page_size, num_blocks, sc, rsc);
     } else {
-      static const int cap = resident_workgroups(paged_store_mfma_kernel<BK, BV, BF16>);
-      paged_store_mfma_kernel<BK, BV, BF16><<<dim3((unsigned)(g < cap ? g : cap)), block, 0, st>>>(
+      static const int cap = resident_workgroups(paged_store_mfma_kernel<D, BK, BV, BF16>);
+      paged_store_mfma_kernel<D, BK, BV, BF16><<<dim3((unsigned)(g < cap ? g : cap)), block, 0, st>>>(
           k, v, n, hkv, ks, vs, kb, vb, slots, cache, page_size, num_blocks, sc, rsc);
     }
-  } else if (dt == F16) {
-    paged_store_kernel<D, BK, BV, F16><<<grid, block, 0, st>>>(k, v, n, hkv, ks, vs, kb, vb, slots, cache, page_size, num_blocks, sc);
-  } else {
-    paged_store_kernel<D, BK, BV, BF16><<<grid, block, 0, st>>>(k, v, n, hkv, ks, vs, kb, vb, slots, cache, page_size, num_blocks, sc);
   }
   return hipGetLastError();
 }

@@ -95,14 +95,15 @@ def test_store_layout_parity(cuda, bk, bv, page):
 @pytest.mark.parametrize("bk,bv", [(3, 3), (4, 2), (2, 4), (4, 4), (2, 2), (3, 4), (4, 3), (2, 3)])
 @pytest.mark.parametrize("page", [16, 48])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-def test_store_prefill_parity(cuda, bk, bv, page, dtype):
+@pytest.mark.parametrize("d", [128, 256])
+def test_store_prefill_parity(cuda, bk, bv, page, dtype, d):
     """A prefill: tokens in slot order over pages taken in a seeded order, so
     every full group of 16 fills one sub-block whole (the matrix-core store).
     Mixed in, in the same call: a group with a skipped slot, a group shifted
     off the sub-block boundary, and a ragged tail (the per-token store)."""
     from fused_turboquant.paged import PagedTurboQuantCache
-    d, hkv, nblk = 128, 3, 7
-    g = torch.Generator().manual_seed(100 + bk * 10 + bv + page)
+    hkv, nblk = 3, 7
+    g = torch.Generator().manual_seed(100 + bk * 10 + bv + page + d)
     cache = PagedTurboQuantCache(nblk, page, hkv, d, bk, bv, device=cuda)
     pages = torch.randperm(nblk, generator=g)
     slots = (pages[:, None] * page + torch.arange(page)[None, :]).reshape(-1)
