@@ -77,19 +77,43 @@ def _check_store(cache, k, v, slots, d, bk, bv, page, tag):
 
 @pytest.mark.parametrize("bk,bv", [(3, 3), (4, 2), (2, 4), (4, 4), (2, 2)])
 @pytest.mark.parametrize("page", [16, 32])
-def test_store_layout_parity(cuda, bk, bv, page):
-    """Scattered slots: every group takes the per-token store."""
+@pytest.mark.parametrize("d,dtype", [(128, torch.bfloat16), (128, torch.float16), (256, torch.bfloat16),
+                                     (128, torch.float32)])
+def test_store_layout_parity(cuda, bk, bv, page, d, dtype):
+    """Scattered slots: every group takes the per-token store (inside the
+    matrix-core kernel for 16-bit input, the VALU kernel for fp32)."""
     from fused_turboquant.paged import PagedTurboQuantCache
-    d, hkv, nblk = 128, 2, 6
-    g = torch.Generator().manual_seed(bk * 10 + bv + page)
+    hkv, nblk = 2, 6
+    g = torch.Generator().manual_seed(bk * 10 + bv + page + d)
     cache = PagedTurboQuantCache(nblk, page, hkv, d, bk, bv, device=cuda)
     n = nblk * page - 5  # leave a few slots untouched
     slots = torch.randperm(nblk * page, generator=g)[:n]
     slots[3] = -1  # skipped slot
-    k = torch.randn(n, hkv, d, generator=g).to(torch.bfloat16)
-    v = torch.randn(n, hkv, d, generator=g).to(torch.bfloat16)
+    k = torch.randn(n, hkv, d, generator=g).to(dtype)
+    v = torch.randn(n, hkv, d, generator=g).to(dtype)
     cache.store(k.to(cuda), v.to(cuda), slots.to(cuda))
     _check_store(cache, k, v, slots, d, bk, bv, page, "scattered")
+
+
+@pytest.mark.parametrize("d", [128, 256])
+@pytest.mark.parametrize("n", [1, 5, 16, 17])
+def test_store_decode_steps(cuda, d, n):
+    """Decode-step sized stores (one token per sequence, a few sequences): no
+    group is a whole sub-block, several steps in a row into the same pages."""
+    from fused_turboquant.paged import PagedTurboQuantCache
+    hkv, page, nblk, bk, bv = 4, 16, 24, 3, 3
+    g = torch.Generator().manual_seed(500 + n + d)
+    cache = PagedTurboQuantCache(nblk, page, hkv, d, bk, bv, device=cuda)
+    ks, vs, ss = [], [], []
+    for step in range(3):  # sequence i writes position `step` of page i
+        slots = torch.arange(n) * page + step
+        k = torch.randn(n, hkv, d, generator=g).to(torch.bfloat16)
+        v = torch.randn(n, hkv, d, generator=g).to(torch.bfloat16)
+        cache.store(k.to(cuda), v.to(cuda), slots.to(cuda))
+        ks.append(k)
+        vs.append(v)
+        ss.append(slots)
+    _check_store(cache, torch.cat(ks), torch.cat(vs), torch.cat(ss), d, bk, bv, page, "decode steps")
 
 
 @pytest.mark.parametrize("bk,bv", [(3, 3), (4, 2), (2, 4), (4, 4), (2, 2), (3, 4), (4, 3), (2, 3)])
