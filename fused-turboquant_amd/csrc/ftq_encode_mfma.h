@@ -111,48 +111,47 @@ __device__ __forceinline__ void quantize_pack(const float (&x)[E], const float (
                                               uint32_t (&w)[E * BITS / 32]) {
   static_assert((E * BITS) % 32 == 0, "whole words per lane");
   static_assert(NS == 1 || NS == 2 || NS == 4, "threshold sets repeat every 4 elements");
+  auto V = [&](int u, int k) { return VS[u % NS][k]; };
 #pragma unroll
   for (int k = 0; k < E * BITS / 32; ++k) w[k] = 0;
 #pragma unroll
   for (int i0 = E - 4; i0 >= 0; i0 -= 4) {
     bool s[4][BITS];
-    // element i0 + u takes threshold set u % NS (i0 is a multiple of 4)
-#define V VS[u % NS]
+    // element i0 + u takes threshold set u % NS (i0 is a multiple of 4): V(u, k)
     if constexpr (BITS == 2) {
 #pragma unroll
-      for (int u = 0; u < 4; ++u) s[u][1] = x[i0 + u] > V[1];
+      for (int u = 0; u < 4; ++u) s[u][1] = x[i0 + u] > V(u, 1);
 #pragma unroll
-      for (int u = 0; u < 4; ++u) s[u][0] = x[i0 + u] > (s[u][1] ? V[2] : V[0]);
+      for (int u = 0; u < 4; ++u) s[u][0] = x[i0 + u] > (s[u][1] ? V(u, 2) : V(u, 0));
     } else if constexpr (BITS == 3) {
 #pragma unroll
-      for (int u = 0; u < 4; ++u) s[u][2] = x[i0 + u] > V[3];
+      for (int u = 0; u < 4; ++u) s[u][2] = x[i0 + u] > V(u, 3);
 #pragma unroll
-      for (int u = 0; u < 4; ++u) s[u][1] = x[i0 + u] > (s[u][2] ? V[5] : V[1]);
+      for (int u = 0; u < 4; ++u) s[u][1] = x[i0 + u] > (s[u][2] ? V(u, 5) : V(u, 1));
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const float lo = s[u][2] ? V[4] : V[0];
-        const float hi = s[u][2] ? V[6] : V[2];
+        const float lo = s[u][2] ? V(u, 4) : V(u, 0);
+        const float hi = s[u][2] ? V(u, 6) : V(u, 2);
         s[u][0] = x[i0 + u] > (s[u][1] ? hi : lo);
       }
     } else {
 #pragma unroll
-      for (int u = 0; u < 4; ++u) s[u][3] = x[i0 + u] > V[7];
+      for (int u = 0; u < 4; ++u) s[u][3] = x[i0 + u] > V(u, 7);
 #pragma unroll
-      for (int u = 0; u < 4; ++u) s[u][2] = x[i0 + u] > (s[u][3] ? V[11] : V[3]);
+      for (int u = 0; u < 4; ++u) s[u][2] = x[i0 + u] > (s[u][3] ? V(u, 11) : V(u, 3));
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const float a = s[u][3] ? V[13] : V[5], bq = s[u][3] ? V[9] : V[1];
+        const float a = s[u][3] ? V(u, 13) : V(u, 5), bq = s[u][3] ? V(u, 9) : V(u, 1);
         s[u][1] = x[i0 + u] > (s[u][2] ? a : bq);
       }
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const float t00 = s[u][3] ? V[8] : V[0], t01 = s[u][3] ? V[10] : V[2];
-        const float t10 = s[u][3] ? V[12] : V[4], t11 = s[u][3] ? V[14] : V[6];
+        const float t00 = s[u][3] ? V(u, 8) : V(u, 0), t01 = s[u][3] ? V(u, 10) : V(u, 2);
+        const float t10 = s[u][3] ? V(u, 12) : V(u, 4), t11 = s[u][3] ? V(u, 14) : V(u, 6);
         const float lo = s[u][1] ? t01 : t00, hi = s[u][1] ? t11 : t10;
         s[u][0] = x[i0 + u] > (s[u][2] ? hi : lo);
       }
     }
-#undef V
 #pragma unroll
     for (int u = 3; u >= 0; --u) {
 #pragma unroll
