@@ -97,6 +97,116 @@ __device__ __forceinline__ void fwht_lanes(float (&x)[E], int lane_in_group) {
   }
 }
 
+// ---- the same butterflies, one VALU op per element per cross-lane stage ----
+// Two changes to the lane layout and the arithmetic; neither changes which
+// values are added in which order, so the magnitudes are fwht_lanes' bits:
+//  - Chunk j of the vector (elements [jE, (j+1)E)) sits in lane
+//    fwht_perm_lane(j) of its group: chunks with bit 2 set swap their low two
+//    lane bits. The stride-4 partner j ^ 4 is then the row_half_mirror
+//    partner (lane l <-> 7 - l of each 8), one DPP move; strides 1, 2 and 8
+//    stay quad_perm / row_ror:8 moves. (The map is its own inverse.)
+//  - The upper lane of a pair takes x - p, the negated p - x, so every lane
+//    does x + c p with c = +1 or -1: one v_fmac with the partner as a DPP
+//    operand (the product by +-1 is exact, so the fma rounds the sum or
+//    difference once, as the add does). The negations accumulate: the value
+//    held is (-1)^popc(j) times the transform's; fwht_perm_sign gives that
+//    factor, which the caller folds into its scale. A result that is an exact
+//    zero may carry the other sign than fwht_lanes' zero.
+template <int LPV>
+__device__ __forceinline__ int fwht_perm_lane(int j) {
+  return LPV >= 8 ? (j ^ ((j & 4) ? 3 : 0)) : j;
+}
+template <int M>
+__device__ __forceinline__ float lane_pair(float v) {
+  static_assert(M == 1 || M == 2 || M == 4 || M == 8, "pair within a 16-lane row");
+  constexpr int ctrl = M == 1 ? 0xB1 : M == 2 ? 0x4E : M == 4 ? 0x141 : 0x128;
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), ctrl, 0xF, 0xF, true));
+}
+// x[o .. o+7] += c * (the same element of the pair partner): one
+// v_fmac_f32_dpp each. Inline asm, since LLVM does not fold a DPP move into
+// v_fmac. A DPP read needs 2 wait states after a VALU write of its register
+// and 5 after a VALU write of EXEC; the block starts with NOP wait states
+// (s_nop n gives n + 1), and no element is written in between.
+#define FTQ_FMAC_DPP8(NOP, DPP)                                                   \
+  asm(NOP "\n"                                                                    \
+      "v_fmac_f32_dpp %0, %0, %8 " DPP " row_mask:0xf bank_mask:0xf bound_ctrl:1\n" \
+      "v_fmac_f32_dpp %1, %1, %8 " DPP " row_mask:0xf bank_mask:0xf bound_ctrl:1\n" \
+      "v_fmac_f32_dpp %2, %2, %8 " DPP " row_mask:0xf bank_mask:0xf bound_ctrl:1\n" \
+      "v_fmac_f32_dpp %3, %3, %8 " DPP " row_mask:0xf bank_mask:0xf bound_ctrl:1\n" \
+      "v_fmac_f32_dpp %4, %4, %8 " DPP " row_mask:0xf bank_mask:0xf bound_ctrl:1\n" \
+      "v_fmac_f32_dpp %5, %5, %8 " DPP " row_mask:0xf bank_mask:0xf bound_ctrl:1\n" \
+      "v_fmac_f32_dpp %6, %6, %8 " DPP " row_mask:0xf bank_mask:0xf bound_ctrl:1\n" \
+      "v_fmac_f32_dpp %7, %7, %8 " DPP " row_mask:0xf bank_mask:0xf bound_ctrl:1"   \
+      : "+v"(x[o]), "+v"(x[o + 1]), "+v"(x[o + 2]), "+v"(x[o + 3]), "+v"(x[o + 4]),   \
+        "+v"(x[o + 5]), "+v"(x[o + 6]), "+v"(x[o + 7])                                \
+      : "v"(c))
+
+template <int M, bool FIRST, int E>
+__device__ __forceinline__ void fmac_pair8(float (&x)[E], int o, float c) {
+  if constexpr (FIRST) {
+    if constexpr (M == 1) FTQ_FMAC_DPP8("s_nop 4", "quad_perm:[1,0,3,2]");
+    else if constexpr (M == 2) FTQ_FMAC_DPP8("s_nop 4", "quad_perm:[2,3,0,1]");
+    else if constexpr (M == 4) FTQ_FMAC_DPP8("s_nop 4", "row_half_mirror");
+    else FTQ_FMAC_DPP8("s_nop 4", "row_ror:8");
+  } else {
+    if constexpr (M == 1) FTQ_FMAC_DPP8("s_nop 1", "quad_perm:[1,0,3,2]");
+    else if constexpr (M == 2) FTQ_FMAC_DPP8("s_nop 1", "quad_perm:[2,3,0,1]");
+    else if constexpr (M == 4) FTQ_FMAC_DPP8("s_nop 1", "row_half_mirror");
+    else FTQ_FMAC_DPP8("s_nop 1", "row_ror:8");
+  }
+}
+#undef FTQ_FMAC_DPP8
+
+template <int LPV>
+__device__ __forceinline__ float fwht_perm_sign(int j) {
+  return (__builtin_popcount((unsigned)j & (LPV - 1)) & 1) ? -1.f : 1.f;
+}
+// j: the chunk index (fwht_perm_lane of the lane in the group)
+template <int E, int LPV>
+__device__ __forceinline__ void fwht_lanes_perm(float (&x)[E], int j) {
+#pragma unroll
+  for (int h = 1; h < E; h <<= 1) {
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+      if ((i & h) == 0) {
+        float a = x[i], b = x[i + h];
+        x[i] = a + b;
+        x[i + h] = a - b;
+      }
+    }
+  }
+  static_assert(E % 8 == 0, "blocks of 8 elements");
+  // The first block waits 5 states (an EXEC write may precede the transform);
+  // every later one 2, whatever the compiler schedules between the blocks.
+#pragma unroll
+  for (int o = 0; o < E; o += 8) {
+    if (o == 0) fmac_pair8<1, true>(x, o, (j & 1) ? -1.f : 1.f);
+    else fmac_pair8<1, false>(x, o, (j & 1) ? -1.f : 1.f);
+  }
+  if constexpr (LPV >= 4) {
+#pragma unroll
+    for (int o = 0; o < E; o += 8) fmac_pair8<2, false>(x, o, (j & 2) ? -1.f : 1.f);
+  }
+  if constexpr (LPV >= 8) {
+#pragma unroll
+    for (int o = 0; o < E; o += 8) fmac_pair8<4, false>(x, o, (j & 4) ? -1.f : 1.f);
+  }
+  if constexpr (LPV >= 16) {
+#pragma unroll
+    for (int o = 0; o < E; o += 8) fmac_pair8<8, false>(x, o, (j & 8) ? -1.f : 1.f);
+  }
+}
+// group_sum over the permuted layout: the same pairs of chunks as group_sum
+// over the plain one, so the same bits
+template <int LPV>
+__device__ __forceinline__ float group_sum_perm(float v) {
+  if constexpr (LPV >= 2) v += lane_pair<1>(v);
+  if constexpr (LPV >= 4) v += lane_pair<2>(v);
+  if constexpr (LPV >= 8) v += lane_pair<4>(v);
+  if constexpr (LPV >= 16) v += lane_pair<8>(v);
+  return v;
+}
+
 // ---- element loads / stores ----------------------------------------------
 enum DType : int { F32 = 0, F16 = 1, BF16 = 2 };
 

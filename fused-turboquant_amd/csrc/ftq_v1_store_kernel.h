@@ -232,8 +232,11 @@ __global__ __launch_bounds__(256) void v1_store_fast_kernel(
   constexpr int NW = NWK > NWV ? NWK : NWV;
   static_assert(RB == 0 || RB == 2 || RB == 3 || RB == 4, "rotation: Hadamard or 2/3/4 blocks");
   static_assert(!KF8 || KB == 8, "fp8 keys take one byte per dim");
-  const int li = threadIdx.x % LPV;
+  // li: the vector chunk the lane holds (the Hadamard rotation uses the
+  // permuted lane layout of fwht_lanes_perm; rsg is its sign times the scale)
+  const int li = RB == 0 ? fwht_perm_lane<LPV>((int)threadIdx.x % LPV) : (int)threadIdx.x % LPV;
   const int grp = threadIdx.x / LPV;
+  const float rsg = rscale * fwht_perm_sign<LPV>(li);
 
   float mids[NMK];
   __shared__ float mid_l[MIDS_LDS ? 256 : 1];
@@ -272,7 +275,7 @@ __global__ __launch_bounds__(256) void v1_store_fast_kernel(
     float ss = 0.f;
 #pragma unroll
     for (int i = 0; i < E; ++i) ss = __builtin_fmaf(x[i], x[i], ss);
-    ss = group_sum<LPV>(ss);
+    ss = RB == 0 ? group_sum_perm<LPV>(ss) : group_sum<LPV>(ss);
     const float nrm = __builtin_sqrtf(ss + 1e-16f);
     const float den = nrm + 1e-8f;
     if constexpr (RB == 0) {
@@ -286,9 +289,9 @@ __global__ __launch_bounds__(256) void v1_store_fast_kernel(
         const float q0 = x[i] * rd;
         x[i] = __builtin_fmaf(__builtin_fmaf(-q0, den, x[i]), rd, q0);
       }
-      fwht_lanes<E, LPV>(x, li);
+      fwht_lanes_perm<E, LPV>(x, li);
 #pragma unroll
-      for (int i = 0; i < E; ++i) x[i] *= rscale;
+      for (int i = 0; i < E; ++i) x[i] *= rsg;
     } else {
       const float inv = 1.f / den;
 #pragma unroll
@@ -310,9 +313,9 @@ __global__ __launch_bounds__(256) void v1_store_fast_kernel(
     load_elems<DT, E>(value, vi * D + li * E, v);
     if (vrot) {
       if constexpr (RB == 0) {
-        fwht_lanes<E, LPV>(v, li);
+        fwht_lanes_perm<E, LPV>(v, li);
 #pragma unroll
-        for (int i = 0; i < E; ++i) v[i] = round_to_dtype<DT>(v[i] * rscale);
+        for (int i = 0; i < E; ++i) v[i] = round_to_dtype<DT>(v[i] * rsg);
       } else {
         rot_blockdiag<D, E, LPV, RB>(v, cf, li);
 #pragma unroll
@@ -326,7 +329,7 @@ __global__ __launch_bounds__(256) void v1_store_fast_kernel(
         float vs = 0.f;
 #pragma unroll
         for (int i = 0; i < E; ++i) vs = __builtin_fmaf(v[i], v[i], vs);
-        vs = group_sum<LPV>(vs);
+        vs = RB == 0 ? group_sum_perm<LPV>(vs) : group_sum<LPV>(vs);
         sc = __builtin_sqrtf(vs + 1e-16f);
         const float vden = sc + 1e-8f;
 #pragma unroll
@@ -347,9 +350,14 @@ __global__ __launch_bounds__(256) void v1_store_fast_kernel(
       for (int m = 1; m < LPV; m <<= 1) {
         if (m == 1) { mn = fminf(mn, lane_xor<1>(mn)); mx = fmaxf(mx, lane_xor<1>(mx)); }
         else if (m == 2) { mn = fminf(mn, lane_xor<2>(mn)); mx = fmaxf(mx, lane_xor<2>(mx)); }
-        else if (m == 4) { mn = fminf(mn, lane_xor<4>(mn)); mx = fmaxf(mx, lane_xor<4>(mx)); }
-        else { mn = fminf(mn, lane_xor<8>(mn)); mx = fmaxf(mx, lane_xor<8>(mx)); }
+        else if (m == 4) {
+          mn = fminf(mn, RB == 0 ? lane_pair<4>(mn) : lane_xor<4>(mn));
+          mx = fmaxf(mx, RB == 0 ? lane_pair<4>(mx) : lane_xor<4>(mx));
+        } else { mn = fminf(mn, lane_xor<8>(mn)); mx = fmaxf(mx, lane_xor<8>(mx)); }
       }
+      // a zero minimum is stored as +0 (the rotated values' zeros can carry
+      // either sign; no code or scale depends on which)
+      mn = mn + 0.f;
       sc = (VB == 1) ? (mx - mn) : (mx - mn) / (float)VTOP;
       sc = sc > 1e-8f ? sc : 1e-8f;
       const float rs = 1.f / sc;

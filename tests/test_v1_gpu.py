@@ -51,7 +51,18 @@ def test_store_parity_16bit_d128(cuda, kb, vb, dtn, vrot):
     _check_v1_store(cuda, 128, kb, vb, vrot, dtn, 7, 16, 5, 900 + kb * 10 + vb + 2 * vrot, outliers=True)
 
 
-def _check_v1_store(cuda, d, kb, vb, vrot, dtn, nb, bs, h, seed, outliers=False):
+@pytest.mark.parametrize("d", [64, 128, 256])
+@pytest.mark.parametrize("kb,vb", [(4, 2), (3, 3)])
+@pytest.mark.parametrize("vrot", [False, True])
+def test_store_zero_and_constant_vectors(cuda, d, kb, vb, vrot):
+    """All-zero rows and rows the Hadamard transform maps to one nonzero
+    element (constant +-1 rows, the alternating row): the rotated vectors hold
+    exact zeros and their minimum or maximum is a zero. Every byte outside the
+    K codes equals the oracle's (a zero minimum is stored as +0)."""
+    _check_v1_store(cuda, d, kb, vb, vrot, "bf16", 3, 16, 2, 77 + d + kb + vrot, special=True)
+
+
+def _check_v1_store(cuda, d, kb, vb, vrot, dtn, nb, bs, h, seed, outliers=False, special=False):
     from fused_turboquant import v1
     g = torch.Generator().manual_seed(seed)
     layer = v1.TurboQuantV1Layer(d, kb, vb, v_rotate=vrot, device=cuda)
@@ -62,6 +73,12 @@ def _check_v1_store(cuda, d, kb, vb, vrot, dtn, nb, bs, h, seed, outliers=False)
     slots[4] = -1
     slots[9] = -5
     k, v = _kv(g, n, h, d, DT[dtn], outliers=outliers)
+    if special:
+        alt = torch.ones(d)
+        alt[1::2] = -1
+        for i, row in zip((0, 1, 2, 3, 5), (torch.zeros(d), torch.ones(d), -torch.ones(d), alt, -alt)):
+            k[i] = row.to(k.dtype)  # token 4 is the skipped one
+            v[i] = row.to(v.dtype)
     layer.store(k.to(cuda), v.to(cuda), cache, slots.to(cuda))
     got = cache.cpu().numpy()
 
