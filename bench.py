@@ -236,11 +236,14 @@ def encode_setup(dev, d, seed, bits=3):
 
 def make_config3(dev, B=32, hq=32, hkv=8, d=128, ctx=8192, page=16, bits=3, seed=0, keep_first=False):
     """Config 3: B sequences of ctx tokens in the library-format paged cache,
-    block table = a seeded random permutation of the pages.  keep_first: also
-    return sequence 0's K / V (CPU bf16, [ctx, Hkv, d]) for the CPU baseline."""
+    block table = a seeded random permutation of the pages.  K, V and the
+    queries are drawn on the device (268 M values each for K and V).
+    keep_first: also return sequence 0's K / V (CPU bf16, [ctx, Hkv, d]) for
+    the CPU baseline."""
     import torch
     from fused_turboquant.paged import PagedTurboQuantCache
     g = torch.Generator(device="cpu").manual_seed(seed)
+    gd = torch.Generator(device=dev).manual_seed(seed)
     pages_per_seq = (ctx + page - 1) // page
     nblocks = B * pages_per_seq
     cache = PagedTurboQuantCache(nblocks, page, hkv, d, bits, bits, seed=42, device=dev)
@@ -253,12 +256,12 @@ def make_config3(dev, B=32, hq=32, hkv=8, d=128, ctx=8192, page=16, bits=3, seed
     first = None
     for s in range(0, n, chunk):
         e = min(n, s + chunk)
-        k = torch.randn(e - s, hkv, d, generator=g).to(torch.bfloat16)
-        v = torch.randn(e - s, hkv, d, generator=g).to(torch.bfloat16)
+        k = torch.randn(e - s, hkv, d, generator=gd, device=dev).to(torch.bfloat16)
+        v = torch.randn(e - s, hkv, d, generator=gd, device=dev).to(torch.bfloat16)
         if keep_first and s == 0:
-            first = (k[:ctx].clone(), v[:ctx].clone())
-        cache.store(k.to(dev), v.to(dev), slots[s:e])
-    q = torch.randn(B, hq, d, generator=g).to(torch.bfloat16).to(dev)
+            first = (k[:ctx].cpu(), v[:ctx].cpu())
+        cache.store(k, v, slots[s:e])
+    q = torch.randn(B, hq, d, generator=gd, device=dev).to(torch.bfloat16)
     seq_lens = torch.full((B,), ctx, dtype=torch.int32, device=dev)
     if keep_first:
         return cache, q, block_table, seq_lens, first

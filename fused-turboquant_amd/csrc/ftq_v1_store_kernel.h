@@ -355,9 +355,10 @@ __global__ __launch_bounds__(256) void v1_store_fast_kernel(
           mx = fmaxf(mx, RB == 0 ? lane_pair<4>(mx) : lane_xor<4>(mx));
         } else { mn = fminf(mn, lane_xor<8>(mn)); mx = fmaxf(mx, lane_xor<8>(mx)); }
       }
-      // a zero minimum is stored as +0 (the rotated values' zeros can carry
-      // either sign; no code or scale depends on which)
-      mn = mn + 0.f;
+      // a rotated zero minimum is stored as +0 (the butterflies' zeros can
+      // carry either sign, the dense product's are +0; no code or scale
+      // depends on which); an input's own -0.0 minimum is kept
+      if (vrot) mn = mn + 0.f;
       sc = (VB == 1) ? (mx - mn) : (mx - mn) / (float)VTOP;
       sc = sc > 1e-8f ? sc : 1e-8f;
       const float rs = 1.f / sc;

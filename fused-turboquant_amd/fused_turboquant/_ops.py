@@ -33,6 +33,14 @@ def _register_fakes() -> None:
         return (x.new_empty((*x.shape[:-1], d * bits // 8), dtype=torch.uint8),
                 x.new_empty(x.shape[:-1], dtype=torch.float16))
 
+    @torch.library.register_fake(lib + "encode_kv")
+    def _encode_kv(k, v, signs, boundaries, bits, codebook_class):
+        d = k.shape[-1]
+        return (k.new_empty((*k.shape[:-1], d * bits // 8), dtype=torch.uint8),
+                k.new_empty(k.shape[:-1], dtype=torch.float16),
+                v.new_empty((*v.shape[:-1], d * bits // 8), dtype=torch.uint8),
+                v.new_empty(v.shape[:-1], dtype=torch.float16))
+
     @torch.library.register_fake(lib + "decode")
     def _decode(packed, norms, levels, signs, bits, d, out_dtype):
         return packed.new_empty((*norms.shape, d), dtype=out_dtype)

@@ -16,8 +16,10 @@ Per call:
   attention over the packed slots with norm correction, LSE merge, V
   un-rotation, output cast), the reference's ``_decode_attention*``
   (``:842-1093``).
-* prefill of a fresh sequence -> SDPA over the full-precision K/V of the
-  batch (the reference uses flash-attn varlen there, ``:1283-1443``).
+* prefill of fresh sequences -> SDPA over the full-precision K/V of the
+  batch, grouped K/V (``enable_gqa``, ``:1355-1358``), one launch per run of
+  consecutive fresh sequences of one length (the reference uses flash-attn
+  varlen there, ``:1283-1443``).
 * prefill continuing a cached sequence -> the decode kernel with one
   synthetic sequence per query token (seq_len = cached + i + 1, same block
   table row): causal attention over the stored slots, the reference's
@@ -31,6 +33,13 @@ and decodes them with ``ftq_raw_decode_attention`` (the reference's
 run the TurboQuant path at that width inside the fp16-sized slot (8: 256
 Lloyd-Max centroids for K, 8-bit uniform V), and ``fp8`` stores fp8 e4m3fn
 keys with 8-bit uniform values (``boundary_tq_config.py``).
+
+Sliding-window layers (``sliding_window=W``, vLLM's window: a query at
+position p sees keys p - W + 1 .. p) decode from ``kv_start = max(0, seq_len
+- W)`` per row, continuation rows likewise, and fresh prefill masks each
+query block to its window.  The reference stores the window and attends the
+whole context (``:316``); logit soft-capping, which it also stores without
+applying (``:318``), is refused here.
 
 Head sizes 64, 128 and 256.  At 128 with 2-4 bit codes decode runs on the
 matrix-core kernels; every other head size and width (1-bit, 8-bit, fp8
@@ -222,9 +231,11 @@ class FusedTurboQuantV1Impl(_ImplBase):
             raise NotImplementedError("ALiBi attention is not supported")
         if kv_sharing_target_layer_name is not None:
             raise NotImplementedError("KV sharing is not yet supported")
-        if sliding_window is not None:
-            raise NotImplementedError("sliding-window attention is not supported by the TURBOQUANT backend")
+        if sliding_window is not None and int(sliding_window) <= 0:
+            raise ValueError(f"sliding_window must be a positive token count, got {sliding_window}")
         if logits_soft_cap is not None:
+            # the reference stores the value and never applies it (v1_backend.py:318); scores
+            # here are not capped either, so a model that needs the cap is refused up front
             raise NotImplementedError("logit soft-capping is not supported by the TURBOQUANT backend")
         # Boundary-protection layers arrive with a plain cache dtype ("auto",
         # "float16", "bfloat16"; reference v1_backend.py:335-366): raw fp16
@@ -260,9 +271,15 @@ class FusedTurboQuantV1Impl(_ImplBase):
         self.scale = float(scale)
         self.num_kv_heads = num_kv_heads
         self.num_kv_groups = num_heads // num_kv_heads
+        # vLLM's window: a query at position p attends keys p - W + 1 .. p (flash-attn
+        # window_size (W - 1, 0)); decode rows start at max(0, seq_len - W)
+        self.sliding_window = int(sliding_window) if sliding_window is not None else None
+        self.logits_soft_cap = logits_soft_cap
         self.kv_cache_dtype = kv_cache_dtype
         self.v_rotate = not self._is_raw and (env_flag("TURBOQUANT_V_ROTATE") or env_flag("TURBOQUANT_V_LLOYD_MAX"))
         self.defer_prefill = not self._is_raw and env_flag("TURBOQUANT_DEFER_PREFILL")
+        if self.defer_prefill and self.sliding_window is not None:
+            raise NotImplementedError("TURBOQUANT_DEFER_PREFILL with sliding-window layers is not supported")
         self._prefix_capacity = _defer_capacity() if self.defer_prefill else 0
         self.max_kv_splits = _max_kv_splits()
         # Lloyd-Max V codes (4-bit V; other widths stay uniform but rotated, as in the reference)
@@ -435,38 +452,109 @@ class FusedTurboQuantV1Impl(_ImplBase):
             ws = _buf(layer, "ws", (wsb,), torch.uint8, dev)
         else:
             ws = None
+        ks = None
+        if self.sliding_window is not None:
+            # each row attends its last W positions: [max(0, seq_len - W), seq_len)
+            ks = _buf(layer, "win_start", (B,), torch.int32, dev) if layer is not None else \
+                torch.empty(B, dtype=torch.int32, device=dev)
+            torch.sub(sl, self.sliding_window, out=ks)
+            ks.clamp_(min=0)
         if self._is_raw:
-            return RAW.raw_decode_attention(q, kv_cache, bt, sl, scale=self.scale, num_splits=splits, out=out,
-                                            workspace=ws)
+            return RAW.raw_decode_attention(q, kv_cache, bt, sl, scale=self.scale, kv_start=ks, num_splits=splits,
+                                            out=out, workspace=ws)
         return V1.v1_decode_attention(q, kv_cache, bt, sl, st.centroids, self.key_bits, self.value_bits,
                                       scale=self.scale, v_rotate=self.v_rotate, v_lloyd_max=self.v_lloyd_max,
-                                      num_splits=splits, rotation=st.rotation, out=out, workspace=ws,
+                                      kv_start=ks, num_splits=splits, rotation=st.rotation, out=out, workspace=ws,
                                       sorted_centroids=True, key_fp8=self.key_fp8)
 
     def _prefill(self, q, k, v, kv_cache, md, nd, ndt, st):
-        """Prefill sequences nd.. of the batch (tokens ndt..N)."""
+        """Prefill sequences nd.. of the batch (tokens ndt..N).  A run of
+        consecutive fresh sequences of one length is one batched SDPA over
+        views of q / k / v (no copies, grouped K/V); a continuing sequence
+        runs the decode kernel with one synthetic row per query token."""
         qsl = md.query_start_loc.tolist()
         sls = md.seq_lens.tolist()
-        res = []
-        for i in range(nd, len(sls)):
+        N = q.shape[0]
+        out = torch.empty(N - ndt, self.num_heads, self.head_size, dtype=q.dtype, device=q.device)
+        n = len(sls)
+        i = nd
+        while i < n:
             a, b = qsl[i], qsl[i + 1]
             n_q = b - a
             if n_q == 0:
+                i += 1
                 continue
             past = sls[i] - n_q
             if past <= 0:
-                # fresh sequence: causal attention over the full-precision K/V of the chunk
-                qq = q[a:b].transpose(0, 1).unsqueeze(0)
-                kk = k[a:b].transpose(0, 1).unsqueeze(0)
-                vv = v[a:b].transpose(0, 1).unsqueeze(0)
-                if self.num_kv_groups > 1:
-                    kk = kk.repeat_interleave(self.num_kv_groups, dim=1)
-                    vv = vv.repeat_interleave(self.num_kv_groups, dim=1)
-                o = F.scaled_dot_product_attention(qq, kk, vv, is_causal=True, scale=self.scale)
-                res.append(o[0].transpose(0, 1))
+                # fresh sequences: causal attention over the full-precision K/V of the chunk
+                j = i + 1
+                while (j < n and qsl[j + 1] - qsl[j] == n_q and sls[j] == n_q
+                       and (j + 1 - i) * n_q <= _FRESH_BATCH_TOKENS):
+                    j += 1
+                g = j - i
+                e = a + g * n_q
+                qq = q[a:e].view(g, n_q, self.num_heads, self.head_size)
+                kk = k[a:e].view(g, n_q, self.num_kv_heads, self.head_size)
+                vv = v[a:e].view(g, n_q, self.num_kv_heads, self.head_size)
+                out[a - ndt:e - ndt] = self._fresh_attention(qq, kk, vv).reshape(g * n_q, self.num_heads,
+                                                                                   self.head_size)
+                i = j
             else:
                 # continuation: one synthetic decode per query token over the stored slots
                 row = md.block_table[i:i + 1].to(torch.int32).expand(n_q, -1).contiguous()
                 syn = torch.arange(past + 1, past + n_q + 1, device=q.device, dtype=torch.int32)
-                res.append(self._decode(q[a:b], kv_cache, row, syn, st, max_seq_len=sls[i]))
-        return torch.cat(res, dim=0) if res else q[ndt:ndt]
+                out[a - ndt:b - ndt] = self._decode(q[a:b], kv_cache, row, syn, st, max_seq_len=sls[i])
+                i += 1
+        return out
+
+    def _fresh_attention(self, q, k, v):
+        """Causal attention of fresh sequences, q [G, L, Hq, D] and k / v
+        [G, L, Hkv, D] (views of the step's tensors) -> [G, L, Hq, D]; with a
+        sliding window, query blocks attend their window of keys only."""
+        G, L = q.shape[0], q.shape[1]
+        qt, kt, vt = q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)
+        W = self.sliding_window
+        if W is None or W >= L:
+            return _sdpa(qt, kt, vt, self.scale).transpose(1, 2)
+        out = torch.empty_like(q)
+        pos = torch.arange(L, device=q.device)
+        for a in range(0, L, _WINDOW_QUERY_BLOCK):
+            b = min(L, a + _WINDOW_QUERY_BLOCK)
+            k0 = max(0, a - W + 1)
+            qi, kj = pos[a:b, None], pos[None, k0:b]
+            mask = (kj <= qi) & (kj > qi - W)
+            o = _sdpa(qt[:, :, a:b], kt[:, :, k0:b], vt[:, :, k0:b], self.scale, mask=mask)
+            out[:, a:b] = o.transpose(1, 2)
+        return out
+
+
+# fresh prefill: tokens per batched SDPA launch, and query rows per block of a
+# windowed one (its mask is block x (block + window) booleans)
+_FRESH_BATCH_TOKENS = 32768
+_WINDOW_QUERY_BLOCK = 2048
+_GQA_KERNELS: Optional[bool] = None  # whether torch's fused SDPA kernels take grouped K/V here
+
+
+def _sdpa(q, k, v, scale: float, mask: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """softmax(q k^T * scale) v over [G, H, L, D] views, causal (mask None)
+    or under a boolean mask.  Causal grouped K/V (Hkv < Hq) go to torch's
+    fused kernels with ``enable_gqa`` (the reference's call,
+    v1_backend.py:1355-1358); where those kernels refuse grouped heads, and
+    under a mask (torch's flash kernel takes no mask and its memory-efficient
+    one no grouped heads), K/V are expanded once per call."""
+    global _GQA_KERNELS
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    rep = q.shape[1] // k.shape[1]
+    kw = dict(attn_mask=mask, is_causal=mask is None, scale=scale)
+    if rep > 1 and mask is None and _GQA_KERNELS is not False:
+        try:
+            with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+                o = F.scaled_dot_product_attention(q, k, v, enable_gqa=True, **kw)
+            _GQA_KERNELS = True
+            return o
+        except RuntimeError:
+            _GQA_KERNELS = False
+    if rep > 1:
+        k = k.repeat_interleave(rep, dim=1)
+        v = v.repeat_interleave(rep, dim=1)
+    return F.scaled_dot_product_attention(q, k, v, **kw)

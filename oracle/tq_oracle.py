@@ -499,6 +499,102 @@ def v1_quantize_v(v: np.ndarray, vb: int):
     return q, sc, mn, t
 
 
+def v1_dense_rotation(d: int, rotation=None, blockdiag=None) -> np.ndarray:
+    """The float32 d x d matrix M of the layer's rotation (``x @ M`` is the
+    forward rotation): Sylvester H / sqrt(d) for ``rht`` (reference
+    rotation/hadamard.py:28-34, a float32 tensor divided by the Python float
+    sqrt(d)), the caller's matrix, or the block-diagonal matrix whose
+    coefficients coeffs[j][e] = M[(e // B) B + j][e] are given
+    (rotation/matrix.py:104-148)."""
+    if blockdiag is not None:
+        coeffs, B = blockdiag
+        c = np.asarray(coeffs, np.float32)
+        m = np.zeros((d, d), np.float32)
+        for e in range(d):
+            for j in range(B):
+                r = (e // B) * B + j
+                if r < d:
+                    m[r, e] = c[j][e]
+        return m
+    if rotation is not None:
+        return np.asarray(rotation, np.float32)
+    return (sylvester(d).astype(np.float32) / np.float32(math.sqrt(d))).astype(np.float32)
+
+
+def v1_rotate_value(value: np.ndarray, M: np.ndarray) -> np.ndarray:
+    """V pre-rotation of ``v_rotate`` / ``V_LLOYD_MAX`` (reference
+    v1_backend.py:736-740): ``einsum('nhd,de->nhe', value.float(), M)`` with
+    the layer's float32 matrix M, cast back to the value dtype afterwards.
+    The einsum is a float32 GEMM whose summation order is the library's; the
+    value every such order approximates is the product formed here in
+    float64 (bf16/fp16/fp32 inputs times float32 entries: each product exact,
+    the sum within ~2^-50 relative).  How far a float32 order may stray from
+    it is bounded in ``v1_v_tie_vectors``."""
+    return np.asarray(value, np.float32).astype(np.float64) @ np.asarray(M, np.float32).astype(np.float64)
+
+
+# Spread allowed between float32 evaluations of the V pre-rotation, in units
+# of 2^-24 * rms of the rotated vector.  Measured on N(0,1) bf16 vectors with
+# 2% x8 outliers (d = 64 / 128 / 256): the Sylvester butterflies stay within
+# 5.2, an sgemm and a sequential float32 dot product within 43 (d = 128, where
+# 1/sqrt(d) is not a power of two and each product rounds).
+V_TIE_UNITS = 64.0
+
+
+def v1_v_tie_vectors(vr: np.ndarray, dtype: str, vb: int, v_lloyd_max: bool = False,
+                     units: float = V_TIE_UNITS) -> np.ndarray:
+    """Boolean [...] mask of the vectors whose stored V bytes can depend on
+    the float32 summation order of the pre-rotation: with every rotated
+    element moved anywhere within +-tol (tol = units * 2^-24 * rms of the
+    vector) of its exact value ``vr`` (float64, ``v1_rotate_value``), a
+    vector is flagged if its stored fields can take more than one value:
+
+    * the rounded element takes two values (it sits within tol of a rounding
+      boundary of the value dtype; for float32 every element moves) and that
+      changes its code, the minimum or the maximum;
+    * uniform codes: the range of (v - min) / scale + 0.5 over the box
+      straddles an integer, or the fp16 scale or minimum straddles an fp16
+      rounding boundary;
+    * Lloyd-Max codes (``v_lloyd_max``, 4-bit V): any element takes two
+      values (the norm and every code depend on all of them).
+
+    Interval arithmetic on monotone float32 formulas, so the mask is a
+    superset of the vectors any float32 order can change."""
+    vr = np.asarray(vr, np.float64)
+    rms = np.sqrt(np.mean(vr * vr, axis=-1, keepdims=True))
+    tol = units * 2.0 ** -24 * rms
+    lo = v1_round_dtype((vr - tol).astype(np.float32), dtype)
+    hi = v1_round_dtype((vr + tol).astype(np.float32), dtype)
+    if v_lloyd_max and vb == 4:
+        # codes and the fp16 norm both depend on every element: any element
+        # with two candidate values flags the vector
+        return np.any(lo != hi, axis=-1)
+    top = (1 << vb) - 1
+    mn_lo, mn_hi = lo.min(axis=-1), hi.min(axis=-1)
+    mx_lo, mx_hi = lo.max(axis=-1), hi.max(axis=-1)
+
+    def _scale(mx, mn):
+        s = (mx - mn).astype(np.float32) if vb == 1 else ((mx - mn) / np.float32(top)).astype(np.float32)
+        return np.where(s > np.float32(1e-8), s, np.float32(1e-8)).astype(np.float32)
+
+    sc_min, sc_max = _scale(mx_lo, mn_hi), _scale(mx_hi, mn_lo)
+    flag = (mn_lo.astype(np.float16) != mn_hi.astype(np.float16)) | \
+           (sc_min.astype(np.float16) != sc_max.astype(np.float16))
+
+    def _t(v, mn, sc):
+        return (((v - mn[..., None]).astype(np.float32) / sc[..., None]).astype(np.float32)
+                + np.float32(0.5)).astype(np.float32)
+
+    # (v - mn) / sc grows with v and falls with mn; where v - mn >= 0 it falls
+    # with sc.  The upper corner (hi, mn_lo, sc_min) always has hi - mn_lo >= 0;
+    # a lower corner with lo - mn_hi < 0 gives t < 0.5, code 0, the least code
+    t_lo = _t(lo, mn_hi, sc_max)
+    t_hi = _t(hi, mn_lo, sc_min)
+    c_lo = np.clip(np.floor(np.maximum(t_lo, 0)), 0, top)
+    c_hi = np.clip(np.floor(np.maximum(t_hi, 0)), 0, top)
+    return flag | np.any(c_lo != c_hi, axis=-1)
+
+
 def v1_round_dtype(x: np.ndarray, dtype: str) -> np.ndarray:
     """float32 -> value dtype -> float32 (round to nearest even)."""
     x = np.asarray(x, np.float32)
@@ -534,7 +630,10 @@ def v1_store(key: np.ndarray, value: np.ndarray, slot_mapping: np.ndarray, kv_ca
     """Write [N, H, d] float32 K/V (already converted from their dtype) into
     ``kv_cache`` uint8[nb, bs, H, slot] in place.  Negative slots are skipped
     (triton_inkernel_store.py:394-395).  With ``v_rotate`` V is first rotated
-    by M = H/sqrt(d) and rounded back to the value dtype (v1_backend.py:736-740).
+    by the layer's dense M (``v1_rotate_value``: H/sqrt(d), the caller's
+    matrix, or the block-diagonal one) and rounded back to the value dtype
+    (v1_backend.py:736-740); ``vrot`` in the result is that product before
+    the rounding, for ``v1_v_tie_vectors``.
     With ``v_lloyd_max`` and 4-bit V, V takes Lloyd-Max codes against the K
     midpoints, its norm goes in the scale field and the min field is 0
     (triton_inkernel_store.py:159-200); other V widths keep the uniform codes.
@@ -556,13 +655,9 @@ def v1_store(key: np.ndarray, value: np.ndarray, slot_mapping: np.ndarray, kv_ca
         kcodes = f32_to_e4m3((y * norm[..., None]).astype(np.float32))
     else:
         kcodes = v1_quantize_k(y, midpoints)
+    vr = None
     if v_rotate:
-        if blockdiag is not None:
-            vr = v1_blockdiag_rotate(value, *blockdiag)
-        elif rotation is None:
-            vr = fwht_unscaled(value) * fwht_scale(d)
-        else:
-            vr = np.asarray(value, np.float64) @ np.asarray(rotation, np.float64)
+        vr = v1_rotate_value(value, v1_dense_rotation(d, rotation, blockdiag))
         value = v1_round_dtype(vr.astype(np.float32), value_dtype)
     if v_lloyd_max and vb == 4:
         vq, sc, t = v1_quantize_v_lloyd(value, midpoints)
@@ -586,7 +681,7 @@ def v1_store(key: np.ndarray, value: np.ndarray, slot_mapping: np.ndarray, kv_ca
         row[:, g["kps"]:g["kps"] + g["vdb"]] = vp[i]
         row[:, g["kps"] + g["vdb"]:g["kps"] + g["vdb"] + 2] = sc16[i]
         row[:, g["kps"] + g["vdb"] + 2:g["raw"]] = mn16[i]
-    return dict(y=y, norm=norm, kcodes=kcodes, vcodes=vq, vscale=sc, vmin=mn, vt=t, value=value)
+    return dict(y=y, norm=norm, kcodes=kcodes, vcodes=vq, vscale=sc, vmin=mn, vt=t, value=value, vrot=vr)
 
 
 def v1_unpack(kv_cache: np.ndarray, d: int, kb: int, vb: int, key_fp8: bool = False):

@@ -221,6 +221,15 @@ def test_encode_decode_under_torch_compile(cuda):
     for got, want in zip(compiled(x), roundtrip(x)):
         assert torch.equal(got, want)
 
+    def roundtrip_kv(k, v):
+        ck, cv = tq.encode_kv(k, v)
+        return ck.indices, ck.norms, cv.indices, cv.norms, tq.decode(ck), tq.decode(cv)
+
+    compiled_kv = torch.compile(roundtrip_kv, fullgraph=True)
+    v = torch.randn(300, 8, 128, generator=torch.Generator().manual_seed(7)).to(torch.bfloat16).to(cuda)
+    for got, want in zip(compiled_kv(x, v), roundtrip_kv(x, v)):
+        assert torch.equal(got, want)
+
 
 @pytest.mark.parametrize("d", [8, 16, 32, 512, 1024, 2048])
 @pytest.mark.parametrize("bits", [2, 3, 4])

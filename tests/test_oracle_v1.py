@@ -520,3 +520,68 @@ def test_unsupported_widths_rejected(kb, vb, fp8):
     assert L.ftq_v1_slot_bytes_flags(128, kb, vb, 4 if fp8 else 0) == -1
     with pytest.raises(ValueError):
         v1.slot_bytes(128, kb, vb, key_fp8=fp8)
+
+
+@pytest.mark.parametrize("kind", ["rht", "planar", "rotor", "iso_full"])
+@pytest.mark.parametrize("dtype,tdt", [("bf16", torch.bfloat16), ("f16", torch.float16), ("f32", torch.float32)])
+def test_v_rotation_is_the_dense_product_up_to_counted_ties(kind, dtype, tdt):
+    """The oracle's V pre-rotation is the reference's expression
+    ``einsum('nhd,de->nhe', value.float(), M).to(value.dtype)``
+    (v1_backend.py:736-740) with M the layer's float32 matrix: the dense
+    matrix it builds equals the reference's Sylvester builder
+    (rotation/hadamard.py:28-34) and the block-diagonal matrices, and V bytes
+    quantised from torch's own float32 einsum and from the Sylvester
+    butterflies (another float32 order) equal the oracle's in every vector
+    that ``v1_v_tie_vectors`` does not flag.  A dropped 1/sqrt(d), a
+    transposed M or a missing cast to the value dtype fails here."""
+    from fused_turboquant import v1
+    rng = np.random.default_rng(90)
+    d, n, vb = 128, 6000, 3
+    if kind == "rht":
+        h = torch.tensor([[1.0]])
+        while h.shape[0] < d:
+            h = torch.cat([torch.cat([h, h], 1), torch.cat([h, -h], 1)], 0)
+        m_ref = (h / math.sqrt(d)).numpy()
+        M = O.v1_dense_rotation(d)
+    else:
+        m_ref = v1.rotation_matrix(kind, d).numpy()
+        M = O.v1_dense_rotation(d, blockdiag=(v1.block_coeffs(torch.from_numpy(m_ref), v1.BLOCK_SIZES[kind]).numpy(),
+                                              v1.BLOCK_SIZES[kind]))
+    assert np.array_equal(M, m_ref)
+    v = rng.standard_normal((n, 1, d)).astype(np.float32)
+    v[: n // 50] *= 8
+    vt = torch.from_numpy(v).to(tdt)
+    v = vt.float().numpy()
+    vr = O.v1_rotate_value(v, M)
+    want = O.v1_quantize_v(O.v1_round_dtype(vr.astype(np.float32), dtype), vb)
+    flagged = O.v1_v_tie_vectors(vr, dtype, vb)
+    assert flagged.mean() < 0.05
+    others = [torch.einsum("nhd,de->nhe", vt.float(), torch.from_numpy(M)).to(tdt).float().numpy()]
+    if kind == "rht":
+        others.append(O.v1_round_dtype((O.fwht_unscaled(v) * O.fwht_scale(d)).astype(np.float32), dtype))
+    for got_v in others:
+        got = O.v1_quantize_v(got_v, vb)
+        diff = (np.any(got[0] != want[0], axis=-1) | (got[1].astype(np.float16) != want[1].astype(np.float16))
+                | (got[2].astype(np.float16) != want[2].astype(np.float16)))
+        assert not (diff & ~flagged).any()
+    # the oracle's store writes the same V fields
+    cache = np.zeros((n // 16 + 1, 16, 1, 128), np.uint8)
+    mids = O.v1_midpoints(O.lloyd_max_codebook(d, 3)[1].astype(np.float32))
+    st = O.v1_store(v, v, np.arange(n), cache, mids, 3, vb, v_rotate=True, value_dtype=dtype,
+                    blockdiag=None if kind == "rht" else (v1.block_coeffs(torch.from_numpy(m_ref),
+                                                                           v1.BLOCK_SIZES[kind]).numpy(),
+                                                          v1.BLOCK_SIZES[kind]))
+    assert np.array_equal(st["vcodes"], want[0]) and np.array_equal(st["vscale"], want[1])
+    assert np.allclose(st["vrot"], vr, rtol=0, atol=0)
+
+
+def test_v_tie_vectors_flag_a_planted_rounding_tie():
+    """A rotated value placed exactly on a bf16 rounding boundary flags its
+    vector when it is the maximum; the vector whose maximum is the bf16 value
+    1.0 itself, with no element near a boundary or a code edge, is not."""
+    d, vb = 8, 2
+    base = np.array([0.1, 0.5, -1.0, 0.3, 0.7, -0.45, 0.15, 1.0], np.float64)
+    tie = base.copy()
+    tie[7] = 1.0 + 2.0 ** -8  # halfway between the bf16 values 1 and 1 + 2^-7
+    assert O.v1_v_tie_vectors(tie[None], "bf16", vb)[0]
+    assert not O.v1_v_tie_vectors(base[None], "bf16", vb)[0]

@@ -48,6 +48,10 @@ def test_fake_implementations_give_shapes():
         assert dec.shape == (5, 7, 128) and dec.dtype == torch.bfloat16
         r = ops.rht(x, s, True, torch.float32)
         assert r.shape == x.shape and r.dtype == torch.float32
+        kp, kn, vp, vn = ops.encode_kv(x, x, s, b, 3, 0)
+        for p, n in ((kp, kn), (vp, vn)):
+            assert p.shape == (5, 7, 48) and p.dtype == torch.uint8
+            assert n.shape == (5, 7) and n.dtype == torch.float16
 
 
 def test_cpu_tensors_rejected_by_the_package():

@@ -3,8 +3,12 @@
 Store: every slot byte read back equals the oracle's store of the same vectors,
 except K codes at midpoint ties (|y - midpoint| < 2e-6, code off by one; the
 K norm is a float reduction whose order differs) and the fp16 K norm (within
-1e-3 relative).  V codes, V scale and V min are bit-exact (their arithmetic
-is order-independent).  Padding and unmapped slots stay untouched.
+1e-3 relative).  V codes, V scale and V min are bit-exact, except with V
+rotated first (v_rotate): the reference rotates V by a dense float32 product
+(v1_backend.py:736-740) whose summation order is its GEMM's, so a vector
+whose rotated values sit within that order's spread of a rounding boundary
+of the value dtype may differ; such vectors are counted and printed
+(``oracle.v1_v_tie_vectors``).  Padding and unmapped slots stay untouched.
 Decode attention: against the oracle's float64 attention over the same cache
 bytes; max abs error <= 2e-2 + 2^-8 |want|, mean <= 2e-3 max(1, mean |want|)
 (bf16 tolerance, widened by one bf16 ulp for large outputs).
@@ -16,6 +20,7 @@ import pytest
 import torch
 
 from oracle import tq_oracle as O
+from _v1_checks import check_v_region
 
 pytestmark = pytest.mark.gpu
 TIE_ULPS = 4  # a code may differ only within 4 float32 ulps of a midpoint (oracle.tie_ulps)
@@ -58,7 +63,8 @@ def test_store_zero_and_constant_vectors(cuda, d, kb, vb, vrot):
     """All-zero rows and rows the Hadamard transform maps to one nonzero
     element (constant +-1 rows, the alternating row): the rotated vectors hold
     exact zeros and their minimum or maximum is a zero. Every byte outside the
-    K codes equals the oracle's (a zero minimum is stored as +0)."""
+    K codes equals the oracle's (a rotated zero minimum is stored as +0, as
+    the dense product gives it; an unrotated -0.0 minimum stays -0.0)."""
     _check_v1_store(cuda, d, kb, vb, vrot, "bf16", 3, 16, 2, 77 + d + kb + vrot, special=True)
 
 
@@ -76,7 +82,11 @@ def _check_v1_store(cuda, d, kb, vb, vrot, dtn, nb, bs, h, seed, outliers=False,
     if special:
         alt = torch.ones(d)
         alt[1::2] = -1
-        for i, row in zip((0, 1, 2, 3, 5), (torch.zeros(d), torch.ones(d), -torch.ones(d), alt, -alt)):
+        # and a row whose minimum is -0.0 (every other element positive): without
+        # the rotation that -0.0 is the stored minimum, fp16 0x8000
+        negz = torch.rand(d, generator=g) + 0.25
+        negz[3] = -0.0
+        for i, row in zip((0, 1, 2, 3, 5, 6), (torch.zeros(d), torch.ones(d), -torch.ones(d), alt, -alt, negz)):
             k[i] = row.to(k.dtype)  # token 4 is the skipped one
             v[i] = row.to(v.dtype)
     layer.store(k.to(cuda), v.to(cuda), cache, slots.to(cuda))
@@ -91,7 +101,7 @@ def _check_v1_store(cuda, d, kb, vb, vrot, dtn, nb, bs, h, seed, outliers=False,
     sl = slots.numpy()
     ok = sl >= 0
     blk, off = sl[ok] // bs, sl[ok] % bs
-    assert np.array_equal(got[..., geo["kps"]:], want[..., geo["kps"]:])
+    check_v_region(got, want, st, ok, blk, off, geo, vrot, dtn, vb, tag=f"v1 store d={d} kb={kb} vb={vb} {dtn}")
     unmapped = np.ones((nb, bs), bool)
     unmapped[blk, off] = False
     assert np.array_equal(got[unmapped], want[unmapped])
@@ -312,15 +322,26 @@ def test_store_parity_v_lloyd_max(cuda, kb):
     gk, gkn, gv, gsc, gzr = O.v1_unpack(got, d, kb, vb)
     wk, wkn, wv, wsc, wzr = O.v1_unpack(want, d, kb, vb)
     assert not gzr[blk, off].any()
+    # V vectors the float32 order of the pre-rotation can change (bf16
+    # rounding ties of the rotated values) are counted and left out below
+    vtie = O.v1_v_tie_vectors(st["vrot"][ok], "bf16", vb, v_lloyd_max=True)
     for name, gn, wn in (("K norm", gkn, wkn), ("V norm", gsc, wsc)):
         a, b = gn[blk, off].astype(np.float32), wn[blk, off].astype(np.float32)
+        if name == "V norm":
+            a, b = a[~vtie], b[~vtie]
         assert np.all(np.abs(a - b) <= 1e-3 * np.abs(b)), name
-    m64 = mids.astype(np.float64)
+    vdiff = np.any(gv[blk, off] != wv[blk, off], axis=-1)
+    print(f"[v1 store lloyd kb={kb}] V rotation ties: {int((vdiff & vtie).sum())} vectors differ, "
+          f"{int(vtie.sum())} flagged of {vtie.size}")
     for name, gc, wc, u in (("K", gk, wk, st["y"]), ("V", gv, wv, st["vt"])):
         a, b = gc[blk, off], wc[blk, off]
+        if name == "V":
+            a, b, u = a[~vtie], b[~vtie], u[ok][~vtie]
+        else:
+            u = u[ok]
         diff = a != b
         if diff.any():
-            assert O.tie_ulps(u[ok][diff], mids, d).max() <= TIE_ULPS, name
+            assert O.tie_ulps(u[diff], mids, d).max() <= TIE_ULPS, name
             assert np.all(np.abs(a[diff].astype(int) - b[diff].astype(int)) == 1), name
         print(f"[v1 store lloyd kb={kb}] {name} code ties={int(diff.sum())} of {a.size}")
 
@@ -414,7 +435,7 @@ def test_store_parity_blockdiag(cuda, kind, d, kb, vb):
     sl = slots.numpy()
     ok = sl >= 0
     blk, off = sl[ok] // bs, sl[ok] % bs
-    assert np.array_equal(got[..., geo["kps"]:], want[..., geo["kps"]:])  # V codes, scale, min, padding
+    check_v_region(got, want, st, ok, blk, off, geo, True, "bf16", vb, tag=f"v1 {kind} store d={d} kb={kb} vb={vb}")
     gk = O.unpack(got[blk, off, :, :geo["mse"]], kb, d)
     wk = st["kcodes"][ok]
     diff = gk != wk

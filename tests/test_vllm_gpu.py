@@ -30,8 +30,9 @@ def _check(got, want, tag):
     assert (err <= bound).all() and err.mean() <= mean_bound, tag
 
 
-def _causal_ref(q, k, v, scale):
-    """float64 causal attention; q [n, Hq, d], k/v [n, Hkv, d] (the chunk is the whole sequence)."""
+def _causal_ref(q, k, v, scale, window=None):
+    """float64 causal attention; q [n, Hq, d], k/v [n, Hkv, d] (the chunk is the whole sequence).
+    With a window W, query i sees keys i - W + 1 .. i."""
     q, k, v = (np.asarray(t, np.float64) for t in (q, k, v))
     n, hq, d = q.shape
     G = hq // k.shape[1]
@@ -39,6 +40,8 @@ def _causal_ref(q, k, v, scale):
     for h in range(hq):
         s = q[:, h] @ k[:, h // G].T * scale
         s = s + np.triu(np.full((n, n), -np.inf), 1)
+        if window is not None:
+            s = s + np.tril(np.full((n, n), -np.inf), -window)
         s = s - s.max(axis=1, keepdims=True)
         p = np.exp(s)
         out[:, h] = (p / p.sum(axis=1, keepdims=True)) @ v[:, h // G]
@@ -46,9 +49,10 @@ def _causal_ref(q, k, v, scale):
 
 
 def _run_step(cuda, seqs, dtype_str, hq, hkv, vrot, monkeypatch, seed, bs=16, protect="0", lloyd=False,
-              kind="rht", D=D):
+              kind="rht", D=D, window=None):
     """seqs: list of (cached_len, query_len), decodes (query_len 1, cached > 0) first.
-    Stores the cached tokens in earlier update calls, then runs one step."""
+    Stores the cached tokens in earlier update calls, then runs one step.
+    ``window``: the layer's sliding window (vLLM's ``sliding_window``)."""
     from fused_turboquant import vllm_plugin as vp
     monkeypatch.setenv("TURBOQUANT_BOUNDARY_PROTECT", protect)
     monkeypatch.setenv("TURBOQUANT_V_ROTATE", "1" if vrot else "0")
@@ -56,7 +60,7 @@ def _run_step(cuda, seqs, dtype_str, hq, hkv, vrot, monkeypatch, seed, bs=16, pr
     monkeypatch.setenv("TURBOQUANT_KIND", kind)
     g = torch.Generator().manual_seed(seed)
     Bk = vp.FusedTurboQuantV1Backend
-    impl = vp.FusedTurboQuantV1Impl(hq, D, 1 / math.sqrt(D), hkv, kv_cache_dtype=dtype_str)
+    impl = vp.FusedTurboQuantV1Impl(hq, D, 1 / math.sqrt(D), hkv, kv_cache_dtype=dtype_str, sliding_window=window)
     layer = SimpleNamespace()
     pages = [(c + q + bs - 1) // bs for c, q in seqs]
     nb = sum(pages) + 5
@@ -117,19 +121,20 @@ def _run_step(cuda, seqs, dtype_str, hq, hkv, vrot, monkeypatch, seed, bs=16, pr
         a = int(qsl[i])
         if c == 0:
             want = _causal_ref(qs[i].float().numpy(), full_k[i].float().numpy(), full_v[i].float().numpy(),
-                               1 / math.sqrt(D))
+                               1 / math.sqrt(D), window=window)
         else:
             sl = np.arange(c + 1, c + q + 1, dtype=np.int32)
+            ks = None if window is None else np.maximum(sl - window, 0).astype(np.int32)
             btr = np.repeat(bt[i:i + 1].numpy(), q, axis=0)
             if raw:
-                want = O.raw_decode_attention(qs[i].float().numpy(), cache_np, btr, sl, 1 / math.sqrt(D))
+                want = O.raw_decode_attention(qs[i].float().numpy(), cache_np, btr, sl, 1 / math.sqrt(D), kv_start=ks)
             else:
                 want = O.v1_decode_attention(qs[i].float().numpy(), cache_np, btr, sl,
                                              None if impl.key_fp8 else cent, kb, vb,
-                                             1 / math.sqrt(D), v_rotate=vrot or lloyd, v_lloyd_max=lloyd,
-                                             rotation=rot, key_fp8=impl.key_fp8)
+                                             1 / math.sqrt(D), kv_start=ks, v_rotate=vrot or lloyd,
+                                             v_lloyd_max=lloyd, rotation=rot, key_fp8=impl.key_fp8)
         kind = "prefill" if c == 0 else ("decode" if q == 1 else "continuation")
-        _check(got[a:a + q], want, f"{dtype_str} vrot={vrot} seq{i} {kind} cached={c} q={q}")
+        _check(got[a:a + q], want, f"{dtype_str} vrot={vrot} W={window} seq{i} {kind} cached={c} q={q}")
 
 
 @pytest.mark.parametrize("dtype_str,vrot", [("turboquant_3bit_nc", False), ("turboquant_k4v2_nc", True),
@@ -141,6 +146,26 @@ def test_decode_batch(cuda, monkeypatch, dtype_str, vrot):
 def test_fresh_prefill_batch(cuda, monkeypatch):
     _run_step(cuda, [(0, 37), (0, 1), (0, 200)], "turboquant_3bit_nc", 16, 4, False, monkeypatch, seed=2)
 
+
+def test_fresh_prefill_runs_of_equal_length(cuda, monkeypatch):
+    """Consecutive fresh sequences of one length go through one batched SDPA
+    launch with grouped K/V; runs of different lengths and a lone sequence
+    between them stay separate.  Every row against float64 causal attention."""
+    _run_step(cuda, [(0, 64), (0, 64), (0, 64), (0, 20), (0, 64), (0, 20), (0, 20)], "turboquant_3bit_nc", 32, 8,
+              True, monkeypatch, seed=12)
+
+
+@pytest.mark.parametrize("dtype_str,protect,d", [("turboquant_3bit_nc", "0", 128), ("turboquant_k4v2_nc", "0", 128),
+                                                 ("turboquant_k3v4_nc", "0", 256), ("auto", "1", 128)])
+def test_sliding_window_step(cuda, monkeypatch, dtype_str, protect, d):
+    """A sliding-window layer (vLLM ``sliding_window=W``; reference
+    v1_backend.py:299-318 accepts it): decode rows attend
+    [max(0, seq_len - W), seq_len), continuation rows their own window, fresh
+    prefill a banded causal mask.  Decodes longer and shorter than the window,
+    a continuation chunk crossing it, fresh sequences longer than W.  Against
+    the oracle's decode with kv_start and float64 banded causal attention."""
+    _run_step(cuda, [(300, 1), (40, 1), (1000, 1), (200, 7), (0, 150), (0, 150), (0, 60)], dtype_str, 16, 4,
+              dtype_str != "auto", monkeypatch, seed=13 + d, protect=protect, D=d, window=64)
 
 def test_continuation_chunks(cuda, monkeypatch):
     _run_step(cuda, [(64, 17), (300, 64), (15, 2)], "turboquant_k4v2_nc", 8, 2, True, monkeypatch, seed=3)

@@ -90,8 +90,18 @@ def test_impl_init_and_refusals(monkeypatch):
         mk(alibi_slopes=[1.0] * 8)
     with pytest.raises(NotImplementedError):
         mk(kv_sharing_target_layer_name="layers.0")
+    # sliding windows are applied (a Gemma-style layer: head 256, window 512); soft-capping is refused
+    gem = mk(head_size=256, num_heads=8, num_kv_heads=4, sliding_window=512, kv_cache_dtype="turboquant_k3v4_nc")
+    assert gem.sliding_window == 512 and gem.head_size == 256
+    assert mk(sliding_window=None).sliding_window is None
+    with pytest.raises(ValueError):
+        mk(sliding_window=0)
+    with pytest.raises(NotImplementedError):
+        mk(logits_soft_cap=30.0)
+    monkeypatch.setenv("TURBOQUANT_DEFER_PREFILL", "1")
     with pytest.raises(NotImplementedError):
         mk(sliding_window=128)
+    monkeypatch.setenv("TURBOQUANT_DEFER_PREFILL", "0")
     with pytest.raises(NotImplementedError):
         mk(head_size=96)
     assert mk(head_size=64).head_size == 64 and mk(head_size=256).head_size == 256
