@@ -18,7 +18,11 @@ Also timed (not part of the step), each with a roofline entry:
   * the stores: the v1 slot store (rht, and the block-diagonal rotations) at
     the reference's published shapes (1024 tokens x 8 kv heads and 1 token x 8
     kv heads, D = 128 / 256) and at a config-4 prefill chunk, and the paged
-    library-format store of a config-3 chunk.
+    library-format store of a config-3 chunk;
+  * config 5 end to end (``e2e_config5``): a random-init Llama-3-8B-shaped
+    model through the TURBOQUANT backend, 64 prompts x 2048 tokens prefilled,
+    255 greedy decode steps replayed from a HIP graph: prefill and decode
+    times and tokens per second.
 Kernel times come from HIP events on the stream the library launches on
 (torch's current stream), in steady state: 20 untimed launches, then the
 median of three windows of back-to-back launches.  The stores at the
@@ -451,6 +455,69 @@ def paged_store_setup(dev, n_tokens=65536, hkv=8, d=128, bits=3, page=16, seed=1
     return {"run": run, "total_bytes": total}
 
 
+def config5_e2e(dev, B=64, prompt=2048, new_tokens=256, seed=0):
+    """Config 5: a random-init Llama-3-8B-shaped decoder (32 layers, hidden
+    4096, 32 q / 8 kv heads, head_dim 128, FFN 14336, vocab 128256, bf16)
+    through the TURBOQUANT backend (turboquant_3bit_nc = K3V3, kind rht,
+    TURBOQUANT_BOUNDARY_PROTECT=0, TURBOQUANT_V_ROTATE=1), driven the way
+    vLLM's v1 runner drives it (fused_turboquant.vllm_plugin.runner): B
+    prompts of ``prompt`` random token ids prefilled in steps of 16384
+    tokens, then greedy decode to ``new_tokens`` output tokens (the first
+    from the prefill logits), each decode step one HIP-graph replay.  A
+    warm-up prefill of 8 prompts runs first (kernel loading), then the page
+    pool is reset.  Times from HIP events on the current stream."""
+    import torch
+    from fused_turboquant.vllm_plugin.runner import LlamaDecoder, LlamaSpec, ModelRunner
+    env = {"TURBOQUANT_BOUNDARY_PROTECT": "0", "TURBOQUANT_V_ROTATE": "1", "TURBOQUANT_KIND": "rht",
+           "TURBOQUANT_V_LLOYD_MAX": "0", "TURBOQUANT_DEFER_PREFILL": "0"}
+    saved = {k: os.environ.get(k) for k in env}
+    os.environ.update(env)
+    try:
+        spec = LlamaSpec()
+        model = LlamaDecoder(spec, dev, seed=seed)
+        gd = torch.Generator(device=dev).manual_seed(seed + 1)
+        prompts = [torch.randint(0, spec.vocab, (prompt,), generator=gd, device=dev) for _ in range(B)]
+        run = ModelRunner(model, max_batch=B, max_context=prompt + new_tokens, kv_cache_dtype="turboquant_3bit_nc",
+                          max_num_batched_tokens=16384)
+        run.prefill(prompts[:8])
+        run.reset()
+        torch.cuda.synchronize()
+        e = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+        e[0].record()
+        bt, first = run.prefill(prompts)
+        e[1].record()
+        steps = new_tokens - 1
+        run.start_decode(bt, first, [prompt] * B, steps, use_graph=True)
+        e[2].record()
+        for _ in range(steps):
+            run.decode_step()
+        e[3].record()
+        torch.cuda.synchronize()
+        pre_s = e[0].elapsed_time(e[1]) / 1e3
+        dec_s = e[2].elapsed_time(e[3]) / 1e3
+        toks = run.decoded_tokens()
+        assert bool((toks[:steps] >= 0).all()) and bool((toks[:steps] < spec.vocab).all())
+        res = {"model": "random-init Llama-3-8B shape (32 layers, hidden 4096, 32/8 heads, d 128, FFN 14336, "
+                        "vocab 128256) bf16",
+               "kv_cache_dtype": "turboquant_3bit_nc", "kind": "rht", "boundary_protect": 0, "v_rotate": True,
+               "batch": B, "prompt_tokens": prompt, "output_tokens": new_tokens,
+               "prefill_s": round(pre_s, 4), "prefill_tok_s": round(B * prompt / pre_s, 1),
+               "decode_steps": steps, "decode_us_per_step": round(dec_s / steps * 1e6, 1),
+               "decode_tok_s": round(B * steps / dec_s, 1),
+               "output_tok_s": round(B * new_tokens / (pre_s + dec_s), 1),
+               "decode_kv_splits": run.attn[0].max_kv_splits,
+               "kv_cache_bytes_per_layer": int(run.kv_caches[0].numel())}
+        del run, model, prompts
+        torch.cuda.empty_cache()
+        return res
+    finally:
+        for k, v in saved.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+
+
 # ---------------------------------------------------------------------------
 # CPU baseline: the torch restatement of the reference's unfused path
 # ---------------------------------------------------------------------------
@@ -554,6 +621,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only", default="",
                     help="comma list of roofline entries to time (profiling runs); the step still runs")
+    ap.add_argument("--no-e2e", action="store_true", help="skip the config-5 end-to-end decode")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run one 256 MiB device-to-device copy (calibrates rocprof byte counters)")
     args = ap.parse_args()
@@ -688,6 +756,14 @@ def main():
     t_a3 = rl["paged_attn_config3"]["kernel_us"] if "paged_attn_config3" in rl else float("nan")
     enc_in_gbs = 2 * n * 128 * 2 / (t_enc * 1e-6) / 1e9
 
+    e2e = None
+    if not args.no_e2e and want("e2e_config5"):
+        log("[bench] config5: random-init Llama-3-8B shape, TURBOQUANT K3V3 rht v_rotate, B=64 x 2048 prompt, "
+            "256 greedy output tokens")
+        e2e = config5_e2e(dev)
+        log(f"[bench] config5: prefill {e2e['prefill_s']} s ({e2e['prefill_tok_s']} tok/s), decode "
+            f"{e2e['decode_us_per_step']} us/step ({e2e['decode_tok_s']} tok/s)")
+
     cpu = None
     if not args.no_cpu:
         log("[bench] cpu baseline (torch restatement of the unfused reference path, host cores)")
@@ -731,6 +807,7 @@ def main():
         "config": cfg,
         "roofline": main_roof,
         "rooflines": rl,
+        "e2e_config5": e2e,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
