@@ -428,6 +428,38 @@ __device__ void build_code_lut(uint8_t* lut, const uint16_t* single, int tid, in
   }
 }
 
+// The same table built by one wave from the f16 bits of the 2^B levels
+// (lane i < 2^B holds level i; the other lanes' values are not read): each
+// lane assembles its entries' pairs with two lane reads and writes their
+// copies, 4 per ds_write_b128 for the 32-copy tables.
+template <int B>
+__device__ __forceinline__ void build_code_lut_wave(uint32_t* lut, uint32_t lev_bits, int lane) {
+  using C = CodeLut<B>;
+  constexpr int NL = 1 << B;
+  constexpr int PER = (C::ENTRIES + 63) / 64;  // entries per lane
+  uint32_t v[PER];
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const int e = lane + 64 * k;  // every lane takes part in the lane reads
+    const uint32_t lo = (uint32_t)__shfl((int)lev_bits, e & (NL - 1));
+    const uint32_t hi = (uint32_t)__shfl((int)lev_bits, (e >> B) & (NL - 1));
+    v[k] = (lo & 0xffffu) | (hi << 16);
+  }
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const int e = lane + 64 * k;
+    if (e < C::ENTRIES) {
+      if constexpr (C::COPIES == 32) {
+        uint4* dst = reinterpret_cast<uint4*>(lut + e * 32);
+#pragma unroll
+        for (int c = 0; c < 8; ++c) dst[c] = make_uint4(v[k], v[k], v[k], v[k]);
+      } else {
+        lut[e] = v[k];
+      }
+    }
+  }
+}
+
 typedef __attribute__((address_space(3))) const uint32_t lds_u32;
 
 // LDS address of this lane's copy of a code table
@@ -462,6 +494,36 @@ __device__ __forceinline__ uint2 lut_quad(const uint32_t (&w)[N], int P, uint32_
   constexpr int SH = 2 + C::LOG_COPIES;
   const uint32_t lo = *(lds_u32*)(uintptr_t)lut_entry_off<SH, C::IDX_BITS>(w, P, base);
   const uint32_t hi = *(lds_u32*)(uintptr_t)lut_entry_off<SH, C::IDX_BITS>(w, P + 2 * B, base);
+  return make_uint2(lo, hi);
+}
+
+// Byte offset, inside a table, of the entry whose index is bits [P, P + W)
+// of the code words, ORed with the lane's copy offset (< 2^SH): one funnel
+// shift that puts the field at bit SH and one v_and_or_b32, as plain
+// arithmetic the compiler schedules itself (no inline asm).
+template <int SH, int W, int N>
+__device__ __forceinline__ uint32_t lut_field(const uint32_t (&w)[N], int P, uint32_t laneoff) {
+  constexpr uint32_t M = ((1u << W) - 1u) << SH;
+  uint32_t v;
+  if (P >= SH) {
+    const int Q = P - SH, i = Q >> 5, o = Q & 31;  // compile-time after unrolling
+    v = (o + W + SH > 32 && i + 1 < N) ? __builtin_amdgcn_alignbit(w[i + 1], w[i], o) : (w[i] >> o);
+  } else {
+    v = w[0] << (SH - P);
+  }
+  return (v & M) | laneoff;
+}
+
+// lut_quad over a table in static LDS (its address a link-time constant the
+// compiler folds into the DS instructions' offset field)
+template <int B, int N>
+__device__ __forceinline__ uint2 lut_quad_s(const uint32_t (&w)[N], int P, uint32_t laneoff, const uint32_t* table) {
+  using C = CodeLut<B>;
+  constexpr int SH = 2 + C::LOG_COPIES;
+  typedef __attribute__((address_space(3))) const uint8_t lds_u8;
+  lds_u8* t = (lds_u8*)(__attribute__((address_space(3))) const void*)table;
+  const uint32_t lo = *(lds_u32*)(t + lut_field<SH, C::IDX_BITS>(w, P, laneoff));
+  const uint32_t hi = *(lds_u32*)(t + lut_field<SH, C::IDX_BITS>(w, P + 2 * B, laneoff));
   return make_uint2(lo, hi);
 }
 
@@ -512,8 +574,7 @@ struct TileRegs {
   uint32_t k[2][Gm::KLANE / 4];
   uint32_t v[2][Gm::VLANE / 4];
   uint32_t kn[2][2];  // 4 fp16 K norms per sub-block (tokens 4q..4q+3)
-  uint32_t vn[2][2];
-  bool ok[2];         // wave-uniform: sub-block holds real tokens
+  uint32_t vn[2][2];  // zero for a sub-block without tokens (see load_tile)
 };
 
 // Page of sub-block j (16 tokens) of a sequence as a multiply-high:
@@ -578,9 +639,10 @@ __device__ __forceinline__ void load_tile(TileRegs<D, BK, BV>& r, const uint8_t*
 #pragma unroll
   for (int sb = 0; sb < 2; ++sb) {
     // block id and base are wave-uniform (scalar).  An inactive or invalid
-    // sub-block (past seq_len, or a bad block id) reads block 0 instead
-    // (always issuing the loads keeps the wait counts static) and is flagged so
-    // the consumer zeroes its V norms; its scores are masked to -inf there too.
+    // sub-block (past seq_len, or a bad block id) gets a descriptor of range
+    // 0 at block 0: the loads still issue (the wait counts stay static) and
+    // return zeros, so its V norms are 0 and it adds nothing to P.V; past
+    // seq_len its scores are masked to -inf by the consumer.
     int phys = __builtin_amdgcn_readlane(btv, sb);
     const bool valid = (uint32_t)phys < (uint32_t)nb32;  // -1 (no entry) and ids >= num_blocks fail
     const int j = 2 * tile + sb;
@@ -588,12 +650,11 @@ __device__ __forceinline__ void load_tile(TileRegs<D, BK, BV>& r, const uint8_t*
     if (!valid) phys = 0;
     const uint8_t* base = cache + ((int64_t)phys * blk_stride + kvh_off + (int64_t)sub * Gm::SUB);
     const __amdgpu_buffer_rsrc_t rs =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(base), (short)0, Gm::SUB, 0x00020000);
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(base), (short)0, valid ? Gm::SUB : 0, 0x00020000);
     buf_dwords(rs, lo.k, r.k[sb]);
     buf_dwords(rs, lo.v, r.v[sb]);
     buf_dwords(rs, lo.n, r.kn[sb]);
     buf_dwords(rs, lo.n + 32u, r.vn[sb]);
-    r.ok[sb] = valid;
   }
 }
 
@@ -602,11 +663,9 @@ __device__ __forceinline__ void load_tile(TileRegs<D, BK, BV>& r, const uint8_t*
 // (tile loop) and the wave-merge buffer (epilogue)
 template <int D, int BK, int BV, bool SHARE, int NW>
 __host__ __device__ constexpr int paged_attn_lds(int G) {
-  const int lut = CodeLut<BK>::BYTES + (SHARE ? 0 : CodeLut<BV>::BYTES);
   const int red = NW * G * (D + 1) * 4;
   const int qs = G * (D + 4) * 4;
-  const int m = lut > red ? lut : red;
-  return m > qs ? m : qs;
+  return red > qs ? red : qs;
 }
 
 // Output of a finished (batch, q head) row: o / L, inverse RHT of V
@@ -659,18 +718,18 @@ __global__ __launch_bounds__(NW * 64, NW == 16 ? 1 : (D == 128 ? (QL ? 3 : 4) : 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int h = lane & 15, q = lane >> 4;
 
-  // LDS pool (paged_attn_lds(G) bytes, dynamic), reused in three phases:
-  // rotated queries (prologue), code tables (tile loop), wave-merge buffer
-  // (epilogue)
-  constexpr int LUTK_BYTES = CodeLut<BK>::BYTES;
+  // LDS: the code tables in static arrays; a dynamic pool
+  // (paged_attn_lds(G) bytes) reused for the rotated queries (prologue) and
+  // the wave-merge buffer (epilogue)
+  __shared__ __attribute__((aligned(16))) uint32_t lutK[CodeLut<BK>::BYTES / 4];
+  __shared__ __attribute__((aligned(16))) uint32_t lutV_own[SHARE ? 1 : CodeLut<BV>::BYTES / 4];
+  uint32_t* lutV = SHARE ? lutK : lutV_own;
   extern __shared__ __attribute__((aligned(16))) uint8_t pool[];
   __shared__ float red_m[NW][16], red_l[NW][16];
-  __shared__ uint16_t lev16[2][16];  // f16(sigma level), K / V
+  __shared__ int tile_next;  // next unclaimed tile of the workgroup's range
   __shared__ float tab_inv[2];       // 1 / (sigma (1 + rmid)), K / V
   float (*qs)[D + 4] = reinterpret_cast<float (*)[D + 4]>(pool);
   float* red_o = reinterpret_cast<float*>(pool);  // [NW waves][G heads][D + 1]
-  uint8_t* lutK = pool;
-  uint8_t* lutV = SHARE ? pool : pool + LUTK_BYTES;
 
   // tile range and the first tile's loads, issued before the prologue so that
   // their latency overlaps it
@@ -709,41 +768,39 @@ __global__ __launch_bounds__(NW * 64, NW == 16 ? 1 : (D == 128 ? (QL ? 3 : 4) : 
     btv = bt_of(tile + NW);
   }
 
-  float y[E];  // this lane's query elements, loaded before the level-table work
-  if ((tid >> 4) < G) load_elems<QT, E>(query, ((int64_t)b * hq + kvh * G + (tid >> 4)) * D + (tid & 15) * E, y);
-
-  // f16 level tables f16(sigma level) with sigma chosen to equalise the
+  // Prologue, one barrier: the query heads are rotated by the first waves
+  // (one head per 16 lanes), while the last wave sizes and builds the K code
+  // table and the one before it the V table; every wave then reads its MFMA
+  // operands of the query.
+  // Code tables hold f16(sigma level) with sigma chosen to equalise the
   // relative rounding errors; the scores and the output are divided by
-  // sigma (1 + rmid), which leaves an error of at most half the spread.
-  // Wave 0 sizes the K table, wave 1 the V table (none for a shared table:
-  // one codebook array for K and V takes the K scale).
+  // sigma (1 + rmid), which leaves an error of at most half the spread (one
+  // codebook array for K and V: one table, the K scale).
   const int wave_s = __builtin_amdgcn_readfirstlane(wave);
-  if (wave_s == 0) {
-    const TableScale t = table_scale<1 << BK>(klev, false);
-    if (lane < (1 << BK)) lev16[0][lane] = (uint16_t)f32_to_f16_bits(t.sigma * klev[lane]);
-    if (lane == 0) tab_inv[0] = 1.f / (t.sigma * (1.f + t.rmid));
-  } else if (wave_s == 1 && !SHARE) {
-    const TableScale t = table_scale<1 << BV>(vlev, false);
-    if (lane < (1 << BV)) lev16[1][lane] = (uint16_t)f32_to_f16_bits(t.sigma * vlev[lane]);
-    if (lane == 0) tab_inv[1] = 1.f / (t.sigma * (1.f + t.rmid));
-  }
-
-  // rotate the G query heads of this kv head: one head per 16 lanes
   {
     const int g = tid >> 4, l16 = tid & 15;
     if (g < G) {
-      float sg[E];
+      float y[E];
+      load_elems<QT, E>(query, ((int64_t)b * hq + kvh * G + g) * D + l16 * E, y);
 #pragma unroll
-      for (int i = 0; i < E; ++i) {
-        sg[i] = ksigns[l16 * E + i];
-        y[i] *= sg[i];
-      }
+      for (int i = 0; i < E; ++i) y[i] *= ksigns[l16 * E + i];
       fwht_lanes<E, 16>(y, l16);
       const float sc = (float)(1.0 / __builtin_sqrt((double)D)) * qscale;
 #pragma unroll
       for (int i = 0; i < E; ++i) qs[g][l16 * E + i] = y[i] * sc;
     }
   }
+  if (wave_s == NW - 1) {
+    const TableScale t = table_scale<1 << BK>(klev, false);
+    build_code_lut_wave<BK>(lutK, f32_to_f16_bits(t.sigma * klev[lane & ((1 << BK) - 1)]), lane);
+    if (lane == 0) tab_inv[0] = 1.f / (t.sigma * (1.f + t.rmid));
+  }
+  if (!SHARE && wave_s == NW - 2) {
+    const TableScale t = table_scale<1 << BV>(vlev, false);
+    build_code_lut_wave<BV>(lutV, f32_to_f16_bits(t.sigma * vlev[lane & ((1 << BV) - 1)]), lane);
+    if (lane == 0) tab_inv[1] = 1.f / (t.sigma * (1.f + t.rmid));
+  }
+  if (tid == 0) tile_next = t_begin + 2 * NW;
   __syncthreads();
 
   // B operand of the Q.K MFMAs: lane (h, q), MFMA s -> Q[h][q*D/4 + 8s + j] as
@@ -752,32 +809,38 @@ __global__ __launch_bounds__(NW * 64, NW == 16 ? 1 : (D == 128 ? (QL ? 3 : 4) : 
   const bool qrem = !QL && G <= 8;
   const float kinv = tab_inv[0];
   Op8 qb[NS], ql[QL ? NS : 1];
+  {
+    const int hh = (qrem && h >= 8) ? h - 8 : h;
+    const bool lo_col = hh != h;
 #pragma unroll
-  for (int s = 0; s < NS; ++s) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      uint32_t w = 0, wl = 0;
-      const int hh = (qrem && h >= 8) ? h - 8 : h;
+    for (int s = 0; s < NS; ++s) {
+      float x[8];
       if (hh < G) {
+        const float4 a = *reinterpret_cast<const float4*>(&qs[hh][q * (D / 4) + 8 * s]);
+        const float4 c = *reinterpret_cast<const float4*>(&qs[hh][q * (D / 4) + 8 * s + 4]);
+        x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w; x[4] = c.x; x[5] = c.y; x[6] = c.z; x[7] = c.w;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = 0.f;
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        uint32_t w = 0, wl = 0;
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
-          const float x = qs[hh][q * (D / 4) + 8 * s + 2 * j + e] * kinv;
-          const _Float16 hi = (_Float16)x;
-          const _Float16 lo = (_Float16)(x - (float)hi);
-          w |= (uint32_t)__builtin_bit_cast(uint16_t, hh == h ? hi : lo) << (16 * e);
+          const float xv = x[2 * j + e] * kinv;
+          const _Float16 hi = (_Float16)xv;
+          const _Float16 lo = (_Float16)(xv - (float)hi);
+          w |= (uint32_t)__builtin_bit_cast(uint16_t, lo_col ? lo : hi) << (16 * e);
           wl |= (uint32_t)__builtin_bit_cast(uint16_t, lo) << (16 * e);
         }
+        qb[s].u[j] = w;
+        if constexpr (QL) ql[s].u[j] = wl;
       }
-      qb[s].u[j] = w;
-      if constexpr (QL) ql[s].u[j] = wl;
     }
   }
-  __syncthreads();  // qs is dead from here on; its LDS holds the code tables
-  build_code_lut<BK>(lutK, lev16[0], tid, NW * 64);
-  if (!SHARE) build_code_lut<BV>(lutV, lev16[1], tid, NW * 64);
-  __syncthreads();
-  const uint32_t tabK = lut_lane_base<BK>(lane, lds_addr(lutK));
-  const uint32_t tabV = lut_lane_base<BV>(lane, lds_addr(lutV));
+  const uint32_t tabK = lut_lane_base<BK>(lane, 0u);  // the lane's copy offset in the table
+  const uint32_t tabV = lut_lane_base<BV>(lane, 0u);
 
 
   float m_run = -INFINITY, l_run = 0.f;
@@ -799,8 +862,8 @@ __global__ __launch_bounds__(NW * 64, NW == 16 ? 1 : (D == 128 ? (QL ? 3 : 4) : 
 #pragma unroll
       for (int st = 0; st < NS; ++st) {
         Op8 a;
-        const uint2 c01 = lut_quad<BK>(cur.k[sb], (8 * st) * BK, tabK);
-        const uint2 c23 = lut_quad<BK>(cur.k[sb], (8 * st + 4) * BK, tabK);
+        const uint2 c01 = lut_quad_s<BK>(cur.k[sb], (8 * st) * BK, tabK, lutK);
+        const uint2 c23 = lut_quad_s<BK>(cur.k[sb], (8 * st + 4) * BK, tabK, lutK);
         a.u[0] = c01.x; a.u[1] = c01.y; a.u[2] = c23.x; a.u[3] = c23.y;
         c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a.h, qb[st].h, c, 0, 0, 0);
         if constexpr (QL) c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a.h, ql[st].h, c, 0, 0, 0);
@@ -845,9 +908,10 @@ __global__ __launch_bounds__(NW * 64, NW == 16 ? 1 : (D == 128 ? (QL ? 3 : 4) : 
     for (int sb = 0; sb < 2; ++sb) {
 #pragma unroll
       for (int i2 = 0; i2 < 2; ++i2) {
-        // V norms of two tokens as f16 halves (zero for a flagged sub-block);
-        // the products are rounded straight into the two halves of the operand
-        const uint32_t vn = cur.ok[sb] ? cur.vn[sb][i2] : 0u;
+        // V norms of two tokens as f16 halves (zero for a sub-block without
+        // tokens); the products are rounded straight into the two halves of
+        // the operand
+        const uint32_t vn = cur.vn[sb][i2];
         const float p0 = __builtin_amdgcn_exp2f(s[sb][2 * i2] - m_sc);
         const float p1 = __builtin_amdgcn_exp2f(s[sb][2 * i2 + 1] - m_sc);
         pr[4 * sb + 2 * i2] = p0;
@@ -855,15 +919,14 @@ __global__ __launch_bounds__(NW * 64, NW == 16 ? 1 : (D == 128 ? (QL ? 3 : 4) : 
         pb.u[2 * sb + i2] = pv_pair(p0, p1, vn);
       }
     }
-    float psum = ((pr[0] + pr[1]) + (pr[2] + pr[3])) + ((pr[4] + pr[5]) + (pr[6] + pr[7]));
-    psum *= 512.f;
-    l_run += psum;
+    // l_run holds the sum of the pre-scaled p (the 2^(TAU+1) goes back at the end)
+    l_run += ((pr[0] + pr[1]) + (pr[2] + pr[3])) + ((pr[4] + pr[5]) + (pr[6] + pr[7]));
 #pragma unroll
     for (int bb = 0; bb < NB; ++bb) {
       Op8 a;
 #pragma unroll
       for (int sb = 0; sb < 2; ++sb) {
-        const uint2 t4 = lut_quad<BV>(cur.v[sb], (4 * bb) * BV, tabV);
+        const uint2 t4 = lut_quad_s<BV>(cur.v[sb], (4 * bb) * BV, tabV, lutV);
         a.u[2 * sb] = t4.x;
         a.u[2 * sb + 1] = t4.y;
       }
@@ -872,27 +935,43 @@ __global__ __launch_bounds__(NW * 64, NW == 16 ? 1 : (D == 128 ? (QL ? 3 : 4) : 
     if constexpr (BK <= 3 && BV <= 3) sched_lds_mfma<NB, 4>();
   };
 
-  // ping-pong over two register sets so the next tile's loads overlap this tile's math
-  // and the block-table entries one tile further ahead
-  // ping-pong over two register sets so the next tile's loads overlap this tile's math
-  // and the block-table entries one tile further ahead
+  // Tiles are handed out on demand: a wave's first two are t_begin + wave
+  // and t_begin + NW + wave, every later one is claimed from the workgroup's
+  // counter (one LDS atomic per tile) when its block-table entry is fetched,
+  // two tiles ahead of its use.  The waves of a workgroup do not progress at
+  // the same rate (the issue arbiter favours some), so with a fixed share per
+  // wave the workgroup would wait for its slowest wave; on demand they all
+  // finish within about one tile of each other.
+  auto claim = [&]() __attribute__((always_inline)) {
+    int v = 0;
+    if (lane == 0) v = atomicAdd(&tile_next, 1);
+    return __builtin_amdgcn_readfirstlane(v);
+  };
+  // ping-pong over two register sets so the next tile's loads overlap this
+  // tile's math and the block-table entries one tile further ahead
+  int tile1 = tile + NW;  // the tile whose loads go out next
   while (tile < t_end) {
-    int btn = bt_of(tile + 2 * NW);
-    load(rb, btv, tile + NW);
+    const int tile2 = claim();
+    int btn = bt_of(tile2);
+    load(rb, btv, tile1);
     btv = btn;
     process(ra, tile);
-    tile += NW;
+    tile = tile1;
+    tile1 = tile2;
     if (tile >= t_end) break;
-    btn = bt_of(tile + 2 * NW);
-    load(ra, btv, tile + NW);
+    const int tile3 = claim();
+    btn = bt_of(tile3);
+    load(ra, btv, tile1);
     btv = btn;
     process(rb, tile);
-    tile += NW;
+    tile = tile1;
+    tile1 = tile3;
   }
   // undo the P' pre-scale and the V table scale
   const float osc = 512.f * tab_inv[SHARE ? 0 : 1];
 #pragma unroll
   for (int bb = 0; bb < NB; ++bb) acc[bb] *= osc;
+  l_run *= 512.f;
 
   // ---- merge the 4 waves through LDS (the code tables' LDS is reused) ----
   __syncthreads();
