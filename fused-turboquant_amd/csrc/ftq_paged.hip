@@ -731,8 +731,26 @@ __global__ __launch_bounds__(NW * 64, NW == 16 ? 1 : (D == 128 ? (QL ? 3 : 4) : 
   float (*qs)[D + 4] = reinterpret_cast<float (*)[D + 4]>(pool);
   float* red_o = reinterpret_cast<float*>(pool);  // [NW waves][G heads][D + 1]
 
-  // tile range and the first tile's loads, issued before the prologue so that
-  // their latency overlaps it
+  // The code tables first, each sized and built by one wave (its level loads
+  // and search overlap the other waves' first loads), and the query heads'
+  // loads (one head per 16 lanes), ahead of the dependent block-table loads.
+  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+  if (wave_s == NW - 1) {
+    const TableScale t = table_scale<1 << BK>(klev, false);
+    build_code_lut_wave<BK>(lutK, f32_to_f16_bits(t.sigma * klev[lane & ((1 << BK) - 1)]), lane);
+    if (lane == 0) tab_inv[0] = 1.f / (t.sigma * (1.f + t.rmid));
+  }
+  if (!SHARE && wave_s == NW - 2) {
+    const TableScale t = table_scale<1 << BV>(vlev, false);
+    build_code_lut_wave<BV>(lutV, f32_to_f16_bits(t.sigma * vlev[lane & ((1 << BV) - 1)]), lane);
+    if (lane == 0) tab_inv[1] = 1.f / (t.sigma * (1.f + t.rmid));
+  }
+  const int qg = tid >> 4, ql16 = tid & 15;
+  float y[E];
+  if (qg < G) load_elems<QT, E>(query, ((int64_t)b * hq + kvh * G + qg) * D + ql16 * E, y);
+
+  // tile range and the first tile's loads, issued before the rest of the
+  // prologue so that their latency overlaps it
   const int seq_len = seq_lens[b];
   const int n_tiles = (seq_len + 31) >> 5;
   const int tps = (n_tiles + num_splits - 1) / num_splits;
@@ -769,36 +787,21 @@ __global__ __launch_bounds__(NW * 64, NW == 16 ? 1 : (D == 128 ? (QL ? 3 : 4) : 
   }
 
   // Prologue, one barrier: the query heads are rotated by the first waves
-  // (one head per 16 lanes), while the last wave sizes and builds the K code
-  // table and the one before it the V table; every wave then reads its MFMA
-  // operands of the query.
-  // Code tables hold f16(sigma level) with sigma chosen to equalise the
-  // relative rounding errors; the scores and the output are divided by
-  // sigma (1 + rmid), which leaves an error of at most half the spread (one
-  // codebook array for K and V: one table, the K scale).
-  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+  // (one head per 16 lanes); the last wave has built the K code table and
+  // the one before it the V table; every wave then reads its MFMA operands of
+  // the query.  Code tables hold f16(sigma level) with sigma chosen to
+  // equalise the relative rounding errors; the scores and the output are
+  // divided by sigma (1 + rmid), which leaves an error of at most half the
+  // spread (one codebook array for K and V: one table, the K scale).
   {
-    const int g = tid >> 4, l16 = tid & 15;
-    if (g < G) {
-      float y[E];
-      load_elems<QT, E>(query, ((int64_t)b * hq + kvh * G + g) * D + l16 * E, y);
+    if (qg < G) {
 #pragma unroll
-      for (int i = 0; i < E; ++i) y[i] *= ksigns[l16 * E + i];
-      fwht_lanes<E, 16>(y, l16);
+      for (int i = 0; i < E; ++i) y[i] *= ksigns[ql16 * E + i];
+      fwht_lanes<E, 16>(y, ql16);
       const float sc = (float)(1.0 / __builtin_sqrt((double)D)) * qscale;
 #pragma unroll
-      for (int i = 0; i < E; ++i) qs[g][l16 * E + i] = y[i] * sc;
+      for (int i = 0; i < E; ++i) qs[qg][ql16 * E + i] = y[i] * sc;
     }
-  }
-  if (wave_s == NW - 1) {
-    const TableScale t = table_scale<1 << BK>(klev, false);
-    build_code_lut_wave<BK>(lutK, f32_to_f16_bits(t.sigma * klev[lane & ((1 << BK) - 1)]), lane);
-    if (lane == 0) tab_inv[0] = 1.f / (t.sigma * (1.f + t.rmid));
-  }
-  if (!SHARE && wave_s == NW - 2) {
-    const TableScale t = table_scale<1 << BV>(vlev, false);
-    build_code_lut_wave<BV>(lutV, f32_to_f16_bits(t.sigma * vlev[lane & ((1 << BV) - 1)]), lane);
-    if (lane == 0) tab_inv[1] = 1.f / (t.sigma * (1.f + t.rmid));
   }
   if (tid == 0) tile_next = t_begin + 2 * NW;
   __syncthreads();
