@@ -44,6 +44,64 @@ __device__ __forceinline__ uint32_t field_off(const uint32_t (&w)[N], int P, int
   return (w[0] << (SH - P)) & m;
 }
 
+// Byte offset, inside a code table, of the entry whose index is bits
+// [P, P + W) of the code words, ORed with the lane's copy offset (< 2^SH):
+// one funnel shift that puts the field at bit SH and one v_and_or_b32, as
+// plain arithmetic the compiler schedules itself.  With the table in static
+// LDS its address folds into the DS instruction's offset field.
+template <int SH, int W, int N>
+__device__ __forceinline__ uint32_t lut_field(const uint32_t (&w)[N], int P, uint32_t laneoff) {
+  constexpr uint32_t M = ((1u << W) - 1u) << SH;
+  uint32_t v;
+  if (P >= SH) {
+    const int Q = P - SH, i = Q >> 5, o = Q & 31;  // compile-time after unrolling
+    v = (o + W + SH > 32 && i + 1 < N) ? __builtin_amdgcn_alignbit(w[i + 1], w[i], o) : (w[i] >> o);
+  } else {
+    v = w[0] << (SH - P);
+  }
+  return (v & M) | laneoff;
+}
+
+// dword at byte offset off of a table in static LDS
+__device__ __forceinline__ uint32_t lds_dword_at(const uint32_t* table, uint32_t off) {
+  typedef __attribute__((address_space(3))) const uint8_t lds_u8;
+  lds_u8* t = (lds_u8*)(__attribute__((address_space(3))) const void*)table;
+  return *(__attribute__((address_space(3))) const uint32_t*)(t + off);
+}
+
+// A pair table built by one wave: entry e = h[e & (2^B - 1)] | h[e >> B] << 16,
+// where lane i < 2^B holds the f16 bits h[i] (the other lanes' values are not
+// read), stored in 2^LOGC consecutive copies (lane l of a reader takes copy
+// l % 2^LOGC).  Each lane assembles its entries with two lane reads (every
+// lane takes part) and writes their copies, 4 per ds_write_b128.
+template <int B, int LOGC>
+__device__ __forceinline__ void build_pair_table_wave(uint32_t* lut, uint32_t hbits, int lane) {
+  constexpr int NL = 1 << B, ENTRIES = 1 << (2 * B), COPIES = 1 << LOGC;
+  constexpr int PER = (ENTRIES + 63) / 64;  // entries per lane
+  uint32_t v[PER];
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const int e = lane + 64 * k;
+    const uint32_t lo = (uint32_t)__shfl((int)hbits, e & (NL - 1));
+    const uint32_t hi = (uint32_t)__shfl((int)hbits, (e >> B) & (NL - 1));
+    v[k] = (lo & 0xffffu) | (hi << 16);
+  }
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const int e = lane + 64 * k;
+    if (e < ENTRIES) {
+      if constexpr (COPIES >= 4) {
+        uint4* dst = reinterpret_cast<uint4*>(lut + e * COPIES);
+#pragma unroll
+        for (int c = 0; c < COPIES / 4; ++c) dst[c] = make_uint4(v[k], v[k], v[k], v[k]);
+      } else {
+#pragma unroll
+        for (int c = 0; c < COPIES; ++c) lut[e * COPIES + c] = v[k];
+      }
+    }
+  }
+}
+
 // Reductions over the four lanes l, l ^ 16, l ^ 32, l ^ 48 (the 16-lane rows):
 // v_permlane16_swap (x, x) leaves rows (0, 0, 2, 2) in one result and
 // (1, 1, 3, 3) in the other, v_permlane32_swap pairs row r with row r ^ 2.

@@ -428,38 +428,6 @@ __device__ void build_code_lut(uint8_t* lut, const uint16_t* single, int tid, in
   }
 }
 
-// The same table built by one wave from the f16 bits of the 2^B levels
-// (lane i < 2^B holds level i; the other lanes' values are not read): each
-// lane assembles its entries' pairs with two lane reads and writes their
-// copies, 4 per ds_write_b128 for the 32-copy tables.
-template <int B>
-__device__ __forceinline__ void build_code_lut_wave(uint32_t* lut, uint32_t lev_bits, int lane) {
-  using C = CodeLut<B>;
-  constexpr int NL = 1 << B;
-  constexpr int PER = (C::ENTRIES + 63) / 64;  // entries per lane
-  uint32_t v[PER];
-#pragma unroll
-  for (int k = 0; k < PER; ++k) {
-    const int e = lane + 64 * k;  // every lane takes part in the lane reads
-    const uint32_t lo = (uint32_t)__shfl((int)lev_bits, e & (NL - 1));
-    const uint32_t hi = (uint32_t)__shfl((int)lev_bits, (e >> B) & (NL - 1));
-    v[k] = (lo & 0xffffu) | (hi << 16);
-  }
-#pragma unroll
-  for (int k = 0; k < PER; ++k) {
-    const int e = lane + 64 * k;
-    if (e < C::ENTRIES) {
-      if constexpr (C::COPIES == 32) {
-        uint4* dst = reinterpret_cast<uint4*>(lut + e * 32);
-#pragma unroll
-        for (int c = 0; c < 8; ++c) dst[c] = make_uint4(v[k], v[k], v[k], v[k]);
-      } else {
-        lut[e] = v[k];
-      }
-    }
-  }
-}
-
 typedef __attribute__((address_space(3))) const uint32_t lds_u32;
 
 // LDS address of this lane's copy of a code table
@@ -497,33 +465,14 @@ __device__ __forceinline__ uint2 lut_quad(const uint32_t (&w)[N], int P, uint32_
   return make_uint2(lo, hi);
 }
 
-// Byte offset, inside a table, of the entry whose index is bits [P, P + W)
-// of the code words, ORed with the lane's copy offset (< 2^SH): one funnel
-// shift that puts the field at bit SH and one v_and_or_b32, as plain
-// arithmetic the compiler schedules itself (no inline asm).
-template <int SH, int W, int N>
-__device__ __forceinline__ uint32_t lut_field(const uint32_t (&w)[N], int P, uint32_t laneoff) {
-  constexpr uint32_t M = ((1u << W) - 1u) << SH;
-  uint32_t v;
-  if (P >= SH) {
-    const int Q = P - SH, i = Q >> 5, o = Q & 31;  // compile-time after unrolling
-    v = (o + W + SH > 32 && i + 1 < N) ? __builtin_amdgcn_alignbit(w[i + 1], w[i], o) : (w[i] >> o);
-  } else {
-    v = w[0] << (SH - P);
-  }
-  return (v & M) | laneoff;
-}
-
 // lut_quad over a table in static LDS (its address a link-time constant the
 // compiler folds into the DS instructions' offset field)
 template <int B, int N>
 __device__ __forceinline__ uint2 lut_quad_s(const uint32_t (&w)[N], int P, uint32_t laneoff, const uint32_t* table) {
   using C = CodeLut<B>;
   constexpr int SH = 2 + C::LOG_COPIES;
-  typedef __attribute__((address_space(3))) const uint8_t lds_u8;
-  lds_u8* t = (lds_u8*)(__attribute__((address_space(3))) const void*)table;
-  const uint32_t lo = *(lds_u32*)(t + lut_field<SH, C::IDX_BITS>(w, P, laneoff));
-  const uint32_t hi = *(lds_u32*)(t + lut_field<SH, C::IDX_BITS>(w, P + 2 * B, laneoff));
+  const uint32_t lo = lds_dword_at(table, lut_field<SH, C::IDX_BITS>(w, P, laneoff));
+  const uint32_t hi = lds_dword_at(table, lut_field<SH, C::IDX_BITS>(w, P + 2 * B, laneoff));
   return make_uint2(lo, hi);
 }
 
@@ -602,6 +551,22 @@ __device__ __forceinline__ int fetch_bt(__amdgpu_buffer_rsrc_t bt_rs, int tile, 
   return ok ? v : -1;
 }
 
+// The same two entries as wave-uniform scalar loads (no vector registers, no
+// lane reads); the branch keeps the loads inside the table row.
+struct BtPair {
+  int e[2];
+};
+__device__ __forceinline__ BtPair fetch_bt_s(const int32_t* __restrict__ bt_row, int tile, bool active,
+                                             int seq_subs, const SubDiv& sd) {
+  BtPair r;
+#pragma unroll
+  for (int sb = 0; sb < 2; ++sb) {
+    const int j = 2 * tile + sb;
+    r.e[sb] = (active && j < seq_subs && j < sd.j_cap) ? bt_row[sd.page(j)] : -1;
+  }
+  return r;
+}
+
 // dwords [I, NDW) at lane offset voff of a buffer, as 16/12/8/4-byte loads
 template <int I = 0, int NDW>
 __device__ __forceinline__ void buf_dwords(__amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t (&w)[NDW]) {
@@ -632,7 +597,7 @@ struct TileOff {
 // (its base; the byte range ends with the sub-block, so no lane reads past it)
 // plus the lane offsets.
 template <int D, int BK, int BV>
-__device__ __forceinline__ void load_tile(TileRegs<D, BK, BV>& r, const uint8_t* __restrict__ cache, int btv,
+__device__ __forceinline__ void load_tile(TileRegs<D, BK, BV>& r, const uint8_t* __restrict__ cache, BtPair bt,
                                           int tile, const SubDiv& sd, int64_t blk_stride, int64_t kvh_off,
                                           int nb32, const TileOff& lo) {
   using Gm = PagedGeom<D, BK, BV>;
@@ -643,7 +608,7 @@ __device__ __forceinline__ void load_tile(TileRegs<D, BK, BV>& r, const uint8_t*
     // 0 at block 0: the loads still issue (the wait counts stay static) and
     // return zeros, so its V norms are 0 and it adds nothing to P.V; past
     // seq_len its scores are masked to -inf by the consumer.
-    int phys = __builtin_amdgcn_readlane(btv, sb);
+    int phys = bt.e[sb];
     const bool valid = (uint32_t)phys < (uint32_t)nb32;  // -1 (no entry) and ids >= num_blocks fail
     const int j = 2 * tile + sb;
     const int sub = valid ? j - sd.page(j) * sd.nsub : 0;
@@ -726,7 +691,6 @@ __global__ __launch_bounds__(NW * 64, NW == 16 ? 1 : (D == 128 ? (QL ? 3 : 4) : 
   uint32_t* lutV = SHARE ? lutK : lutV_own;
   extern __shared__ __attribute__((aligned(16))) uint8_t pool[];
   __shared__ float red_m[NW][16], red_l[NW][16];
-  __shared__ int tile_next;  // next unclaimed tile of the workgroup's range
   __shared__ float tab_inv[2];       // 1 / (sigma (1 + rmid)), K / V
   float (*qs)[D + 4] = reinterpret_cast<float (*)[D + 4]>(pool);
   float* red_o = reinterpret_cast<float*>(pool);  // [NW waves][G heads][D + 1]
@@ -737,12 +701,12 @@ __global__ __launch_bounds__(NW * 64, NW == 16 ? 1 : (D == 128 ? (QL ? 3 : 4) : 
   const int wave_s = __builtin_amdgcn_readfirstlane(wave);
   if (wave_s == NW - 1) {
     const TableScale t = table_scale<1 << BK>(klev, false);
-    build_code_lut_wave<BK>(lutK, f32_to_f16_bits(t.sigma * klev[lane & ((1 << BK) - 1)]), lane);
+    build_pair_table_wave<BK, CodeLut<BK>::LOG_COPIES>(lutK, f32_to_f16_bits(t.sigma * klev[lane & ((1 << BK) - 1)]), lane);
     if (lane == 0) tab_inv[0] = 1.f / (t.sigma * (1.f + t.rmid));
   }
   if (!SHARE && wave_s == NW - 2) {
     const TableScale t = table_scale<1 << BV>(vlev, false);
-    build_code_lut_wave<BV>(lutV, f32_to_f16_bits(t.sigma * vlev[lane & ((1 << BV) - 1)]), lane);
+    build_pair_table_wave<BV, CodeLut<BV>::LOG_COPIES>(lutV, f32_to_f16_bits(t.sigma * vlev[lane & ((1 << BV) - 1)]), lane);
     if (lane == 0) tab_inv[1] = 1.f / (t.sigma * (1.f + t.rmid));
   }
   const int qg = tid >> 4, ql16 = tid & 15;
@@ -764,23 +728,19 @@ __global__ __launch_bounds__(NW * 64, NW == 16 ? 1 : (D == 128 ? (QL ? 3 : 4) : 
   const int nb32 = (int)min(num_blocks, (int64_t)0x7fffffff);
   const int64_t blk_stride = (int64_t)hkv * sd.nsub * Gm::SUB;
   const int64_t kvh_off = (int64_t)kvh * sd.nsub * Gm::SUB;
-  const __amdgpu_buffer_rsrc_t bt_rs = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<int32_t*>(block_table + (int64_t)b * max_blocks), (short)0,
-      (int)min((int64_t)max_blocks * 4, (int64_t)0x7ffffffc), 0x00020000);
+  const int32_t* bt_row = block_table + (int64_t)b * max_blocks;
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);  // wave-uniform -> scalar tile math
   TileRegs<D, BK, BV> ra, rb;
   int tile = t_begin + wave_u;
-  auto bt_of = [&](int t) __attribute__((always_inline)) {
-    return fetch_bt(bt_rs, t, t < t_end, seq_subs, sd, (uint32_t)lane);
-  };
+  auto bt_of = [&](int t) __attribute__((always_inline)) { return fetch_bt_s(bt_row, t, t < t_end, seq_subs, sd); };
   TileOff lo;
   lo.k = (uint32_t)h * Gm::KTOK + (uint32_t)q * Gm::KLANE;
   lo.v = (uint32_t)Gm::KSEC + (uint32_t)lane * Gm::VLANE;
   lo.n = (uint32_t)Gm::KNORM + (uint32_t)q * 8u;
-  auto load = [&](TileRegs<D, BK, BV>& r, int btv, int t) __attribute__((always_inline)) {
-    load_tile(r, cache, btv, t, sd, blk_stride, kvh_off, nb32, lo);
+  auto load = [&](TileRegs<D, BK, BV>& r, BtPair bt, int t) __attribute__((always_inline)) {
+    load_tile(r, cache, bt, t, sd, blk_stride, kvh_off, nb32, lo);
   };
-  int btv = 0;
+  BtPair btv{{-1, -1}};
   if (tile < t_end) {
     load(ra, bt_of(tile), tile);
     btv = bt_of(tile + NW);
@@ -803,7 +763,6 @@ __global__ __launch_bounds__(NW * 64, NW == 16 ? 1 : (D == 128 ? (QL ? 3 : 4) : 
       for (int i = 0; i < E; ++i) qs[qg][ql16 * E + i] = y[i] * sc;
     }
   }
-  if (tid == 0) tile_next = t_begin + 2 * NW;
   __syncthreads();
 
   // B operand of the Q.K MFMAs: lane (h, q), MFMA s -> Q[h][q*D/4 + 8s + j] as
@@ -938,31 +897,21 @@ __global__ __launch_bounds__(NW * 64, NW == 16 ? 1 : (D == 128 ? (QL ? 3 : 4) : 
     if constexpr (BK <= 3 && BV <= 3) sched_lds_mfma<NB, 4>();
   };
 
-  // Tiles are handed out on demand: a wave's first two are t_begin + wave
-  // and t_begin + NW + wave, every later one is claimed from the workgroup's
-  // counter (one LDS atomic per tile) when its block-table entry is fetched,
-  // two tiles ahead of its use.  The waves of a workgroup do not progress at
-  // the same rate (the issue arbiter favours some), so with a fixed share per
-  // wave the workgroup would wait for its slowest wave; on demand they all
-  // finish within about one tile of each other.
-  auto claim = [&]() __attribute__((always_inline)) {
-    int v = 0;
-    if (lane == 0) v = atomicAdd(&tile_next, 1);
-    return __builtin_amdgcn_readfirstlane(v);
-  };
   // ping-pong over two register sets so the next tile's loads overlap this
-  // tile's math and the block-table entries one tile further ahead
+  // tile's math and the block-table entries one tile further ahead.  Each
+  // wave takes every NW-th tile: a fixed assignment, so the sums (and the
+  // output bits) do not depend on how fast the waves progress.
   int tile1 = tile + NW;  // the tile whose loads go out next
   while (tile < t_end) {
-    const int tile2 = claim();
-    int btn = bt_of(tile2);
+    const int tile2 = tile1 + NW;
+    BtPair btn = bt_of(tile2);
     load(rb, btv, tile1);
     btv = btn;
     process(ra, tile);
     tile = tile1;
     tile1 = tile2;
     if (tile >= t_end) break;
-    const int tile3 = claim();
+    const int tile3 = tile1 + NW;
     btn = bt_of(tile3);
     load(ra, btv, tile1);
     btv = btn;
@@ -1313,18 +1262,23 @@ __global__ __launch_bounds__(256, 2) void paged_attn_valu_kernel(
     __asm__ volatile("" ::: "memory");
   };
 
+  int tile1 = tile + NW;  // the tile whose loads go out next
   while (tile < t_end) {
-    int btn = bt_of(tile + 2 * NW);
-    load(rb, btv, tile + NW);
+    const int tile2 = tile1 + NW;
+    int btn = bt_of(tile2);
+    load(rb, btv, tile1);
     btv = btn;
     process(ra, tile);
-    tile += NW;
+    tile = tile1;
+    tile1 = tile2;
     if (tile >= t_end) break;
-    btn = bt_of(tile + 2 * NW);
-    load(ra, btv, tile + NW);
+    const int tile3 = tile1 + NW;
+    btn = bt_of(tile3);
+    load(ra, btv, tile1);
     btv = btn;
     process(rb, tile);
-    tile += NW;
+    tile = tile1;
+    tile1 = tile3;
   }
 
   // ---- wave totals, then the 4 waves merged through LDS ----

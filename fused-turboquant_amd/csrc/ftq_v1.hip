@@ -390,79 +390,50 @@ __global__ __launch_bounds__(256, 2) void v1_attn_kernel(
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int m = lane & 15, g = lane >> 4;
 
-  // LDS pool, reused in three phases: rotated queries (prologue), the K code
-  // pair table (tile loop), the wave-merge buffer (epilogue)
   // K pair table: entry e = f16(sigma c[e & mask]) | f16(sigma c[e >> KB]) << 16, in LUT_C
   // interleaved copies (lane l reads copy l % LUT_C), so the random lookups of
-  // a 32-lane LDS phase spread over the banks
+  // a 32-lane LDS phase spread over the banks.  Static, so its address folds
+  // into the lookups' DS offsets; a separate pool holds the rotated queries
+  // (prologue) and the wave-merge buffer (epilogue).
   constexpr int LUT_LOGC = 5;
   constexpr int LUT_BYTES = (4 << (2 * KB)) << LUT_LOGC;
   constexpr int RED_BYTES = 4 * 16 * (D + 1) * 4;
   constexpr int QS_BYTES = 16 * (D + 4) * 4;
-  constexpr int POOL0 = LUT_BYTES > RED_BYTES ? LUT_BYTES : RED_BYTES;
-  constexpr int POOL = POOL0 > QS_BYTES ? POOL0 : QS_BYTES;
+  constexpr int POOL = RED_BYTES > QS_BYTES ? RED_BYTES : QS_BYTES;
+  __shared__ __attribute__((aligned(16))) uint32_t lut[LUT_BYTES / 4];
   __shared__ __attribute__((aligned(16))) uint8_t pool[POOL];
   __shared__ float red_m[4][16], red_l[4][16];
   __shared__ __attribute__((aligned(16))) uint16_t tail_l[4][2][4][16];
   __shared__ __attribute__((aligned(16))) float diag_l[4][2][16];
-  __shared__ float centl[16];
+  __shared__ float tab_sc;   // sigma of the pair tables
   static_assert(!VLM || VB == 4, "Lloyd-Max V needs the 4-bit V layout");
   __shared__ uint2 lutv[VLM ? 256 : 1];  // Lloyd-Max V: centroid pairs (c[e & 15], c[e >> 4]), hi and lo
   __shared__ float diagv_l[VLM ? 4 : 1][2][16];   // Lloyd-Max V: sum c^2 per token
   float (*qs)[D + 4] = reinterpret_cast<float (*)[D + 4]>(pool);
   float (*red_o)[16][D + 1] = reinterpret_cast<float (*)[16][D + 1]>(pool);
-  uint8_t* lut = pool;
-  const uint8_t* lutl = pool + 4 * (lane & ((1 << LUT_LOGC) - 1));  // this lane's copy of the K pair table
+  const uint32_t laneoff = 4u * (uint32_t)(lane & ((1 << LUT_LOGC) - 1));  // this lane's copy of the table
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
 
-  if (tid < (1 << KB)) centl[tid] = cent[tid];
-  // q_rot = q H / sqrt(D) for the G query heads of this kv head (one per 16 lanes),
-  // with scale * log2(e) folded in
-  {
-    const int gg = tid >> 4, l16 = tid & 15;
-    if (gg < G) {
-      float y[E];
-      load_elems<QT, E>(query, ((int64_t)b * hq + kvh * G + gg) * D + l16 * E, y);
-      if (rot != nullptr) rot_matrix_lanes<D, E>(y, rot, &qs[gg][0], l16);  // q M (matrix strategies)
-      else fwht_lanes<E, 16>(y, l16);
+  // Prologue, one barrier.  The last wave sizes and builds the pair tables;
+  // the query heads' loads go out ahead of the dependent block-table loads,
+  // and the first waves rotate them (one head per 16 lanes) once the first
+  // tile's loads are out: q_rot = q H / sqrt(D), scale * log2(e) folded in.
+  if (wave_u == 3) {
+    const float csc = table_scale<1 << KB>(cent, true).sigma;
+    build_pair_table_wave<KB, LUT_LOGC>(lut, f32_to_f16_bits(csc * cent[lane & ((1 << KB) - 1)]), lane);
+    if constexpr (VLM) {
+      constexpr int NC = 1 << KB;  // codes >= NC do not occur; they read the top centroid
 #pragma unroll
-      for (int i = 0; i < E; ++i) qs[gg][l16 * E + i] = y[i] * qscale;
-    }
-  }
-  __syncthreads();
-  // B operand of the Q.K MFMAs (f16 hi + lo): lane (n, g), MFMA s -> Q[n][g*D/4 + 8s + j]
-  Op8 qb[NS], ql[NS];
-#pragma unroll
-  for (int s = 0; s < NS; ++s) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      uint32_t wh = 0, wl = 0;
-      if (m < G) {
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-          const float x = qs[m][g * (D / 4) + 8 * s + 2 * j + e];
-          const _Float16 hi = (_Float16)x;
-          const _Float16 lo = (_Float16)(x - (float)hi);
-          wh |= (uint32_t)__builtin_bit_cast(uint16_t, hi) << (16 * e);
-          wl |= (uint32_t)__builtin_bit_cast(uint16_t, lo) << (16 * e);
-        }
+      for (int k = 0; k < 4; ++k) {
+        const int e = lane + 64 * k, c0 = e & 15, c1 = e >> 4;
+        lutv[e] = cent_hilo_pair(csc * cent[c0 < NC ? c0 : NC - 1], csc * cent[c1 < NC ? c1 : NC - 1]);
       }
-      qb[s].u[j] = wh;
-      ql[s].u[j] = wl;
     }
+    if (lane == 0) tab_sc = csc;
   }
-  __syncthreads();  // qs is dead; its LDS now holds the pair table
-  const float csc = table_scale<1 << KB>(cent, true).sigma;
-  const float vk = csc * (1.f / 256.f), vinv = 256.f / csc;  // Lloyd-Max V: P' scale and its inverse
-  for (int k = tid; k < ((1 << (2 * KB)) << LUT_LOGC); k += 256) {
-    const int e = k >> LUT_LOGC;
-    reinterpret_cast<uint32_t*>(lut)[k] = cent_hilo_pair(csc * centl[e & ((1 << KB) - 1)], csc * centl[e >> KB]).x;
-  }
-  if constexpr (VLM) {
-    constexpr int NC = 1 << KB;  // codes >= NC do not occur; they read the top centroid
-    const int c0 = tid & 15, c1 = tid >> 4;
-    lutv[tid] = cent_hilo_pair(csc * centl[c0 < NC ? c0 : NC - 1], csc * centl[c1 < NC ? c1 : NC - 1]);
-  }
-  __syncthreads();
+  const int qg = tid >> 4, ql16 = tid & 15;
+  float y[E];
+  if (qg < G) load_elems<QT, E>(query, ((int64_t)b * hq + kvh * G + qg) * D + ql16 * E, y);
 
   const int seq_len = seq_lens[b];
   int k0 = kv_start ? kv_start[b] : 0;
@@ -475,7 +446,6 @@ __global__ __launch_bounds__(256, 2) void v1_attn_kernel(
   const int t_end = min(t_begin + tps, t_last);
   const int32_t* bt_row = block_table + (int64_t)b * max_blocks;
   const int64_t kvh_off = (int64_t)kvh * s_head;
-  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
 
   // lane offsets (fixed for the kernel)
   V1Addr ad;
@@ -498,6 +468,54 @@ __global__ __launch_bounds__(256, 2) void v1_attn_kernel(
   const uint32_t sel0 = o3 | ((o3 + 1) << 8) | ((o3 + 4) << 16) | ((o3 + 5) << 24);
   const uint32_t sel1 = (o3 + 1) | ((o3 + 2) << 8) | ((o3 + 5) << 16) | ((o3 + 6) << 24);
 
+  // the first tile's loads (two register sets: the next tile's loads overlap
+  // this tile's math, and the block-table entries come one tile further ahead)
+  V1Tile<D, KB, VB> ra, rb;
+  int tile = t_begin + wave_u;
+  int btv = 0;
+  if (tile < t_end) {
+    v1_load<D, KB, VB, VLM>(ra, ad, tile, v1_fetch_bt(ad, tile, true, lane));
+    btv = v1_fetch_bt(ad, tile + 4, tile + 4 < t_end, lane);
+  }
+
+  if (qg < G) {
+    if (rot != nullptr) rot_matrix_lanes<D, E>(y, rot, &qs[qg][0], ql16);  // q M (matrix strategies)
+    else fwht_lanes<E, 16>(y, ql16);
+#pragma unroll
+    for (int i = 0; i < E; ++i) qs[qg][ql16 * E + i] = y[i] * qscale;
+  }
+  __syncthreads();
+  const float csc = tab_sc;
+  const float vk = csc * (1.f / 256.f), vinv = 256.f / csc;  // Lloyd-Max V: P' scale and its inverse
+  // B operand of the Q.K MFMAs (f16 hi + lo): lane (n, g), MFMA s -> Q[n][g*D/4 + 8s + j]
+  Op8 qb[NS], ql[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    float x[8];
+    if (m < G) {
+      const float4 a4 = *reinterpret_cast<const float4*>(&qs[m][g * (D / 4) + 8 * s]);
+      const float4 c4 = *reinterpret_cast<const float4*>(&qs[m][g * (D / 4) + 8 * s + 4]);
+      x[0] = a4.x; x[1] = a4.y; x[2] = a4.z; x[3] = a4.w; x[4] = c4.x; x[5] = c4.y; x[6] = c4.z; x[7] = c4.w;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = 0.f;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      uint32_t wh = 0, wl = 0;
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const float xv = x[2 * j + e];
+        const _Float16 hi = (_Float16)xv;
+        const _Float16 lo = (_Float16)(xv - (float)hi);
+        wh |= (uint32_t)__builtin_bit_cast(uint16_t, hi) << (16 * e);
+        wl |= (uint32_t)__builtin_bit_cast(uint16_t, lo) << (16 * e);
+      }
+      qb[s].u[j] = wh;
+      ql[s].u[j] = wl;
+    }
+  }
+
   float m_run = -INFINITY, l_run = 0.f, z_run = 0.f, u_run = 0.f;
   floatx4 acc[NB];
 #pragma unroll
@@ -519,7 +537,7 @@ __global__ __launch_bounds__(256, 2) void v1_attn_kernel(
         Op8 a;
 #pragma unroll
         for (int p = 0; p < 4; ++p)
-          a.u[p] = *reinterpret_cast<const uint32_t*>(lutl + field_off<2 + LUT_LOGC>(cur.k[st], (8 * s + 2 * p) * KB, 2 * KB));
+          a.u[p] = lds_dword_at(lut, lut_field<2 + LUT_LOGC, 2 * KB>(cur.k[st], (8 * s + 2 * p) * KB, laneoff));
         sacc[st] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a.h, qb[s].h, sacc[st], 0, 0, 0);
         sacc[st] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a.h, ql[s].h, sacc[st], 0, 0, 0);
         gacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a.h, a.h, gacc, 0, 0, 0);
@@ -699,15 +717,8 @@ __global__ __launch_bounds__(256, 2) void v1_attn_kernel(
     }
   };
 
-  // two register sets: the next tile's loads overlap this tile's math, and
-  // the block-table entries come one tile further ahead
-  V1Tile<D, KB, VB> ra, rb;
-  int tile = t_begin + wave_u;
-  int btv = 0;
-  if (tile < t_end) {
-    v1_load<D, KB, VB, VLM>(ra, ad, tile, v1_fetch_bt(ad, tile, true, lane));
-    btv = v1_fetch_bt(ad, tile + 4, tile + 4 < t_end, lane);
-  }
+  // each wave takes every 4th tile (a fixed assignment, so the sums and the
+  // output bits do not depend on how fast the waves progress)
   while (tile < t_end) {
     int btn = v1_fetch_bt(ad, tile + 8, tile + 8 < t_end, lane);
     v1_load<D, KB, VB, VLM>(rb, ad, tile + 4, btv);
@@ -722,7 +733,7 @@ __global__ __launch_bounds__(256, 2) void v1_attn_kernel(
     tile += 4;
   }
 
-  // ---- merge the 4 waves through LDS (the pair table's LDS is reused) ----
+  // ---- merge the 4 waves through LDS (the pool of the rotated queries) ----
   __syncthreads();
   const float l_tot = warp_sum_q(l_run);
   const float z_tot = warp_sum_q(z_run);
@@ -803,67 +814,36 @@ __global__ __launch_bounds__(256, VB == 2 ? 4 : 2) void v1_attn_g4_kernel(
 
   // K pair table in LUT_C interleaved copies (lane l reads copy l % LUT_C):
   // 32 for 2- and 3-bit keys; 16 for 4-bit (16 KB, so that 4 workgroups still
-  // fit a CU's LDS)
+  // fit a CU's LDS).  Static, so its address folds into the lookups' DS
+  // offsets; a separate pool holds the rotated queries (prologue) and the
+  // wave-merge buffer (epilogue).
   constexpr int LUT_LOGC = KB == 4 ? 4 : 5;
   constexpr int LUT_BYTES = (4 << (2 * KB)) << LUT_LOGC;
   constexpr int RED_BYTES = 4 * G * (D + 1) * 4;
   constexpr int QS_BYTES = G * (D + 4) * 4;
-  constexpr int POOL0 = LUT_BYTES > RED_BYTES ? LUT_BYTES : RED_BYTES;
-  constexpr int POOL = POOL0 > QS_BYTES ? POOL0 : QS_BYTES;
+  constexpr int POOL = RED_BYTES > QS_BYTES ? RED_BYTES : QS_BYTES;
+  __shared__ __attribute__((aligned(16))) uint32_t lut[LUT_BYTES / 4];
   __shared__ __attribute__((aligned(16))) uint8_t pool[POOL];
   __shared__ float red_m[4][G], red_l[4][G];
   __shared__ __attribute__((aligned(16))) uint16_t tail_l[4][2][4][16];  // [wave][S-tile][field][token]
   __shared__ __attribute__((aligned(16))) float diag_l[4][2][64][4];  // [wave][S-tile][lane][register]
-  __shared__ float centl[16];
   float (*qs)[D + 4] = reinterpret_cast<float (*)[D + 4]>(pool);
   float (*red_o)[G][D + 1] = reinterpret_cast<float (*)[G][D + 1]>(pool);
-  uint8_t* lut = pool;
-  const uint8_t* lutl = pool + 4 * (lane & ((1 << LUT_LOGC) - 1));  // this lane's copy of the K pair table
+  const uint32_t laneoff = 4u * (uint32_t)(lane & ((1 << LUT_LOGC) - 1));  // this lane's copy of the table
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
 
-  if (tid < (1 << KB)) centl[tid] = cent[tid];
-  {
-    const int gg = tid >> 4, l16 = tid & 15;
-    if (gg < G) {
-      float y[E];
-      load_elems<QT, E>(query, ((int64_t)b * hq + kvh * G + gg) * D + l16 * E, y);
-      if (rot != nullptr) rot_matrix_lanes<D, E>(y, rot, &qs[gg][0], l16);  // q M (matrix strategies)
-      else fwht_lanes<E, 16>(y, l16);
-#pragma unroll
-      for (int i = 0; i < E; ++i) qs[gg][l16 * E + i] = y[i] * qscale;
-    }
-  }
-  __syncthreads();
-  // B operand of the Q.K MFMAs: column n < G holds f16(q) of head n, column
-  // G + n its remainder q - f16(q); the two score columns are summed after the
-  // K loop, so q enters in about fp32 precision at no extra MFMA
-  Op8 qb[NS];
-#pragma unroll
-  for (int s = 0; s < NS; ++s) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      uint32_t w = 0;
-      if (m < 2 * G) {
-        const int h = m < G ? m : m - G;
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-          const float x = qs[h][g * (D / 4) + 8 * s + 2 * j + e];
-          const _Float16 hi = (_Float16)x;
-          const _Float16 v = m < G ? hi : (_Float16)(x - (float)hi);
-          w |= (uint32_t)__builtin_bit_cast(uint16_t, v) << (16 * e);
-        }
-      }
-      qb[s].u[j] = w;
-    }
-  }
-  __syncthreads();
-  {
+  // Prologue, one barrier.  The last wave sizes and builds the K pair table
+  // (f16(sigma c), sigma from table_scale; the norm correction divides by the
+  // norm of the same f16 values, so sigma cancels); the query heads' loads go
+  // out ahead of the dependent block-table loads, and wave 0 rotates them
+  // (one head per 16 lanes) once the first tile's loads are out.
+  if (wave_u == 3) {
     const float csc = table_scale<1 << KB>(cent, true).sigma;
-    for (int k = tid; k < ((1 << (2 * KB)) << LUT_LOGC); k += 256) {
-      const int e = k >> LUT_LOGC;
-      reinterpret_cast<uint32_t*>(lut)[k] = cent_hilo_pair(csc * centl[e & ((1 << KB) - 1)], csc * centl[e >> KB]).x;
-    }
+    build_pair_table_wave<KB, LUT_LOGC>(lut, f32_to_f16_bits(csc * cent[lane & ((1 << KB) - 1)]), lane);
   }
-  __syncthreads();
+  const int qg = tid >> 4, ql16 = tid & 15;
+  float y[E];
+  if (qg < G) load_elems<QT, E>(query, ((int64_t)b * hq + kvh * G + qg) * D + ql16 * E, y);
 
   const int seq_len = seq_lens[b];
   int k0 = kv_start ? kv_start[b] : 0;
@@ -876,7 +856,6 @@ __global__ __launch_bounds__(256, VB == 2 ? 4 : 2) void v1_attn_g4_kernel(
   const int t_end = min(t_begin + tps, t_last);
   const int32_t* bt_row = block_table + (int64_t)b * max_blocks;
   const int64_t kvh_off = (int64_t)kvh * s_head;
-  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
 
   V1Addr ad;
   ad.cache = cache;
@@ -898,6 +877,55 @@ __global__ __launch_bounds__(256, VB == 2 ? 4 : 2) void v1_attn_g4_kernel(
   const uint32_t sel1 = (o3 + 1) | ((o3 + 2) << 8) | ((o3 + 5) << 16) | ((o3 + 6) << 24);
   const uint32_t sel2 = (o3 + 2) | (0x0Cu << 8) | ((o3 + 6) << 16) | (0x0Cu << 24);
 
+  // the first tile's loads (two register sets: the next tile's loads overlap
+  // this tile's math, and the block-table entries come one tile further ahead)
+  V1Tile<D, KB, VB> ra, rb;
+  int tile = t_begin + wave_u;
+  int btv = 0;
+  if (tile < t_end) {
+    v1_load(ra, ad, tile, v1_fetch_bt(ad, tile, true, lane));
+    btv = v1_fetch_bt(ad, tile + 4, tile + 4 < t_end, lane);
+  }
+
+  if (qg < G) {
+    if (rot != nullptr) rot_matrix_lanes<D, E>(y, rot, &qs[qg][0], ql16);  // q M (matrix strategies)
+    else fwht_lanes<E, 16>(y, ql16);
+#pragma unroll
+    for (int i = 0; i < E; ++i) qs[qg][ql16 * E + i] = y[i] * qscale;
+  }
+  __syncthreads();
+  // B operand of the Q.K MFMAs: column n < G holds f16(q) of head n, column
+  // G + n its remainder q - f16(q); the two score columns are summed after the
+  // K loop, so q enters in about fp32 precision at no extra MFMA
+  Op8 qb[NS];
+  {
+    const int hq_ = m < G ? m : m - G;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      float x[8];
+      if (m < 2 * G) {
+        const float4 a4 = *reinterpret_cast<const float4*>(&qs[hq_][g * (D / 4) + 8 * s]);
+        const float4 c4 = *reinterpret_cast<const float4*>(&qs[hq_][g * (D / 4) + 8 * s + 4]);
+        x[0] = a4.x; x[1] = a4.y; x[2] = a4.z; x[3] = a4.w; x[4] = c4.x; x[5] = c4.y; x[6] = c4.z; x[7] = c4.w;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = 0.f;
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        uint32_t w = 0;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const float xv = x[2 * j + e];
+          const _Float16 hi = (_Float16)xv;
+          const _Float16 v = m < G ? hi : (_Float16)(xv - (float)hi);
+          w |= (uint32_t)__builtin_bit_cast(uint16_t, v) << (16 * e);
+        }
+        qb[s].u[j] = w;
+      }
+    }
+  }
+
   float m_run = -INFINITY, l_run = 0.f, z_run = 0.f, u_run = 0.f;  // per compact lane, head cn
   floatx4 acc[NB];
 #pragma unroll
@@ -916,7 +944,7 @@ __global__ __launch_bounds__(256, VB == 2 ? 4 : 2) void v1_attn_g4_kernel(
         Op8 a;
 #pragma unroll
         for (int p = 0; p < 4; ++p)
-          a.u[p] = *reinterpret_cast<const uint32_t*>(lutl + field_off<2 + LUT_LOGC>(cur.k[st], (8 * s + 2 * p) * KB, 2 * KB));
+          a.u[p] = lds_dword_at(lut, lut_field<2 + LUT_LOGC, 2 * KB>(cur.k[st], (8 * s + 2 * p) * KB, laneoff));
         sacc[st] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a.h, qb[s].h, sacc[st], 0, 0, 0);
         gacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a.h, a.h, gacc, 0, 0, 0);
       }
@@ -1054,15 +1082,8 @@ __global__ __launch_bounds__(256, VB == 2 ? 4 : 2) void v1_attn_g4_kernel(
     }
   };
 
-  // two register sets: the next tile's loads overlap this tile's math, and
-  // the block-table entries come one tile further ahead
-  V1Tile<D, KB, VB> ra, rb;
-  int tile = t_begin + wave_u;
-  int btv = 0;
-  if (tile < t_end) {
-    v1_load(ra, ad, tile, v1_fetch_bt(ad, tile, true, lane));
-    btv = v1_fetch_bt(ad, tile + 4, tile + 4 < t_end, lane);
-  }
+  // each wave takes every 4th tile (a fixed assignment, so the sums and the
+  // output bits do not depend on how fast the waves progress)
   while (tile < t_end) {
     int btn = v1_fetch_bt(ad, tile + 8, tile + 8 < t_end, lane);
     v1_load(rb, ad, tile + 4, btv);
