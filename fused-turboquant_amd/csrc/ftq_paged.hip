@@ -335,6 +335,9 @@ __global__ __launch_bounds__(256) void paged_store_mfma_kernel(
 
     float t[32 * NB];
     float nrm;
+    // The cache writes are non-temporal (streamed past the caches, which then
+    // hold the K / V reads): 9% faster on a config-3 chunk.  (Full-line fp32
+    // output streams, as the decoder's, measured 2x slower that way.)
     {  // K: codes per token, block b's BK words of token j at word BK (4 b + q) of its row
       const float sv = rotate(key, t0, head, ksm, t, nrm);
       float T[1][NTK];
@@ -346,14 +349,15 @@ __global__ __launch_bounds__(256) void paged_store_mfma_kernel(
       for (int b = 0; b < NB; ++b) {
         uint32_t* dst = reinterpret_cast<uint32_t*>(sbp + j * Gm::KTOK) + BK * (4 * b + q);
 #pragma unroll
-        for (int k = 0; k < BK; ++k) dst[k] = w[BK * b + k];
+        for (int k = 0; k < BK; ++k) __builtin_nontemporal_store(w[BK * b + k], dst + k);
       }
-      if (q == 0) reinterpret_cast<uint16_t*>(sbp + Gm::KNORM)[j] = (uint16_t)f32_to_f16_bits(nrm);
+      if (q == 0)
+        __builtin_nontemporal_store((uint16_t)f32_to_f16_bits(nrm), reinterpret_cast<uint16_t*>(sbp + Gm::KNORM) + j);
     }
     {  // V: through the LDS tile into lane-major chunks, 128 dims at a time
       const float sv = rotate(value, t0, head, vsm, t, nrm);
       if (q == 0) {
-        reinterpret_cast<uint16_t*>(sbp + Gm::VNORM)[j] = (uint16_t)f32_to_f16_bits(nrm);
+        __builtin_nontemporal_store((uint16_t)f32_to_f16_bits(nrm), reinterpret_cast<uint16_t*>(sbp + Gm::VNORM) + j);
         vsc[wv][j] = sv;
       }
       __asm__ volatile("" ::: "memory");
@@ -385,7 +389,7 @@ __global__ __launch_bounds__(256) void paged_store_mfma_kernel(
         uint32_t w[BV];
         quantize_pack<BV, 32, 4>(x, T, w);
 #pragma unroll
-        for (int k = 0; k < BV; ++k) chunk[BV * hb + k] = w[k];
+        for (int k = 0; k < BV; ++k) __builtin_nontemporal_store(w[k], chunk + BV * hb + k);
         __asm__ volatile("" ::: "memory");  // the tile is rewritten next
       }
     }
