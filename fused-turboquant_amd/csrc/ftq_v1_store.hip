@@ -3,8 +3,49 @@
 // ftq_v1_store_kernel.h; 1-bit codes, 8-bit K / V and fp8 keys are launched
 // from ftq_v1_store_ext.hip).
 #include "ftq_v1_store_kernel.h"
+#include "ftq_v1_store_mfma.h"
 
 namespace ftq {
+
+// The matrix-core store (ftq_v1_store_mfma.h) takes: the Hadamard rotation at
+// d = 128, 16-bit inputs, K and V in 2..4 bits, no Lloyd-Max V, and 32-bit
+// vector and slot numbers.
+static bool v1_store_mfma_ok(int d, int dt, int kb, int vb, int flags, int rb, int64_t nvec, int64_t slots_total) {
+  const bool vlm = (flags & V1F_VLM) != 0 && vb == 4;
+  return rb == 0 && d == 128 && dt != F32 && kb >= 2 && kb <= 4 && vb >= 2 && vb <= 4 && !vlm &&
+         (flags & V1F_KFP8) == 0 && nvec < ((int64_t)1 << 31) - 64 && slots_total < ((int64_t)1 << 31);
+}
+
+template <int DT, int KB, int VB>
+static hipError_t launch_store_mfma3(const void* k, const void* v, int64_t nvec, int hkv, const float* mids,
+                                     int vflags, const int64_t* slots, uint8_t* cache, int64_t slots_total, int bs,
+                                     int64_t sb, int64_t sp, int64_t sh, hipStream_t st) {
+  // one pass of resident workgroups, each wave looping over groups of 16 vectors
+  static const int cap = resident_workgroups(v1_store_mfma_kernel<DT, KB, VB>);
+  const int64_t want = ((nvec + 15) / 16 + 3) / 4;
+  v1_store_mfma_kernel<DT, KB, VB><<<dim3((unsigned)(want < cap ? want : cap)), dim3(256), 0, st>>>(
+      k, v, (int)nvec, hkv, FastDiv::make(hkv), mids, vflags, slots, cache, (int)slots_total, bs,
+      FastDiv::make(bs), sb, sp, sh, fwht_scale(128));
+  return hipGetLastError();
+}
+
+template <int DT, int KB>
+static hipError_t launch_store_mfma2(int vb, const void* k, const void* v, int64_t nvec, int hkv, const float* mids,
+                                     int vflags, const int64_t* slots, uint8_t* cache, int64_t slots_total, int bs,
+                                     int64_t sb, int64_t sp, int64_t sh, hipStream_t st) {
+  if (vb == 2) return launch_store_mfma3<DT, KB, 2>(k, v, nvec, hkv, mids, vflags, slots, cache, slots_total, bs, sb, sp, sh, st);
+  if (vb == 3) return launch_store_mfma3<DT, KB, 3>(k, v, nvec, hkv, mids, vflags, slots, cache, slots_total, bs, sb, sp, sh, st);
+  return launch_store_mfma3<DT, KB, 4>(k, v, nvec, hkv, mids, vflags, slots, cache, slots_total, bs, sb, sp, sh, st);
+}
+
+template <int DT>
+static hipError_t launch_store_mfma1(int kb, int vb, const void* k, const void* v, int64_t nvec, int hkv,
+                                     const float* mids, int vflags, const int64_t* slots, uint8_t* cache,
+                                     int64_t slots_total, int bs, int64_t sb, int64_t sp, int64_t sh, hipStream_t st) {
+  if (kb == 2) return launch_store_mfma2<DT, 2>(vb, k, v, nvec, hkv, mids, vflags, slots, cache, slots_total, bs, sb, sp, sh, st);
+  if (kb == 3) return launch_store_mfma2<DT, 3>(vb, k, v, nvec, hkv, mids, vflags, slots, cache, slots_total, bs, sb, sp, sh, st);
+  return launch_store_mfma2<DT, 4>(vb, k, v, nvec, hkv, mids, vflags, slots, cache, slots_total, bs, sb, sp, sh, st);
+}
 
 template <int D, int KB>
 static hipError_t launch_fast_store2(int vb, int rb, const void* k, const void* v, int dt, int64_t n, int hkv,
@@ -74,7 +115,18 @@ static int v1_store_fast(const void* key, const void* value, int dtype, int64_t 
   hipStream_t st = (hipStream_t)stream;
   hipError_t e;
   const bool kf8 = (v_rotate & V1F_KFP8) != 0;
-  if (kf8 || key_bits < 2 || key_bits > 4 || value_bits < 2 || value_bits > 4)
+  const int64_t nvec = n_tokens * num_kv_heads;
+  const int64_t slots_total = num_blocks * (int64_t)block_size;
+  if (v1_store_mfma_ok(d, dtype, key_bits, value_bits, v_rotate, rb, nvec, slots_total)) {
+    if (dtype == F16)
+      e = launch_store_mfma1<F16>(key_bits, value_bits, key, value, nvec, num_kv_heads, midpoints, v_rotate,
+                                  slot_mapping, kv_cache, slots_total, block_size, stride_block, stride_pos,
+                                  stride_head, st);
+    else
+      e = launch_store_mfma1<BF16>(key_bits, value_bits, key, value, nvec, num_kv_heads, midpoints, v_rotate,
+                                   slot_mapping, kv_cache, slots_total, block_size, stride_block, stride_pos,
+                                   stride_head, st);
+  } else if (kf8 || key_bits < 2 || key_bits > 4 || value_bits < 2 || value_bits > 4)
     e = v1_store_ext_launch(d, key_bits, value_bits, kf8, rb, key, value, dtype, n_tokens, num_kv_heads, midpoints,
                             v_rotate, slot_mapping, kv_cache, num_blocks, block_size, stride_block, stride_pos,
                             stride_head, coeffs, st);
