@@ -167,53 +167,30 @@ __device__ __forceinline__ void v1_kcodes_sym(const float (&x)[E], const float (
 }
 
 // Min / max uniform codes of the lane's E elements, code = trunc((v - mn) /
-// sc + 0.5) clamped to [0, 2^VB - 1] with the division correctly rounded
-// (reference triton_inkernel_store.py:202-330).  The quotient is formed
-// through the reciprocal, within 2 ulps of the rounded division; the code can
-// differ from the division's only where q lies within that distance of a
-// half-integer.  q < 16 here (v - mn <= (2^VB - 1) sc up to rounding), so its
-// ulp is at most 2^-20 and a window of 8e-6 (8 ulps) holds every such case:
-// where any element of the wave falls in it, the wave redoes the lane's codes
-// with the IEEE division.  Codes are packed at bit VB e of E * VB / 32 words;
-// v is left holding v - mn.
+// sc + 0.5) clamped to [0, 2^VB - 1] (reference
+// triton_inkernel_store.py:202-330), with the division correctly rounded by
+// one fused correction of the reciprocal's quotient: rs = RN(1 / sc) (an IEEE
+// division, once per vector), q0 = RN(d rs), r = d - q0 sc (exact, one fma),
+// q = RN(q0 + r rs) = RN(d / sc) (Markstein's theorem: rs within half an ulp
+// of 1 / sc and q0 within an ulp of d / sc make the corrected quotient the
+// rounded one).  Codes are packed at bit VB e of E * VB / 32 words.
 template <int VB, int E>
-__device__ __forceinline__ void v1_vcodes_uniform(float (&v)[E], float mn, float sc, uint32_t (&w)[E * VB / 32]) {
+__device__ __forceinline__ void v1_vcodes_uniform(const float (&v)[E], float mn, float sc,
+                                                  uint32_t (&w)[E * VB / 32]) {
   constexpr int VTOP = (1 << VB) - 1;
   const float rs = 1.f / sc;
-  // v - mn in place; the quotients are formed twice (the check, then the
-  // codes) rather than held beside it: 32 registers fewer
-  bool near = false;
-#pragma unroll
-  for (int i = 0; i < E; ++i) {
-    v[i] = v[i] - mn;
-    const float q = v[i] * rs;
-    const float f = __builtin_amdgcn_fractf(q);
-    near |= __builtin_fabsf(f - 0.5f) < 8e-6f;  // no short circuit: no branches
-    // (left to itself the scheduler forms every f - 0.5 before the first
-    // compare: 30 registers more, at the kernel's peak)
-    if ((i & 7) == 7) __builtin_amdgcn_sched_barrier(0);
-  }
 #pragma unroll
   for (int k = 0; k < E * VB / 32; ++k) w[k] = 0;
-  auto code = [&](int i, float q) __attribute__((always_inline)) {
-    const float t = q + 0.5f;
-    // trunc toward zero, clamped to [0, VTOP]; NaN -> 0
-    const uint32_t c = t >= 1.f ? (uint32_t)fminf(t, (float)VTOP) : 0u;
+#pragma unroll
+  for (int i = 0; i < E; ++i) {
+    const float d = v[i] - mn;
+    const float q0 = d * rs;
+    const float q = __builtin_fmaf(__builtin_fmaf(-q0, sc, d), rs, q0);
+    // trunc(q + 0.5) clamped to [0, VTOP]; NaN -> 0 (fmaxf takes the number)
+    const uint32_t c = (uint32_t)fminf(fmaxf(q + 0.5f, 0.f), (float)VTOP);
     const int p = VB * i, k = p >> 5, o = p & 31;
     w[k] |= c << o;
     if (o + VB > 32) w[k + 1] |= c >> (32 - o);
-  };
-  if (__builtin_amdgcn_ballot_w64(near) != 0) {  // rare: the IEEE division
-    // one element at a time (interleaved, the divisions' temporaries would
-    // set the kernel's register count)
-#pragma unroll
-    for (int i = 0; i < E; ++i) {
-      code(i, v[i] / sc);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < E; ++i) code(i, v[i] * rs);
   }
 }
 
