@@ -29,10 +29,9 @@
 // per element instead of 2^bits - 1 compares and adds); the 255 midpoints of
 // 8-bit codes live in LDS and are searched by binary lifting.
 // K is divided by its norm through the reciprocal and one fma correction.
-// The uniform V codes divide by the scale through its reciprocal; where that
-// quotient lies within 1e-5 of a half-integer (the only place trunc(q + 0.5)
-// can differ from the correctly rounded division), the wave recomputes the
-// lane's elements with the IEEE division.
+// The uniform V codes divide by the scale through its correctly rounded
+// reciprocal and one fused correction of the quotient, which gives the
+// correctly rounded division (Markstein's theorem).
 #pragma once
 
 #include "ftq_internal.h"
@@ -361,24 +360,16 @@ __global__ __launch_bounds__(256) void v1_store_fast_kernel(
       if (vrot) mn = mn + 0.f;
       sc = (VB == 1) ? (mx - mn) : (mx - mn) / (float)VTOP;
       sc = sc > 1e-8f ? sc : 1e-8f;
+      // (v - mn) / sc correctly rounded: the reciprocal's quotient and one
+      // fused correction (Markstein: rs = RN(1 / sc), q0 within an ulp)
       const float rs = 1.f / sc;
-      float q[E];
-      bool near = false;
 #pragma unroll
       for (int i = 0; i < E; ++i) {
-        q[i] = (v[i] - mn) * rs;
-        const float f = q[i] - __builtin_floorf(q[i]);
-        near = near || (__builtin_fabsf(f - 0.5f) < 1e-5f * fmaxf(q[i], 1.f));
-      }
-      if (__builtin_amdgcn_ballot_w64(near) != 0) {  // rare: the correctly rounded quotient
-#pragma unroll
-        for (int i = 0; i < E; ++i) q[i] = (v[i] - mn) / sc;
-      }
-#pragma unroll
-      for (int i = 0; i < E; ++i) {
-        const float t = q[i] + 0.5f;
-        // trunc toward zero, clamped to [0, VTOP]; NaN -> 0
-        c[i] = t >= 1.f ? (uint32_t)fminf(t, (float)VTOP) : 0u;
+        const float dv = v[i] - mn;
+        const float q0 = dv * rs;
+        const float q = __builtin_fmaf(__builtin_fmaf(-q0, sc, dv), rs, q0);
+        // trunc(q + 0.5) clamped to [0, VTOP]; NaN -> 0 (fmaxf takes the number)
+        c[i] = (uint32_t)fminf(fmaxf(q + 0.5f, 0.f), (float)VTOP);
       }
       pack_codes<E, VB, NW>(c, w);
     }
