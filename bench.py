@@ -643,12 +643,19 @@ def main():
 
     log("[bench] config2 encode: [32768,8,128] and [32768,8,256] bf16 3-bit, K and V")
     e128 = encode_setup(dev, 128, 0)
-    e256 = encode_setup(dev, 256, 10) if want("encode_d256_3bit") else None
+    e256 = encode_setup(dev, 256, 10) if (want("encode_d256_3bit") or want("decode_d256_3bit_f32")) else None
     n = e128["n"]
     ck = e128["ck"]
     lev, sg = e128["tq"].quantizer.levels, e128["tq"].rotation.signs
     dec_out = torch.empty(32768, 8, 128, dtype=torch.float32, device=dev)
     dec_k = lean_launch(L.ftq_decode, ck.indices, ck.norms, n, 128, lev, sg, 3, dec_out, 0, sp)
+    dec_k256 = None
+    if e256 is not None and want("decode_d256_3bit_f32"):
+        ck256 = e256["ck"]
+        tq256 = e256["tq"]
+        dec_out256 = torch.empty(32768, 8, 256, dtype=torch.float32, device=dev)
+        dec_k256 = lean_launch(L.ftq_decode, ck256.indices, ck256.norms, n, 256, tq256.quantizer.levels,
+                               tq256.rotation.signs, 3, dec_out256, 0, sp)
 
     log("[bench] config3 paged cache (B=32 ctx=8192 K3V3)")
     cfg3 = make_config3(dev, keep_first=not args.no_cpu)
@@ -735,6 +742,8 @@ def main():
     if e256 is not None:
         entry("encode_d256_3bit", e256["enc_k"], n * 256 * 2 + n * (256 * 3 // 8) + n * 2)
     entry("decode_d128_3bit_f32", dec_k, n * (128 * 3 // 8) + n * 2 + n * 128 * 4)
+    if dec_k256 is not None:
+        entry("decode_d256_3bit_f32", dec_k256, n * (256 * 3 // 8) + n * 2 + n * 256 * 4)
     entry("paged_attn_config3", attn3["run"], attn3["total_bytes"])
     if attn3v is not None:
         entry("paged_attn_config3_fp32_valu", attn3v["run"], attn3v["total_bytes"])

@@ -18,6 +18,7 @@
 #include "ftq_encode_fast.h"
 #include "ftq_encode_mfma.h"
 #include "ftq_internal.h"
+#include "ftq_merge.h"
 
 #include <cmath>
 
@@ -110,6 +111,14 @@ __global__ __launch_bounds__(256) void decode_kernel(const uint8_t* __restrict__
 #pragma unroll
   for (int i = 0; i < E; ++i) sg[i] = signs[lane * E + i];
 
+  // d = 256: the row goes out through LDS, so that each store instruction
+  // writes one contiguous run per vector (16 contiguous bytes per lane, lanes
+  // side by side) instead of 16 bytes of every lane's 64; the scattered form
+  // left the write stream at 3.0 TB/s.  A wave's LDS accesses run in order,
+  // and each 16-lane group only reads back its own row.
+  constexpr bool XPOSE = (D == 256);
+  __shared__ __attribute__((aligned(16))) float rowbuf[XPOSE ? GPB : 1][XPOSE ? D : 1];
+
   for (int64_t v = (int64_t)blockIdx.x * GPB + grp; v < n; v += (int64_t)gridDim.x * GPB) {
     uint32_t c[E];
     unpack_load<E, BITS>(packed + v * PD, lane, c);
@@ -120,7 +129,31 @@ __global__ __launch_bounds__(256) void decode_kernel(const uint8_t* __restrict__
     fwht_lanes<E, LPV>(y, lane);
 #pragma unroll
     for (int i = 0; i < E; ++i) y[i] = (y[i] * scale) * sg[i];
-    store_elems<OT, E>(out, v * D + lane * E, y);
+    if constexpr (XPOSE) {
+      float* rb = rowbuf[grp];
+#pragma unroll
+      for (int k = 0; k < E / 4; ++k)
+        *reinterpret_cast<float4*>(rb + lane * E + 4 * k) = make_float4(y[4 * k], y[4 * k + 1], y[4 * k + 2], y[4 * k + 3]);
+      __asm__ volatile("" ::: "memory");
+      // lane l now takes elements [64 k + 4 l, 64 k + 4 l + 4), k = 0 .. 3
+      float z[E];
+#pragma unroll
+      for (int k = 0; k < E / 4; ++k) {
+        const float4 t = *reinterpret_cast<const float4*>(rb + 64 * k + 4 * lane);
+        z[4 * k] = t.x;
+        z[4 * k + 1] = t.y;
+        z[4 * k + 2] = t.z;
+        z[4 * k + 3] = t.w;
+      }
+      __asm__ volatile("" ::: "memory");  // the row is rewritten next iteration
+#pragma unroll
+      for (int k = 0; k < E / 4; ++k) {
+        float z4[4] = {z[4 * k], z[4 * k + 1], z[4 * k + 2], z[4 * k + 3]};
+        store_small<OT, 4>(out, v * D + 64 * k + 4 * lane, z4);
+      }
+    } else {
+      store_elems<OT, E>(out, v * D + lane * E, y);
+    }
   }
 }
 
