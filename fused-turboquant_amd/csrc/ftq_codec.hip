@@ -92,6 +92,32 @@ __global__ __launch_bounds__(256) void encode_kernel(const void* __restrict__ x,
   }
 }
 
+// Store a d = 256 row held as 16 contiguous elements per lane over 16 lanes
+// (lane l: elements [16 l, 16 l + 16)) through the group's LDS row, so that
+// each store instruction writes one contiguous run per vector (lane l:
+// elements [64 k + 4 l, 64 k + 4 l + 4)) instead of 16 bytes of every lane's
+// 64; the scattered form left the write stream at 3.0 TB/s.  A wave's LDS
+// accesses run in order and each 16-lane group reads back only its own row.
+template <int OT>
+__device__ __forceinline__ void store_row256(float* rb, const float (&y)[16], void* out, int64_t off, int lane) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    *reinterpret_cast<float4*>(rb + lane * 16 + 4 * k) = make_float4(y[4 * k], y[4 * k + 1], y[4 * k + 2], y[4 * k + 3]);
+  __asm__ volatile("" ::: "memory");
+  float z[4][4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const float4 t = *reinterpret_cast<const float4*>(rb + 64 * k + 4 * lane);
+    z[k][0] = t.x;
+    z[k][1] = t.y;
+    z[k][2] = t.z;
+    z[k][3] = t.w;
+  }
+  __asm__ volatile("" ::: "memory");  // the row is rewritten by the next vector
+#pragma unroll
+  for (int k = 0; k < 4; ++k) store_small<OT, 4>(out, off + 64 * k + 4 * lane, z[k]);
+}
+
 template <int D, int BITS, int OT>
 __global__ __launch_bounds__(256) void decode_kernel(const uint8_t* __restrict__ packed,
                                                      const uint16_t* __restrict__ norms, int64_t n,
@@ -111,12 +137,7 @@ __global__ __launch_bounds__(256) void decode_kernel(const uint8_t* __restrict__
 #pragma unroll
   for (int i = 0; i < E; ++i) sg[i] = signs[lane * E + i];
 
-  // d = 256: the row goes out through LDS, so that each store instruction
-  // writes one contiguous run per vector (16 contiguous bytes per lane, lanes
-  // side by side) instead of 16 bytes of every lane's 64; the scattered form
-  // left the write stream at 3.0 TB/s.  A wave's LDS accesses run in order,
-  // and each 16-lane group only reads back its own row.
-  constexpr bool XPOSE = (D == 256);
+  constexpr bool XPOSE = (D == 256);  // rows through LDS (store_row256)
   __shared__ __attribute__((aligned(16))) float rowbuf[XPOSE ? GPB : 1][XPOSE ? D : 1];
 
   for (int64_t v = (int64_t)blockIdx.x * GPB + grp; v < n; v += (int64_t)gridDim.x * GPB) {
@@ -130,27 +151,7 @@ __global__ __launch_bounds__(256) void decode_kernel(const uint8_t* __restrict__
 #pragma unroll
     for (int i = 0; i < E; ++i) y[i] = (y[i] * scale) * sg[i];
     if constexpr (XPOSE) {
-      float* rb = rowbuf[grp];
-#pragma unroll
-      for (int k = 0; k < E / 4; ++k)
-        *reinterpret_cast<float4*>(rb + lane * E + 4 * k) = make_float4(y[4 * k], y[4 * k + 1], y[4 * k + 2], y[4 * k + 3]);
-      __asm__ volatile("" ::: "memory");
-      // lane l now takes elements [64 k + 4 l, 64 k + 4 l + 4), k = 0 .. 3
-      float z[E];
-#pragma unroll
-      for (int k = 0; k < E / 4; ++k) {
-        const float4 t = *reinterpret_cast<const float4*>(rb + 64 * k + 4 * lane);
-        z[4 * k] = t.x;
-        z[4 * k + 1] = t.y;
-        z[4 * k + 2] = t.z;
-        z[4 * k + 3] = t.w;
-      }
-      __asm__ volatile("" ::: "memory");  // the row is rewritten next iteration
-#pragma unroll
-      for (int k = 0; k < E / 4; ++k) {
-        float z4[4] = {z[4 * k], z[4 * k + 1], z[4 * k + 2], z[4 * k + 3]};
-        store_small<OT, 4>(out, v * D + 64 * k + 4 * lane, z4);
-      }
+      store_row256<OT>(rowbuf[grp], y, out, v * D, lane);
     } else {
       store_elems<OT, E>(out, v * D + lane * E, y);
     }
@@ -168,6 +169,8 @@ __global__ __launch_bounds__(256) void rht_kernel(const void* __restrict__ x, in
   float sg[E];
 #pragma unroll
   for (int i = 0; i < E; ++i) sg[i] = signs[lane * E + i];
+  constexpr bool XPOSE = (D == 256);  // rows through LDS (store_row256)
+  __shared__ __attribute__((aligned(16))) float rowbuf[XPOSE ? GPB : 1][XPOSE ? D : 1];
   for (int64_t v = (int64_t)blockIdx.x * GPB + grp; v < n; v += (int64_t)gridDim.x * GPB) {
     float y[E];
     load_elems<IT, E>(x, v * D + lane * E, y);
@@ -181,7 +184,8 @@ __global__ __launch_bounds__(256) void rht_kernel(const void* __restrict__ x, in
       y[i] *= scale;
       if (inverse) y[i] *= sg[i];
     }
-    store_elems<OT, E>(out, v * D + lane * E, y);
+    if constexpr (XPOSE) store_row256<OT>(rowbuf[grp], y, out, v * D, lane);
+    else store_elems<OT, E>(out, v * D + lane * E, y);
   }
 }
 

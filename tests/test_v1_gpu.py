@@ -68,6 +68,18 @@ def test_store_zero_and_constant_vectors(cuda, d, kb, vb, vrot):
     _check_v1_store(cuda, d, kb, vb, vrot, "bf16", 3, 16, 2, 77 + d + kb + vrot, special=True)
 
 
+@pytest.mark.parametrize("kb,vb", [(4, 2), (3, 3), (2, 4)])
+@pytest.mark.parametrize("dtn", ["bf16", "f16"])
+@pytest.mark.parametrize("vrot", [False, True])
+def test_store_parity_matrix_core_path(cuda, kb, vb, dtn, vrot):
+    """At least 32768 (token, head) vectors at d = 128 with 16-bit inputs take
+    the matrix-core store: 4153 tokens x 8 heads (a partial last group of 16),
+    skipped slots, outlier keys and the zero / constant rows, byte for byte
+    against the oracle like the small cases."""
+    _check_v1_store(cuda, 128, kb, vb, vrot, dtn, 260, 16, 8, 4400 + kb * 10 + vb + 2 * vrot, outliers=True,
+                    special=True)
+
+
 def _check_v1_store(cuda, d, kb, vb, vrot, dtn, nb, bs, h, seed, outliers=False, special=False):
     from fused_turboquant import v1
     g = torch.Generator().manual_seed(seed)
