@@ -717,6 +717,22 @@ __global__ __launch_bounds__(256, 2) void v1_attn_kernel(
     }
   };
 
+  // The uniform V codes enter the P.V MFMAs as 2^e (1 + q 2^-k): the sums
+  // carry an offset, sum p sc (u_run), that the epilogue subtracts.  Its fp32
+  // rounding grows with the tiles summed (a wave of ~950 tiles erred by 8e-2
+  // on config 4), so every 16 tiles the offset so far leaves both sums.
+  int since = 0;
+  auto rebase = [&]() __attribute__((always_inline)) {
+    if constexpr (!VLM) {
+      if (++since == 16) {
+        since = 0;
+        const float u = warp_sum_q(u_run);
+#pragma unroll
+        for (int bb = 0; bb < NB; ++bb) acc[bb] -= u;
+        u_run = 0.f;
+      }
+    }
+  };
   // each wave takes every 4th tile (a fixed assignment, so the sums and the
   // output bits do not depend on how fast the waves progress)
   while (tile < t_end) {
@@ -724,12 +740,14 @@ __global__ __launch_bounds__(256, 2) void v1_attn_kernel(
     v1_load<D, KB, VB, VLM>(rb, ad, tile + 4, btv);
     btv = btn;
     process(ra, tile);
+    rebase();
     tile += 4;
     if (tile >= t_end) break;
     btn = v1_fetch_bt(ad, tile + 8, tile + 8 < t_end, lane);
     v1_load<D, KB, VB, VLM>(ra, ad, tile + 4, btv);
     btv = btn;
     process(rb, tile);
+    rebase();
     tile += 4;
   }
 
@@ -1082,24 +1100,6 @@ __global__ __launch_bounds__(256, VB == 2 ? 4 : 2) void v1_attn_g4_kernel(
     }
   };
 
-  // each wave takes every 4th tile (a fixed assignment, so the sums and the
-  // output bits do not depend on how fast the waves progress)
-  while (tile < t_end) {
-    int btn = v1_fetch_bt(ad, tile + 8, tile + 8 < t_end, lane);
-    v1_load(rb, ad, tile + 4, btv);
-    btv = btn;
-    process(ra, tile);
-    tile += 4;
-    if (tile >= t_end) break;
-    btn = v1_fetch_bt(ad, tile + 8, tile + 8 < t_end, lane);
-    v1_load(ra, ad, tile + 4, btv);
-    btv = btn;
-    process(rb, tile);
-    tile += 4;
-  }
-
-  // ---- per-head totals over the 16 compact lanes of each head, wave merge ----
-  __syncthreads();
   auto head_sum = [](float x) __attribute__((always_inline)) {
     x += dpp_xor4(x);
     x += dpp_xor8(x);
@@ -1107,6 +1107,41 @@ __global__ __launch_bounds__(256, VB == 2 ? 4 : 2) void v1_attn_g4_kernel(
     x += __shfl_xor(x, 32);
     return x;
   };
+  // The V codes enter the P.V MFMAs as 2^e (1 + q 2^-k): the sums carry an
+  // offset, sum p sc (u_run), that the epilogue subtracts.  Its fp32 rounding
+  // grows with the tiles summed (a wave of ~950 tiles erred by 8e-2 on config
+  // 4), so every 16 tiles the offset so far leaves both sums (acc column m < 4
+  // is head lane & 3, whose compact lanes head_sum adds).
+  int since = 0;
+  auto rebase = [&]() __attribute__((always_inline)) {
+    if (++since == 16) {
+      since = 0;
+      const float u = head_sum(u_run);
+#pragma unroll
+      for (int bb = 0; bb < NB; ++bb) acc[bb] -= u;
+      u_run = 0.f;
+    }
+  };
+  // each wave takes every 4th tile (a fixed assignment, so the sums and the
+  // output bits do not depend on how fast the waves progress)
+  while (tile < t_end) {
+    int btn = v1_fetch_bt(ad, tile + 8, tile + 8 < t_end, lane);
+    v1_load(rb, ad, tile + 4, btv);
+    btv = btn;
+    process(ra, tile);
+    rebase();
+    tile += 4;
+    if (tile >= t_end) break;
+    btn = v1_fetch_bt(ad, tile + 8, tile + 8 < t_end, lane);
+    v1_load(ra, ad, tile + 4, btv);
+    btv = btn;
+    process(rb, tile);
+    rebase();
+    tile += 4;
+  }
+
+  // ---- per-head totals over the 16 compact lanes of each head, wave merge ----
+  __syncthreads();
   const float l_tot = head_sum(l_run);
   const float z_tot = head_sum(z_run);
   const float u_tot = head_sum(u_run);

@@ -163,7 +163,7 @@ def _check_attn(got, want, tag):
 
 
 @pytest.mark.parametrize("kb,vb", [(4, 2), (3, 3), (4, 4), (2, 2), (3, 4), (2, 3)])
-@pytest.mark.parametrize("hq,hkv", [(8, 2), (4, 4), (16, 1)])
+@pytest.mark.parametrize("hq,hkv", [(8, 2), (4, 4), (16, 1), (16, 4), (32, 8)])
 @pytest.mark.parametrize("splits", [1, 3, 16])
 def test_decode_parity(cuda, kb, vb, hq, hkv, splits):
     from fused_turboquant import v1
