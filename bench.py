@@ -61,10 +61,11 @@ RAMP_S = 0.3  # untimed seconds of back-to-back steps before any timing (clock r
 # Keyed by roofline entry; None where no counter run covers the kernel (the
 # small v1 stores, whose counts stay below the copy calibration's resolution).
 TRAFFIC_BYTES: dict = {
-    "encode_kv_d128_3bit": 160576907, "encode_kv_d128_3bit_same_input": 160539838,
-    "encode_d128_3bit": 80318141, "encode_d256_3bit": 160115067, "decode_d128_3bit_f32": 149007945,
-    "paged_attn_config3": 219882404, "v1_attn_config4": 406670855, "raw_attn_boundary": 1081506403,
-    "v1_store_config4_chunk": 170116581, "paged_store_config3_chunk": 322480568,
+    "encode_kv_d128_3bit": 160822360, "encode_kv_d128_3bit_same_input": 161017535,
+    "encode_d128_3bit": 80597591, "encode_d256_3bit": 161826378, "decode_d128_3bit_f32": 149008797,
+    "decode_d256_3bit_f32": 295825734, "paged_attn_config3": 219891991, "v1_attn_config4": 406750850,
+    "raw_attn_boundary": 1081599888, "v1_store_config4_chunk": 171769851,
+    "paged_store_config3_chunk": 323828547,
 }
 
 # config-1 outlier channels (x10), fixed here so the CPU baseline's input is reproducible
