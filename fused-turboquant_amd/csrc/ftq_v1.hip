@@ -195,6 +195,60 @@ __global__ __launch_bounds__(256) void v1_store_kernel(
   }
 }
 
+// One split (num_splits == 1) and no caller matrix: the workgroup writes the
+// output itself (the merge's arithmetic for a single partial: o / L, then the
+// un-rotation and the dtype) and no merge launch follows.  mode -1: partials
+// to the workspace as usual; 0: output, V not rotated; 1: output, V rotated
+// (o <- (H o) d^-1/2).
+struct V1Direct {
+  void* out;
+  float* lse;  // optional natural-log LSE per row
+  float scale;  // d^-1/2 (the merge's factor)
+  int ot, mode;
+};
+
+// Rows of one (batch, kv head) written straight to the output: wave w takes
+// heads w, w + 4, ...; lane l elements [2 l, 2 l + 2).  Bit for bit what the
+// merge writes for one split: y = o / L (its workspace value, times the merge's
+// weight 1 and 1 / W = 1), then the inverse transform and the dtype.
+template <int D, int RW, int RS>
+__device__ __forceinline__ void v1_direct_rows(const float (&red_m)[4][RW], const float (&red_l)[4][RW],
+                                               const float (*red_o)[RW][RS], int G, int wave, int lane,
+                                               int64_t row0, const V1Direct& dout) {
+  constexpr int E2 = D / 64;
+  for (int gg = wave; gg < G; gg += 4) {
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) M = fmaxf(M, red_m[w][gg]);
+    float L = 0.f, o[E2];
+#pragma unroll
+    for (int i = 0; i < E2; ++i) o[i] = 0.f;
+    if (M != -INFINITY) {
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float f = __builtin_amdgcn_exp2f(red_m[w][gg] - M);
+        L += f * red_l[w][gg];
+#pragma unroll
+        for (int i = 0; i < E2; ++i) o[i] += f * red_o[w][gg][E2 * lane + i];
+      }
+    }
+    float y[E2];
+#pragma unroll
+    for (int i = 0; i < E2; ++i) y[i] = (L > 0.f) ? o[i] / L : 0.f;
+    if (dout.mode == 1) {
+      fwht_wave64<E2>(y, lane);
+#pragma unroll
+      for (int i = 0; i < E2; ++i) y[i] *= dout.scale;
+    }
+    const int64_t row = row0 + gg;
+    if (dout.lse != nullptr && lane == 0)
+      dout.lse[row] = (L > 0.f) ? (M + __builtin_log2f(L)) * 0.69314718055994531f : -INFINITY;
+    if (dout.ot == F32) store_small<F32, E2>(dout.out, row * D + lane * E2, y);
+    else if (dout.ot == F16) store_small<F16, E2>(dout.out, row * D + lane * E2, y);
+    else store_small<BF16, E2>(dout.out, row * D + lane * E2, y);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // decode attention, stage 1 (per split)
 // ---------------------------------------------------------------------------
@@ -382,7 +436,7 @@ __global__ __launch_bounds__(256, 2) void v1_attn_kernel(
     const int32_t* __restrict__ kv_start, int hq, int hkv, int lbs, int max_blocks,
     int64_t num_blocks, int64_t s_blk, int64_t s_pos, int64_t s_head,
     const float* __restrict__ cent, float qscale, int num_splits, float* __restrict__ ws_o,
-    float* __restrict__ ws_lse, const float* __restrict__ rot) {
+    float* __restrict__ ws_lse, const float* __restrict__ rot, V1Direct dout) {
   using A = V1A<D, KB, VB>;
   constexpr int NS = A::NS, NB = A::NB, E = D / 16;
   const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
@@ -768,6 +822,10 @@ __global__ __launch_bounds__(256, 2) void v1_attn_kernel(
       red_o[wave][m][8 * (4 * g + i) + bb] = VLM ? acc[bb][i] * vinv : __builtin_fmaf(acc[bb][i] - u_tot, VSC, z_tot);
   __syncthreads();
 
+  if (dout.mode >= 0) {  // one split: the output itself
+    v1_direct_rows<D, 16, D + 1>(red_m, red_l, red_o, G, wave, lane, (int64_t)b * hq + kvh * G, dout);
+    return;
+  }
   const int64_t row0 = ((int64_t)b * hq + kvh * G) * num_splits + split;  // (b, head 0 of the group, split)
   for (int idx = tid; idx < G * D; idx += 256) {
     const int gg = idx / D, d = idx % D;
@@ -821,7 +879,7 @@ __global__ __launch_bounds__(256, VB == 2 ? 4 : 2) void v1_attn_g4_kernel(
     const int32_t* __restrict__ kv_start, int hq, int hkv, int lbs, int max_blocks,
     int64_t num_blocks, int64_t s_blk, int64_t s_pos, int64_t s_head,
     const float* __restrict__ cent, float qscale, int num_splits, float* __restrict__ ws_o,
-    float* __restrict__ ws_lse, const float* __restrict__ rot) {
+    float* __restrict__ ws_lse, const float* __restrict__ rot, V1Direct dout) {
   using A = V1A<D, KB, VB>;
   constexpr int NS = A::NS, NB = A::NB, E = D / 16;
   constexpr int G = 4;
@@ -1160,6 +1218,10 @@ __global__ __launch_bounds__(256, VB == 2 ? 4 : 2) void v1_attn_g4_kernel(
   }
   __syncthreads();
 
+  if (dout.mode >= 0) {  // one split: the output itself
+    v1_direct_rows<D, G, D + 1>(red_m, red_l, red_o, G, wave, lane, (int64_t)b * hq + kvh * G, dout);
+    return;
+  }
   const int64_t row0 = ((int64_t)b * hq + kvh * G) * num_splits + split;
   for (int idx = tid; idx < G * D; idx += 256) {
     const int gg = idx / D, d = idx % D;
@@ -1211,33 +1273,36 @@ static hipError_t v1_launch_store_dense(const void* k, const void* v, int dt, in
 template <int D, int KB, int VB>
 static hipError_t v1_launch_attn3(const V1Args& a, hipStream_t st) {
   dim3 grid(a.splits, a.hkv, a.B), block(256);
+  // one split and no caller matrix: the kernel writes the output, no merge
+  const bool direct = a.splits == 1 && !((a.vrot & 1) && a.rot != nullptr);
+  const V1Direct dout{a.out, a.lse, fwht_scale(D), a.ot, direct ? (a.vrot & 1) : -1};
   if constexpr (VB == 4) {
     if (a.vrot & 2) {  // Lloyd-Max V codes
       if (a.qt == F32)
-        v1_attn_kernel<D, KB, VB, F32, true><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.ks, a.hq, a.hkv, a.lbs, a.max_blocks, a.nb, a.sblk, a.spos, a.shead, a.cent, a.qscale, a.splits, a.wo, a.wl, a.rot);
+        v1_attn_kernel<D, KB, VB, F32, true><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.ks, a.hq, a.hkv, a.lbs, a.max_blocks, a.nb, a.sblk, a.spos, a.shead, a.cent, a.qscale, a.splits, a.wo, a.wl, a.rot, dout);
       else if (a.qt == F16)
-        v1_attn_kernel<D, KB, VB, F16, true><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.ks, a.hq, a.hkv, a.lbs, a.max_blocks, a.nb, a.sblk, a.spos, a.shead, a.cent, a.qscale, a.splits, a.wo, a.wl, a.rot);
+        v1_attn_kernel<D, KB, VB, F16, true><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.ks, a.hq, a.hkv, a.lbs, a.max_blocks, a.nb, a.sblk, a.spos, a.shead, a.cent, a.qscale, a.splits, a.wo, a.wl, a.rot, dout);
       else
-        v1_attn_kernel<D, KB, VB, BF16, true><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.ks, a.hq, a.hkv, a.lbs, a.max_blocks, a.nb, a.sblk, a.spos, a.shead, a.cent, a.qscale, a.splits, a.wo, a.wl, a.rot);
+        v1_attn_kernel<D, KB, VB, BF16, true><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.ks, a.hq, a.hkv, a.lbs, a.max_blocks, a.nb, a.sblk, a.spos, a.shead, a.cent, a.qscale, a.splits, a.wo, a.wl, a.rot, dout);
       goto merge;
     }
   }
   if (a.hq == 4 * a.hkv) {
     if (a.qt == F32)
-      v1_attn_g4_kernel<D, KB, VB, F32><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.ks, a.hq, a.hkv, a.lbs, a.max_blocks, a.nb, a.sblk, a.spos, a.shead, a.cent, a.qscale, a.splits, a.wo, a.wl, a.rot);
+      v1_attn_g4_kernel<D, KB, VB, F32><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.ks, a.hq, a.hkv, a.lbs, a.max_blocks, a.nb, a.sblk, a.spos, a.shead, a.cent, a.qscale, a.splits, a.wo, a.wl, a.rot, dout);
     else if (a.qt == F16)
-      v1_attn_g4_kernel<D, KB, VB, F16><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.ks, a.hq, a.hkv, a.lbs, a.max_blocks, a.nb, a.sblk, a.spos, a.shead, a.cent, a.qscale, a.splits, a.wo, a.wl, a.rot);
+      v1_attn_g4_kernel<D, KB, VB, F16><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.ks, a.hq, a.hkv, a.lbs, a.max_blocks, a.nb, a.sblk, a.spos, a.shead, a.cent, a.qscale, a.splits, a.wo, a.wl, a.rot, dout);
     else
-      v1_attn_g4_kernel<D, KB, VB, BF16><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.ks, a.hq, a.hkv, a.lbs, a.max_blocks, a.nb, a.sblk, a.spos, a.shead, a.cent, a.qscale, a.splits, a.wo, a.wl, a.rot);
+      v1_attn_g4_kernel<D, KB, VB, BF16><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.ks, a.hq, a.hkv, a.lbs, a.max_blocks, a.nb, a.sblk, a.spos, a.shead, a.cent, a.qscale, a.splits, a.wo, a.wl, a.rot, dout);
   } else if (a.qt == F32)
-    v1_attn_kernel<D, KB, VB, F32><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.ks, a.hq, a.hkv, a.lbs, a.max_blocks, a.nb, a.sblk, a.spos, a.shead, a.cent, a.qscale, a.splits, a.wo, a.wl, a.rot);
+    v1_attn_kernel<D, KB, VB, F32><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.ks, a.hq, a.hkv, a.lbs, a.max_blocks, a.nb, a.sblk, a.spos, a.shead, a.cent, a.qscale, a.splits, a.wo, a.wl, a.rot, dout);
   else if (a.qt == F16)
-    v1_attn_kernel<D, KB, VB, F16><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.ks, a.hq, a.hkv, a.lbs, a.max_blocks, a.nb, a.sblk, a.spos, a.shead, a.cent, a.qscale, a.splits, a.wo, a.wl, a.rot);
+    v1_attn_kernel<D, KB, VB, F16><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.ks, a.hq, a.hkv, a.lbs, a.max_blocks, a.nb, a.sblk, a.spos, a.shead, a.cent, a.qscale, a.splits, a.wo, a.wl, a.rot, dout);
   else
-    v1_attn_kernel<D, KB, VB, BF16><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.ks, a.hq, a.hkv, a.lbs, a.max_blocks, a.nb, a.sblk, a.spos, a.shead, a.cent, a.qscale, a.splits, a.wo, a.wl, a.rot);
+    v1_attn_kernel<D, KB, VB, BF16><<<grid, block, 0, st>>>(a.q, a.cache, a.bt, a.sl, a.ks, a.hq, a.hkv, a.lbs, a.max_blocks, a.nb, a.sblk, a.spos, a.shead, a.cent, a.qscale, a.splits, a.wo, a.wl, a.rot, dout);
 merge:
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
+  if (e != hipSuccess || direct) return e;
   const int64_t rows = (int64_t)a.B * a.hq;
   const float rs = fwht_scale(D);
   if ((a.vrot & 1) && a.rot != nullptr) {  // o M^T
@@ -1319,6 +1384,11 @@ extern "C" int64_t ftq_v1_workspace_bytes(int batch, int num_q_heads, int d, int
 }
 
 extern "C" int ftq_v1_default_splits(int batch, int num_kv_heads, int max_seq_len) {
+  // 384 or more (batch, kv head) workgroups already give each CU 1.5 of them:
+  // one split writes the output directly and saves the merge launch (config
+  // 5's shape, 64 x 8 units over 2176 positions: 44.1 us at one split against
+  // 49.7 us at two)
+  if ((int64_t)batch * num_kv_heads >= 384) return 1;
   return auto_splits(batch, num_kv_heads, max_seq_len, 1024);
 }
 

@@ -188,6 +188,53 @@ def test_decode_parity(cuda, kb, vb, hq, hkv, splits):
     _check_attn(got, want, f"v1 attn kb={kb} vb={vb} hq={hq} hkv={hkv} S={splits} vrot={vrot}")
 
 
+@pytest.mark.parametrize("hq,hkv", [(8, 2), (32, 8)])
+@pytest.mark.parametrize("vrot,lloyd", [(False, False), (True, False), (True, True)])
+@pytest.mark.parametrize("odt", ["f32", "bf16"])
+def test_decode_single_split_direct_output(cuda, hq, hkv, vrot, lloyd, odt):
+    """One split writes the output from the attention kernel (no merge launch):
+    output and natural-log LSE against the merged two-split result (they
+    differ only in the order of the partial sums) and the oracle, empty rows
+    zero with LSE -inf, and the default split count at 384+ (batch, kv head)
+    units is that single split."""
+    from fused_turboquant import v1
+    d, bs, nb, kb = 128, 16, 48, 3
+    vb = 4 if lloyd else 3
+    g = torch.Generator().manual_seed(31 + hq + 2 * vrot + 4 * lloyd)
+    cache, c = _oracle_cache(g, nb, bs, hkv, d, kb, vb, nb * bs, vrot, lloyd=lloyd)
+    lens = [0, 1, 15, 17, 100, 257, 16, 64]
+    starts = [0, 0, 3, 0, 99, 10, 16, 0]
+    B = len(lens)
+    bt = torch.randint(0, nb, (B, 20), generator=g, dtype=torch.int32)
+    q = torch.randn(B, hq, d, generator=g).to(torch.bfloat16)
+    sl, ks = torch.tensor(lens, dtype=torch.int32), torch.tensor(starts, dtype=torch.int32)
+    res = {}
+    for s in (1, 2):
+        out = torch.full((B, hq, d), 7.0, dtype=DT[odt], device=cuda)
+        lse = torch.full((B, hq), 7.0, device=cuda)
+        v1.v1_decode_attention(q.to(cuda), torch.from_numpy(cache).to(cuda), bt.to(cuda), sl.to(cuda),
+                               torch.from_numpy(c).to(cuda), kb, vb, v_rotate=vrot, v_lloyd_max=lloyd,
+                               kv_start=ks.to(cuda), num_splits=s, out=out, lse=lse)
+        res[s] = (out.float().cpu().numpy(), lse.cpu().numpy())
+    (o1, l1), (o2, l2) = res[1], res[2]
+    empty = [b for b in range(B) if lens[b] <= starts[b]]
+    assert empty == [0, 6]
+    for b in empty:
+        assert not o1[b].any() and np.isneginf(l1[b]).all()
+    live = [b for b in range(B) if b not in empty]
+    assert np.isfinite(l1[live]).all()
+    assert np.abs(l1[live] - l2[live]).max() <= 1e-5 * max(1.0, float(np.abs(l2[live]).max()))
+    # the two splits start their running maxima, the f16 hi/lo parts of the
+    # probabilities and the P.V offset terms at different tokens: fp32 sums in
+    # another order (measured 7e-5 at |o| <= 3.2)
+    tol = 5e-4 if odt == "f32" else 2.0 ** -7
+    assert np.abs(o1 - o2).max() <= tol * max(1.0, float(np.abs(o2).max())), np.abs(o1 - o2).max()
+    want = O.v1_decode_attention(q.float().numpy(), cache, bt.numpy(), sl.numpy(), c, kb, vb,
+                                 1 / math.sqrt(d), kv_start=ks.numpy(), v_rotate=vrot, v_lloyd_max=lloyd)
+    _check_attn(o1, want, f"v1 direct hq={hq} hkv={hkv} vrot={vrot} lloyd={lloyd} {odt}")
+    assert v1.default_splits(48, 8, 4096) == 1 and v1.default_splits(4, 8, 131072) > 1
+
+
 @pytest.mark.parametrize("bs", [16, 32, 64])
 def test_decode_kv_start_and_block_size(cuda, bs):
     from fused_turboquant import v1
