@@ -39,6 +39,7 @@
 #include "ftq_encode_mfma.h"
 #include "ftq_internal.h"
 
+#include <algorithm>
 #include <cmath>
 
 namespace ftq {
@@ -1513,9 +1514,10 @@ static hipError_t launch_attn_valu2(int bv, const AttnArgs& a, hipStream_t st) {
 }
 
 int auto_splits(int batch, int hkv, int seq_hint, int target_wgs) {
-  // aim for target_wgs workgroups with at least 8 tiles per wave
-  const int units = batch * hkv;
-  int s = (target_wgs + units - 1) / units;
+  // aim for target_wgs workgroups with at least 8 tiles per wave (an empty
+  // batch or head count counts as one unit)
+  const int64_t units = (batch > 0 && hkv > 0) ? (int64_t)batch * hkv : 1;
+  int s = (int)std::min<int64_t>((target_wgs + units - 1) / units, 64);
   const int max_by_len = seq_hint / (32 * 4 * 8);
   if (s > max_by_len) s = max_by_len;
   if (s < 1) s = 1;
@@ -1533,8 +1535,7 @@ extern "C" int64_t ftq_paged_subblock_bytes(int d, int bits_k, int bits_v) {
 }
 
 extern "C" int64_t ftq_paged_workspace_bytes(int batch, int num_q_heads, int d, int num_splits) {
-  if (batch < 0 || num_q_heads < 0 || d <= 0 || num_splits <= 0) return -1;
-  return (int64_t)batch * num_q_heads * num_splits * (d + 1) * 4;
+  return split_workspace_bytes(batch, num_q_heads, d, num_splits);
 }
 
 extern "C" int ftq_paged_default_splits(int batch, int num_kv_heads, int max_seq_len) {
@@ -1545,7 +1546,9 @@ extern "C" int ftq_paged_choose_splits(int batch, int num_q_heads, int num_kv_he
   if (batch <= 0 || num_kv_heads <= 0 || num_q_heads <= 0) return 1;
   // one split when the single-workgroup form applies and its 16-wave
   // workgroups (one per CU at a time) keep the 256 CUs at least 3/4 busy
-  const int64_t units = (int64_t)batch * num_kv_heads;
+  // (past 768 units every whole-round count fills 3/4: the cap keeps the
+  // products small without changing the answer)
+  const int64_t units = std::min<int64_t>((int64_t)batch * num_kv_heads, 1 << 20);
   if (fused_form(d, num_q_heads, num_kv_heads, 1) && units >= 256) {
     const int64_t rounds = (units + 255) / 256;
     if (units * 4 >= rounds * 256 * 3) return 1;

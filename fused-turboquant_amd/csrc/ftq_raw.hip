@@ -413,7 +413,7 @@ extern "C" int ftq_raw_store(const void* key, const void* value, int dtype, int6
   FTQ_REQUIRE(n_tokens >= 0 && num_kv_heads > 0 && num_blocks >= 0 && block_size > 0,
               "bad token / head / block counts");
   FTQ_REQUIRE(stride_head >= 4 * (int64_t)d, "stride_head is smaller than the raw slot (4 * head_dim bytes)");
-  FTQ_REQUIRE(stride_pos >= stride_head * num_kv_heads && stride_block >= stride_pos * block_size,
+  FTQ_REQUIRE(cache_strides_ok(num_blocks, stride_block, stride_pos, stride_head, num_kv_heads, block_size),
               "kv_cache strides must describe [num_blocks][block_size][num_kv_heads][slot]");
   FTQ_REQUIRE(stride_head % 16 == 0 && stride_pos % 16 == 0 && stride_block % 16 == 0,
               "kv_cache strides must be multiples of 16 bytes");
@@ -439,8 +439,8 @@ extern "C" int ftq_raw_store(const void* key, const void* value, int dtype, int6
 }
 
 extern "C" int64_t ftq_raw_workspace_bytes(int batch, int num_q_heads, int d, int num_splits) {
-  if (batch < 0 || num_q_heads <= 0 || d <= 0 || num_splits <= 0) return -1;
-  return (int64_t)batch * num_q_heads * num_splits * (d + 1) * 4;
+  if (num_q_heads <= 0) return -1;
+  return split_workspace_bytes(batch, num_q_heads, d, num_splits);
 }
 
 extern "C" int ftq_raw_default_splits(int batch, int num_kv_heads, int max_seq_len) {
@@ -467,7 +467,7 @@ extern "C" int ftq_raw_decode_attention_lse(
   FTQ_REQUIRE(q_dtype >= F32 && q_dtype <= BF16 && out_dtype >= F32 && out_dtype <= BF16,
               "dtype must be FTQ_F32, FTQ_F16 or FTQ_BF16");
   FTQ_REQUIRE(stride_head >= 4 * (int64_t)d, "stride_head is smaller than the raw slot (4 * head_dim bytes)");
-  FTQ_REQUIRE(stride_pos >= stride_head * num_kv_heads && stride_block >= stride_pos * block_size,
+  FTQ_REQUIRE(cache_strides_ok(num_blocks, stride_block, stride_pos, stride_head, num_kv_heads, block_size),
               "kv_cache strides must describe [num_blocks][block_size][num_kv_heads][slot]");
   FTQ_REQUIRE(stride_head % 16 == 0 && stride_pos % 16 == 0 && stride_block % 16 == 0,
               "kv_cache strides must be multiples of 16 bytes");

@@ -1379,8 +1379,7 @@ extern "C" int ftq_v1_store_rot(const void* key, const void* value, int dtype, i
 }
 
 extern "C" int64_t ftq_v1_workspace_bytes(int batch, int num_q_heads, int d, int num_splits) {
-  if (batch < 0 || num_q_heads < 0 || d <= 0 || num_splits <= 0) return -1;
-  return (int64_t)batch * num_q_heads * num_splits * (d + 1) * 4;
+  return split_workspace_bytes(batch, num_q_heads, d, num_splits);
 }
 
 extern "C" int ftq_v1_default_splits(int batch, int num_kv_heads, int max_seq_len) {
@@ -1392,14 +1391,17 @@ extern "C" int ftq_v1_default_splits(int batch, int num_kv_heads, int max_seq_le
   return auto_splits(batch, num_kv_heads, max_seq_len, 1024);
 }
 
-extern "C" int ftq_v1_decode_attention_rot(
-    const void* query, int q_dtype, const uint8_t* kv_cache, int64_t num_blocks, int block_size,
-    int64_t stride_block, int64_t stride_pos, int64_t stride_head, const int32_t* block_table,
-    int max_blocks_per_seq, const int32_t* seq_lens, const int32_t* kv_start, int batch,
-    int num_q_heads, int num_kv_heads, int d, const float* centroids, int key_bits,
-    int value_bits, float scale, int v_rotate, int num_splits, void* workspace,
-    int64_t workspace_bytes, void* out, int out_dtype, float* lse_out, const float* rotation,
-    void* stream) {
+namespace {
+// Argument checks of the v1 decode attention entry points and the launch
+// arguments they imply.  check_ws: the caller's workspace (the no-alloc form
+// brings its own afterwards).  FTQ_OK with a.B == 0: nothing to launch.
+int v1_attn_prepare(V1Args& a, const void* query, int q_dtype, const uint8_t* kv_cache, int64_t num_blocks,
+                    int block_size, int64_t stride_block, int64_t stride_pos, int64_t stride_head,
+                    const int32_t* block_table, int max_blocks_per_seq, const int32_t* seq_lens,
+                    const int32_t* kv_start, int batch, int num_q_heads, int num_kv_heads, int d,
+                    const float* centroids, int key_bits, int value_bits, float scale, int v_rotate,
+                    int num_splits, void* workspace, int64_t workspace_bytes, bool check_ws, void* out,
+                    int out_dtype, float* lse_out, const float* rotation) {
   FTQ_REQUIRE(d == 64 || d == 128 || d == 256, "v1 decode attention: head_dim must be 64, 128 or 256");
   FTQ_REQUIRE(v_rotate >= 0 && v_rotate <= 15,
               "v_flags: bit 0 = un-rotate V, bit 1 = Lloyd-Max V codes, bit 2 = fp8 keys, bit 3 = fp32 products");
@@ -1419,20 +1421,24 @@ extern "C" int ftq_v1_decode_attention_rot(
   const bool kf8 = (v_rotate & V1F_KFP8) != 0;
   const V1Geom g = v1_geom(d, key_bits, value_bits, kf8);
   FTQ_REQUIRE(stride_head >= g.raw, "stride_head is smaller than the slot bytes (see ftq_v1_slot_bytes)");
-  FTQ_REQUIRE(stride_pos >= stride_head * num_kv_heads && stride_block >= stride_pos * block_size,
+  FTQ_REQUIRE(cache_strides_ok(num_blocks, stride_block, stride_pos, stride_head, num_kv_heads, block_size),
               "kv_cache strides must describe [num_blocks][block_size][num_kv_heads][slot]");
   FTQ_REQUIRE(stride_head % 4 == 0 && stride_pos % 4 == 0 && stride_block % 4 == 0,
               "kv_cache strides must be multiples of 4 bytes");
   FTQ_REQUIRE(stride_pos * 16 < ((int64_t)1 << 31), "stride_pos too large");
+  a.B = batch;
   if (batch == 0) return FTQ_OK;
   FTQ_REQUIRE(num_blocks >= 1, "kv_cache must hold at least one block");
-  FTQ_REQUIRE(query && kv_cache && block_table && seq_lens && workspace && out, "null pointer argument");
+  FTQ_REQUIRE(query && kv_cache && block_table && seq_lens && out, "null pointer argument");
   FTQ_REQUIRE(centroids != nullptr || kf8, "null centroids");
-  FTQ_REQUIRE(workspace_bytes >= ftq_v1_workspace_bytes(batch, num_q_heads, d, num_splits),
-              "workspace too small (see ftq_v1_workspace_bytes)");
-  FTQ_REQUIRE(aligned16(query) && aligned16(out) && aligned16(workspace) && aligned4(kv_cache),
-              "query, out and workspace must be 16-byte aligned, kv_cache 4-byte aligned");
-  V1Args a;
+  if (check_ws) {
+    FTQ_REQUIRE(workspace != nullptr, "null pointer argument");
+    FTQ_REQUIRE(workspace_bytes >= ftq_v1_workspace_bytes(batch, num_q_heads, d, num_splits),
+                "workspace too small (see ftq_v1_workspace_bytes)");
+    FTQ_REQUIRE(aligned16(workspace), "workspace must be 16-byte aligned");
+  }
+  FTQ_REQUIRE(aligned16(query) && aligned16(out) && aligned4(kv_cache),
+              "query and out must be 16-byte aligned, kv_cache 4-byte aligned");
   a.q = query; a.qt = q_dtype; a.cache = kv_cache; a.bt = block_table; a.sl = seq_lens; a.ks = kv_start;
   a.B = batch; a.hq = num_q_heads; a.hkv = num_kv_heads; a.max_blocks = max_blocks_per_seq;
   a.lbs = 0;
@@ -1442,10 +1448,14 @@ extern "C" int ftq_v1_decode_attention_rot(
   a.qscale = (rotation != nullptr ? 1.f : fwht_scale(d)) * scale * 1.4426950408889634f;
   a.rot = rotation;
   a.splits = num_splits; a.vrot = v_rotate;
-  a.wo = static_cast<float*>(workspace);
-  a.wl = a.wo + (int64_t)batch * num_q_heads * num_splits * d;
   a.out = out; a.ot = out_dtype; a.lse = lse_out;
+  return FTQ_OK;
+}
+
+// The launches for prepared arguments (a.wo / a.wl set).
+int v1_attn_launch(const V1Args& a, int d, int key_bits, int value_bits, int v_rotate, void* stream) {
   hipStream_t st = (hipStream_t)stream;
+  const bool kf8 = (v_rotate & V1F_KFP8) != 0;
   hipError_t e;
   // the matrix-core kernels: head_dim 128, 2-4 bit codes, f16 operands; every
   // other format, and fp32 products on request, on the VALU kernel
@@ -1456,6 +1466,26 @@ extern "C" int ftq_v1_decode_attention_rot(
   else if (key_bits == 3) e = v1_launch_attn2<128, 3>(value_bits, a, st);
   else e = v1_launch_attn2<128, 4>(value_bits, a, st);
   return hip_status(e);
+}
+}  // namespace
+
+extern "C" int ftq_v1_decode_attention_rot(
+    const void* query, int q_dtype, const uint8_t* kv_cache, int64_t num_blocks, int block_size,
+    int64_t stride_block, int64_t stride_pos, int64_t stride_head, const int32_t* block_table,
+    int max_blocks_per_seq, const int32_t* seq_lens, const int32_t* kv_start, int batch,
+    int num_q_heads, int num_kv_heads, int d, const float* centroids, int key_bits,
+    int value_bits, float scale, int v_rotate, int num_splits, void* workspace,
+    int64_t workspace_bytes, void* out, int out_dtype, float* lse_out, const float* rotation,
+    void* stream) {
+  V1Args a;
+  const int rc = v1_attn_prepare(a, query, q_dtype, kv_cache, num_blocks, block_size, stride_block, stride_pos,
+                                 stride_head, block_table, max_blocks_per_seq, seq_lens, kv_start, batch,
+                                 num_q_heads, num_kv_heads, d, centroids, key_bits, value_bits, scale, v_rotate,
+                                 num_splits, workspace, workspace_bytes, true, out, out_dtype, lse_out, rotation);
+  if (rc != FTQ_OK || batch == 0) return rc;
+  a.wo = static_cast<float*>(workspace);
+  a.wl = a.wo + (int64_t)batch * num_q_heads * num_splits * d;
+  return v1_attn_launch(a, d, key_bits, value_bits, v_rotate, stream);
 }
 
 extern "C" int ftq_v1_decode_attention_lse(
@@ -1530,6 +1560,12 @@ extern "C" int ftq_v1_decode_attention_noalloc(
     int num_q_heads, int num_kv_heads, int d, const float* centroids, int key_bits,
     int value_bits, float scale, int v_rotate, int num_splits, void* out, int out_dtype,
     void* stream) {
+  V1Args a;
+  int rc = v1_attn_prepare(a, query, q_dtype, kv_cache, num_blocks, block_size, stride_block, stride_pos,
+                           stride_head, block_table, max_blocks_per_seq, seq_lens, kv_start, batch, num_q_heads,
+                           num_kv_heads, d, centroids, key_bits, value_bits, scale, v_rotate, num_splits, nullptr,
+                           0, false, out, out_dtype, nullptr, nullptr);
+  if (rc != FTQ_OK) return rc;
   const int64_t need = ftq_v1_workspace_bytes(batch, num_q_heads, d, num_splits);
   FTQ_REQUIRE(need >= 0, "bad batch / head / split counts");
   FTQ_REQUIRE(need <= kV1ScratchBytes,
@@ -1544,10 +1580,9 @@ extern "C" int ftq_v1_decode_attention_noalloc(
     FTQ_REQUIRE(cur == sdev, "stream belongs to another device than the current one");
   }
   void* ws = nullptr;
-  const int rc = current_scratch(&ws);
+  rc = current_scratch(&ws);
   if (rc != FTQ_OK) return rc;
-  return ftq_v1_decode_attention(query, q_dtype, kv_cache, num_blocks, block_size, stride_block, stride_pos,
-                                 stride_head, block_table, max_blocks_per_seq, seq_lens, kv_start, batch,
-                                 num_q_heads, num_kv_heads, d, centroids, key_bits, value_bits, scale,
-                                 v_rotate, num_splits, ws, kV1ScratchBytes, out, out_dtype, stream);
+  a.wo = static_cast<float*>(ws);
+  a.wl = a.wo + (int64_t)batch * num_q_heads * num_splits * d;
+  return v1_attn_launch(a, d, key_bits, value_bits, v_rotate, stream);
 }

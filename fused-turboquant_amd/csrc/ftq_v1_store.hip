@@ -94,7 +94,7 @@ int v1_store_checks(int d, int key_bits, int value_bits, int64_t n_tokens, int n
   FTQ_REQUIRE(dtype >= F32 && dtype <= BF16, "dtype must be FTQ_F32, FTQ_F16 or FTQ_BF16");
   const V1Geom g = v1_geom(d, key_bits, value_bits, (v_rotate & V1F_KFP8) != 0);
   FTQ_REQUIRE(stride_head >= g.raw, "stride_head is smaller than the slot bytes (see ftq_v1_slot_bytes)");
-  FTQ_REQUIRE(stride_pos >= stride_head * num_kv_heads && stride_block >= stride_pos * block_size,
+  FTQ_REQUIRE(cache_strides_ok(num_blocks, stride_block, stride_pos, stride_head, num_kv_heads, block_size),
               "kv_cache strides must describe [num_blocks][block_size][num_kv_heads][slot]");
   FTQ_REQUIRE(stride_head % 4 == 0 && stride_pos % 4 == 0 && stride_block % 4 == 0,
               "kv_cache strides must be multiples of 4 bytes");

@@ -275,9 +275,9 @@ int ftq_v1_store_blockdiag(const void* key, const void* value, int dtype, int64_
 /* Workspace bytes ftq_v1_decode_attention needs: batch*Hq*splits*(d+1)*4. */
 int64_t ftq_v1_workspace_bytes(int batch, int num_q_heads, int d, int num_splits);
 /* Split-K factor that fills the GPU for this shape (host-side heuristic): 1
- * once batch*Hkv >= 384, where ftq_v1_decode_attention writes the output from
- * the attention kernel itself (no merge launch, workspace unused) unless a
- * caller rotation matrix is given. */
+ * once batch*Hkv >= 384.  With one split ftq_v1_decode_attention writes the
+ * output from the attention kernel itself (no merge launch; the workspace is
+ * still checked but not written) unless a caller rotation matrix is given. */
 int ftq_v1_default_splits(int batch, int num_kv_heads, int max_seq_len);
 
 /*

@@ -97,11 +97,12 @@ def test_noalloc_rejects_shapes_beyond_the_scratch(cuda):
     layer, cache, q, bt, sl = _case(cuda, 3, 1, 4, 2, [64], 4, 2, False)
     B, hq, d = q.shape
     nb, bs, hkv, _ = cache.shape
-    # 64 * 64 * 1024 * 129 * 4 bytes of partials > 16 MiB: rejected before any launch
-    out = torch.empty(64, 64, d, dtype=torch.bfloat16, device=cuda)
+    # 64 * 32 * 1024 * 129 * 4 bytes of partials > 16 MiB (an otherwise valid
+    # shape: GQA 16): rejected before any launch
+    out = torch.empty(64, 32, d, dtype=torch.bfloat16, device=cuda)
     rc = L.ftq_v1_decode_attention_noalloc(
         q.data_ptr(), _lib.BF16, cache.data_ptr(), nb, bs, cache.stride(0), cache.stride(1), cache.stride(2),
-        bt.data_ptr(), bt.shape[1], sl.data_ptr(), None, 64, 64, hkv, d, layer.centroids.data_ptr(),
+        bt.data_ptr(), bt.shape[1], sl.data_ptr(), None, 64, 32, hkv, d, layer.centroids.data_ptr(),
         4, 2, 0.088, 0, 1024, out.data_ptr(), _lib.BF16, _lib.stream_ptr(cuda))
     assert rc == -1
     assert b"16 MiB" in L.ftq_last_error()
