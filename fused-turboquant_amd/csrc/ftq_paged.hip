@@ -337,7 +337,7 @@ __global__ __launch_bounds__(256) void paged_store_mfma_kernel(
     float t[32 * NB];
     float nrm;
     // The cache writes are non-temporal (streamed past the caches, which then
-    // hold the K / V reads): 9% faster on a config-3 chunk.  (Full-line fp32
+    // hold the K / V reads): 9% faster on 65 536 tokens x 8 heads, K3 V3.  (Full-line fp32
     // output streams, as the decoder's, measured 2x slower that way.)
     {  // K: codes per token, block b's BK words of token j at word BK (4 b + q) of its row
       const float sv = rotate(key, t0, head, ksm, t, nrm);

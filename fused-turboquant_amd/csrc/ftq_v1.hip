@@ -774,7 +774,8 @@ __global__ __launch_bounds__(256, 2) void v1_attn_kernel(
   // The uniform V codes enter the P.V MFMAs as 2^e (1 + q 2^-k): the sums
   // carry an offset, sum p sc (u_run), that the epilogue subtracts.  Its fp32
   // rounding grows with the tiles summed (a wave of ~950 tiles erred by 8e-2
-  // on config 4), so every 16 tiles the offset so far leaves both sums.
+  // on fp32 outputs of a 122K-position sequence, K4 V2), so every 16 tiles
+  // the offset so far leaves both sums.
   int since = 0;
   auto rebase = [&]() __attribute__((always_inline)) {
     if constexpr (!VLM) {
@@ -870,7 +871,8 @@ template <int VB> __host__ __device__ constexpr int v1_vpos(int bb) {
        : (bb <= 2 ? 3 * bb : bb <= 5 ? 3 * bb - 8 : 3 * bb - 16);
 }
 
-// 2-bit V: 4 workgroups per CU (<= 128 VGPRs, no spills; config 4 ran 83 us
+// 2-bit V: 4 workgroups per CU (<= 128 VGPRs, no spills; B = 4, 32 / 8 heads,
+// 64K-128K positions, K4 V2 ran 83 us
 // against 90 us at 3 per CU); 3- and 4-bit V need more registers
 template <int D, int KB, int VB, int QT>
 __global__ __launch_bounds__(256, VB == 2 ? 4 : 2) void v1_attn_g4_kernel(
@@ -1167,9 +1169,10 @@ __global__ __launch_bounds__(256, VB == 2 ? 4 : 2) void v1_attn_g4_kernel(
   };
   // The V codes enter the P.V MFMAs as 2^e (1 + q 2^-k): the sums carry an
   // offset, sum p sc (u_run), that the epilogue subtracts.  Its fp32 rounding
-  // grows with the tiles summed (a wave of ~950 tiles erred by 8e-2 on config
-  // 4), so every 16 tiles the offset so far leaves both sums (acc column m < 4
-  // is head lane & 3, whose compact lanes head_sum adds).
+  // grows with the tiles summed (a wave of ~950 tiles erred by 8e-2 on fp32
+  // outputs of a 122K-position sequence, K4 V2), so every 16 tiles the offset
+  // so far leaves both sums (acc column m < 4 is head lane & 3, whose compact
+  // lanes head_sum adds).
   int since = 0;
   auto rebase = [&]() __attribute__((always_inline)) {
     if (++since == 16) {
@@ -1384,9 +1387,9 @@ extern "C" int64_t ftq_v1_workspace_bytes(int batch, int num_q_heads, int d, int
 
 extern "C" int ftq_v1_default_splits(int batch, int num_kv_heads, int max_seq_len) {
   // 384 or more (batch, kv head) workgroups already give each CU 1.5 of them:
-  // one split writes the output directly and saves the merge launch (config
-  // 5's shape, 64 x 8 units over 2176 positions: 44.1 us at one split against
-  // 49.7 us at two)
+  // one split writes the output directly and saves the merge launch (64
+  // sequences x 8 kv heads over ~2200 positions, K3 V3: 39.8 us at one split
+  // against 49.5 us at two)
   if ((int64_t)batch * num_kv_heads >= 384) return 1;
   return auto_splits(batch, num_kv_heads, max_seq_len, 1024);
 }

@@ -174,7 +174,8 @@ int ftq_paged_decode_attention(const void* query, int q_dtype, const uint8_t* kv
  * (kernels/triton_flash_decode.py:66-221); same arguments and semantics.
  * Always the split form (stage 1 into the workspace, then the merge + inverse
  * RHT launch).  d = 128 and at most 4 query heads per kv head.  About 2.3x the
- * time of the default matrix-core form at BASELINE config 3.
+ * time of the default matrix-core form at B = 32, 32 / 8 heads, 8192
+ * positions, 3-bit K and V.
  */
 int ftq_paged_decode_attention_valu(const void* query, int q_dtype, const uint8_t* kv_cache,
                                     const int32_t* block_table, const int32_t* seq_lens, int batch,

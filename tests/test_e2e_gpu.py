@@ -1,4 +1,4 @@
-"""BASELINE config 5 at reduced size: a Llama-architecture decoder driven the
+"""The end-to-end decode benchmark at reduced size: a Llama-architecture decoder driven the
 way vLLM's v1 runner drives the TURBOQUANT backend (reference
 vllm_plugin/v1_backend.py:646-686 do_kv_cache_update, :755-836 forward):
 K3V3, kind rht, TURBOQUANT_BOUNDARY_PROTECT=0, TURBOQUANT_V_ROTATE=1, block

@@ -158,7 +158,7 @@ def test_paged_choose_splits_host_heuristic():
     from fused_turboquant import paged as P
     L = P._bind()
     dflt = L.ftq_paged_default_splits
-    assert P.default_splits(32, 8, 8192, 32, 128) == 1       # config 3: 256 workgroups
+    assert P.default_splits(32, 8, 8192, 32, 128) == 1       # B 32 x 8 kv heads: 256 workgroups
     assert P.default_splits(64, 8, 8192, 32, 128) == 1       # two full rounds
     assert P.default_splits(48, 8, 8192, 32, 128) == 1       # 384 of 512 slots: 3/4
     assert P.default_splits(40, 8, 8192, 32, 128) == dflt(40, 8, 8192)  # 320 of 512: below 3/4

@@ -288,7 +288,7 @@ def test_store_then_decode_end_to_end(cuda):
 
 
 def test_config4_full_size(cuda):
-    """K4V2, v_rotate, B=4, 32/8 heads, ctx ~ U[65536, 131072],
+    """The v1 benchmark shape: K4V2, v_rotate, B=4, 32/8 heads, ctx ~ U[65536, 131072],
     2% of tokens x8.  Oracle on a subset of (sequence, kv head); split-count
     invariance over the whole output."""
     from fused_turboquant import v1
