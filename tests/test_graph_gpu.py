@@ -79,7 +79,8 @@ def test_paged_decode_under_graph(cuda, splits):
     _replay_check(cuda, refill, eager, lambda: out_g, g, f"paged decode splits={splits}")
 
 
-def test_v1_decode_under_graph(cuda):
+@pytest.mark.parametrize("splits", [1, 5])  # one launch writing the output itself, split form + merge launch
+def test_v1_decode_under_graph(cuda, splits):
     from fused_turboquant import v1
     d, bs, hkv, hq, kb, vb = 128, 16, 4, 16, 4, 2
     layer = v1.TurboQuantV1Layer(d, kb, vb, v_rotate=True, device=cuda)
@@ -92,7 +93,6 @@ def test_v1_decode_under_graph(cuda):
     bt = (slots.view(B, L)[:, ::bs] // bs).to(torch.int32).contiguous()  # any page ids: values need not match
     sl = torch.full((B,), L, dtype=torch.int32, device=cuda)
     q = torch.randn(B, hq, d, device=cuda).to(torch.bfloat16)
-    splits = 5
     out_g = torch.empty(B, hq, d, dtype=torch.bfloat16, device=cuda)
     ws = torch.empty(v1.workspace_bytes(B, hq, d, splits), dtype=torch.uint8, device=cuda)
     g = _capture(lambda: layer.decode(q, cache, bt, sl, num_splits=splits, out=out_g, workspace=ws))
@@ -102,7 +102,7 @@ def test_v1_decode_under_graph(cuda):
         sl.fill_(L - 100 * rep)
 
     _replay_check(cuda, refill, lambda: layer.decode(q, cache, bt, sl, num_splits=splits), lambda: out_g, g,
-                  "v1 decode")
+                  f"v1 decode splits={splits}")
 
 
 def test_raw_decode_under_graph(cuda):
