@@ -46,6 +46,7 @@
 #include "ftq_v1_dev.h"
 
 #include <cmath>
+#include <type_traits>
 #include <mutex>
 
 namespace ftq {
@@ -266,14 +267,27 @@ struct V1A {
   static_assert(KQ % 4 == 0, "K lane chunk must be whole dwords");
 };
 
-template <int D, int KB, int VB>
+template <int D, int KB, int VB, bool DEFER>
 struct V1Tile {
   using A = V1A<D, KB, VB>;
   uint32_t k[2][A::KQW];  // per S-tile: K code dwords of token (lane & 15), bytes (lane >> 4) * KQ
-  uint32_t v[A::NV];      // V codes of the lane's 8 tokens (see v1_load)
-  uint32_t tail[2];       // per S-tile: K norm / V scale / V min (by lane >> 4), f16 bits
+  // V codes of the lane's 8 tokens (see v1_load).  DEFER: as loaded, 16 bits
+  // each; operand word j is va[j] | vb[j] << 16, formed where it is used, in
+  // the next tile's step -- formed at the load, the OR waits in the loading
+  // step for loads it has just issued, a full memory round trip per step.
+  // Without DEFER (where the registers are not there) va holds the words.
+  // The halves stay 16-bit values until then, so that no zero-extension
+  // either is computed in the loading step.
+  using VH = typename std::conditional<DEFER, uint16_t, uint32_t>::type;
+  VH va[A::NV];
+  uint16_t vb[DEFER ? A::NV : 1];
+  uint16_t tail[2];       // per S-tile: K norm / V scale / V min (by lane >> 4), f16 bits
   uint32_t vt[2][4];      // Lloyd-Max V only: token (lane & 15)'s V codes, bytes (lane >> 4) * 16 ..
   bool ok[2];             // wave-uniform: S-tile has a real page
+  __device__ __forceinline__ uint32_t vword(int j) const {
+    if constexpr (DEFER) return (uint32_t)va[j] | ((uint32_t)vb[j] << 16);
+    else return va[j];
+  }
 };
 
 // Loads of one 32-token tile, as raw buffer loads: one wave-uniform buffer
@@ -306,29 +320,44 @@ __device__ __forceinline__ void v1_addr_rows(V1Addr& ad, const int32_t* bt_row, 
   ad.nb32 = (int)min(num_blocks, (int64_t)0x7fffffff);
 }
 
+// Is S-tile st of `tile` a real position range with a block-table entry?
+__device__ __forceinline__ bool v1_stile_ok(const V1Addr& ad, int tile, int st, bool active) {
+  const int pos0 = tile * 32 + st * 16;
+  return active && pos0 < ad.seq_len && (pos0 >> ad.lbs) < ad.max_blocks;
+}
+
 // Block-table entries of a tile's two S-tiles, as a vector load issued one tile
-// ahead of the loads that need them (lane l holds S-tile l & 1; -1 when the
-// S-tile is inactive, past seq_len or past the row).  A vector load retires in
-// order, so the wait before v1_load's readlane covers only this load.
+// ahead of the loads that need them (lane l holds S-tile l & 1; entry 0 is
+// read where the S-tile is inactive, past seq_len or past the row).  LATE:
+// the entry is returned as loaded and v1_load makes the inactive ones -1,
+// so nothing in the fetching step waits for this load; otherwise -1 here.
+// A vector load retires in order, so the wait before v1_load's readlane
+// covers only this load.
+template <bool LATE>
 __device__ __forceinline__ int v1_fetch_bt(const V1Addr& ad, int tile, bool active, int lane) {
-  const int pos0 = tile * 32 + (lane & 1) * 16;
-  const int page = pos0 >> ad.lbs;
-  const bool ok = active && pos0 < ad.seq_len && page < ad.max_blocks;
+  const bool ok = v1_stile_ok(ad, tile, lane & 1, active);
+  const int page = (tile * 32 + (lane & 1) * 16) >> ad.lbs;
   const int v = (int)__builtin_amdgcn_raw_buffer_load_b32(ad.bt_rs, (uint32_t)(ok ? page : 0) * 4u, 0, 0);
-  return ok ? v : -1;
+  if constexpr (LATE) return v;
+  else return ok ? v : -1;
 }
 
 __device__ __forceinline__ uint32_t buf_u16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
   return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0);
 }
 
-template <int D, int KB, int VB, bool VLM = false>
-__device__ __forceinline__ void v1_load(V1Tile<D, KB, VB>& r, const V1Addr& ad, int tile, int btv) {
+// DEFER tiles take their block-table entries from v1_fetch_bt<true> (the
+// inactive test here); the others from v1_fetch_bt<false>.
+template <int D, int KB, int VB, bool VLM = false, bool DEFER>
+__device__ __forceinline__ void v1_load(V1Tile<D, KB, VB, DEFER>& r, const V1Addr& ad, int tile, bool active,
+                                        int btv) {
   using A = V1A<D, KB, VB>;
 #pragma unroll
   for (int st = 0; st < 2; ++st) {
     const int pos0 = tile * 32 + st * 16;
-    int phys = __builtin_amdgcn_readlane(btv, st);
+    int phys;
+    if constexpr (DEFER) phys = v1_stile_ok(ad, tile, st, active) ? __builtin_amdgcn_readlane(btv, st) : -1;
+    else phys = __builtin_amdgcn_readlane(btv, st);
     const bool valid = (uint32_t)phys < (uint32_t)ad.nb32;  // -1 (no entry) and ids >= num_blocks fail
     if (!valid) phys = 0;
     const uint32_t within = valid ? (uint32_t)(pos0 & ((1 << ad.lbs) - 1)) : 0u;
@@ -346,7 +375,7 @@ __device__ __forceinline__ void v1_load(V1Tile<D, KB, VB>& r, const V1Addr& ad, 
       const uint2 k = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs, ad.koff, 0, 0));
       r.k[st][0] = k.x; r.k[st][1] = k.y;
     }
-    r.tail[st] = buf_u16(rs, ad.toff, 0);
+    r.tail[st] = (uint16_t)buf_u16(rs, ad.toff, 0);
     if constexpr (VLM) {
       const uint4 x = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, ad.vtoff, 0, 0));
       r.vt[st][0] = x.x; r.vt[st][1] = x.y; r.vt[st][2] = x.z; r.vt[st][3] = x.w;
@@ -356,24 +385,26 @@ __device__ __forceinline__ void v1_load(V1Tile<D, KB, VB>& r, const V1Addr& ad, 
       // scalar offset of token 4g+i; uniform, but LLVM otherwise keeps the
       // i >= 2 products in VGPRs and wraps each load in a waterfall loop
       const uint32_t so = __builtin_amdgcn_readfirstlane((uint32_t)i * ad.s_pos);
+      // half (i & 1) of word w: into vb[w] (DEFER) or the high half of va[w]
+      auto put = [&](int w, int half, uint32_t x) __attribute__((always_inline)) {
+        if constexpr (DEFER) {
+          if (half) r.vb[w] = (uint16_t)x;
+          else r.va[w] = (uint16_t)x;
+        } else {
+          if (half) r.va[w] |= x << 16;
+          else r.va[w] = x;
+        }
+      };
       if constexpr (VB == 2) {
-        const uint32_t h = buf_u16(rs, ad.voff, so);
-        if (i & 1) r.v[2 * st + (i >> 1)] |= h << 16;
-        else r.v[2 * st + (i >> 1)] = h;
+        put(2 * st + (i >> 1), i & 1, buf_u16(rs, ad.voff, so));
       } else if constexpr (VB == 4) {
         const uint32_t lo = buf_u16(rs, ad.voff, so);
         const uint32_t hi = buf_u16(rs, ad.voff + 2u, so);
-        if (i & 1) {
-          r.v[2 * st + (i >> 1)] |= lo << 16;
-          r.v[4 + 2 * st + (i >> 1)] |= hi << 16;
-        } else {
-          r.v[2 * st + (i >> 1)] = lo;
-          r.v[4 + 2 * st + (i >> 1)] = hi;
-        }
+        put(2 * st + (i >> 1), i & 1, lo);
+        put(4 + 2 * st + (i >> 1), i & 1, hi);
       } else {
-        const uint32_t lo = buf_u16(rs, ad.voff, so);
-        const uint32_t hi = buf_u16(rs, ad.voff + 2u, so);
-        r.v[4 * st + i] = lo | (hi << 16);
+        put(4 * st + i, 0, buf_u16(rs, ad.voff, so));
+        put(4 * st + i, 1, buf_u16(rs, ad.voff + 2u, so));
       }
     }
     r.ok[st] = valid;
@@ -523,13 +554,15 @@ __global__ __launch_bounds__(256, 2) void v1_attn_kernel(
   const uint32_t sel1 = (o3 + 1) | ((o3 + 2) << 8) | ((o3 + 5) << 16) | ((o3 + 6) << 24);
 
   // the first tile's loads (two register sets: the next tile's loads overlap
-  // this tile's math, and the block-table entries come one tile further ahead)
-  V1Tile<D, KB, VB> ra, rb;
+  // this tile's math, and the block-table entries come one tile further ahead).
+  // V words formed at the load: deferred, the raw halves would cost this
+  // kernel a wave per SIMD at several widths (e.g. K2 V3 165 -> 187 VGPRs).
+  V1Tile<D, KB, VB, false> ra, rb;
   int tile = t_begin + wave_u;
   int btv = 0;
   if (tile < t_end) {
-    v1_load<D, KB, VB, VLM>(ra, ad, tile, v1_fetch_bt(ad, tile, true, lane));
-    btv = v1_fetch_bt(ad, tile + 4, tile + 4 < t_end, lane);
+    v1_load<D, KB, VB, VLM>(ra, ad, tile, true, v1_fetch_bt<false>(ad, tile, true, lane));
+    btv = v1_fetch_bt<false>(ad, tile + 4, tile + 4 < t_end, lane);
   }
 
   if (qg < G) {
@@ -576,7 +609,7 @@ __global__ __launch_bounds__(256, 2) void v1_attn_kernel(
   for (int i = 0; i < NB; ++i) acc[i] = floatx4{0.f, 0.f, 0.f, 0.f};
 
   constexpr float TAU = 8.f;  // p <= 2^TAU
-  auto process = [&](const V1Tile<D, KB, VB>& cur, int tile) __attribute__((always_inline)) {
+  auto process = [&](const V1Tile<D, KB, VB, false>& cur, int tile) __attribute__((always_inline)) {
     // scores and Gram diagonal per S-tile; the per-token fields (K norm, V
     // scale, V min, sum C^2) go to the score layout (lane (n, g) holds tokens
     // 4g+i) through LDS
@@ -737,12 +770,15 @@ __global__ __launch_bounds__(256, 2) void v1_attn_kernel(
     }
     }
     l_run += psum;
+    uint32_t cv[A::NV];  // the V operand words
+#pragma unroll
+    for (int k = 0; k < A::NV; ++k) cv[k] = cur.vword(k);
     uint32_t w3[8];
     if constexpr (VB == 3) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        w3[2 * j] = __builtin_amdgcn_perm(cur.v[2 * j + 1], cur.v[2 * j], sel0);
-        w3[2 * j + 1] = __builtin_amdgcn_perm(cur.v[2 * j + 1], cur.v[2 * j], sel1);
+        w3[2 * j] = __builtin_amdgcn_perm(cv[2 * j + 1], cv[2 * j], sel0);
+        w3[2 * j + 1] = __builtin_amdgcn_perm(cv[2 * j + 1], cv[2 * j], sel1);
       }
     }
 #pragma unroll
@@ -754,7 +790,7 @@ __global__ __launch_bounds__(256, 2) void v1_attn_kernel(
         Op8 alo;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const uint32_t X = bb < 4 ? cur.v[j] : cur.v[4 + j];
+          const uint32_t X = bb < 4 ? cv[j] : cv[4 + j];
           const uint32_t idx = __builtin_amdgcn_ubfe(X, 4 * (bb & 3), 4) |
                                (__builtin_amdgcn_ubfe(X, 16 + 4 * (bb & 3), 4) << 4);
           const uint2 e = lutv[idx];
@@ -764,7 +800,7 @@ __global__ __launch_bounds__(256, 2) void v1_attn_kernel(
         acc[bb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo.h, pb.h, acc[bb], 0, 0, 0);
       } else {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) a.u[j] = v1_vpair<VB>(cur.v, w3, j, bb, ex[j]);
+        for (int j = 0; j < 4; ++j) a.u[j] = v1_vpair<VB>(cv, w3, j, bb, ex[j]);
       }
       acc[bb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a.h, pb.h, acc[bb], 0, 0, 0);
       acc[bb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a.h, pl.h, acc[bb], 0, 0, 0);
@@ -791,15 +827,15 @@ __global__ __launch_bounds__(256, 2) void v1_attn_kernel(
   // each wave takes every 4th tile (a fixed assignment, so the sums and the
   // output bits do not depend on how fast the waves progress)
   while (tile < t_end) {
-    int btn = v1_fetch_bt(ad, tile + 8, tile + 8 < t_end, lane);
-    v1_load<D, KB, VB, VLM>(rb, ad, tile + 4, btv);
+    int btn = v1_fetch_bt<false>(ad, tile + 8, tile + 8 < t_end, lane);
+    v1_load<D, KB, VB, VLM>(rb, ad, tile + 4, true, btv);
     btv = btn;
     process(ra, tile);
     rebase();
     tile += 4;
     if (tile >= t_end) break;
-    btn = v1_fetch_bt(ad, tile + 8, tile + 8 < t_end, lane);
-    v1_load<D, KB, VB, VLM>(ra, ad, tile + 4, btv);
+    btn = v1_fetch_bt<false>(ad, tile + 8, tile + 8 < t_end, lane);
+    v1_load<D, KB, VB, VLM>(ra, ad, tile + 4, true, btv);
     btv = btn;
     process(rb, tile);
     rebase();
@@ -957,12 +993,18 @@ __global__ __launch_bounds__(256, VB == 2 ? 4 : 2) void v1_attn_g4_kernel(
 
   // the first tile's loads (two register sets: the next tile's loads overlap
   // this tile's math, and the block-table entries come one tile further ahead)
-  V1Tile<D, KB, VB> ra, rb;
+  // DEFER (3- and 4-bit V): the V words and the block-table test are formed
+  // in the step that uses them, so no wait in a loading step covers the
+  // loads it has just issued (two splits over 64 x 8 (batch, kv head) units,
+  // K3 V3: 49.6 -> 44.2 us).  2-bit V forms them at the load: deferred, its
+  // registers would pass the 128 of 4 workgroups per CU.
+  constexpr bool DEFER = VB != 2;
+  V1Tile<D, KB, VB, DEFER> ra, rb;
   int tile = t_begin + wave_u;
   int btv = 0;
   if (tile < t_end) {
-    v1_load(ra, ad, tile, v1_fetch_bt(ad, tile, true, lane));
-    btv = v1_fetch_bt(ad, tile + 4, tile + 4 < t_end, lane);
+    v1_load(ra, ad, tile, true, v1_fetch_bt<DEFER>(ad, tile, true, lane));
+    btv = v1_fetch_bt<DEFER>(ad, tile + 4, tile + 4 < t_end, lane);
   }
 
   if (qg < G) {
@@ -1010,7 +1052,7 @@ __global__ __launch_bounds__(256, VB == 2 ? 4 : 2) void v1_attn_g4_kernel(
   for (int i = 0; i < NB; ++i) acc[i] = floatx4{0.f, 0.f, 0.f, 0.f};
 
   constexpr float TAU = 8.f;  // p <= 2^TAU
-  auto process = [&](const V1Tile<D, KB, VB>& cur, int tile) __attribute__((always_inline)) {
+  auto process = [&](const V1Tile<D, KB, VB, DEFER>& cur, int tile) __attribute__((always_inline)) {
     floatx4 sacc[2];
     wave_lds_fence();
 #pragma unroll
@@ -1133,13 +1175,14 @@ __global__ __launch_bounds__(256, VB == 2 ? 4 : 2) void v1_attn_g4_kernel(
     for (int j = 0; j < A::NV; ++j) {
       if constexpr (VB == 3) {
         if (j < 4) {
-          vw[0][j] = __builtin_amdgcn_perm(cur.v[2 * j + 1], cur.v[2 * j], sel0);
-          vw[1][j] = __builtin_amdgcn_perm(cur.v[2 * j + 1], cur.v[2 * j], sel1);
-          vw[2][j] = __builtin_amdgcn_perm(cur.v[2 * j + 1], cur.v[2 * j], sel2);
+          const uint32_t v0 = cur.vword(2 * j), v1 = cur.vword(2 * j + 1);
+          vw[0][j] = __builtin_amdgcn_perm(v1, v0, sel0);
+          vw[1][j] = __builtin_amdgcn_perm(v1, v0, sel1);
+          vw[2][j] = __builtin_amdgcn_perm(v1, v0, sel2);
         }
       } else {
-        vw[0][j] = cur.v[j];
-        vw[1][j] = cur.v[j] >> 8;
+        vw[0][j] = cur.vword(j);
+        vw[1][j] = vw[0][j] >> 8;
       }
     }
 #pragma unroll
@@ -1186,15 +1229,15 @@ __global__ __launch_bounds__(256, VB == 2 ? 4 : 2) void v1_attn_g4_kernel(
   // each wave takes every 4th tile (a fixed assignment, so the sums and the
   // output bits do not depend on how fast the waves progress)
   while (tile < t_end) {
-    int btn = v1_fetch_bt(ad, tile + 8, tile + 8 < t_end, lane);
-    v1_load(rb, ad, tile + 4, btv);
+    int btn = v1_fetch_bt<DEFER>(ad, tile + 8, tile + 8 < t_end, lane);
+    v1_load(rb, ad, tile + 4, tile + 4 < t_end, btv);
     btv = btn;
     process(ra, tile);
     rebase();
     tile += 4;
     if (tile >= t_end) break;
-    btn = v1_fetch_bt(ad, tile + 8, tile + 8 < t_end, lane);
-    v1_load(ra, ad, tile + 4, btv);
+    btn = v1_fetch_bt<DEFER>(ad, tile + 8, tile + 8 < t_end, lane);
+    v1_load(ra, ad, tile + 4, tile + 4 < t_end, btv);
     btv = btn;
     process(rb, tile);
     rebase();
