@@ -143,6 +143,16 @@ def test_decode_batch(cuda, monkeypatch, dtype_str, vrot):
     _run_step(cuda, [(1, 1), (100, 1), (513, 1), (4000, 1)], dtype_str, 32, 8, vrot, monkeypatch, seed=1)
 
 
+@pytest.mark.parametrize("dtype_str,vrot", [("turboquant_3bit_nc", True), ("turboquant_k4v2_nc", False)])
+def test_decode_batch_one_split(cuda, monkeypatch, dtype_str, vrot):
+    """48 sequences x 8 kv heads: the Impl's split count is 1, where the decode
+    kernel writes the output itself (no merge launch)."""
+    from fused_turboquant import v1
+    assert v1.default_splits(48, 8, 400) == 1
+    seqs = [(1 + 7 * i, 1) for i in range(48)]
+    _run_step(cuda, seqs, dtype_str, 32, 8, vrot, monkeypatch, seed=48)
+
+
 def test_fresh_prefill_batch(cuda, monkeypatch):
     _run_step(cuda, [(0, 37), (0, 1), (0, 200)], "turboquant_3bit_nc", 16, 4, False, monkeypatch, seed=2)
 
