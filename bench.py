@@ -14,6 +14,9 @@ Also timed (not part of the step), each with a roofline entry:
     beside the default f16-operand matrix-core kernel;
   * config 4 (vLLM v1 slot format, K4V2, v_rotate, B=4, contexts
     U[65536, 131072]);
+  * one layer of config 5's decode-step attention (v1 slot format, K3V3,
+    v_rotate, B=64, contexts U[2048, 2304], one split: the kernel writes the
+    output, no merge launch);
   * the boundary-layer raw fp16 decode attention at the config-3 shape;
   * the stores: the v1 slot store (rht, and the block-diagonal rotations) at
     the reference's published shapes (1024 tokens x 8 kv heads and 1 token x 8
@@ -63,7 +66,7 @@ RAMP_S = 0.3  # untimed seconds of back-to-back steps before any timing (clock r
 TRAFFIC_BYTES: dict = {
     "encode_kv_d128_3bit": 160822360, "encode_kv_d128_3bit_same_input": 161017535,
     "encode_d128_3bit": 80597591, "encode_d256_3bit": 161826378, "decode_d128_3bit_f32": 149008797,
-    "decode_d256_3bit_f32": 295825734, "paged_attn_config3": 219891991, "v1_attn_config4": 406750850,
+    "decode_d256_3bit_f32": 295825734, "paged_attn_config3": 219891991, "v1_attn_config4": 406750850, "v1_attn_config5_decode": 144843675,
     "raw_attn_boundary": 1081599888, "v1_store_config4_chunk": 171769851,
     "paged_store_config3_chunk": 323828547,
 }
@@ -340,9 +343,41 @@ def make_config4(dev, seed=4):
     return layer, cache, q, bt.to(dev), sl, lens
 
 
+def make_config5_attn(dev, seed=6):
+    """One layer of config 5's decode step: the TURBOQUANT slot cache of a
+    64-sequence batch after its 2048-token prompts (turboquant_3bit_nc = K3V3,
+    rht, V rotated, 32 q / 8 kv heads, d 128, page 16), contexts
+    ~ U[2048, 2304] (the positions the 256 decode steps attend), K/V N(0,1)
+    bf16, block table a seeded permutation of the pages."""
+    import torch
+    from fused_turboquant import v1 as V1
+    d, bs, hkv, hq, kb, vb, B = 128, 16, 8, 32, 3, 3, 64
+    g = torch.Generator().manual_seed(seed)
+    lens = torch.randint(2048, 2305, (B,), generator=g).tolist()
+    layer = V1.TurboQuantV1Layer(d, kb, vb, v_rotate=True, device=dev)
+    pages = [(n + bs - 1) // bs for n in lens]
+    nb = sum(pages)
+    cache = torch.zeros(layer.kv_cache_shape(nb, bs, hkv), dtype=torch.uint8, device=dev)
+    perm = torch.randperm(nb, generator=g).to(torch.int32)
+    bt = torch.zeros(B, max(pages), dtype=torch.int32)
+    used = 0
+    gd = torch.Generator(device=dev).manual_seed(seed + 1)
+    for b, n in enumerate(lens):
+        bt[b, :pages[b]] = perm[used:used + pages[b]]
+        used += pages[b]
+        pos = torch.arange(n, device=dev)
+        k = torch.randn(n, hkv, d, generator=gd, device=dev).to(torch.bfloat16)
+        v = torch.randn(n, hkv, d, generator=gd, device=dev).to(torch.bfloat16)
+        layer.store(k, v, cache, bt[b].to(dev).long()[pos // bs] * bs + pos % bs)
+    q = torch.randn(B, hq, d, generator=g).to(torch.bfloat16).to(dev)
+    sl = torch.tensor(lens, dtype=torch.int32, device=dev)
+    return layer, cache, q, bt.to(dev), sl, lens
+
+
 def v1_setup(dev, cfg4=None, operands="f16"):
-    """The config-4 v1 decode; operands "fp32" = the fp32-product VALU kernel
-    (v_flags bit 3) over the same cache."""
+    """A v1 decode over a cache made by make_config4 (the default) or
+    make_config5_attn, at the library's default split count; operands "fp32"
+    = the fp32-product VALU kernel (v_flags bit 3) over the same cache."""
     import torch
     from fused_turboquant import _lib
     from fused_turboquant import v1 as V1
@@ -362,7 +397,7 @@ def v1_setup(dev, cfg4=None, operands="f16"):
                       bt, bt.shape[1], sl, None, B, hq, hkv, d, layer.centroids, layer.key_bits,
                       layer.value_bits, 1.0 / math.sqrt(d), flags, splits, ws, ws.numel(), out,
                       _lib.dtype_code(out.dtype), _lib.stream_ptr(dev))
-    per_tok = V1.slot_bytes(d, layer.key_bits, layer.value_bits)  # 66 B of K + 36 B of V
+    per_tok = V1.slot_bytes(d, layer.key_bits, layer.value_bits)  # K4V2: 66 B of K + 36 B of V
     kv_bytes = sum(lens) * hkv * per_tok
     total = kv_bytes + q.numel() * 2 + out.numel() * 2 + sum((n + 15) // 16 for n in lens) * 4 + B * 4
     return {"run": run, "kv_bytes": kv_bytes, "total_bytes": total, "splits": splits, "lens": lens,
@@ -668,6 +703,10 @@ def main():
         attn4 = v1_setup(dev)
         if want("v1_attn_config4_fp32_valu"):
             attn4v = v1_setup(dev, attn4["cfg4"], "fp32")
+    attn5 = None
+    if want("v1_attn_config5_decode"):
+        log("[bench] config5 decode-step attention, one layer (B=64 ctx~U[2048,2304] K3V3 v_rotate)")
+        attn5 = v1_setup(dev, make_config5_attn(dev))
     if want("raw_attn_boundary"):
         log("[bench] boundary-layer raw fp16 cache (config3 shape, 512 B slots)")
         attnr = raw_setup(dev)
@@ -752,6 +791,8 @@ def main():
         entry("v1_attn_config4", attn4["run"], attn4["total_bytes"])
     if attn4v is not None:
         entry("v1_attn_config4_fp32_valu", attn4v["run"], attn4v["total_bytes"])
+    if attn5 is not None:
+        entry("v1_attn_config5_decode", attn5["run"], attn5["total_bytes"])
     if attnr is not None:
         entry("raw_attn_boundary", attnr["run"], attnr["total_bytes"])
     for name, st in stores.items():
@@ -805,6 +846,8 @@ def main():
         cfg.update({"config4_attn_us_per_step": round(t_a4, 2),
                     "config4_kv_gbs": round(attn4["kv_bytes"] / (t_a4 * 1e-6) / 1e9, 1),
                     "config4_ctx": attn4["lens"], "config4_splits": attn4["splits"]})
+    if attn5 is not None and "v1_attn_config5_decode" in rl:
+        cfg.update({"config5_attn_splits": attn5["splits"]})
     out = {
         "metric": "3-bit d128 encode GB/s + paged decode-attn us/step @8K ctx; % of HBM peak",
         "value": round(enc_in_gbs, 1),
