@@ -23,13 +23,6 @@ union Op8 {
   half8 h;
 };
 
-template <int NDW>
-__device__ __forceinline__ void load_dwords(const uint8_t* p, uint32_t (&w)[NDW]) {
-  const uint32_t* q = reinterpret_cast<const uint32_t*>(p);
-#pragma unroll
-  for (int i = 0; i < NDW; ++i) w[i] = q[i];
-}
-
 // entry_bytes * bits [P, P+W) of a little-endian multi-dword value: the byte
 // offset of a table entry (P, W compile-time after unrolling)
 template <int SH, int N>
