@@ -235,6 +235,49 @@ def test_decode_single_split_direct_output(cuda, hq, hkv, vrot, lloyd, odt):
     assert v1.default_splits(48, 8, 4096) == 1 and v1.default_splits(4, 8, 131072) > 1
 
 
+@pytest.mark.parametrize("case", range(24))
+def test_decode_random_shapes(cuda, case):
+    """Seeded random configurations of the matrix-core decode: GQA group 1..16,
+    K and V widths 2..4, V rotated or not (Lloyd-Max V at 4 bits), 1..40
+    splits, block sizes 16..64, ragged contexts with empty and offset ranges
+    (kv_start), bf16 / fp16 / fp32 queries and outputs, against the oracle."""
+    from fused_turboquant import v1
+    rng = np.random.default_rng(1000 + case)
+    d = 128
+    hkv = int(rng.choice([1, 2, 4, 8]))
+    G = int(rng.choice([1, 2, 3, 4, 8, 16]))
+    hq = hkv * G
+    kb, vb = int(rng.integers(2, 5)), int(rng.integers(2, 5))
+    lloyd = vb == 4 and rng.random() < 0.5
+    vrot = lloyd or rng.random() < 0.5
+    bs = int(rng.choice([16, 32, 64]))
+    B = int(rng.integers(1, 7))
+    lens = [int(x) for x in rng.integers(0, 700, B)]
+    starts = [int(rng.integers(0, L + 1)) if rng.random() < 0.4 else 0 for L in lens]
+    splits = int(rng.choice([1, 2, 3, 7, 16, 40]))
+    qdt = [torch.bfloat16, torch.float16, torch.float32][int(rng.integers(0, 3))]
+    odt = [torch.bfloat16, torch.float16, torch.float32][int(rng.integers(0, 3))]
+    mb = max(1, max((L + bs - 1) // bs for L in lens))
+    nb = mb * B + 3
+    g = torch.Generator().manual_seed(case)
+    cache, c = _oracle_cache(g, nb, bs, hkv, d, kb, vb, nb * bs, vrot, lloyd=lloyd)
+    bt = torch.stack([torch.randperm(nb, generator=g)[:mb] for _ in range(B)]).to(torch.int32)
+    q = torch.randn(B, hq, d, generator=g).to(qdt)
+    sl, ks = torch.tensor(lens, dtype=torch.int32), torch.tensor(starts, dtype=torch.int32)
+    out = torch.empty(B, hq, d, dtype=odt, device=cuda)
+    v1.v1_decode_attention(q.to(cuda), torch.from_numpy(cache).to(cuda), bt.to(cuda), sl.to(cuda),
+                           torch.from_numpy(c).to(cuda), kb, vb, v_rotate=vrot, v_lloyd_max=lloyd,
+                           kv_start=ks.to(cuda), num_splits=splits, out=out)
+    want = O.v1_decode_attention(q.float().numpy(), cache, bt.numpy(), sl.numpy(), c, kb, vb,
+                                 1 / math.sqrt(d), kv_start=ks.numpy(), v_rotate=vrot, v_lloyd_max=lloyd)
+    got = out.float().cpu().numpy()
+    for b in range(B):
+        if lens[b] <= starts[b]:
+            assert not got[b].any()
+    _check_attn(got, want, f"v1 random case={case} B={B} hq={hq} hkv={hkv} K{kb}V{vb} vrot={vrot} "
+                           f"lloyd={lloyd} bs={bs} S={splits} {qdt}->{odt}")
+
+
 @pytest.mark.parametrize("bs", [16, 32, 64])
 def test_decode_kv_start_and_block_size(cuda, bs):
     from fused_turboquant import v1
