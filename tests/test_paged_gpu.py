@@ -298,6 +298,47 @@ def _dense_ref(cache, lens, bt, q, bk, bv, d):
     return O.dense_decode_attention(q.float().numpy(), Kd, Vd, lens, 1 / math.sqrt(d))
 
 
+@pytest.mark.parametrize("case", range(20))
+def test_decode_attention_random_shapes(cuda, case):
+    """Seeded random configurations of the paged decode: head_dim 128 / 256,
+    K and V widths 2..4, GQA group 1..16, page sizes 16..64, ragged contexts
+    with empty rows, the single-launch and split forms (1..24 splits), bf16 /
+    fp16 / fp32 queries and outputs; against float64 attention over the
+    oracle's decode of the stored pages."""
+    from fused_turboquant.paged import PagedTurboQuantCache
+    rng = np.random.default_rng(2000 + case)
+    d = int(rng.choice([128, 256]))
+    bk, bv = int(rng.integers(2, 5)), int(rng.integers(2, 5))
+    hkv = int(rng.choice([1, 2, 4, 8]))
+    hq = hkv * int(rng.choice([1, 2, 3, 4, 8, 16]))
+    page = int(rng.choice([16, 32, 48, 64]))
+    B = int(rng.integers(1, 6))
+    lens = [int(x) for x in rng.integers(0, 600, B)]
+    lens[int(rng.integers(0, B))] = max(lens[0], 1)  # at least one non-empty row
+    splits = int(rng.choice([1, 2, 3, 8, 24]))
+    qdt = [torch.bfloat16, torch.float16, torch.float32][int(rng.integers(0, 3))]
+    odt = [torch.bfloat16, torch.float16, torch.float32][int(rng.integers(0, 3))]
+    maxp = max(1, max((L + page - 1) // page for L in lens))
+    g = torch.Generator().manual_seed(case)
+    nblk = B * maxp + 2
+    cache = PagedTurboQuantCache(nblk, page, hkv, d, bk, bv, device=cuda)
+    bt = torch.randperm(nblk, generator=g)[: B * maxp].view(B, maxp).to(torch.int32)
+    _fill(cache, lens, bt, hkv, d, g, cuda)
+    q = torch.randn(B, hq, d, generator=g).to(qdt)
+    ref = _dense_ref(cache, lens, bt, q, bk, bv, d)
+    sl = torch.tensor(lens, dtype=torch.int32, device=cuda)
+    out = cache.decode_attention(q.to(cuda), bt.to(cuda), sl, num_splits=splits,
+                                 out=torch.empty(B, hq, d, dtype=odt, device=cuda)).float().cpu().numpy()
+    for b, L in enumerate(lens):
+        if L == 0:
+            assert not out[b].any()
+    err = np.abs(out - ref)
+    tag = (f"[paged random case={case} d={d} K{bk}V{bv} hq={hq} hkv={hkv} page={page} B={B} S={splits} "
+           f"{qdt}->{odt}]")
+    print(f"{tag} max={err.max():.2e} mean={err.mean():.2e}")
+    assert err.max() <= 2e-2 and err.mean() <= 2e-3, tag
+
+
 @pytest.mark.parametrize("bk,bv", [(3, 3), (4, 2), (2, 4), (4, 4), (2, 2)])
 @pytest.mark.parametrize("hq,hkv", [(32, 8), (8, 8), (12, 4)])
 @pytest.mark.parametrize("outliers", [False, True])
