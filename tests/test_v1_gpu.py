@@ -80,6 +80,24 @@ def test_store_parity_matrix_core_path(cuda, kb, vb, dtn, vrot):
                     special=True)
 
 
+@pytest.mark.parametrize("case", range(16))
+def test_store_random_shapes(cuda, case):
+    """Seeded random store configurations: head_dim 64 / 128 / 256, K and V
+    widths 2..4, V rotated or not, bf16 / fp16 / fp32 input, block sizes
+    16..64, 1..12 heads, 2..40 blocks, outlier keys and the special rows;
+    every slot byte against the oracle as in the fixed cases."""
+    rng = np.random.default_rng(3000 + case)
+    d = int(rng.choice([64, 128, 256]))
+    kb, vb = int(rng.integers(2, 5)), int(rng.integers(2, 5))
+    vrot = bool(rng.random() < 0.5)
+    dtn = ["bf16", "f16", "f32"][int(rng.integers(0, 3))]
+    bs = int(rng.choice([16, 32, 64]))
+    h = int(rng.integers(1, 13))
+    nb = int(rng.integers(2, 41))  # at least 17 slots: the checker skips slots 4 and 9
+    _check_v1_store(cuda, d, kb, vb, vrot, dtn, nb, bs, h, 5000 + case, outliers=bool(rng.random() < 0.5),
+                    special=bool(rng.random() < 0.3))
+
+
 def _check_v1_store(cuda, d, kb, vb, vrot, dtn, nb, bs, h, seed, outliers=False, special=False):
     from fused_turboquant import v1
     g = torch.Generator().manual_seed(seed)
