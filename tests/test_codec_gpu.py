@@ -107,6 +107,81 @@ def test_config1_outliers_4bit(cuda, golden):
     assert np.array_equal(tq.decode(ct).cpu().numpy(), enc["dec_cfg1"])
 
 
+def _decode_c(packed, norms16, levels, signs, bits, d, odt, dev):
+    """ftq_decode on host arrays (packed uint8 [n, d bits / 8], norms as fp16
+    bit patterns, float32 levels and signs); returns the output tensor."""
+    from fused_turboquant import _lib
+    n = packed.shape[0]
+    pk = torch.from_numpy(np.ascontiguousarray(packed)).to(dev)
+    nm = torch.from_numpy(np.ascontiguousarray(norms16.view(np.int16))).to(dev)
+    lv = torch.from_numpy(np.ascontiguousarray(levels, np.float32)).to(dev)
+    sg = torch.from_numpy(np.ascontiguousarray(signs, np.float32)).to(dev)
+    out = torch.empty(n, d, dtype=odt, device=dev)
+    L = _lib.lib()
+    _lib.check(L.ftq_decode(pk.data_ptr(), nm.data_ptr(), n, d, lv.data_ptr(), sg.data_ptr(), bits, out.data_ptr(),
+                            _lib.dtype_code(odt), _lib.stream_ptr(dev)))
+    torch.cuda.synchronize(dev)
+    return out
+
+
+def _same_bits(got, want, label):
+    """Equal bit patterns, the sign of every zero included; NaNs only by
+    position (a NaN's sign and payload are the producing unit's choice)."""
+    gn, wn = np.isnan(got), np.isnan(want)
+    assert np.array_equal(gn, wn), f"{label}: NaN positions differ"
+    ok = ~wn
+    gb = got.view(np.uint32)[ok]
+    wb = want.view(np.uint32)[ok]
+    bad = np.flatnonzero(gb != wb)
+    assert bad.size == 0, f"{label}: {bad.size} values differ, first {got[ok][bad[0]]!r} vs {want[ok][bad[0]]!r}"
+
+
+@pytest.mark.parametrize("d", [64, 128, 256])
+@pytest.mark.parametrize("bits", [2, 3, 4])
+def test_decode_bitwise_with_zero_signs(cuda, d, bits):
+    """Decode equals the oracle bit for bit, including the sign of every zero,
+    on rows built to cancel exactly: pairs of mirrored codes over a symmetric
+    level table and constant rows (where all but one output is an exact zero).
+    The norms include +0, -0, NaN, +-inf, the smallest subnormal, the largest
+    fp16 and negative values, on scattered rows of waves that otherwise hold
+    ordinary rows. The level tables include one with a +0 level, one with a
+    -0 level, one with an infinite level and one so large that the sums
+    overflow."""
+    rng = np.random.default_rng(1000 + 10 * d + bits)
+    L = 1 << bits
+    pos = np.sort(rng.uniform(0.01, 0.3, L // 2).astype(np.float32))
+    sym = np.concatenate([-pos[::-1], pos]).astype(np.float32)
+    tables = {"symmetric": sym}
+    t = sym.copy(); t[L // 2] = 0.0; tables["plus_zero"] = t
+    t = sym.copy(); t[L // 2 - 1] = -0.0; tables["minus_zero"] = t
+    t = sym.copy(); t[-1] = np.inf; tables["inf"] = t
+    tables["overflow"] = (sym * np.float32(1e36)).astype(np.float32)
+    n = 1031
+    codes = rng.integers(0, L, (n, d))
+    mir = rng.random(n) < 0.3                      # mirrored pairs: y[2m + 1] = -y[2m]
+    codes[mir, 1::2] = (L - 1) - codes[mir, 0::2]
+    const = rng.random(n) < 0.1                    # constant rows
+    codes[const] = codes[const, :1]
+    packed = O.pack(codes, bits)
+    norms = rng.uniform(0.25, 4.0, n).astype(np.float16)
+    special = np.array([0x0000, 0x8000, 0x7E00, 0x7C00, 0xFC00, 0x0001, 0x7BFF, 0xBC00, 0xC400], np.uint16)
+    rows = rng.choice(n, 4 * special.size, replace=False)
+    nb = norms.view(np.uint16).copy()
+    nb[rows] = np.resize(special, rows.size)
+    signs = np.where(rng.random(d) < 0.5, -1.0, 1.0).astype(np.float32)
+    for name, lev in tables.items():
+        with np.errstate(all="ignore"):
+            want = O.decode(packed, nb.view(np.float16), lev, signs, bits, d)
+        got = _decode_c(packed, nb, lev, signs, bits, d, torch.float32, cuda).cpu().numpy()
+        _same_bits(got, want, f"d={d} bits={bits} {name} f32")
+        if name == "symmetric":
+            assert (want == 0).sum() > 0 and np.signbit(want[want == 0]).any()
+            # bf16 values widened exactly to float32, so NaNs are found by value
+            wb = torch.from_numpy(want).to(torch.bfloat16).float().numpy()
+            gb = _decode_c(packed, nb, lev, signs, bits, d, torch.bfloat16, cuda).float().cpu().numpy()
+            _same_bits(gb, wb, f"d={d} bits={bits} {name} bf16")
+
+
 def _encode_c(x, signs, bnd, bits, cls, dev):
     """ftq_encode_cb on device tensors x [n, d], signs [d], boundaries [2^bits + 1]."""
     from fused_turboquant import _lib
