@@ -246,6 +246,33 @@ def test_rht_forward_inverse(cuda, d, dtype):
     assert np.array_equal(fwht(x.to(cuda)).cpu().numpy(), O.fwht(x.float().numpy()))
 
 
+@pytest.mark.parametrize("d", [64, 128, 256])
+def test_rht_bitwise_with_zero_signs(cuda, d):
+    """Forward and inverse RHT equal the oracle bit for bit, the sign of every
+    zero included, on rows that cancel exactly (x[2m + 1] = +-x[2m], constant
+    rows), rows of +0 and -0 entries, and rows holding an infinity or a NaN."""
+    from fused_turboquant.core.hadamard import generate_rht_signs, inverse_randomized_hadamard, randomized_hadamard
+    rng = np.random.default_rng(77 + d)
+    n = 517
+    x = rng.standard_normal((n, d)).astype(np.float32)
+    r = rng.random(n)
+    same, opp, const, zero = r < 0.2, (r >= 0.2) & (r < 0.4), (r >= 0.4) & (r < 0.5), (r >= 0.5) & (r < 0.6)
+    x[same, 1::2] = x[same, 0::2]
+    x[opp, 1::2] = -x[opp, 0::2]
+    x[const] = x[const, :1]
+    x[zero] = np.where(rng.random((int(zero.sum()), d)) < 0.5, np.float32(0.0), np.float32(-0.0))
+    x[7, 3], x[11, 5], x[13, 0] = np.inf, -np.inf, np.nan
+    s = generate_rht_signs(d, 3)
+    with np.errstate(all="ignore"):
+        want = O.rht(x, s.numpy())
+        want_inv = O.inverse_rht(want, s.numpy())
+    assert np.signbit(want[want == 0]).any() and (~np.signbit(want[want == 0])).any()
+    got = randomized_hadamard(torch.from_numpy(x).to(cuda), s.to(cuda)).cpu().numpy()
+    _same_bits(got, want, f"rht d={d}")
+    got_inv = inverse_randomized_hadamard(torch.from_numpy(want).to(cuda), s.to(cuda)).cpu().numpy()
+    _same_bits(got_inv, want_inv, f"inverse rht d={d}")
+
+
 def test_small_and_empty_batches(cuda):
     from fused_turboquant import TurboQuantMSE
     tq = TurboQuantMSE(128, bits=3, device=cuda)
