@@ -144,6 +144,42 @@ def test_store_prefill_parity(cuda, bk, bv, page, dtype, d):
     _check_store(cache, k, v, slots, d, bk, bv, page, "prefill")
 
 
+@pytest.mark.parametrize("case", range(16))
+def test_store_random_shapes(cuda, case):
+    """Seeded random store configurations: head_dim 128 / 256, K and V widths
+    2..4, pages of 16..64 tokens, bf16 / fp16 / fp32 input, 1..8 kv heads,
+    2..12 pages.  The slots run in page order (whole sub-blocks: the
+    matrix-core store) with a seeded scattered stretch, skipped slots and a
+    ragged tail (the per-token store); outlier keys in half the cases.
+    Codes and norms against the oracle as in the fixed cases."""
+    from fused_turboquant.paged import PagedTurboQuantCache
+    rng = np.random.default_rng(7000 + case)
+    d = int(rng.choice([128, 256]))
+    bk, bv = int(rng.integers(2, 5)), int(rng.integers(2, 5))
+    page = int(rng.choice([16, 32, 48, 64]))
+    dtype = [torch.bfloat16, torch.float16, torch.float32][int(rng.integers(0, 3))]
+    hkv, nblk = int(rng.integers(1, 9)), int(rng.integers(2, 13))
+    g = torch.Generator().manual_seed(7000 + case)
+    cache = PagedTurboQuantCache(nblk, page, hkv, d, bk, bv, device=cuda)
+    pages = torch.randperm(nblk, generator=g)
+    slots = (pages[:, None] * page + torch.arange(page)[None, :]).reshape(-1)
+    total = slots.numel()
+    a = int(rng.integers(0, total))
+    b = min(total, a + int(rng.integers(2, 40)))
+    slots[a:b] = slots[a:b][torch.from_numpy(rng.permutation(b - a))]
+    slots[torch.from_numpy(rng.choice(total, size=3, replace=False))] = -1
+    n = int(rng.integers(1, total + 1))
+    slots = slots[:n].clone()
+    k = torch.randn(n, hkv, d, generator=g)
+    v = torch.randn(n, hkv, d, generator=g)
+    if rng.random() < 0.5:
+        k[::29] *= 8
+    k, v = k.to(dtype), v.to(dtype)
+    cache.store(k.to(cuda), v.to(cuda), slots.to(cuda))
+    _check_store(cache, k, v, slots, d, bk, bv, page,
+                 f"random case={case} d={d} hkv={hkv} nblk={nblk} n={n} {dtype}")
+
+
 @pytest.mark.parametrize("bk,bv", [(3, 3), (4, 2), (2, 4), (4, 4)])
 @pytest.mark.parametrize("hq,hkv", [(32, 8), (8, 8), (16, 2)])
 def test_decode_attention_parity(cuda, bk, bv, hq, hkv):
