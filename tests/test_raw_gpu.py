@@ -107,6 +107,46 @@ def test_decode_kv_start_block_size_and_padded_slot(cuda, bs):
     _check(got, want, torch.float32, f"raw kv_start bs={bs}")
 
 
+@pytest.mark.parametrize("case", range(16))
+def test_decode_random_shapes(cuda, case):
+    """Seeded random raw-slot decode configurations: head_dim 64 / 128 / 256,
+    GQA groups up to 8 (16 at 64 / 256), 1..6 sequences with ragged, empty and
+    offset ranges (kv_start), 1..40 splits, block sizes 16..64, slots wider
+    than the data, bf16 / fp16 / fp32 queries and outputs, against the oracle."""
+    from fused_turboquant import raw
+    rng = np.random.default_rng(9000 + case)
+    d = int(rng.choice([64, 128, 256]))
+    hkv = int(rng.choice([1, 2, 4, 8]))
+    G = int(rng.choice([x for x in (1, 2, 3, 4, 7, 8, 16) if x <= (8 if d == 128 else 16)]))
+    hq = hkv * G
+    bs = int(rng.choice([16, 32, 64]))
+    B = int(rng.integers(1, 7))
+    lens = [int(x) for x in rng.integers(0, 700, B)]
+    starts = [int(rng.integers(0, L + 1)) if rng.random() < 0.4 else 0 for L in lens]
+    splits = int(rng.choice([1, 2, 3, 7, 16, 40]))
+    qdt = [torch.bfloat16, torch.float16, torch.float32][int(rng.integers(0, 3))]
+    odt = [torch.bfloat16, torch.float16, torch.float32][int(rng.integers(0, 3))]
+    pad = int(rng.choice([0, 32, 64]))
+    mb = max(1, max((L + bs - 1) // bs for L in lens))
+    nb = mb * B + 3
+    g = torch.Generator().manual_seed(9000 + case)
+    cache = _oracle_cache(g, nb, bs, hkv, d, nb * bs, slot=4 * d + pad)
+    bt = torch.stack([torch.randperm(nb, generator=g)[:mb] for _ in range(B)]).to(torch.int32)
+    q = torch.randn(B, hq, d, generator=g).to(qdt)
+    sl, ks = torch.tensor(lens, dtype=torch.int32), torch.tensor(starts, dtype=torch.int32)
+    out = torch.empty(B, hq, d, dtype=odt, device=cuda)
+    raw.raw_decode_attention(q.to(cuda), torch.from_numpy(cache).to(cuda), bt.to(cuda), sl.to(cuda),
+                             kv_start=ks.to(cuda), num_splits=splits, out=out)
+    want = O.raw_decode_attention(q.float().numpy(), cache, bt.numpy(), sl.numpy(), 1 / math.sqrt(d),
+                                  kv_start=ks.numpy())
+    got = out.float().cpu().numpy()
+    for b in range(B):
+        if lens[b] <= starts[b]:
+            assert not got[b].any()
+    _check(got, want, odt, f"raw random case={case} d={d} B={B} hq={hq} hkv={hkv} bs={bs} S={splits} "
+                           f"pad={pad} {qdt}->{odt}")
+
+
 def test_store_then_decode_end_to_end(cuda):
     """GPU store, then GPU decode, against the oracle pipeline on the same inputs
     (large-magnitude outliers, bf16 input)."""
