@@ -203,6 +203,34 @@ def test_decode_parity_lloyd_v(cuda, d, kb):
     _decode_case(cuda, d, kb, 4, 8, 2, splits=4, lloyd=True, seed=d + kb)
 
 
+@pytest.mark.parametrize("case", range(16))
+def test_decode_random_formats(cuda, case):
+    """Seeded random configurations of the fp32-product decode over every
+    slot format: head_dim 64 / 128 / 256; K / V widths from 1..4 and 8, fp8
+    keys, or Lloyd-Max V at 4 bits; GQA groups 1..16; 1..16 splits; V
+    rotated or not; fp32 or bf16 output; with or without kv_start."""
+    rng = np.random.default_rng(11000 + case)
+    d = int(rng.choice([64, 128, 256]))
+    fmt = int(rng.integers(0, 4))
+    fp8 = lloyd = False
+    if fmt == 0:
+        kb, vb = EXT_WIDTHS[int(rng.integers(0, len(EXT_WIDTHS)))]
+    elif fmt == 1:
+        kb = vb = 8
+        fp8 = True
+    elif fmt == 2:
+        kb, vb, lloyd = int(rng.integers(1, 5)), 4, True
+    else:
+        kb, vb = int(rng.integers(2, 5)), int(rng.integers(2, 5))
+    hkv = int(rng.choice([1, 2, 4]))
+    hq = hkv * int(rng.choice([1, 2, 3, 4, 8, 16]))
+    splits = int(rng.choice([1, 2, 5, 16]))
+    vrot = lloyd or bool(rng.random() < 0.5)
+    _decode_case(cuda, d, kb, vb, hq, hkv, splits, vrot=vrot, key_fp8=fp8, lloyd=lloyd,
+                 fp32_out=bool(rng.random() < 0.5), operands="fp32", kv_start=bool(rng.random() < 0.5),
+                 seed=11000 + case)
+
+
 @pytest.mark.parametrize("d", [64, 256])
 def test_decode_bf16_out_and_kv_start(cuda, d):
     _decode_case(cuda, d, 3, 3, 8, 2, splits=16, fp32_out=False, kv_start=True, seed=d * 3)
