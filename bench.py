@@ -404,7 +404,7 @@ def v1_setup(dev, cfg4=None, operands="f16"):
     flags = V1.VROT | (V1.FP32 if operands == "fp32" else 0)
     B, hq, d = q.shape
     hkv = cache.shape[2]
-    splits = V1.default_splits(B, hkv, max(lens))
+    splits = V1.default_splits(B, hkv, max(lens), hq, d, layer.key_bits, layer.value_bits, flags)
     out = torch.empty(B, hq, d, dtype=torch.bfloat16, device=dev)
     ws = torch.empty(V1.workspace_bytes(B, hq, d, splits), dtype=torch.uint8, device=dev)
     V1.v1_decode_attention(q, cache, bt, sl, layer.centroids, layer.key_bits, layer.value_bits,

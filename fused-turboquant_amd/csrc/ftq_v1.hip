@@ -1438,6 +1438,61 @@ extern "C" int ftq_v1_default_splits(int batch, int num_kv_heads, int max_seq_le
 }
 
 namespace {
+// Workgroups of the matrix-core decode kernel that runs this shape that the
+// GPU holds at once (the occupancy of the bf16-query instantiation; the query
+// type does not change the register count).
+template <int KB, int VB>
+int v1_attn_resident(int group, bool lloyd) {
+  if constexpr (VB == 4) {
+    if (lloyd) {
+      static const int c = resident_workgroups(v1_attn_kernel<128, KB, VB, BF16, true>);
+      return c;
+    }
+  }
+  if (group == 4) {
+    static const int c = resident_workgroups(v1_attn_g4_kernel<128, KB, VB, BF16>);
+    return c;
+  }
+  static const int c = resident_workgroups(v1_attn_kernel<128, KB, VB, BF16>);
+  return c;
+}
+template <int KB>
+int v1_attn_resident_k(int value_bits, int group, bool lloyd) {
+  if (value_bits == 2) return v1_attn_resident<KB, 2>(group, lloyd);
+  if (value_bits == 3) return v1_attn_resident<KB, 3>(group, lloyd);
+  return v1_attn_resident<KB, 4>(group, lloyd);
+}
+}  // namespace
+
+extern "C" int ftq_v1_choose_splits(int batch, int num_q_heads, int num_kv_heads, int d, int key_bits,
+                                    int value_bits, int v_flags, int max_seq_len) {
+  if (batch <= 0 || num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads != 0) return 1;
+  const bool mfma = d == 128 && (v_flags & (V1F_KFP8 | V1F_FP32)) == 0 && key_bits >= 2 && key_bits <= 4 &&
+                    value_bits >= 2 && value_bits <= 4;
+  if (!mfma) return ftq_v1_default_splits(batch, num_kv_heads, max_seq_len);
+  // The most splits whose grid the GPU holds in one round: past that a second
+  // round of workgroups (or an uneven first one) costs more than the longer
+  // tiles per wave.  Measured on 32 query / 8 kv heads, K3 V3 (3 workgroups
+  // per CU) and K4 V2 (4): 384 units, 2K-32K positions, 2 splits 11-22%
+  // faster than 1; 448 and 512 units at K3 V3, 1 split best (two splits
+  // would need a second round); K4 V2 at 448 and 512, 2 splits 1-11%
+  // faster; 4 x 8 units at 64K-128K, K4 V2, 32 splits.  No more splits than
+  // leave 8 tiles per wave, and at most 64.
+  const int group = num_q_heads / num_kv_heads;
+  const bool lloyd = value_bits == 4 && (v_flags & V1F_VLM) != 0;
+  int cap;
+  if (key_bits == 2) cap = v1_attn_resident_k<2>(value_bits, group, lloyd);
+  else if (key_bits == 3) cap = v1_attn_resident_k<3>(value_bits, group, lloyd);
+  else cap = v1_attn_resident_k<4>(value_bits, group, lloyd);
+  const int64_t units = std::min<int64_t>((int64_t)batch * num_kv_heads, 1 << 20);
+  int64_t s = cap / units;
+  const int64_t by_len = max_seq_len / (32 * 4 * 8);
+  if (s > by_len) s = by_len;
+  if (s > 64) s = 64;
+  return s < 1 ? 1 : (int)s;
+}
+
+namespace {
 // Argument checks of the v1 decode attention entry points and the launch
 // arguments they imply.  check_ws: the caller's workspace (the no-alloc form
 // brings its own afterwards).  FTQ_OK with a.B == 0: nothing to launch.

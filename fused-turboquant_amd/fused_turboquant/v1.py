@@ -69,6 +69,8 @@ def _bind():
     L.ftq_v1_workspace_bytes.argtypes = [ctypes.c_int] * 4
     L.ftq_v1_default_splits.restype = ctypes.c_int
     L.ftq_v1_default_splits.argtypes = [ctypes.c_int] * 3
+    L.ftq_v1_choose_splits.restype = ctypes.c_int
+    L.ftq_v1_choose_splits.argtypes = [ctypes.c_int] * 8
     L._v1_bound = True
     return L
 
@@ -349,7 +351,17 @@ def v1_store(key: torch.Tensor, value: torch.Tensor, kv_cache: torch.Tensor,
                         _v_flags(v_rotate, v_lloyd_max, key_fp8), rot, cf)
 
 
-def default_splits(batch: int, num_kv_heads: int, max_seq_len: int) -> int:
+def default_splits(batch: int, num_kv_heads: int, max_seq_len: int, num_q_heads: int | None = None,
+                   head_dim: int | None = None, key_bits: int | None = None, value_bits: int | None = None,
+                   v_flags: int = 0) -> int:
+    """Split-K factor of the decode.  With the head geometry and widths
+    (``num_q_heads``, ``head_dim``, ``key_bits``, ``value_bits``, and the
+    ``v_flags`` bits of the call) it is sized to the kernel that runs: for the
+    matrix-core kernels the most splits whose workgroups the GPU holds at once
+    (``ftq_v1_choose_splits``); without them, ``ftq_v1_default_splits``."""
+    if None not in (num_q_heads, head_dim, key_bits, value_bits):
+        return int(_bind().ftq_v1_choose_splits(batch, num_q_heads, num_kv_heads, head_dim, key_bits,
+                                                value_bits, v_flags, max_seq_len))
     return int(_bind().ftq_v1_default_splits(batch, num_kv_heads, max_seq_len))
 
 
@@ -411,9 +423,10 @@ def v1_decode_attention(query: torch.Tensor, kv_cache: torch.Tensor, block_table
         q = q.float()
     if scale is None:
         scale = 1.0 / math.sqrt(d)
+    flags = _v_flags(v_rotate, v_lloyd_max, key_fp8, operands == "fp32")
     if num_splits is None:
         msl = max_seq_len if max_seq_len is not None else block_table.shape[1] * bs
-        num_splits = default_splits(B, hkv, msl)
+        num_splits = default_splits(B, hkv, msl, hq, d, key_bits, value_bits, flags)
     if out is None:
         out = torch.empty(B, hq, d, dtype=q.dtype, device=dev)
     need = workspace_bytes(B, hq, d, num_splits)
@@ -427,8 +440,7 @@ def v1_decode_attention(query: torch.Tensor, kv_cache: torch.Tensor, block_table
     rot = _rotation_arg(rotation, d, dev) if rotation is not None else None  # q M, and o M^T with v_rotate
     _ops.ops().v1_decode_attention(q, kv_cache, block_table.contiguous(), seq_lens.contiguous(), ks,
                                    cent.contiguous(), key_bits, value_bits, float(scale),
-                                   _v_flags(v_rotate, v_lloyd_max, key_fp8, operands == "fp32"),
-                                   int(num_splits), workspace, out, lse, rot)
+                                   flags, int(num_splits), workspace, out, lse, rot)
     return out
 
 

@@ -392,8 +392,13 @@ class FusedTurboQuantV1Impl(_ImplBase):
         being captured, else sized to the step's context, capped by it."""
         if torch.cuda.is_current_stream_capturing():
             return self.max_kv_splits
-        fn = RAW.default_splits if self._is_raw else V1.default_splits
-        return max(1, min(self.max_kv_splits, fn(B, self.num_kv_heads, max_seq_len)))
+        if self._is_raw:
+            s = RAW.default_splits(B, self.num_kv_heads, max_seq_len)
+        else:
+            flags = V1._v_flags(self.v_rotate, self.v_lloyd_max, self.key_fp8)
+            s = V1.default_splits(B, self.num_kv_heads, max_seq_len, self.num_heads, self.head_size,
+                                  self.key_bits, self.value_bits, flags)
+        return max(1, min(self.max_kv_splits, s))
 
     def _decode_hybrid(self, q, kv_cache, block_table, seq_lens, st, max_seq_len=None, layer=None, out=None):
         """Deferred-prefill decode (reference _decode_attention_hybrid,

@@ -280,6 +280,16 @@ int64_t ftq_v1_workspace_bytes(int batch, int num_q_heads, int d, int num_splits
  * output from the attention kernel itself (no merge launch; the workspace is
  * still checked but not written) unless a caller rotation matrix is given. */
 int ftq_v1_default_splits(int batch, int num_kv_heads, int max_seq_len);
+/* Split-K factor with the head geometry and slot format known: for the
+ * matrix-core kernels (d = 128, 2-4 bit K and V, no FTQ_V1_KFP8 / FTQ_V1_FP32
+ * flag) the most splits whose batch*Hkv*splits workgroups the GPU holds at
+ * once (the kernel's occupancy, from the HIP runtime), leaving at least 8
+ * tiles of 32 positions per wave, at most 64; other formats take
+ * ftq_v1_default_splits.  Host-side heuristic; no counterpart in the
+ * reference, whose decode takes vLLM's fixed NUM_KV_SPLITS
+ * (vllm_plugin/v1_backend.py:568-573, 895). */
+int ftq_v1_choose_splits(int batch, int num_q_heads, int num_kv_heads, int d, int key_bits,
+                         int value_bits, int v_flags, int max_seq_len);
 
 /*
  * Decode attention over the slot cache, one query token per sequence:

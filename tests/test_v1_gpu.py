@@ -253,6 +253,24 @@ def test_decode_single_split_direct_output(cuda, hq, hkv, vrot, lloyd, odt):
     assert v1.default_splits(48, 8, 4096) == 1 and v1.default_splits(4, 8, 131072) > 1
 
 
+def test_choose_splits_fills_one_round(cuda):
+    """The split factor with the slot format known (ftq_v1_choose_splits):
+    the most splits whose workgroups the GPU holds at once -- 3 per CU for
+    the GQA-4 kernel at K3 V3, 4 at K4 V2 -- with at least 8 tiles per wave.
+    The values are the measured best split counts at these shapes (32 query /
+    8 kv heads); the VALU formats keep the default rule."""
+    from fused_turboquant import v1
+
+    def ds(B, L, kb, vb, flags=v1.VROT):
+        return v1.default_splits(B, 8, L, 32, 128, kb, vb, flags)
+    assert ds(48, 2048, 3, 3) == 2 and ds(48, 32768, 3, 3) == 2
+    assert ds(56, 8192, 3, 3) == 1 and ds(64, 2300, 3, 3) == 1
+    assert ds(48, 2048, 4, 2) == 2 and ds(56, 8192, 4, 2) == 2 and ds(64, 8192, 4, 2) == 2
+    assert ds(4, 131072, 4, 2) == 32
+    assert ds(4, 1000, 4, 2) == 1  # 2 splits would leave under 8 tiles per wave
+    assert ds(4, 131072, 4, 2, v1.VROT | v1.FP32) == v1.default_splits(4, 8, 131072)
+
+
 @pytest.mark.parametrize("case", range(24))
 def test_decode_random_shapes(cuda, case):
     """Seeded random configurations of the matrix-core decode: GQA group 1..16,
