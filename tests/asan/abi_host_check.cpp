@@ -120,6 +120,12 @@ static void sizes() {
           for (int d : {64, 128, 256}) {
             const int c = ftq_paged_choose_splits(b, hq, h, d, L);
             EXPECT(c >= 1 && c <= 1024, "choose_splits(%d,%d,%d,%d,%d) = %d", b, hq, h, d, L, c);
+            // widths in and out of the matrix-core range, flags with and without the VALU bit
+            for (int kb : {1, 2, 4, 8})
+              for (int fl : {0, 3, 8}) {
+                const int v = ftq_v1_choose_splits(b, hq, h, d, kb, kb == 8 ? 8 : 6 - kb, fl, L);
+                EXPECT(v >= 1 && v <= 1024, "v1_choose_splits(%d,%d,%d,%d,%d,%d,%d) = %d", b, hq, h, d, kb, fl, L, v);
+              }
           }
       }
   EXPECT(ftq_v1_scratch_bytes() > 0, "scratch bytes");
