@@ -213,8 +213,9 @@ def test_decode_single_split_direct_output(cuda, hq, hkv, vrot, lloyd, odt):
     """One split writes the output from the attention kernel (no merge launch):
     output and natural-log LSE against the merged two-split result (they
     differ only in the order of the partial sums) and the oracle, empty rows
-    zero with LSE -inf, and the default split count at 384+ (batch, kv head)
-    units is that single split."""
+    zero with LSE -inf, and the three-argument default split count
+    (ftq_v1_default_splits) at 384+ (batch, kv head) units is that single
+    split."""
     from fused_turboquant import v1
     d, bs, nb, kb = 128, 16, 48, 3
     vb = 4 if lloyd else 3
